@@ -1,0 +1,399 @@
+#!/usr/bin/env python3
+"""Benchmark of the fused elementwise / row-reduction layer path on one MI355X.
+
+A step is one launch of the path's kernel over one batch of the BASELINE
+configuration (`--workload`, default configs[1]: residual add + RMSNorm on
+fp32 [4096 x 4096]).  Inputs are resident in HBM before the timed region;
+several buffer sets are rotated so the footprint of consecutive steps exceeds
+the 256 MiB Infinity Cache and every step streams from HBM.  Time is taken
+with HIP events recorded on the context's stream around exactly K steps,
+between two stream synchronisations.
+
+Prints ONE JSON line on stdout (progress goes to stderr).  Besides the
+headline workload, `ops` lists every op of configs[0..4] measured the same
+way, and `cpu_baseline` times the reference's own CPU code (compiled from the
+reference sources into oracle/_ref) on the host, single-threaded as the
+reference ops are.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import platform
+import sys
+
+import numpy as np
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(REPO, "mimir-framework_amd"))
+
+import mimir_hip as M  # noqa: E402
+from mimir_hip import datagen as G  # noqa: E402
+
+METRIC = "achieved HBM GB/s (% of MI355X peak) + rows/s per fused layer op vs host CPU"
+PEAK_GBS = 8000.0  # MI355X HBM3E
+MALL_BYTES = 256 << 20
+MIN_FOOTPRINT = 5 * MALL_BYTES  # rotate buffer sets until one pass covers 1.25 GiB
+MAX_SETS = 32
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+class OpBench:
+    """One op of one configuration: its inputs on the device (nsets copies)
+    and a closure that launches it on set i."""
+
+    def __init__(self, key, config, desc, kernel, nbytes, rows, row_unit, make):
+        self.key, self.config, self.desc, self.kernel = key, config, desc, kernel
+        self.nbytes, self.rows, self.row_unit = nbytes, rows, row_unit
+        self.make = make  # make(ctx, nsets) -> (step(i), buffers)
+
+    def nsets(self):
+        return max(2, min(MAX_SETS, math.ceil(MIN_FOOTPRINT / self.nbytes)))
+
+
+def _replicate(ctx, host_arrays, nsets):
+    """Upload each array once and device-copy it into nsets buffers."""
+    sets = []
+    for s in range(nsets):
+        bufs = []
+        for a in host_arrays:
+            d = ctx.empty(a.shape, a.dtype)
+            if s == 0:
+                ctx.upload(d, a)
+            else:
+                ctx.copy(d, sets[0][len(bufs)], a.nbytes)
+            bufs.append(d)
+        sets.append(bufs)
+    return sets
+
+
+def build_ops():
+    ops = []
+    f4 = 4
+
+    def ln_op(key, cfg, gen, rows, cols):
+        def make(ctx, nsets):
+            x, g, b, eps = gen()
+            gb = _replicate(ctx, [g, b], 1)[0]
+            sets = _replicate(ctx, [x, np.empty_like(x)], nsets)
+            return (lambda i: ctx.layernorm(sets[i][0], gb[0], gb[1], sets[i][1], rows, cols, eps)), sets
+        return OpBench(key, cfg, f"LayerNorm fp32 [{rows}x{cols}]", "norm_rows_vec<Layer>",
+                       2 * rows * cols * f4 + 2 * cols * f4, rows, "rows", make)
+
+    ops.append(ln_op("cfg0_layernorm", 0, G.cfg0_layernorm, 256, 512))
+
+    def make_cfg1(ctx, nsets):
+        x, r, w, eps = G.cfg1_add_rmsnorm()
+        wd = _replicate(ctx, [w], 1)[0][0]
+        sets = _replicate(ctx, [x, r, np.empty_like(x)], nsets)
+        return (lambda i: ctx.add_rmsnorm(sets[i][0], sets[i][1], sets[i][1], wd, sets[i][2], 4096, 4096,
+                                          eps)), sets
+    ops.append(OpBench("cfg1_add_rmsnorm", 1, "residual add + RMSNorm fp32 x,r [4096x4096] -> y, residual'",
+                       "norm_rows_vec<AddRms>", 4 * 4096 * 4096 * f4 + 4096 * f4, 4096, "rows", make_cfg1))
+
+    def make_cfg2(ctx, nsets):
+        s = G.cfg2_softmax().reshape(-1, 1024)
+        sets = _replicate(ctx, [s, np.empty_like(s)], nsets)
+        del s
+        return (lambda i: ctx.softmax(sets[i][0], sets[i][1], 262144, 1024, M.SOFTMAX_DIV_EPS)), sets
+    ops.append(OpBench("cfg2_softmax", 2, "causal row softmax fp32 [8x32x1024x1024]", "softmax_rows_vec",
+                       2 * 262144 * 1024 * f4, 262144, "rows", make_cfg2))
+
+    def make_cfg3a(ctx, nsets):
+        table, ids = G.cfg3_gather()
+        sets = _replicate(ctx, [table, ids, np.empty((ids.size, 4096), np.float32)], nsets)
+        del table
+        return (lambda i: ctx.embedding(sets[i][1], 32768, sets[i][0], 32000 * 4096, 32000, 4096, -1,
+                                        sets[i][2])), sets
+    ops.append(OpBench("cfg3_gather", 3, "token-embedding gather table [32000x4096] ids int32 [16x2048]",
+                       "embed_vec", 32768 * 4 + 2 * 32768 * 4096 * f4, 32768, "token rows", make_cfg3a))
+
+    def make_cfg3b(ctx, nsets):
+        q, k, theta = G.cfg3_rope()
+        c, s = M.rope_table(2048, 128, theta)
+        cs = _replicate(ctx, [c, s], 1)[0]
+        sets = _replicate(ctx, [q, k], nsets)
+        del q, k
+        return (lambda i: ctx.rope(sets[i][0], sets[i][0], 32, sets[i][1], sets[i][1], 32, 16, 2048, 128, 0,
+                                   cs[0], cs[1], 2048)), sets
+    ops.append(OpBench("cfg3_rope", 3, "RoPE q,k [16x2048x32x128] in place, one launch", "rope_vec",
+                       2 * 2 * 16 * 2048 * 32 * 128 * f4, 2 * 16 * 2048 * 32, "head rows", make_cfg3b))
+
+    ops.append(ln_op("cfg4_layernorm", 4, G.cfg4_layernorm, 8192, 4096))
+
+    def make_gelu(ctx, nsets):
+        a = G.cfg4_gelu()
+        sets = _replicate(ctx, [a, np.empty_like(a)], nsets)
+        return (lambda i: ctx.gelu(sets[i][0], sets[i][1], a.size)), sets
+    ops.append(OpBench("cfg4_gelu", 4, "tanh-GELU fp32 [8192x11008]", "unary_vec<Gelu>",
+                       2 * 8192 * 11008 * f4, 8192, "rows", make_gelu))
+
+    def make_swiglu(ctx, nsets):
+        g, u = G.cfg4_swiglu()
+        sets = _replicate(ctx, [g, u, np.empty_like(g)], nsets)
+        return (lambda i: ctx.silu_mul(sets[i][0], sets[i][1], sets[i][2], g.size)), sets
+    ops.append(OpBench("cfg4_silu_mul", 4, "SiLU-gated product silu(gate)*up fp32 [8192x11008]",
+                       "binary_vec<SiluMul>", 3 * 8192 * 11008 * f4, 8192, "rows", make_swiglu))
+
+    def make_add(ctx, nsets):
+        a, b = G.cfg4_add()
+        sets = _replicate(ctx, [a, b, np.empty_like(a)], nsets)
+        return (lambda i: ctx.add(sets[i][0], a.size, sets[i][1], b.size, sets[i][2])), sets
+    ops.append(OpBench("cfg4_add", 4, "residual add fp32 [8192x4096]", "binary_vec<Add>",
+                       3 * 8192 * 4096 * f4, 8192, "rows", make_add))
+
+    # Calibration: a plain streaming copy of 512 MiB (mimir_copy), the
+    # practical HBM ceiling and the yardstick for the FETCH/WRITE counters.
+    def make_copy(ctx, nsets):
+        n = 128 << 20
+        sets = [[ctx.empty(n), ctx.empty(n)] for _ in range(nsets)]
+        return (lambda i: ctx.copy(sets[i][1], sets[i][0], n * 4)), sets
+    ops.append(OpBench("calib_copy", -1, "streaming copy 512 MiB (mimir_copy)", "copy16_kernel",
+                       2 * (128 << 20) * f4, 128 << 20, "floats", make_copy))
+    return ops
+
+
+def time_op(ctx, op, steps, warmup):
+    nsets = op.nsets()
+    step, sets = op.make(ctx, nsets)
+    try:
+        for i in range(warmup):
+            step(i % nsets)
+        ctx.sync()
+        e0, e1 = ctx.event(), ctx.event()
+        e0.record()
+        for i in range(steps):
+            step(i % nsets)
+        e1.record()
+        ctx.sync()
+        ms = e0.elapsed_ms(e1)
+        e0.close()
+        e1.close()
+    finally:
+        for bufs in sets:
+            for b in bufs:
+                b.free()
+    us = ms * 1e3 / steps
+    gbs = op.nbytes / (us * 1e-6) / 1e9
+    return {
+        "op": op.key, "config": op.config, "desc": op.desc, "kernel": op.kernel,
+        "algorithmic_bytes": op.nbytes, "us_per_launch": round(us, 3), "GB_s": round(gbs, 1),
+        "frac_of_peak": round(gbs / PEAK_GBS, 4), "rows_per_s": round(op.rows / (us * 1e-6), 1),
+        "row_unit": op.row_unit, "launches": steps, "buffer_sets": nsets,
+        "footprint_MiB": round(nsets * op.nbytes / 2**20, 1),
+    }
+
+
+# ---------------------------------------------------------------------------
+# CPU baseline leg: the reference's own code (oracle/_ref) or, for ops with no
+# reference function, the C restatement (oracle/lib), single-threaded.
+# ---------------------------------------------------------------------------
+
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or "unknown"
+
+
+def cpu_leg(which, reps):
+    sys.path.insert(0, os.path.join(REPO, "oracle"))
+    import oracle as O
+    have_ref = O.ref_available()
+    out = {}
+
+    def rec(key, seconds, nbytes, rows, kind, sample):
+        gbs = nbytes / seconds / 1e9
+        out[key] = {"value": round(gbs, 3), "unit": "GB/s", "seconds": round(seconds, 6),
+                    "rows_per_s": round(rows / seconds, 1), "cores": 1, "kind": kind, "sample": sample}
+
+    for key in which:
+        log(f"cpu baseline: {key}")
+        if key == "cfg1_add_rmsnorm":
+            x, r, w, eps = G.cfg1_add_rmsnorm()
+            nb = 4 * x.nbytes + w.nbytes
+            if have_ref:
+                t = O.ref_time_op(O.REF_T_ADD_RMSNORM, x, r, w, 4096, 4096, eps, reps)
+                rec(key, t, nb, 4096, "reference",
+                    "full configs[1] (4096x4096): LayerOps::add_forward then Normalization::rms_norm, "
+                    f"median of {reps} calls")
+            else:
+                t = O.time_port(lambda: O.add_rmsnorm(x, r, w, eps), reps)
+                rec(key, t, nb, 4096, "port", f"full configs[1], oracle add_rmsnorm, median of {reps}")
+        elif key in ("cfg0_layernorm", "cfg4_layernorm"):
+            x, g, b, eps = (G.cfg0_layernorm() if key == "cfg0_layernorm" else G.cfg4_layernorm())
+            rows, cols = x.shape
+            nb = 2 * x.nbytes + g.nbytes + b.nbytes
+            if have_ref:
+                t = O.ref_time_op(O.REF_T_LAYERNORM, x, None, np.concatenate([g, b]), rows, cols, eps, reps)
+                rec(key, t, nb, rows, "reference", f"full [{rows}x{cols}] LayerOps::layernorm_forward")
+            else:
+                t = O.time_port(lambda: O.layernorm(x, cols, g, b, eps), reps)
+                rec(key, t, nb, rows, "port", f"full [{rows}x{cols}] oracle layernorm")
+        elif key == "cfg2_softmax":
+            s = G.cfg2_softmax(batch=1, heads=4).reshape(-1, 1024)  # 1/64 of the rows
+            nb = 2 * s.nbytes
+            if have_ref:
+                t = O.ref_time_op(O.REF_T_SOFTMAX, s, rows=s.shape[0], cols=1024, reps=reps)
+                rec(key, t, nb, s.shape[0], "reference",
+                    "4096 of 262144 causal rows (batch 1, heads 4) LayerOps::softmax_inplace")
+            else:
+                t = O.time_port(lambda: O.softmax_rows(s), reps)
+                rec(key, t, nb, s.shape[0], "port", "4096 causal rows, oracle softmax_rows")
+        elif key == "cfg3_gather":
+            table, ids = G.cfg3_gather()
+            t = O.time_port(lambda: O.embedding(ids, table, 32000, 4096, -1), reps)
+            rec(key, t, ids.nbytes + 2 * ids.size * 4096 * 4, ids.size, "port",
+                "full configs[3] gather, oracle embedding_i32 (the reference gather is inline in Model.cpp)")
+        elif key == "cfg3_rope":
+            q, k, theta = G.cfg3_rope(batch=2)
+            c, s = O.rope_table(2048, 128, theta)
+            t = O.time_port(lambda: (O.rope(q, c, s), O.rope(k, c, s)), reps)
+            rec(key, t, 2 * (q.nbytes + k.nbytes), 2 * 2 * 2048 * 32, "port",
+                "batch 2 of 16, q and k, oracle rope (no reference RoPE exists)")
+        elif key == "cfg4_gelu":
+            a = G.cfg4_gelu(rows=512)
+            if have_ref:
+                t = O.ref_time_op(O.REF_T_GELU, a, reps=reps)
+                rec(key, t, 2 * a.nbytes, 512, "reference", "512 of 8192 rows, LayerOps::gelu_forward")
+            else:
+                t = O.time_port(lambda: O.gelu(a), reps)
+                rec(key, t, 2 * a.nbytes, 512, "port", "512 of 8192 rows, oracle gelu")
+        elif key == "cfg4_silu_mul":
+            g, u = G.cfg4_swiglu(rows=512)
+            if have_ref:
+                t = O.ref_time_op(O.REF_T_SILU_MUL, g, u, reps=reps)
+                rec(key, t, 3 * g.nbytes, 512, "reference",
+                    "512 of 8192 rows, multiply_forward(silu_forward(gate), up)")
+            else:
+                t = O.time_port(lambda: O.silu_mul(g, u), reps)
+                rec(key, t, 3 * g.nbytes, 512, "port", "512 of 8192 rows, oracle silu_mul")
+        elif key == "cfg4_add":
+            a, b = G.cfg4_add()
+            if have_ref:
+                t = O.ref_time_op(O.REF_T_ADD, a, b, reps=reps)
+                rec(key, t, 3 * a.nbytes, 8192, "reference", "full [8192x4096] LayerOps::add_forward")
+            else:
+                t = O.time_port(lambda: O.add(a, b), reps)
+                rec(key, t, 3 * a.nbytes, 8192, "port", "full [8192x4096] oracle add")
+    return out
+
+
+def load_traffic(workload):
+    path = os.path.join(REPO, "profiles", f"traffic_{workload}.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        return json.load(f)
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--workload", default="cfg1_add_rmsnorm")
+    ap.add_argument("--op-steps", type=int, default=30, help="launches per op in the `ops` sweep")
+    ap.add_argument("--ops", default="all", help="'all', 'none', or a comma list of op keys")
+    ap.add_argument("--cpu", default="all", help="'all', 'workload' or 'none'")
+    ap.add_argument("--cpu-reps", type=int, default=3)
+    args = ap.parse_args()
+
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py measures one MI355X: this path has no multi-GPU form in this build "
+              f"(--gpus {args.gpus}, WORLD_SIZE {world} requested); run with --gpus 1.",
+              file=sys.stderr)
+        sys.exit(2)
+
+    ops = build_ops()
+    by_key = {o.key: o for o in ops}
+    if args.workload not in by_key:
+        sys.exit(f"unknown workload {args.workload}; choose from {sorted(by_key)}")
+    head = by_key[args.workload]
+
+    ctx = M.Context(0)
+    log(f"workload {head.key}: {head.desc}")
+    res = time_op(ctx, head, args.steps, args.warmup)
+    log(f"  {res['us_per_launch']} us/launch, {res['GB_s']} GB/s ({100 * res['frac_of_peak']:.1f}% of peak)")
+
+    sweep = []
+    keys = ([o.key for o in ops] if args.ops == "all" else
+            [] if args.ops == "none" else args.ops.split(","))
+    for k in keys:
+        if k == head.key:
+            sweep.append(res)
+            continue
+        r = time_op(ctx, by_key[k], args.op_steps, 3)
+        log(f"op {k}: {r['us_per_launch']} us/launch, {r['GB_s']} GB/s ({100 * r['frac_of_peak']:.1f}%)")
+        sweep.append(r)
+    ctx.close()
+
+    cpu = {}
+    if args.cpu != "none":
+        try:
+            cpu = cpu_leg([head.key] if args.cpu == "workload" else keys or [head.key], args.cpu_reps)
+        except Exception as e:  # the baseline is reported, never required
+            log(f"cpu baseline unavailable: {e}")
+    for r in sweep:
+        if r["op"] in cpu:
+            r["cpu_GB_s"] = cpu[r["op"]]["value"]
+            r["cpu_kind"] = cpu[r["op"]]["kind"]
+            r["speedup_vs_cpu"] = round(r["GB_s"] / cpu[r["op"]]["value"], 1)
+
+    traffic = load_traffic(head.key)
+    host = {"cpu_model": cpu_model(), "nproc": os.cpu_count()}
+    cb = cpu.get(head.key)
+    line = {
+        "metric": METRIC,
+        "value": res["GB_s"],
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(res["us_per_launch"] / 1e3, 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic: seeded N(0,1) inputs of the BASELINE configs (numpy PCG64), resident in HBM",
+        "config": {
+            "workload": (f"configs[{head.config}]: {head.desc}" if head.config >= 0 else head.desc),
+            "op": head.key,
+            "algorithmic_bytes_per_step": head.nbytes,
+            "rows_per_step": head.rows,
+            "buffer_sets": res["buffer_sets"],
+            "footprint_MiB": res["footprint_MiB"],
+            "mall": "buffer sets rotated so one pass exceeds 1.25 GiB (Infinity Cache 256 MiB)",
+        },
+        "rows_per_s": res["rows_per_s"],
+        "frac_of_peak": res["frac_of_peak"],
+        "roofline": {
+            "bound": "hbm",
+            "kernel": head.kernel,
+            "achieved": res["GB_s"],
+            "peak": PEAK_GBS,
+            "unit": "GB/s",
+            "frac": res["frac_of_peak"],
+            "traffic": None if traffic is None else traffic.get("traffic_bytes"),
+            "algorithmic_bytes": head.nbytes,
+        },
+        "cpu_baseline": None if cb is None else {
+            "value": cb["value"], "unit": cb["unit"], "cores": cb["cores"], "kind": cb["kind"],
+            "sample": cb["sample"], "rows_per_s": cb["rows_per_s"], **host},
+        "ops": sweep,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,202 @@
+/*
+ * mimir_hip.h -- C ABI of the MI355X (gfx950) backend for Mimir's fused
+ * elementwise and row-reduction layer path.
+ *
+ * The library (libmimir_hip.so) replaces the CPU forward entry points listed
+ * next to each function below (file:line in brit45/mimir-framework).  All
+ * tensors are fp32 (ids int32), row-major and contiguous, and live in device
+ * memory: every `float*` / `int32_t*` argument of an op is a DEVICE pointer
+ * (from mimir_malloc, hipMalloc or any other HIP allocation on the context's
+ * device).  Ops never allocate and never synchronise: they enqueue on the
+ * context's stream and return.  Stream order is the only ordering;
+ * mimir_sync() and the download copy are the blocking calls.
+ *
+ * Status codes: every function returns MIMIR_OK or one of the codes below.
+ * Argument errors are detected on the host before anything is enqueued (the
+ * cases where the reference throws std::runtime_error), and the message is
+ * available from mimir_last_error(ctx).
+ *
+ * Threading: one context per host thread; a context is not safe for
+ * concurrent use without external locking.
+ */
+#ifndef MIMIR_HIP_H
+#define MIMIR_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MIMIR_OK 0
+#define MIMIR_EINVAL 1  /* invalid shape / argument; the reference throws here */
+#define MIMIR_ENOMEM 2  /* device allocation failed or exceeded the context cap */
+#define MIMIR_EDEVICE 3 /* HIP runtime error or no usable device */
+
+typedef struct mimir_ctx mimir_ctx;
+typedef struct mimir_event mimir_event;
+
+/* ---------------------------------------------------------------------------
+ * Context, memory, ordering.  These replace the host-side storage the
+ * reference ops read and write (std::vector<float> activations in
+ * Model::tensor_store, Model.hpp:608-610; weight blocks via Layer::getWeights,
+ * Layers.hpp:232-240; RuntimeAllocator::allocate_tensor,
+ * RuntimeAllocator.hpp:191-226) with device-resident buffers.
+ * ------------------------------------------------------------------------- */
+
+/* Create a context on HIP device `device` with its own (default-priority)
+ * stream. */
+int mimir_ctx_create(int device, mimir_ctx** out);
+int mimir_ctx_destroy(mimir_ctx* ctx);
+/* Enqueue on an existing HIP stream (hipStream_t passed as void*) instead of
+ * the context's own; NULL restores the context's stream. */
+int mimir_ctx_set_stream(mimir_ctx* ctx, void* hip_stream);
+void* mimir_ctx_stream(mimir_ctx* ctx);
+/* Cap on the bytes mimir_malloc may hold at once (0 = no cap).  Mirrors
+ * MemoryGuard::setLimit (MemoryGuard.hpp:75-130): over the cap -> ENOMEM. */
+int mimir_ctx_set_alloc_limit(mimir_ctx* ctx, size_t bytes);
+/* Message for the last non-OK status returned on this context. */
+const char* mimir_last_error(const mimir_ctx* ctx);
+
+int mimir_malloc(mimir_ctx* ctx, size_t bytes, void** dptr);
+int mimir_free(mimir_ctx* ctx, void* dptr);
+/* Stream-ordered copies.  Upload returns once the source may be reused;
+ * download returns once the data is on the host. */
+int mimir_upload(mimir_ctx* ctx, void* dst_dev, const void* src_host, size_t bytes);
+int mimir_download(mimir_ctx* ctx, void* dst_host, const void* src_dev, size_t bytes);
+/* Device-to-device copy (a plain streaming-copy kernel; n bytes, any alignment). */
+int mimir_copy(mimir_ctx* ctx, void* dst_dev, const void* src_dev, size_t bytes);
+/* Fill `n` floats with `value` (a fill kernel, so it is safe under graph capture). */
+int mimir_fill_f32(mimir_ctx* ctx, float* dst_dev, int64_t n, float value);
+int mimir_sync(mimir_ctx* ctx);
+
+/* Stream-ordered timing events on the context's current stream. */
+int mimir_event_create(mimir_ctx* ctx, mimir_event** out);
+int mimir_event_destroy(mimir_event* ev);
+int mimir_event_record(mimir_ctx* ctx, mimir_event* ev);
+/* Milliseconds between two recorded events (waits for `stop`). */
+int mimir_event_elapsed_ms(mimir_event* start, mimir_event* stop, float* ms);
+
+/* ---------------------------------------------------------------------------
+ * Normalisation
+ * ------------------------------------------------------------------------- */
+
+/* LayerOps::layernorm_forward, LayerOps.hpp:264-319.
+ * x and y hold `groups * n` floats; each group of n is normalised with the
+ * two-pass mean / variance: y = (x - mean) / sqrt(var + eps) [* gamma[i]
+ * [+ beta[i]]].  gamma == NULL is the non-affine layer; beta == NULL is
+ * use_bias == false; beta without gamma is EINVAL (the reference adds the
+ * bias only inside the affine branch).  The reference's group size is
+ * `in_features > 0 ? in_features : N`; n <= 0 is EINVAL.  y may alias x. */
+int mimir_layernorm_fwd(mimir_ctx* ctx, const float* x, const float* gamma, const float* beta,
+                        float* y, int64_t groups, int64_t n, float eps);
+
+/* RMSNorm over `rows` rows of `cols`: y = x / sqrt(sum(x^2)/cols + eps) * w[c].
+ * rows == 1, cols == N is the reference layer LayerOpsExt::rms_norm_forward
+ * (LayerOpsExt.hpp:345-378), which normalises the WHOLE input as one group
+ * and multiplies element c by w[c] only while c < w_len.  rows > 1 is the
+ * per-row form Normalization::rms_norm (Layers.hpp:1003-1021), with
+ * w_len == cols.  w == NULL (or w_len == 0) -> no scale.  y may alias x. */
+int mimir_rmsnorm_fwd(mimir_ctx* ctx, const float* x, const float* w, int64_t w_len, float* y,
+                      int64_t rows, int64_t cols, float eps);
+
+/* Residual add fused with per-row RMSNorm, one HBM pass:
+ *   h = x + residual   (LayerOps::add_forward, LayerOps.hpp:142-169)
+ *   residual_out = h;  y = h / sqrt(sum(h^2)/cols + eps) * w[c]
+ *                      (Normalization::rms_norm, Layers.hpp:1003-1021).
+ * The reference has no fused op; it runs the two calls back to back.
+ * residual_out may alias residual (in-place residual update); y must not
+ * alias residual_out.  w may be NULL. */
+int mimir_add_rmsnorm_fwd(mimir_ctx* ctx, const float* x, const float* residual,
+                          float* residual_out, const float* w, float* y, int64_t rows,
+                          int64_t cols, float eps);
+
+/* ---------------------------------------------------------------------------
+ * Softmax
+ * ------------------------------------------------------------------------- */
+
+/* y[j] = e[j] / (sum + 1e-9f): LayerOps::softmax_inplace, LayerOps.hpp:952-974
+ * (the row softmax used by attention). */
+#define MIMIR_SOFTMAX_DIV_EPS 0
+/* y[j] = e[j] * (1.0f / sum): LayerOps::softmax_forward, LayerOps.hpp:325-361
+ * (the Softmax layer; the layer itself is rows == 1, cols == N). */
+#define MIMIR_SOFTMAX_MUL_INV 1
+/* y[j] = (x[j] - max) - log(sum): LogSoftmax branch, LayerOps.hpp:345-353. */
+#define MIMIR_SOFTMAX_LOG 2
+
+/* Max-subtracted softmax of each of `rows` rows of `cols` (cols >= 1), with
+ * e[j] = exp(x[j] - max).  -inf entries give exactly 0.  y may alias x. */
+int mimir_softmax_fwd(mimir_ctx* ctx, const float* x, float* y, int64_t rows, int64_t cols,
+                      int mode);
+
+/* ---------------------------------------------------------------------------
+ * Elementwise
+ * ------------------------------------------------------------------------- */
+
+/* LayerOps::gelu_forward, LayerOps.hpp:556-568 (tanh form):
+ * y = x * 0.5f*(1 + tanh(sqrt(2/pi)*(x + 0.044715f*x^3))).  y may alias x. */
+int mimir_gelu_fwd(mimir_ctx* ctx, const float* x, float* y, int64_t n);
+/* LayerOps::silu_forward, LayerOps.hpp:570-581: y = x * (1/(1+exp(-x))). */
+int mimir_silu_fwd(mimir_ctx* ctx, const float* x, float* y, int64_t n);
+/* SiLU-gated product in one pass: y = silu(gate) * up, i.e.
+ * multiply_forward(silu_forward(gate), up) (LayerOps.hpp:570-581, 205-230). */
+int mimir_silu_mul_fwd(mimir_ctx* ctx, const float* gate, const float* up, float* y, int64_t n);
+/* GELU-gated product: multiply_forward(gelu_forward(gate), up). */
+int mimir_gelu_mul_fwd(mimir_ctx* ctx, const float* gate, const float* up, float* y, int64_t n);
+/* LayerOps::add_forward, LayerOps.hpp:142-199.  Output has max(na, nb) floats:
+ * equal sizes -> elementwise; the shorter operand of size 1 -> scalar
+ * broadcast; the longer size a multiple of the shorter -> repeat
+ * (y[i] = big[i] + small[i % small_n]); otherwise EINVAL; either size 0 ->
+ * EINVAL.  Bit-identical to the reference (one IEEE add per element). */
+int mimir_add_fwd(mimir_ctx* ctx, const float* a, int64_t na, const float* b, int64_t nb,
+                  float* y);
+/* LayerOps::multiply_forward, LayerOps.hpp:205-230: na != nb -> EINVAL. */
+int mimir_mul_fwd(mimir_ctx* ctx, const float* a, int64_t na, const float* b, int64_t nb,
+                  float* y);
+
+/* ---------------------------------------------------------------------------
+ * Embedding gather and rotary position embedding
+ * ------------------------------------------------------------------------- */
+
+/* Token-embedding gather, inline in Model::forwardPassView (int ids),
+ * Model.cpp:1152-1205.  vocab and dim are clamped to >= 1 (Model.cpp:1176-1177);
+ * table_len < vocab*dim is EINVAL (:1181-1182).  y is [n_ids x dim]; the row of
+ * an id equal to padding_idx (when padding_idx >= 0) or outside [0, vocab) is
+ * all zeros (silently, as in the reference); every other row is a bit-exact
+ * copy of table[id]. */
+int mimir_embedding_fwd(mimir_ctx* ctx, const int32_t* ids, int64_t n_ids, const float* table,
+                        int64_t table_len, int32_t vocab, int32_t dim, int32_t padding_idx,
+                        float* y);
+/* Float-id form, Model.cpp:5301-5334: id = (int) llround((double) ids[t]),
+ * including the x86-64 conversion of non-finite / huge values (id 0) and
+ * the wrap of the 64-bit result to int. */
+int mimir_embedding_f32ids_fwd(mimir_ctx* ctx, const float* ids, int64_t n_ids,
+                               const float* table, int64_t table_len, int32_t vocab, int32_t dim,
+                               int32_t padding_idx, float* y);
+
+/* Host-side rotary table (the reference has no RoPE): for p in [0, rows),
+ * i in [0, head_dim/2): inv_freq = 1 / theta^(2i/head_dim), a = p*inv_freq in
+ * double; cos_tab/sin_tab[p*head_dim/2 + i] = (float)cos(a) / (float)sin(a).
+ * cos_tab and sin_tab are HOST arrays of rows*head_dim/2 floats. */
+int mimir_rope_table(int64_t rows, int64_t head_dim, double theta, float* cos_tab,
+                     float* sin_tab);
+
+/* Rotate-half RoPE on q and k in one launch, both laid out
+ * [batch, seq, heads, head_dim] (k may have its own head count k_heads;
+ * k == NULL skips it).  For position p = pos_offset + s and pair i < D/2:
+ *   y[i]     = x[i]*cos[p,i] - x[i+D/2]*sin[p,i]
+ *   y[i+D/2] = x[i+D/2]*cos[p,i] + x[i]*sin[p,i]
+ * cos_tab / sin_tab are DEVICE tables of table_rows x D/2 (mimir_rope_table);
+ * pos_offset + seq > table_rows is EINVAL.  head_dim must be even.
+ * q_out may alias q and k_out may alias k (in place). */
+int mimir_rope_fwd(mimir_ctx* ctx, const float* q, float* q_out, int64_t q_heads, const float* k,
+                   float* k_out, int64_t k_heads, int64_t batch, int64_t seq, int64_t head_dim,
+                   int64_t pos_offset, const float* cos_tab, const float* sin_tab,
+                   int64_t table_rows);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MIMIR_HIP_H */

@@ -1,0 +1,113 @@
+// common.hpp -- device helpers shared by the gfx950 kernels of libmimir_hip.
+//
+// Wave64 throughout.  Reductions run inside one wavefront with DPP lane moves
+// (quad_perm, row_half_mirror, row_mirror) and finish with four readlanes, so
+// the reduced value is wave-uniform (held in an SGPR) and bitwise identical
+// for every lane.  LDS is used only to combine the per-wave partials of a
+// multi-wave row.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace mimir {
+
+constexpr int kWave = 64;
+constexpr int kBlock = 256;  // every kernel here launches 256-thread workgroups
+
+typedef float f4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u4 __attribute__((ext_vector_type(4)));
+
+// ---------------------------------------------------------------------------
+// memory: 128-bit global accesses.  `nt` selects the non-temporal variants
+// (the data is streamed once; keep it out of the way of reused lines).
+// ---------------------------------------------------------------------------
+template <bool NT>
+__device__ __forceinline__ f4 ld4(const float* p) {
+    if constexpr (NT) return __builtin_nontemporal_load(reinterpret_cast<const f4*>(p));
+    else return *reinterpret_cast<const f4*>(p);
+}
+
+template <bool NT>
+__device__ __forceinline__ void st4(float* p, f4 v) {
+    if constexpr (NT) __builtin_nontemporal_store(v, reinterpret_cast<f4*>(p));
+    else *reinterpret_cast<f4*>(p) = v;
+}
+
+// ---------------------------------------------------------------------------
+// DPP wave reductions
+// ---------------------------------------------------------------------------
+enum : int {
+    kDppQuadXor1 = 0xB1,      // quad_perm [1,0,3,2]
+    kDppQuadXor2 = 0x4E,      // quad_perm [2,3,0,1]
+    kDppRowHalfMirror = 0x141,
+    kDppRowMirror = 0x140,
+};
+
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+    return __builtin_bit_cast(
+        float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+
+__device__ __forceinline__ float readlane(float v, int lane) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
+}
+
+// Sum over the 64 lanes.  Every lane of a 16-lane row first holds its row
+// sum (4 DPP steps), then the four row sums are combined in a fixed order.
+__device__ __forceinline__ float wave_sum(float v) {
+    v += dpp<kDppQuadXor1>(v);
+    v += dpp<kDppQuadXor2>(v);
+    v += dpp<kDppRowHalfMirror>(v);
+    v += dpp<kDppRowMirror>(v);
+    return (readlane(v, 0) + readlane(v, 16)) + (readlane(v, 32) + readlane(v, 48));
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+    v = fmaxf(v, dpp<kDppQuadXor1>(v));
+    v = fmaxf(v, dpp<kDppQuadXor2>(v));
+    v = fmaxf(v, dpp<kDppRowHalfMirror>(v));
+    v = fmaxf(v, dpp<kDppRowMirror>(v));
+    return fmaxf(fmaxf(readlane(v, 0), readlane(v, 16)), fmaxf(readlane(v, 32), readlane(v, 48)));
+}
+
+// Block-wide reductions for rows spread over NW waves.  `lds` must hold NW
+// floats and not be reused by another reduction until the caller syncs again
+// (each call ends with every thread having read the partials; the leading
+// barrier of the next call orders the reuse).
+template <int NW>
+__device__ __forceinline__ float block_sum(float v, float* lds) {
+    const float w = wave_sum(v);
+    if constexpr (NW == 1) {
+        return w;
+    } else {
+        const int wid = threadIdx.x / kWave;
+        __syncthreads();
+        if ((threadIdx.x & (kWave - 1)) == 0) lds[wid] = w;
+        __syncthreads();
+        float s = lds[0];
+#pragma unroll
+        for (int i = 1; i < NW; ++i) s += lds[i];
+        return s;
+    }
+}
+
+template <int NW>
+__device__ __forceinline__ float block_max(float v, float* lds) {
+    const float w = wave_max(v);
+    if constexpr (NW == 1) {
+        return w;
+    } else {
+        const int wid = threadIdx.x / kWave;
+        __syncthreads();
+        if ((threadIdx.x & (kWave - 1)) == 0) lds[wid] = w;
+        __syncthreads();
+        float s = lds[0];
+#pragma unroll
+        for (int i = 1; i < NW; ++i) s = fmaxf(s, lds[i]);
+        return s;
+    }
+}
+
+}  // namespace mimir

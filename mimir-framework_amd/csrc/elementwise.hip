@@ -1,0 +1,290 @@
+// elementwise.hip -- GELU, SiLU, gated products, add (with the reference's
+// broadcast rules) and multiply for gfx950.
+//
+// Streaming layout: each thread owns VPT 16-byte vectors spaced one
+// workgroup-width apart (so each wave instruction moves 1 KiB of contiguous
+// data), issues all its loads before any arithmetic, and writes with
+// non-temporal stores: every input byte is read once and every output byte
+// written once.  Buffers that are not 16-byte aligned, and the n % 4 tail,
+// run through a scalar grid-stride kernel with the same per-element functor.
+#include "common.hpp"
+#include "internal.hpp"
+
+#include <math.h>
+
+using namespace mimir;
+
+namespace {
+
+// LayerOps::gelu_forward, LayerOps.hpp:556-568.  The constant is the float
+// sqrt of the float quotient, as in the reference (correctly rounded sqrt).
+__device__ __forceinline__ float gelu1(float x) {
+    const float k = __builtin_sqrtf(2.0f / 3.14159265359f);
+    const float cdf = 0.5f * (1.0f + tanhf(k * (x + 0.044715f * x * x * x)));
+    return x * cdf;
+}
+
+// LayerOps::silu_forward, LayerOps.hpp:570-581.
+__device__ __forceinline__ float silu1(float x) {
+    const float sigmoid = 1.0f / (1.0f + expf(-x));
+    return x * sigmoid;
+}
+
+struct Gelu {
+    __device__ float operator()(float x) const { return gelu1(x); }
+};
+struct Silu {
+    __device__ float operator()(float x) const { return silu1(x); }
+};
+// multiply_forward(silu_forward(gate), up): LayerOps.hpp:570-581 then :205-230.
+struct SiluMul {
+    __device__ float operator()(float g, float u) const { return silu1(g) * u; }
+};
+// multiply_forward(gelu_forward(gate), up).
+struct GeluMul {
+    __device__ float operator()(float g, float u) const { return gelu1(g) * u; }
+};
+struct Add {
+    __device__ float operator()(float a, float b) const { return a + b; }
+};
+struct Mul {
+    __device__ float operator()(float a, float b) const { return a * b; }
+};
+
+constexpr int kVpt = 4;  // 16-byte vectors per thread (64 B of each input in flight)
+
+template <class F>
+__device__ __forceinline__ f4 map4(F f, f4 a) {
+    return f4{f(a.x), f(a.y), f(a.z), f(a.w)};
+}
+template <class F>
+__device__ __forceinline__ f4 map4(F f, f4 a, f4 b) {
+    return f4{f(a.x, b.x), f(a.y, b.y), f(a.z, b.z), f(a.w, b.w)};
+}
+
+template <class F, int VPT>
+__global__ __launch_bounds__(kBlock) void unary_vec(const float* x, float* y, int64_t n4, F f) {
+    const int64_t first = static_cast<int64_t>(blockIdx.x) * VPT * kBlock + threadIdx.x;
+    f4 v[VPT];
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) {
+        const int64_t i = first + static_cast<int64_t>(j) * kBlock;
+        if (i < n4) v[j] = ld4<true>(x + 4 * i);
+    }
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) {
+        const int64_t i = first + static_cast<int64_t>(j) * kBlock;
+        if (i < n4) st4<true>(y + 4 * i, map4(f, v[j]));
+    }
+}
+
+template <class F, int VPT>
+__global__ __launch_bounds__(kBlock) void binary_vec(const float* a, const float* b, float* y,
+                                                     int64_t n4, F f) {
+    const int64_t first = static_cast<int64_t>(blockIdx.x) * VPT * kBlock + threadIdx.x;
+    f4 va[VPT], vb[VPT];
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) {
+        const int64_t i = first + static_cast<int64_t>(j) * kBlock;
+        if (i < n4) {
+            va[j] = ld4<true>(a + 4 * i);
+            vb[j] = ld4<true>(b + 4 * i);
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) {
+        const int64_t i = first + static_cast<int64_t>(j) * kBlock;
+        if (i < n4) st4<true>(y + 4 * i, map4(f, va[j], vb[j]));
+    }
+}
+
+template <class F>
+__global__ __launch_bounds__(kBlock) void unary_scalar(const float* x, float* y, int64_t n, F f) {
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * kBlock;
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x; i < n; i += stride)
+        y[i] = f(x[i]);
+}
+
+template <class F>
+__global__ __launch_bounds__(kBlock) void binary_scalar(const float* a, const float* b, float* y,
+                                                        int64_t n, F f) {
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * kBlock;
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x; i < n; i += stride)
+        y[i] = f(a[i], b[i]);
+}
+
+// add_forward scalar broadcast, LayerOps.hpp:181-188: y[i] = big[i] + small[0].
+__global__ __launch_bounds__(kBlock) void add_scalar_kernel(const float* big, const float* small,
+                                                            float* y, int64_t n) {
+    const float s = small[0];
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * kBlock;
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x; i < n; i += stride)
+        y[i] = big[i] + s;
+}
+
+// add_forward repeat broadcast, LayerOps.hpp:194-197: y[i] = big[i] + small[i % small_n],
+// as `rows` rows of small_n.  Each thread keeps its 16 bytes of `small` in
+// registers and walks the rows (blockIdx.y strided).
+__global__ __launch_bounds__(kBlock) void add_repeat_vec(const float* big, const float* small,
+                                                         float* y, int64_t rows, int64_t small_n4) {
+    const int64_t c4 = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
+    if (c4 >= small_n4) return;
+    const f4 s = *reinterpret_cast<const f4*>(small + 4 * c4);
+    for (int64_t r = blockIdx.y; r < rows; r += gridDim.y) {
+        const int64_t i = r * small_n4 + c4;
+        st4<true>(y + 4 * i, ld4<true>(big + 4 * i) + s);
+    }
+}
+
+__global__ __launch_bounds__(kBlock) void add_repeat_scalar(const float* big, const float* small,
+                                                            float* y, int64_t n, int64_t small_n) {
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * kBlock;
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x; i < n; i += stride)
+        y[i] = big[i] + small[i % small_n];
+}
+
+unsigned stride_grid(int64_t n) {
+    const int64_t b = (n + kBlock - 1) / kBlock;
+    return static_cast<unsigned>(b < 1 ? 1 : (b > 65536 ? 65536 : b));
+}
+
+template <class F>
+int run_unary(mimir_ctx* ctx, const float* x, float* y, int64_t n, F f, const char* name) {
+    int64_t done = 0;
+    if (aligned16(x) && aligned16(y)) {
+        const int64_t n4 = n / 4;
+        if (n4 > 0) {
+            unsigned blocks;
+            if (!grid_for(n4, static_cast<int64_t>(kVpt) * kBlock, &blocks))
+                return fail(ctx, MIMIR_EINVAL, "%s: n=%lld exceeds the grid limit", name, (long long)n);
+            unary_vec<F, kVpt><<<blocks, kBlock, 0, ctx->stream>>>(x, y, n4, f);
+            if (int st = launched(ctx, name)) return st;
+        }
+        done = n4 * 4;
+    }
+    if (n > done) {
+        unary_scalar<F><<<stride_grid(n - done), kBlock, 0, ctx->stream>>>(x + done, y + done, n - done, f);
+        return launched(ctx, name);
+    }
+    return MIMIR_OK;
+}
+
+template <class F>
+int run_binary(mimir_ctx* ctx, const float* a, const float* b, float* y, int64_t n, F f,
+               const char* name) {
+    int64_t done = 0;
+    if (aligned16(a) && aligned16(b) && aligned16(y)) {
+        const int64_t n4 = n / 4;
+        if (n4 > 0) {
+            unsigned blocks;
+            if (!grid_for(n4, static_cast<int64_t>(kVpt) * kBlock, &blocks))
+                return fail(ctx, MIMIR_EINVAL, "%s: n=%lld exceeds the grid limit", name, (long long)n);
+            binary_vec<F, kVpt><<<blocks, kBlock, 0, ctx->stream>>>(a, b, y, n4, f);
+            if (int st = launched(ctx, name)) return st;
+        }
+        done = n4 * 4;
+    }
+    if (n > done) {
+        binary_scalar<F><<<stride_grid(n - done), kBlock, 0, ctx->stream>>>(a + done, b + done, y + done,
+                                                                          n - done, f);
+        return launched(ctx, name);
+    }
+    return MIMIR_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int mimir_gelu_fwd(mimir_ctx* ctx, const float* x, float* y, int64_t n) {
+    if (!ctx) return MIMIR_EINVAL;
+    MIMIR_REQUIRE(ctx, n >= 0, "GELU: n < 0");
+    if (n == 0) return MIMIR_OK;
+    MIMIR_REQUIRE(ctx, x && y, "GELU: null tensor");
+    MIMIR_ENTER(ctx);
+    return run_unary(ctx, x, y, n, Gelu{}, "gelu");
+}
+
+int mimir_silu_fwd(mimir_ctx* ctx, const float* x, float* y, int64_t n) {
+    if (!ctx) return MIMIR_EINVAL;
+    MIMIR_REQUIRE(ctx, n >= 0, "SiLU: n < 0");
+    if (n == 0) return MIMIR_OK;
+    MIMIR_REQUIRE(ctx, x && y, "SiLU: null tensor");
+    MIMIR_ENTER(ctx);
+    return run_unary(ctx, x, y, n, Silu{}, "silu");
+}
+
+int mimir_silu_mul_fwd(mimir_ctx* ctx, const float* gate, const float* up, float* y, int64_t n) {
+    if (!ctx) return MIMIR_EINVAL;
+    MIMIR_REQUIRE(ctx, n >= 0, "SiLU*up: n < 0");
+    if (n == 0) return MIMIR_OK;
+    MIMIR_REQUIRE(ctx, gate && up && y, "SiLU*up: null tensor");
+    MIMIR_ENTER(ctx);
+    return run_binary(ctx, gate, up, y, n, SiluMul{}, "silu_mul");
+}
+
+int mimir_gelu_mul_fwd(mimir_ctx* ctx, const float* gate, const float* up, float* y, int64_t n) {
+    if (!ctx) return MIMIR_EINVAL;
+    MIMIR_REQUIRE(ctx, n >= 0, "GELU*up: n < 0");
+    if (n == 0) return MIMIR_OK;
+    MIMIR_REQUIRE(ctx, gate && up && y, "GELU*up: null tensor");
+    MIMIR_ENTER(ctx);
+    return run_binary(ctx, gate, up, y, n, GeluMul{}, "gelu_mul");
+}
+
+int mimir_add_fwd(mimir_ctx* ctx, const float* a, int64_t na, const float* b, int64_t nb,
+                  float* y) {
+    if (!ctx) return MIMIR_EINVAL;
+    // LayerOps.hpp:150-152: both inputs must be non-empty.
+    MIMIR_REQUIRE(ctx, na > 0 && nb > 0, "Add: inputs must be non-empty");
+    MIMIR_REQUIRE(ctx, a && b && y, "Add: null tensor");
+    if (na == nb) {  // LayerOps.hpp:154-169
+        MIMIR_ENTER(ctx);
+        return run_binary(ctx, a, b, y, na, Add{}, "add");
+    }
+    const float* big = a;
+    const float* small = b;
+    int64_t big_n = na, small_n = nb;
+    if (nb > na) {  // LayerOps.hpp:172-177
+        big = b;
+        small = a;
+        big_n = nb;
+        small_n = na;
+    }
+    MIMIR_REQUIRE(ctx, small_n == 1 || big_n % small_n == 0,
+                  "Add: input sizes must match or be broadcastable (%lld vs %lld)", (long long)na,
+                  (long long)nb);
+    MIMIR_ENTER(ctx);
+    if (small_n == 1) {
+        add_scalar_kernel<<<stride_grid(big_n), kBlock, 0, ctx->stream>>>(big, small, y, big_n);
+        return launched(ctx, "add_scalar_kernel");
+    }
+    const int64_t rows = big_n / small_n;
+    if (small_n % 4 == 0 && aligned16(big) && aligned16(small) && aligned16(y)) {
+        const int64_t small_n4 = small_n / 4;
+        unsigned bx;
+        if (!grid_for(small_n4, kBlock, &bx))
+            return fail(ctx, MIMIR_EINVAL, "Add: operand of %lld exceeds the grid limit", (long long)small_n);
+        // Enough rows per launch to give every CU work; each thread then strides rows.
+        const int64_t want_y = (static_cast<int64_t>(2048) + bx - 1) / bx;
+        const unsigned by = static_cast<unsigned>(rows < want_y ? rows : (want_y > 65535 ? 65535 : want_y));
+        add_repeat_vec<<<dim3(bx, by), kBlock, 0, ctx->stream>>>(big, small, y, rows, small_n4);
+        return launched(ctx, "add_repeat_vec");
+    }
+    add_repeat_scalar<<<stride_grid(big_n), kBlock, 0, ctx->stream>>>(big, small, y, big_n, small_n);
+    return launched(ctx, "add_repeat_scalar");
+}
+
+int mimir_mul_fwd(mimir_ctx* ctx, const float* a, int64_t na, const float* b, int64_t nb,
+                  float* y) {
+    if (!ctx) return MIMIR_EINVAL;
+    // LayerOps.hpp:209-211
+    MIMIR_REQUIRE(ctx, na == nb && na >= 0, "Multiply: input sizes must match (%lld vs %lld)",
+                  (long long)na, (long long)nb);
+    if (na == 0) return MIMIR_OK;
+    MIMIR_REQUIRE(ctx, a && b && y, "Multiply: null tensor");
+    MIMIR_ENTER(ctx);
+    return run_binary(ctx, a, b, y, na, Mul{}, "mul");
+}
+
+}  // extern "C"

@@ -1,0 +1,136 @@
+// gather.hip -- token-embedding gather for gfx950 (bit-exact).
+//
+// One wavefront per token row: the id is read once per wave (wave-uniform),
+// then the 64 lanes move the row as 16-byte vectors, VPT per lane, loads
+// issued before stores.  Rows of padding / out-of-range ids are written as
+// zeros without touching the table.  Payload moves as raw 32-bit words, so
+// every bit pattern (NaN payloads, -0, denormals) is copied unchanged.
+//
+// Semantics: Model::forwardPassView inline gather, Model.cpp:1152-1205 (int
+// ids) and Model.cpp:5301-5334 (float ids rounded with llround).
+#include "common.hpp"
+#include "internal.hpp"
+
+#include <math.h>
+
+using namespace mimir;
+
+namespace {
+
+// static_cast<int>(std::llround(static_cast<double>(f))) as compiled for
+// x86-64 with glibc (Model.cpp:5321): llround rounds half away from zero;
+// values whose magnitude reaches 2^63, and NaN, convert to the x86 "integer
+// indefinite" 0x8000000000000000, whose low 32 bits are 0; the 64-bit result
+// is then narrowed to int by keeping its low 32 bits.
+__device__ __forceinline__ int32_t float_id(float f) {
+    const double d = static_cast<double>(f);
+    if (!(fabs(d) < 9223372036854775808.0)) return 0;
+    const long long r = static_cast<long long>(round(d));
+    return static_cast<int32_t>(static_cast<uint32_t>(static_cast<unsigned long long>(r)));
+}
+
+template <bool FLOAT_IDS>
+__device__ __forceinline__ int32_t load_id(const void* ids, int64_t t) {
+    if constexpr (FLOAT_IDS) return float_id(static_cast<const float*>(ids)[t]);
+    else return static_cast<const int32_t*>(ids)[t];
+}
+
+struct GatherArgs {
+    const void* ids;
+    int64_t n_ids;
+    const float* table;
+    int32_t vocab;
+    int32_t dim;
+    int32_t pad;
+    float* y;
+};
+
+constexpr int kWavesPerBlock = kBlock / kWave;
+
+template <bool FLOAT_IDS, int VPT>
+__global__ __launch_bounds__(kBlock) void embed_vec(GatherArgs a) {
+    const int lane = threadIdx.x & (kWave - 1);
+    const int64_t token = static_cast<int64_t>(blockIdx.x) * kWavesPerBlock + threadIdx.x / kWave;
+    if (token >= a.n_ids) return;
+    const int32_t id = load_id<FLOAT_IDS>(a.ids, token);
+    const bool copy = !(a.pad >= 0 && id == a.pad) && id >= 0 && id < a.vocab;
+    const int64_t dim4 = a.dim >> 2;
+    const u4* src = reinterpret_cast<const u4*>(a.table) + (copy ? static_cast<int64_t>(id) * dim4 : 0);
+    u4* dst = reinterpret_cast<u4*>(a.y) + token * dim4;
+    for (int64_t c0 = 0; c0 < dim4; c0 += static_cast<int64_t>(VPT) * kWave) {
+        u4 v[VPT];
+#pragma unroll
+        for (int j = 0; j < VPT; ++j) {
+            const int64_t c = c0 + static_cast<int64_t>(j) * kWave + lane;
+            v[j] = (copy && c < dim4) ? __builtin_nontemporal_load(src + c) : u4(0u);
+        }
+#pragma unroll
+        for (int j = 0; j < VPT; ++j) {
+            const int64_t c = c0 + static_cast<int64_t>(j) * kWave + lane;
+            if (c < dim4) __builtin_nontemporal_store(v[j], dst + c);
+        }
+    }
+}
+
+// Any dim / alignment: one wavefront per token, 32-bit words.
+template <bool FLOAT_IDS>
+__global__ __launch_bounds__(kBlock) void embed_scalar(GatherArgs a) {
+    const int lane = threadIdx.x & (kWave - 1);
+    const int64_t token = static_cast<int64_t>(blockIdx.x) * kWavesPerBlock + threadIdx.x / kWave;
+    if (token >= a.n_ids) return;
+    const int32_t id = load_id<FLOAT_IDS>(a.ids, token);
+    const bool copy = !(a.pad >= 0 && id == a.pad) && id >= 0 && id < a.vocab;
+    const uint32_t* src = reinterpret_cast<const uint32_t*>(a.table) +
+                          (copy ? static_cast<int64_t>(id) * a.dim : 0);
+    uint32_t* dst = reinterpret_cast<uint32_t*>(a.y) + token * a.dim;
+    for (int64_t c = lane; c < a.dim; c += kWave) dst[c] = copy ? src[c] : 0u;
+}
+
+template <bool FLOAT_IDS>
+int run(mimir_ctx* ctx, const void* ids, int64_t n_ids, const float* table, int64_t table_len,
+        int32_t vocab, int32_t dim, int32_t pad, float* y) {
+    MIMIR_REQUIRE(ctx, n_ids >= 0, "Embedding: n_ids < 0");
+    // Model.cpp:1176-1177: vocab and dim are clamped to at least 1.
+    vocab = vocab < 1 ? 1 : vocab;
+    dim = dim < 1 ? 1 : dim;
+    // Model.cpp:1181-1182: the table must hold vocab*dim floats.
+    MIMIR_REQUIRE(ctx, table_len >= static_cast<int64_t>(vocab) * dim,
+                  "Embedding: invalid weight size (%lld < %d x %d)", (long long)table_len, vocab, dim);
+    if (n_ids == 0) return MIMIR_OK;
+    MIMIR_REQUIRE(ctx, ids && table && y, "Embedding: null tensor");
+    MIMIR_ENTER(ctx);
+    const GatherArgs a{ids, n_ids, table, vocab, dim, pad, y};
+    unsigned blocks;
+    if (!grid_for(n_ids, kWavesPerBlock, &blocks))
+        return fail(ctx, MIMIR_EINVAL, "Embedding: %lld ids exceed the grid limit", (long long)n_ids);
+    if (dim % 4 == 0 && aligned16(table) && aligned16(y)) {
+        const int64_t dim4 = dim / 4;
+        if (dim4 <= 64) embed_vec<FLOAT_IDS, 1><<<blocks, kBlock, 0, ctx->stream>>>(a);
+        else if (dim4 <= 256) embed_vec<FLOAT_IDS, 4><<<blocks, kBlock, 0, ctx->stream>>>(a);
+        else if (dim4 <= 512) embed_vec<FLOAT_IDS, 8><<<blocks, kBlock, 0, ctx->stream>>>(a);
+        else embed_vec<FLOAT_IDS, 16><<<blocks, kBlock, 0, ctx->stream>>>(a);
+        return launched(ctx, "embed_vec");
+    }
+    embed_scalar<FLOAT_IDS><<<blocks, kBlock, 0, ctx->stream>>>(a);
+    return launched(ctx, "embed_scalar");
+}
+
+}  // namespace
+
+extern "C" {
+
+int mimir_embedding_fwd(mimir_ctx* ctx, const int32_t* ids, int64_t n_ids, const float* table,
+                        int64_t table_len, int32_t vocab, int32_t dim, int32_t padding_idx,
+                        float* y) {
+    if (!ctx) return MIMIR_EINVAL;
+    return run<false>(ctx, ids, n_ids, table, table_len, vocab, dim, padding_idx, y);
+}
+
+int mimir_embedding_f32ids_fwd(mimir_ctx* ctx, const float* ids, int64_t n_ids,
+                               const float* table, int64_t table_len, int32_t vocab, int32_t dim,
+                               int32_t padding_idx, float* y) {
+    if (!ctx) return MIMIR_EINVAL;
+    return run<true>(ctx, ids, n_ids, table, table_len, vocab, dim, padding_idx, y);
+}
+
+}  // extern "C"

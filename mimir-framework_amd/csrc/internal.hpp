@@ -1,0 +1,90 @@
+// internal.hpp -- host-side context and status plumbing shared by the
+// translation units of libmimir_hip (not part of the public ABI).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdint>
+#include <cstdio>
+#include <string>
+#include <unordered_map>
+
+#include "../../include/mimir_hip.h"
+
+struct mimir_ctx {
+    int device = 0;
+    hipStream_t own_stream = nullptr;
+    hipStream_t stream = nullptr;  // where ops are enqueued
+    size_t alloc_limit = 0;        // 0 = unlimited
+    size_t alloc_used = 0;
+    std::unordered_map<void*, size_t> allocs;
+    std::string last_error;
+};
+
+struct mimir_event {
+    hipEvent_t ev = nullptr;
+    int device = 0;
+};
+
+namespace mimir {
+
+// Record a message on the context and return `code`.
+inline int fail(mimir_ctx* ctx, int code, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    std::vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    if (ctx) ctx->last_error = buf;
+    return code;
+}
+
+inline int hip_fail(mimir_ctx* ctx, hipError_t e, const char* what) {
+    return fail(ctx, MIMIR_EDEVICE, "%s: %s", what, hipGetErrorString(e));
+}
+
+// Make the context's device current for this host thread.
+inline int enter(mimir_ctx* ctx) {
+    if (!ctx) return MIMIR_EINVAL;
+    int cur = -1;
+    hipError_t e = hipGetDevice(&cur);
+    if (e != hipSuccess) return hip_fail(ctx, e, "hipGetDevice");
+    if (cur != ctx->device) {
+        e = hipSetDevice(ctx->device);
+        if (e != hipSuccess) return hip_fail(ctx, e, "hipSetDevice");
+    }
+    return MIMIR_OK;
+}
+
+// Status of the launch just enqueued.
+inline int launched(mimir_ctx* ctx, const char* kernel) {
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return hip_fail(ctx, e, kernel);
+    return MIMIR_OK;
+}
+
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// Number of 256-thread blocks for `units` work items of `per_block` each,
+// refusing grids beyond the 32-bit grid limit.
+inline bool grid_for(int64_t units, int64_t per_block, unsigned* blocks) {
+    const int64_t b = (units + per_block - 1) / per_block;
+    if (b <= 0 || b > 0x7fffffffLL) return false;
+    *blocks = static_cast<unsigned>(b);
+    return true;
+}
+
+}  // namespace mimir
+
+#define MIMIR_ENTER(ctx)                         \
+    do {                                         \
+        if (!(ctx)) return MIMIR_EINVAL;         \
+        const int _st = ::mimir::enter(ctx);     \
+        if (_st != MIMIR_OK) return _st;         \
+    } while (0)
+
+#define MIMIR_REQUIRE(ctx, cond, ...)                                   \
+    do {                                                                \
+        if (!(cond)) return ::mimir::fail((ctx), MIMIR_EINVAL, __VA_ARGS__); \
+    } while (0)

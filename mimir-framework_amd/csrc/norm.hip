@@ -1,0 +1,269 @@
+// norm.hip -- LayerNorm, RMSNorm and residual-add + RMSNorm for gfx950.
+//
+// Row layout: a row of `cols` fp32 is held in VGPRs by TPR threads (64 = one
+// wavefront, 256 = the whole workgroup), each owning VPT 16-byte vectors at
+// float4 columns t, t+TPR, t+2*TPR, ... so every load instruction of a wave
+// covers 1 KiB of contiguous row.  Each input byte crosses HBM once: the row
+// is loaded, reduced (DPP wave reductions, LDS only for the 4-wave combine)
+// and written from registers.  Rows that do not fit that register budget, or
+// whose width is not a multiple of 4 / whose buffers are not 16-byte aligned,
+// take the generic kernel: one workgroup per row, scalar strided passes.
+//
+// Arithmetic follows the reference step by step:
+//   LayerNorm  LayerOps::layernorm_forward, LayerOps.hpp:264-319
+//              mean = sum/n; var = sum((x-mean)^2)/n (two-pass);
+//              inv_std = 1/sqrt(var+eps); y = (x-mean)*inv_std [*g [+b]]
+//   RMSNorm    LayerOpsExt::rms_norm_forward, LayerOpsExt.hpp:345-378 and
+//              Normalization::rms_norm, Layers.hpp:1003-1021
+//              rms = sqrt(sum(x^2)/n + eps); y = x/rms [*w]
+//   add+RMS    h = x + r (LayerOps::add_forward, LayerOps.hpp:154-169), then
+//              RMSNorm of h; h is also written out (the updated residual).
+#include "common.hpp"
+#include "internal.hpp"
+
+using namespace mimir;
+
+namespace {
+
+enum class Norm { Layer, Rms, AddRms };
+
+struct NormArgs {
+    const float* x;
+    const float* r;   // AddRms: residual in
+    float* r_out;     // AddRms: residual out (x + r)
+    const float* g;   // gamma / weight (may be null)
+    const float* b;   // beta (LayerNorm, may be null)
+    float* y;
+    int64_t rows;
+    int64_t cols;
+    int64_t w_len;    // RMSNorm: weight applies to columns < w_len
+    float eps;
+};
+
+// Scale by the RMSNorm weight where the column is below w_len.
+__device__ __forceinline__ f4 rms_scale(f4 o, const float* w, int64_t w_len, int64_t c) {
+    if (c + 3 < w_len) {
+        const f4 g = *reinterpret_cast<const f4*>(w + c);
+        o *= g;
+    } else {
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+            if (c + k < w_len) o[k] *= w[c + k];
+    }
+    return o;
+}
+
+template <Norm K, int TPR, int VPT, bool NT>
+__global__ __launch_bounds__(kBlock) void norm_rows_vec(NormArgs a) {
+    constexpr int RPB = kBlock / TPR;  // rows per workgroup
+    constexpr int NW = TPR / kWave;    // waves per row
+    __shared__ float lds[2][NW];
+    const int t = threadIdx.x % TPR;
+    const int64_t row = static_cast<int64_t>(blockIdx.x) * RPB + threadIdx.x / TPR;
+    if constexpr (NW == 1) {
+        if (row >= a.rows) return;  // whole wavefront leaves together
+    }
+    const int64_t c4n = a.cols >> 2;
+    const int64_t base = row * a.cols;
+
+    f4 v[VPT];
+    if constexpr (K == Norm::AddRms) {
+        f4 rr[VPT];
+#pragma unroll
+        for (int j = 0; j < VPT; ++j) {
+            const int64_t c4 = static_cast<int64_t>(j) * TPR + t;
+            const bool ok = c4 < c4n;
+            v[j] = ok ? ld4<NT>(a.x + base + 4 * c4) : f4(0.0f);
+            rr[j] = ok ? ld4<NT>(a.r + base + 4 * c4) : f4(0.0f);
+        }
+#pragma unroll
+        for (int j = 0; j < VPT; ++j) {
+            const int64_t c4 = static_cast<int64_t>(j) * TPR + t;
+            v[j] = v[j] + rr[j];  // one IEEE add per element, as add_forward
+            if (c4 < c4n) st4<NT>(a.r_out + base + 4 * c4, v[j]);
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < VPT; ++j) {
+            const int64_t c4 = static_cast<int64_t>(j) * TPR + t;
+            v[j] = (c4 < c4n) ? ld4<NT>(a.x + base + 4 * c4) : f4(0.0f);
+        }
+    }
+
+    const float n = static_cast<float>(a.cols);
+    if constexpr (K == Norm::Layer) {
+        float s = 0.0f;
+#pragma unroll
+        for (int j = 0; j < VPT; ++j) s += (v[j].x + v[j].y) + (v[j].z + v[j].w);
+        const float mean = block_sum<NW>(s, lds[0]) / n;
+        float q = 0.0f;
+#pragma unroll
+        for (int j = 0; j < VPT; ++j) {
+            const int64_t c4 = static_cast<int64_t>(j) * TPR + t;
+            if (c4 < c4n) {
+                const f4 d = v[j] - mean;
+                q += (d.x * d.x + d.y * d.y) + (d.z * d.z + d.w * d.w);
+            }
+        }
+        const float var = block_sum<NW>(q, lds[1]) / n;
+        const float inv_std = 1.0f / sqrtf(var + a.eps);
+#pragma unroll
+        for (int j = 0; j < VPT; ++j) {
+            const int64_t c4 = static_cast<int64_t>(j) * TPR + t;
+            if (c4 < c4n) {
+                f4 o = (v[j] - mean) * inv_std;
+                if (a.g) {
+                    o *= *reinterpret_cast<const f4*>(a.g + 4 * c4);
+                    if (a.b) o += *reinterpret_cast<const f4*>(a.b + 4 * c4);
+                }
+                st4<NT>(a.y + base + 4 * c4, o);
+            }
+        }
+    } else {
+        float q = 0.0f;
+#pragma unroll
+        for (int j = 0; j < VPT; ++j)
+            q += (v[j].x * v[j].x + v[j].y * v[j].y) + (v[j].z * v[j].z + v[j].w * v[j].w);
+        const float rms = sqrtf(block_sum<NW>(q, lds[0]) / n + a.eps);
+#pragma unroll
+        for (int j = 0; j < VPT; ++j) {
+            const int64_t c4 = static_cast<int64_t>(j) * TPR + t;
+            if (c4 < c4n) {
+                f4 o = v[j] / rms;
+                if (a.g) o = rms_scale(o, a.g, a.w_len, 4 * c4);
+                st4<NT>(a.y + base + 4 * c4, o);
+            }
+        }
+    }
+}
+
+// Generic rows: one workgroup per row, scalar strided passes over global
+// memory (the re-reads of a row hit L2).  Any width, any alignment.
+template <Norm K>
+__global__ __launch_bounds__(kBlock) void norm_rows_generic(NormArgs a) {
+    constexpr int NW = kBlock / kWave;
+    __shared__ float lds[2][NW];
+    const int64_t row = blockIdx.x;
+    const int64_t base = row * a.cols;
+    const float n = static_cast<float>(a.cols);
+    const float* x = a.x + base;
+    float* y = a.y + base;
+
+    if constexpr (K == Norm::Layer) {
+        float s = 0.0f;
+        for (int64_t c = threadIdx.x; c < a.cols; c += kBlock) s += x[c];
+        const float mean = block_sum<NW>(s, lds[0]) / n;
+        float q = 0.0f;
+        for (int64_t c = threadIdx.x; c < a.cols; c += kBlock) {
+            const float d = x[c] - mean;
+            q += d * d;
+        }
+        const float var = block_sum<NW>(q, lds[1]) / n;
+        const float inv_std = 1.0f / sqrtf(var + a.eps);
+        for (int64_t c = threadIdx.x; c < a.cols; c += kBlock) {
+            float o = (x[c] - mean) * inv_std;
+            if (a.g) {
+                o *= a.g[c];
+                if (a.b) o += a.b[c];
+            }
+            y[c] = o;
+        }
+    } else {
+        const float* h = x;
+        float q = 0.0f;
+        if constexpr (K == Norm::AddRms) {
+            const float* r = a.r + base;
+            float* ro = a.r_out + base;
+            for (int64_t c = threadIdx.x; c < a.cols; c += kBlock) {
+                const float v = x[c] + r[c];
+                ro[c] = v;
+                q += v * v;
+            }
+            h = ro;  // the second pass reads back this thread's own writes
+        } else {
+            for (int64_t c = threadIdx.x; c < a.cols; c += kBlock) q += x[c] * x[c];
+        }
+        const float rms = sqrtf(block_sum<NW>(q, lds[0]) / n + a.eps);
+        for (int64_t c = threadIdx.x; c < a.cols; c += kBlock) {
+            float o = h[c] / rms;
+            if (a.g && c < a.w_len) o *= a.g[c];
+            y[c] = o;
+        }
+    }
+}
+
+template <Norm K, int TPR, int VPT>
+int launch_vec(mimir_ctx* ctx, const NormArgs& a) {
+    unsigned blocks;
+    if (!grid_for(a.rows, kBlock / TPR, &blocks))
+        return fail(ctx, MIMIR_EINVAL, "norm: %lld rows exceed the grid limit", (long long)a.rows);
+    norm_rows_vec<K, TPR, VPT, true><<<blocks, kBlock, 0, ctx->stream>>>(a);
+    return launched(ctx, "norm_rows_vec");
+}
+
+template <Norm K>
+int dispatch(mimir_ctx* ctx, const NormArgs& a) {
+    bool vec = (a.cols % 4) == 0 && aligned16(a.x) && aligned16(a.y) &&
+               (!a.g || aligned16(a.g)) && (!a.b || aligned16(a.b));
+    if constexpr (K == Norm::AddRms) vec = vec && aligned16(a.r) && aligned16(a.r_out);
+    const int64_t c4 = a.cols / 4;
+    if (vec) {
+        if (c4 <= 64) return launch_vec<K, 64, 1>(ctx, a);
+        if (c4 <= 128) return launch_vec<K, 64, 2>(ctx, a);
+        if (c4 <= 256) return launch_vec<K, 64, 4>(ctx, a);
+        if (c4 <= 512) return launch_vec<K, 64, 8>(ctx, a);
+        if (c4 <= 1024) return launch_vec<K, 256, 4>(ctx, a);
+        if (c4 <= 2048) return launch_vec<K, 256, 8>(ctx, a);
+        if (c4 <= 4096) return launch_vec<K, 256, 16>(ctx, a);
+    }
+    if (a.rows > 0x7fffffffLL)
+        return fail(ctx, MIMIR_EINVAL, "norm: %lld rows exceed the grid limit", (long long)a.rows);
+    norm_rows_generic<K><<<static_cast<unsigned>(a.rows), kBlock, 0, ctx->stream>>>(a);
+    return launched(ctx, "norm_rows_generic");
+}
+
+}  // namespace
+
+extern "C" {
+
+int mimir_layernorm_fwd(mimir_ctx* ctx, const float* x, const float* gamma, const float* beta,
+                        float* y, int64_t groups, int64_t n, float eps) {
+    if (!ctx) return MIMIR_EINVAL;
+    MIMIR_REQUIRE(ctx, n > 0 && groups >= 0, "LayerNorm: invalid normalized_size (groups=%lld, n=%lld)",
+                  (long long)groups, (long long)n);
+    MIMIR_REQUIRE(ctx, !(beta && !gamma), "LayerNorm: bias without scale (use_bias needs affine)");
+    if (groups == 0) return MIMIR_OK;
+    MIMIR_REQUIRE(ctx, x && y, "LayerNorm: null tensor");
+    MIMIR_ENTER(ctx);
+    NormArgs a{x, nullptr, nullptr, gamma, beta, y, groups, n, n, eps};
+    return dispatch<Norm::Layer>(ctx, a);
+}
+
+int mimir_rmsnorm_fwd(mimir_ctx* ctx, const float* x, const float* w, int64_t w_len, float* y,
+                      int64_t rows, int64_t cols, float eps) {
+    if (!ctx) return MIMIR_EINVAL;
+    MIMIR_REQUIRE(ctx, rows >= 0 && cols > 0 && w_len >= 0, "RMSNorm: invalid shape (rows=%lld, cols=%lld)",
+                  (long long)rows, (long long)cols);
+    if (rows == 0) return MIMIR_OK;
+    MIMIR_REQUIRE(ctx, x && y, "RMSNorm: null tensor");
+    MIMIR_ENTER(ctx);
+    NormArgs a{x, nullptr, nullptr, (w && w_len > 0) ? w : nullptr, nullptr, y, rows, cols, w ? w_len : 0, eps};
+    return dispatch<Norm::Rms>(ctx, a);
+}
+
+int mimir_add_rmsnorm_fwd(mimir_ctx* ctx, const float* x, const float* residual,
+                          float* residual_out, const float* w, float* y, int64_t rows,
+                          int64_t cols, float eps) {
+    if (!ctx) return MIMIR_EINVAL;
+    MIMIR_REQUIRE(ctx, rows >= 0 && cols > 0, "add+RMSNorm: invalid shape (rows=%lld, cols=%lld)",
+                  (long long)rows, (long long)cols);
+    if (rows == 0) return MIMIR_OK;
+    MIMIR_REQUIRE(ctx, x && residual && residual_out && y, "add+RMSNorm: null tensor");
+    MIMIR_REQUIRE(ctx, static_cast<const void*>(y) != static_cast<const void*>(residual_out),
+                  "add+RMSNorm: y must not alias residual_out");
+    MIMIR_ENTER(ctx);
+    NormArgs a{x, residual, residual_out, w, nullptr, y, rows, cols, w ? cols : 0, eps};
+    return dispatch<Norm::AddRms>(ctx, a);
+}
+
+}  // extern "C"

@@ -1,0 +1,170 @@
+// softmax.hip -- max-subtracted row softmax / log-softmax for gfx950.
+//
+// Same row layout as norm.hip: TPR threads (one wavefront, or the 4-wave
+// workgroup for rows above 2048) hold the row in VGPRs as 16-byte vectors;
+// the row max and the sum of exponentials are wave-uniform DPP reductions, so
+// each element is read from HBM once and written once.  Rows too wide for the
+// register budget, or unaligned, take one workgroup per row with three
+// strided passes.
+//
+// Arithmetic (per row): m = max_j x[j]; e[j] = expf(x[j] - m); s = sum e[j];
+//   MIMIR_SOFTMAX_DIV_EPS  y = e / (s + 1e-9f)    LayerOps::softmax_inplace,
+//                                                  LayerOps.hpp:952-974
+//   MIMIR_SOFTMAX_MUL_INV  y = e * (1.0f / s)     LayerOps::softmax_forward,
+//                                                  LayerOps.hpp:325-361
+//   MIMIR_SOFTMAX_LOG      y = (x - m) - logf(s)  LogSoftmax, LayerOps.hpp:345-353
+#include "common.hpp"
+#include "internal.hpp"
+
+#include <math.h>
+
+using namespace mimir;
+
+namespace {
+
+struct SoftmaxArgs {
+    const float* x;
+    float* y;
+    int64_t rows;
+    int64_t cols;
+};
+
+template <int MODE>
+__device__ __forceinline__ float finish(float xv, float e, float m, float s, float inv_or_log) {
+    if constexpr (MODE == MIMIR_SOFTMAX_DIV_EPS) return e / s;  // s already holds sum + 1e-9f
+    else if constexpr (MODE == MIMIR_SOFTMAX_MUL_INV) return e * inv_or_log;
+    else return (xv - m) - inv_or_log;
+}
+
+template <int MODE>
+__device__ __forceinline__ void row_constants(float sum, float* s, float* aux) {
+    if constexpr (MODE == MIMIR_SOFTMAX_DIV_EPS) {
+        *s = sum + 1e-9f;
+        *aux = 0.0f;
+    } else if constexpr (MODE == MIMIR_SOFTMAX_MUL_INV) {
+        *s = sum;
+        *aux = 1.0f / sum;
+    } else {
+        *s = sum;
+        *aux = logf(sum);
+    }
+}
+
+template <int MODE, int TPR, int VPT, bool NT>
+__global__ __launch_bounds__(kBlock) void softmax_rows_vec(SoftmaxArgs a) {
+    constexpr int RPB = kBlock / TPR;
+    constexpr int NW = TPR / kWave;
+    __shared__ float lds[2][NW];
+    const int t = threadIdx.x % TPR;
+    const int64_t row = static_cast<int64_t>(blockIdx.x) * RPB + threadIdx.x / TPR;
+    if constexpr (NW == 1) {
+        if (row >= a.rows) return;
+    }
+    const int64_t c4n = a.cols >> 2;
+    const int64_t base = row * a.cols;
+
+    f4 v[VPT];
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) {
+        const int64_t c4 = static_cast<int64_t>(j) * TPR + t;
+        v[j] = (c4 < c4n) ? ld4<NT>(a.x + base + 4 * c4) : f4(-INFINITY);
+    }
+    float m = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) m = fmaxf(m, fmaxf(fmaxf(v[j].x, v[j].y), fmaxf(v[j].z, v[j].w)));
+    m = block_max<NW>(m, lds[0]);
+
+    f4 e[VPT];
+    float s = 0.0f;
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) {
+        const int64_t c4 = static_cast<int64_t>(j) * TPR + t;
+        if (c4 < c4n) {
+#pragma unroll
+            for (int k = 0; k < 4; ++k) e[j][k] = expf(v[j][k] - m);
+            s += (e[j].x + e[j].y) + (e[j].z + e[j].w);
+        } else {
+            e[j] = f4(0.0f);
+        }
+    }
+    float sum, aux;
+    row_constants<MODE>(block_sum<NW>(s, lds[1]), &sum, &aux);
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) {
+        const int64_t c4 = static_cast<int64_t>(j) * TPR + t;
+        if (c4 < c4n) {
+            f4 o;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) o[k] = finish<MODE>(v[j][k], e[j][k], m, sum, aux);
+            st4<NT>(a.y + base + 4 * c4, o);
+        }
+    }
+}
+
+template <int MODE>
+__global__ __launch_bounds__(kBlock) void softmax_rows_generic(SoftmaxArgs a) {
+    constexpr int NW = kBlock / kWave;
+    __shared__ float lds[2][NW];
+    const int64_t base = static_cast<int64_t>(blockIdx.x) * a.cols;
+    const float* x = a.x + base;
+    float* y = a.y + base;
+    float m = -INFINITY;
+    for (int64_t c = threadIdx.x; c < a.cols; c += kBlock) m = fmaxf(m, x[c]);
+    m = block_max<NW>(m, lds[0]);
+    float s = 0.0f;
+    for (int64_t c = threadIdx.x; c < a.cols; c += kBlock) s += expf(x[c] - m);
+    float sum, aux;
+    row_constants<MODE>(block_sum<NW>(s, lds[1]), &sum, &aux);
+    for (int64_t c = threadIdx.x; c < a.cols; c += kBlock) {
+        const float xv = x[c];
+        y[c] = finish<MODE>(xv, expf(xv - m), m, sum, aux);
+    }
+}
+
+template <int MODE, int TPR, int VPT>
+int launch_vec(mimir_ctx* ctx, const SoftmaxArgs& a) {
+    unsigned blocks;
+    if (!grid_for(a.rows, kBlock / TPR, &blocks))
+        return fail(ctx, MIMIR_EINVAL, "softmax: %lld rows exceed the grid limit", (long long)a.rows);
+    softmax_rows_vec<MODE, TPR, VPT, true><<<blocks, kBlock, 0, ctx->stream>>>(a);
+    return launched(ctx, "softmax_rows_vec");
+}
+
+template <int MODE>
+int dispatch(mimir_ctx* ctx, const SoftmaxArgs& a) {
+    const int64_t c4 = a.cols / 4;
+    if ((a.cols % 4) == 0 && aligned16(a.x) && aligned16(a.y)) {
+        if (c4 <= 64) return launch_vec<MODE, 64, 1>(ctx, a);
+        if (c4 <= 128) return launch_vec<MODE, 64, 2>(ctx, a);
+        if (c4 <= 256) return launch_vec<MODE, 64, 4>(ctx, a);
+        if (c4 <= 512) return launch_vec<MODE, 64, 8>(ctx, a);
+        if (c4 <= 1024) return launch_vec<MODE, 256, 4>(ctx, a);
+        if (c4 <= 2048) return launch_vec<MODE, 256, 8>(ctx, a);
+        if (c4 <= 4096) return launch_vec<MODE, 256, 16>(ctx, a);
+    }
+    if (a.rows > 0x7fffffffLL)
+        return fail(ctx, MIMIR_EINVAL, "softmax: %lld rows exceed the grid limit", (long long)a.rows);
+    softmax_rows_generic<MODE><<<static_cast<unsigned>(a.rows), kBlock, 0, ctx->stream>>>(a);
+    return launched(ctx, "softmax_rows_generic");
+}
+
+}  // namespace
+
+extern "C" int mimir_softmax_fwd(mimir_ctx* ctx, const float* x, float* y, int64_t rows,
+                                 int64_t cols, int mode) {
+    if (!ctx) return MIMIR_EINVAL;
+    MIMIR_REQUIRE(ctx, rows >= 0 && cols > 0, "Softmax: invalid shape (rows=%lld, cols=%lld)",
+                  (long long)rows, (long long)cols);
+    MIMIR_REQUIRE(ctx, mode == MIMIR_SOFTMAX_DIV_EPS || mode == MIMIR_SOFTMAX_MUL_INV ||
+                           mode == MIMIR_SOFTMAX_LOG,
+                  "Softmax: unknown mode %d", mode);
+    if (rows == 0) return MIMIR_OK;
+    MIMIR_REQUIRE(ctx, x && y, "Softmax: null tensor");
+    MIMIR_ENTER(ctx);
+    const SoftmaxArgs a{x, y, rows, cols};
+    switch (mode) {
+        case MIMIR_SOFTMAX_DIV_EPS: return dispatch<MIMIR_SOFTMAX_DIV_EPS>(ctx, a);
+        case MIMIR_SOFTMAX_MUL_INV: return dispatch<MIMIR_SOFTMAX_MUL_INV>(ctx, a);
+        default: return dispatch<MIMIR_SOFTMAX_LOG>(ctx, a);
+    }
+}

@@ -1,0 +1,360 @@
+// mimir_layerops_hip.hpp -- header-only C++ adapter that puts libmimir_hip
+// (include/mimir_hip.h) behind the reference's own forward-op signatures, so
+// Mimir's runtime can switch these ops to the MI355X without touching its
+// callers.  Same names, argument meaning and exceptions as the reference
+// (brit45/mimir-framework):
+//
+//   mimir_hip::LayerOps::layernorm_forward   LayerOps.hpp:264-319
+//   mimir_hip::LayerOps::softmax_forward     LayerOps.hpp:325-361
+//   mimir_hip::LayerOps::softmax_inplace     LayerOps.hpp:952-974
+//   mimir_hip::LayerOps::gelu_forward        LayerOps.hpp:556-568
+//   mimir_hip::LayerOps::silu_forward        LayerOps.hpp:570-581
+//   mimir_hip::LayerOps::add_forward         LayerOps.hpp:142-199
+//   mimir_hip::LayerOps::multiply_forward    LayerOps.hpp:205-230
+//   mimir_hip::LayerOpsExt::rms_norm_forward LayerOpsExt.hpp:345-378
+//   mimir_hip::Normalization::rms_norm       Layers.hpp:1003-1021
+//   mimir_hip::embedding_forward(_float_ids) Model.cpp:1152-1205 / 5301-5334 (inline there)
+//
+// The op templates take the reference's `Layer` (or anything with the same
+// fields: eps, affine, use_bias, in_features, vocab_size, embed_dim,
+// padding_idx, type_enum, getWeights(), getWeightsSize()).  The host-vector
+// overloads upload, run and download; the `device::` functions take device
+// pointers and only enqueue, for a device-resident TensorStore.
+//
+// Errors: invalid shapes throw std::runtime_error, as the reference does;
+// device failures throw mimir_hip::Error (also a std::runtime_error).
+#pragma once
+
+#include <mimir_hip.h>
+
+#include <cstddef>
+#include <cstdint>
+#include <stdexcept>
+#include <string>
+#include <utility>
+#include <vector>
+
+namespace mimir_hip {
+
+class Error : public std::runtime_error {
+public:
+    Error(int status, const std::string& msg) : std::runtime_error(msg), status_(status) {}
+    int status() const { return status_; }
+
+private:
+    int status_;
+};
+
+// One device + stream.  Context::instance() is the process-wide default,
+// created on first use (as the reference's static compute engines are).
+class Context {
+public:
+    explicit Context(int device = 0) {
+        const int st = mimir_ctx_create(device, &ctx_);
+        if (st != MIMIR_OK)
+            throw Error(st, "mimir_ctx_create(device " + std::to_string(device) + ") failed");
+    }
+    ~Context() {
+        if (ctx_) mimir_ctx_destroy(ctx_);
+    }
+    Context(const Context&) = delete;
+    Context& operator=(const Context&) = delete;
+
+    static Context& instance() {
+        static Context ctx(0);
+        return ctx;
+    }
+
+    mimir_ctx* get() const { return ctx_; }
+
+    // MIMIR_EINVAL -> std::runtime_error (the reference's convention); others -> Error.
+    void check(int st, const char* what) const {
+        if (st == MIMIR_OK) return;
+        std::string msg = std::string(what) + ": " + mimir_last_error(ctx_);
+        if (st == MIMIR_EINVAL) throw std::runtime_error(msg);
+        throw Error(st, msg);
+    }
+    void sync() const { check(mimir_sync(ctx_), "mimir_sync"); }
+
+private:
+    mimir_ctx* ctx_ = nullptr;
+};
+
+// Owning device buffer of T.
+template <class T>
+class DeviceBuffer {
+public:
+    DeviceBuffer(Context& ctx, size_t n) : ctx_(&ctx), n_(n) {
+        if (n_) ctx_->check(mimir_malloc(ctx_->get(), n_ * sizeof(T), reinterpret_cast<void**>(&p_)),
+                            "mimir_malloc");
+    }
+    DeviceBuffer(Context& ctx, const std::vector<T>& host) : DeviceBuffer(ctx, host.size()) {
+        upload(host.data(), host.size());
+    }
+    DeviceBuffer(Context& ctx, const T* host, size_t n) : DeviceBuffer(ctx, n) { upload(host, n); }
+    ~DeviceBuffer() {
+        if (p_) mimir_free(ctx_->get(), p_);
+    }
+    DeviceBuffer(DeviceBuffer&& o) noexcept : ctx_(o.ctx_), p_(o.p_), n_(o.n_) { o.p_ = nullptr; }
+    DeviceBuffer(const DeviceBuffer&) = delete;
+    DeviceBuffer& operator=(const DeviceBuffer&) = delete;
+
+    T* data() const { return p_; }
+    size_t size() const { return n_; }
+    void upload(const T* host, size_t n) {
+        if (n) ctx_->check(mimir_upload(ctx_->get(), p_, host, n * sizeof(T)), "mimir_upload");
+    }
+    std::vector<T> download() const {
+        std::vector<T> out(n_);
+        if (n_) ctx_->check(mimir_download(ctx_->get(), out.data(), p_, n_ * sizeof(T)), "mimir_download");
+        return out;
+    }
+
+private:
+    Context* ctx_;
+    T* p_ = nullptr;
+    size_t n_ = 0;
+};
+
+// ---------------------------------------------------------------------------
+// Device-resident entry points (enqueue only).
+// ---------------------------------------------------------------------------
+namespace device {
+
+inline void layernorm(Context& c, const float* x, const float* gamma, const float* beta, float* y,
+                      int64_t groups, int64_t n, float eps) {
+    c.check(mimir_layernorm_fwd(c.get(), x, gamma, beta, y, groups, n, eps), "LayerNorm");
+}
+inline void rmsnorm(Context& c, const float* x, const float* w, int64_t w_len, float* y, int64_t rows,
+                    int64_t cols, float eps) {
+    c.check(mimir_rmsnorm_fwd(c.get(), x, w, w_len, y, rows, cols, eps), "RMSNorm");
+}
+inline void add_rmsnorm(Context& c, const float* x, const float* residual, float* residual_out,
+                        const float* w, float* y, int64_t rows, int64_t cols, float eps) {
+    c.check(mimir_add_rmsnorm_fwd(c.get(), x, residual, residual_out, w, y, rows, cols, eps),
+            "add+RMSNorm");
+}
+inline void softmax(Context& c, const float* x, float* y, int64_t rows, int64_t cols, int mode) {
+    c.check(mimir_softmax_fwd(c.get(), x, y, rows, cols, mode), "Softmax");
+}
+inline void gelu(Context& c, const float* x, float* y, int64_t n) {
+    c.check(mimir_gelu_fwd(c.get(), x, y, n), "GELU");
+}
+inline void silu(Context& c, const float* x, float* y, int64_t n) {
+    c.check(mimir_silu_fwd(c.get(), x, y, n), "SiLU");
+}
+inline void silu_mul(Context& c, const float* gate, const float* up, float* y, int64_t n) {
+    c.check(mimir_silu_mul_fwd(c.get(), gate, up, y, n), "SiLU*up");
+}
+inline void gelu_mul(Context& c, const float* gate, const float* up, float* y, int64_t n) {
+    c.check(mimir_gelu_mul_fwd(c.get(), gate, up, y, n), "GELU*up");
+}
+inline void add(Context& c, const float* a, int64_t na, const float* b, int64_t nb, float* y) {
+    c.check(mimir_add_fwd(c.get(), a, na, b, nb, y), "Add");
+}
+inline void mul(Context& c, const float* a, int64_t na, const float* b, int64_t nb, float* y) {
+    c.check(mimir_mul_fwd(c.get(), a, na, b, nb, y), "Multiply");
+}
+inline void embedding(Context& c, const int32_t* ids, int64_t n_ids, const float* table,
+                      int64_t table_len, int32_t vocab, int32_t dim, int32_t pad, float* y) {
+    c.check(mimir_embedding_fwd(c.get(), ids, n_ids, table, table_len, vocab, dim, pad, y), "Embedding");
+}
+inline void rope(Context& c, const float* q, float* q_out, int64_t q_heads, const float* k, float* k_out,
+                 int64_t k_heads, int64_t batch, int64_t seq, int64_t head_dim, int64_t pos_offset,
+                 const float* cos_tab, const float* sin_tab, int64_t table_rows) {
+    c.check(mimir_rope_fwd(c.get(), q, q_out, q_heads, k, k_out, k_heads, batch, seq, head_dim,
+                           pos_offset, cos_tab, sin_tab, table_rows),
+            "RoPE");
+}
+
+}  // namespace device
+
+namespace detail {
+
+// Run `op(device ptrs..., y)` on host vectors: upload inputs, allocate the
+// output, download it (the PCIe-inclusive path of a host-vector caller).
+template <class Op>
+std::vector<float> run1(Context& c, const std::vector<float>& x, size_t out_n, Op op) {
+    DeviceBuffer<float> dx(c, x);
+    DeviceBuffer<float> dy(c, out_n);
+    op(dx.data(), dy.data());
+    return dy.download();
+}
+
+template <class Op>
+std::vector<float> run2(Context& c, const std::vector<float>& a, const std::vector<float>& b,
+                        size_t out_n, Op op) {
+    DeviceBuffer<float> da(c, a);
+    DeviceBuffer<float> db(c, b);
+    DeviceBuffer<float> dy(c, out_n);
+    op(da.data(), db.data(), dy.data());
+    return dy.download();
+}
+
+}  // namespace detail
+
+// ---------------------------------------------------------------------------
+// Host-vector mirrors of the reference entry points.
+// ---------------------------------------------------------------------------
+namespace LayerOps {
+
+template <class LayerT>
+std::vector<float> layernorm_forward(const std::vector<float>& input, const LayerT& layer,
+                                     bool training = true) {
+    (void)training;
+    Context& c = Context::instance();
+    const int64_t N = static_cast<int64_t>(input.size());
+    const int64_t n = layer.in_features > 0 ? layer.in_features : N;
+    if (n <= 0 || (N % n) != 0) throw std::runtime_error("LayerNorm: invalid normalized_size");
+    const float* w = layer.affine ? layer.getWeights() : nullptr;
+    const bool bias = layer.affine && layer.use_bias;
+    std::vector<float> gamma, beta;
+    if (w) {
+        const size_t need = static_cast<size_t>(n) * (bias ? 2 : 1);
+        if (layer.getWeightsSize() < need) throw std::runtime_error("LayerNorm: weight block too small");
+        gamma.assign(w, w + n);
+        if (bias) beta.assign(w + n, w + 2 * n);
+    }
+    DeviceBuffer<float> dg(c, gamma), db(c, beta);
+    return detail::run1(c, input, input.size(), [&](const float* x, float* y) {
+        device::layernorm(c, x, w ? dg.data() : nullptr, bias && w ? db.data() : nullptr, y, N / n, n,
+                          layer.eps);
+    });
+}
+
+template <class LayerT>
+std::vector<float> softmax_forward(const std::vector<float>& input, const LayerT& layer) {
+    Context& c = Context::instance();
+    const bool log = layer.type_enum == decltype(layer.type_enum)::LogSoftmax;
+    return detail::run1(c, input, input.size(), [&](const float* x, float* y) {
+        device::softmax(c, x, y, 1, static_cast<int64_t>(input.size()),
+                        log ? MIMIR_SOFTMAX_LOG : MIMIR_SOFTMAX_MUL_INV);
+    });
+}
+
+inline void softmax_inplace(std::vector<float>& x, int seq_len, int dim) {
+    Context& c = Context::instance();
+    x = detail::run1(c, x, x.size(), [&](const float* in, float* y) {
+        device::softmax(c, in, y, seq_len, dim, MIMIR_SOFTMAX_DIV_EPS);
+    });
+}
+
+inline std::vector<float> gelu_forward(const std::vector<float>& input) {
+    Context& c = Context::instance();
+    return detail::run1(c, input, input.size(), [&](const float* x, float* y) {
+        device::gelu(c, x, y, static_cast<int64_t>(input.size()));
+    });
+}
+
+inline std::vector<float> silu_forward(const std::vector<float>& input) {
+    Context& c = Context::instance();
+    return detail::run1(c, input, input.size(), [&](const float* x, float* y) {
+        device::silu(c, x, y, static_cast<int64_t>(input.size()));
+    });
+}
+
+inline std::vector<float> add_forward(const std::vector<float>& input1, const std::vector<float>& input2) {
+    if (input1.empty() || input2.empty()) throw std::runtime_error("Add: inputs must be non-empty");
+    Context& c = Context::instance();
+    const size_t out_n = input1.size() > input2.size() ? input1.size() : input2.size();
+    return detail::run2(c, input1, input2, out_n, [&](const float* a, const float* b, float* y) {
+        device::add(c, a, static_cast<int64_t>(input1.size()), b, static_cast<int64_t>(input2.size()), y);
+    });
+}
+
+inline std::vector<float> multiply_forward(const std::vector<float>& input1,
+                                           const std::vector<float>& input2) {
+    if (input1.size() != input2.size()) throw std::runtime_error("Multiply: input sizes must match");
+    Context& c = Context::instance();
+    return detail::run2(c, input1, input2, input1.size(), [&](const float* a, const float* b, float* y) {
+        device::mul(c, a, static_cast<int64_t>(input1.size()), b, static_cast<int64_t>(input2.size()), y);
+    });
+}
+
+// Fused form of multiply_forward(silu_forward(gate), up): one pass, no intermediate vector.
+inline std::vector<float> silu_mul_forward(const std::vector<float>& gate, const std::vector<float>& up) {
+    if (gate.size() != up.size()) throw std::runtime_error("Multiply: input sizes must match");
+    Context& c = Context::instance();
+    return detail::run2(c, gate, up, gate.size(), [&](const float* g, const float* u, float* y) {
+        device::silu_mul(c, g, u, y, static_cast<int64_t>(gate.size()));
+    });
+}
+
+}  // namespace LayerOps
+
+namespace LayerOpsExt {
+
+template <class LayerT>
+std::vector<float> rms_norm_forward(const std::vector<float>& input, const LayerT& layer) {
+    Context& c = Context::instance();
+    if (input.empty()) return {};
+    const float* w = layer.getWeights();
+    const size_t wn = (layer.affine && w) ? layer.getWeightsSize() : 0;
+    DeviceBuffer<float> dw(c, w, wn);
+    return detail::run1(c, input, input.size(), [&](const float* x, float* y) {
+        device::rmsnorm(c, x, wn ? dw.data() : nullptr, static_cast<int64_t>(wn), y, 1,
+                        static_cast<int64_t>(input.size()), layer.eps);
+    });
+}
+
+}  // namespace LayerOpsExt
+
+namespace Normalization {
+
+inline void rms_norm(std::vector<float>& data, const std::vector<float>& gamma, int normalized_size,
+                     float eps = 1e-6f) {
+    Context& c = Context::instance();
+    if (normalized_size <= 0 || gamma.size() < static_cast<size_t>(normalized_size))
+        throw std::runtime_error("rms_norm: invalid normalized_size");
+    const int64_t rows = static_cast<int64_t>(data.size()) / normalized_size;
+    DeviceBuffer<float> dg(c, gamma);
+    data = detail::run1(c, data, data.size(), [&](const float* x, float* y) {
+        device::rmsnorm(c, x, dg.data(), normalized_size, y, rows, normalized_size, eps);
+    });
+}
+
+}  // namespace Normalization
+
+// The embedding gather of Model::forwardPassView (int ids), Model.cpp:1152-1205.
+template <class LayerT>
+std::vector<float> embedding_forward(const std::vector<int>& ids, const LayerT& layer) {
+    Context& c = Context::instance();
+    const int32_t vocab = layer.vocab_size > 1 ? layer.vocab_size : 1;
+    const int32_t dim = layer.embed_dim > 1 ? layer.embed_dim : 1;
+    const float* w = layer.getWeights();
+    if (!w) throw std::runtime_error("Embedding: weights not initialized");
+    const size_t wn = layer.getWeightsSize();
+    if (wn < static_cast<size_t>(vocab) * static_cast<size_t>(dim))
+        throw std::runtime_error("Embedding: invalid weight size");
+    if (ids.empty()) return {};
+    static_assert(sizeof(int) == sizeof(int32_t), "int ids are 32-bit");
+    DeviceBuffer<int32_t> di(c, reinterpret_cast<const int32_t*>(ids.data()), ids.size());
+    DeviceBuffer<float> dt(c, w, wn);
+    DeviceBuffer<float> dy(c, ids.size() * static_cast<size_t>(dim));
+    device::embedding(c, di.data(), static_cast<int64_t>(ids.size()), dt.data(), static_cast<int64_t>(wn),
+                      vocab, dim, layer.padding_idx, dy.data());
+    return dy.download();
+}
+
+// Float-id form, Model.cpp:5301-5334 (ids rounded with llround).
+template <class LayerT>
+std::vector<float> embedding_forward_float_ids(const std::vector<float>& x, const LayerT& layer) {
+    Context& c = Context::instance();
+    const int32_t vocab = layer.vocab_size > 1 ? layer.vocab_size : 1;
+    const int32_t dim = layer.embed_dim > 1 ? layer.embed_dim : 1;
+    const float* w = layer.getWeights();
+    if (!w) throw std::runtime_error("Embedding: weights not initialized");
+    const size_t wn = layer.getWeightsSize();
+    if (wn < static_cast<size_t>(vocab) * static_cast<size_t>(dim))
+        throw std::runtime_error("Embedding: invalid weight size");
+    if (x.empty()) return {};
+    DeviceBuffer<float> di(c, x);
+    DeviceBuffer<float> dt(c, w, wn);
+    DeviceBuffer<float> dy(c, x.size() * static_cast<size_t>(dim));
+    c.check(mimir_embedding_f32ids_fwd(c.get(), di.data(), static_cast<int64_t>(x.size()), dt.data(),
+                                       static_cast<int64_t>(wn), vocab, dim, layer.padding_idx, dy.data()),
+            "Embedding");
+    return dy.download();
+}
+
+}  // namespace mimir_hip

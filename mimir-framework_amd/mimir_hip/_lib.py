@@ -1,0 +1,77 @@
+"""ctypes binding of libmimir_hip.so (the C ABI declared in include/mimir_hip.h).
+
+Loading fails loudly when the library is not built: there is no CPU fallback
+anywhere in this package.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from ctypes import POINTER, c_char_p, c_double, c_float, c_int, c_int32, c_int64, c_size_t, c_void_p
+
+PKG_ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+LIB_PATH = os.path.join(PKG_ROOT, "lib", "libmimir_hip.so")
+REPO_ROOT = os.path.dirname(PKG_ROOT)
+HEADER_PATH = os.path.join(REPO_ROOT, "include", "mimir_hip.h")
+
+OK, EINVAL, ENOMEM, EDEVICE = 0, 1, 2, 3
+SOFTMAX_DIV_EPS, SOFTMAX_MUL_INV, SOFTMAX_LOG = 0, 1, 2
+
+_P = c_void_p
+_PP = POINTER(c_void_p)
+
+# name -> (restype, argtypes); mirrors include/mimir_hip.h one to one.
+SIGNATURES = {
+    "mimir_ctx_create": (c_int, [c_int, _PP]),
+    "mimir_ctx_destroy": (c_int, [_P]),
+    "mimir_ctx_set_stream": (c_int, [_P, _P]),
+    "mimir_ctx_stream": (c_void_p, [_P]),
+    "mimir_ctx_set_alloc_limit": (c_int, [_P, c_size_t]),
+    "mimir_last_error": (c_char_p, [_P]),
+    "mimir_malloc": (c_int, [_P, c_size_t, _PP]),
+    "mimir_free": (c_int, [_P, _P]),
+    "mimir_upload": (c_int, [_P, _P, _P, c_size_t]),
+    "mimir_download": (c_int, [_P, _P, _P, c_size_t]),
+    "mimir_copy": (c_int, [_P, _P, _P, c_size_t]),
+    "mimir_fill_f32": (c_int, [_P, _P, c_int64, c_float]),
+    "mimir_sync": (c_int, [_P]),
+    "mimir_event_create": (c_int, [_P, _PP]),
+    "mimir_event_destroy": (c_int, [_P]),
+    "mimir_event_record": (c_int, [_P, _P]),
+    "mimir_event_elapsed_ms": (c_int, [_P, _P, POINTER(c_float)]),
+    "mimir_layernorm_fwd": (c_int, [_P, _P, _P, _P, _P, c_int64, c_int64, c_float]),
+    "mimir_rmsnorm_fwd": (c_int, [_P, _P, _P, c_int64, _P, c_int64, c_int64, c_float]),
+    "mimir_add_rmsnorm_fwd": (c_int, [_P, _P, _P, _P, _P, _P, c_int64, c_int64, c_float]),
+    "mimir_softmax_fwd": (c_int, [_P, _P, _P, c_int64, c_int64, c_int]),
+    "mimir_gelu_fwd": (c_int, [_P, _P, _P, c_int64]),
+    "mimir_silu_fwd": (c_int, [_P, _P, _P, c_int64]),
+    "mimir_silu_mul_fwd": (c_int, [_P, _P, _P, _P, c_int64]),
+    "mimir_gelu_mul_fwd": (c_int, [_P, _P, _P, _P, c_int64]),
+    "mimir_add_fwd": (c_int, [_P, _P, c_int64, _P, c_int64, _P]),
+    "mimir_mul_fwd": (c_int, [_P, _P, c_int64, _P, c_int64, _P]),
+    "mimir_embedding_fwd": (c_int, [_P, _P, c_int64, _P, c_int64, c_int32, c_int32, c_int32, _P]),
+    "mimir_embedding_f32ids_fwd": (c_int, [_P, _P, c_int64, _P, c_int64, c_int32, c_int32, c_int32,
+                                           _P]),
+    "mimir_rope_table": (c_int, [c_int64, c_int64, c_double, _P, _P]),
+    "mimir_rope_fwd": (c_int, [_P, _P, _P, c_int64, _P, _P, c_int64, c_int64, c_int64, c_int64,
+                               c_int64, _P, _P, c_int64]),
+}
+
+_lib = None
+
+
+def load():
+    """Load libmimir_hip.so once; raise if it is not built."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise ImportError(
+                f"{LIB_PATH} is not built: run `make -C mimir-framework_amd` "
+                "(or __graft_entry__.build()); mimir_hip has no CPU fallback")
+        lib = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = lib
+    return _lib

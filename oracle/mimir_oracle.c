@@ -1,0 +1,270 @@
+/*
+ * mimir_oracle.c -- CPU restatement of Mimir's fused elementwise / row-reduction
+ * layer path.  TEST INFRASTRUCTURE ONLY (the checker for the HIP kernels and the
+ * "port" CPU baseline); never part of the product library.
+ *
+ * Each function restates the reference's scalar algorithm in plain C with the
+ * same float32 intermediates and the same glibc libm calls.  Citations are to
+ * brit45/mimir-framework.  Single-threaded, like the reference ops.
+ */
+#include "mimir_oracle.h"
+
+#include <math.h>
+#include <string.h>
+
+#define ORACLE_OK 0
+#define ORACLE_EINVAL 1
+
+/* LayerOps.hpp:264-319 */
+int oracle_layernorm(const float* x, int64_t N, int64_t in_features,
+                     const float* gamma, const float* beta, float eps, float* y) {
+    /* LayerOps.hpp:276-280: normalized = in_features > 0 ? in_features : N,
+     * throw unless normalized > 0 and N % normalized == 0. */
+    const int64_t n = in_features > 0 ? in_features : N;
+    if (n <= 0 || N < 0 || (N % n) != 0) return ORACLE_EINVAL;
+    /* The reference only adds the bias inside `if (weights)` (:310-313): a bias
+     * without a scale is not expressible there. */
+    if (beta && !gamma) return ORACLE_EINVAL;
+    const int64_t groups = N / n;
+    for (int64_t g = 0; g < groups; ++g) {
+        const float* xr = x + g * n;
+        float* yr = y + g * n;
+        float mean = 0.0f; /* :291-295 */
+        for (int64_t i = 0; i < n; ++i) mean += xr[i];
+        mean /= (float)n;
+        float var = 0.0f; /* :297-303, two-pass variance */
+        for (int64_t i = 0; i < n; ++i) {
+            const float d = xr[i] - mean;
+            var += d * d;
+        }
+        var /= (float)n;
+        const float inv_std = 1.0f / sqrtf(var + eps); /* :305 */
+        for (int64_t i = 0; i < n; ++i) {           /* :307-315 */
+            float v = (xr[i] - mean) * inv_std;
+            if (gamma) {
+                v *= gamma[i];
+                if (beta) v += beta[i];
+            }
+            yr[i] = v;
+        }
+    }
+    return ORACLE_OK;
+}
+
+/* LayerOpsExt.hpp:345-378 (one group over the whole input). */
+int oracle_rmsnorm_whole(const float* x, int64_t N, const float* w, int64_t w_len,
+                         float eps, float* y) {
+    if (N < 0 || w_len < 0) return ORACLE_EINVAL;
+    float rms_sq = 0.0f; /* :357-361 */
+    for (int64_t i = 0; i < N; ++i) rms_sq += x[i] * x[i];
+    rms_sq /= (float)N;
+    const float rms = sqrtf(rms_sq + eps);
+    const int64_t wn = w ? w_len : 0; /* :364-366 */
+    for (int64_t i = 0; i < N; ++i) { /* :368-375 */
+        float v = x[i] / rms;
+        if (wn && i < wn) v *= w[i];
+        y[i] = v;
+    }
+    return ORACLE_OK;
+}
+
+/* Layers.hpp:1003-1021 (per-row twin). */
+int oracle_rmsnorm_rows(const float* x, int64_t rows, int64_t cols,
+                        const float* gamma, float eps, float* y) {
+    if (rows < 0 || cols <= 0) return ORACLE_EINVAL;
+    for (int64_t g = 0; g < rows; ++g) {
+        const float* xr = x + g * cols;
+        float* yr = y + g * cols;
+        float rms = 0.0f; /* :1009-1013 */
+        for (int64_t i = 0; i < cols; ++i) {
+            const float v = xr[i];
+            rms += v * v;
+        }
+        rms = sqrtf(rms / (float)cols + eps); /* :1014 */
+        for (int64_t i = 0; i < cols; ++i) {   /* :1016-1019 */
+            float v = xr[i] / rms;
+            if (gamma) v *= gamma[i];
+            yr[i] = v;
+        }
+    }
+    return ORACLE_OK;
+}
+
+int oracle_add_rmsnorm(const float* x, const float* residual, int64_t rows,
+                       int64_t cols, const float* gamma, float eps,
+                       float* residual_out, float* y) {
+    if (rows < 0 || cols <= 0) return ORACLE_EINVAL;
+    const int64_t n = rows * cols;
+    /* add_forward equal-size branch, LayerOps.hpp:154-169: one rounding per element */
+    for (int64_t i = 0; i < n; ++i) residual_out[i] = x[i] + residual[i];
+    return oracle_rmsnorm_rows(residual_out, rows, cols, gamma, eps, y);
+}
+
+/* LayerOps.hpp:142-199 */
+int oracle_add(const float* a, int64_t na, const float* b, int64_t nb, float* y) {
+    if (na <= 0 || nb <= 0) return ORACLE_EINVAL; /* :150-152 */
+    if (na == nb) {                                /* :154-169 */
+        for (int64_t i = 0; i < na; ++i) y[i] = a[i] + b[i];
+        return ORACLE_OK;
+    }
+    const float* big = a;
+    const float* small = b;
+    int64_t big_n = na, small_n = nb;
+    if (nb > na) { /* :172-177 */
+        big = b; small = a; big_n = nb; small_n = na;
+    }
+    if (small_n == 1) { /* :181-188 */
+        const float s = small[0];
+        for (int64_t i = 0; i < big_n; ++i) y[i] = big[i] + s;
+        return ORACLE_OK;
+    }
+    if (big_n % small_n != 0) return ORACLE_EINVAL; /* :190-192 */
+    for (int64_t i = 0; i < big_n; ++i) y[i] = big[i] + small[i % small_n]; /* :194-197 */
+    return ORACLE_OK;
+}
+
+/* LayerOps.hpp:205-230 */
+int oracle_mul(const float* a, int64_t na, const float* b, int64_t nb, float* y) {
+    if (na != nb || na < 0) return ORACLE_EINVAL; /* :209-211 */
+    for (int64_t i = 0; i < na; ++i) y[i] = a[i] * b[i];
+    return ORACLE_OK;
+}
+
+/* std::max(m, v) returns m unless m < v (so a NaN already held in m stays). */
+static inline float ref_max(float m, float v) { return (m < v) ? v : m; }
+
+int oracle_softmax_rows(const float* x, int64_t rows, int64_t cols, int mode, float* y) {
+    if (rows < 0 || cols <= 0) return ORACLE_EINVAL;
+    if (mode != ORACLE_SOFTMAX_DIV_EPS && mode != ORACLE_SOFTMAX_MUL_INV &&
+        mode != ORACLE_SOFTMAX_LOG)
+        return ORACLE_EINVAL;
+    for (int64_t r = 0; r < rows; ++r) {
+        const float* xr = x + r * cols;
+        float* yr = y + r * cols;
+        float m = xr[0]; /* LayerOps.hpp:957-960 / std::max_element at :331 */
+        for (int64_t j = 1; j < cols; ++j) m = ref_max(m, xr[j]);
+        float sum = 0.0f; /* :963-967 / :334-339 */
+        for (int64_t j = 0; j < cols; ++j) {
+            const float e = expf(xr[j] - m);
+            yr[j] = e;
+            sum += e;
+        }
+        if (mode == ORACLE_SOFTMAX_DIV_EPS) { /* :970-972 */
+            for (int64_t j = 0; j < cols; ++j) yr[j] /= (sum + 1e-9f);
+        } else if (mode == ORACLE_SOFTMAX_MUL_INV) { /* :342, :355-358 */
+            const float inv_sum = 1.0f / sum;
+            for (int64_t j = 0; j < cols; ++j) yr[j] *= inv_sum;
+        } else { /* LogSoftmax, :345-353 */
+            const float log_denom = logf(sum);
+            for (int64_t j = 0; j < cols; ++j) yr[j] = (xr[j] - m) - log_denom;
+        }
+    }
+    return ORACLE_OK;
+}
+
+/* LayerOps.hpp:556-568 */
+static inline float gelu1(float x) {
+    const float k = sqrtf(2.0f / 3.14159265359f);
+    const float cdf = 0.5f * (1.0f + tanhf(k * (x + 0.044715f * x * x * x)));
+    return x * cdf;
+}
+
+/* LayerOps.hpp:570-581 */
+static inline float silu1(float x) {
+    const float sigmoid = 1.0f / (1.0f + expf(-x));
+    return x * sigmoid;
+}
+
+void oracle_gelu(const float* x, int64_t n, float* y) {
+    for (int64_t i = 0; i < n; ++i) y[i] = gelu1(x[i]);
+}
+
+void oracle_silu(const float* x, int64_t n, float* y) {
+    for (int64_t i = 0; i < n; ++i) y[i] = silu1(x[i]);
+}
+
+void oracle_silu_mul(const float* gate, const float* up, int64_t n, float* y) {
+    for (int64_t i = 0; i < n; ++i) y[i] = silu1(gate[i]) * up[i];
+}
+
+void oracle_gelu_mul(const float* gate, const float* up, int64_t n, float* y) {
+    for (int64_t i = 0; i < n; ++i) y[i] = gelu1(gate[i]) * up[i];
+}
+
+/* Shared body of the two inline gathers (Model.cpp:1176-1203, 5307-5330). */
+static int embed_check(int64_t n_ids, int64_t table_len, int32_t* vocab, int32_t* dim) {
+    if (n_ids < 0) return ORACLE_EINVAL;
+    if (*vocab < 1) *vocab = 1; /* Model.cpp:1176-1177: std::max(1, ...) */
+    if (*dim < 1) *dim = 1;
+    if (table_len < (int64_t)(*vocab) * (int64_t)(*dim)) return ORACLE_EINVAL; /* :1181-1182 */
+    return ORACLE_OK;
+}
+
+static void embed_row(int32_t id, int64_t t, const float* table, int32_t vocab,
+                      int32_t dim, int32_t pad, float* y) {
+    float* out = y + t * (int64_t)dim;
+    memset(out, 0, (size_t)dim * sizeof(float)); /* out.assign(outN, 0.0f), :1190 */
+    if (pad >= 0 && id == pad) return;           /* :1196 */
+    if (id < 0 || id >= vocab) return;           /* :1197, silent */
+    const float* w = table + (int64_t)id * (int64_t)dim;
+    for (int32_t d = 0; d < dim; ++d) out[d] = w[d]; /* :1200-1202 */
+}
+
+int oracle_embedding_i32(const int32_t* ids, int64_t n_ids, const float* table,
+                         int64_t table_len, int32_t vocab, int32_t dim,
+                         int32_t padding_idx, float* y) {
+    if (embed_check(n_ids, table_len, &vocab, &dim)) return ORACLE_EINVAL;
+    for (int64_t t = 0; t < n_ids; ++t) embed_row(ids[t], t, table, vocab, dim, padding_idx, y);
+    return ORACLE_OK;
+}
+
+int oracle_embedding_f32(const float* ids, int64_t n_ids, const float* table,
+                         int64_t table_len, int32_t vocab, int32_t dim,
+                         int32_t padding_idx, float* y) {
+    if (embed_check(n_ids, table_len, &vocab, &dim)) return ORACLE_EINVAL;
+    for (int64_t t = 0; t < n_ids; ++t) {
+        /* Model.cpp:5321: static_cast<int>(std::llround(static_cast<double>(x[t]))) */
+        const int32_t id = (int32_t)llround((double)ids[t]);
+        embed_row(id, t, table, vocab, dim, padding_idx, y);
+    }
+    return ORACLE_OK;
+}
+
+int oracle_rope_table(int64_t rows, int64_t head_dim, double theta,
+                      float* cos_tab, float* sin_tab) {
+    if (rows < 0 || head_dim <= 0 || (head_dim & 1) || !(theta > 0.0)) return ORACLE_EINVAL;
+    const int64_t half = head_dim / 2;
+    for (int64_t p = 0; p < rows; ++p) {
+        for (int64_t i = 0; i < half; ++i) {
+            const double inv_freq = 1.0 / pow(theta, (double)(2 * i) / (double)head_dim);
+            const double a = (double)p * inv_freq;
+            cos_tab[p * half + i] = (float)cos(a);
+            sin_tab[p * half + i] = (float)sin(a);
+        }
+    }
+    return ORACLE_OK;
+}
+
+int oracle_rope(const float* x, float* y, int64_t B, int64_t S, int64_t H,
+                int64_t D, int64_t pos_offset, const float* cos_tab,
+                const float* sin_tab, int64_t table_rows) {
+    if (B < 0 || S < 0 || H < 0 || D <= 0 || (D & 1) || pos_offset < 0) return ORACLE_EINVAL;
+    if (S > 0 && pos_offset + S > table_rows) return ORACLE_EINVAL;
+    const int64_t half = D / 2;
+    for (int64_t b = 0; b < B; ++b) {
+        for (int64_t s = 0; s < S; ++s) {
+            const float* c = cos_tab + (pos_offset + s) * half;
+            const float* sn = sin_tab + (pos_offset + s) * half;
+            for (int64_t h = 0; h < H; ++h) {
+                const int64_t base = ((b * S + s) * H + h) * D;
+                for (int64_t i = 0; i < half; ++i) {
+                    const float x0 = x[base + i];
+                    const float x1 = x[base + half + i];
+                    y[base + i] = x0 * c[i] - x1 * sn[i];
+                    y[base + half + i] = x1 * c[i] + x0 * sn[i];
+                }
+            }
+        }
+    }
+    return ORACLE_OK;
+}

@@ -1,0 +1,361 @@
+"""numpy front end for the CPU checkers.  TEST INFRASTRUCTURE ONLY.
+
+Only tests/, ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of
+bench.py may import this module; the product (``mimir_hip``) never does.
+
+Two libraries are wrapped:
+
+* ``lib/libmimir_oracle.so`` -- the C restatement (``mimir_oracle.c``) of the
+  reference algorithms, the parity checker for every HIP kernel;
+* ``_ref/libmimir_ref.so`` -- the reference's own op functions compiled in
+  place (``ref_harness.cpp``), used to pin the restatement.  It exists only
+  where it was built from a reference tree; :func:`ref_available` says so.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from ctypes import POINTER, c_double, c_float, c_int32, c_int64, c_void_p
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ORACLE_SO = os.path.join(HERE, "lib", "libmimir_oracle.so")
+REF_SO = os.path.join(HERE, "_ref", "libmimir_ref.so")
+
+SOFTMAX_DIV_EPS = 0  # LayerOps::softmax_inplace, LayerOps.hpp:952-974
+SOFTMAX_MUL_INV = 1  # LayerOps::softmax_forward, LayerOps.hpp:325-361
+SOFTMAX_LOG = 2      # LogSoftmax branch, LayerOps.hpp:345-353
+
+
+class OracleError(RuntimeError):
+    """Raised where the reference throws std::runtime_error (status 1)."""
+
+
+def _load(path):
+    if not os.path.exists(path):
+        raise FileNotFoundError(f"{path} is not built (run `make -C oracle`)")
+    return ctypes.CDLL(path)
+
+
+_o = None
+_r = None
+
+
+def _oracle():
+    global _o
+    if _o is None:
+        lib = _load(ORACLE_SO)
+        P = c_void_p
+        sig = {
+            "oracle_layernorm": [P, c_int64, c_int64, P, P, c_float, P],
+            "oracle_rmsnorm_whole": [P, c_int64, P, c_int64, c_float, P],
+            "oracle_rmsnorm_rows": [P, c_int64, c_int64, P, c_float, P],
+            "oracle_add_rmsnorm": [P, P, c_int64, c_int64, P, c_float, P, P],
+            "oracle_add": [P, c_int64, P, c_int64, P],
+            "oracle_mul": [P, c_int64, P, c_int64, P],
+            "oracle_softmax_rows": [P, c_int64, c_int64, c_int32, P],
+            "oracle_gelu": [P, c_int64, P],
+            "oracle_silu": [P, c_int64, P],
+            "oracle_silu_mul": [P, P, c_int64, P],
+            "oracle_gelu_mul": [P, P, c_int64, P],
+            "oracle_embedding_i32": [P, c_int64, P, c_int64, c_int32, c_int32, c_int32, P],
+            "oracle_embedding_f32": [P, c_int64, P, c_int64, c_int32, c_int32, c_int32, P],
+            "oracle_rope_table": [c_int64, c_int64, c_double, P, P],
+            "oracle_rope": [P, P, c_int64, c_int64, c_int64, c_int64, c_int64, P, P, c_int64],
+        }
+        for name, args in sig.items():
+            fn = getattr(lib, name)
+            fn.argtypes = args
+            fn.restype = None if name in ("oracle_gelu", "oracle_silu", "oracle_silu_mul",
+                                          "oracle_gelu_mul") else c_int32
+        _o = lib
+    return _o
+
+
+def ref_available() -> bool:
+    return os.path.exists(REF_SO)
+
+
+def _ref():
+    global _r
+    if _r is None:
+        lib = _load(REF_SO)
+        P = c_void_p
+        sig = {
+            "ref_layernorm": [P, c_int64, c_int32, P, c_int64, c_int32, c_int32, c_float, P],
+            "ref_rms_norm_forward": [P, c_int64, P, c_int64, c_int32, c_float, P],
+            "ref_rms_norm_rows": [P, c_int64, c_int64, P, c_float, P],
+            "ref_add": [P, c_int64, P, c_int64, P],
+            "ref_mul": [P, c_int64, P, c_int64, P],
+            "ref_softmax_inplace": [P, c_int64, c_int64, P],
+            "ref_softmax_forward": [P, c_int64, c_int32, P],
+            "ref_gelu": [P, c_int64, P],
+            "ref_silu": [P, c_int64, P],
+        }
+        for name, args in sig.items():
+            fn = getattr(lib, name)
+            fn.argtypes = args
+            fn.restype = c_int32
+        _r = lib
+    return _r
+
+
+def _f32(a):
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def _p(a):
+    return None if a is None else a.ctypes.data_as(c_void_p)
+
+
+def _check(status, what):
+    if status:
+        raise OracleError(f"{what}: invalid argument")
+
+
+# --------------------------------------------------------------------------
+# C restatement
+# --------------------------------------------------------------------------
+
+def layernorm(x, in_features, gamma=None, beta=None, eps=1e-5):
+    x = _f32(x).ravel()
+    g = None if gamma is None else _f32(gamma)
+    b = None if beta is None else _f32(beta)
+    y = np.empty_like(x)
+    _check(_oracle().oracle_layernorm(_p(x), x.size, int(in_features), _p(g), _p(b),
+                                      eps, _p(y)), "layernorm")
+    return y
+
+
+def rmsnorm_whole(x, w=None, eps=1e-5):
+    x = _f32(x).ravel()
+    w = None if w is None else _f32(w)
+    y = np.empty_like(x)
+    _check(_oracle().oracle_rmsnorm_whole(_p(x), x.size, _p(w), 0 if w is None else w.size,
+                                          eps, _p(y)), "rmsnorm_whole")
+    return y
+
+
+def rmsnorm_rows(x, gamma=None, eps=1e-6):
+    x = _f32(x)
+    rows, cols = x.shape
+    g = None if gamma is None else _f32(gamma)
+    y = np.empty_like(x)
+    _check(_oracle().oracle_rmsnorm_rows(_p(x), rows, cols, _p(g), eps, _p(y)), "rmsnorm_rows")
+    return y
+
+
+def add_rmsnorm(x, residual, gamma=None, eps=1e-6):
+    x = _f32(x)
+    r = _f32(residual)
+    rows, cols = x.shape
+    g = None if gamma is None else _f32(gamma)
+    h = np.empty_like(x)
+    y = np.empty_like(x)
+    _check(_oracle().oracle_add_rmsnorm(_p(x), _p(r), rows, cols, _p(g), eps, _p(h), _p(y)),
+           "add_rmsnorm")
+    return y, h
+
+
+def add(a, b):
+    a = _f32(a).ravel()
+    b = _f32(b).ravel()
+    y = np.empty(max(a.size, b.size), np.float32)
+    _check(_oracle().oracle_add(_p(a), a.size, _p(b), b.size, _p(y)), "add")
+    return y
+
+
+def mul(a, b):
+    a = _f32(a).ravel()
+    b = _f32(b).ravel()
+    y = np.empty(a.size, np.float32)
+    _check(_oracle().oracle_mul(_p(a), a.size, _p(b), b.size, _p(y)), "mul")
+    return y
+
+
+def softmax_rows(x, mode=SOFTMAX_DIV_EPS):
+    x = _f32(x)
+    if x.ndim == 1:
+        x = x.reshape(1, -1)
+    rows, cols = x.shape
+    y = np.empty_like(x)
+    _check(_oracle().oracle_softmax_rows(_p(x), rows, cols, mode, _p(y)), "softmax_rows")
+    return y
+
+
+def _unary(name, x):
+    x = _f32(x)
+    y = np.empty_like(x)
+    getattr(_oracle(), name)(_p(x), x.size, _p(y))
+    return y
+
+
+def gelu(x):
+    return _unary("oracle_gelu", x)
+
+
+def silu(x):
+    return _unary("oracle_silu", x)
+
+
+def silu_mul(gate, up):
+    g, u = _f32(gate), _f32(up)
+    y = np.empty_like(g)
+    _oracle().oracle_silu_mul(_p(g), _p(u), g.size, _p(y))
+    return y
+
+
+def gelu_mul(gate, up):
+    g, u = _f32(gate), _f32(up)
+    y = np.empty_like(g)
+    _oracle().oracle_gelu_mul(_p(g), _p(u), g.size, _p(y))
+    return y
+
+
+def embedding(ids, table, vocab, dim, padding_idx=-1):
+    table = _f32(table).ravel()
+    ids = np.asarray(ids)
+    n = ids.size
+    d = max(1, int(dim))
+    y = np.empty(n * d, np.float32)
+    if ids.dtype == np.float32:
+        ids = np.ascontiguousarray(ids).ravel()
+        st = _oracle().oracle_embedding_f32(_p(ids), n, _p(table), table.size, int(vocab),
+                                            int(dim), int(padding_idx), _p(y))
+    else:
+        ids = np.ascontiguousarray(ids, dtype=np.int32).ravel()
+        st = _oracle().oracle_embedding_i32(_p(ids), n, _p(table), table.size, int(vocab),
+                                            int(dim), int(padding_idx), _p(y))
+    _check(st, "embedding")
+    return y.reshape(n, d)
+
+
+def rope_table(rows, head_dim, theta=10000.0):
+    half = head_dim // 2
+    c = np.empty((rows, half), np.float32)
+    s = np.empty((rows, half), np.float32)
+    _check(_oracle().oracle_rope_table(rows, head_dim, theta, _p(c), _p(s)), "rope_table")
+    return c, s
+
+
+def rope(x, cos_tab, sin_tab, pos_offset=0):
+    x = _f32(x)
+    B, S, H, D = x.shape
+    c, s = _f32(cos_tab), _f32(sin_tab)
+    y = np.empty_like(x)
+    _check(_oracle().oracle_rope(_p(x), _p(y), B, S, H, D, pos_offset, _p(c), _p(s),
+                                 c.shape[0]), "rope")
+    return y
+
+
+# --------------------------------------------------------------------------
+# The reference's own functions (compiled in place)
+# --------------------------------------------------------------------------
+
+def ref_layernorm(x, in_features, params=None, affine=True, use_bias=True, eps=1e-5):
+    x = _f32(x).ravel()
+    p = np.zeros(0, np.float32) if params is None else _f32(params)
+    y = np.empty_like(x)
+    _check(_ref().ref_layernorm(_p(x), x.size, int(in_features), _p(p), p.size, int(affine),
+                                int(use_bias), eps, _p(y)), "ref_layernorm")
+    return y
+
+
+def ref_rms_norm_forward(x, w=None, affine=True, eps=1e-5):
+    x = _f32(x).ravel()
+    w = np.zeros(0, np.float32) if w is None else _f32(w)
+    y = np.empty_like(x)
+    _check(_ref().ref_rms_norm_forward(_p(x), x.size, _p(w), w.size, int(affine), eps, _p(y)),
+           "ref_rms_norm_forward")
+    return y
+
+
+def ref_rms_norm_rows(x, gamma, eps=1e-6):
+    x = _f32(x)
+    rows, cols = x.shape
+    g = _f32(gamma)
+    y = np.empty_like(x)
+    _check(_ref().ref_rms_norm_rows(_p(x), rows, cols, _p(g), eps, _p(y)), "ref_rms_norm_rows")
+    return y
+
+
+def ref_add(a, b):
+    a = _f32(a).ravel()
+    b = _f32(b).ravel()
+    y = np.empty(max(a.size, b.size), np.float32)
+    _check(_ref().ref_add(_p(a), a.size, _p(b), b.size, _p(y)), "ref_add")
+    return y
+
+
+def ref_mul(a, b):
+    a = _f32(a).ravel()
+    b = _f32(b).ravel()
+    y = np.empty(a.size, np.float32)
+    _check(_ref().ref_mul(_p(a), a.size, _p(b), b.size, _p(y)), "ref_mul")
+    return y
+
+
+def ref_softmax_inplace(x):
+    x = _f32(x)
+    rows, cols = x.shape
+    y = np.empty_like(x)
+    _check(_ref().ref_softmax_inplace(_p(x), rows, cols, _p(y)), "ref_softmax_inplace")
+    return y
+
+
+def ref_softmax_forward(x, log_softmax=False):
+    x = _f32(x).ravel()
+    y = np.empty_like(x)
+    _check(_ref().ref_softmax_forward(_p(x), x.size, int(log_softmax), _p(y)),
+           "ref_softmax_forward")
+    return y
+
+
+def ref_gelu(x):
+    x = _f32(x).ravel()
+    y = np.empty_like(x)
+    _check(_ref().ref_gelu(_p(x), x.size, _p(y)), "ref_gelu")
+    return y
+
+
+def ref_silu(x):
+    x = _f32(x).ravel()
+    y = np.empty_like(x)
+    _check(_ref().ref_silu(_p(x), x.size, _p(y)), "ref_silu")
+    return y
+
+
+# --------------------------------------------------------------------------
+# CPU baseline timing (bench.py's cpu_baseline leg)
+# --------------------------------------------------------------------------
+
+REF_T_ADD_RMSNORM, REF_T_LAYERNORM, REF_T_SOFTMAX, REF_T_GELU, REF_T_SILU_MUL, REF_T_ADD = range(6)
+
+
+def ref_time_op(op, a, b=None, w=None, rows=0, cols=0, eps=1e-5, reps=3):
+    """Median seconds of one call of the reference path `op` (ref_harness.cpp)."""
+    lib = _ref()
+    fn = lib.ref_time_op
+    fn.argtypes = [c_int32, c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_int64, c_int64,
+                   c_int64, c_float, c_int32]
+    fn.restype = c_double
+    a = _f32(a).ravel()
+    b = np.zeros(0, np.float32) if b is None else _f32(b).ravel()
+    w = np.zeros(0, np.float32) if w is None else _f32(w).ravel()
+    t = fn(op, _p(a), a.size, _p(b), b.size, _p(w), w.size, rows, cols, eps, reps)
+    if t < 0:
+        raise OracleError(f"ref_time_op({op}) failed")
+    return t
+
+
+def time_port(fn, reps=3):
+    """Median seconds of fn() (a call into the C restatement) after one warm-up."""
+    import time
+    fn()
+    ts = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    return sorted(ts)[len(ts) // 2]

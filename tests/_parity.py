@@ -1,0 +1,55 @@
+"""Parity predicates shared by the tests.
+
+Tolerance: an element passes when
+|got - ref| <= max(1e-6, 1e-5 * |ref|); NaN must meet NaN and +-inf the same
+infinity.  Integer / byte / copy results are compared bit for bit.
+"""
+import numpy as np
+
+REL = 1e-5
+ABS = 1e-6
+
+
+def err_stats(got, ref):
+    g = np.asarray(got, np.float64).ravel()
+    r = np.asarray(ref, np.float64).ravel()
+    fin = np.isfinite(r)
+    d = np.abs(g[fin] - r[fin])
+    tol = np.maximum(ABS, REL * np.abs(r[fin]))
+    if d.size == 0:
+        return 0.0, 0.0, 0.0
+    rel = d / np.maximum(np.abs(r[fin]), 1e-30)
+    return float(d.max()), float(rel.max()), float((d / tol).max())
+
+
+def assert_close(got, ref, what="", rel=REL, abs_=ABS):
+    got = np.asarray(got)
+    ref = np.asarray(ref)
+    assert got.shape == ref.shape, f"{what}: shape {got.shape} != {ref.shape}"
+    g = got.astype(np.float64).ravel()
+    r = ref.astype(np.float64).ravel()
+    nan_r = np.isnan(r)
+    assert np.array_equal(np.isnan(g), nan_r), f"{what}: NaN pattern differs"
+    inf_r = np.isinf(r)
+    assert np.array_equal(g[inf_r], r[inf_r]) and not np.isinf(g[~inf_r]).any(), \
+        f"{what}: infinities differ"
+    fin = np.isfinite(r)
+    d = np.abs(g[fin] - r[fin])
+    tol = np.maximum(abs_, rel * np.abs(r[fin]))
+    bad = d > tol
+    if bad.any():
+        idx = np.flatnonzero(fin)[np.argmax(d / tol)]
+        raise AssertionError(
+            f"{what}: {int(bad.sum())} of {fin.sum()} elements out of tolerance; worst at flat "
+            f"index {idx}: got {g[idx]!r} ref {r[idx]!r} (|d|={abs(g[idx]-r[idx]):.3g})")
+
+
+def assert_bitexact(got, ref, what=""):
+    got = np.ascontiguousarray(got)
+    ref = np.ascontiguousarray(ref)
+    assert got.shape == ref.shape, f"{what}: shape {got.shape} != {ref.shape}"
+    gv = got.view(np.uint32) if got.dtype.itemsize == 4 else got.view(np.uint8)
+    rv = ref.view(np.uint32) if ref.dtype.itemsize == 4 else ref.view(np.uint8)
+    diff = np.flatnonzero(gv.ravel() != rv.ravel())
+    assert diff.size == 0, (f"{what}: {diff.size} elements differ bitwise; first at {diff[0]}: "
+                            f"got {got.ravel()[diff[0]]!r} ref {ref.ravel()[diff[0]]!r}")

@@ -1,0 +1,66 @@
+"""CPU checks of the C ABI boundary: the library loads without a GPU, exports
+exactly the entry points include/mimir_hip.h declares (and the Python binding
+declares the same set), and the host-side helpers match the oracle."""
+import os
+import re
+
+import numpy as np
+import pytest
+
+import mimir_hip as M
+import oracle as O
+from _parity import assert_bitexact
+
+
+def header_functions():
+    text = open(M.HEADER_PATH).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(mimir_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declares_the_binding_set():
+    assert header_functions() == sorted(M.SIGNATURES)
+
+
+def test_library_exports_every_declared_symbol():
+    lib = M.load()
+    missing = [n for n in header_functions() if not hasattr(lib, n)]
+    assert not missing, f"not exported: {missing}"
+
+
+def test_context_without_device_fails_cleanly():
+    # No GPU in the CPU test environment: ctx creation reports EDEVICE (or
+    # succeeds on a GPU host); it must never crash.
+    lib = M.load()
+    from ctypes import byref, c_void_p
+    h = c_void_p()
+    st = lib.mimir_ctx_create(0, byref(h))
+    assert st in (M.OK, M.EDEVICE)
+    if st == M.OK:
+        lib.mimir_ctx_destroy(h)
+    assert lib.mimir_ctx_create(-1, byref(h)) in (M.EINVAL, M.EDEVICE)
+
+
+def test_null_context_is_einval():
+    lib = M.load()
+    assert lib.mimir_gelu_fwd(None, None, None, 4) == M.EINVAL
+    assert lib.mimir_sync(None) == M.EINVAL
+    assert lib.mimir_last_error(None) == b"null context"
+
+
+@pytest.mark.parametrize("rows,D", [(2048, 128), (17, 6), (4, 512), (0, 8)])
+def test_rope_table_matches_oracle(rows, D):
+    c, s = M.rope_table(rows, D)
+    oc, os_ = O.rope_table(rows, D)
+    assert_bitexact(c, oc, "cos")
+    assert_bitexact(s, os_, "sin")
+
+
+def test_rope_table_rejects_odd_dim():
+    with pytest.raises(M.MimirError):
+        M.rope_table(4, 7)
+
+
+def test_cpp_adapter_program_built():
+    kat = os.path.join(os.path.dirname(M.LIB_PATH), "test_layerops_hip")
+    assert os.path.exists(kat), "C++ adapter KAT program not built"
