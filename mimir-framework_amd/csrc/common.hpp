@@ -13,7 +13,7 @@
 namespace mimir {
 
 constexpr int kWave = 64;
-constexpr int kBlock = 256;  // every kernel here launches 256-thread workgroups
+constexpr int kBlock = 256;  // workgroup size of the streaming kernels (row kernels pick their own)
 
 typedef float f4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u4 __attribute__((ext_vector_type(4)));
@@ -72,42 +72,51 @@ __device__ __forceinline__ float wave_max(float v) {
     return fmaxf(fmaxf(readlane(v, 0), readlane(v, 16)), fmaxf(readlane(v, 32), readlane(v, 48)));
 }
 
-// Block-wide reductions for rows spread over NW waves.  `lds` must hold NW
-// floats and not be reused by another reduction until the caller syncs again
-// (each call ends with every thread having read the partials; the leading
-// barrier of the next call orders the reuse).
-template <int NW>
-__device__ __forceinline__ float block_sum(float v, float* lds) {
+// Reductions for a row spread over NW waves of a workgroup that holds
+// several rows (row `sub` owns waves sub*NW .. sub*NW+NW-1).  `lds` holds one
+// float per wave of the workgroup.  REUSE adds a leading barrier, needed when
+// the same `lds` array served an earlier reduction of the kernel.
+template <int NW, bool REUSE = true>
+__device__ __forceinline__ float row_sum(float v, float* lds, int sub) {
     const float w = wave_sum(v);
     if constexpr (NW == 1) {
         return w;
     } else {
-        const int wid = threadIdx.x / kWave;
+        if constexpr (REUSE) __syncthreads();
+        if ((threadIdx.x & (kWave - 1)) == 0) lds[threadIdx.x / kWave] = w;
         __syncthreads();
-        if ((threadIdx.x & (kWave - 1)) == 0) lds[wid] = w;
-        __syncthreads();
-        float s = lds[0];
+        float s = lds[sub * NW];
 #pragma unroll
-        for (int i = 1; i < NW; ++i) s += lds[i];
+        for (int i = 1; i < NW; ++i) s += lds[sub * NW + i];
         return s;
     }
 }
 
 template <int NW>
-__device__ __forceinline__ float block_max(float v, float* lds) {
+__device__ __forceinline__ float row_max(float v, float* lds, int sub) {
     const float w = wave_max(v);
     if constexpr (NW == 1) {
         return w;
     } else {
-        const int wid = threadIdx.x / kWave;
         __syncthreads();
-        if ((threadIdx.x & (kWave - 1)) == 0) lds[wid] = w;
+        if ((threadIdx.x & (kWave - 1)) == 0) lds[threadIdx.x / kWave] = w;
         __syncthreads();
-        float s = lds[0];
+        float s = lds[sub * NW];
 #pragma unroll
-        for (int i = 1; i < NW; ++i) s = fmaxf(s, lds[i]);
+        for (int i = 1; i < NW; ++i) s = fmaxf(s, lds[sub * NW + i]);
         return s;
     }
+}
+
+// Whole-workgroup reductions (one row per workgroup of NW waves).
+template <int NW>
+__device__ __forceinline__ float block_sum(float v, float* lds) {
+    return row_sum<NW>(v, lds, 0);
+}
+
+template <int NW>
+__device__ __forceinline__ float block_max(float v, float* lds) {
+    return row_max<NW>(v, lds, 0);
 }
 
 }  // namespace mimir

@@ -5,7 +5,8 @@
 // workgroup-width apart (so each wave instruction moves 1 KiB of contiguous
 // data), issues all its loads before any arithmetic, and writes with
 // non-temporal stores: every input byte is read once and every output byte
-// written once.  Buffers that are not 16-byte aligned, and the n % 4 tail,
+// written once.  VPT = 1 (one vector per thread, many waves in flight)
+// streams fastest on MI355X; 2 and 4 stay available for sweeps (MIMIR_TUNE).  Buffers that are not 16-byte aligned, and the n % 4 tail,
 // run through a scalar grid-stride kernel with the same per-element functor.
 #include "common.hpp"
 #include "internal.hpp"
@@ -16,17 +17,26 @@ using namespace mimir;
 
 namespace {
 
-// LayerOps::gelu_forward, LayerOps.hpp:556-568.  The constant is the float
-// sqrt of the float quotient, as in the reference (correctly rounded sqrt).
+// LayerOps::gelu_forward, LayerOps.hpp:556-568, computes
+//   y = x * 0.5f*(1 + tanhf(u)),  u = sqrt(2/pi)*(x + 0.044715f*x^3)
+// with the float sqrt of the float quotient as the constant.  Since
+// 0.5*(1 + tanh(u)) = 1/(1 + exp(-2u)) exactly, the kernel evaluates the
+// logistic form: one expf and one hardware reciprocal (v_rcp_f32, 1 ulp)
+// instead of the branchy tanhf, which left the op compute-bound on MI355X.
+// It is also the better-conditioned form: the reference's 1 + tanhf(u)
+// cancels for x < -3 (absolute error <= 1.5e-7 there), so the two agree to
+// the path's tolerance everywhere, including the -0 / +-inf / NaN cases
+// (exp overflow gives x * 0).
 __device__ __forceinline__ float gelu1(float x) {
     const float k = __builtin_sqrtf(2.0f / 3.14159265359f);
-    const float cdf = 0.5f * (1.0f + tanhf(k * (x + 0.044715f * x * x * x)));
-    return x * cdf;
+    const float u = k * (x + 0.044715f * x * x * x);
+    return x * __builtin_amdgcn_rcpf(1.0f + expf(-2.0f * u));
 }
 
-// LayerOps::silu_forward, LayerOps.hpp:570-581.
+// LayerOps::silu_forward, LayerOps.hpp:570-581: y = x * (1/(1 + exp(-x))),
+// with the reciprocal taken by v_rcp_f32 (1 ulp).
 __device__ __forceinline__ float silu1(float x) {
-    const float sigmoid = 1.0f / (1.0f + expf(-x));
+    const float sigmoid = __builtin_amdgcn_rcpf(1.0f + expf(-x));
     return x * sigmoid;
 }
 
@@ -50,8 +60,6 @@ struct Add {
 struct Mul {
     __device__ float operator()(float a, float b) const { return a * b; }
 };
-
-constexpr int kVpt = 4;  // 16-byte vectors per thread (64 B of each input in flight)
 
 template <class F>
 __device__ __forceinline__ f4 map4(F f, f4 a) {
@@ -148,17 +156,38 @@ unsigned stride_grid(int64_t n) {
     return static_cast<unsigned>(b < 1 ? 1 : (b > 65536 ? 65536 : b));
 }
 
+template <class F, int VPT>
+int launch_unary(mimir_ctx* ctx, const float* x, float* y, int64_t n4, F f, const char* name) {
+    unsigned blocks;
+    if (!grid_for(n4, static_cast<int64_t>(VPT) * kBlock, &blocks))
+        return fail(ctx, MIMIR_EINVAL, "%s: n=%lld exceeds the grid limit", name, (long long)(4 * n4));
+    unary_vec<F, VPT><<<blocks, kBlock, 0, ctx->stream>>>(x, y, n4, f);
+    return launched(ctx, name);
+}
+
+template <class F, int VPT>
+int launch_binary(mimir_ctx* ctx, const float* a, const float* b, float* y, int64_t n4, F f,
+                  const char* name) {
+    unsigned blocks;
+    if (!grid_for(n4, static_cast<int64_t>(VPT) * kBlock, &blocks))
+        return fail(ctx, MIMIR_EINVAL, "%s: n=%lld exceeds the grid limit", name, (long long)(4 * n4));
+    binary_vec<F, VPT><<<blocks, kBlock, 0, ctx->stream>>>(a, b, y, n4, f);
+    return launched(ctx, name);
+}
+
 template <class F>
 int run_unary(mimir_ctx* ctx, const float* x, float* y, int64_t n, F f, const char* name) {
     int64_t done = 0;
     if (aligned16(x) && aligned16(y)) {
         const int64_t n4 = n / 4;
         if (n4 > 0) {
-            unsigned blocks;
-            if (!grid_for(n4, static_cast<int64_t>(kVpt) * kBlock, &blocks))
-                return fail(ctx, MIMIR_EINVAL, "%s: n=%lld exceeds the grid limit", name, (long long)n);
-            unary_vec<F, kVpt><<<blocks, kBlock, 0, ctx->stream>>>(x, y, n4, f);
-            if (int st = launched(ctx, name)) return st;
+            int st;
+            switch (ctx->tune.ew_vpt) {
+                case 2: st = launch_unary<F, 2>(ctx, x, y, n4, f, name); break;
+                case 4: st = launch_unary<F, 4>(ctx, x, y, n4, f, name); break;
+                default: st = launch_unary<F, 1>(ctx, x, y, n4, f, name); break;
+            }
+            if (st) return st;
         }
         done = n4 * 4;
     }
@@ -176,11 +205,13 @@ int run_binary(mimir_ctx* ctx, const float* a, const float* b, float* y, int64_t
     if (aligned16(a) && aligned16(b) && aligned16(y)) {
         const int64_t n4 = n / 4;
         if (n4 > 0) {
-            unsigned blocks;
-            if (!grid_for(n4, static_cast<int64_t>(kVpt) * kBlock, &blocks))
-                return fail(ctx, MIMIR_EINVAL, "%s: n=%lld exceeds the grid limit", name, (long long)n);
-            binary_vec<F, kVpt><<<blocks, kBlock, 0, ctx->stream>>>(a, b, y, n4, f);
-            if (int st = launched(ctx, name)) return st;
+            int st;
+            switch (ctx->tune.ew_vpt) {
+                case 2: st = launch_binary<F, 2>(ctx, a, b, y, n4, f, name); break;
+                case 4: st = launch_binary<F, 4>(ctx, a, b, y, n4, f, name); break;
+                default: st = launch_binary<F, 1>(ctx, a, b, y, n4, f, name); break;
+            }
+            if (st) return st;
         }
         done = n4 * 4;
     }

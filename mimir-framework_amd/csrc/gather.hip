@@ -1,8 +1,9 @@
 // gather.hip -- token-embedding gather for gfx950 (bit-exact).
 //
-// One wavefront per token row: the id is read once per wave (wave-uniform),
-// then the 64 lanes move the row as 16-byte vectors, VPT per lane, loads
-// issued before stores.  Rows of padding / out-of-range ids are written as
+// One workgroup (or a slice of one, for narrow rows) per token row: the id
+// is read once per wave (wave-uniform), then the threads move the row as
+// 16-byte vectors, one per thread per pass -- for the 4096-wide rows of the
+// benchmark, 1024 threads each moving one vector.  Rows of padding / out-of-range ids are written as
 // zeros without touching the table.  Payload moves as raw 32-bit words, so
 // every bit pattern (NaN payloads, -0, denormals) is copied unchanged.
 //
@@ -47,29 +48,20 @@ struct GatherArgs {
 
 constexpr int kWavesPerBlock = kBlock / kWave;
 
-template <bool FLOAT_IDS, int VPT>
-__global__ __launch_bounds__(kBlock) void embed_vec(GatherArgs a) {
-    const int lane = threadIdx.x & (kWave - 1);
-    const int64_t token = static_cast<int64_t>(blockIdx.x) * kWavesPerBlock + threadIdx.x / kWave;
-    if (token >= a.n_ids) return;
+// TPT threads per token row (BS / TPT token rows per workgroup), one 16-byte
+// vector per thread per pass; rows wider than TPT vectors take several passes.
+template <bool FLOAT_IDS, int TPT, int BS>
+__global__ __launch_bounds__(BS) void embed_vec(GatherArgs a) {
+    const int t = threadIdx.x % TPT;
+    const int64_t token = static_cast<int64_t>(blockIdx.x) * (BS / TPT) + threadIdx.x / TPT;
+    if (token >= a.n_ids) return;  // no barriers in this kernel
     const int32_t id = load_id<FLOAT_IDS>(a.ids, token);
     const bool copy = !(a.pad >= 0 && id == a.pad) && id >= 0 && id < a.vocab;
     const int64_t dim4 = a.dim >> 2;
     const u4* src = reinterpret_cast<const u4*>(a.table) + (copy ? static_cast<int64_t>(id) * dim4 : 0);
     u4* dst = reinterpret_cast<u4*>(a.y) + token * dim4;
-    for (int64_t c0 = 0; c0 < dim4; c0 += static_cast<int64_t>(VPT) * kWave) {
-        u4 v[VPT];
-#pragma unroll
-        for (int j = 0; j < VPT; ++j) {
-            const int64_t c = c0 + static_cast<int64_t>(j) * kWave + lane;
-            v[j] = (copy && c < dim4) ? __builtin_nontemporal_load(src + c) : u4(0u);
-        }
-#pragma unroll
-        for (int j = 0; j < VPT; ++j) {
-            const int64_t c = c0 + static_cast<int64_t>(j) * kWave + lane;
-            if (c < dim4) __builtin_nontemporal_store(v[j], dst + c);
-        }
-    }
+    for (int64_t c = t; c < dim4; c += TPT)
+        __builtin_nontemporal_store(copy ? __builtin_nontemporal_load(src + c) : u4(0u), dst + c);
 }
 
 // Any dim / alignment: one wavefront per token, 32-bit words.
@@ -105,10 +97,20 @@ int run(mimir_ctx* ctx, const void* ids, int64_t n_ids, const float* table, int6
         return fail(ctx, MIMIR_EINVAL, "Embedding: %lld ids exceed the grid limit", (long long)n_ids);
     if (dim % 4 == 0 && aligned16(table) && aligned16(y)) {
         const int64_t dim4 = dim / 4;
-        if (dim4 <= 64) embed_vec<FLOAT_IDS, 1><<<blocks, kBlock, 0, ctx->stream>>>(a);
-        else if (dim4 <= 256) embed_vec<FLOAT_IDS, 4><<<blocks, kBlock, 0, ctx->stream>>>(a);
-        else if (dim4 <= 512) embed_vec<FLOAT_IDS, 8><<<blocks, kBlock, 0, ctx->stream>>>(a);
-        else embed_vec<FLOAT_IDS, 16><<<blocks, kBlock, 0, ctx->stream>>>(a);
+        int tpt = ctx->tune.gather_tpt;
+        if (tpt != 64 && tpt != 128 && tpt != 256 && tpt != 512 && tpt != 1024)
+            tpt = dim4 <= 64 ? 64 : dim4 <= 128 ? 128 : dim4 <= 256 ? 256 : dim4 <= 512 ? 512 : 1024;
+        const int bs = tpt < kBlock ? kBlock : tpt;
+        unsigned vb;
+        if (!grid_for(n_ids, bs / tpt, &vb))
+            return fail(ctx, MIMIR_EINVAL, "Embedding: %lld ids exceed the grid limit", (long long)n_ids);
+        switch (tpt) {
+            case 64: embed_vec<FLOAT_IDS, 64, 256><<<vb, 256, 0, ctx->stream>>>(a); break;
+            case 128: embed_vec<FLOAT_IDS, 128, 256><<<vb, 256, 0, ctx->stream>>>(a); break;
+            case 256: embed_vec<FLOAT_IDS, 256, 256><<<vb, 256, 0, ctx->stream>>>(a); break;
+            case 512: embed_vec<FLOAT_IDS, 512, 512><<<vb, 512, 0, ctx->stream>>>(a); break;
+            default: embed_vec<FLOAT_IDS, 1024, 1024><<<vb, 1024, 0, ctx->stream>>>(a); break;
+        }
         return launched(ctx, "embed_vec");
     }
     embed_scalar<FLOAT_IDS><<<blocks, kBlock, 0, ctx->stream>>>(a);

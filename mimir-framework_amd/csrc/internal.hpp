@@ -11,6 +11,7 @@
 #include <unordered_map>
 
 #include "../../include/mimir_hip.h"
+#include "rows.hpp"
 
 struct mimir_ctx {
     int device = 0;
@@ -20,6 +21,7 @@ struct mimir_ctx {
     size_t alloc_used = 0;
     std::unordered_map<void*, size_t> allocs;
     std::string last_error;
+    mimir::Tuning tune;  // launch-shape override (MIMIR_TUNE), read at creation
 };
 
 struct mimir_event {

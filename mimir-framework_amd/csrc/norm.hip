@@ -1,11 +1,11 @@
 // norm.hip -- LayerNorm, RMSNorm and residual-add + RMSNorm for gfx950.
 //
-// Row layout: a row of `cols` fp32 is held in VGPRs by TPR threads (64 = one
-// wavefront, 256 = the whole workgroup), each owning VPT 16-byte vectors at
-// float4 columns t, t+TPR, t+2*TPR, ... so every load instruction of a wave
-// covers 1 KiB of contiguous row.  Each input byte crosses HBM once: the row
-// is loaded, reduced (DPP wave reductions, LDS only for the 4-wave combine)
-// and written from registers.  Rows that do not fit that register budget, or
+// Row layout (rows.hpp): a row of `cols` fp32 is held in VGPRs by TPR
+// threads, each owning VPT 16-byte vectors at float4 columns t, t+TPR, ...,
+// so every load instruction of a wave covers 1 KiB of contiguous row.  Each
+// input byte crosses HBM once: the row is loaded, reduced (DPP wave
+// reductions, LDS only to combine the waves of one row) and written from
+// registers.  Rows that do not fit that register budget, or
 // whose width is not a multiple of 4 / whose buffers are not 16-byte aligned,
 // take the generic kernel: one workgroup per row, scalar strided passes.
 //
@@ -53,19 +53,25 @@ __device__ __forceinline__ f4 rms_scale(f4 o, const float* w, int64_t w_len, int
     return o;
 }
 
-template <Norm K, int TPR, int VPT, bool NT>
-__global__ __launch_bounds__(kBlock) void norm_rows_vec(NormArgs a) {
-    constexpr int RPB = kBlock / TPR;  // rows per workgroup
-    constexpr int NW = TPR / kWave;    // waves per row
-    __shared__ float lds[2][NW];
+template <Norm K, int TPR, int VPT, int BS>
+__global__ __launch_bounds__(BS) void norm_rows_vec(NormArgs a) {
+    constexpr int RPB = BS / TPR;  // rows per workgroup
+    constexpr int NW = TPR / kWave;  // waves per row
+    __shared__ float lds[2][BS / kWave];
     const int t = threadIdx.x % TPR;
-    const int64_t row = static_cast<int64_t>(blockIdx.x) * RPB + threadIdx.x / TPR;
+    const int sub = threadIdx.x / TPR;
+    const int64_t row = static_cast<int64_t>(blockIdx.x) * RPB + sub;
     if constexpr (NW == 1) {
         if (row >= a.rows) return;  // whole wavefront leaves together
     }
-    const int64_t c4n = a.cols >> 2;
+    // Rows past the end (only in the last workgroup) keep taking part in the
+    // workgroup barriers but touch no memory.
+    const int64_t c4n = row < a.rows ? (a.cols >> 2) : 0;
     const int64_t base = row * a.cols;
 
+    // LayerNorm: issue the row's loads at raised wave priority, so the loads
+    // of resident rows are not held up behind other waves' reduction math.
+    if constexpr (K == Norm::Layer) __builtin_amdgcn_s_setprio(3);
     f4 v[VPT];
     if constexpr (K == Norm::AddRms) {
         f4 rr[VPT];
@@ -73,29 +79,31 @@ __global__ __launch_bounds__(kBlock) void norm_rows_vec(NormArgs a) {
         for (int j = 0; j < VPT; ++j) {
             const int64_t c4 = static_cast<int64_t>(j) * TPR + t;
             const bool ok = c4 < c4n;
-            v[j] = ok ? ld4<NT>(a.x + base + 4 * c4) : f4(0.0f);
-            rr[j] = ok ? ld4<NT>(a.r + base + 4 * c4) : f4(0.0f);
+            v[j] = ok ? ld4<true>(a.x + base + 4 * c4) : f4(0.0f);
+            rr[j] = ok ? ld4<true>(a.r + base + 4 * c4) : f4(0.0f);
         }
 #pragma unroll
         for (int j = 0; j < VPT; ++j) {
             const int64_t c4 = static_cast<int64_t>(j) * TPR + t;
             v[j] = v[j] + rr[j];  // one IEEE add per element, as add_forward
-            if (c4 < c4n) st4<NT>(a.r_out + base + 4 * c4, v[j]);
+            if (c4 < c4n) st4<true>(a.r_out + base + 4 * c4, v[j]);
         }
     } else {
 #pragma unroll
         for (int j = 0; j < VPT; ++j) {
             const int64_t c4 = static_cast<int64_t>(j) * TPR + t;
-            v[j] = (c4 < c4n) ? ld4<NT>(a.x + base + 4 * c4) : f4(0.0f);
+            v[j] = (c4 < c4n) ? ld4<true>(a.x + base + 4 * c4) : f4(0.0f);
         }
     }
+
+    if constexpr (K == Norm::Layer) __builtin_amdgcn_s_setprio(0);
 
     const float n = static_cast<float>(a.cols);
     if constexpr (K == Norm::Layer) {
         float s = 0.0f;
 #pragma unroll
         for (int j = 0; j < VPT; ++j) s += (v[j].x + v[j].y) + (v[j].z + v[j].w);
-        const float mean = block_sum<NW>(s, lds[0]) / n;
+        const float mean = row_sum<NW, false>(s, lds[0], sub) / n;
         float q = 0.0f;
 #pragma unroll
         for (int j = 0; j < VPT; ++j) {
@@ -105,7 +113,7 @@ __global__ __launch_bounds__(kBlock) void norm_rows_vec(NormArgs a) {
                 q += (d.x * d.x + d.y * d.y) + (d.z * d.z + d.w * d.w);
             }
         }
-        const float var = block_sum<NW>(q, lds[1]) / n;
+        const float var = row_sum<NW, false>(q, lds[1], sub) / n;
         const float inv_std = 1.0f / sqrtf(var + a.eps);
 #pragma unroll
         for (int j = 0; j < VPT; ++j) {
@@ -116,7 +124,7 @@ __global__ __launch_bounds__(kBlock) void norm_rows_vec(NormArgs a) {
                     o *= *reinterpret_cast<const f4*>(a.g + 4 * c4);
                     if (a.b) o += *reinterpret_cast<const f4*>(a.b + 4 * c4);
                 }
-                st4<NT>(a.y + base + 4 * c4, o);
+                st4<true>(a.y + base + 4 * c4, o);
             }
         }
     } else {
@@ -124,14 +132,14 @@ __global__ __launch_bounds__(kBlock) void norm_rows_vec(NormArgs a) {
 #pragma unroll
         for (int j = 0; j < VPT; ++j)
             q += (v[j].x * v[j].x + v[j].y * v[j].y) + (v[j].z * v[j].z + v[j].w * v[j].w);
-        const float rms = sqrtf(block_sum<NW>(q, lds[0]) / n + a.eps);
+        const float rms = sqrtf(row_sum<NW, false>(q, lds[0], sub) / n + a.eps);
 #pragma unroll
         for (int j = 0; j < VPT; ++j) {
             const int64_t c4 = static_cast<int64_t>(j) * TPR + t;
             if (c4 < c4n) {
                 f4 o = v[j] / rms;
                 if (a.g) o = rms_scale(o, a.g, a.w_len, 4 * c4);
-                st4<NT>(a.y + base + 4 * c4, o);
+                st4<true>(a.y + base + 4 * c4, o);
             }
         }
     }
@@ -192,12 +200,12 @@ __global__ __launch_bounds__(kBlock) void norm_rows_generic(NormArgs a) {
     }
 }
 
-template <Norm K, int TPR, int VPT>
+template <Norm K, int TPR, int VPT, int BS>
 int launch_vec(mimir_ctx* ctx, const NormArgs& a) {
     unsigned blocks;
-    if (!grid_for(a.rows, kBlock / TPR, &blocks))
+    if (!grid_for(a.rows, BS / TPR, &blocks))
         return fail(ctx, MIMIR_EINVAL, "norm: %lld rows exceed the grid limit", (long long)a.rows);
-    norm_rows_vec<K, TPR, VPT, true><<<blocks, kBlock, 0, ctx->stream>>>(a);
+    norm_rows_vec<K, TPR, VPT, BS><<<blocks, BS, 0, ctx->stream>>>(a);
     return launched(ctx, "norm_rows_vec");
 }
 
@@ -208,13 +216,13 @@ int dispatch(mimir_ctx* ctx, const NormArgs& a) {
     if constexpr (K == Norm::AddRms) vec = vec && aligned16(a.r) && aligned16(a.r_out);
     const int64_t c4 = a.cols / 4;
     if (vec) {
-        if (c4 <= 64) return launch_vec<K, 64, 1>(ctx, a);
-        if (c4 <= 128) return launch_vec<K, 64, 2>(ctx, a);
-        if (c4 <= 256) return launch_vec<K, 64, 4>(ctx, a);
-        if (c4 <= 512) return launch_vec<K, 64, 8>(ctx, a);
-        if (c4 <= 1024) return launch_vec<K, 256, 4>(ctx, a);
-        if (c4 <= 2048) return launch_vec<K, 256, 8>(ctx, a);
-        if (c4 <= 4096) return launch_vec<K, 256, 16>(ctx, a);
+        const RowShape over = K == Norm::Layer ? ctx->tune.layernorm : ctx->tune.rmsnorm;
+        const RowShape s = shape_fits(over, c4) ? over
+                           : (K == Norm::Layer ? default_layernorm_shape(c4) : default_norm_shape(c4));
+#define MIMIR_NORM_CASE(T, V, B) \
+        if (s.tpr == T && s.vpt == V && s.bs == B) return launch_vec<K, T, V, B>(ctx, a);
+        MIMIR_ROW_SHAPES(MIMIR_NORM_CASE)
+#undef MIMIR_NORM_CASE
     }
     if (a.rows > 0x7fffffffLL)
         return fail(ctx, MIMIR_EINVAL, "norm: %lld rows exceed the grid limit", (long long)a.rows);

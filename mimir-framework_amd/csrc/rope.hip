@@ -11,8 +11,9 @@
 // Work unit ("slot"): 4 consecutive pairs of one head row -- a 16-byte vector
 // from the first half, the matching one from the second half, and the two
 // table vectors.  Q = D/8 slots per head row; q's slots come first, then k's.
-// Each thread handles PPT slots spaced one workgroup-width apart, so a wave
-// instruction reads 4 head rows' half-rows (4 x 256 B for D = 128).
+// Each thread handles PPT slots spaced one workgroup-width apart (PPT = 1 by
+// default), so a wave instruction reads 4 head rows' half-rows (4 x 256 B
+// for D = 128).
 #include "common.hpp"
 #include "internal.hpp"
 
@@ -104,15 +105,23 @@ __global__ __launch_bounds__(kBlock) void rope_scalar(RopeArgs a, int64_t q_pair
     }
 }
 
-constexpr int kPpt = 2;
+template <int LOG2Q, int PPT>
+int launch_ppt(mimir_ctx* ctx, const RopeArgs& a) {
+    unsigned blocks;
+    if (!grid_for(a.total_slots, static_cast<int64_t>(PPT) * kBlock, &blocks))
+        return fail(ctx, MIMIR_EINVAL, "RoPE: tensor exceeds the grid limit");
+    rope_vec<LOG2Q, PPT><<<blocks, kBlock, 0, ctx->stream>>>(a);
+    return launched(ctx, "rope_vec");
+}
 
+// One slot per thread streams fastest on MI355X; 2 and 4 stay for sweeps.
 template <int LOG2Q>
 int launch_vec(mimir_ctx* ctx, const RopeArgs& a) {
-    unsigned blocks;
-    if (!grid_for(a.total_slots, static_cast<int64_t>(kPpt) * kBlock, &blocks))
-        return fail(ctx, MIMIR_EINVAL, "RoPE: tensor exceeds the grid limit");
-    rope_vec<LOG2Q, kPpt><<<blocks, kBlock, 0, ctx->stream>>>(a);
-    return launched(ctx, "rope_vec");
+    switch (ctx->tune.rope_ppt) {
+        case 2: return launch_ppt<LOG2Q, 2>(ctx, a);
+        case 4: return launch_ppt<LOG2Q, 4>(ctx, a);
+        default: return launch_ppt<LOG2Q, 1>(ctx, a);
+    }
 }
 
 }  // namespace

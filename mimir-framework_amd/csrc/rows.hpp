@@ -1,0 +1,125 @@
+// rows.hpp -- launch shapes for the row kernels (LayerNorm, RMSNorm, add +
+// RMSNorm, softmax) and the tuning override shared by every kernel family.
+//
+// A row of `cols` fp32 is held in VGPRs by TPR threads, each owning VPT
+// 16-byte vectors at float4 columns t, t+TPR, ..., in workgroups of BS
+// threads (BS/TPR rows per workgroup).  The shapes below were chosen by
+// measurement on MI355X: one or two vectors per thread with many waves in
+// flight streams better than deep per-thread unrolling.
+#pragma once
+
+#include <cstdint>
+#include <cstdlib>
+#include <cstring>
+
+namespace mimir {
+
+struct RowShape {
+    int tpr;
+    int vpt;
+    int bs;
+};
+
+// Every (TPR, VPT, BS) the row kernels are compiled for.  X(tpr, vpt, bs).
+#define MIMIR_ROW_SHAPES(X) \
+    X(64, 1, 64)            \
+    X(64, 1, 256)           \
+    X(64, 2, 64)            \
+    X(64, 2, 256)           \
+    X(64, 4, 64)            \
+    X(64, 4, 256)           \
+    X(128, 1, 256)          \
+    X(128, 2, 256)          \
+    X(128, 2, 512)          \
+    X(128, 4, 512)          \
+    X(256, 1, 256)          \
+    X(256, 2, 256)          \
+    X(256, 4, 256)          \
+    X(256, 4, 1024)         \
+    X(512, 1, 512)          \
+    X(512, 2, 512)          \
+    X(512, 2, 1024)         \
+    X(512, 4, 512)          \
+    X(1024, 1, 1024)        \
+    X(1024, 2, 1024)        \
+    X(1024, 4, 1024)
+
+// Tuning override, read once per context from MIMIR_TUNE, e.g.
+//   MIMIR_TUNE="norm=1024x1x1024,layernorm=512x2x512,softmax=64x4x64,ew=1,gather=1024,rope=1"
+// Each entry selects among the compiled variants above; an entry that does
+// not fit a call (row too wide for it) is ignored for that call.  Unset, the
+// measured defaults apply.  Used for sweeps; results are identical.
+struct Tuning {
+    RowShape layernorm{0, 0, 0};
+    RowShape rmsnorm{0, 0, 0};  // RMSNorm and add + RMSNorm
+    RowShape softmax{0, 0, 0};
+    int ew_vpt = 0;
+    int gather_tpt = 0;
+    int rope_ppt = 0;
+};
+
+inline bool parse_shape(const char* v, RowShape* s) {
+    int a = 0, b = 0, c = 0;
+    char* end = nullptr;
+    a = static_cast<int>(std::strtol(v, &end, 10));
+    if (*end != 'x') return false;
+    b = static_cast<int>(std::strtol(end + 1, &end, 10));
+    if (*end != 'x') return false;
+    c = static_cast<int>(std::strtol(end + 1, &end, 10));
+    *s = RowShape{a, b, c};
+    return true;
+}
+
+inline Tuning read_tuning() {
+    Tuning t;
+    const char* env = std::getenv("MIMIR_TUNE");
+    if (!env) return t;
+    char buf[512];
+    std::strncpy(buf, env, sizeof buf - 1);
+    buf[sizeof buf - 1] = 0;
+    for (char* tok = std::strtok(buf, ","); tok; tok = std::strtok(nullptr, ",")) {
+        char* eq = std::strchr(tok, '=');
+        if (!eq) continue;
+        *eq = 0;
+        const char* k = tok;
+        const char* v = eq + 1;
+        if (!std::strcmp(k, "layernorm")) parse_shape(v, &t.layernorm);
+        else if (!std::strcmp(k, "norm")) parse_shape(v, &t.rmsnorm);
+        else if (!std::strcmp(k, "softmax")) parse_shape(v, &t.softmax);
+        else if (!std::strcmp(k, "ew")) t.ew_vpt = std::atoi(v);
+        else if (!std::strcmp(k, "gather")) t.gather_tpt = std::atoi(v);
+        else if (!std::strcmp(k, "rope")) t.rope_ppt = std::atoi(v);
+    }
+    return t;
+}
+
+// Default shapes by row width in float4 (c4 = cols / 4), from the sweeps.
+inline RowShape default_norm_shape(int64_t c4) {
+    if (c4 <= 64) return {64, 1, 256};
+    if (c4 <= 128) return {128, 1, 256};
+    if (c4 <= 256) return {64, 4, 64};
+    if (c4 <= 512) return {512, 1, 512};
+    if (c4 <= 1024) return {512, 2, 512};
+    if (c4 <= 2048) return {512, 4, 512};
+    if (c4 <= 4096) return {1024, 4, 1024};
+    return {0, 0, 0};
+}
+
+inline RowShape default_layernorm_shape(int64_t c4) { return default_norm_shape(c4); }
+
+inline RowShape default_softmax_shape(int64_t c4) {
+    if (c4 <= 64) return {64, 1, 64};
+    if (c4 <= 128) return {64, 2, 64};
+    if (c4 <= 256) return {128, 2, 512};
+    if (c4 <= 512) return {128, 4, 512};
+    if (c4 <= 1024) return {1024, 1, 1024};
+    if (c4 <= 2048) return {1024, 2, 1024};
+    if (c4 <= 4096) return {1024, 4, 1024};
+    return {0, 0, 0};
+}
+
+inline bool shape_fits(const RowShape& s, int64_t c4) {
+    return s.tpr > 0 && static_cast<int64_t>(s.tpr) * s.vpt >= c4;
+}
+
+}  // namespace mimir

@@ -12,12 +12,18 @@ using namespace mimir;
 
 namespace {
 
-// Streaming copy: 16-byte vectors for the aligned body, bytes for the rest.
+// Streaming copy: one 16-byte vector per thread for the aligned body (the
+// grid covers it in one pass up to 2^30 workgroups), bytes for the rest.
 __global__ __launch_bounds__(kBlock) void copy16_kernel(const u4* __restrict__ src,
                                                          u4* __restrict__ dst, int64_t n16) {
     const int64_t stride = static_cast<int64_t>(gridDim.x) * kBlock;
     for (int64_t i = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x; i < n16; i += stride)
         __builtin_nontemporal_store(__builtin_nontemporal_load(src + i), dst + i);
+}
+
+unsigned full_grid(int64_t n) {
+    const int64_t b = (n + kBlock - 1) / kBlock;
+    return static_cast<unsigned>(b < 1 ? 1 : (b > (int64_t(1) << 30) ? (int64_t(1) << 30) : b));
 }
 
 __global__ __launch_bounds__(kBlock) void copy1_kernel(const uint8_t* __restrict__ src,
@@ -54,6 +60,7 @@ int mimir_ctx_create(int device, mimir_ctx** out) {
     mimir_ctx* ctx = new (std::nothrow) mimir_ctx();
     if (!ctx) return MIMIR_ENOMEM;
     ctx->device = device;
+    ctx->tune = read_tuning();
     if (hipStreamCreateWithFlags(&ctx->own_stream, hipStreamNonBlocking) != hipSuccess) {
         delete ctx;
         return MIMIR_EDEVICE;
@@ -163,7 +170,7 @@ int mimir_copy(mimir_ctx* ctx, void* dst_dev, const void* src_dev, size_t bytes)
     if (aligned16(s) && aligned16(d)) {
         n16 = static_cast<int64_t>(bytes / 16);
         if (n16 > 0) {
-            copy16_kernel<<<stride_grid(n16), kBlock, 0, ctx->stream>>>(
+            copy16_kernel<<<full_grid(n16), kBlock, 0, ctx->stream>>>(
                 reinterpret_cast<const u4*>(s), reinterpret_cast<u4*>(d), n16);
             if (int st = launched(ctx, "copy16_kernel")) return st;
         }

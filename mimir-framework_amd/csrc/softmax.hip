@@ -1,7 +1,7 @@
 // softmax.hip -- max-subtracted row softmax / log-softmax for gfx950.
 //
-// Same row layout as norm.hip: TPR threads (one wavefront, or the 4-wave
-// workgroup for rows above 2048) hold the row in VGPRs as 16-byte vectors;
+// Same row layout as norm.hip (rows.hpp): TPR threads hold the row in VGPRs
+// as 16-byte vectors;
 // the row max and the sum of exponentials are wave-uniform DPP reductions, so
 // each element is read from HBM once and written once.  Rows too wide for the
 // register budget, or unaligned, take one workgroup per row with three
@@ -50,29 +50,30 @@ __device__ __forceinline__ void row_constants(float sum, float* s, float* aux) {
     }
 }
 
-template <int MODE, int TPR, int VPT, bool NT>
-__global__ __launch_bounds__(kBlock) void softmax_rows_vec(SoftmaxArgs a) {
-    constexpr int RPB = kBlock / TPR;
+template <int MODE, int TPR, int VPT, int BS>
+__global__ __launch_bounds__(BS) void softmax_rows_vec(SoftmaxArgs a) {
+    constexpr int RPB = BS / TPR;
     constexpr int NW = TPR / kWave;
-    __shared__ float lds[2][NW];
+    __shared__ float lds[2][BS / kWave];
     const int t = threadIdx.x % TPR;
-    const int64_t row = static_cast<int64_t>(blockIdx.x) * RPB + threadIdx.x / TPR;
+    const int sub = threadIdx.x / TPR;
+    const int64_t row = static_cast<int64_t>(blockIdx.x) * RPB + sub;
     if constexpr (NW == 1) {
         if (row >= a.rows) return;
     }
-    const int64_t c4n = a.cols >> 2;
+    const int64_t c4n = row < a.rows ? (a.cols >> 2) : 0;  // rows past the end touch no memory
     const int64_t base = row * a.cols;
 
     f4 v[VPT];
 #pragma unroll
     for (int j = 0; j < VPT; ++j) {
         const int64_t c4 = static_cast<int64_t>(j) * TPR + t;
-        v[j] = (c4 < c4n) ? ld4<NT>(a.x + base + 4 * c4) : f4(-INFINITY);
+        v[j] = (c4 < c4n) ? ld4<true>(a.x + base + 4 * c4) : f4(-INFINITY);
     }
     float m = -INFINITY;
 #pragma unroll
     for (int j = 0; j < VPT; ++j) m = fmaxf(m, fmaxf(fmaxf(v[j].x, v[j].y), fmaxf(v[j].z, v[j].w)));
-    m = block_max<NW>(m, lds[0]);
+    m = row_max<NW>(m, lds[0], sub);
 
     f4 e[VPT];
     float s = 0.0f;
@@ -88,7 +89,7 @@ __global__ __launch_bounds__(kBlock) void softmax_rows_vec(SoftmaxArgs a) {
         }
     }
     float sum, aux;
-    row_constants<MODE>(block_sum<NW>(s, lds[1]), &sum, &aux);
+    row_constants<MODE>(row_sum<NW>(s, lds[1], sub), &sum, &aux);
 #pragma unroll
     for (int j = 0; j < VPT; ++j) {
         const int64_t c4 = static_cast<int64_t>(j) * TPR + t;
@@ -96,7 +97,7 @@ __global__ __launch_bounds__(kBlock) void softmax_rows_vec(SoftmaxArgs a) {
             f4 o;
 #pragma unroll
             for (int k = 0; k < 4; ++k) o[k] = finish<MODE>(v[j][k], e[j][k], m, sum, aux);
-            st4<NT>(a.y + base + 4 * c4, o);
+            st4<true>(a.y + base + 4 * c4, o);
         }
     }
 }
@@ -121,12 +122,12 @@ __global__ __launch_bounds__(kBlock) void softmax_rows_generic(SoftmaxArgs a) {
     }
 }
 
-template <int MODE, int TPR, int VPT>
+template <int MODE, int TPR, int VPT, int BS>
 int launch_vec(mimir_ctx* ctx, const SoftmaxArgs& a) {
     unsigned blocks;
-    if (!grid_for(a.rows, kBlock / TPR, &blocks))
+    if (!grid_for(a.rows, BS / TPR, &blocks))
         return fail(ctx, MIMIR_EINVAL, "softmax: %lld rows exceed the grid limit", (long long)a.rows);
-    softmax_rows_vec<MODE, TPR, VPT, true><<<blocks, kBlock, 0, ctx->stream>>>(a);
+    softmax_rows_vec<MODE, TPR, VPT, BS><<<blocks, BS, 0, ctx->stream>>>(a);
     return launched(ctx, "softmax_rows_vec");
 }
 
@@ -134,13 +135,11 @@ template <int MODE>
 int dispatch(mimir_ctx* ctx, const SoftmaxArgs& a) {
     const int64_t c4 = a.cols / 4;
     if ((a.cols % 4) == 0 && aligned16(a.x) && aligned16(a.y)) {
-        if (c4 <= 64) return launch_vec<MODE, 64, 1>(ctx, a);
-        if (c4 <= 128) return launch_vec<MODE, 64, 2>(ctx, a);
-        if (c4 <= 256) return launch_vec<MODE, 64, 4>(ctx, a);
-        if (c4 <= 512) return launch_vec<MODE, 64, 8>(ctx, a);
-        if (c4 <= 1024) return launch_vec<MODE, 256, 4>(ctx, a);
-        if (c4 <= 2048) return launch_vec<MODE, 256, 8>(ctx, a);
-        if (c4 <= 4096) return launch_vec<MODE, 256, 16>(ctx, a);
+        const RowShape s = shape_fits(ctx->tune.softmax, c4) ? ctx->tune.softmax : default_softmax_shape(c4);
+#define MIMIR_SOFTMAX_CASE(T, V, B) \
+        if (s.tpr == T && s.vpt == V && s.bs == B) return launch_vec<MODE, T, V, B>(ctx, a);
+        MIMIR_ROW_SHAPES(MIMIR_SOFTMAX_CASE)
+#undef MIMIR_SOFTMAX_CASE
     }
     if (a.rows > 0x7fffffffLL)
         return fail(ctx, MIMIR_EINVAL, "softmax: %lld rows exceed the grid limit", (long long)a.rows);
