@@ -50,7 +50,9 @@ typedef struct mimir_event mimir_event;
 int mimir_ctx_create(int device, mimir_ctx** out);
 int mimir_ctx_destroy(mimir_ctx* ctx);
 /* Enqueue on an existing HIP stream (hipStream_t passed as void*) instead of
- * the context's own; NULL restores the context's stream. */
+ * the context's own; NULL restores the context's stream.  Waits for the work
+ * already enqueued on the previous stream (the context's scratch memory is
+ * reused in stream order). */
 int mimir_ctx_set_stream(mimir_ctx* ctx, void* hip_stream);
 void* mimir_ctx_stream(mimir_ctx* ctx);
 /* Cap on the bytes mimir_malloc may hold at once (0 = no cap).  Mirrors
@@ -194,6 +196,82 @@ int mimir_rope_fwd(mimir_ctx* ctx, const float* q, float* q_out, int64_t q_heads
                    float* k_out, int64_t k_heads, int64_t batch, int64_t seq, int64_t head_dim,
                    int64_t pos_offset, const float* cos_tab, const float* sin_tab,
                    int64_t table_rows);
+
+/* ---------------------------------------------------------------------------
+ * Device-resident runtime: a named tensor store and a layer runner with the
+ * routing of the reference's Model::forwardPassNamed (Model.cpp:1352-1408,
+ * forwardPassView Model.cpp:4621-6824) for the layer types of this path.
+ * Replaces Model::tensor_store / tensor_store_int (Model.hpp:608-610), which
+ * hold every activation as a host std::vector, with device buffers, so
+ * consecutive layers never leave HBM.  Inference only (training=false).
+ * Buffers are pooled per store and reused in stream order: once a graph has
+ * run, running it again allocates nothing.
+ * ------------------------------------------------------------------------- */
+
+typedef struct mimir_store mimir_store;
+
+#define MIMIR_DTYPE_F32 0
+#define MIMIR_DTYPE_I32 1
+
+/* Layer types (the reference's LayerType names, LayerTypes.hpp:13-120). */
+#define MIMIR_LAYER_LAYERNORM 1  /* LayerOps::layernorm_forward, LayerOps.hpp:264-319 */
+#define MIMIR_LAYER_RMSNORM 2    /* LayerOpsExt::rms_norm_forward (whole vector) */
+#define MIMIR_LAYER_SOFTMAX 3    /* LayerOps::softmax_forward (whole vector) */
+#define MIMIR_LAYER_LOGSOFTMAX 4 /* LayerOps::softmax_forward, LogSoftmax branch */
+#define MIMIR_LAYER_GELU 5       /* LayerOps::gelu_forward */
+#define MIMIR_LAYER_SILU 6       /* LayerOps::silu_forward */
+#define MIMIR_LAYER_ADD 7        /* LayerOps::add_forward (inputs[0], inputs[1]) */
+#define MIMIR_LAYER_MULTIPLY 8   /* LayerOps::multiply_forward */
+#define MIMIR_LAYER_EMBEDDING 9  /* inline gather, Model.cpp:5301-5334 */
+#define MIMIR_LAYER_IDENTITY 10  /* LayerOps::identity_forward */
+#define MIMIR_LAYER_DROPOUT 11   /* LayerOps::dropout_forward at inference: identity */
+
+/* One layer: the fields of the reference's `Layer` (Layers.hpp:86-309) this
+ * path reads.  `weights` is a DEVICE pointer to the layer's weight block
+ * (Layer::getWeights) of `weights_len` floats (Layer::getWeightsSize). */
+typedef struct mimir_layer {
+    int32_t type;
+    const char* name;           /* used in error messages */
+    const char* const* inputs;  /* n_inputs names; n_inputs == 0 -> {"x"} */
+    int32_t n_inputs;
+    const char* output;         /* NULL or "" -> "x" */
+    const float* weights;
+    int64_t weights_len;
+    float eps;
+    int32_t affine;
+    int32_t use_bias;
+    int32_t in_features;
+    int32_t vocab_size;
+    int32_t embed_dim;
+    int32_t padding_idx;
+    int32_t seq_len;
+} mimir_layer;
+
+int mimir_store_create(mimir_ctx* ctx, mimir_store** out);
+int mimir_store_destroy(mimir_store* store);
+/* Drop every name (buffers go back to the store's pool). */
+int mimir_store_clear(mimir_store* store);
+/* Upload `n` elements of `dtype` from host memory under `name` (replacing a
+ * tensor of that name and dtype). */
+int mimir_store_put(mimir_store* store, const char* name, int dtype, const void* host, int64_t n);
+/* Device pointer and element count of a stored tensor (EINVAL if absent). */
+int mimir_store_info(mimir_store* store, const char* name, int dtype, void** dptr, int64_t* n);
+/* Download a stored tensor into `host` (cap elements); *n gets its size. */
+int mimir_store_get(mimir_store* store, const char* name, int dtype, void* host, int64_t cap,
+                    int64_t* n);
+/* The input setup of Model::forwardPassNamed(float_inputs, int_inputs):
+ * clears both stores, stores "x" and "__input__" = float_inputs["x"] (else
+ * float_inputs["__input__"], else empty), the int inputs (an int "seq" also
+ * under "text_ids", "__input__" and "x"), then every float input.  Host data. */
+int mimir_store_set_inputs(mimir_store* store, const char* const* fnames, const float* const* fdata,
+                           const int64_t* fsizes, int32_t nf, const char* const* inames,
+                           const int32_t* const* idata, const int64_t* isizes, int32_t ni);
+/* Run layers in order (Model::forwardPassView's layer loop): inputs by name
+ * from the float store (Embedding input 0 also from the int store, read as
+ * float ids, else seq_len padding ids stored under that name), output stored
+ * under layer.output or "x".  Errors where the reference throws: EINVAL with
+ * the message, e.g. "Missing input tensor: <name>". */
+int mimir_store_run(mimir_store* store, const mimir_layer* layers, int32_t n_layers);
 
 #ifdef __cplusplus
 }

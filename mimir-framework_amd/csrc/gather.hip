@@ -30,9 +30,14 @@ __device__ __forceinline__ int32_t float_id(float f) {
     return static_cast<int32_t>(static_cast<uint32_t>(static_cast<unsigned long long>(r)));
 }
 
-template <bool FLOAT_IDS>
+// Id modes: int32 ids (Model.cpp:1152-1205); float ids (Model.cpp:5301-5334);
+// int32 ids read as float first, as the forwardPassView float path does when
+// an Embedding's input comes from the int store (Model.cpp:4836-4840).
+template <int MODE>
 __device__ __forceinline__ int32_t load_id(const void* ids, int64_t t) {
-    if constexpr (FLOAT_IDS) return float_id(static_cast<const float*>(ids)[t]);
+    if constexpr (MODE == kIdsF32) return float_id(static_cast<const float*>(ids)[t]);
+    else if constexpr (MODE == kIdsI32AsF32)
+        return float_id(static_cast<float>(static_cast<const int32_t*>(ids)[t]));
     else return static_cast<const int32_t*>(ids)[t];
 }
 
@@ -50,12 +55,12 @@ constexpr int kWavesPerBlock = kBlock / kWave;
 
 // TPT threads per token row (BS / TPT token rows per workgroup), one 16-byte
 // vector per thread per pass; rows wider than TPT vectors take several passes.
-template <bool FLOAT_IDS, int TPT, int BS>
+template <int MODE, int TPT, int BS>
 __global__ __launch_bounds__(BS) void embed_vec(GatherArgs a) {
     const int t = threadIdx.x % TPT;
     const int64_t token = static_cast<int64_t>(blockIdx.x) * (BS / TPT) + threadIdx.x / TPT;
     if (token >= a.n_ids) return;  // no barriers in this kernel
-    const int32_t id = load_id<FLOAT_IDS>(a.ids, token);
+    const int32_t id = load_id<MODE>(a.ids, token);
     const bool copy = !(a.pad >= 0 && id == a.pad) && id >= 0 && id < a.vocab;
     const int64_t dim4 = a.dim >> 2;
     const u4* src = reinterpret_cast<const u4*>(a.table) + (copy ? static_cast<int64_t>(id) * dim4 : 0);
@@ -65,12 +70,12 @@ __global__ __launch_bounds__(BS) void embed_vec(GatherArgs a) {
 }
 
 // Any dim / alignment: one wavefront per token, 32-bit words.
-template <bool FLOAT_IDS>
+template <int MODE>
 __global__ __launch_bounds__(kBlock) void embed_scalar(GatherArgs a) {
     const int lane = threadIdx.x & (kWave - 1);
     const int64_t token = static_cast<int64_t>(blockIdx.x) * kWavesPerBlock + threadIdx.x / kWave;
     if (token >= a.n_ids) return;
-    const int32_t id = load_id<FLOAT_IDS>(a.ids, token);
+    const int32_t id = load_id<MODE>(a.ids, token);
     const bool copy = !(a.pad >= 0 && id == a.pad) && id >= 0 && id < a.vocab;
     const uint32_t* src = reinterpret_cast<const uint32_t*>(a.table) +
                           (copy ? static_cast<int64_t>(id) * a.dim : 0);
@@ -78,7 +83,7 @@ __global__ __launch_bounds__(kBlock) void embed_scalar(GatherArgs a) {
     for (int64_t c = lane; c < a.dim; c += kWave) dst[c] = copy ? src[c] : 0u;
 }
 
-template <bool FLOAT_IDS>
+template <int MODE>
 int run(mimir_ctx* ctx, const void* ids, int64_t n_ids, const float* table, int64_t table_len,
         int32_t vocab, int32_t dim, int32_t pad, float* y) {
     MIMIR_REQUIRE(ctx, n_ids >= 0, "Embedding: n_ids < 0");
@@ -105,19 +110,28 @@ int run(mimir_ctx* ctx, const void* ids, int64_t n_ids, const float* table, int6
         if (!grid_for(n_ids, bs / tpt, &vb))
             return fail(ctx, MIMIR_EINVAL, "Embedding: %lld ids exceed the grid limit", (long long)n_ids);
         switch (tpt) {
-            case 64: embed_vec<FLOAT_IDS, 64, 256><<<vb, 256, 0, ctx->stream>>>(a); break;
-            case 128: embed_vec<FLOAT_IDS, 128, 256><<<vb, 256, 0, ctx->stream>>>(a); break;
-            case 256: embed_vec<FLOAT_IDS, 256, 256><<<vb, 256, 0, ctx->stream>>>(a); break;
-            case 512: embed_vec<FLOAT_IDS, 512, 512><<<vb, 512, 0, ctx->stream>>>(a); break;
-            default: embed_vec<FLOAT_IDS, 1024, 1024><<<vb, 1024, 0, ctx->stream>>>(a); break;
+            case 64: embed_vec<MODE, 64, 256><<<vb, 256, 0, ctx->stream>>>(a); break;
+            case 128: embed_vec<MODE, 128, 256><<<vb, 256, 0, ctx->stream>>>(a); break;
+            case 256: embed_vec<MODE, 256, 256><<<vb, 256, 0, ctx->stream>>>(a); break;
+            case 512: embed_vec<MODE, 512, 512><<<vb, 512, 0, ctx->stream>>>(a); break;
+            default: embed_vec<MODE, 1024, 1024><<<vb, 1024, 0, ctx->stream>>>(a); break;
         }
         return launched(ctx, "embed_vec");
     }
-    embed_scalar<FLOAT_IDS><<<blocks, kBlock, 0, ctx->stream>>>(a);
+    embed_scalar<MODE><<<blocks, kBlock, 0, ctx->stream>>>(a);
     return launched(ctx, "embed_scalar");
 }
 
 }  // namespace
+
+int mimir::embedding_launch(mimir_ctx* ctx, const void* ids, int mode, int64_t n_ids, const float* table,
+                            int64_t table_len, int32_t vocab, int32_t dim, int32_t pad, float* y) {
+    switch (mode) {
+        case kIdsF32: return run<kIdsF32>(ctx, ids, n_ids, table, table_len, vocab, dim, pad, y);
+        case kIdsI32AsF32: return run<kIdsI32AsF32>(ctx, ids, n_ids, table, table_len, vocab, dim, pad, y);
+        default: return run<kIdsI32>(ctx, ids, n_ids, table, table_len, vocab, dim, pad, y);
+    }
+}
 
 extern "C" {
 
@@ -125,14 +139,14 @@ int mimir_embedding_fwd(mimir_ctx* ctx, const int32_t* ids, int64_t n_ids, const
                         int64_t table_len, int32_t vocab, int32_t dim, int32_t padding_idx,
                         float* y) {
     if (!ctx) return MIMIR_EINVAL;
-    return run<false>(ctx, ids, n_ids, table, table_len, vocab, dim, padding_idx, y);
+    return run<kIdsI32>(ctx, ids, n_ids, table, table_len, vocab, dim, padding_idx, y);
 }
 
 int mimir_embedding_f32ids_fwd(mimir_ctx* ctx, const float* ids, int64_t n_ids,
                                const float* table, int64_t table_len, int32_t vocab, int32_t dim,
                                int32_t padding_idx, float* y) {
     if (!ctx) return MIMIR_EINVAL;
-    return run<true>(ctx, ids, n_ids, table, table_len, vocab, dim, padding_idx, y);
+    return run<kIdsF32>(ctx, ids, n_ids, table, table_len, vocab, dim, padding_idx, y);
 }
 
 }  // extern "C"

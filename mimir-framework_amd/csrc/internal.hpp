@@ -22,6 +22,10 @@ struct mimir_ctx {
     std::unordered_map<void*, size_t> allocs;
     std::string last_error;
     mimir::Tuning tune;  // launch-shape override (MIMIR_TUNE), read at creation
+    // Scratch for the partial results of multi-workgroup row reductions
+    // (longrow.hip); grows on demand, reused in stream order.
+    void* scratch = nullptr;
+    size_t scratch_bytes = 0;
 };
 
 struct mimir_event {
@@ -76,6 +80,24 @@ inline bool grid_for(int64_t units, int64_t per_block, unsigned* blocks) {
     *blocks = static_cast<unsigned>(b);
     return true;
 }
+
+// Context scratch of at least `bytes` (runtime.hip).  Growing it waits for
+// the work already enqueued, which may still read the old buffer.
+int ensure_scratch(mimir_ctx* ctx, size_t bytes, void** out);
+
+// Rows too long for one workgroup's registers, few of them: split each row
+// over many workgroups (longrow.hip).  `kind`: 0 LayerNorm, 1 RMSNorm,
+// 2 add + RMSNorm; softmax `mode` as in mimir_softmax_fwd.
+bool longrow_applies(int64_t rows, int64_t cols);
+int longrow_norm(mimir_ctx* ctx, int kind, const float* x, const float* r, float* r_out, const float* g,
+                 const float* b, int64_t w_len, float* y, int64_t rows, int64_t cols, float eps);
+int longrow_softmax(mimir_ctx* ctx, int mode, const float* x, float* y, int64_t rows, int64_t cols);
+
+// Embedding gather with an id mode (gather.hip); used by the C ABI and the
+// device-resident runtime (store.hip).
+enum : int { kIdsI32 = 0, kIdsF32 = 1, kIdsI32AsF32 = 2 };
+int embedding_launch(mimir_ctx* ctx, const void* ids, int mode, int64_t n_ids, const float* table,
+                     int64_t table_len, int32_t vocab, int32_t dim, int32_t pad, float* y);
 
 }  // namespace mimir
 

@@ -1,0 +1,253 @@
+// longrow.hip -- row reductions split over many workgroups, for a few very
+// long rows.
+//
+// The reference's RMSNorm and Softmax layers normalise the whole input as one
+// row (LayerOpsExt.hpp:345-378, LayerOps.hpp:325-361), and so does LayerNorm
+// when in_features is unset (LayerOps.hpp:276); a transformer's activations
+// make that row millions of elements long.  One workgroup per row would leave
+// all but one CU idle, so such rows are cut into chunks of 4096 floats, one
+// 256-thread workgroup each:
+//   1. partial : per chunk, the partial statistic (sum, sum of squares,
+//                sum of squared deviations, or softmax's (max, sum of exp));
+//   2. combine : one workgroup per row folds the chunk partials in a fixed
+//                order (per-thread strided sums, then the DPP/LDS tree), so
+//                the result does not depend on scheduling;
+//   3. apply   : per chunk, the elementwise normalisation with the row stats.
+// LayerNorm keeps the reference's two-pass variance: partial/combine for the
+// mean, then partial/combine of sum((x-mean)^2), then apply.  The extra reads
+// of x hit L2/MALL for rows that fit there and HBM otherwise: 3 (RMSNorm,
+// softmax) or 4 (LayerNorm) passes instead of 2.  Partials live in the
+// context's scratch buffer, reused in stream order.
+#include "common.hpp"
+#include "internal.hpp"
+
+#include <math.h>
+
+using namespace mimir;
+
+namespace {
+
+constexpr int kChunkVec = 4;                          // float4 per thread per chunk
+constexpr int64_t kChunk4 = kChunkVec * kBlock;       // float4 per chunk (1024)
+constexpr int64_t kChunkFloats = 4 * kChunk4;         // 4096 floats
+
+enum Stat { kSumX = 0, kSumSq = 1, kSumDev = 2, kSumSqAdd = 3, kSoftmax = 4 };
+
+struct LongArgs {
+    const float* x;
+    const float* r;
+    float* r_out;
+    const float* g;
+    const float* b;
+    int64_t w_len;
+    float* y;
+    int64_t rows;
+    int64_t cols;
+    int64_t nchunks;
+    float eps;
+    float* partial;  // [rows][nchunks][2]
+    float* stats;    // [rows][2]
+};
+
+// Pass 1: one chunk's partial statistic.
+template <int S>
+__global__ __launch_bounds__(kBlock) void lr_partial(LongArgs a) {
+    __shared__ float lds[2][kBlock / kWave];
+    const int64_t row = blockIdx.y;
+    const int64_t chunk = blockIdx.x;
+    const int64_t c4n = a.cols >> 2;
+    const int64_t base = row * a.cols;
+    f4 v[kChunkVec];
+    bool ok[kChunkVec];
+#pragma unroll
+    for (int j = 0; j < kChunkVec; ++j) {
+        const int64_t c4 = chunk * kChunk4 + static_cast<int64_t>(j) * kBlock + threadIdx.x;
+        ok[j] = c4 < c4n;
+        if constexpr (S == kSumSqAdd) {
+            if (ok[j]) {
+                v[j] = ld4<true>(a.x + base + 4 * c4) + ld4<true>(a.r + base + 4 * c4);
+                st4<true>(a.r_out + base + 4 * c4, v[j]);  // the updated residual
+            }
+        } else {
+            if (ok[j]) v[j] = ld4<true>(a.x + base + 4 * c4);
+        }
+    }
+    float p0 = 0.0f, p1 = 0.0f;
+    if constexpr (S == kSoftmax) {
+        float m = -INFINITY;
+#pragma unroll
+        for (int j = 0; j < kChunkVec; ++j)
+            if (ok[j]) m = fmaxf(m, fmaxf(fmaxf(v[j].x, v[j].y), fmaxf(v[j].z, v[j].w)));
+        m = block_max<kBlock / kWave>(m, lds[0]);
+        float s = 0.0f;
+        if (m != -INFINITY) {  // an all -inf chunk contributes nothing
+#pragma unroll
+            for (int j = 0; j < kChunkVec; ++j)
+                if (ok[j])
+                    s += (expf(v[j].x - m) + expf(v[j].y - m)) + (expf(v[j].z - m) + expf(v[j].w - m));
+        }
+        p0 = m;
+        p1 = block_sum<kBlock / kWave>(s, lds[1]);
+    } else {
+        const float mean = (S == kSumDev) ? a.stats[2 * row] : 0.0f;
+        float s = 0.0f;
+#pragma unroll
+        for (int j = 0; j < kChunkVec; ++j) {
+            if (!ok[j]) continue;
+            if constexpr (S == kSumX) {
+                s += (v[j].x + v[j].y) + (v[j].z + v[j].w);
+            } else {
+                const f4 d = (S == kSumDev) ? v[j] - mean : v[j];
+                s += (d.x * d.x + d.y * d.y) + (d.z * d.z + d.w * d.w);
+            }
+        }
+        p0 = block_sum<kBlock / kWave>(s, lds[0]);
+    }
+    if (threadIdx.x == 0) {
+        float* p = a.partial + 2 * (row * a.nchunks + chunk);
+        p[0] = p0;
+        p[1] = p1;
+    }
+}
+
+// Pass 2: fold one row's chunk partials (fixed order) into its statistics.
+//   kSumX  -> stats = (mean, -)            kSumDev -> stats.y = 1/sqrt(var+eps)
+//   kSumSq / kSumSqAdd -> stats = (rms, -) kSoftmax -> stats = (max, sum)
+template <int S>
+__global__ __launch_bounds__(kBlock) void lr_combine(LongArgs a) {
+    __shared__ float lds[2][kBlock / kWave];
+    const int64_t row = blockIdx.x;
+    const float* p = a.partial + 2 * row * a.nchunks;
+    const float n = static_cast<float>(a.cols);
+    if constexpr (S == kSoftmax) {
+        float m = -INFINITY;
+        for (int64_t c = threadIdx.x; c < a.nchunks; c += kBlock) m = fmaxf(m, p[2 * c]);
+        m = block_max<kBlock / kWave>(m, lds[0]);
+        float s = 0.0f;
+        for (int64_t c = threadIdx.x; c < a.nchunks; c += kBlock) {
+            const float mc = p[2 * c];
+            if (mc != -INFINITY) s += p[2 * c + 1] * expf(mc - m);
+        }
+        s = block_sum<kBlock / kWave>(s, lds[1]);
+        if (threadIdx.x == 0) {
+            a.stats[2 * row] = m;
+            a.stats[2 * row + 1] = s;
+        }
+    } else {
+        float s = 0.0f;
+        for (int64_t c = threadIdx.x; c < a.nchunks; c += kBlock) s += p[2 * c];
+        s = block_sum<kBlock / kWave>(s, lds[0]);
+        if (threadIdx.x == 0) {
+            if constexpr (S == kSumX) a.stats[2 * row] = s / n;
+            else if constexpr (S == kSumDev) a.stats[2 * row + 1] = 1.0f / sqrtf(s / n + a.eps);
+            else a.stats[2 * row] = sqrtf(s / n + a.eps);
+        }
+    }
+}
+
+template <int MODE>
+__device__ __forceinline__ float softmax_out(float xv, float m, float s) {
+    if constexpr (MODE == MIMIR_SOFTMAX_DIV_EPS) return expf(xv - m) / (s + 1e-9f);
+    else if constexpr (MODE == MIMIR_SOFTMAX_MUL_INV) return expf(xv - m) * (1.0f / s);
+    else return (xv - m) - logf(s);
+}
+
+// Pass 3: normalise one chunk.  K: 0 LayerNorm, 1 RMSNorm, 2 add+RMSNorm, 3 softmax.
+template <int K, int MODE>
+__global__ __launch_bounds__(kBlock) void lr_apply(LongArgs a) {
+    const int64_t row = blockIdx.y;
+    const int64_t chunk = blockIdx.x;
+    const int64_t c4n = a.cols >> 2;
+    const int64_t base = row * a.cols;
+    const float s0 = a.stats[2 * row];
+    const float s1 = a.stats[2 * row + 1];
+    const float* src = (K == 2) ? a.r_out : a.x;  // add+RMSNorm re-reads the residual it wrote
+    f4 v[kChunkVec];
+#pragma unroll
+    for (int j = 0; j < kChunkVec; ++j) {
+        const int64_t c4 = chunk * kChunk4 + static_cast<int64_t>(j) * kBlock + threadIdx.x;
+        if (c4 < c4n) v[j] = ld4<true>(src + base + 4 * c4);
+    }
+#pragma unroll
+    for (int j = 0; j < kChunkVec; ++j) {
+        const int64_t c4 = chunk * kChunk4 + static_cast<int64_t>(j) * kBlock + threadIdx.x;
+        if (c4 >= c4n) continue;
+        const int64_t c = 4 * c4;
+        f4 o;
+        if constexpr (K == 0) {
+            o = (v[j] - s0) * s1;
+            if (a.g) {
+                o *= *reinterpret_cast<const f4*>(a.g + c);
+                if (a.b) o += *reinterpret_cast<const f4*>(a.b + c);
+            }
+        } else if constexpr (K == 1 || K == 2) {
+            o = v[j] / s0;
+            if (a.g) {
+#pragma unroll
+                for (int k = 0; k < 4; ++k)
+                    if (c + k < a.w_len) o[k] *= a.g[c + k];
+            }
+        } else {
+#pragma unroll
+            for (int k = 0; k < 4; ++k) o[k] = softmax_out<MODE>(v[j][k], s0, s1);
+        }
+        st4<true>(a.y + base + c, o);
+    }
+}
+
+int setup(mimir_ctx* ctx, LongArgs& a, int64_t rows, int64_t cols) {
+    a.rows = rows;
+    a.cols = cols;
+    a.nchunks = (cols + kChunkFloats - 1) / kChunkFloats;
+    const size_t bytes = sizeof(float) * (2 * static_cast<size_t>(rows) * a.nchunks + 2 * rows);
+    void* s = nullptr;
+    if (int st = ensure_scratch(ctx, bytes, &s)) return st;
+    a.partial = static_cast<float*>(s);
+    a.stats = a.partial + 2 * rows * a.nchunks;
+    return MIMIR_OK;
+}
+
+}  // namespace
+
+bool mimir::longrow_applies(int64_t rows, int64_t cols) {
+    return cols > 16384 && rows <= 256 && (cols + kChunkFloats - 1) / kChunkFloats <= 0x7fffffffLL;
+}
+
+int mimir::longrow_norm(mimir_ctx* ctx, int kind, const float* x, const float* r, float* r_out,
+                        const float* g, const float* b, int64_t w_len, float* y, int64_t rows, int64_t cols,
+                        float eps) {
+    LongArgs a{x, r, r_out, g, b, w_len, y, 0, 0, 0, eps, nullptr, nullptr};
+    if (int st = setup(ctx, a, rows, cols)) return st;
+    const dim3 grid(static_cast<unsigned>(a.nchunks), static_cast<unsigned>(rows));
+    const unsigned nrows = static_cast<unsigned>(rows);
+    if (kind == 0) {
+        lr_partial<kSumX><<<grid, kBlock, 0, ctx->stream>>>(a);
+        lr_combine<kSumX><<<nrows, kBlock, 0, ctx->stream>>>(a);
+        lr_partial<kSumDev><<<grid, kBlock, 0, ctx->stream>>>(a);
+        lr_combine<kSumDev><<<nrows, kBlock, 0, ctx->stream>>>(a);
+        lr_apply<0, 0><<<grid, kBlock, 0, ctx->stream>>>(a);
+    } else if (kind == 1) {
+        lr_partial<kSumSq><<<grid, kBlock, 0, ctx->stream>>>(a);
+        lr_combine<kSumSq><<<nrows, kBlock, 0, ctx->stream>>>(a);
+        lr_apply<1, 0><<<grid, kBlock, 0, ctx->stream>>>(a);
+    } else {
+        lr_partial<kSumSqAdd><<<grid, kBlock, 0, ctx->stream>>>(a);
+        lr_combine<kSumSqAdd><<<nrows, kBlock, 0, ctx->stream>>>(a);
+        lr_apply<2, 0><<<grid, kBlock, 0, ctx->stream>>>(a);
+    }
+    return launched(ctx, "longrow_norm");
+}
+
+int mimir::longrow_softmax(mimir_ctx* ctx, int mode, const float* x, float* y, int64_t rows, int64_t cols) {
+    LongArgs a{x, nullptr, nullptr, nullptr, nullptr, 0, y, 0, 0, 0, 0.0f, nullptr, nullptr};
+    if (int st = setup(ctx, a, rows, cols)) return st;
+    const dim3 grid(static_cast<unsigned>(a.nchunks), static_cast<unsigned>(rows));
+    lr_partial<kSoftmax><<<grid, kBlock, 0, ctx->stream>>>(a);
+    lr_combine<kSoftmax><<<static_cast<unsigned>(rows), kBlock, 0, ctx->stream>>>(a);
+    switch (mode) {
+        case MIMIR_SOFTMAX_DIV_EPS: lr_apply<3, MIMIR_SOFTMAX_DIV_EPS><<<grid, kBlock, 0, ctx->stream>>>(a); break;
+        case MIMIR_SOFTMAX_MUL_INV: lr_apply<3, MIMIR_SOFTMAX_MUL_INV><<<grid, kBlock, 0, ctx->stream>>>(a); break;
+        default: lr_apply<3, MIMIR_SOFTMAX_LOG><<<grid, kBlock, 0, ctx->stream>>>(a); break;
+    }
+    return launched(ctx, "longrow_softmax");
+}

@@ -48,6 +48,28 @@ unsigned stride_grid(int64_t n) {
 
 }  // namespace
 
+int mimir::ensure_scratch(mimir_ctx* ctx, size_t bytes, void** out) {
+    if (bytes > ctx->scratch_bytes) {
+        if (ctx->scratch) {
+            hipError_t e = hipStreamSynchronize(ctx->stream);
+            if (e != hipSuccess) return hip_fail(ctx, e, "hipStreamSynchronize");
+            (void)hipFree(ctx->scratch);
+            ctx->scratch = nullptr;
+            ctx->scratch_bytes = 0;
+        }
+        const size_t want = bytes < (size_t(1) << 20) ? (size_t(1) << 20) : bytes;
+        hipError_t e = hipMalloc(&ctx->scratch, want);
+        if (e != hipSuccess) {
+            (void)hipGetLastError();
+            ctx->scratch = nullptr;
+            return fail(ctx, MIMIR_ENOMEM, "scratch of %zu bytes: %s", want, hipGetErrorString(e));
+        }
+        ctx->scratch_bytes = want;
+    }
+    *out = ctx->scratch;
+    return MIMIR_OK;
+}
+
 extern "C" {
 
 int mimir_ctx_create(int device, mimir_ctx** out) {
@@ -76,6 +98,7 @@ int mimir_ctx_destroy(mimir_ctx* ctx) {
     if (st == MIMIR_OK) {
         (void)hipStreamSynchronize(ctx->stream);
         for (auto& kv : ctx->allocs) (void)hipFree(kv.first);
+        if (ctx->scratch) (void)hipFree(ctx->scratch);
         (void)hipStreamDestroy(ctx->own_stream);
     }
     delete ctx;
@@ -83,7 +106,11 @@ int mimir_ctx_destroy(mimir_ctx* ctx) {
 }
 
 int mimir_ctx_set_stream(mimir_ctx* ctx, void* hip_stream) {
-    if (!ctx) return MIMIR_EINVAL;
+    MIMIR_ENTER(ctx);
+    // The context's scratch is reused in the order of its current stream:
+    // finish what the old stream may still do with it before switching.
+    hipError_t e = hipStreamSynchronize(ctx->stream);
+    if (e != hipSuccess) return hip_fail(ctx, e, "hipStreamSynchronize");
     ctx->stream = hip_stream ? static_cast<hipStream_t>(hip_stream) : ctx->own_stream;
     return MIMIR_OK;
 }

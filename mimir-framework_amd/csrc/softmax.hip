@@ -3,9 +3,10 @@
 // Same row layout as norm.hip (rows.hpp): TPR threads hold the row in VGPRs
 // as 16-byte vectors;
 // the row max and the sum of exponentials are wave-uniform DPP reductions, so
-// each element is read from HBM once and written once.  Rows too wide for the
-// register budget, or unaligned, take one workgroup per row with three
-// strided passes.
+// each element is read from HBM once and written once.  A few rows too wide
+// for the register budget are split over many workgroups (longrow.hip);
+// other wide or unaligned rows take one workgroup per row with three strided
+// passes.
 //
 // Arithmetic (per row): m = max_j x[j]; e[j] = expf(x[j] - m); s = sum e[j];
 //   MIMIR_SOFTMAX_DIV_EPS  y = e / (s + 1e-9f)    LayerOps::softmax_inplace,
@@ -140,6 +141,7 @@ int dispatch(mimir_ctx* ctx, const SoftmaxArgs& a) {
         if (s.tpr == T && s.vpt == V && s.bs == B) return launch_vec<MODE, T, V, B>(ctx, a);
         MIMIR_ROW_SHAPES(MIMIR_SOFTMAX_CASE)
 #undef MIMIR_SOFTMAX_CASE
+        if (longrow_applies(a.rows, a.cols)) return longrow_softmax(ctx, MODE, a.x, a.y, a.rows, a.cols);
     }
     if (a.rows > 0x7fffffffLL)
         return fail(ctx, MIMIR_EINVAL, "softmax: %lld rows exceed the grid limit", (long long)a.rows);

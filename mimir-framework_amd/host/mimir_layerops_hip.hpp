@@ -14,6 +14,8 @@
 //   mimir_hip::LayerOpsExt::rms_norm_forward LayerOpsExt.hpp:345-378
 //   mimir_hip::Normalization::rms_norm       Layers.hpp:1003-1021
 //   mimir_hip::embedding_forward(_float_ids) Model.cpp:1152-1205 / 5301-5334 (inline there)
+//   mimir_hip::DeviceModel::forwardPassNamed Model.cpp:1352-1408, 4621-6824
+//                                            (device-resident TensorStore)
 //
 // The op templates take the reference's `Layer` (or anything with the same
 // fields: eps, affine, use_bias, in_features, vocab_size, embed_dim,
@@ -31,6 +33,7 @@
 #include <cstdint>
 #include <stdexcept>
 #include <string>
+#include <unordered_map>
 #include <utility>
 #include <vector>
 
@@ -356,5 +359,119 @@ std::vector<float> embedding_forward_float_ids(const std::vector<float>& x, cons
             "Embedding");
     return dy.download();
 }
+
+// ---------------------------------------------------------------------------
+// Device-resident runtime: Model::forwardPassNamed (Model.cpp:1352-1408,
+// forwardPassView Model.cpp:4621-6824) over a reference layer list, with every
+// activation held in HBM by a mimir_store and only "x" downloaded.  Inference
+// only.  Layer types: LayerNorm, RMSNorm, Softmax, LogSoftmax, GELU, SiLU,
+// Add, Multiply, Embedding, Identity, Dropout (others throw at construction).
+// ---------------------------------------------------------------------------
+template <class LayerT>
+class DeviceModel {
+public:
+    DeviceModel(Context& c, const std::vector<LayerT>& layers) : ctx_(&c), layers_(&layers) {
+        ctx_->check(mimir_store_create(ctx_->get(), &store_), "mimir_store_create");
+        for (const LayerT& L : layers) {
+            const int t = type_of(L.type);
+            if (t == 0) {
+                mimir_store_destroy(store_);
+                throw std::runtime_error("DeviceModel: layer type " + L.type + " (" + L.name +
+                                         ") is not on the HIP path");
+            }
+            types_.push_back(t);
+        }
+        syncWeights();
+    }
+    ~DeviceModel() {
+        if (store_) mimir_store_destroy(store_);
+    }
+    DeviceModel(const DeviceModel&) = delete;
+    DeviceModel& operator=(const DeviceModel&) = delete;
+
+    // Upload every layer's weight block (Layer::getWeights / getWeightsSize);
+    // call again after the host weights change.
+    void syncWeights() {
+        weights_.clear();
+        for (const LayerT& L : *layers_) {
+            const float* w = L.getWeights();
+            const size_t n = w ? L.getWeightsSize() : 0;
+            weights_.emplace_back(*ctx_, w, n);
+        }
+    }
+
+    std::vector<float> forwardPassNamed(const std::unordered_map<std::string, std::vector<float>>& fin,
+                                        const std::unordered_map<std::string, std::vector<int>>& iin,
+                                        bool training = false) {
+        if (training) throw std::runtime_error("DeviceModel: inference only (training=false)");
+        std::vector<const char*> fn, in;
+        std::vector<const float*> fd;
+        std::vector<const int32_t*> id;
+        std::vector<int64_t> fs, is;
+        for (const auto& kv : fin) {
+            fn.push_back(kv.first.c_str());
+            fd.push_back(kv.second.data());
+            fs.push_back(static_cast<int64_t>(kv.second.size()));
+        }
+        for (const auto& kv : iin) {
+            in.push_back(kv.first.c_str());
+            id.push_back(reinterpret_cast<const int32_t*>(kv.second.data()));
+            is.push_back(static_cast<int64_t>(kv.second.size()));
+        }
+        ctx_->check(mimir_store_set_inputs(store_, fn.data(), fd.data(), fs.data(), static_cast<int32_t>(fn.size()),
+                                           in.data(), id.data(), is.data(), static_cast<int32_t>(in.size())),
+                    "DeviceModel inputs");
+        std::vector<mimir_layer> ls(layers_->size());
+        std::vector<std::vector<const char*>> names(layers_->size());
+        for (size_t i = 0; i < layers_->size(); ++i) {
+            const LayerT& L = (*layers_)[i];
+            for (const auto& nm : L.inputs) names[i].push_back(nm.c_str());
+            mimir_layer& c = ls[i];
+            c.type = types_[i];
+            c.name = L.name.c_str();
+            c.inputs = names[i].data();
+            c.n_inputs = static_cast<int32_t>(names[i].size());
+            c.output = L.output.c_str();
+            c.weights = weights_[i].data();
+            c.weights_len = static_cast<int64_t>(weights_[i].size());
+            c.eps = L.eps;
+            c.affine = L.affine;
+            c.use_bias = L.use_bias;
+            c.in_features = L.in_features;
+            c.vocab_size = L.vocab_size;
+            c.embed_dim = L.embed_dim;
+            c.padding_idx = L.padding_idx;
+            c.seq_len = L.seq_len;
+        }
+        ctx_->check(mimir_store_run(store_, ls.data(), static_cast<int32_t>(ls.size())), "DeviceModel forward");
+        int64_t n = 0;
+        void* p = nullptr;
+        ctx_->check(mimir_store_info(store_, "x", MIMIR_DTYPE_F32, &p, &n), "DeviceModel output");
+        std::vector<float> out(static_cast<size_t>(n));
+        ctx_->check(mimir_store_get(store_, "x", MIMIR_DTYPE_F32, out.data(), n, &n), "DeviceModel output");
+        return out;
+    }
+
+    mimir_store* store() const { return store_; }
+
+private:
+    static int type_of(const std::string& t) {
+        static const std::unordered_map<std::string, int> m = {
+            {"LayerNorm", MIMIR_LAYER_LAYERNORM}, {"RMSNorm", MIMIR_LAYER_RMSNORM},
+            {"Softmax", MIMIR_LAYER_SOFTMAX},     {"LogSoftmax", MIMIR_LAYER_LOGSOFTMAX},
+            {"GELU", MIMIR_LAYER_GELU},           {"SiLU", MIMIR_LAYER_SILU},
+            {"Add", MIMIR_LAYER_ADD},             {"Multiply", MIMIR_LAYER_MULTIPLY},
+            {"Embedding", MIMIR_LAYER_EMBEDDING}, {"Identity", MIMIR_LAYER_IDENTITY},
+            {"Dropout", MIMIR_LAYER_DROPOUT}};
+        auto it = m.find(t);
+        return it == m.end() ? 0 : it->second;
+    }
+
+    Context* ctx_;
+    const std::vector<LayerT>* layers_;
+    mimir_store* store_ = nullptr;
+    std::vector<int> types_;
+    std::vector<DeviceBuffer<float>> weights_;
+};
 
 }  // namespace mimir_hip

@@ -7,7 +7,8 @@ from __future__ import annotations
 
 import ctypes
 import os
-from ctypes import POINTER, c_char_p, c_double, c_float, c_int, c_int32, c_int64, c_size_t, c_void_p
+from ctypes import (POINTER, Structure, c_char_p, c_double, c_float, c_int, c_int32, c_int64, c_size_t,
+                    c_void_p)
 
 PKG_ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 LIB_PATH = os.path.join(PKG_ROOT, "lib", "libmimir_hip.so")
@@ -19,6 +20,20 @@ SOFTMAX_DIV_EPS, SOFTMAX_MUL_INV, SOFTMAX_LOG = 0, 1, 2
 
 _P = c_void_p
 _PP = POINTER(c_void_p)
+
+DTYPE_F32, DTYPE_I32 = 0, 1
+LAYER_TYPES = {"LayerNorm": 1, "RMSNorm": 2, "Softmax": 3, "LogSoftmax": 4, "GELU": 5, "SiLU": 6,
+               "Add": 7, "Multiply": 8, "Embedding": 9, "Identity": 10, "Dropout": 11}
+
+
+class Layer_C(Structure):
+    """struct mimir_layer (include/mimir_hip.h)."""
+    _fields_ = [("type", c_int32), ("name", c_char_p), ("inputs", POINTER(c_char_p)),
+                ("n_inputs", c_int32), ("output", c_char_p), ("weights", c_void_p),
+                ("weights_len", c_int64), ("eps", c_float), ("affine", c_int32), ("use_bias", c_int32),
+                ("in_features", c_int32), ("vocab_size", c_int32), ("embed_dim", c_int32),
+                ("padding_idx", c_int32), ("seq_len", c_int32)]
+
 
 # name -> (restype, argtypes); mirrors include/mimir_hip.h one to one.
 SIGNATURES = {
@@ -55,6 +70,15 @@ SIGNATURES = {
     "mimir_rope_table": (c_int, [c_int64, c_int64, c_double, _P, _P]),
     "mimir_rope_fwd": (c_int, [_P, _P, _P, c_int64, _P, _P, c_int64, c_int64, c_int64, c_int64,
                                c_int64, _P, _P, c_int64]),
+    "mimir_store_create": (c_int, [_P, _PP]),
+    "mimir_store_destroy": (c_int, [_P]),
+    "mimir_store_clear": (c_int, [_P]),
+    "mimir_store_put": (c_int, [_P, c_char_p, c_int, _P, c_int64]),
+    "mimir_store_info": (c_int, [_P, c_char_p, c_int, _PP, POINTER(c_int64)]),
+    "mimir_store_get": (c_int, [_P, c_char_p, c_int, _P, c_int64, POINTER(c_int64)]),
+    "mimir_store_set_inputs": (c_int, [_P, POINTER(c_char_p), POINTER(c_void_p), POINTER(c_int64), c_int32,
+                                       POINTER(c_char_p), POINTER(c_void_p), POINTER(c_int64), c_int32]),
+    "mimir_store_run": (c_int, [_P, POINTER(Layer_C), c_int32]),
 }
 
 _lib = None

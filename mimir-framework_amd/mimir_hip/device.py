@@ -234,3 +234,97 @@ def rope_table(rows, head_dim, theta=10000.0):
     if st != OK:
         raise MimirError(st, "mimir_rope_table: invalid argument")
     return c, s
+
+
+class Store:
+    """Device-resident named tensor store + layer runner (mimir_store_*)."""
+
+    def __init__(self, ctx: Context):
+        self.ctx = ctx
+        h = c_void_p()
+        ctx.check(ctx.lib.mimir_store_create(ctx.handle, byref(h)), "mimir_store_create")
+        self.handle = h
+
+    def close(self):
+        if self.handle:
+            self.ctx.check(self.ctx.lib.mimir_store_destroy(self.handle), "mimir_store_destroy")
+            self.handle = None
+
+    def clear(self):
+        self.ctx.check(self.ctx.lib.mimir_store_clear(self.handle))
+
+    def put(self, name, arr):
+        a = np.ascontiguousarray(arr)
+        dt = _lib.DTYPE_I32 if a.dtype.kind in "iu" else _lib.DTYPE_F32
+        a = np.ascontiguousarray(a, np.int32 if dt == _lib.DTYPE_I32 else np.float32).ravel()
+        self.ctx.check(self.ctx.lib.mimir_store_put(self.handle, name.encode(), dt, a.ctypes.data_as(c_void_p),
+                                                    a.size))
+
+    def info(self, name, dtype=_lib.DTYPE_F32):
+        p, n = c_void_p(), ctypes.c_int64()
+        self.ctx.check(self.ctx.lib.mimir_store_info(self.handle, name.encode(), dtype, byref(p), byref(n)))
+        return p.value, n.value
+
+    def get(self, name, dtype=_lib.DTYPE_F32):
+        _, n = self.info(name, dtype)
+        out = np.empty(n, np.int32 if dtype == _lib.DTYPE_I32 else np.float32)
+        got = ctypes.c_int64()
+        self.ctx.check(self.ctx.lib.mimir_store_get(self.handle, name.encode(), dtype,
+                                                    out.ctypes.data_as(c_void_p), n, byref(got)))
+        return out
+
+    def set_inputs(self, fin=None, iin=None):
+        fin = {k: np.ascontiguousarray(v, np.float32).ravel() for k, v in (fin or {}).items()}
+        iin = {k: np.ascontiguousarray(v, np.int32).ravel() for k, v in (iin or {}).items()}
+        nf, ni = len(fin), len(iin)
+        fn = (ctypes.c_char_p * max(1, nf))(*[k.encode() for k in fin])
+        fd = (c_void_p * max(1, nf))(*[v.ctypes.data for v in fin.values()])
+        fs = (ctypes.c_int64 * max(1, nf))(*[v.size for v in fin.values()])
+        inn = (ctypes.c_char_p * max(1, ni))(*[k.encode() for k in iin])
+        idd = (c_void_p * max(1, ni))(*[v.ctypes.data for v in iin.values()])
+        isz = (ctypes.c_int64 * max(1, ni))(*[v.size for v in iin.values()])
+        self.ctx.check(self.ctx.lib.mimir_store_set_inputs(self.handle, fn, fd, fs, nf, inn, idd, isz, ni))
+
+    def run(self, graph: "DeviceGraph"):
+        self.ctx.check(self.ctx.lib.mimir_store_run(self.handle, graph.c_layers, len(graph.layers)))
+
+    def forward_named(self, graph: "DeviceGraph", fin=None, iin=None):
+        """Model::forwardPassNamed(fin, iin, training=false) on the device."""
+        self.set_inputs(fin, iin)
+        self.run(graph)
+        return self.get("x")
+
+
+class DeviceGraph:
+    """A layer list (dicts with the reference Layer fields and host `weights`)
+    with its weight blocks uploaded once to the device."""
+
+    def __init__(self, ctx: Context, layers):
+        self.ctx = ctx
+        self.layers = list(layers)
+        self._keep = []
+        self.weights = []
+        arr = (_lib.Layer_C * max(1, len(self.layers)))()
+        for i, L in enumerate(self.layers):
+            w = L.get("weights")
+            dw = None
+            if w is not None and np.asarray(w).size > 0:
+                dw = ctx.to_device(np.ascontiguousarray(w, np.float32).ravel())
+            self.weights.append(dw)
+            names = [n.encode() for n in L.get("inputs", [])]
+            cnames = (ctypes.c_char_p * max(1, len(names)))(*names)
+            name_b, out_b = L.get("name", "").encode(), L.get("output", "").encode()
+            self._keep += [cnames, name_b, out_b]
+            arr[i] = _lib.Layer_C(
+                _lib.LAYER_TYPES.get(L["type"], -1), name_b, cnames, len(names), out_b,
+                dw.ptr if dw is not None else None, 0 if dw is None else dw.size,
+                float(L.get("eps", 1e-5)), int(L.get("affine", True)), int(L.get("use_bias", True)),
+                int(L.get("in_features", 0)), int(L.get("vocab_size", 0)), int(L.get("embed_dim", 0)),
+                int(L.get("padding_idx", -1)), int(L.get("seq_len", 0)))
+        self.c_layers = arr
+
+    def close(self):
+        for d in self.weights:
+            if d is not None:
+                d.free()
+        self.weights = []

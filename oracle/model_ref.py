@@ -1,0 +1,82 @@
+"""ctypes front end for oracle/_ref/libmimir_ref_model.so: the reference's own
+Model::forwardPassNamed (Model.cpp:1352-1408, 4621-6824) on a layer list.
+TEST INFRASTRUCTURE ONLY (pins oracle/model_oracle.py; writes golden fixtures)."""
+from __future__ import annotations
+
+import ctypes
+import os
+from ctypes import POINTER, Structure, c_char, c_char_p, c_float, c_int32, c_int64, c_void_p
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+REF_MODEL_SO = os.path.join(HERE, "_ref", "libmimir_ref_model.so")
+
+
+class _Spec(Structure):
+    _fields_ = [("name", c_char_p), ("type", c_char_p), ("inputs", c_char_p), ("output", c_char_p),
+                ("params_count", c_int64), ("weights", c_void_p), ("eps", c_float),
+                ("affine", c_int32), ("use_bias", c_int32), ("in_features", c_int32),
+                ("vocab_size", c_int32), ("embed_dim", c_int32), ("padding_idx", c_int32),
+                ("seq_len", c_int32)]
+
+
+class RefModelError(RuntimeError):
+    pass
+
+
+_lib = None
+
+
+def available() -> bool:
+    return os.path.exists(REF_MODEL_SO)
+
+
+def _load():
+    global _lib
+    if _lib is None:
+        lib = ctypes.CDLL(REF_MODEL_SO)
+        f = lib.ref_model_forward
+        f.argtypes = [POINTER(_Spec), c_int32, POINTER(c_char_p), POINTER(c_void_p), POINTER(c_int64),
+                      c_int32, POINTER(c_char_p), POINTER(c_void_p), POINTER(c_int64), c_int32,
+                      c_void_p, c_int64, POINTER(c_int64), c_char_p, c_int32]
+        f.restype = c_int32
+        _lib = lib
+    return _lib
+
+
+def forward_named(layers, fin=None, iin=None, out_cap=1 << 24):
+    """layers: list of dicts (see oracle.model_oracle.Layer fields); fin/iin:
+    {name: float32 / int32 array}.  Returns the float32 "x" output."""
+    fin = fin or {}
+    iin = iin or {}
+    keep = []
+    specs = (_Spec * max(1, len(layers)))()
+    for i, L in enumerate(layers):
+        w = L.get("weights")
+        w = None if w is None else np.ascontiguousarray(w, np.float32)
+        keep.append(w)
+        specs[i] = _Spec(L["name"].encode(), L["type"].encode(), ",".join(L.get("inputs", [])).encode(),
+                         L.get("output", "").encode(), int(L.get("params_count", 0 if w is None else w.size)),
+                         None if w is None else w.ctypes.data, float(L.get("eps", 1e-5)),
+                         int(L.get("affine", True)), int(L.get("use_bias", True)),
+                         int(L.get("in_features", 0)), int(L.get("vocab_size", 0)),
+                         int(L.get("embed_dim", 0)), int(L.get("padding_idx", -1)),
+                         int(L.get("seq_len", 0)))
+    fa = {k: np.ascontiguousarray(v, np.float32).ravel() for k, v in fin.items()}
+    ia = {k: np.ascontiguousarray(v, np.int32).ravel() for k, v in iin.items()}
+    fn = (c_char_p * max(1, len(fa)))(*[k.encode() for k in fa])
+    fd = (c_void_p * max(1, len(fa)))(*[v.ctypes.data for v in fa.values()])
+    fs = (c_int64 * max(1, len(fa)))(*[v.size for v in fa.values()])
+    inn = (c_char_p * max(1, len(ia)))(*[k.encode() for k in ia])
+    idd = (c_void_p * max(1, len(ia)))(*[v.ctypes.data for v in ia.values()])
+    isz = (c_int64 * max(1, len(ia)))(*[v.size for v in ia.values()])
+    out = np.empty(out_cap, np.float32)
+    n = c_int64(0)
+    err = ctypes.create_string_buffer(512)
+    st = _load().ref_model_forward(specs, len(layers), fn, fd, fs, len(fa), inn, idd, isz, len(ia),
+                                   out.ctypes.data, out_cap, ctypes.byref(n), err, 512)
+    if st:
+        raise RefModelError(err.value.decode(errors="replace"))
+    assert n.value <= out_cap, "output larger than out_cap"
+    return out[:n.value].copy()

@@ -7,6 +7,8 @@
 
 #include <cmath>
 #include <cstdio>
+#include <string>
+#include <unordered_map>
 #include <vector>
 
 namespace {
@@ -16,6 +18,11 @@ namespace {
 enum class LayerType { Softmax, LogSoftmax, Other };
 
 struct TestLayer {
+    std::string name;
+    std::string type;
+    std::vector<std::string> inputs;
+    std::string output;
+    int seq_len = 0;
     LayerType type_enum = LayerType::Other;
     float eps = 1e-5f;
     bool affine = true;
@@ -214,6 +221,51 @@ int main() {
             mimir_hip::Normalization::rms_norm(h_ref, w, cols, 1e-6f);
             for (size_t i = 0; i < y.size(); ++i)
                 CHECK(std::fabs(y[i] - h_ref[i]) <= std::fmax(1e-6f, 1e-5f * std::fabs(h_ref[i])));
+        }
+        // Device-resident runtime: the reference runtime KATs through
+        // DeviceModel::forwardPassNamed (Tests/test_layers_named_routing.cpp:14-51,
+        // Tests/test_runtime_embedding_int_inputs.cpp:8-74).
+        {
+            auto& c = mimir_hip::Context::instance();
+            std::vector<TestLayer> layers(2);
+            layers[0].name = "sum";
+            layers[0].type = "Add";
+            layers[0].inputs = {"a", "b"};
+            layers[0].output = "sum";
+            layers[1].name = "x";
+            layers[1].type = "Multiply";
+            layers[1].inputs = {"sum", "c"};
+            layers[1].output = "x";
+            mimir_hip::DeviceModel<TestLayer> m(c, layers);
+            std::unordered_map<std::string, std::vector<float>> fin{
+                {"x", {0, 0}}, {"a", {1, 2}}, {"b", {3, 4}}, {"c", {2, 2}}};
+            const auto out = m.forwardPassNamed(fin, {});
+            CHECK(out.size() == 2);
+            CHECK_NEAR(out[0], 8.0f, 1e-6f);
+            CHECK_NEAR(out[1], 12.0f, 1e-6f);
+            fin.erase("c");  // a missing named input throws
+            CHECK(throws([&] { m.forwardPassNamed(fin, {}); }));
+
+            std::vector<TestLayer> emb(1);
+            emb[0].name = "emb";
+            emb[0].type = "Embedding";
+            emb[0].inputs = {"ids"};
+            emb[0].output = "x";
+            emb[0].vocab_size = 4;
+            emb[0].embed_dim = 4;
+            emb[0].padding_idx = 0;
+            emb[0].seq_len = 5;
+            for (int id = 0; id < 4; ++id)
+                for (int d = 0; d < 4; ++d) emb[0].weights.push_back(static_cast<float>(id * 10 + d));
+            mimir_hip::DeviceModel<TestLayer> me(c, emb);
+            auto e = me.forwardPassNamed({}, {{"ids", {1, 0, 2}}});
+            CHECK(e.size() == 12);
+            CHECK_NEAR(e[0], 10.0f, 1e-6f);
+            CHECK_NEAR(e[5], 0.0f, 1e-6f);
+            CHECK_NEAR(e[11], 23.0f, 1e-6f);
+            e = me.forwardPassNamed({}, {});  // missing ids -> seq_len padding ids -> zeros
+            CHECK(e.size() == 20);
+            for (float v : e) CHECK_NEAR(v, 0.0f, 1e-6f);
         }
     } catch (const std::exception& e) {
         std::fprintf(stderr, "FAIL: unexpected exception: %s\n", e.what());

@@ -120,5 +120,29 @@ def main():
     print("wrote", sorted(manifest))
 
 
+
+
+def write_model_graphs():
+    """Outputs of the reference's Model::forwardPassNamed on tests/_graphs.py."""
+    sys.path.insert(0, os.path.join(REPO, "tests"))
+    import model_ref as MR
+    from _graphs import graphs
+    if not MR.available():
+        sys.exit("oracle/_ref/libmimir_ref_model.so is not built: make -C oracle ref_model")
+    outs = {name: MR.forward_named(layers, fin, iin) for name, layers, fin, iin in graphs()}
+    np.savez_compressed(os.path.join(HERE, "model_graphs.npz"), **outs)
+    path = os.path.join(HERE, "MANIFEST.json")
+    manifest = json.load(open(path))
+    manifest["model_graphs"] = {
+        "note": "Model::forwardPassNamed (Model.cpp:1352-1408, 4621-6824) on the graphs of tests/_graphs.py",
+        "arrays": {k: {"shape": list(v.shape), "dtype": str(v.dtype), "sha256": sha(v)} for k, v in outs.items()},
+        "regenerated_inputs": {"tests/_graphs.py": "graphs()"},
+    }
+    with open(path, "w") as f:
+        json.dump(manifest, f, indent=1, sort_keys=True)
+    print("wrote model_graphs", sorted(outs))
+
+
 if __name__ == "__main__":
     main()
+    write_model_graphs()

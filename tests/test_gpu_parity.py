@@ -346,3 +346,57 @@ def test_rope_qk(ctx, B, S, H, Hk, D):
         ctx.rope(dq, dqo, H, dk, dko, Hk, B, S, D + 1, 0, dc, ds, rows)  # odd head_dim
     for d in (dq, dk, dqo, dko, dc, ds):
         d.free()
+
+
+# ---------------------------------------------------------------------------
+# Long rows split over many workgroups (longrow.hip)
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("rows,cols", [(1, 1 << 20), (3, 65536), (2, 20004), (1, 4097 * 4)])
+def test_longrow_layernorm_rmsnorm(ctx, rows, cols):
+    x = (rng.standard_normal((rows, cols), dtype=np.float32) * 1.3 + 0.2)
+    g = (1 + 0.05 * rng.standard_normal(cols)).astype(np.float32)
+    b = (0.05 * rng.standard_normal(cols)).astype(np.float32)
+    got = run(ctx, lambda dx, dg, db, y: ctx.layernorm(dx, dg, db, y, rows, cols, 1e-5), x, g, b,
+              out_shape=x.shape)
+    assert_close_or_nearer_exact(got, O.layernorm(x, cols, g, b, 1e-5).reshape(x.shape),
+                                 X.layernorm(x, cols, g, b, 1e-5), "long LN")
+    wl = cols // 3  # the whole-vector layer: weights shorter than the row
+    got = run(ctx, lambda dx, dw, y: ctx.rmsnorm(dx, dw, wl, y, rows, cols, 1e-6), x, g, out_shape=x.shape)
+    ref = np.concatenate([O.rmsnorm_whole(x[i], g[:wl], 1e-6) for i in range(rows)]).reshape(x.shape)
+    assert_close_or_nearer_exact(got, ref, X.rmsnorm(x, cols, g, wl, 1e-6), "long RMSNorm")
+
+
+def test_longrow_add_rmsnorm_inplace(ctx):
+    rows, cols = 2, 3 * 4096 * 4 + 8
+    x = rng.standard_normal((rows, cols), dtype=np.float32)
+    r = rng.standard_normal((rows, cols), dtype=np.float32)
+    w = (1 + 0.02 * rng.standard_normal(cols)).astype(np.float32)
+    y_ref, h_ref = O.add_rmsnorm(x, r, w, 1e-6)
+    dx, dr, dw, dy = ctx.to_device(x), ctx.to_device(r), ctx.to_device(w), ctx.empty(x.shape)
+    ctx.add_rmsnorm(dx, dr, dr, dw, dy, rows, cols, 1e-6)
+    assert_bitexact(dr.numpy(), h_ref, "residual")
+    assert_close_or_nearer_exact(dy.numpy(), y_ref, X.rmsnorm(h_ref, cols, w, cols, 1e-6), "y")
+    for d in (dx, dr, dw, dy):
+        d.free()
+
+
+@pytest.mark.parametrize("mode", [M.SOFTMAX_DIV_EPS, M.SOFTMAX_MUL_INV, M.SOFTMAX_LOG])
+def test_longrow_softmax_with_masked_chunks(ctx, mode):
+    rows, cols = 4, 9 * 4096
+    s = (3 * rng.standard_normal((rows, cols))).astype(np.float32)
+    s[0, 4096:3 * 4096] = -np.inf          # whole chunks masked
+    s[1, :] = -np.inf                        # an all -inf row -> NaN, as the reference
+    s[1, 5] = -np.inf
+    s[2, 12345] = np.nan                     # NaN -> the row is NaN
+    got = run(ctx, lambda dx, y: ctx.softmax(dx, y, rows, cols, mode), s, out_shape=s.shape)
+    assert_close_or_nearer_exact(got, O.softmax_rows(s, mode), X.softmax(s, mode), f"long softmax {mode}")
+    assert np.isnan(got[1]).all() and np.isnan(got[2]).all()
+
+
+def test_longrow_softmax_layer_whole_vector(ctx):
+    x = (3 * rng.standard_normal(1 << 21)).astype(np.float32)
+    got = run(ctx, lambda dx, y: ctx.softmax(dx, y, 1, x.size, M.SOFTMAX_MUL_INV), x, out_shape=x.shape)
+    ref = O.softmax_rows(x, M.SOFTMAX_MUL_INV)[0]
+    assert_close_or_nearer_exact(got, ref, X.softmax(x, 1)[0], "whole-vector softmax")
+    assert abs(got.sum(dtype=np.float64) - 1.0) < 1e-5
