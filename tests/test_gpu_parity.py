@@ -352,7 +352,7 @@ def test_rope_qk(ctx, B, S, H, Hk, D):
 # Long rows split over many workgroups (longrow.hip)
 # ---------------------------------------------------------------------------
 
-@pytest.mark.parametrize("rows,cols", [(1, 1 << 20), (3, 65536), (2, 20004), (1, 4097 * 4)])
+@pytest.mark.parametrize("rows,cols", [(1, 1 << 20), (3, 65536), (2, 20004), (1, 4097 * 4), (2, 20001)])
 def test_longrow_layernorm_rmsnorm(ctx, rows, cols):
     x = (rng.standard_normal((rows, cols), dtype=np.float32) * 1.3 + 0.2)
     g = (1 + 0.05 * rng.standard_normal(cols)).astype(np.float32)
