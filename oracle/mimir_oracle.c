@@ -10,6 +10,7 @@
 #include "mimir_oracle.h"
 
 #include <math.h>
+#include <stdlib.h>
 #include <string.h>
 
 #define ORACLE_OK 0
@@ -265,6 +266,170 @@ int oracle_rope(const float* x, float* y, int64_t B, int64_t S, int64_t H,
                 }
             }
         }
+    }
+    return ORACLE_OK;
+}
+
+/* ------------------------------------------------------------------------
+ * Backward of the same ops: the branches of Model::backwardPass
+ * (Model.cpp:7305-9153) for the path's layer types.
+ * ------------------------------------------------------------------------ */
+
+/* accumulate_grad, Model.cpp:7329-7341: dst += src (dst already holds a
+ * gradient; the "dst empty -> copy" case is a plain copy). */
+void oracle_accumulate(float* dst, const float* src, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) dst[i] += src[i];
+}
+
+/* LayerNorm branch, Model.cpp:7719-7821. */
+int oracle_layernorm_bwd(const float* x, const float* dy, int64_t N, int64_t in_features,
+                         const float* gamma, int has_bias, float eps, float* dx,
+                         float* grad_params) {
+    const int64_t feat = in_features > 0 ? in_features : N; /* :7730 */
+    if (feat <= 0 || N <= 0 || (N % feat) != 0) return ORACLE_EINVAL; /* :7732-7737 */
+    const int64_t tokens = N / feat;
+    const int affine = gamma != NULL;
+    float* dgamma = NULL;
+    float* dbeta = NULL;
+    if (affine) { /* :7757-7758, zero-initialised, added to grad_weights at :7809-7819 */
+        dgamma = (float*)calloc((size_t)feat, sizeof(float));
+        dbeta = (float*)calloc((size_t)feat, sizeof(float));
+        if (!dgamma || !dbeta) {
+            free(dgamma);
+            free(dbeta);
+            return ORACLE_EINVAL;
+        }
+    }
+    for (int64_t t = 0; t < tokens; ++t) {
+        const float* xr = x + t * feat;
+        const float* g = dy + t * feat;
+        float* d = dx + t * feat;
+        float mean = 0.0f; /* :7765-7768 */
+        for (int64_t i = 0; i < feat; ++i) mean += xr[i];
+        mean /= (float)feat;
+        float var = 0.0f; /* :7770-7776 */
+        for (int64_t i = 0; i < feat; ++i) {
+            const float dd = xr[i] - mean;
+            var += dd * dd;
+        }
+        var /= (float)feat;
+        const float inv_std = 1.0f / sqrtf(var + eps); /* :7777 */
+        float sum_dxhat = 0.0f, sum_dxhat_xhat = 0.0f;
+        for (int64_t i = 0; i < feat; ++i) { /* :7783-7797 */
+            const float xhat = (xr[i] - mean) * inv_std;
+            const float gm = gamma ? gamma[i] : 1.0f;
+            const float dxhat = g[i] * gm;
+            if (affine) {
+                dgamma[i] += g[i] * xhat;
+                if (has_bias) dbeta[i] += g[i];
+            }
+            sum_dxhat += dxhat;
+            sum_dxhat_xhat += dxhat * xhat;
+        }
+        const float invF = 1.0f / (float)feat; /* :7799-7805 */
+        for (int64_t i = 0; i < feat; ++i) {
+            const float xhat = (xr[i] - mean) * inv_std;
+            const float gm = gamma ? gamma[i] : 1.0f;
+            const float dxhat = g[i] * gm;
+            d[i] = inv_std * invF * ((float)feat * dxhat - sum_dxhat - xhat * sum_dxhat_xhat);
+        }
+    }
+    if (affine && grad_params) { /* :7809-7819 */
+        for (int64_t i = 0; i < feat; ++i) grad_params[i] += dgamma[i];
+        if (has_bias)
+            for (int64_t i = 0; i < feat; ++i) grad_params[feat + i] += dbeta[i];
+    }
+    free(dgamma);
+    free(dbeta);
+    return ORACLE_OK;
+}
+
+/* GELU branch, Model.cpp:9026-9051 (tanh approximation). */
+void oracle_gelu_bwd(const float* x, const float* dy, int64_t n, float* dx) {
+    for (int64_t i = 0; i < n; ++i) {
+        const float xv = x[i];
+        const float c = 0.044715f;
+        const float s = sqrtf(2.0f / 3.14159265359f);
+        const float u = s * (xv + c * xv * xv * xv);
+        const float t = tanhf(u);
+        const float sech2 = 1.0f - t * t;
+        const float du_dx = s * (1.0f + 3.0f * c * xv * xv);
+        const float dgelu = 0.5f * (1.0f + t) + 0.5f * xv * sech2 * du_dx;
+        dx[i] = dy[i] * dgelu;
+    }
+}
+
+/* SiLU branch, Model.cpp:7993-8032. */
+void oracle_silu_bwd(const float* x, const float* dy, int64_t n, float* dx) {
+    for (int64_t i = 0; i < n; ++i) {
+        const float xv = x[i];
+        const float s = 1.0f / (1.0f + expf(-xv));
+        const float ds = s * (1.0f - s);
+        const float dy_dx = s + xv * ds;
+        dx[i] = dy[i] * dy_dx;
+    }
+}
+
+/* Multiply branch, Model.cpp:7647-7665: da = dy*b, db = dy*a. */
+void oracle_mul_bwd(const float* a, const float* b, const float* dy, int64_t n, float* da,
+                    float* db) {
+    for (int64_t i = 0; i < n; ++i) {
+        da[i] = dy[i] * b[i];
+        db[i] = dy[i] * a[i];
+    }
+}
+
+/* Add branch, Model.cpp:7541-7601: the gradient of the broadcast (smaller)
+ * operand, a sum over the big operand's gradient (scalar: all of it; repeat:
+ * per position j over the tiles).  The big operand's gradient is dy itself. */
+int oracle_add_bwd_small(const float* dy, int64_t n_big, int64_t n_small, float* d_small) {
+    if (n_small <= 0 || n_big <= 0) return ORACLE_EINVAL;
+    if (n_small == 1) { /* :7581-7585 */
+        float sum = 0.0f;
+        for (int64_t i = 0; i < n_big; ++i) sum += dy[i];
+        d_small[0] = sum;
+        return ORACLE_OK;
+    }
+    if (n_big % n_small != 0) return ORACLE_EINVAL; /* :7595-7599 */
+    for (int64_t j = 0; j < n_small; ++j) d_small[j] = 0.0f; /* :7586-7594 */
+    for (int64_t t = 0; t < n_big / n_small; ++t)
+        for (int64_t j = 0; j < n_small; ++j) d_small[j] += dy[t * n_small + j];
+    return ORACLE_OK;
+}
+
+/* Embedding branch, Model.cpp:7429-7461: grad_table[id*dim + d] +=
+ * dy[t*dim + d] in token order; padding and out-of-range ids are skipped. */
+static int embed_bwd_check(int64_t n_ids, int64_t table_len, int32_t* vocab, int32_t* dim) {
+    if (n_ids < 0) return ORACLE_EINVAL;
+    if (*vocab < 1) *vocab = 1; /* :7434-7435 */
+    if (*dim < 1) *dim = 1;
+    if (table_len < (int64_t)(*vocab) * (int64_t)(*dim)) return ORACLE_EINVAL; /* :7443-7447 */
+    return ORACLE_OK;
+}
+
+static void embed_bwd_row(int32_t id, int64_t t, const float* dy, float* grad_table,
+                          int32_t vocab, int32_t dim, int32_t pad) {
+    if (pad >= 0 && id == pad) return; /* :7454 */
+    if (id < 0 || id >= vocab) return; /* :7455 */
+    float* gw = grad_table + (int64_t)id * dim;
+    const float* g = dy + t * (int64_t)dim;
+    for (int32_t d = 0; d < dim; ++d) gw[d] += g[d]; /* :7456-7460 */
+}
+
+int oracle_embedding_bwd_i32(const int32_t* ids, int64_t n_ids, const float* dy,
+                             float* grad_table, int64_t table_len, int32_t vocab, int32_t dim,
+                             int32_t padding_idx) {
+    if (embed_bwd_check(n_ids, table_len, &vocab, &dim)) return ORACLE_EINVAL;
+    for (int64_t t = 0; t < n_ids; ++t) embed_bwd_row(ids[t], t, dy, grad_table, vocab, dim, padding_idx);
+    return ORACLE_OK;
+}
+
+int oracle_embedding_bwd_f32(const float* ids, int64_t n_ids, const float* dy, float* grad_table,
+                             int64_t table_len, int32_t vocab, int32_t dim, int32_t padding_idx) {
+    if (embed_bwd_check(n_ids, table_len, &vocab, &dim)) return ORACLE_EINVAL;
+    for (int64_t t = 0; t < n_ids; ++t) {
+        const int32_t id = (int32_t)llround((double)ids[t]); /* :7453 */
+        embed_bwd_row(id, t, dy, grad_table, vocab, dim, padding_idx);
     }
     return ORACLE_OK;
 }

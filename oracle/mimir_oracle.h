@@ -24,6 +24,10 @@
  *   oracle_rope*            no reference implementation exists; pinned by the
  *                           float64 closed form of rotary embedding (Su et al.
  *                           2021, "RoFormer") and its invariants.
+ *   oracle_*_bwd            the reference's own Model::backwardPass, compiled
+ *                           in place (oracle/_ref), on graphs of these layers;
+ *                           float64 derivatives of the forward closed forms;
+ *                           brute-force scatter-add for the embedding.
  */
 #ifndef MIMIR_ORACLE_H
 #define MIMIR_ORACLE_H
@@ -102,6 +106,39 @@ int oracle_rope_table(int64_t rows, int64_t head_dim, double theta,
 int oracle_rope(const float* x, float* y, int64_t B, int64_t S, int64_t H,
                 int64_t D, int64_t pos_offset, const float* cos_tab,
                 const float* sin_tab, int64_t table_rows);
+
+/* ---- Backward (Model::backwardPass branches, Model.cpp:7305-9153) ---- */
+
+/* accumulate_grad, Model.cpp:7329-7341: dst[i] += src[i]. */
+void oracle_accumulate(float* dst, const float* src, int64_t n);
+
+/* LayerNorm branch, Model.cpp:7719-7821.  Groups of n = in_features (or N);
+ * gamma NULL when the layer is not affine.  dx is written; grad_params (the
+ * [dgamma | dbeta] block, feat*(1+has_bias) floats) is added to, as the
+ * reference adds into Layer::grad_weights. */
+int oracle_layernorm_bwd(const float* x, const float* dy, int64_t N, int64_t in_features,
+                         const float* gamma, int has_bias, float eps, float* dx,
+                         float* grad_params);
+
+/* GELU branch, Model.cpp:9026-9051; SiLU branch, Model.cpp:7993-8032. */
+void oracle_gelu_bwd(const float* x, const float* dy, int64_t n, float* dx);
+void oracle_silu_bwd(const float* x, const float* dy, int64_t n, float* dx);
+
+/* Multiply branch, Model.cpp:7647-7665. */
+void oracle_mul_bwd(const float* a, const float* b, const float* dy, int64_t n, float* da,
+                    float* db);
+
+/* Add branch, Model.cpp:7541-7601: gradient of the broadcast operand
+ * (n_small == 1: the sum of dy; else sums over the n_big/n_small tiles). */
+int oracle_add_bwd_small(const float* dy, int64_t n_big, int64_t n_small, float* d_small);
+
+/* Embedding branch, Model.cpp:7429-7461 (ids as int32 or as floats rounded
+ * with llround): grad_table rows += dy rows in token order. */
+int oracle_embedding_bwd_i32(const int32_t* ids, int64_t n_ids, const float* dy,
+                             float* grad_table, int64_t table_len, int32_t vocab, int32_t dim,
+                             int32_t padding_idx);
+int oracle_embedding_bwd_f32(const float* ids, int64_t n_ids, const float* dy, float* grad_table,
+                             int64_t table_len, int32_t vocab, int32_t dim, int32_t padding_idx);
 
 #ifdef __cplusplus
 }

@@ -133,3 +133,179 @@ def forward_named(layers, fin=None, iin=None):
             raise ModelError(f"Missing input tensor: {name}")
         fstore[L.get("output") or "x"] = np.asarray(_apply(L, ins), np.float32).ravel()
     return fstore["x"].copy()
+
+
+# ---------------------------------------------------------------------------
+# Training step without the optimizer: forwardPassNamed(training=true) with
+# the input snapshots, then Model::backwardPass (Model.cpp:7307-9153).
+# ---------------------------------------------------------------------------
+
+BACKWARD_SUPPORTED = ("LayerNorm", "RMSNorm", "Softmax", "LogSoftmax", "GELU", "SiLU", "Add", "Multiply",
+                      "Embedding", "Identity")
+# Model.cpp:7390-7402 (needs_input_values_for_backward): Add and Identity
+# keep only the input sizes.
+_SIZES_ONLY = ("Add", "Identity")
+
+
+def _forward_snap(layers, fin, iin):
+    """forward_named with the per-layer input snapshots the reference keeps in
+    training mode (Model.cpp:4858-4878): (values or None, sizes)."""
+    fin = {k: np.ascontiguousarray(v, np.float32).ravel() for k, v in (fin or {}).items()}
+    iin = {k: np.ascontiguousarray(v, np.int32).ravel() for k, v in (iin or {}).items()}
+    x0 = fin.get("x", fin.get("__input__", np.zeros(0, np.float32)))
+    fstore = {"x": x0, "__input__": x0}
+    istore = dict(iin)
+    if "seq" in iin:
+        for alias in ("text_ids", "__input__", "x"):
+            istore[alias] = iin["seq"]
+    fstore.update(fin)
+    snaps = []
+    for L in layers:
+        if L["type"] not in BACKWARD_SUPPORTED:
+            raise ModelError(f"unsupported layer type {L['type']} for backward")
+        names = L.get("inputs") or ["x"]
+        ins = []
+        for k, name in enumerate(names):
+            if name in fstore:
+                ins.append(fstore[name])
+                continue
+            if L["type"] == "Embedding" and k == 0:
+                if name not in istore:
+                    seq = L.get("seq_len", 0)
+                    pad = L.get("padding_idx", -1)
+                    istore[name] = np.full(seq if seq > 0 else 1, pad if pad >= 0 else 0, np.int32)
+                ins.append(istore[name].astype(np.float32))
+                continue
+            raise ModelError(f"Missing input tensor: {name}")
+        vals = None if L["type"] in _SIZES_ONLY else [a.copy() for a in ins]
+        snaps.append((vals, [a.size for a in ins]))
+        fstore[L.get("output") or "x"] = np.asarray(_apply(L, ins), np.float32).ravel()
+    return fstore["x"].copy(), snaps
+
+
+def backward_named(layers, fin, iin, loss_grad, scales=False):
+    """Returns (grads, input_grad) as oracle/model_ref.py's backward: the
+    per-layer grad_weights (None for layers without parameters) and the
+    gradient that reached "__input__" (None if none did).  With scales=True
+    also returns, per layer, the float64 sum of the magnitudes added into each
+    grad_weights element (the condition of those float32 sums; None where
+    nothing was added), for tolerances that must not depend on cancellation.
+
+    The gradient store mirrors the reference's std::unordered_map of vectors:
+    accumulate_grad (Model.cpp:7329-7341) copies into an absent name and adds
+    in place into a present one, and a branch's grad_out is a reference into
+    that map, so a layer whose input and output share a name adds its input
+    gradient onto its own output gradient (numpy in-place ops on the same
+    array reproduce this)."""
+    _, snaps = _forward_snap(layers, fin, iin)
+    grads = []
+    for L in layers:
+        w = L.get("weights")
+        pc = int(L.get("params_count", 0 if w is None else np.asarray(w).size))
+        grads.append(np.zeros(pc, np.float32) if pc > 0 else None)
+    store = {"x": np.ascontiguousarray(loss_grad, np.float32).ravel().copy()}
+    mags = [None] * len(layers)
+
+    def acc(name, src):
+        if name not in store:
+            store[name] = np.array(src, np.float32, copy=True)
+        else:
+            dst = store[name]
+            if dst.size != src.size:
+                raise ModelError("Gradient accumulate: size mismatch")
+            O.oracle_accumulate_inplace(dst, src)
+
+    for i in range(len(layers) - 1, -1, -1):
+        L = layers[i]
+        out = L.get("output") or "x"
+        if out not in store:
+            continue
+        g = store[out]
+        names = L.get("inputs") or ["x"]
+        vals, sizes = snaps[i]
+        n0 = sizes[0] if sizes else 0
+        t = L["type"]
+        if t == "Embedding":  # :7429-7461
+            ids = vals[0]
+            vocab = max(1, L.get("vocab_size", 0))
+            dim = max(1, L.get("embed_dim", 0))
+            if g.size != ids.size * dim:
+                continue
+            wv = L.get("weights")
+            if wv is None or np.asarray(wv).size < vocab * dim or grads[i] is None:
+                continue
+            grads[i] = O.embedding_bwd(ids, g, grads[i], vocab, dim, L.get("padding_idx", -1))
+            m = np.zeros((vocab, dim))
+            iid = np.array([int(np.round(v)) if abs(v - np.trunc(v)) != 0.5 else int(np.trunc(v) + np.sign(v))
+                            for v in ids.astype(np.float64)], np.int64)
+            keep = (iid >= 0) & (iid < vocab) & ~((L.get("padding_idx", -1) >= 0) & (iid == L.get("padding_idx", -1)))
+            np.add.at(m, iid[keep], np.abs(g.reshape(-1, dim)[keep].astype(np.float64)))
+            mags[i] = np.concatenate([m.ravel(), np.zeros(grads[i].size - m.size)])
+        elif t == "Identity":  # :7463-7468
+            if g.size != n0:
+                continue
+            acc(names[0], g)
+        elif t == "Add":  # :7541-7601
+            if len(sizes) < 2:
+                continue
+            n1 = sizes[1]
+            if g.size == n0 and g.size == n1:
+                acc(names[0], g)
+                acc(names[1], g)
+                continue
+            if g.size != n0 and g.size != n1:
+                continue
+            big0 = g.size == n0
+            big_name, small_name = (names[0], names[1]) if big0 else (names[1], names[0])
+            small_n = n1 if big0 else n0
+            acc(big_name, g)
+            if small_n == 1 or (small_n > 1 and g.size % small_n == 0):
+                acc(small_name, O.add_bwd_small(g, small_n))
+        elif t == "Multiply":  # :7647-7665
+            if len(vals) < 2 or g.size != vals[0].size or g.size != vals[1].size:
+                continue
+            g0, g1 = O.mul_bwd(vals[0], vals[1], g)
+            acc(names[0], g0)
+            acc(names[1], g1)
+        elif t == "LayerNorm":  # :7719-7821
+            x = vals[0]
+            if g.size != x.size:
+                continue
+            N = x.size
+            feat = L.get("in_features", 0) if L.get("in_features", 0) > 0 else N
+            if feat <= 0 or N % feat:
+                continue
+            affine = bool(L.get("affine", True))
+            has_bias = affine and bool(L.get("use_bias", True))
+            gamma = None
+            if affine:
+                wv = L.get("weights")
+                need = feat * (2 if has_bias else 1)
+                if wv is None or np.asarray(wv).size < need:
+                    continue
+                gamma = np.asarray(wv, np.float32)[:feat]
+            dx, gp = O.layernorm_bwd(x, g, feat, gamma, has_bias, L.get("eps", 1e-5),
+                                     None if gamma is None else grads[i][:feat * (2 if has_bias else 1)])
+            if gamma is not None:
+                grads[i][:gp.size] = gp
+                x64 = x.astype(np.float64).reshape(-1, feat)
+                xh = (x64 - x64.mean(axis=1, keepdims=True)) / np.sqrt(x64.var(axis=1, keepdims=True) + 1e-5)
+                g64 = np.abs(g.astype(np.float64).reshape(-1, feat))
+                m = [(g64 * np.abs(xh)).sum(axis=0)] + ([g64.sum(axis=0)] if has_bias else [])
+                mags[i] = np.concatenate(m + [np.zeros(grads[i].size - feat * len(m))])
+            acc(names[0], dx)
+        elif t == "GELU":  # :9026-9051
+            if g.size != vals[0].size:
+                continue
+            acc(names[0], O.gelu_bwd(vals[0], g))
+        elif t == "SiLU":  # :7993-8032
+            if g.size != vals[0].size:
+                continue
+            acc(names[0], O.silu_bwd(vals[0], g))
+        else:  # RMSNorm, Softmax, LogSoftmax: the fallback at :9133-9140
+            if g.size == n0:
+                acc(names[0], g)
+    gin = store.get("__input__")
+    if scales:
+        return grads, (None if gin is None else gin.copy()), mags
+    return grads, (None if gin is None else gin.copy())

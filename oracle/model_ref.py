@@ -1,5 +1,6 @@
 """ctypes front end for oracle/_ref/libmimir_ref_model.so: the reference's own
-Model::forwardPassNamed (Model.cpp:1352-1408, 4621-6824) on a layer list.
+Model::forwardPassNamed (Model.cpp:1352-1408, 4621-6824) and
+Model::backwardPass (Model.cpp:7307-9153) on a layer list.
 TEST INFRASTRUCTURE ONLY (pins oracle/model_oracle.py; writes golden fixtures)."""
 from __future__ import annotations
 
@@ -41,13 +42,17 @@ def _load():
                       c_int32, POINTER(c_char_p), POINTER(c_void_p), POINTER(c_int64), c_int32,
                       c_void_p, c_int64, POINTER(c_int64), c_char_p, c_int32]
         f.restype = c_int32
+        b = lib.ref_model_backward
+        b.argtypes = [POINTER(_Spec), c_int32, POINTER(c_char_p), POINTER(c_void_p), POINTER(c_int64),
+                      c_int32, POINTER(c_char_p), POINTER(c_void_p), POINTER(c_int64), c_int32,
+                      c_void_p, c_int64, POINTER(c_void_p), c_void_p, c_int64, POINTER(c_int64),
+                      c_char_p, c_int32]
+        b.restype = c_int32
         _lib = lib
     return _lib
 
 
-def forward_named(layers, fin=None, iin=None, out_cap=1 << 24):
-    """layers: list of dicts (see oracle.model_oracle.Layer fields); fin/iin:
-    {name: float32 / int32 array}.  Returns the float32 "x" output."""
+def _marshal(layers, fin, iin):
     fin = fin or {}
     iin = iin or {}
     keep = []
@@ -65,18 +70,51 @@ def forward_named(layers, fin=None, iin=None, out_cap=1 << 24):
                          int(L.get("seq_len", 0)))
     fa = {k: np.ascontiguousarray(v, np.float32).ravel() for k, v in fin.items()}
     ia = {k: np.ascontiguousarray(v, np.int32).ravel() for k, v in iin.items()}
+    keep += list(fa.values()) + list(ia.values())
     fn = (c_char_p * max(1, len(fa)))(*[k.encode() for k in fa])
     fd = (c_void_p * max(1, len(fa)))(*[v.ctypes.data for v in fa.values()])
     fs = (c_int64 * max(1, len(fa)))(*[v.size for v in fa.values()])
     inn = (c_char_p * max(1, len(ia)))(*[k.encode() for k in ia])
     idd = (c_void_p * max(1, len(ia)))(*[v.ctypes.data for v in ia.values()])
     isz = (c_int64 * max(1, len(ia)))(*[v.size for v in ia.values()])
+    return keep, (specs, len(layers), fn, fd, fs, len(fa), inn, idd, isz, len(ia))
+
+
+def forward_named(layers, fin=None, iin=None, out_cap=1 << 24):
+    """layers: list of dicts (see oracle.model_oracle.Layer fields); fin/iin:
+    {name: float32 / int32 array}.  Returns the float32 "x" output."""
+    keep, args = _marshal(layers, fin, iin)
     out = np.empty(out_cap, np.float32)
     n = c_int64(0)
     err = ctypes.create_string_buffer(512)
-    st = _load().ref_model_forward(specs, len(layers), fn, fd, fs, len(fa), inn, idd, isz, len(ia),
-                                   out.ctypes.data, out_cap, ctypes.byref(n), err, 512)
+    st = _load().ref_model_forward(*args, out.ctypes.data, out_cap, ctypes.byref(n), err, 512)
+    del keep
     if st:
         raise RefModelError(err.value.decode(errors="replace"))
     assert n.value <= out_cap, "output larger than out_cap"
     return out[:n.value].copy()
+
+
+def backward(layers, fin, iin, loss_grad, in_cap=1 << 24):
+    """forwardPassNamed(training=true) then backwardPass(loss_grad).  Returns
+    (grads, input_grad): grads[i] = the layer's grad_weights (params_count
+    floats, or None for a layer without parameters); input_grad = the gradient
+    that reached "__input__" (None if none did)."""
+    keep, args = _marshal(layers, fin, iin)
+    g = np.ascontiguousarray(loss_grad, np.float32).ravel()
+    grads = []
+    for L in layers:
+        w = L.get("weights")
+        pc = int(L.get("params_count", 0 if w is None else np.asarray(w).size))
+        grads.append(np.zeros(pc, np.float32) if pc > 0 else None)
+    gp = (c_void_p * max(1, len(layers)))(*[0 if a is None else a.ctypes.data for a in grads])
+    ig = np.empty(in_cap, np.float32)
+    n = c_int64(0)
+    err = ctypes.create_string_buffer(512)
+    st = _load().ref_model_backward(*args, g.ctypes.data, g.size, gp, ig.ctypes.data, in_cap,
+                                    ctypes.byref(n), err, 512)
+    del keep
+    if st:
+        raise RefModelError(err.value.decode(errors="replace"))
+    assert n.value <= in_cap, "input gradient larger than in_cap"
+    return grads, (None if n.value < 0 else ig[:n.value].copy())

@@ -63,12 +63,21 @@ def _oracle():
             "oracle_embedding_f32": [P, c_int64, P, c_int64, c_int32, c_int32, c_int32, P],
             "oracle_rope_table": [c_int64, c_int64, c_double, P, P],
             "oracle_rope": [P, P, c_int64, c_int64, c_int64, c_int64, c_int64, P, P, c_int64],
+            "oracle_accumulate": [P, P, c_int64],
+            "oracle_layernorm_bwd": [P, P, c_int64, c_int64, P, c_int32, c_float, P, P],
+            "oracle_gelu_bwd": [P, P, c_int64, P],
+            "oracle_silu_bwd": [P, P, c_int64, P],
+            "oracle_mul_bwd": [P, P, P, c_int64, P, P],
+            "oracle_add_bwd_small": [P, c_int64, c_int64, P],
+            "oracle_embedding_bwd_i32": [P, c_int64, P, P, c_int64, c_int32, c_int32, c_int32],
+            "oracle_embedding_bwd_f32": [P, c_int64, P, P, c_int64, c_int32, c_int32, c_int32],
         }
         for name, args in sig.items():
             fn = getattr(lib, name)
             fn.argtypes = args
             fn.restype = None if name in ("oracle_gelu", "oracle_silu", "oracle_silu_mul",
-                                          "oracle_gelu_mul") else c_int32
+                                          "oracle_gelu_mul", "oracle_accumulate", "oracle_gelu_bwd",
+                                          "oracle_silu_bwd", "oracle_mul_bwd") else c_int32
         _o = lib
     return _o
 
@@ -247,6 +256,88 @@ def rope(x, cos_tab, sin_tab, pos_offset=0):
     _check(_oracle().oracle_rope(_p(x), _p(y), B, S, H, D, pos_offset, _p(c), _p(s),
                                  c.shape[0]), "rope")
     return y
+
+
+# --------------------------------------------------------------------------
+# C restatement: backward (Model::backwardPass branches)
+# --------------------------------------------------------------------------
+
+def accumulate(dst, src):
+    """accumulate_grad's add (Model.cpp:7329-7341): returns dst + src."""
+    d = _f32(dst).ravel().copy()
+    s = _f32(src).ravel()
+    assert d.size == s.size
+    _oracle().oracle_accumulate(_p(d), _p(s), d.size)
+    return d
+
+
+def oracle_accumulate_inplace(dst, src):
+    """accumulate_grad's add in place on dst (a float32 C-contiguous array;
+    src may be dst itself, as in the reference's aliasing case)."""
+    assert dst.dtype == np.float32 and dst.flags.c_contiguous and dst.size == src.size
+    s = src if src is dst else _f32(src)
+    _oracle().oracle_accumulate(_p(dst), _p(s), dst.size)
+
+
+def layernorm_bwd(x, dy, in_features, gamma=None, has_bias=False, eps=1e-5, grad_params=None):
+    """Returns (dx, grad_params): dx of x's shape; grad_params = the
+    [dgamma | dbeta] block added onto the given one (zeros when None)."""
+    x = _f32(x).ravel()
+    dy = _f32(dy).ravel()
+    assert x.size == dy.size
+    feat = in_features if in_features > 0 else x.size
+    g = None if gamma is None else _f32(gamma)
+    gp = None
+    if g is not None:
+        gp = (np.zeros(feat * (2 if has_bias else 1), np.float32) if grad_params is None
+              else _f32(grad_params).copy())
+    dx = np.empty_like(x)
+    _check(_oracle().oracle_layernorm_bwd(_p(x), _p(dy), x.size, int(in_features), _p(g), int(bool(has_bias)),
+                                          eps, _p(dx), _p(gp)), "layernorm_bwd")
+    return dx, gp
+
+
+def gelu_bwd(x, dy):
+    x, dy = _f32(x), _f32(dy)
+    dx = np.empty_like(x)
+    _oracle().oracle_gelu_bwd(_p(x), _p(dy), x.size, _p(dx))
+    return dx
+
+
+def silu_bwd(x, dy):
+    x, dy = _f32(x), _f32(dy)
+    dx = np.empty_like(x)
+    _oracle().oracle_silu_bwd(_p(x), _p(dy), x.size, _p(dx))
+    return dx
+
+
+def mul_bwd(a, b, dy):
+    a, b, dy = _f32(a), _f32(b), _f32(dy)
+    da, db = np.empty_like(a), np.empty_like(a)
+    _oracle().oracle_mul_bwd(_p(a), _p(b), _p(dy), a.size, _p(da), _p(db))
+    return da, db
+
+
+def add_bwd_small(dy, n_small):
+    dy = _f32(dy).ravel()
+    out = np.empty(n_small, np.float32)
+    _check(_oracle().oracle_add_bwd_small(_p(dy), dy.size, int(n_small), _p(out)), "add_bwd_small")
+    return out
+
+
+def embedding_bwd(ids, dy, grad_table, vocab, dim, padding_idx=-1):
+    """Returns grad_table + the scatter-added rows (ids int32, or float ids)."""
+    dy = _f32(dy).ravel()
+    gt = _f32(grad_table).ravel().copy()
+    if np.asarray(ids).dtype == np.float32:
+        ids = _f32(ids).ravel()
+        fn = _oracle().oracle_embedding_bwd_f32
+    else:
+        ids = np.ascontiguousarray(ids, np.int32).ravel()
+        fn = _oracle().oracle_embedding_bwd_i32
+    _check(fn(_p(ids), ids.size, _p(dy), _p(gt), gt.size, int(vocab), int(dim), int(padding_idx)),
+           "embedding_bwd")
+    return gt
 
 
 # --------------------------------------------------------------------------

@@ -1,7 +1,8 @@
 // ref_model_harness.cpp -- TEST INFRASTRUCTURE ONLY.
 //
 // Drives the reference's own runtime, Model::forwardPassNamed
-// (Model.cpp:1352-1408 -> forwardPassView, Model.cpp:4621-6824), on a layer
+// (Model.cpp:1352-1408 -> forwardPassView, Model.cpp:4621-6824) and
+// Model::backwardPass (Model.cpp:7307-9153), on a layer
 // list described by plain C structs.  Compiled with the reference's sources
 // in place (oracle/Makefile, target `ref_model`) into
 // oracle/_ref/libmimir_ref_model.so; used only to pin the routing
@@ -38,6 +39,58 @@ struct ref_layer_spec {
     int32_t seq_len;
 };
 
+// Layers from the specs, weights copied into the blocks allocateParams made.
+static void build_model(Model& m, const ref_layer_spec* specs, int32_t n_layers) {
+    for (int32_t i = 0; i < n_layers; ++i)
+        m.push(specs[i].name, specs[i].type, static_cast<size_t>(specs[i].params_count));
+    auto& layers = m.getMutableLayers();
+    for (int32_t i = 0; i < n_layers; ++i) {
+        Layer& L = layers[i];
+        const ref_layer_spec& s = specs[i];
+        L.inputs.clear();
+        if (s.inputs && *s.inputs) {
+            std::stringstream ss(s.inputs);
+            std::string tok;
+            while (std::getline(ss, tok, ',')) L.inputs.push_back(tok);
+        }
+        L.output = s.output ? s.output : "";
+        L.eps = s.eps;
+        L.affine = s.affine != 0;
+        L.use_bias = s.use_bias != 0;
+        L.in_features = s.in_features;
+        L.vocab_size = s.vocab_size;
+        L.embed_dim = s.embed_dim;
+        L.padding_idx = s.padding_idx;
+        L.seq_len = s.seq_len;
+    }
+    m.allocateParams();
+    for (int32_t i = 0; i < n_layers; ++i) {
+        const ref_layer_spec& s = specs[i];
+        if (s.params_count > 0 && s.weights) {
+            float* w = layers[i].getWeights();
+            std::memcpy(w, s.weights, static_cast<size_t>(s.params_count) * sizeof(float));
+        }
+    }
+}
+
+static void copy_error(const std::exception& e, char* err, int32_t err_cap) {
+    if (err && err_cap > 0) {
+        std::strncpy(err, e.what(), static_cast<size_t>(err_cap) - 1);
+        err[err_cap - 1] = 0;
+    }
+}
+
+static std::vector<float> run_forward(Model& m, const char* const* fnames, const float* const* fdata,
+                                      const int64_t* fsizes, int32_t nf, const char* const* inames,
+                                      const int32_t* const* idata, const int64_t* isizes, int32_t ni,
+                                      bool training) {
+    std::unordered_map<std::string, std::vector<float>> fin;
+    std::unordered_map<std::string, std::vector<int>> iin;
+    for (int32_t i = 0; i < nf; ++i) fin[fnames[i]] = std::vector<float>(fdata[i], fdata[i] + fsizes[i]);
+    for (int32_t i = 0; i < ni; ++i) iin[inames[i]] = std::vector<int>(idata[i], idata[i] + isizes[i]);
+    return m.forwardPassNamed(fin, iin, training);
+}
+
 // Named inputs: nf float tensors and ni int tensors.  Writes at most out_cap
 // floats of the returned "x" to out and its size to *out_n.  Returns 0, or 1
 // when the reference throws (message copied to err).
@@ -48,50 +101,51 @@ int ref_model_forward(const ref_layer_spec* specs, int32_t n_layers, const char*
                       int32_t err_cap) {
     try {
         Model m;
-        for (int32_t i = 0; i < n_layers; ++i)
-            m.push(specs[i].name, specs[i].type, static_cast<size_t>(specs[i].params_count));
-        auto& layers = m.getMutableLayers();
-        for (int32_t i = 0; i < n_layers; ++i) {
-            Layer& L = layers[i];
-            const ref_layer_spec& s = specs[i];
-            L.inputs.clear();
-            if (s.inputs && *s.inputs) {
-                std::stringstream ss(s.inputs);
-                std::string tok;
-                while (std::getline(ss, tok, ',')) L.inputs.push_back(tok);
-            }
-            L.output = s.output ? s.output : "";
-            L.eps = s.eps;
-            L.affine = s.affine != 0;
-            L.use_bias = s.use_bias != 0;
-            L.in_features = s.in_features;
-            L.vocab_size = s.vocab_size;
-            L.embed_dim = s.embed_dim;
-            L.padding_idx = s.padding_idx;
-            L.seq_len = s.seq_len;
-        }
-        m.allocateParams();
-        for (int32_t i = 0; i < n_layers; ++i) {
-            const ref_layer_spec& s = specs[i];
-            if (s.params_count > 0 && s.weights) {
-                float* w = layers[i].getWeights();
-                std::memcpy(w, s.weights, static_cast<size_t>(s.params_count) * sizeof(float));
-            }
-        }
-        std::unordered_map<std::string, std::vector<float>> fin;
-        std::unordered_map<std::string, std::vector<int>> iin;
-        for (int32_t i = 0; i < nf; ++i) fin[fnames[i]] = std::vector<float>(fdata[i], fdata[i] + fsizes[i]);
-        for (int32_t i = 0; i < ni; ++i) iin[inames[i]] = std::vector<int>(idata[i], idata[i] + isizes[i]);
-        const std::vector<float> y = m.forwardPassNamed(fin, iin, /*training=*/false);
+        build_model(m, specs, n_layers);
+        const std::vector<float> y = run_forward(m, fnames, fdata, fsizes, nf, inames, idata, isizes, ni, false);
         *out_n = static_cast<int64_t>(y.size());
         const size_t n = std::min(static_cast<size_t>(out_cap), y.size());
         if (n) std::memcpy(out, y.data(), n * sizeof(float));
         return 0;
     } catch (const std::exception& e) {
-        if (err && err_cap > 0) {
-            std::strncpy(err, e.what(), static_cast<size_t>(err_cap) - 1);
-            err[err_cap - 1] = 0;
+        copy_error(e, err, err_cap);
+        return 1;
+    }
+}
+
+// Training step without the optimizer: forwardPassNamed(training=true), then
+// Model::backwardPass(loss_grad) (Model.cpp:7307-9153).  Per layer i with
+// grads_out[i] non-null, writes params_count floats of Layer::grad_weights
+// (zeros where the reference left it empty).  The gradient that reached the
+// tensor "__input__" (Model::getLastInputGradient) goes to in_grad (at most
+// in_cap floats; *in_n = its size, or -1 when none reached it).
+int ref_model_backward(const ref_layer_spec* specs, int32_t n_layers, const char* const* fnames,
+                       const float* const* fdata, const int64_t* fsizes, int32_t nf,
+                       const char* const* inames, const int32_t* const* idata, const int64_t* isizes,
+                       int32_t ni, const float* loss_grad, int64_t n_grad, float* const* grads_out,
+                       float* in_grad, int64_t in_cap, int64_t* in_n, char* err, int32_t err_cap) {
+    try {
+        Model m;
+        build_model(m, specs, n_layers);
+        run_forward(m, fnames, fdata, fsizes, nf, inames, idata, isizes, ni, true);
+        m.backwardPass(std::vector<float>(loss_grad, loss_grad + n_grad));
+        const auto& layers = m.getLayers();
+        for (int32_t i = 0; i < n_layers; ++i) {
+            if (!grads_out || !grads_out[i]) continue;
+            const size_t pc = static_cast<size_t>(specs[i].params_count);
+            const std::vector<float>& g = layers[i].grad_weights;
+            for (size_t k = 0; k < pc; ++k) grads_out[i][k] = k < g.size() ? g[k] : 0.0f;
         }
+        *in_n = -1;
+        if (m.hasLastInputGradient()) {
+            const std::vector<float>& g = m.getLastInputGradient();
+            *in_n = static_cast<int64_t>(g.size());
+            const size_t n = std::min(static_cast<size_t>(in_cap), g.size());
+            if (n) std::memcpy(in_grad, g.data(), n * sizeof(float));
+        }
+        return 0;
+    } catch (const std::exception& e) {
+        copy_error(e, err, err_cap);
         return 1;
     }
 }

@@ -106,3 +106,109 @@ def error_graphs():
          [dict(name="e", type="Embedding", inputs=["ids"], vocab_size=4, embed_dim=4,
                weights=np.ones(15, np.float32))], {}, {"ids": [1]}),
     ]
+
+
+# Graphs for a training step (forwardPassNamed(training=true) then
+# Model::backwardPass): (name, layers, float_inputs, int_inputs, loss_grad).
+# What the reference exposes after backwardPass is each layer's grad_weights
+# and the gradient that reached "__input__", so every graph routes its
+# gradient into parameters and/or "__input__".
+def train_graphs():
+    out = []
+
+    # Embedding (repeated, padding and out-of-range ids) -> per-token LN ->
+    # GELU -> residual Add -> RMSNorm layer -> SiLU -> gate Multiply -> Softmax.
+    r = _rng(11)
+    vocab, d, seq = 20, 64, 24
+    table = (0.5 * r.standard_normal(vocab * d)).astype(np.float32)
+    ln_w = np.concatenate([1 + 0.1 * r.standard_normal(d), 0.1 * r.standard_normal(d)]).astype(np.float32)
+    rms_w = (1 + 0.1 * r.standard_normal(seq * d)).astype(np.float32)
+    gate = r.standard_normal(seq * d).astype(np.float32)
+    ids = r.integers(-2, vocab + 2, seq).astype(np.int32)
+    ids[:4] = 5  # one row hit several times: its gradient is a sum in token order
+    out.append(("block_train",
+                [dict(name="tok", type="Embedding", inputs=["text_ids"], output="h", vocab_size=vocab,
+                      embed_dim=d, padding_idx=1, weights=table),
+                 dict(name="ln", type="LayerNorm", inputs=["h"], output="n", in_features=d, eps=1e-5,
+                      weights=ln_w),
+                 dict(name="act", type="GELU", inputs=["n"], output="g"),
+                 dict(name="residual", type="Add", inputs=["g", "h"], output="h2"),
+                 dict(name="rms", type="RMSNorm", inputs=["h2"], output="r", eps=1e-6, weights=rms_w),
+                 dict(name="silu", type="SiLU", inputs=["r"], output="s"),
+                 dict(name="gate", type="Multiply", inputs=["s", "gate"], output="m"),
+                 dict(name="sm", type="Softmax", inputs=["m"], output="x")],
+                {"gate": gate}, {"seq": ids}, r.standard_normal(seq * d).astype(np.float32)))
+
+    # The gradient reaches "__input__" through LN (no bias), SiLU, a bias
+    # broadcast Add, GELU, Multiply and Identity.
+    r = _rng(12)
+    rows, d = 10, 48
+    xin = (1.5 * r.standard_normal(rows * d) + 0.2).astype(np.float32)
+    out.append(("input_chain",
+                [dict(name="ln", type="LayerNorm", inputs=["__input__"], output="a", in_features=d,
+                      use_bias=False, weights=(1 + 0.2 * r.standard_normal(d)).astype(np.float32)),
+                 dict(name="silu", type="SiLU", inputs=["a"], output="b"),
+                 dict(name="bias", type="Add", inputs=["bvec", "b"], output="c"),
+                 dict(name="gelu", type="GELU", inputs=["c"], output="e"),
+                 dict(name="mul", type="Multiply", inputs=["e", "scale"], output="f"),
+                 dict(name="id", type="Identity", inputs=["f"], output="x")],
+                {"__input__": xin, "bvec": r.standard_normal(d).astype(np.float32),
+                 "scale": r.standard_normal(rows * d).astype(np.float32)}, {},
+                r.standard_normal(rows * d).astype(np.float32)))
+
+    # "__input__" as the broadcast operand: its gradient is the per-position
+    # sum over the tiles (repeat) and, through a scalar Add, the total sum.
+    r = _rng(13)
+    big = r.standard_normal(16 * 32).astype(np.float32)
+    out.append(("broadcast_reduce",
+                [dict(name="rep", type="Add", inputs=["big", "__input__"], output="h"),
+                 dict(name="ln", type="LayerNorm", inputs=["h"], output="x", in_features=32,
+                      weights=np.concatenate([np.ones(32), np.zeros(32)]).astype(np.float32))],
+                {"big": big, "__input__": r.standard_normal(32).astype(np.float32)}, {},
+                r.standard_normal(16 * 32).astype(np.float32)))
+    out.append(("scalar_reduce",
+                [dict(name="sc", type="Add", inputs=["__input__", "big"], output="h"),
+                 dict(name="gelu", type="GELU", inputs=["h"], output="x")],
+                {"big": big, "__input__": np.array([0.25], np.float32)}, {},
+                r.standard_normal(16 * 32).astype(np.float32)))
+
+    # Every layer reads and writes "x": the reference's gradient map then
+    # adds a layer's input gradient onto its own output gradient (the same
+    # vector), and Add(x, x) doubles it twice.  LN's grad_weights observe it.
+    r = _rng(14)
+    x = (r.standard_normal(8 * 16) + 0.5).astype(np.float32)
+    out.append(("same_name_aliasing",
+                [dict(name="ln", type="LayerNorm", in_features=16,
+                      weights=np.concatenate([1 + 0.1 * r.standard_normal(16),
+                                              0.1 * r.standard_normal(16)]).astype(np.float32)),
+                 dict(name="gelu", type="GELU"),
+                 dict(name="twice", type="Add", inputs=["x", "x"]),
+                 dict(name="id", type="Identity"),
+                 dict(name="rms", type="RMSNorm", affine=False, eps=1e-5),
+                 dict(name="lsm", type="LogSoftmax")],
+                {"x": x}, {}, r.standard_normal(8 * 16).astype(np.float32)))
+
+    # Float ids (llround) with a padding id and ids outside the vocab; a
+    # non-affine LN and a whole-vector LN (in_features 0).
+    r = _rng(15)
+    fids = np.array([0.0, 1.4, 1.5, 2.5, -0.5, 7.49, 7.5, 9.0, 100.0, -3.0, 2.0, 2.2], np.float32)
+    out.append(("float_ids_train",
+                [dict(name="e", type="Embedding", inputs=["ids_f"], output="e", vocab_size=8, embed_dim=16,
+                      padding_idx=7, weights=r.standard_normal(8 * 16).astype(np.float32)),
+                 dict(name="ln1", type="LayerNorm", inputs=["e"], output="a", in_features=16, affine=False),
+                 dict(name="ln2", type="LayerNorm", inputs=["a"], output="x",
+                      weights=np.concatenate([1 + 0.1 * r.standard_normal(12 * 16),
+                                              0.1 * r.standard_normal(12 * 16)]).astype(np.float32))],
+                {"ids_f": fids}, {}, r.standard_normal(12 * 16).astype(np.float32)))
+
+    # A residual block at the BASELINE width, [32 tokens x 4096].
+    r = _rng(16)
+    xs = r.standard_normal(32 * 4096).astype(np.float32)
+    w2 = np.concatenate([1 + 0.02 * r.standard_normal(4096), 0.02 * r.standard_normal(4096)]).astype(np.float32)
+    out.append(("wide_block_train",
+                [dict(name="ln", type="LayerNorm", inputs=["__input__"], output="n", in_features=4096,
+                      weights=w2),
+                 dict(name="gelu", type="GELU", inputs=["n"], output="g"),
+                 dict(name="res", type="Add", inputs=["g", "__input__"], output="x")],
+                {"__input__": xs}, {}, r.standard_normal(32 * 4096).astype(np.float32)))
+    return out

@@ -80,3 +80,24 @@ def assert_close_or_nearer_exact(got, ref, exact, what=""):
         i = np.flatnonzero(bad)[0]
         raise AssertionError(f"{what}: {int(bad.sum())} elements fail; first: got {g[i]!r} "
                              f"ref {r[i]!r} exact {e[i]!r}")
+
+
+def assert_close_sum(got, ref, scale, what=""):
+    """For results that are float32 sums (gradient accumulations over tokens):
+    |got - ref| <= max(1e-6, 1e-5 * max(|ref|, scale)), scale = the sum of the
+    magnitudes added into the element.  Two float32 summation orders differ
+    by up to ~u * scale, so a tolerance relative to the (possibly cancelled)
+    result alone would reject correct sums."""
+    got = np.asarray(got, np.float64).ravel()
+    ref = np.asarray(ref, np.float64).ravel()
+    sc = np.zeros_like(ref) if scale is None else np.asarray(scale, np.float64).ravel()
+    assert got.shape == ref.shape, f"{what}: shape {got.shape} != {ref.shape}"
+    assert np.array_equal(np.isnan(got), np.isnan(ref)), f"{what}: NaN pattern differs"
+    fin = np.isfinite(ref)
+    d = np.abs(got[fin] - ref[fin])
+    tol = np.maximum(ABS, REL * np.maximum(np.abs(ref[fin]), sc[fin]))
+    bad = d > tol
+    if bad.any():
+        idx = np.flatnonzero(fin)[np.argmax(d / tol)]
+        raise AssertionError(f"{what}: {int(bad.sum())} of {fin.sum()} elements out of tolerance; worst at "
+                             f"{idx}: got {got[idx]!r} ref {ref[idx]!r} scale {sc[idx]:.3g}")

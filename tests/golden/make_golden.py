@@ -143,6 +143,38 @@ def write_model_graphs():
     print("wrote model_graphs", sorted(outs))
 
 
+def write_model_backward():
+    """Gradients of the reference's Model::backwardPass on tests/_graphs.py
+    train_graphs(): per graph, each layer's grad_weights and the gradient
+    that reached "__input__"."""
+    sys.path.insert(0, os.path.join(REPO, "tests"))
+    import model_ref as MR
+    from _graphs import train_graphs
+    if not MR.available():
+        sys.exit("oracle/_ref/libmimir_ref_model.so is not built: make -C oracle ref_model")
+    outs = {}
+    for name, layers, fin, iin, lg in train_graphs():
+        grads, gin = MR.backward(layers, fin, iin, lg)
+        if gin is not None:
+            outs[f"{name}/__input__"] = gin
+        for L, g in zip(layers, grads):
+            if g is not None:
+                outs[f"{name}/{L['name']}"] = g
+    np.savez_compressed(os.path.join(HERE, "model_backward.npz"), **outs)
+    path = os.path.join(HERE, "MANIFEST.json")
+    manifest = json.load(open(path))
+    manifest["model_backward"] = {
+        "note": "Model::forwardPassNamed(training=true) then Model::backwardPass (Model.cpp:7307-9153) on "
+                "tests/_graphs.py train_graphs(): grad_weights per layer and the __input__ gradient",
+        "arrays": {k: {"shape": list(v.shape), "dtype": str(v.dtype), "sha256": sha(v)} for k, v in outs.items()},
+        "regenerated_inputs": {"tests/_graphs.py": "train_graphs()"},
+    }
+    with open(path, "w") as f:
+        json.dump(manifest, f, indent=1, sort_keys=True)
+    print("wrote model_backward", len(outs), "arrays")
+
+
 if __name__ == "__main__":
     main()
     write_model_graphs()
+    write_model_backward()
