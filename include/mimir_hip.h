@@ -198,6 +198,65 @@ int mimir_rope_fwd(mimir_ctx* ctx, const float* q, float* q_out, int64_t q_heads
                    int64_t table_rows);
 
 /* ---------------------------------------------------------------------------
+ * Backward of the path's ops: the branches of the reference's
+ * Model::backwardPass (Model.cpp:7305-9153).  Device pointers, stream order.
+ *
+ * Gradient outputs follow the reference's accumulate_grad (Model.cpp:
+ * 7329-7341): with `accumulate` 0 the gradient is written (the name had no
+ * gradient yet), with 1 it is added onto what the buffer holds.  Products
+ * and sums are rounded where the reference rounds them (no FMA
+ * contraction), so Multiply / Add gradients and the accumulation itself are
+ * bit-identical; the Embedding scatter-add adds in token order and is
+ * bit-identical too.  Reductions over tokens (dgamma, dbeta, the broadcast
+ * operand of Add) are deterministic: the same inputs give the same bits.
+ * Scratch for partial sums is the context's (reused in stream order).
+ * ------------------------------------------------------------------------- */
+
+/* LayerNorm branch, Model.cpp:7719-7821, over `groups` groups of n
+ * (n = in_features, or the whole input).  gamma NULL when the layer is not
+ * affine.  dx gets the input gradient ((+)= per `accumulate`); dgamma /
+ * dbeta (n floats each, or NULL) are ADDED to, as the reference adds into
+ * Layer::grad_weights (:7809-7819); dbeta needs dgamma, dgamma needs gamma.
+ * dx may alias dy. */
+int mimir_layernorm_bwd(mimir_ctx* ctx, const float* x, const float* dy, const float* gamma, float* dx,
+                        float* dgamma, float* dbeta, int64_t groups, int64_t n, float eps, int accumulate);
+
+/* GELU branch, Model.cpp:9026-9051 (tanh approximation): dx (+)= dy * gelu'(x). */
+int mimir_gelu_bwd(mimir_ctx* ctx, const float* x, const float* dy, float* dx, int64_t n, int accumulate);
+
+/* SiLU branch, Model.cpp:7993-8032: dx (+)= dy * (s + x*s*(1-s)), s = sigmoid(x). */
+int mimir_silu_bwd(mimir_ctx* ctx, const float* x, const float* dy, float* dx, int64_t n, int accumulate);
+
+/* Multiply branch, Model.cpp:7647-7665: da (+)= dy*b, db (+)= dy*a, both
+ * products formed before either accumulation.  da or db may be NULL.  When
+ * da == db (a tensor times itself) the second accumulation adds onto the
+ * first. */
+int mimir_mul_bwd(mimir_ctx* ctx, const float* a, const float* b, const float* dy, float* da, float* db,
+                  int64_t n, int acc_a, int acc_b);
+
+/* Add branch, Model.cpp:7541-7601, for add_forward(a[na], b[nb]) whose output
+ * gradient dy has max(na, nb) floats.  Equal sizes: da (+)= dy, then
+ * db (+)= dy.  Broadcast: the big operand's gradient (+)= dy, then the small
+ * operand's (+)= the sum of dy over the tiles (nb == 1: over all of it).
+ * Accumulations run in the reference's order and see each other where the
+ * buffers alias (dy, da, db may be the same buffer, as names can be in the
+ * reference's gradient map).  da or db may be NULL. */
+int mimir_add_bwd(mimir_ctx* ctx, const float* dy, int64_t na, int64_t nb, float* da, float* db, int acc_a,
+                  int acc_b);
+
+/* Embedding branch, Model.cpp:7429-7461: grad_table[id*dim + d] += dy[t*dim + d]
+ * for every token t in order; the padding id and ids outside [0, vocab) are
+ * skipped.  grad_table holds at least vocab*dim floats (table_len); dy holds
+ * n_ids*dim. */
+int mimir_embedding_bwd(mimir_ctx* ctx, const int32_t* ids, int64_t n_ids, const float* dy,
+                        float* grad_table, int64_t table_len, int32_t vocab, int32_t dim,
+                        int32_t padding_idx);
+/* Same with float ids rounded by llround (Model.cpp:7453). */
+int mimir_embedding_f32ids_bwd(mimir_ctx* ctx, const float* ids, int64_t n_ids, const float* dy,
+                               float* grad_table, int64_t table_len, int32_t vocab, int32_t dim,
+                               int32_t padding_idx);
+
+/* ---------------------------------------------------------------------------
  * Device-resident runtime: a named tensor store and a layer runner with the
  * routing of the reference's Model::forwardPassNamed (Model.cpp:1352-1408,
  * forwardPassView Model.cpp:4621-6824) for the layer types of this path.

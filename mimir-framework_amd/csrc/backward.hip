@@ -1,0 +1,861 @@
+// backward.hip -- backward of the path's ops for gfx950: the branches of
+// Model::backwardPass (Model.cpp:7305-9153) for LayerNorm, GELU, SiLU,
+// Multiply, Add and Embedding.
+//
+// The reference builds with -std=c++17 (CMakeLists.txt:8-10, no GNU
+// extensions), so GCC does not contract a*b+c into FMAs there; this file
+// turns contraction off as well, so every product and sum is rounded where
+// the reference rounds it.  That keeps Multiply's and Add's gradients, and
+// accumulate_grad's `dst += src` (Model.cpp:7329-7341), bit-identical.
+//
+// Kernels:
+//   dact_vec / dact_scalar   GELU and SiLU input gradients (3 streams)
+//   mul_bwd_*                Multiply: da = dy*b, db = dy*a (5 streams)
+//   add_bwd_*                Add: the big operand's gradient is dy itself;
+//                            the broadcast operand's is a column (or total)
+//                            sum of dy, reduced in two deterministic passes
+//   ln_bwd_vec               LayerNorm, rows held in VGPRs as in the forward
+//                            (rows.hpp shapes), a persistent grid: each
+//                            workgroup slot keeps its dgamma/dbeta column
+//                            sums in registers over the rows it visits and
+//                            writes them once; sum_slots adds the slots in a
+//                            fixed order into grad_weights
+//   ln_stats_generic, ln_bwd_params_part, ln_bwd_generic  any width / alignment
+//   embed_bwd_*              scatter-add of dy rows into the gradient table:
+//                            (id, token) pairs are sorted by id (stable radix
+//                            sort), then one workgroup per distinct id adds
+//                            its tokens' rows in token order -- the same
+//                            sequence of float adds as the reference, so the
+//                            result is bit-identical and deterministic.
+#include "common.hpp"
+#include "internal.hpp"
+#include "ids.hpp"
+
+#include <math.h>
+
+#include <rocprim/device/device_radix_sort.hpp>
+
+#pragma clang fp contract(off)
+
+using namespace mimir;
+
+namespace {
+
+// ---------------------------------------------------------------------------
+// Elementwise input gradients
+// ---------------------------------------------------------------------------
+
+// GELU branch, Model.cpp:9026-9051:
+//   u = s*(x + c*x^3), t = tanh(u),
+//   dgelu = 0.5*(1+t) + 0.5*x*(1-t*t)*du_dx,   du_dx = s*(1 + 3c*x^2)
+// evaluated with e = exp(-2|u|) and r = 1/(1+e), for which
+//   0.5*(1+t) = sigmoid(2u) = (u >= 0 ? r : e*r)   and   1 - t*t = 4*e*r^2
+// exactly: the same function without the cancellation of 1+t and 1-t*t
+// (the reference's float result carries a few ulp of 1 there, times
+// 0.5*|x|*du_dx).  inf / NaN inputs give NaN, as in the reference.
+__device__ __forceinline__ float dgelu1(float x) {
+    const float s = __builtin_sqrtf(2.0f / 3.14159265359f);
+    const float c = 0.044715f;
+    const float u = s * (x + c * x * x * x);
+    const float e = expf(-2.0f * fabsf(u));
+    const float r = __builtin_amdgcn_rcpf(1.0f + e);
+    const float half_1pt = u >= 0.0f ? r : e * r;
+    const float sech2 = 4.0f * e * r * r;
+    const float du_dx = s * (1.0f + 3.0f * c * x * x);
+    return half_1pt + 0.5f * x * sech2 * du_dx;
+}
+
+// SiLU branch, Model.cpp:8021-8027: s = 1/(1+exp(-x)); dy_dx = s + x*s*(1-s).
+__device__ __forceinline__ float dsilu1(float x) {
+    const float s = 1.0f / (1.0f + expf(-x));
+    const float ds = s * (1.0f - s);
+    return s + x * ds;
+}
+
+struct DGelu {
+    __device__ float operator()(float x) const { return dgelu1(x); }
+};
+struct DSilu {
+    __device__ float operator()(float x) const { return dsilu1(x); }
+};
+
+// dx = dy * f'(x), or dx += that (accumulate_grad into a present gradient).
+template <class F, bool ACC>
+__global__ __launch_bounds__(kBlock) void dact_vec(const float* x, const float* dy, float* dx, int64_t n4, F f) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
+    if (i >= n4) return;
+    const f4 xv = ld4<true>(x + 4 * i);
+    const f4 g = ld4<true>(dy + 4 * i);
+    f4 o{g.x * f(xv.x), g.y * f(xv.y), g.z * f(xv.z), g.w * f(xv.w)};
+    if constexpr (ACC) o = ld4<true>(dx + 4 * i) + o;
+    st4<true>(dx + 4 * i, o);
+}
+
+template <class F, bool ACC>
+__global__ __launch_bounds__(kBlock) void dact_scalar(const float* x, const float* dy, float* dx, int64_t n, F f) {
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * kBlock;
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x; i < n; i += stride) {
+        float o = dy[i] * f(x[i]);
+        if constexpr (ACC) o = dx[i] + o;
+        dx[i] = o;
+    }
+}
+
+unsigned stride_grid(int64_t n) {
+    const int64_t b = (n + kBlock - 1) / kBlock;
+    return static_cast<unsigned>(b < 1 ? 1 : (b > 65536 ? 65536 : b));
+}
+
+template <class F, bool ACC>
+int run_dact(mimir_ctx* ctx, const float* x, const float* dy, float* dx, int64_t n, F f, const char* name) {
+    int64_t done = 0;
+    if (aligned16(x) && aligned16(dy) && aligned16(dx)) {
+        const int64_t n4 = n / 4;
+        if (n4 > 0) {
+            unsigned blocks;
+            if (!grid_for(n4, kBlock, &blocks))
+                return fail(ctx, MIMIR_EINVAL, "%s: n=%lld exceeds the grid limit", name, (long long)n);
+            dact_vec<F, ACC><<<blocks, kBlock, 0, ctx->stream>>>(x, dy, dx, n4, f);
+            if (int st = launched(ctx, name)) return st;
+        }
+        done = n4 * 4;
+    }
+    if (n > done) {
+        dact_scalar<F, ACC><<<stride_grid(n - done), kBlock, 0, ctx->stream>>>(x + done, dy + done, dx + done,
+                                                                             n - done, f);
+        return launched(ctx, name);
+    }
+    return MIMIR_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Multiply (Model.cpp:7647-7665) and Add (7541-7601)
+// ---------------------------------------------------------------------------
+
+// g0 = dy*b and g1 = dy*a are formed before either is accumulated, as in
+// the reference, so da / db may alias dy (element for element).
+template <bool ACC_A, bool ACC_B>
+__global__ __launch_bounds__(kBlock) void mul_bwd_vec(const float* a, const float* b, const float* dy, float* da,
+                                                      float* db, int64_t n4) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
+    if (i >= n4) return;
+    const f4 g = ld4<true>(dy + 4 * i);
+    f4 g0 = g * ld4<true>(b + 4 * i);
+    f4 g1 = g * ld4<true>(a + 4 * i);
+    if (da) {
+        if constexpr (ACC_A) g0 = ld4<true>(da + 4 * i) + g0;
+    }
+    if (db) {
+        if constexpr (ACC_B) g1 = ld4<true>(db + 4 * i) + g1;
+    }
+    if (da) st4<true>(da + 4 * i, g0);
+    if (db) st4<true>(db + 4 * i, g1);
+}
+
+// da == db (Multiply of a tensor with itself): the second accumulation adds
+// onto the first, ((da) + g0) + g1, as two accumulate_grad calls on one name.
+template <bool ACC_A>
+__global__ __launch_bounds__(kBlock) void mul_bwd_same(const float* a, const float* b, const float* dy, float* d,
+                                                       int64_t n) {
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * kBlock;
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x; i < n; i += stride) {
+        const float g = dy[i];
+        const float g0 = g * b[i];
+        const float g1 = g * a[i];
+        float o = ACC_A ? d[i] + g0 : g0;
+        d[i] = o + g1;
+    }
+}
+
+template <bool ACC_A, bool ACC_B>
+__global__ __launch_bounds__(kBlock) void mul_bwd_scalar(const float* a, const float* b, const float* dy, float* da,
+                                                         float* db, int64_t n) {
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * kBlock;
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x; i < n; i += stride) {
+        const float g = dy[i];
+        float g0 = g * b[i];
+        float g1 = g * a[i];
+        if (da && ACC_A) g0 = da[i] + g0;
+        if (db && ACC_B) g1 = db[i] + g1;
+        if (da) da[i] = g0;
+        if (db) db[i] = g1;
+    }
+}
+
+// dst = src or dst += src over n floats (accumulate_grad, Model.cpp:7329-7341).
+template <bool ACC>
+__global__ __launch_bounds__(kBlock) void acc_vec(const float* src, float* dst, int64_t n4) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
+    if (i >= n4) return;
+    f4 o = ld4<true>(src + 4 * i);
+    if constexpr (ACC) o = ld4<true>(dst + 4 * i) + o;
+    st4<true>(dst + 4 * i, o);
+}
+
+template <bool ACC>
+__global__ __launch_bounds__(kBlock) void acc_scalar(const float* src, float* dst, int64_t n) {
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * kBlock;
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x; i < n; i += stride) {
+        float o = src[i];
+        if constexpr (ACC) o = dst[i] + o;
+        dst[i] = o;
+    }
+}
+
+// Equal sizes and no aliasing: da (+)= dy and db (+)= dy in one pass.
+template <bool ACC_A, bool ACC_B>
+__global__ __launch_bounds__(kBlock) void add_bwd_vec(const float* dy, float* da, float* db, int64_t n4) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
+    if (i >= n4) return;
+    const f4 g = ld4<true>(dy + 4 * i);
+    if (da) st4<true>(da + 4 * i, ACC_A ? ld4<true>(da + 4 * i) + g : g);
+    if (db) st4<true>(db + 4 * i, ACC_B ? ld4<true>(db + 4 * i) + g : g);
+}
+
+int accumulate(mimir_ctx* ctx, const float* src, float* dst, int64_t n, bool acc, const char* name) {
+    int64_t done = 0;
+    if (aligned16(src) && aligned16(dst)) {
+        const int64_t n4 = n / 4;
+        if (n4 > 0) {
+            unsigned blocks;
+            if (!grid_for(n4, kBlock, &blocks))
+                return fail(ctx, MIMIR_EINVAL, "%s: n=%lld exceeds the grid limit", name, (long long)n);
+            if (acc) acc_vec<true><<<blocks, kBlock, 0, ctx->stream>>>(src, dst, n4);
+            else acc_vec<false><<<blocks, kBlock, 0, ctx->stream>>>(src, dst, n4);
+            if (int st = launched(ctx, name)) return st;
+        }
+        done = n4 * 4;
+    }
+    if (n > done) {
+        if (acc) acc_scalar<true><<<stride_grid(n - done), kBlock, 0, ctx->stream>>>(src + done, dst + done, n - done);
+        else acc_scalar<false><<<stride_grid(n - done), kBlock, 0, ctx->stream>>>(src + done, dst + done, n - done);
+        return launched(ctx, name);
+    }
+    return MIMIR_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Deterministic column sums: partial sums per slot, then slots in order
+// ---------------------------------------------------------------------------
+
+constexpr int kSumLanes = 16;  // waves per sum_slots workgroup, one slot lane each
+
+// out[c] (+)= sum over slots k of part[k*stride + c], c < width: wave l of
+// the workgroup adds slots l, l+16, ... for 64 consecutive columns; the 16
+// lane sums are then added in lane order.  Columns below `split` go to out0,
+// the rest to out1 (dgamma | dbeta).
+__global__ __launch_bounds__(kSumLanes * kWave) void sum_slots(const float* part, int64_t nslots, int64_t stride,
+                                                               int64_t width, float* out0, float* out1, int64_t split,
+                                                               int acc) {
+    __shared__ float lds[kSumLanes][kWave];
+    const int lane = threadIdx.x / kWave;
+    const int col = threadIdx.x % kWave;
+    const int64_t c = static_cast<int64_t>(blockIdx.x) * kWave + col;
+    float s = 0.0f;
+    if (c < width)
+        for (int64_t k = lane; k < nslots; k += kSumLanes) s += part[k * stride + c];
+    lds[lane][col] = s;
+    __syncthreads();
+    if (lane == 0 && c < width) {
+        float t = lds[0][col];
+#pragma unroll
+        for (int l = 1; l < kSumLanes; ++l) t += lds[l][col];
+        float* o = c < split ? out0 + c : out1 + (c - split);
+        *o = acc ? *o + t : t;
+    }
+}
+
+int launch_sum_slots(mimir_ctx* ctx, const float* part, int64_t nslots, int64_t stride, int64_t width, float* out0,
+                     float* out1, int64_t split, bool acc) {
+    unsigned blocks;
+    if (!grid_for(width, kWave, &blocks))
+        return fail(ctx, MIMIR_EINVAL, "sum_slots: width %lld exceeds the grid limit", (long long)width);
+    sum_slots<<<blocks, kSumLanes * kWave, 0, ctx->stream>>>(part, nslots, stride, width, out0, out1, split,
+                                                             acc ? 1 : 0);
+    return launched(ctx, "sum_slots");
+}
+
+// Column sums of dy viewed as [rows x cols] over row chunks of `chunk` rows:
+// part[k*cols + c] = sum of dy[r*cols + c], r in chunk k, in row order.
+__global__ __launch_bounds__(kBlock) void colsum_part(const float* dy, int64_t rows, int64_t cols, int64_t chunk,
+                                                     float* part) {
+    const int64_t c = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
+    if (c >= cols) return;
+    const int64_t r0 = static_cast<int64_t>(blockIdx.y) * chunk;
+    const int64_t r1 = r0 + chunk < rows ? r0 + chunk : rows;
+    float s = 0.0f;
+    for (int64_t r = r0; r < r1; ++r) s += dy[r * cols + c];
+    part[static_cast<int64_t>(blockIdx.y) * cols + c] = s;
+}
+
+// Sum of n floats in contiguous chunks: part[k] = sum of chunk k.
+__global__ __launch_bounds__(kBlock) void total_part(const float* dy, int64_t n, int64_t chunk, float* part) {
+    __shared__ float lds[kBlock / kWave];
+    const int64_t i0 = static_cast<int64_t>(blockIdx.x) * chunk;
+    const int64_t i1 = i0 + chunk < n ? i0 + chunk : n;
+    float s = 0.0f;
+    for (int64_t i = i0 + threadIdx.x; i < i1; i += kBlock) s += dy[i];
+    s = block_sum<kBlock / kWave>(s, lds);
+    if (threadIdx.x == 0) part[blockIdx.x] = s;
+}
+
+// Gradient of the broadcast operand of add_forward: the sum of dy over the
+// big operand's tiles (small_n > 1) or over all of it (small_n == 1).
+int add_small_grad(mimir_ctx* ctx, const float* dy, int64_t n_big, int64_t n_small, float* out, bool acc) {
+    if (n_small == 1) {
+        const int64_t chunk = 16384;
+        const int64_t nchunks = (n_big + chunk - 1) / chunk;
+        void* s = nullptr;
+        if (int st = ensure_scratch(ctx, sizeof(float) * static_cast<size_t>(nchunks), &s)) return st;
+        unsigned blocks;
+        if (!grid_for(nchunks, 1, &blocks)) return fail(ctx, MIMIR_EINVAL, "Add backward: operand too large");
+        total_part<<<blocks, kBlock, 0, ctx->stream>>>(dy, n_big, chunk, static_cast<float*>(s));
+        if (int st = launched(ctx, "total_part")) return st;
+        return launch_sum_slots(ctx, static_cast<float*>(s), nchunks, 1, 1, out, out, 1, acc);
+    }
+    const int64_t rows = n_big / n_small;
+    // About 1024 workgroups over (columns x row chunks), chunks of at least 8 rows.
+    const int64_t cblocks = (n_small + kBlock - 1) / kBlock;
+    int64_t nchunks = (1024 + cblocks - 1) / cblocks;
+    if (nchunks > rows / 8) nchunks = rows / 8;
+    if (nchunks < 1) nchunks = 1;
+    if (nchunks > 65535) nchunks = 65535;
+    const int64_t chunk = (rows + nchunks - 1) / nchunks;
+    nchunks = (rows + chunk - 1) / chunk;
+    void* s = nullptr;
+    if (int st = ensure_scratch(ctx, sizeof(float) * static_cast<size_t>(nchunks * n_small), &s)) return st;
+    if (cblocks > 0x7fffffffLL) return fail(ctx, MIMIR_EINVAL, "Add backward: operand too large");
+    colsum_part<<<dim3(static_cast<unsigned>(cblocks), static_cast<unsigned>(nchunks)), kBlock, 0, ctx->stream>>>(
+        dy, rows, n_small, chunk, static_cast<float*>(s));
+    if (int st = launched(ctx, "colsum_part")) return st;
+    return launch_sum_slots(ctx, static_cast<float*>(s), nchunks, n_small, n_small, out, out, n_small, acc);
+}
+
+// ---------------------------------------------------------------------------
+// LayerNorm backward (Model.cpp:7719-7821)
+// ---------------------------------------------------------------------------
+
+struct LnBwdArgs {
+    const float* x;
+    const float* dy;
+    const float* g;  // gamma (null: not affine, gamma = 1)
+    float* dx;
+    float* part;     // [slots][2*cols] dgamma | dbeta partial sums (null: not wanted)
+    float* stats;    // generic path: [rows][2] mean, inv_std
+    int64_t rows;
+    int64_t cols;
+    float eps;
+    int acc;         // dx += value instead of dx = value
+};
+
+// Two sums over one row at once (one LDS round).
+template <int NW>
+__device__ __forceinline__ void row_sum2(float& a, float& b, float* la, float* lb, int sub) {
+    a = wave_sum(a);
+    b = wave_sum(b);
+    if constexpr (NW > 1) {
+        if ((threadIdx.x & (kWave - 1)) == 0) {
+            la[threadIdx.x / kWave] = a;
+            lb[threadIdx.x / kWave] = b;
+        }
+        __syncthreads();
+        float sa = la[sub * NW], sb = lb[sub * NW];
+#pragma unroll
+        for (int i = 1; i < NW; ++i) {
+            sa += la[sub * NW + i];
+            sb += lb[sub * NW + i];
+        }
+        a = sa;
+        b = sb;
+    }
+}
+
+__device__ __forceinline__ float hsum(f4 v) { return (v.x + v.y) + (v.z + v.w); }
+
+// One workgroup slot per (block, sub-row); the grid is persistent (fewer
+// blocks than row groups), so each slot visits rows sub + RPB*(block +
+// k*grid) and keeps dgamma / dbeta for its TPR*VPT*4 columns in registers.
+// Every reduction is a fresh LDS array or is separated from its previous
+// use by another barrier, so no leading barriers are needed.
+template <int TPR, int VPT, int BS>
+__global__ __launch_bounds__(BS) void ln_bwd_vec(LnBwdArgs a) {
+    constexpr int RPB = BS / TPR;
+    constexpr int NW = TPR / kWave;
+    __shared__ float lds[4][BS / kWave];
+    const int t = threadIdx.x % TPR;
+    const int sub = threadIdx.x / TPR;
+    const int64_t c4n = a.cols >> 2;
+    const float n = static_cast<float>(a.cols);
+    const float invF = 1.0f / n;  // Model.cpp:7799
+    f4 gm[VPT], dg[VPT], db[VPT];
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) {
+        const int64_t c4 = static_cast<int64_t>(j) * TPR + t;
+        gm[j] = (a.g && c4 < c4n) ? *reinterpret_cast<const f4*>(a.g + 4 * c4) : f4(1.0f);
+        dg[j] = f4(0.0f);
+        db[j] = f4(0.0f);
+    }
+    const int64_t step = static_cast<int64_t>(gridDim.x) * RPB;
+    for (int64_t base = static_cast<int64_t>(blockIdx.x) * RPB; base < a.rows; base += step) {
+        const int64_t row = base + sub;
+        const int64_t lim = row < a.rows ? c4n : 0;  // past-end rows join the barriers only
+        const int64_t off = row * a.cols;
+        f4 xv[VPT], gv[VPT];
+#pragma unroll
+        for (int j = 0; j < VPT; ++j) {
+            const int64_t c4 = static_cast<int64_t>(j) * TPR + t;
+            const bool ok = c4 < lim;
+            xv[j] = ok ? ld4<true>(a.x + off + 4 * c4) : f4(0.0f);
+            gv[j] = ok ? ld4<true>(a.dy + off + 4 * c4) : f4(0.0f);
+        }
+        float s = 0.0f;
+#pragma unroll
+        for (int j = 0; j < VPT; ++j) s += hsum(xv[j]);
+        const float mean = row_sum<NW, false>(s, lds[0], sub) / n;  // :7765-7768
+        float q = 0.0f;
+#pragma unroll
+        for (int j = 0; j < VPT; ++j) {
+            const int64_t c4 = static_cast<int64_t>(j) * TPR + t;
+            if (c4 < lim) {
+                const f4 d = xv[j] - mean;
+                q += (d.x * d.x + d.y * d.y) + (d.z * d.z + d.w * d.w);
+            }
+        }
+        const float var = row_sum<NW, false>(q, lds[1], sub) / n;  // :7770-7776
+        const float inv_std = 1.0f / sqrtf(var + a.eps);             // :7777
+        float s1 = 0.0f, s2 = 0.0f;
+        f4 xh[VPT], dxh[VPT];
+#pragma unroll
+        for (int j = 0; j < VPT; ++j) {  // :7783-7797
+            const int64_t c4 = static_cast<int64_t>(j) * TPR + t;
+            if (c4 < lim) {
+                xh[j] = (xv[j] - mean) * inv_std;
+                dxh[j] = gv[j] * gm[j];
+                dg[j] += gv[j] * xh[j];
+                db[j] += gv[j];
+                s1 += hsum(dxh[j]);
+                s2 += hsum(dxh[j] * xh[j]);
+            } else {
+                xh[j] = f4(0.0f);
+                dxh[j] = f4(0.0f);
+            }
+        }
+        row_sum2<NW>(s1, s2, lds[2], lds[3], sub);
+        const float k = inv_std * invF;
+#pragma unroll
+        for (int j = 0; j < VPT; ++j) {  // :7800-7805
+            const int64_t c4 = static_cast<int64_t>(j) * TPR + t;
+            if (c4 < lim) {
+                f4 o = k * ((n * dxh[j] - s1) - xh[j] * s2);
+                if (a.acc) o = ld4<true>(a.dx + off + 4 * c4) + o;
+                st4<true>(a.dx + off + 4 * c4, o);
+            }
+        }
+    }
+    if (a.part) {
+        float* p = a.part + (static_cast<int64_t>(blockIdx.x) * RPB + sub) * 2 * a.cols;
+#pragma unroll
+        for (int j = 0; j < VPT; ++j) {
+            const int64_t c4 = static_cast<int64_t>(j) * TPR + t;
+            if (c4 < c4n) {
+                *reinterpret_cast<f4*>(p + 4 * c4) = dg[j];
+                *reinterpret_cast<f4*>(p + a.cols + 4 * c4) = db[j];
+            }
+        }
+    }
+}
+
+// Any width / alignment: one workgroup per row, strided passes (the re-reads
+// of a row hit L2).  Three kernels, so that dx may overwrite dy: the row
+// statistics (mean, inv_std) first, then the parameter gradients (which read
+// dy), then dx.
+__global__ __launch_bounds__(kBlock) void ln_stats_generic(LnBwdArgs a) {
+    constexpr int NW = kBlock / kWave;
+    __shared__ float lds[2][NW];
+    const int64_t row = blockIdx.x;
+    const float* x = a.x + row * a.cols;
+    const float n = static_cast<float>(a.cols);
+    float s = 0.0f;
+    for (int64_t c = threadIdx.x; c < a.cols; c += kBlock) s += x[c];
+    const float mean = block_sum<NW>(s, lds[0]) / n;
+    float q = 0.0f;
+    for (int64_t c = threadIdx.x; c < a.cols; c += kBlock) {
+        const float d = x[c] - mean;
+        q += d * d;
+    }
+    const float var = block_sum<NW>(q, lds[1]) / n;
+    if (threadIdx.x == 0) {
+        a.stats[2 * row] = mean;
+        a.stats[2 * row + 1] = 1.0f / sqrtf(var + a.eps);
+    }
+}
+
+__global__ __launch_bounds__(kBlock) void ln_bwd_generic(LnBwdArgs a) {
+    constexpr int NW = kBlock / kWave;
+    __shared__ float lds[2][NW];
+    const int64_t row = blockIdx.x;
+    const float* x = a.x + row * a.cols;
+    const float* dy = a.dy + row * a.cols;
+    float* dx = a.dx + row * a.cols;
+    const float n = static_cast<float>(a.cols);
+    const float mean = a.stats[2 * row];
+    const float inv_std = a.stats[2 * row + 1];
+    float s1 = 0.0f, s2 = 0.0f;
+    for (int64_t c = threadIdx.x; c < a.cols; c += kBlock) {
+        const float xh = (x[c] - mean) * inv_std;
+        const float dxh = dy[c] * (a.g ? a.g[c] : 1.0f);
+        s1 += dxh;
+        s2 += dxh * xh;
+    }
+    row_sum2<NW>(s1, s2, lds[0], lds[1], 0);
+    const float k = inv_std * (1.0f / n);
+    // Each thread reads dy[c] before writing dx[c], so dx may alias dy.
+    for (int64_t c = threadIdx.x; c < a.cols; c += kBlock) {
+        const float xh = (x[c] - mean) * inv_std;
+        const float dxh = dy[c] * (a.g ? a.g[c] : 1.0f);
+        float o = k * ((n * dxh - s1) - xh * s2);
+        if (a.acc) o = dx[c] + o;
+        dx[c] = o;
+    }
+}
+
+// Parameter gradients for the generic path: part[k][c] = sum over the rows r
+// of chunk k of dy*xhat, part[k][cols + c] = sum of dy.
+__global__ __launch_bounds__(kBlock) void ln_bwd_params_part(LnBwdArgs a, int64_t chunk) {
+    const int64_t c = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
+    if (c >= a.cols) return;
+    const int64_t r0 = static_cast<int64_t>(blockIdx.y) * chunk;
+    const int64_t r1 = r0 + chunk < a.rows ? r0 + chunk : a.rows;
+    float sg = 0.0f, sb = 0.0f;
+    for (int64_t r = r0; r < r1; ++r) {
+        const float g = a.dy[r * a.cols + c];
+        const float xh = (a.x[r * a.cols + c] - a.stats[2 * r]) * a.stats[2 * r + 1];
+        sg += g * xh;
+        sb += g;
+    }
+    float* p = a.part + static_cast<int64_t>(blockIdx.y) * 2 * a.cols;
+    p[c] = sg;
+    p[a.cols + c] = sb;
+}
+
+template <int TPR, int VPT, int BS>
+int launch_ln_bwd_vec(mimir_ctx* ctx, LnBwdArgs a, float* dgamma, float* dbeta) {
+    constexpr int RPB = BS / TPR;
+    const int64_t groups = (a.rows + RPB - 1) / RPB;
+    int64_t grid = ctx->tune.lnbwd_grid > 0 ? ctx->tune.lnbwd_grid : 512;
+    if (grid > groups) grid = groups;
+    const int64_t nslots = grid * RPB;
+    if (dgamma) {
+        void* s = nullptr;
+        if (int st = ensure_scratch(ctx, sizeof(float) * static_cast<size_t>(nslots * 2 * a.cols), &s)) return st;
+        a.part = static_cast<float*>(s);
+    }
+    ln_bwd_vec<TPR, VPT, BS><<<static_cast<unsigned>(grid), BS, 0, ctx->stream>>>(a);
+    if (int st = launched(ctx, "ln_bwd_vec")) return st;
+    if (!dgamma) return MIMIR_OK;
+    // dbeta null: sum only the dgamma half.
+    return launch_sum_slots(ctx, a.part, nslots, 2 * a.cols, dbeta ? 2 * a.cols : a.cols, dgamma, dbeta, a.cols,
+                            true);
+}
+
+int ln_bwd_generic_run(mimir_ctx* ctx, LnBwdArgs a, float* dgamma, float* dbeta) {
+    if (a.rows > 0x7fffffffLL)
+        return fail(ctx, MIMIR_EINVAL, "LayerNorm backward: %lld rows exceed the grid limit", (long long)a.rows);
+    const int64_t cblocks = (a.cols + kBlock - 1) / kBlock;
+    if (cblocks > 0x7fffffffLL) return fail(ctx, MIMIR_EINVAL, "LayerNorm backward: row too wide");
+    int64_t nchunks = 0, chunk = a.rows;
+    if (dgamma) {
+        nchunks = (1024 + cblocks - 1) / cblocks;
+        if (nchunks > a.rows) nchunks = a.rows;
+        if (nchunks > 65535) nchunks = 65535;
+        chunk = (a.rows + nchunks - 1) / nchunks;
+        nchunks = (a.rows + chunk - 1) / chunk;
+    }
+    void* s = nullptr;
+    const size_t bytes = sizeof(float) * static_cast<size_t>(2 * a.rows + nchunks * 2 * a.cols);
+    if (int st = ensure_scratch(ctx, bytes, &s)) return st;
+    a.stats = static_cast<float*>(s);
+    a.part = a.stats + 2 * a.rows;
+    const unsigned rows = static_cast<unsigned>(a.rows);
+    ln_stats_generic<<<rows, kBlock, 0, ctx->stream>>>(a);
+    if (int st = launched(ctx, "ln_stats_generic")) return st;
+    if (dgamma) {
+        ln_bwd_params_part<<<dim3(static_cast<unsigned>(cblocks), static_cast<unsigned>(nchunks)), kBlock, 0,
+                             ctx->stream>>>(a, chunk);
+        if (int st = launched(ctx, "ln_bwd_params_part")) return st;
+    }
+    ln_bwd_generic<<<rows, kBlock, 0, ctx->stream>>>(a);
+    if (int st = launched(ctx, "ln_bwd_generic")) return st;
+    if (!dgamma) return MIMIR_OK;
+    return launch_sum_slots(ctx, a.part, nchunks, 2 * a.cols, dbeta ? 2 * a.cols : a.cols, dgamma, dbeta, a.cols,
+                            true);
+}
+
+// ---------------------------------------------------------------------------
+// Embedding backward (Model.cpp:7429-7461)
+// ---------------------------------------------------------------------------
+
+// Sort keys: the id, or `vocab` (sorted last, skipped) for the padding id and
+// ids outside [0, vocab) (Model.cpp:7454-7455).
+template <int MODE>
+__global__ __launch_bounds__(kBlock) void embed_bwd_keys(const void* ids, int64_t n, int32_t vocab, int32_t pad,
+                                                         uint32_t* keys, uint32_t* toks) {
+    const int64_t t = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
+    if (t >= n) return;
+    const int32_t id = load_id<MODE>(ids, t);
+    const bool use = !(pad >= 0 && id == pad) && id >= 0 && id < vocab;
+    keys[t] = use ? static_cast<uint32_t>(id) : static_cast<uint32_t>(vocab);
+    toks[t] = static_cast<uint32_t>(t);
+}
+
+// One workgroup per sorted position; the first position of each id's run
+// adds the run's dy rows (token order, the sort is stable) onto the id's
+// gradient row, four tokens' loads in flight at a time.
+template <int TPT>
+__global__ __launch_bounds__(TPT) void embed_bwd_rows_vec(const uint32_t* keys, const uint32_t* toks, int64_t n,
+                                                          uint32_t vocab, const float* dy, float* grad,
+                                                          int64_t dim4) {
+    const int64_t i = blockIdx.x;
+    const uint32_t id = keys[i];
+    if (id >= vocab || (i > 0 && keys[i - 1] == id)) return;
+    int64_t end = i + 1;
+    while (end < n && keys[end] == id) ++end;
+    f4* g = reinterpret_cast<f4*>(grad) + static_cast<int64_t>(id) * dim4;
+    const f4* src = reinterpret_cast<const f4*>(dy);
+    for (int64_t c = threadIdx.x; c < dim4; c += TPT) {
+        f4 acc = g[c];
+        int64_t j = i;
+        for (; j + 4 <= end; j += 4) {
+            const f4 v0 = src[static_cast<int64_t>(toks[j]) * dim4 + c];
+            const f4 v1 = src[static_cast<int64_t>(toks[j + 1]) * dim4 + c];
+            const f4 v2 = src[static_cast<int64_t>(toks[j + 2]) * dim4 + c];
+            const f4 v3 = src[static_cast<int64_t>(toks[j + 3]) * dim4 + c];
+            acc += v0;
+            acc += v1;
+            acc += v2;
+            acc += v3;
+        }
+        for (; j < end; ++j) acc += src[static_cast<int64_t>(toks[j]) * dim4 + c];
+        g[c] = acc;
+    }
+}
+
+__global__ __launch_bounds__(kBlock) void embed_bwd_rows_scalar(const uint32_t* keys, const uint32_t* toks,
+                                                                int64_t n, uint32_t vocab, const float* dy,
+                                                                float* grad, int64_t dim) {
+    const int64_t i = blockIdx.x;
+    const uint32_t id = keys[i];
+    if (id >= vocab || (i > 0 && keys[i - 1] == id)) return;
+    int64_t end = i + 1;
+    while (end < n && keys[end] == id) ++end;
+    float* g = grad + static_cast<int64_t>(id) * dim;
+    for (int64_t c = threadIdx.x; c < dim; c += kBlock) {
+        float acc = g[c];
+        for (int64_t j = i; j < end; ++j) acc += dy[static_cast<int64_t>(toks[j]) * dim + c];
+        g[c] = acc;
+    }
+}
+
+size_t align256(size_t b) { return (b + 255) & ~size_t(255); }
+
+template <int MODE>
+int embed_bwd(mimir_ctx* ctx, const void* ids, int64_t n_ids, const float* dy, float* grad, int64_t table_len,
+              int32_t vocab, int32_t dim, int32_t pad) {
+    MIMIR_REQUIRE(ctx, n_ids >= 0, "Embedding backward: n_ids < 0");
+    vocab = vocab < 1 ? 1 : vocab;  // Model.cpp:7434-7435
+    dim = dim < 1 ? 1 : dim;
+    MIMIR_REQUIRE(ctx, table_len >= static_cast<int64_t>(vocab) * dim,  // :7443-7447
+                  "Embedding backward: invalid weight size (%lld < %d x %d)", (long long)table_len, vocab, dim);
+    MIMIR_REQUIRE(ctx, vocab < 0x7fffffff, "Embedding backward: vocab too large");
+    if (n_ids == 0) return MIMIR_OK;
+    MIMIR_REQUIRE(ctx, ids && dy && grad, "Embedding backward: null tensor");
+    MIMIR_REQUIRE(ctx, n_ids <= 0x7fffffffLL, "Embedding backward: %lld ids exceed the grid limit",
+                  (long long)n_ids);
+    MIMIR_ENTER(ctx);
+    const unsigned n = static_cast<unsigned>(n_ids);
+    unsigned end_bit = 1;
+    while (end_bit < 32 && (static_cast<uint32_t>(vocab) >> end_bit) != 0) ++end_bit;
+    size_t sort_bytes = 0;
+    hipError_t e = rocprim::radix_sort_pairs(nullptr, sort_bytes, static_cast<const uint32_t*>(nullptr),
+                                             static_cast<uint32_t*>(nullptr), static_cast<const uint32_t*>(nullptr),
+                                             static_cast<uint32_t*>(nullptr), n, 0u, end_bit, ctx->stream);
+    if (e != hipSuccess) return hip_fail(ctx, e, "radix_sort_pairs (size)");
+    const size_t vec = align256(sizeof(uint32_t) * n);
+    void* s = nullptr;
+    if (int st = ensure_scratch(ctx, 4 * vec + align256(sort_bytes), &s)) return st;
+    char* base = static_cast<char*>(s);
+    uint32_t* keys = reinterpret_cast<uint32_t*>(base);
+    uint32_t* toks = reinterpret_cast<uint32_t*>(base + vec);
+    uint32_t* skeys = reinterpret_cast<uint32_t*>(base + 2 * vec);
+    uint32_t* stoks = reinterpret_cast<uint32_t*>(base + 3 * vec);
+    void* temp = base + 4 * vec;
+    embed_bwd_keys<MODE><<<(n + kBlock - 1) / kBlock, kBlock, 0, ctx->stream>>>(ids, n_ids, vocab, pad, keys, toks);
+    if (int st = launched(ctx, "embed_bwd_keys")) return st;
+    e = rocprim::radix_sort_pairs(temp, sort_bytes, static_cast<const uint32_t*>(keys), skeys,
+                                  static_cast<const uint32_t*>(toks), stoks, n, 0u, end_bit, ctx->stream);
+    if (e != hipSuccess) return hip_fail(ctx, e, "radix_sort_pairs");
+    if ((dim % 4) == 0 && aligned16(dy) && aligned16(grad)) {
+        embed_bwd_rows_vec<256><<<n, 256, 0, ctx->stream>>>(skeys, stoks, n_ids, static_cast<uint32_t>(vocab), dy,
+                                                            grad, dim / 4);
+        return launched(ctx, "embed_bwd_rows_vec");
+    }
+    embed_bwd_rows_scalar<<<n, kBlock, 0, ctx->stream>>>(skeys, stoks, n_ids, static_cast<uint32_t>(vocab), dy,
+                                                         grad, dim);
+    return launched(ctx, "embed_bwd_rows_scalar");
+}
+
+}  // namespace
+
+extern "C" {
+
+int mimir_layernorm_bwd(mimir_ctx* ctx, const float* x, const float* dy, const float* gamma, float* dx,
+                        float* dgamma, float* dbeta, int64_t groups, int64_t n, float eps, int accumulate) {
+    if (!ctx) return MIMIR_EINVAL;
+    MIMIR_REQUIRE(ctx, n > 0 && groups >= 0, "LayerNorm backward: invalid shape (groups=%lld, n=%lld)",
+                  (long long)groups, (long long)n);
+    MIMIR_REQUIRE(ctx, !(dgamma && !gamma) && !(dbeta && !dgamma),
+                  "LayerNorm backward: dgamma needs gamma (affine), dbeta needs dgamma");
+    if (groups == 0) return MIMIR_OK;
+    MIMIR_REQUIRE(ctx, x && dy && dx, "LayerNorm backward: null tensor");
+    MIMIR_ENTER(ctx);
+    LnBwdArgs a{x, dy, gamma, dx, nullptr, nullptr, groups, n, eps, accumulate ? 1 : 0};
+    const int64_t c4 = n / 4;
+    const bool vec = (n % 4) == 0 && aligned16(x) && aligned16(dy) && aligned16(dx) && (!gamma || aligned16(gamma));
+    if (vec) {
+        const RowShape over = ctx->tune.lnbwd;
+        const RowShape s = shape_fits(over, c4) ? over : default_norm_shape(c4);
+#define MIMIR_LNBWD_CASE(T, V, B) \
+        if (s.tpr == T && s.vpt == V && s.bs == B) return launch_ln_bwd_vec<T, V, B>(ctx, a, dgamma, dbeta);
+        MIMIR_ROW_SHAPES(MIMIR_LNBWD_CASE)
+#undef MIMIR_LNBWD_CASE
+    }
+    return ln_bwd_generic_run(ctx, a, dgamma, dbeta);
+}
+
+int mimir_gelu_bwd(mimir_ctx* ctx, const float* x, const float* dy, float* dx, int64_t n, int accumulate) {
+    if (!ctx) return MIMIR_EINVAL;
+    MIMIR_REQUIRE(ctx, n >= 0, "GELU backward: n < 0");
+    if (n == 0) return MIMIR_OK;
+    MIMIR_REQUIRE(ctx, x && dy && dx, "GELU backward: null tensor");
+    MIMIR_ENTER(ctx);
+    return accumulate ? run_dact<DGelu, true>(ctx, x, dy, dx, n, DGelu{}, "gelu_bwd")
+                      : run_dact<DGelu, false>(ctx, x, dy, dx, n, DGelu{}, "gelu_bwd");
+}
+
+int mimir_silu_bwd(mimir_ctx* ctx, const float* x, const float* dy, float* dx, int64_t n, int accumulate) {
+    if (!ctx) return MIMIR_EINVAL;
+    MIMIR_REQUIRE(ctx, n >= 0, "SiLU backward: n < 0");
+    if (n == 0) return MIMIR_OK;
+    MIMIR_REQUIRE(ctx, x && dy && dx, "SiLU backward: null tensor");
+    MIMIR_ENTER(ctx);
+    return accumulate ? run_dact<DSilu, true>(ctx, x, dy, dx, n, DSilu{}, "silu_bwd")
+                      : run_dact<DSilu, false>(ctx, x, dy, dx, n, DSilu{}, "silu_bwd");
+}
+
+int mimir_mul_bwd(mimir_ctx* ctx, const float* a, const float* b, const float* dy, float* da, float* db, int64_t n,
+                  int acc_a, int acc_b) {
+    if (!ctx) return MIMIR_EINVAL;
+    MIMIR_REQUIRE(ctx, n >= 0, "Multiply backward: n < 0");
+    if (n == 0 || (!da && !db)) return MIMIR_OK;
+    MIMIR_REQUIRE(ctx, a && b && dy, "Multiply backward: null tensor");
+    MIMIR_ENTER(ctx);
+    const bool A = acc_a != 0, B = acc_b != 0;
+    if (da && da == db) {
+        if (A) mul_bwd_same<true><<<stride_grid(n), kBlock, 0, ctx->stream>>>(a, b, dy, da, n);
+        else mul_bwd_same<false><<<stride_grid(n), kBlock, 0, ctx->stream>>>(a, b, dy, da, n);
+        return launched(ctx, "mul_bwd_same");
+    }
+    int64_t done = 0;
+    if (aligned16(a) && aligned16(b) && aligned16(dy) && (!da || aligned16(da)) && (!db || aligned16(db))) {
+        const int64_t n4 = n / 4;
+        if (n4 > 0) {
+            unsigned blocks;
+            if (!grid_for(n4, kBlock, &blocks))
+                return fail(ctx, MIMIR_EINVAL, "Multiply backward: n=%lld exceeds the grid limit", (long long)n);
+            if (A && B) mul_bwd_vec<true, true><<<blocks, kBlock, 0, ctx->stream>>>(a, b, dy, da, db, n4);
+            else if (A) mul_bwd_vec<true, false><<<blocks, kBlock, 0, ctx->stream>>>(a, b, dy, da, db, n4);
+            else if (B) mul_bwd_vec<false, true><<<blocks, kBlock, 0, ctx->stream>>>(a, b, dy, da, db, n4);
+            else mul_bwd_vec<false, false><<<blocks, kBlock, 0, ctx->stream>>>(a, b, dy, da, db, n4);
+            if (int st = launched(ctx, "mul_bwd_vec")) return st;
+        }
+        done = n4 * 4;
+    }
+    if (n > done) {
+        const unsigned g = stride_grid(n - done);
+        float* da2 = da ? da + done : nullptr;
+        float* db2 = db ? db + done : nullptr;
+        if (A && B) mul_bwd_scalar<true, true><<<g, kBlock, 0, ctx->stream>>>(a + done, b + done, dy + done, da2, db2, n - done);
+        else if (A) mul_bwd_scalar<true, false><<<g, kBlock, 0, ctx->stream>>>(a + done, b + done, dy + done, da2, db2, n - done);
+        else if (B) mul_bwd_scalar<false, true><<<g, kBlock, 0, ctx->stream>>>(a + done, b + done, dy + done, da2, db2, n - done);
+        else mul_bwd_scalar<false, false><<<g, kBlock, 0, ctx->stream>>>(a + done, b + done, dy + done, da2, db2, n - done);
+        return launched(ctx, "mul_bwd_scalar");
+    }
+    return MIMIR_OK;
+}
+
+int mimir_add_bwd(mimir_ctx* ctx, const float* dy, int64_t na, int64_t nb, float* da, float* db, int acc_a,
+                  int acc_b) {
+    if (!ctx) return MIMIR_EINVAL;
+    MIMIR_REQUIRE(ctx, na > 0 && nb > 0, "Add backward: inputs must be non-empty");
+    MIMIR_REQUIRE(ctx, dy, "Add backward: null tensor");
+    const bool A = acc_a != 0, B = acc_b != 0;
+    if (na == nb) {  // Model.cpp:7552-7555: both inputs receive dy, in that order
+        if (!da && !db) return MIMIR_OK;
+        MIMIR_ENTER(ctx);
+        const bool alias = da == dy || db == dy || (da && da == db);
+        if (!alias && aligned16(dy) && (!da || aligned16(da)) && (!db || aligned16(db)) && (na % 4) == 0) {
+            unsigned blocks;
+            if (!grid_for(na / 4, kBlock, &blocks))
+                return fail(ctx, MIMIR_EINVAL, "Add backward: n=%lld exceeds the grid limit", (long long)na);
+            if (A && B) add_bwd_vec<true, true><<<blocks, kBlock, 0, ctx->stream>>>(dy, da, db, na / 4);
+            else if (A) add_bwd_vec<true, false><<<blocks, kBlock, 0, ctx->stream>>>(dy, da, db, na / 4);
+            else if (B) add_bwd_vec<false, true><<<blocks, kBlock, 0, ctx->stream>>>(dy, da, db, na / 4);
+            else add_bwd_vec<false, false><<<blocks, kBlock, 0, ctx->stream>>>(dy, da, db, na / 4);
+            return launched(ctx, "add_bwd_vec");
+        }
+        // Aliased gradients: the second accumulation sees the first, as the
+        // reference's in-place adds into its gradient map do.
+        if (da)
+            if (int st = accumulate(ctx, dy, da, na, A, "add_bwd")) return st;
+        if (db)
+            if (int st = accumulate(ctx, dy, db, nb, B || db == da, "add_bwd")) return st;
+        return MIMIR_OK;
+    }
+    const bool a_big = na > nb;  // dy has the big operand's size
+    const int64_t big_n = a_big ? na : nb, small_n = a_big ? nb : na;
+    MIMIR_REQUIRE(ctx, small_n == 1 || big_n % small_n == 0,  // Model.cpp:7595-7599
+                  "Add backward: broadcast unsupported (big=%lld, small=%lld)", (long long)big_n, (long long)small_n);
+    float* d_big = a_big ? da : db;
+    float* d_small = a_big ? db : da;
+    MIMIR_ENTER(ctx);
+    if (d_big)  // :7577
+        if (int st = accumulate(ctx, dy, d_big, big_n, a_big ? A : B, "add_bwd")) return st;
+    if (d_small)  // :7580-7594, reading dy after the big operand's accumulation
+        return add_small_grad(ctx, dy, big_n, small_n, d_small, a_big ? B : A);
+    return MIMIR_OK;
+}
+
+int mimir_embedding_bwd(mimir_ctx* ctx, const int32_t* ids, int64_t n_ids, const float* dy, float* grad_table,
+                        int64_t table_len, int32_t vocab, int32_t dim, int32_t padding_idx) {
+    if (!ctx) return MIMIR_EINVAL;
+    return embed_bwd<kIdsI32>(ctx, ids, n_ids, dy, grad_table, table_len, vocab, dim, padding_idx);
+}
+
+int mimir_embedding_f32ids_bwd(mimir_ctx* ctx, const float* ids, int64_t n_ids, const float* dy, float* grad_table,
+                               int64_t table_len, int32_t vocab, int32_t dim, int32_t padding_idx) {
+    if (!ctx) return MIMIR_EINVAL;
+    return embed_bwd<kIdsF32>(ctx, ids, n_ids, dy, grad_table, table_len, vocab, dim, padding_idx);
+}
+
+}  // extern "C"
+
+namespace mimir {
+
+int embedding_bwd_launch(mimir_ctx* ctx, const void* ids, int mode, int64_t n_ids, const float* dy, float* grad,
+                         int64_t table_len, int32_t vocab, int32_t dim, int32_t pad) {
+    if (mode == kIdsF32) return embed_bwd<kIdsF32>(ctx, ids, n_ids, dy, grad, table_len, vocab, dim, pad);
+    if (mode == kIdsI32AsF32) return embed_bwd<kIdsI32AsF32>(ctx, ids, n_ids, dy, grad, table_len, vocab, dim, pad);
+    return embed_bwd<kIdsI32>(ctx, ids, n_ids, dy, grad, table_len, vocab, dim, pad);
+}
+
+}  // namespace mimir

@@ -98,6 +98,9 @@ int longrow_softmax(mimir_ctx* ctx, int mode, const float* x, float* y, int64_t 
 enum : int { kIdsI32 = 0, kIdsF32 = 1, kIdsI32AsF32 = 2 };
 int embedding_launch(mimir_ctx* ctx, const void* ids, int mode, int64_t n_ids, const float* table,
                      int64_t table_len, int32_t vocab, int32_t dim, int32_t pad, float* y);
+// Its backward, the scatter-add into the gradient table (backward.hip).
+int embedding_bwd_launch(mimir_ctx* ctx, const void* ids, int mode, int64_t n_ids, const float* dy, float* grad,
+                         int64_t table_len, int32_t vocab, int32_t dim, int32_t pad);
 
 }  // namespace mimir
 

@@ -45,7 +45,8 @@ struct RowShape {
     X(1024, 4, 1024)
 
 // Tuning override, read once per context from MIMIR_TUNE, e.g.
-//   MIMIR_TUNE="norm=1024x1x1024,layernorm=512x2x512,softmax=64x4x64,ew=1,gather=1024,rope=1"
+//   MIMIR_TUNE="norm=1024x1x1024,layernorm=512x2x512,softmax=64x4x64,ew=1,gather=1024,rope=1,
+//               lnbwd=512x2x512,lnbwd_grid=512"
 // Each entry selects among the compiled variants above; an entry that does
 // not fit a call (row too wide for it) is ignored for that call.  Unset, the
 // measured defaults apply.  Used for sweeps; results are identical.
@@ -56,6 +57,8 @@ struct Tuning {
     int ew_vpt = 0;
     int gather_tpt = 0;
     int rope_ppt = 0;
+    RowShape lnbwd{0, 0, 0};  // LayerNorm backward
+    int lnbwd_grid = 0;       // its persistent grid (workgroups)
 };
 
 inline bool parse_shape(const char* v, RowShape* s) {
@@ -89,6 +92,8 @@ inline Tuning read_tuning() {
         else if (!std::strcmp(k, "ew")) t.ew_vpt = std::atoi(v);
         else if (!std::strcmp(k, "gather")) t.gather_tpt = std::atoi(v);
         else if (!std::strcmp(k, "rope")) t.rope_ppt = std::atoi(v);
+        else if (!std::strcmp(k, "lnbwd")) parse_shape(v, &t.lnbwd);
+        else if (!std::strcmp(k, "lnbwd_grid")) t.lnbwd_grid = std::atoi(v);
     }
     return t;
 }

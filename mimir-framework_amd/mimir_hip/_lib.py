@@ -70,6 +70,13 @@ SIGNATURES = {
     "mimir_rope_table": (c_int, [c_int64, c_int64, c_double, _P, _P]),
     "mimir_rope_fwd": (c_int, [_P, _P, _P, c_int64, _P, _P, c_int64, c_int64, c_int64, c_int64,
                                c_int64, _P, _P, c_int64]),
+    "mimir_layernorm_bwd": (c_int, [_P, _P, _P, _P, _P, _P, _P, c_int64, c_int64, c_float, c_int]),
+    "mimir_gelu_bwd": (c_int, [_P, _P, _P, _P, c_int64, c_int]),
+    "mimir_silu_bwd": (c_int, [_P, _P, _P, _P, c_int64, c_int]),
+    "mimir_mul_bwd": (c_int, [_P, _P, _P, _P, _P, _P, c_int64, c_int, c_int]),
+    "mimir_add_bwd": (c_int, [_P, _P, c_int64, c_int64, _P, _P, c_int, c_int]),
+    "mimir_embedding_bwd": (c_int, [_P, _P, c_int64, _P, _P, c_int64, c_int32, c_int32, c_int32]),
+    "mimir_embedding_f32ids_bwd": (c_int, [_P, _P, c_int64, _P, _P, c_int64, c_int32, c_int32, c_int32]),
     "mimir_store_create": (c_int, [_P, _PP]),
     "mimir_store_destroy": (c_int, [_P]),
     "mimir_store_clear": (c_int, [_P]),

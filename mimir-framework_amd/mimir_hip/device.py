@@ -197,6 +197,32 @@ class Context:
                                            _ptr(k_out), k_heads, batch, seq, head_dim, pos_offset,
                                            _ptr(cos_tab), _ptr(sin_tab), table_rows))
 
+    # -- backward (Model::backwardPass branches) -------------------------------
+
+    def layernorm_bwd(self, x, dy, gamma, dx, dgamma, dbeta, groups, n, eps, accumulate=False):
+        self.check(self.lib.mimir_layernorm_bwd(self.handle, _ptr(x), _ptr(dy), _ptr(gamma), _ptr(dx),
+                                                _ptr(dgamma), _ptr(dbeta), groups, n, eps,
+                                                int(bool(accumulate))))
+
+    def gelu_bwd(self, x, dy, dx, n, accumulate=False):
+        self.check(self.lib.mimir_gelu_bwd(self.handle, _ptr(x), _ptr(dy), _ptr(dx), n, int(bool(accumulate))))
+
+    def silu_bwd(self, x, dy, dx, n, accumulate=False):
+        self.check(self.lib.mimir_silu_bwd(self.handle, _ptr(x), _ptr(dy), _ptr(dx), n, int(bool(accumulate))))
+
+    def mul_bwd(self, a, b, dy, da, db, n, acc_a=False, acc_b=False):
+        self.check(self.lib.mimir_mul_bwd(self.handle, _ptr(a), _ptr(b), _ptr(dy), _ptr(da), _ptr(db), n,
+                                          int(bool(acc_a)), int(bool(acc_b))))
+
+    def add_bwd(self, dy, na, nb, da, db, acc_a=False, acc_b=False):
+        self.check(self.lib.mimir_add_bwd(self.handle, _ptr(dy), na, nb, _ptr(da), _ptr(db),
+                                          int(bool(acc_a)), int(bool(acc_b))))
+
+    def embedding_bwd(self, ids, n_ids, dy, grad_table, table_len, vocab, dim, padding_idx, float_ids=False):
+        fn = self.lib.mimir_embedding_f32ids_bwd if float_ids else self.lib.mimir_embedding_bwd
+        self.check(fn(self.handle, _ptr(ids), n_ids, _ptr(dy), _ptr(grad_table), table_len, vocab, dim,
+                      padding_idx))
+
 
 class Event:
     """A stream-ordered timing event (``mimir_event``)."""

@@ -1,0 +1,313 @@
+"""Backward ops (libmimir_hip, backward.hip) against the CPU oracle's
+restatement of Model::backwardPass (Model.cpp:7305-9153) on the same seeded
+inputs.
+
+Tolerances: input gradients |gpu - ref| <= max(1e-6, 1e-5*|ref|) (widths
+beyond 4096 may instead be nearer the float64 value than the reference);
+gradient sums over tokens (dgamma, dbeta, a broadcast operand's gradient)
+the same bound relative to the magnitudes summed (float32 sums in another
+order differ by ~u * that); Multiply / Add gradients, accumulate_grad and the
+Embedding scatter-add bit for bit."""
+import numpy as np
+import pytest
+
+import mimir_hip as M
+import oracle as O
+import _exact as X
+from _parity import assert_bitexact, assert_close, assert_close_or_nearer_exact, assert_close_sum
+
+pytestmark = pytest.mark.gpu
+
+rng = np.random.default_rng(0xBAC)
+
+
+def dev(ctx, a, offset=0):
+    a = np.ascontiguousarray(a)
+    buf = ctx.empty(a.size + offset, a.dtype)
+    view = buf.offset(offset, a.shape) if offset else buf
+    ctx.upload(view, a)
+    return buf, view
+
+
+# ---------------------------------------------------------------------------
+# LayerNorm
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("cols", [1, 3, 4, 64, 100, 256, 512, 1000, 1024, 2048, 4096, 4100, 8192, 20000])
+@pytest.mark.parametrize("affine", ["gb", "g", "none"])
+def test_layernorm_bwd(ctx, cols, affine):
+    rows = 37 if cols <= 4096 else 5
+    x = (1.5 * rng.standard_normal((rows, cols)) + 0.25).astype(np.float32)
+    dy = rng.standard_normal((rows, cols)).astype(np.float32)
+    g = (1 + 0.2 * rng.standard_normal(cols)).astype(np.float32) if affine != "none" else None
+    has_b = affine == "gb"
+    prev = rng.standard_normal(2 * cols).astype(np.float32)
+    dx_ref, gp_ref = O.layernorm_bwd(x, dy, cols, g, has_b, 1e-5, prev[:cols * (2 if has_b else 1)] if g is not None
+                                     else None)
+    ex_dx, _, _, (sg, sb), dxs = X.layernorm_bwd(x, dy, cols, g, 1e-5)
+    bufs = [dev(ctx, a) for a in (x, dy)]
+    gb = dev(ctx, g) if g is not None else (None, None)
+    dxb = ctx.empty(x.shape)
+    dgb = dev(ctx, prev[:cols]) if g is not None else (None, None)
+    dbb = dev(ctx, prev[cols:]) if has_b else (None, None)
+    try:
+        ctx.layernorm_bwd(bufs[0][1], bufs[1][1], gb[1], dxb, dgb[1], dbb[1], rows, cols, 1e-5)
+        dx = dxb.numpy()
+        # dx = inv/n * (n*dxh - sum - xhat*sum2) cancels: held to the tolerance
+        # relative to the terms' magnitude (dxs); beyond 4096 it may instead be
+        # nearer the float64 value than the reference.
+        assert_close_or_nearer_exact(dx.ravel(), dx_ref, ex_dx, f"dx cols={cols}")
+        if cols <= 4096:
+            assert_close_sum(dx.ravel(), dx_ref, dxs, f"dx cols={cols}")
+        if g is not None:
+            assert_close_sum(dgb[1].numpy(), gp_ref[:cols], np.abs(prev[:cols]) + sg, "dgamma")
+        if has_b:
+            assert_close_sum(dbb[1].numpy(), gp_ref[cols:], np.abs(prev[cols:]) + sb, "dbeta")
+        # accumulate_grad into a present gradient: dx += value
+        base = rng.standard_normal(x.shape).astype(np.float32)
+        ctx.upload(dxb, base)
+        ctx.layernorm_bwd(bufs[0][1], bufs[1][1], gb[1], dxb, None, None, rows, cols, 1e-5, accumulate=True)
+        assert_bitexact(dxb.numpy().ravel(), O.accumulate(base, dx.ravel()), f"dx accumulate cols={cols}")
+    finally:
+        for b in (bufs[0][0], bufs[1][0], gb[0], dgb[0], dbb[0], dxb):
+            if b is not None:
+                b.free()
+
+
+@pytest.mark.parametrize("rows,cols", [(8192, 4096), (3000, 512), (1025, 64), (70000, 16)])
+def test_layernorm_bwd_many_rows(ctx, rows, cols):
+    # Many rows per persistent-grid slot: dgamma / dbeta sums over thousands of tokens.
+    x = rng.standard_normal((rows, cols), dtype=np.float32)
+    dy = rng.standard_normal((rows, cols), dtype=np.float32)
+    g = (1 + 0.02 * rng.standard_normal(cols)).astype(np.float32)
+    dx_ref, gp_ref = O.layernorm_bwd(x, dy, cols, g, True, 1e-5)
+    _, _, _, (sg, sb), dxs = X.layernorm_bwd(x, dy, cols, g, 1e-5)
+    (bx, vx), (bd, vd), (bg, vg) = dev(ctx, x), dev(ctx, dy), dev(ctx, g)
+    dxb = ctx.empty(x.shape)
+    dgb, dbb = ctx.to_device(np.zeros(cols, np.float32)), ctx.to_device(np.zeros(cols, np.float32))
+    try:
+        ctx.layernorm_bwd(vx, vd, vg, dxb, dgb, dbb, rows, cols, 1e-5)
+        assert_close_sum(dxb.numpy().ravel(), dx_ref, dxs, "dx")
+        assert_close_sum(dgb.numpy(), gp_ref[:cols], sg, "dgamma")
+        assert_close_sum(dbb.numpy(), gp_ref[cols:], sb, "dbeta")
+        # Deterministic: a second run gives the same bits.
+        d1 = dgb.numpy().copy()
+        ctx.upload(dgb, np.zeros(cols, np.float32))
+        ctx.layernorm_bwd(vx, vd, vg, dxb, dgb, None, rows, cols, 1e-5)
+        assert_bitexact(dgb.numpy(), d1, "dgamma rerun")
+    finally:
+        for b in (bx, bd, bg, dxb, dgb, dbb):
+            b.free()
+
+
+def test_layernorm_bwd_unaligned_and_inplace(ctx):
+    rows, cols = 9, 256
+    x = rng.standard_normal((rows, cols), dtype=np.float32)
+    dy = rng.standard_normal((rows, cols), dtype=np.float32)
+    g = (1 + 0.1 * rng.standard_normal(cols)).astype(np.float32)
+    dx_ref, gp_ref = O.layernorm_bwd(x, dy, cols, g, True, 1e-5)
+    (bx, vx), (bd, vd), (bg, vg) = dev(ctx, x, 1), dev(ctx, dy, 1), dev(ctx, g, 1)
+    dgb, dbb = ctx.to_device(np.zeros(cols, np.float32)), ctx.to_device(np.zeros(cols, np.float32))
+    try:
+        ctx.layernorm_bwd(vx, vd, vg, vd, dgb, dbb, rows, cols, 1e-5)  # unaligned (generic), dx over dy
+        _, _, _, (sg, sb), dxs = X.layernorm_bwd(x, dy, cols, g, 1e-5)
+        assert_close_sum(vd.numpy().ravel(), dx_ref, dxs, "dx unaligned in place")
+        assert_close_sum(dgb.numpy(), gp_ref[:cols], sg, "dgamma generic")
+        assert_close_sum(dbb.numpy(), gp_ref[cols:], sb, "dbeta generic")
+        # Aligned (register-resident rows), dx over dy as well.
+        (ax, avx), (ad, avd), (ag, avg) = dev(ctx, x), dev(ctx, dy), dev(ctx, g)
+        ctx.upload(dgb, np.zeros(cols, np.float32))
+        ctx.layernorm_bwd(avx, avd, avg, avd, dgb, None, rows, cols, 1e-5)
+        assert_close_sum(avd.numpy().ravel(), dx_ref, dxs, "dx aligned in place")
+        assert_close_sum(dgb.numpy(), gp_ref[:cols], sg, "dgamma aligned, dx over dy")
+        for b in (ax, ad, ag):
+            b.free()
+    finally:
+        for b in (bx, bd, bg, dgb, dbb):
+            b.free()
+
+
+def test_layernorm_bwd_errors(ctx):
+    d = ctx.to_device(np.ones(8, np.float32))
+    try:
+        with pytest.raises(M.MimirError):
+            ctx.layernorm_bwd(d, d, None, d, d, None, 2, 4, 1e-5)  # dgamma without gamma
+        with pytest.raises(M.MimirError):
+            ctx.layernorm_bwd(d, d, d, d, None, d, 2, 4, 1e-5)  # dbeta without dgamma
+        with pytest.raises(M.MimirError):
+            ctx.layernorm_bwd(d, d, None, d, None, None, 2, 0, 1e-5)
+    finally:
+        d.free()
+
+
+# ---------------------------------------------------------------------------
+# GELU / SiLU
+# ---------------------------------------------------------------------------
+
+SPECIALS = np.array([0.0, -0.0, 1e-30, -1e-40, 3.0, -3.0, 5.0, -5.0, 9.0, -9.0, 20.0, -20.0, 88.0, -88.0,
+                     100.0, -100.0, 1e20, -1e20, np.inf, -np.inf, np.nan], np.float32)
+
+
+@pytest.mark.parametrize("offset", [0, 1])
+@pytest.mark.parametrize("acc", [False, True])
+def test_gelu_silu_bwd(ctx, offset, acc):
+    x = np.concatenate([np.linspace(-10, 10, 40001, dtype=np.float32), SPECIALS,
+                        rng.standard_normal(50001).astype(np.float32) * 3])
+    dy = rng.standard_normal(x.size).astype(np.float32)
+    base = rng.standard_normal(x.size).astype(np.float32)
+    (bx, vx), (bd, vd), (bo, vo) = dev(ctx, x, offset), dev(ctx, dy, offset), dev(ctx, base, offset)
+    try:
+        for name, fn, ref_fn, ex in (("gelu", ctx.gelu_bwd, O.gelu_bwd, X.dgelu), ("silu", ctx.silu_bwd,
+                                                                                   O.silu_bwd, X.dsilu)):
+            ctx.upload(vo, base)
+            fn(vx, vd, vo, x.size, accumulate=acc)
+            got = vo.numpy()
+            ref = ref_fn(x, dy)
+            exact = dy.astype(np.float64) * ex(x)
+            if acc:
+                ref = O.accumulate(base, ref)
+                exact = base.astype(np.float64) + exact
+            # GELU: the reference's 1+tanh and 1-tanh^2 cancel for |x| > 3; the
+            # kernel's logistic form does not, and must then be nearer the
+            # float64 value than the reference when it leaves the tolerance.
+            assert_close_or_nearer_exact(got, ref, exact, f"{name}_bwd acc={acc}")
+            if name == "silu":
+                assert_close(got, ref, f"{name}_bwd acc={acc}")
+            else:
+                ok = np.abs(x) <= 3
+                assert_close(got[ok], ref[ok], "gelu_bwd |x|<=3")
+    finally:
+        for b in (bx, bd, bo):
+            b.free()
+
+
+# ---------------------------------------------------------------------------
+# Multiply / Add (bit-exact)
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("n", [1, 7, 4096, 100003])
+def test_mul_bwd_bitexact(ctx, n):
+    a, b, dy, pa, pb = (rng.standard_normal(n).astype(np.float32) for _ in range(5))
+    ra, rb = O.mul_bwd(a, b, dy)
+    ba, bb, bdy = ctx.to_device(a), ctx.to_device(b), ctx.to_device(dy)
+    da, db = ctx.to_device(pa), ctx.to_device(pb)
+    try:
+        ctx.mul_bwd(ba, bb, bdy, da, db, n)
+        assert_bitexact(da.numpy(), ra, "da")
+        assert_bitexact(db.numpy(), rb, "db")
+        ctx.upload(da, pa)
+        ctx.upload(db, pb)
+        ctx.mul_bwd(ba, bb, bdy, da, db, n, acc_a=True, acc_b=True)
+        assert_bitexact(da.numpy(), O.accumulate(pa, ra), "da accumulate")
+        assert_bitexact(db.numpy(), O.accumulate(pb, rb), "db accumulate")
+        # da aliases dy (output and first input share a name): products first.
+        ctx.mul_bwd(ba, bb, bdy, bdy, db, n, acc_a=True)
+        assert_bitexact(bdy.numpy(), O.accumulate(dy, ra), "da aliasing dy")
+        # Multiply(x, x): both accumulations land on one buffer, in order.
+        ctx.upload(bdy, dy)
+        ctx.upload(da, pa)
+        ctx.mul_bwd(ba, ba, bdy, da, da, n, acc_a=True, acc_b=True)
+        r0, r1 = O.mul_bwd(a, a, dy)
+        assert_bitexact(da.numpy(), O.accumulate(O.accumulate(pa, r0), r1), "da == db")
+    finally:
+        for d in (ba, bb, bdy, da, db):
+            d.free()
+
+
+@pytest.mark.parametrize("na,nb", [(4096, 4096), (4097, 4097), (64 * 4096, 4096), (4096, 64 * 4096),
+                                   (3 * 48, 48), (8192 * 4096, 1), (1, 1000), (999, 999)])
+def test_add_bwd(ctx, na, nb):
+    n = max(na, nb)
+    dy = rng.standard_normal(n).astype(np.float32)
+    pa = rng.standard_normal(na).astype(np.float32)
+    pb = rng.standard_normal(nb).astype(np.float32)
+    bdy, da, db = ctx.to_device(dy), ctx.to_device(pa), ctx.to_device(pb)
+    try:
+        for acc in (False, True):
+            ctx.upload(da, pa)
+            ctx.upload(db, pb)
+            ctx.add_bwd(bdy, na, nb, da, db, acc_a=acc, acc_b=acc)
+            for got, mine, prev in ((da.numpy(), na, pa), (db.numpy(), nb, pb)):
+                if mine == n:
+                    assert_bitexact(got, O.accumulate(prev, dy) if acc else dy, f"big operand acc={acc}")
+                else:
+                    s = O.add_bwd_small(dy, mine)
+                    ref = O.accumulate(prev, s) if acc else s
+                    scale = np.abs(dy.astype(np.float64)).reshape(-1, mine).sum(axis=0) + (np.abs(prev) if acc else 0)
+                    assert_close_sum(got, ref, scale, f"small operand acc={acc}")
+    finally:
+        for d in (bdy, da, db):
+            d.free()
+
+
+def test_add_bwd_aliasing_is_the_references(ctx):
+    # Add(x, x) -> x: the reference adds dy onto itself twice (4*dy).
+    dy = rng.standard_normal(1000).astype(np.float32)
+    d = ctx.to_device(dy)
+    try:
+        ctx.add_bwd(d, 1000, 1000, d, d, acc_a=True, acc_b=True)
+        assert_bitexact(d.numpy(), (dy + dy) + (dy + dy), "x + x")
+        # Broadcast with the big operand's gradient aliasing dy: the small
+        # operand's sum reads the doubled dy.
+        dy2 = rng.standard_normal(64 * 32).astype(np.float32)
+        big = ctx.to_device(dy2)
+        small = ctx.to_device(np.zeros(32, np.float32))
+        ctx.add_bwd(big, 64 * 32, 32, big, small, acc_a=True, acc_b=False)
+        assert_bitexact(big.numpy(), dy2 + dy2, "big aliasing dy")
+        assert_close_sum(small.numpy(), O.add_bwd_small(dy2 + dy2, 32),
+                         2 * np.abs(dy2.astype(np.float64)).reshape(-1, 32).sum(axis=0), "small after doubling")
+        big.free()
+        small.free()
+    finally:
+        d.free()
+
+
+def test_add_bwd_errors(ctx):
+    d = ctx.to_device(np.ones(10, np.float32))
+    try:
+        with pytest.raises(M.MimirError):
+            ctx.add_bwd(d, 10, 3, d, d)  # not broadcastable
+        with pytest.raises(M.MimirError):
+            ctx.add_bwd(d, 0, 3, d, d)
+    finally:
+        d.free()
+
+
+# ---------------------------------------------------------------------------
+# Embedding scatter-add (bit-exact)
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("vocab,dim,n,pad", [(32000, 4096, 2048, -1), (50, 64, 5000, 3), (7, 6, 100, 0),
+                                             (1000, 128, 32768, -1), (1, 4, 10, -1)])
+@pytest.mark.parametrize("float_ids", [False, True])
+def test_embedding_bwd_bitexact(ctx, vocab, dim, n, pad, float_ids):
+    ids = rng.integers(-2, vocab + 2, n).astype(np.int32)
+    ids[: n // 4] = min(5, vocab - 1)  # one row hit many times: adds in token order
+    arg = ids.astype(np.float32) + np.float32(0.25) if float_ids else ids
+    dy = rng.standard_normal((n, dim)).astype(np.float32)
+    gt = rng.standard_normal(vocab * dim).astype(np.float32)
+    ref = O.embedding_bwd(arg, dy, gt, vocab, dim, pad)
+    bi, bdy, bg = ctx.to_device(arg), ctx.to_device(dy), ctx.to_device(gt)
+    try:
+        ctx.embedding_bwd(bi, n, bdy, bg, gt.size, vocab, dim, pad, float_ids=float_ids)
+        assert_bitexact(bg.numpy(), ref, "grad table")
+    finally:
+        for d in (bi, bdy, bg):
+            d.free()
+
+
+def test_embedding_bwd_unaligned_rows_and_errors(ctx):
+    vocab, dim, n = 9, 5, 300
+    ids = rng.integers(0, vocab, n).astype(np.int32)
+    dy = rng.standard_normal((n, dim)).astype(np.float32)
+    gt = np.zeros(vocab * dim, np.float32)
+    ref = O.embedding_bwd(ids, dy, gt, vocab, dim, -1)
+    bi, bdy, bg = ctx.to_device(ids), ctx.to_device(dy), ctx.to_device(gt)
+    try:
+        ctx.embedding_bwd(bi, n, bdy, bg, gt.size, vocab, dim, -1)
+        assert_bitexact(bg.numpy(), ref, "dim 5 (scalar rows)")
+        with pytest.raises(M.MimirError):
+            ctx.embedding_bwd(bi, n, bdy, bg, gt.size - 1, vocab, dim, -1)  # table too small
+    finally:
+        for d in (bi, bdy, bg):
+            d.free()
