@@ -265,9 +265,120 @@ __global__ __launch_bounds__(kSumLanes * kWave) void sum_slots(const float* part
     }
 }
 
+// The same with 16-byte columns (width, stride and split multiples of 4):
+// each slot lane issues U loads before adding them in slot order, so the sum
+// order (hence every bit of the result) is that of sum_slots.
+template <int U>
+__global__ __launch_bounds__(kSumLanes * kWave) void sum_slots4(const float* part, int64_t nslots, int64_t stride,
+                                                                int64_t width, float* out0, float* out1,
+                                                                int64_t split, int acc) {
+    __shared__ f4 lds[kSumLanes][kWave];
+    const int lane = threadIdx.x / kWave;
+    const int col = threadIdx.x % kWave;
+    const int64_t c4 = static_cast<int64_t>(blockIdx.x) * kWave + col;
+    // The values accumulated onto are loaded first, off the critical path.
+    float prev[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (acc && lane == 0 && 4 * c4 < width) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int64_t c = 4 * c4 + i;
+            prev[i] = c < split ? out0[c] : out1[c - split];
+        }
+    }
+    f4 s = f4(0.0f);
+    if (4 * c4 < width) {
+        const f4* p = reinterpret_cast<const f4*>(part) + c4;
+        const int64_t st4 = stride / 4;
+        int64_t k = lane;
+        for (; k + (U - 1) * kSumLanes < nslots; k += U * kSumLanes) {
+            f4 v[U];
+#pragma unroll
+            for (int u = 0; u < U; ++u) v[u] = p[(k + u * kSumLanes) * st4];
+#pragma unroll
+            for (int u = 0; u < U; ++u) s += v[u];
+        }
+        for (; k < nslots; k += kSumLanes) s += p[k * st4];
+    }
+    lds[lane][col] = s;
+    __syncthreads();
+    if (lane == 0 && 4 * c4 < width) {
+        f4 t = lds[0][col];
+#pragma unroll
+        for (int l = 1; l < kSumLanes; ++l) t += lds[l][col];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int64_t c = 4 * c4 + i;
+            float* o = c < split ? out0 + c : out1 + (c - split);
+            *o = acc ? prev[i] + t[i] : t[i];
+        }
+    }
+}
+
+// First level of a two-level slot sum for many slots: group g (blockIdx.y)
+// of kGroups sums its contiguous range of slots for 64 float4 columns
+// (blockIdx.x); its 4 waves take interleaved slots, each adding U loads at
+// a time in slot order, and the 4 wave sums are added in wave order:
+// lvl2[g*width + c] = the group's sum.  sum_slots4 then adds the kGroups
+// rows in order.  (Folding that second level into this kernel with an
+// arrival counter needs a device-scope release per block, which on this
+// GPU writes back the XCD's L2 each time and costs far more than a launch.)
+constexpr int kGroups = 16;
+
+template <int U>
+__global__ __launch_bounds__(kBlock) void slot_groups4(const float* part, int64_t nslots, int64_t stride,
+                                                       int64_t width, float* lvl2) {
+    constexpr int W = kBlock / kWave;
+    __shared__ f4 lds[W][kWave];
+    const int w = threadIdx.x / kWave;
+    const int col = threadIdx.x % kWave;
+    const int64_t c4 = static_cast<int64_t>(blockIdx.x) * kWave + col;
+    const int64_t per = (nslots + kGroups - 1) / kGroups;
+    const int64_t k0 = static_cast<int64_t>(blockIdx.y) * per;
+    const int64_t k1 = k0 + per < nslots ? k0 + per : nslots;
+    f4 s = f4(0.0f);
+    if (4 * c4 < width) {
+        const f4* p = reinterpret_cast<const f4*>(part) + c4;
+        const int64_t st4 = stride / 4;
+        int64_t k = k0 + w;
+        for (; k + (U - 1) * W < k1; k += U * W) {
+            f4 v[U];
+#pragma unroll
+            for (int u = 0; u < U; ++u) v[u] = p[(k + u * W) * st4];
+#pragma unroll
+            for (int u = 0; u < U; ++u) s += v[u];
+        }
+        for (; k < k1; k += W) s += p[k * st4];
+    }
+    lds[w][col] = s;
+    __syncthreads();
+    if (w == 0 && 4 * c4 < width) {
+        f4 t = lds[0][col];
+#pragma unroll
+        for (int l = 1; l < W; ++l) t += lds[l][col];
+        reinterpret_cast<f4*>(lvl2 + static_cast<int64_t>(blockIdx.y) * width)[c4] = t;
+    }
+}
+
+// out (+)= the sum of nslots slot rows of `part` (row stride `stride`, first
+// `width` columns; columns below `split` to out0, the rest to out1).  With
+// `tmp` (kGroups*width floats) and many slots, two levels; else one.
 int launch_sum_slots(mimir_ctx* ctx, const float* part, int64_t nslots, int64_t stride, int64_t width, float* out0,
-                     float* out1, int64_t split, bool acc) {
+                     float* out1, int64_t split, bool acc, float* tmp = nullptr) {
     unsigned blocks;
+    if (width % 4 == 0 && stride % 4 == 0 && split % 4 == 0 && aligned16(part)) {
+        if (!grid_for(width / 4, kWave, &blocks))
+            return fail(ctx, MIMIR_EINVAL, "sum_slots: width %lld exceeds the grid limit", (long long)width);
+        if (tmp && aligned16(tmp) && nslots >= 4 * kGroups) {
+            slot_groups4<8><<<dim3(blocks, kGroups), kBlock, 0, ctx->stream>>>(part, nslots, stride, width, tmp);
+            if (int st = launched(ctx, "slot_groups4")) return st;
+            part = tmp;
+            nslots = kGroups;
+            stride = width;
+        }
+        sum_slots4<8><<<blocks, kSumLanes * kWave, 0, ctx->stream>>>(part, nslots, stride, width, out0, out1, split,
+                                                                     acc ? 1 : 0);
+        return launched(ctx, "sum_slots4");
+    }
     if (!grid_for(width, kWave, &blocks))
         return fail(ctx, MIMIR_EINVAL, "sum_slots: width %lld exceeds the grid limit", (long long)width);
     sum_slots<<<blocks, kSumLanes * kWave, 0, ctx->stream>>>(part, nslots, stride, width, out0, out1, split,
@@ -372,11 +483,12 @@ __device__ __forceinline__ void row_sum2(float& a, float& b, float* la, float* l
 
 __device__ __forceinline__ float hsum(f4 v) { return (v.x + v.y) + (v.z + v.w); }
 
-// One workgroup slot per (block, sub-row); the grid is persistent (fewer
-// blocks than row groups), so each slot visits rows sub + RPB*(block +
-// k*grid) and keeps dgamma / dbeta for its TPR*VPT*4 columns in registers.
-// Every reduction is a fresh LDS array or is separated from its previous
-// use by another barrier, so no leading barriers are needed.
+// A persistent grid (fewer blocks than row groups): sub-row `sub` of block b
+// visits rows sub + RPB*(b + k*grid) and keeps dgamma / dbeta for its
+// TPR*VPT*4 columns in registers; the block writes one slot of partial sums.
+// The two reduction rounds of a row use separate LDS arrays, so each
+// array's reuse (next row) is separated from its reads by the other round's
+// barrier: no leading barriers are needed.
 template <int TPR, int VPT, int BS>
 __global__ __launch_bounds__(BS) void ln_bwd_vec(LnBwdArgs a) {
     constexpr int RPB = BS / TPR;
@@ -396,71 +508,105 @@ __global__ __launch_bounds__(BS) void ln_bwd_vec(LnBwdArgs a) {
         db[j] = f4(0.0f);
     }
     const int64_t step = static_cast<int64_t>(gridDim.x) * RPB;
+    // Row group `b`'s x and dy for this thread (zeros past the end).
+    auto load_rows = [&](int64_t b, f4* xo, f4* go) {
+        const int64_t r = b + sub;
+        const int64_t l = r < a.rows ? c4n : 0;
+#pragma unroll
+        for (int j = 0; j < VPT; ++j) {
+            const int64_t c4 = static_cast<int64_t>(j) * TPR + t;
+            const bool ok = c4 < l;
+            xo[j] = ok ? ld4<true>(a.x + r * a.cols + 4 * c4) : f4(0.0f);
+            go[j] = ok ? ld4<true>(a.dy + r * a.cols + 4 * c4) : f4(0.0f);
+        }
+    };
+    f4 xv[VPT], gv[VPT];
+    load_rows(static_cast<int64_t>(blockIdx.x) * RPB, xv, gv);
     for (int64_t base = static_cast<int64_t>(blockIdx.x) * RPB; base < a.rows; base += step) {
         const int64_t row = base + sub;
         const int64_t lim = row < a.rows ? c4n : 0;  // past-end rows join the barriers only
         const int64_t off = row * a.cols;
-        f4 xv[VPT], gv[VPT];
+        // The next row group's loads go out before this one's reductions, so
+        // each wave keeps memory busy while it waits at the barriers.
+        f4 xn[VPT], gn[VPT];
+        load_rows(base + step, xn, gn);
+        // Two reduction rounds per row.  Round 1: sum(x) and sum(dxhat)
+        // (dxhat = dy*gamma needs no statistics).  Round 2, with the mean:
+        // sum((x-mean)^2) for the reference's two-pass variance and
+        // sum(dxhat*(x-mean)), which times inv_std is the reference's
+        // sum(dxhat*xhat) (:7783-7797) up to rounding.
+        float s = 0.0f, s1 = 0.0f;
 #pragma unroll
         for (int j = 0; j < VPT; ++j) {
-            const int64_t c4 = static_cast<int64_t>(j) * TPR + t;
-            const bool ok = c4 < lim;
-            xv[j] = ok ? ld4<true>(a.x + off + 4 * c4) : f4(0.0f);
-            gv[j] = ok ? ld4<true>(a.dy + off + 4 * c4) : f4(0.0f);
+            s += hsum(xv[j]);
+            s1 += hsum(gv[j] * gm[j]);
         }
-        float s = 0.0f;
-#pragma unroll
-        for (int j = 0; j < VPT; ++j) s += hsum(xv[j]);
-        const float mean = row_sum<NW, false>(s, lds[0], sub) / n;  // :7765-7768
-        float q = 0.0f;
+        row_sum2<NW>(s, s1, lds[0], lds[1], sub);
+        const float mean = s / n;  // :7765-7768
+        float q = 0.0f, p2 = 0.0f;
 #pragma unroll
         for (int j = 0; j < VPT; ++j) {
             const int64_t c4 = static_cast<int64_t>(j) * TPR + t;
             if (c4 < lim) {
                 const f4 d = xv[j] - mean;
                 q += (d.x * d.x + d.y * d.y) + (d.z * d.z + d.w * d.w);
+                p2 += hsum(gv[j] * gm[j] * d);
             }
         }
-        const float var = row_sum<NW, false>(q, lds[1], sub) / n;  // :7770-7776
-        const float inv_std = 1.0f / sqrtf(var + a.eps);             // :7777
-        float s1 = 0.0f, s2 = 0.0f;
-        f4 xh[VPT], dxh[VPT];
-#pragma unroll
-        for (int j = 0; j < VPT; ++j) {  // :7783-7797
-            const int64_t c4 = static_cast<int64_t>(j) * TPR + t;
-            if (c4 < lim) {
-                xh[j] = (xv[j] - mean) * inv_std;
-                dxh[j] = gv[j] * gm[j];
-                dg[j] += gv[j] * xh[j];
-                db[j] += gv[j];
-                s1 += hsum(dxh[j]);
-                s2 += hsum(dxh[j] * xh[j]);
-            } else {
-                xh[j] = f4(0.0f);
-                dxh[j] = f4(0.0f);
-            }
-        }
-        row_sum2<NW>(s1, s2, lds[2], lds[3], sub);
+        row_sum2<NW>(q, p2, lds[2], lds[3], sub);
+        const float var = q / n;                          // :7770-7776
+        const float inv_std = 1.0f / sqrtf(var + a.eps);  // :7777
+        const float s2 = p2 * inv_std;
         const float k = inv_std * invF;
 #pragma unroll
-        for (int j = 0; j < VPT; ++j) {  // :7800-7805
+        for (int j = 0; j < VPT; ++j) {  // :7783-7805
             const int64_t c4 = static_cast<int64_t>(j) * TPR + t;
             if (c4 < lim) {
-                f4 o = k * ((n * dxh[j] - s1) - xh[j] * s2);
+                const f4 xh = (xv[j] - mean) * inv_std;
+                const f4 dxh = gv[j] * gm[j];
+                dg[j] += gv[j] * xh;
+                db[j] += gv[j];
+                f4 o = k * ((n * dxh - s1) - xh * s2);
                 if (a.acc) o = ld4<true>(a.dx + off + 4 * c4) + o;
                 st4<true>(a.dx + off + 4 * c4, o);
             }
         }
-    }
-    if (a.part) {
-        float* p = a.part + (static_cast<int64_t>(blockIdx.x) * RPB + sub) * 2 * a.cols;
 #pragma unroll
         for (int j = 0; j < VPT; ++j) {
-            const int64_t c4 = static_cast<int64_t>(j) * TPR + t;
-            if (c4 < c4n) {
-                *reinterpret_cast<f4*>(p + 4 * c4) = dg[j];
-                *reinterpret_cast<f4*>(p + a.cols + 4 * c4) = db[j];
+            xv[j] = xn[j];
+            gv[j] = gn[j];
+        }
+    }
+    if (!a.part) return;
+    // One slot per workgroup: the sub-rows' sums are added in sub-row order
+    // through LDS, then written once.
+    float* p = a.part + static_cast<int64_t>(blockIdx.x) * 2 * a.cols;
+    if constexpr (RPB > 1) {
+        __shared__ f4 comb[2 * TPR * VPT];
+        for (int r = 0; r < RPB; ++r) {
+            if (sub == r) {
+#pragma unroll
+                for (int j = 0; j < VPT; ++j) {
+                    const int i = j * TPR + t;
+                    comb[i] = r == 0 ? dg[j] : comb[i] + dg[j];
+                    comb[TPR * VPT + i] = r == 0 ? db[j] : comb[TPR * VPT + i] + db[j];
+                }
             }
+            __syncthreads();
+        }
+        if (sub != 0) return;
+#pragma unroll
+        for (int j = 0; j < VPT; ++j) {
+            dg[j] = comb[j * TPR + t];
+            db[j] = comb[TPR * VPT + j * TPR + t];
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) {
+        const int64_t c4 = static_cast<int64_t>(j) * TPR + t;
+        if (c4 < c4n) {
+            *reinterpret_cast<f4*>(p + 4 * c4) = dg[j];
+            *reinterpret_cast<f4*>(p + a.cols + 4 * c4) = db[j];
         }
     }
 }
@@ -544,18 +690,21 @@ int launch_ln_bwd_vec(mimir_ctx* ctx, LnBwdArgs a, float* dgamma, float* dbeta) 
     const int64_t groups = (a.rows + RPB - 1) / RPB;
     int64_t grid = ctx->tune.lnbwd_grid > 0 ? ctx->tune.lnbwd_grid : 512;
     if (grid > groups) grid = groups;
-    const int64_t nslots = grid * RPB;
-    if (dgamma) {
+    const int64_t nslots = grid;
+    float* tmp = nullptr;
+    if (dgamma) {  // partial slots, then room for the second level of their sum
         void* s = nullptr;
-        if (int st = ensure_scratch(ctx, sizeof(float) * static_cast<size_t>(nslots * 2 * a.cols), &s)) return st;
+        const size_t bytes = sizeof(float) * static_cast<size_t>((nslots + kGroups) * 2 * a.cols);
+        if (int st = ensure_scratch(ctx, bytes, &s)) return st;
         a.part = static_cast<float*>(s);
+        tmp = a.part + nslots * 2 * a.cols;
     }
     ln_bwd_vec<TPR, VPT, BS><<<static_cast<unsigned>(grid), BS, 0, ctx->stream>>>(a);
     if (int st = launched(ctx, "ln_bwd_vec")) return st;
     if (!dgamma) return MIMIR_OK;
     // dbeta null: sum only the dgamma half.
     return launch_sum_slots(ctx, a.part, nslots, 2 * a.cols, dbeta ? 2 * a.cols : a.cols, dgamma, dbeta, a.cols,
-                            true);
+                            true, tmp);
 }
 
 int ln_bwd_generic_run(mimir_ctx* ctx, LnBwdArgs a, float* dgamma, float* dbeta) {
