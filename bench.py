@@ -149,6 +149,60 @@ def build_ops():
     ops.append(OpBench("cfg4_add", 4, "residual add fp32 [8192x4096]", "binary_vec<Add>",
                        3 * 8192 * 4096 * f4, 8192, "rows", make_add))
 
+    # Backward of the same ops (Model::backwardPass branches, Model.cpp:7305-9153)
+    # at the configs[3] / configs[4] shapes.
+    def make_lnb(ctx, nsets):
+        x, g, b, eps = G.cfg4_layernorm()
+        dy = G.cfg4_grad(x.shape, 8)
+        pd = _replicate(ctx, [g, np.zeros_like(g), np.zeros_like(b)], 1)[0]
+        sets = _replicate(ctx, [x, dy, np.empty_like(x)], nsets)
+        return (lambda i: ctx.layernorm_bwd(sets[i][0], sets[i][1], pd[0], sets[i][2], pd[1], pd[2], 8192, 4096,
+                                            eps)), sets
+    ops.append(OpBench("cfg4_layernorm_bwd", 4, "LayerNorm backward fp32 [8192x4096]: dx, dgamma, dbeta",
+                       "ln_bwd_vec + slot sums", 3 * 8192 * 4096 * f4 + 5 * 4096 * f4, 8192, "rows", make_lnb))
+
+    def make_act_bwd(fn_name):
+        def make(ctx, nsets):
+            a = G.cfg4_gelu()
+            dy = G.cfg4_grad(a.shape, 9)
+            sets = _replicate(ctx, [a, dy, np.empty_like(a)], nsets)
+            fn = getattr(ctx, fn_name)
+            return (lambda i: fn(sets[i][0], sets[i][1], sets[i][2], a.size)), sets
+        return make
+    ops.append(OpBench("cfg4_gelu_bwd", 4, "GELU backward fp32 [8192x11008]", "dact_vec<DGelu>",
+                       3 * 8192 * 11008 * f4, 8192, "rows", make_act_bwd("gelu_bwd")))
+    ops.append(OpBench("cfg4_silu_bwd", 4, "SiLU backward fp32 [8192x11008]", "dact_vec<DSilu>",
+                       3 * 8192 * 11008 * f4, 8192, "rows", make_act_bwd("silu_bwd")))
+
+    def make_mulb(ctx, nsets):
+        g, u = G.cfg4_swiglu()
+        dy = G.cfg4_grad(g.shape, 10)
+        sets = _replicate(ctx, [g, u, dy, np.empty_like(g), np.empty_like(g)], nsets)
+        return (lambda i: ctx.mul_bwd(sets[i][0], sets[i][1], sets[i][2], sets[i][3], sets[i][4], g.size)), sets
+    ops.append(OpBench("cfg4_mul_bwd", 4, "Multiply backward fp32 [8192x11008]: da, db", "mul_bwd_vec",
+                       5 * 8192 * 11008 * f4, 8192, "rows", make_mulb))
+
+    def make_addb(ctx, nsets):
+        a, _ = G.cfg4_add()
+        sets = _replicate(ctx, [a, np.empty_like(a), np.empty_like(a)], nsets)
+        return (lambda i: ctx.add_bwd(sets[i][0], a.size, a.size, sets[i][1], sets[i][2])), sets
+    ops.append(OpBench("cfg4_add_bwd", 4, "residual Add backward fp32 [8192x4096]: da, db", "add_bwd_vec",
+                       3 * 8192 * 4096 * f4, 8192, "rows", make_addb))
+
+    uniq3 = int(np.unique(G.cfg3_ids()).size)
+
+    def make_embb(ctx, nsets):
+        ids = G.cfg3_ids()
+        dy = G.cfg3_embedding_grad()
+        gt = _replicate(ctx, [np.zeros(32000 * 4096, np.float32)], 1)[0][0]
+        sets = _replicate(ctx, [ids, dy], nsets)
+        return (lambda i: ctx.embedding_bwd(sets[i][0], ids.size, sets[i][1], gt, 32000 * 4096, 32000, 4096, -1)), \
+            sets + [[gt]]
+    ops.append(OpBench("cfg3_embedding_bwd", 3,
+                       f"Embedding backward (scatter-add) ids int32 [16x2048] -> table grad [32000x4096], "
+                       f"{uniq3} distinct ids", "radix sort + embed_bwd_rows_vec",
+                       32768 * 4 + 32768 * 4096 * f4 + 2 * uniq3 * 4096 * f4, 32768, "token rows", make_embb))
+
     # Calibration: a plain streaming copy of 512 MiB (mimir_copy), the
     # practical HBM ceiling and the yardstick for the FETCH/WRITE counters.
     def make_copy(ctx, nsets):
@@ -308,6 +362,37 @@ def cpu_leg(which, reps):
             else:
                 t = O.time_port(lambda: O.add(a, b), reps)
                 rec(key, t, 3 * a.nbytes, 8192, "port", "full [8192x4096] oracle add")
+        elif key == "cfg4_layernorm_bwd":
+            x, g, b, eps = G.cfg4_layernorm(rows=512)
+            dy = G.cfg4_grad((8192, 4096), 8)[:512]
+            t = O.time_port(lambda: O.layernorm_bwd(x, dy, 4096, g, True, eps), reps)
+            rec(key, t, 3 * x.nbytes + 5 * g.nbytes, 512, "port",
+                "512 of 8192 rows, oracle layernorm_bwd (Model.cpp:7719-7821 restated)")
+        elif key in ("cfg4_gelu_bwd", "cfg4_silu_bwd"):
+            a = G.cfg4_gelu(rows=512)
+            dy = G.cfg4_grad((8192, 11008), 9)[:512]
+            fn = O.gelu_bwd if key == "cfg4_gelu_bwd" else O.silu_bwd
+            t = O.time_port(lambda: fn(a, dy), reps)
+            rec(key, t, 3 * a.nbytes, 512, "port", f"512 of 8192 rows, oracle {fn.__name__}")
+        elif key == "cfg4_mul_bwd":
+            g, u = G.cfg4_swiglu(rows=512)
+            dy = G.cfg4_grad((8192, 11008), 10)[:512]
+            t = O.time_port(lambda: O.mul_bwd(g, u, dy), reps)
+            rec(key, t, 5 * g.nbytes, 512, "port", "512 of 8192 rows, oracle mul_bwd")
+        elif key == "cfg4_add_bwd":
+            a, _ = G.cfg4_add()
+            t = O.time_port(lambda: (a.copy(), a.copy()), reps)
+            rec(key, t, 3 * a.nbytes, 8192, "port",
+                "full [8192x4096]: accumulate_grad into two absent names is two vector copies (Model.cpp:7552-7555)")
+        elif key == "cfg3_embedding_bwd":
+            ids = G.cfg3_ids().ravel()[:4096].copy()
+            dy = G.cfg3_embedding_grad()[:4096].copy()
+            gt = np.zeros(32000 * 4096, np.float32)
+            fn = O._oracle().oracle_embedding_bwd_i32
+            t = O.time_port(lambda: fn(O._p(ids), ids.size, O._p(dy), O._p(gt), gt.size, 32000, 4096, -1), reps)
+            u = int(np.unique(ids).size)
+            rec(key, t, ids.nbytes + dy.nbytes + 2 * u * 4096 * 4, 4096, "port",
+                f"first 4096 of 32768 tokens ({u} distinct ids), oracle embedding_bwd_i32 into a resident table")
     return out
 
 
@@ -348,6 +433,17 @@ def main():
     log(f"workload {head.key}: {head.desc}")
     res = time_op(ctx, head, args.steps, args.warmup)
     log(f"  {res['us_per_launch']} us/launch, {res['GB_s']} GB/s ({100 * res['frac_of_peak']:.1f}% of peak)")
+
+    # The practical ceiling at this size: a plain copy moving the same bytes
+    # per launch (half read, half written), timed the same way.
+    n_copy = (head.nbytes // 8) // 4 * 4
+
+    def make_same_copy(ctx, nsets):
+        sets = [[ctx.empty(n_copy), ctx.empty(n_copy)] for _ in range(nsets)]
+        return (lambda i: ctx.copy(sets[i][1], sets[i][0], n_copy * 4)), sets
+    same = time_op(ctx, OpBench("copy_same_bytes", -1, "copy of the workload's bytes", "copy16_kernel",
+                                8 * n_copy, n_copy, "floats", make_same_copy), args.steps, args.warmup)
+    log(f"  copy of the same bytes: {same['us_per_launch']} us/launch, {same['GB_s']} GB/s")
 
     sweep = []
     keys = ([o.key for o in ops] if args.ops == "all" else
@@ -410,6 +506,9 @@ def main():
             "frac": res["frac_of_peak"],
             "traffic": None if traffic is None else traffic.get("traffic_bytes"),
             "algorithmic_bytes": head.nbytes,
+            "copy_same_bytes": {"GB_s": same["GB_s"], "frac": same["frac_of_peak"],
+                                "us_per_launch": same["us_per_launch"]},
+            "frac_of_copy": round(res["GB_s"] / same["GB_s"], 4),
         },
         "cpu_baseline": None if cb is None else {
             "value": cb["value"], "unit": cb["unit"], "cores": cb["cores"], "kind": cb["kind"],

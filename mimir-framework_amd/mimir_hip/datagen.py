@@ -90,3 +90,20 @@ def cfg4_swiglu(rows=8192, cols=11008):
 
 def cfg4_add(rows=8192, cols=4096):
     return normal(4, 6, (rows, cols)), normal(4, 7, (rows, cols))
+
+
+# --------------------------------------------------------------------------
+# Output gradients for the backward ops at the same shapes (N(0,1); the
+# embedding's scaled by 0.01 like a small loss gradient)
+# --------------------------------------------------------------------------
+
+def cfg4_grad(shape, tensor=8):
+    return normal(4, tensor, shape)
+
+
+def cfg3_embedding_grad(batch=16, seq=2048, dim=4096):
+    return normal(3, 4, (batch * seq, dim), 0.01)
+
+
+def cfg3_ids(batch=16, seq=2048, vocab=32000):
+    return ids(3, 1, (batch, seq), vocab)
