@@ -359,6 +359,18 @@ __global__ __launch_bounds__(kBlock) void slot_groups4(const float* part, int64_
     }
 }
 
+// out[0] (+)= the sum of the first float of nslots slots (row stride
+// `stride`): 1024 threads add slots t, t+1024, ... in order, then the block
+// tree adds the threads in order.
+__global__ __launch_bounds__(1024) void sum_total(const float* part, int64_t nslots, int64_t stride, float* out,
+                                                  int acc) {
+    __shared__ float lds[1024 / kWave];
+    float s = 0.0f;
+    for (int64_t k = threadIdx.x; k < nslots; k += 1024) s += part[k * stride];
+    s = block_sum<1024 / kWave>(s, lds);
+    if (threadIdx.x == 0) *out = acc ? *out + s : s;
+}
+
 // out (+)= the sum of nslots slot rows of `part` (row stride `stride`, first
 // `width` columns; columns below `split` to out0, the rest to out1).  With
 // `tmp` (kGroups*width floats) and many slots, two levels; else one.
@@ -379,6 +391,10 @@ int launch_sum_slots(mimir_ctx* ctx, const float* part, int64_t nslots, int64_t 
                                                                      acc ? 1 : 0);
         return launched(ctx, "sum_slots4");
     }
+    if (width == 1) {
+        sum_total<<<1, 1024, 0, ctx->stream>>>(part, nslots, stride, out0, acc ? 1 : 0);
+        return launched(ctx, "sum_total");
+    }
     if (!grid_for(width, kWave, &blocks))
         return fail(ctx, MIMIR_EINVAL, "sum_slots: width %lld exceeds the grid limit", (long long)width);
     sum_slots<<<blocks, kSumLanes * kWave, 0, ctx->stream>>>(part, nslots, stride, width, out0, out1, split,
@@ -386,60 +402,204 @@ int launch_sum_slots(mimir_ctx* ctx, const float* part, int64_t nslots, int64_t 
     return launched(ctx, "sum_slots");
 }
 
-// Column sums of dy viewed as [rows x cols] over row chunks of `chunk` rows:
-// part[k*cols + c] = sum of dy[r*cols + c], r in chunk k, in row order.
-__global__ __launch_bounds__(kBlock) void colsum_part(const float* dy, int64_t rows, int64_t cols, int64_t chunk,
-                                                     float* part) {
-    const int64_t c = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
-    if (c >= cols) return;
-    const int64_t r0 = static_cast<int64_t>(blockIdx.y) * chunk;
-    const int64_t r1 = r0 + chunk < rows ? r0 + chunk : rows;
-    float s = 0.0f;
-    for (int64_t r = r0; r < r1; ++r) s += dy[r * cols + c];
-    part[static_cast<int64_t>(blockIdx.y) * cols + c] = s;
+// 16-byte columns per block of add_bcast_part: all kBlock threads for wide
+// rows, else the next power of two above the row's float4 count.
+__host__ __device__ inline int bcast_cols_per_block(int64_t w4) {
+    int cw = 1;
+    while (cw < kBlock && cw < w4) cw *= 2;
+    return cw;
 }
 
-// Sum of n floats in contiguous chunks: part[k] = sum of chunk k.
-__global__ __launch_bounds__(kBlock) void total_part(const float* dy, int64_t n, int64_t chunk, float* part) {
+// Broadcast Add backward in one pass over dy, viewed as [rows x cols]
+// (cols = the small operand's size): the big operand's gradient d_big (+)= dy
+// (:7577), and per chunk of `chunk` rows the column sums of what the
+// reference then reduces (:7586-7594) -- dy, or the updated d_big when it is
+// the same buffer as dy (the reference's grad_out is that map entry).
+// part[k*cols + c], rows in order.  VEC: 16-byte columns, four rows' loads in
+// flight per thread (each element is read before it is written, so d_big may
+// alias dy).
+template <bool VEC>
+__global__ __launch_bounds__(kBlock) void add_bcast_part(const float* dy, float* d_big, int acc_big, int64_t rows,
+                                                         int64_t cols, int64_t chunk, float* part) {
+    const int64_t r0 = static_cast<int64_t>(blockIdx.y) * chunk;
+    const int64_t r1 = r0 + chunk < rows ? r0 + chunk : rows;
+    const bool same = d_big == dy;
+    if constexpr (VEC) {
+        // cw = 16-byte columns per block (a power of two up to kBlock); narrow
+        // rows pack L = kBlock / cw row lanes per block, lane l taking rows
+        // l, l+L, ... of the chunk; the lanes are added in lane order.
+        __shared__ f4 lds[kBlock];
+        const int64_t w4 = cols / 4;
+        const int cw = bcast_cols_per_block(w4);
+        const int L = kBlock / cw;
+        const int col = threadIdx.x % cw;
+        const int lane = threadIdx.x / cw;
+        const int64_t c4 = static_cast<int64_t>(blockIdx.x) * cw + col;
+        const bool live = c4 < w4;
+        const f4* src = reinterpret_cast<const f4*>(dy) + c4;
+        f4* dst = d_big ? reinterpret_cast<f4*>(d_big) + c4 : nullptr;
+        f4 s = f4(0.0f);
+        if (live) {
+            int64_t r = r0 + lane;
+            for (; r + 3 * L < r1; r += 4 * L) {
+                f4 v[4], o[4];
+#pragma unroll
+                for (int u = 0; u < 4; ++u) v[u] = __builtin_nontemporal_load(src + (r + u * L) * w4);
+                if (dst) {
+#pragma unroll
+                    for (int u = 0; u < 4; ++u)
+                        o[u] = acc_big ? __builtin_nontemporal_load(dst + (r + u * L) * w4) + v[u] : v[u];
+#pragma unroll
+                    for (int u = 0; u < 4; ++u) __builtin_nontemporal_store(o[u], dst + (r + u * L) * w4);
+                }
+#pragma unroll
+                for (int u = 0; u < 4; ++u) s += (same ? o[u] : v[u]);
+            }
+            for (; r < r1; r += L) {
+                const f4 v = __builtin_nontemporal_load(src + r * w4);
+                f4 o = v;
+                if (dst) {
+                    o = acc_big ? __builtin_nontemporal_load(dst + r * w4) + v : v;
+                    __builtin_nontemporal_store(o, dst + r * w4);
+                }
+                s += (same ? o : v);
+            }
+        }
+        if (L > 1) {
+            lds[threadIdx.x] = s;
+            __syncthreads();
+            if (lane != 0) return;
+            for (int l = 1; l < L; ++l) s += lds[l * cw + col];
+        }
+        if (live) reinterpret_cast<f4*>(part + static_cast<int64_t>(blockIdx.y) * cols)[c4] = s;
+    } else {
+        const int64_t c = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
+        if (c >= cols) return;
+        float s = 0.0f;
+        for (int64_t r = r0; r < r1; ++r) {
+            const float v = dy[r * cols + c];
+            float o = v;
+            if (d_big) {
+                o = acc_big ? d_big[r * cols + c] + v : v;
+                d_big[r * cols + c] = o;
+            }
+            s += (same ? o : v);
+        }
+        part[static_cast<int64_t>(blockIdx.y) * cols + c] = s;
+    }
+}
+
+// The scalar broadcast (small_n == 1): the same over contiguous chunks of
+// `chunk` floats (a multiple of 4 * kBlock when VEC), one block each;
+// part[k] = the chunk's sum.
+template <bool VEC>
+__global__ __launch_bounds__(kBlock) void add_total_part(const float* dy, float* d_big, int acc_big, int64_t n,
+                                                         int64_t chunk, float* part) {
     __shared__ float lds[kBlock / kWave];
     const int64_t i0 = static_cast<int64_t>(blockIdx.x) * chunk;
     const int64_t i1 = i0 + chunk < n ? i0 + chunk : n;
+    const bool same = d_big == dy;
     float s = 0.0f;
-    for (int64_t i = i0 + threadIdx.x; i < i1; i += kBlock) s += dy[i];
+    if constexpr (VEC) {
+        const f4* src = reinterpret_cast<const f4*>(dy);
+        f4* dst = reinterpret_cast<f4*>(d_big);
+        const int64_t e4 = i1 / 4;
+        f4 acc = f4(0.0f);
+        int64_t i = i0 / 4 + threadIdx.x;
+        for (; i + 3 * kBlock < e4; i += 4 * kBlock) {
+            f4 v[4], o[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) v[u] = __builtin_nontemporal_load(src + i + u * kBlock);
+            if (dst) {
+#pragma unroll
+                for (int u = 0; u < 4; ++u)
+                    o[u] = acc_big ? __builtin_nontemporal_load(dst + i + u * kBlock) + v[u] : v[u];
+#pragma unroll
+                for (int u = 0; u < 4; ++u) __builtin_nontemporal_store(o[u], dst + i + u * kBlock);
+            }
+#pragma unroll
+            for (int u = 0; u < 4; ++u) acc += (same ? o[u] : v[u]);
+        }
+        for (; i < e4; i += kBlock) {
+            const f4 v = __builtin_nontemporal_load(src + i);
+            f4 o = v;
+            if (dst) {
+                o = acc_big ? __builtin_nontemporal_load(dst + i) + v : v;
+                __builtin_nontemporal_store(o, dst + i);
+            }
+            acc += (same ? o : v);
+        }
+        s = (acc.x + acc.y) + (acc.z + acc.w);
+        // The tail of n beyond the last multiple of 4 (last chunk only).
+        for (int64_t k = 4 * e4 + threadIdx.x; k < i1; k += kBlock) {
+            const float v = dy[k];
+            float o = v;
+            if (d_big) {
+                o = acc_big ? d_big[k] + v : v;
+                d_big[k] = o;
+            }
+            s += (same ? o : v);
+        }
+    } else {
+        for (int64_t i = i0 + threadIdx.x; i < i1; i += kBlock) {
+            const float v = dy[i];
+            float o = v;
+            if (d_big) {
+                o = acc_big ? d_big[i] + v : v;
+                d_big[i] = o;
+            }
+            s += (same ? o : v);
+        }
+    }
     s = block_sum<kBlock / kWave>(s, lds);
     if (threadIdx.x == 0) part[blockIdx.x] = s;
 }
 
-// Gradient of the broadcast operand of add_forward: the sum of dy over the
-// big operand's tiles (small_n > 1) or over all of it (small_n == 1).
-int add_small_grad(mimir_ctx* ctx, const float* dy, int64_t n_big, int64_t n_small, float* out, bool acc) {
+// Add backward with a broadcast operand (Model.cpp:7561-7594): d_big (+)= dy,
+// then d_small (+)= the sum of dy over the big operand's tiles (small_n > 1)
+// or over all of it (small_n == 1), in one pass over dy and a deterministic
+// sum of the per-chunk partial sums.
+int add_bcast_bwd(mimir_ctx* ctx, const float* dy, int64_t n_big, int64_t n_small, float* d_big, bool acc_big,
+                  float* d_small, bool acc_small) {
     if (n_small == 1) {
-        const int64_t chunk = 16384;
+        const bool vec = aligned16(dy) && (!d_big || aligned16(d_big));
+        const int64_t chunk = 16 * 4 * kBlock;  // 16 KiB floats per block
         const int64_t nchunks = (n_big + chunk - 1) / chunk;
         void* s = nullptr;
         if (int st = ensure_scratch(ctx, sizeof(float) * static_cast<size_t>(nchunks), &s)) return st;
         unsigned blocks;
         if (!grid_for(nchunks, 1, &blocks)) return fail(ctx, MIMIR_EINVAL, "Add backward: operand too large");
-        total_part<<<blocks, kBlock, 0, ctx->stream>>>(dy, n_big, chunk, static_cast<float*>(s));
-        if (int st = launched(ctx, "total_part")) return st;
-        return launch_sum_slots(ctx, static_cast<float*>(s), nchunks, 1, 1, out, out, 1, acc);
+        if (vec) add_total_part<true><<<blocks, kBlock, 0, ctx->stream>>>(dy, d_big, acc_big, n_big, chunk,
+                                                                         static_cast<float*>(s));
+        else add_total_part<false><<<blocks, kBlock, 0, ctx->stream>>>(dy, d_big, acc_big, n_big, chunk,
+                                                                      static_cast<float*>(s));
+        if (int st = launched(ctx, "add_total_part")) return st;
+        return launch_sum_slots(ctx, static_cast<float*>(s), nchunks, 1, 1, d_small, d_small, 1, acc_small);
     }
     const int64_t rows = n_big / n_small;
-    // About 1024 workgroups over (columns x row chunks), chunks of at least 8 rows.
-    const int64_t cblocks = (n_small + kBlock - 1) / kBlock;
+    const bool vec = n_small % 4 == 0 && aligned16(dy) && (!d_big || aligned16(d_big));
+    // About 1024 workgroups over (column blocks x row chunks), chunks of at
+    // least 8 rows: partial sums stay a few percent of dy.
+    const int64_t cw = vec ? bcast_cols_per_block(n_small / 4) : kBlock;
+    const int64_t lanes = vec ? kBlock / cw : 1;
+    const int64_t cblocks = ((vec ? n_small / 4 : n_small) + cw - 1) / cw;
     int64_t nchunks = (1024 + cblocks - 1) / cblocks;
-    if (nchunks > rows / 8) nchunks = rows / 8;
+    if (nchunks > rows / (8 * lanes)) nchunks = rows / (8 * lanes);
     if (nchunks < 1) nchunks = 1;
     if (nchunks > 65535) nchunks = 65535;
     const int64_t chunk = (rows + nchunks - 1) / nchunks;
     nchunks = (rows + chunk - 1) / chunk;
-    void* s = nullptr;
-    if (int st = ensure_scratch(ctx, sizeof(float) * static_cast<size_t>(nchunks * n_small), &s)) return st;
     if (cblocks > 0x7fffffffLL) return fail(ctx, MIMIR_EINVAL, "Add backward: operand too large");
-    colsum_part<<<dim3(static_cast<unsigned>(cblocks), static_cast<unsigned>(nchunks)), kBlock, 0, ctx->stream>>>(
-        dy, rows, n_small, chunk, static_cast<float*>(s));
-    if (int st = launched(ctx, "colsum_part")) return st;
-    return launch_sum_slots(ctx, static_cast<float*>(s), nchunks, n_small, n_small, out, out, n_small, acc);
+    void* s = nullptr;
+    const size_t part_floats = static_cast<size_t>((nchunks + kGroups) * n_small);
+    if (int st = ensure_scratch(ctx, sizeof(float) * part_floats, &s)) return st;
+    float* part = static_cast<float*>(s);
+    const dim3 grid(static_cast<unsigned>(cblocks), static_cast<unsigned>(nchunks));
+    if (vec) add_bcast_part<true><<<grid, kBlock, 0, ctx->stream>>>(dy, d_big, acc_big, rows, n_small, chunk, part);
+    else add_bcast_part<false><<<grid, kBlock, 0, ctx->stream>>>(dy, d_big, acc_big, rows, n_small, chunk, part);
+    if (int st = launched(ctx, "add_bcast_part")) return st;
+    return launch_sum_slots(ctx, part, nchunks, n_small, n_small, d_small, d_small, n_small, acc_small,
+                            part + nchunks * n_small);
 }
 
 // ---------------------------------------------------------------------------
@@ -1024,10 +1184,9 @@ int mimir_add_bwd(mimir_ctx* ctx, const float* dy, int64_t na, int64_t nb, float
     float* d_big = a_big ? da : db;
     float* d_small = a_big ? db : da;
     MIMIR_ENTER(ctx);
-    if (d_big)  // :7577
-        if (int st = accumulate(ctx, dy, d_big, big_n, a_big ? A : B, "add_bwd")) return st;
-    if (d_small)  // :7580-7594, reading dy after the big operand's accumulation
-        return add_small_grad(ctx, dy, big_n, small_n, d_small, a_big ? B : A);
+    if (d_small)  // :7577 then :7580-7594, in one pass over dy
+        return add_bcast_bwd(ctx, dy, big_n, small_n, d_big, a_big ? A : B, d_small, a_big ? B : A);
+    if (d_big) return accumulate(ctx, dy, d_big, big_n, a_big ? A : B, "add_bwd");
     return MIMIR_OK;
 }
 
