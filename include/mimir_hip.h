@@ -304,6 +304,9 @@ typedef struct mimir_layer {
     int32_t embed_dim;
     int32_t padding_idx;
     int32_t seq_len;
+    float* grad_weights;        /* DEVICE, weights_len floats, or NULL: the layer's
+                                   Layer::grad_weights for mimir_store_backward
+                                   (added to, as the reference adds into it) */
 } mimir_layer;
 
 int mimir_store_create(mimir_ctx* ctx, mimir_store** out);
@@ -331,6 +334,35 @@ int mimir_store_set_inputs(mimir_store* store, const char* const* fnames, const 
  * under layer.output or "x".  Errors where the reference throws: EINVAL with
  * the message, e.g. "Missing input tensor: <name>". */
 int mimir_store_run(mimir_store* store, const mimir_layer* layers, int32_t n_layers);
+
+/* mimir_store_run with the reference's training bookkeeping (forwardPassView
+ * with training=true, Model.cpp:4723-4878): each layer's inputs are kept for
+ * mimir_store_backward.  The store never writes a tensor in place, so the
+ * snapshots are references to its buffers, not copies.  Dropout is refused
+ * (its training form draws a random mask).  The snapshots live until the
+ * next run, set_inputs or clear. */
+int mimir_store_run_training(mimir_store* store, const mimir_layer* layers, int32_t n_layers);
+
+/* Model::backwardPass(loss_gradient), Model.cpp:7307-9153, over the layers of
+ * the last mimir_store_run_training (the same array): the gradient map starts
+ * as {"x": loss_grad} (n_grad host floats) and each layer, last to first,
+ * routes its output's gradient to its inputs with the branches of the
+ * mimir_*_bwd entry points and accumulate_grad's copy-or-add (an input named
+ * like the output adds onto that same gradient, as in the reference).
+ * Layer parameter gradients are added into layers[i].grad_weights (skipped
+ * when NULL).  Layers whose types have no backward branch in the reference
+ * (RMSNorm, Softmax, LogSoftmax) pass the gradient through when the sizes
+ * match, as its fallback does (:9133-9140); shape mismatches that the
+ * reference skips with a warning are skipped. */
+int mimir_store_backward(mimir_store* store, const mimir_layer* layers, int32_t n_layers, const float* loss_grad,
+                         int64_t n_grad);
+
+/* A gradient of the last mimir_store_backward by tensor name ("__input__"
+ * for Model::getLastInputGradient): device pointer and size, or a download
+ * of at most cap floats (*n = its size).  EINVAL when no gradient reached
+ * that name. */
+int mimir_store_grad_info(mimir_store* store, const char* name, void** dptr, int64_t* n);
+int mimir_store_grad_get(mimir_store* store, const char* name, float* host, int64_t cap, int64_t* n);
 
 #ifdef __cplusplus
 }

@@ -13,6 +13,13 @@
 //     layer can be reused by a later layer in stream order with no sync.
 // The routing follows Model::forwardPassView (Model.cpp:4621-6824): see
 // mimir_store_set_inputs / mimir_store_run in include/mimir_hip.h.
+//
+// Training (mimir_store_run_training + mimir_store_backward) mirrors
+// forwardPassView(training=true) and Model::backwardPass (Model.cpp:
+// 7307-9153): the forward keeps each layer's input buffers by reference
+// (nothing is copied: no buffer is ever written in place), and the backward
+// routes gradients through a name -> buffer map with accumulate_grad's
+// copy-or-add, calling the backward kernels (backward.hip) for each branch.
 #include "common.hpp"
 #include "internal.hpp"
 
@@ -45,10 +52,21 @@ __global__ __launch_bounds__(kBlock) void fill_i32_kernel(int32_t* dst, int64_t 
 
 }  // namespace
 
+// A layer's inputs as a training forward saw them (forwardPassView's
+// layer_inputs_multi / layer_input_sizes_multi, Model.cpp:4858-4878): the
+// buffers are held by reference (the store never writes one in place).
+struct Snap {
+    std::vector<Slot> vals;    // empty for Add / Identity (sizes only, :4757-4766)
+    std::vector<bool> ids_i32;  // Embedding ids read from the int store
+    std::vector<int64_t> sizes;
+};
+
 struct mimir_store {
     mimir_ctx* ctx = nullptr;
     std::unordered_map<std::string, Slot> f32;
     std::unordered_map<std::string, Slot> i32;
+    std::vector<Snap> snaps;                      // last mimir_store_run_training
+    std::unordered_map<std::string, Slot> grads;  // last mimir_store_backward
     std::vector<std::unique_ptr<Buf>> bufs;
     std::multimap<size_t, Buf*> free_bufs;  // capacity -> idle buffer
 
@@ -96,11 +114,24 @@ struct mimir_store {
         if (b && b->refs == 0) free_bufs.emplace(b->cap, b);
     }
 
+    void release_snaps() {
+        for (auto& sn : snaps)
+            for (auto& v : sn.vals) release(v.buf);
+        snaps.clear();
+    }
+
+    void release_grads() {
+        for (auto& kv : grads) release(kv.second.buf);
+        grads.clear();
+    }
+
     void clear() {
         for (auto& kv : f32) release(kv.second.buf);
         for (auto& kv : i32) release(kv.second.buf);
         f32.clear();
         i32.clear();
+        release_snaps();
+        release_grads();
     }
 };
 
@@ -123,8 +154,9 @@ int put_host(mimir_store* s, int dtype, const std::string& name, const void* hos
 
 const char* layer_name(const mimir_layer& L) { return L.name ? L.name : "?"; }
 
-// One layer of Model::forwardPassView's loop (Model.cpp:4795-6680), inference.
-int run_layer(mimir_store* s, const mimir_layer& L) {
+// One layer of Model::forwardPassView's loop (Model.cpp:4795-6680); with
+// `snap`, the training form that keeps the layer's inputs.
+int run_layer(mimir_store* s, const mimir_layer& L, Snap* snap) {
     mimir_ctx* ctx = s->ctx;
     static const char* const kDefaultInput[] = {"x"};
     const char* const* names = L.n_inputs > 0 ? L.inputs : kDefaultInput;
@@ -138,6 +170,7 @@ int run_layer(mimir_store* s, const mimir_layer& L) {
         const void* p;
         int64_t n;
         bool ids_i32;
+        Buf* buf;
     };
     std::vector<In> in;
     in.reserve(n_in);
@@ -145,7 +178,7 @@ int run_layer(mimir_store* s, const mimir_layer& L) {
         const std::string name = names[k] ? names[k] : "";
         auto itf = s->f32.find(name);
         if (itf != s->f32.end()) {
-            in.push_back(In{itf->second.buf->p, itf->second.n, false});
+            in.push_back(In{itf->second.buf->p, itf->second.n, false, itf->second.buf});
             continue;
         }
         if (L.type == MIMIR_LAYER_EMBEDDING && k == 0) {
@@ -164,13 +197,27 @@ int run_layer(mimir_store* s, const mimir_layer& L) {
                 s->bind(MIMIR_DTYPE_I32, name, b, len);
                 iti = s->i32.find(name);
             }
-            in.push_back(In{iti->second.buf->p, iti->second.n, true});
+            in.push_back(In{iti->second.buf->p, iti->second.n, true, iti->second.buf});
             continue;
         }
         return fail(ctx, MIMIR_EINVAL, "Missing input tensor: %s (layer %s)", name.c_str(), layer_name(L));
     }
     const int64_t N = in[0].n;
     const float* x = static_cast<const float*>(in[0].p);
+
+    if (snap) {  // Model.cpp:4858-4878
+        if (L.type == MIMIR_LAYER_DROPOUT)
+            return fail(ctx, MIMIR_EINVAL, "Dropout (layer %s): its training form draws a random mask, which is "
+                        "not on this path", layer_name(L));
+        for (const In& v : in) snap->sizes.push_back(v.n);
+        if (L.type != MIMIR_LAYER_ADD && L.type != MIMIR_LAYER_IDENTITY) {
+            for (const In& v : in) {
+                ++v.buf->refs;
+                snap->vals.push_back(Slot{v.buf, v.n});
+                snap->ids_i32.push_back(v.ids_i32);
+            }
+        }
+    }
 
     // Identity / inference Dropout: the output name shares the input buffer.
     if (L.type == MIMIR_LAYER_IDENTITY || L.type == MIMIR_LAYER_DROPOUT) {
@@ -271,6 +318,132 @@ int run_layer(mimir_store* s, const mimir_layer& L) {
     }
     s->bind(MIMIR_DTYPE_F32, out_name, ob, out_n);  // STORE OUTPUT, Model.cpp:6655,6674
     return MIMIR_OK;
+}
+
+// accumulate_grad's destination (Model.cpp:7329-7341): the gradient of
+// `name`, present (acc: add onto it) or new (written by the first
+// contribution).  A present gradient of another size is the reference's
+// "Gradient accumulate: size mismatch".
+int grad_dst(mimir_store* s, const std::string& name, int64_t n, float** out, int* acc) {
+    auto it = s->grads.find(name);
+    if (it != s->grads.end() && it->second.n > 0) {
+        if (it->second.n != n)
+            return fail(s->ctx, MIMIR_EINVAL, "Gradient accumulate: size mismatch (%s: %lld vs %lld)", name.c_str(),
+                        (long long)it->second.n, (long long)n);
+        *out = static_cast<float*>(it->second.buf->p);
+        *acc = 1;
+        return MIMIR_OK;
+    }
+    Buf* b = nullptr;
+    if (int st = s->acquire(static_cast<size_t>(n) * 4, &b)) return st;
+    ++b->refs;
+    if (it != s->grads.end()) {
+        s->release(it->second.buf);
+        it->second = Slot{b, n};
+    } else {
+        s->grads.emplace(name, Slot{b, n});
+    }
+    *out = static_cast<float*>(b->p);
+    *acc = 0;
+    return MIMIR_OK;
+}
+
+// accumulate_grad(grad_store[name], g) for a whole gradient g (Identity, the
+// pass-through fallback); when name's gradient is g itself it doubles, as the
+// reference's in-place add of a vector onto itself does.
+int grad_pass(mimir_store* s, const std::string& name, const float* g, int64_t n) {
+    float* d = nullptr;
+    int acc = 0;
+    if (int st = grad_dst(s, name, n, &d, &acc)) return st;
+    return mimir_add_bwd(s->ctx, g, n, n, d, nullptr, acc, 0);
+}
+
+// One layer of Model::backwardPass (Model.cpp:7349-9141).
+int backward_layer(mimir_store* s, const mimir_layer& L, const Snap& sn) {
+    mimir_ctx* ctx = s->ctx;
+    const std::string out_name = (L.output && *L.output) ? L.output : "x";
+    auto it = s->grads.find(out_name);
+    if (it == s->grads.end()) return MIMIR_OK;  // :7352-7356
+    const Slot go = it->second;
+    const float* g = static_cast<const float*>(go.buf->p);
+    const int64_t gn = go.n;
+    if (gn == 0) return MIMIR_OK;
+    static const char* const kDefaultInput[] = {"x"};
+    const char* const* names = L.n_inputs > 0 ? L.inputs : kDefaultInput;
+    auto nm = [&](int k) { return std::string(names[k] ? names[k] : ""); };
+    const int64_t n0 = sn.sizes.empty() ? 0 : sn.sizes[0];
+    float* d0 = nullptr;
+    float* d1 = nullptr;
+    int a0 = 0, a1 = 0;
+    switch (L.type) {
+        case MIMIR_LAYER_EMBEDDING: {  // :7429-7461
+            if (sn.vals.empty()) return MIMIR_OK;
+            const int64_t vocab = L.vocab_size > 1 ? L.vocab_size : 1;
+            const int64_t dim = L.embed_dim > 1 ? L.embed_dim : 1;
+            const Slot& ids = sn.vals[0];
+            if (gn != ids.n * dim) return MIMIR_OK;                               // shape mismatch: skipped
+            if (!L.weights || L.weights_len < vocab * dim) return MIMIR_OK;       // weights invalid: skipped
+            if (!L.grad_weights) return MIMIR_OK;
+            return embedding_bwd_launch(ctx, ids.buf->p, sn.ids_i32[0] ? kIdsI32AsF32 : kIdsF32, ids.n, g,
+                                        L.grad_weights, L.weights_len, L.vocab_size, L.embed_dim, L.padding_idx);
+        }
+        case MIMIR_LAYER_IDENTITY:  // :7463-7468
+            if (gn != n0) return MIMIR_OK;
+            return grad_pass(s, nm(0), g, gn);
+        case MIMIR_LAYER_ADD: {  // :7541-7601
+            if (sn.sizes.size() < 2 || L.n_inputs < 2) return MIMIR_OK;
+            const int64_t n1 = sn.sizes[1];
+            if (gn == n0 && gn == n1) {
+                if (int st = grad_dst(s, nm(0), gn, &d0, &a0)) return st;
+                if (int st = grad_dst(s, nm(1), gn, &d1, &a1)) return st;
+                return mimir_add_bwd(ctx, g, gn, gn, d0, d1, a0, a1);
+            }
+            if (gn != n0 && gn != n1) return MIMIR_OK;
+            const int big = gn == n0 ? 0 : 1;
+            const int64_t small_n = big == 0 ? n1 : n0;
+            if (int st = grad_dst(s, nm(big), gn, &d0, &a0)) return st;
+            if (!(small_n == 1 || (small_n > 1 && gn % small_n == 0)))  // :7595-7599, after the big one's gradient
+                return mimir_add_bwd(ctx, g, gn, gn, d0, nullptr, a0, 0);
+            if (int st = grad_dst(s, nm(1 - big), small_n, &d1, &a1)) return st;
+            return big == 0 ? mimir_add_bwd(ctx, g, gn, small_n, d0, d1, a0, a1)
+                            : mimir_add_bwd(ctx, g, small_n, gn, d1, d0, a1, a0);
+        }
+        case MIMIR_LAYER_MULTIPLY: {  // :7647-7665
+            if (sn.vals.size() < 2) return MIMIR_OK;
+            if (gn != sn.vals[0].n || gn != sn.vals[1].n) return MIMIR_OK;
+            if (int st = grad_dst(s, nm(0), gn, &d0, &a0)) return st;
+            if (int st = grad_dst(s, nm(1), gn, &d1, &a1)) return st;
+            return mimir_mul_bwd(ctx, static_cast<const float*>(sn.vals[0].buf->p),
+                                 static_cast<const float*>(sn.vals[1].buf->p), g, d0, d1, gn, a0, a1);
+        }
+        case MIMIR_LAYER_LAYERNORM: {  // :7719-7821
+            if (sn.vals.empty()) return MIMIR_OK;
+            const Slot& x = sn.vals[0];
+            if (gn != x.n) return MIMIR_OK;
+            const int64_t N = x.n;
+            const int64_t feat = L.in_features > 0 ? L.in_features : N;
+            if (feat <= 0 || N % feat != 0) return MIMIR_OK;
+            const bool affine = L.affine != 0;
+            const bool has_bias = affine && L.use_bias;
+            if (affine && (!L.weights || L.weights_len < feat * (has_bias ? 2 : 1))) return MIMIR_OK;
+            if (int st = grad_dst(s, nm(0), N, &d0, &a0)) return st;
+            float* dg = (affine && L.grad_weights) ? L.grad_weights : nullptr;
+            float* db = (has_bias && dg) ? L.grad_weights + feat : nullptr;
+            return mimir_layernorm_bwd(ctx, static_cast<const float*>(x.buf->p), g, affine ? L.weights : nullptr, d0,
+                                       dg, db, N / feat, feat, L.eps, a0);
+        }
+        case MIMIR_LAYER_GELU:  // :9026-9051
+        case MIMIR_LAYER_SILU: {  // :7993-8032
+            if (sn.vals.empty() || gn != sn.vals[0].n) return MIMIR_OK;
+            if (int st = grad_dst(s, nm(0), gn, &d0, &a0)) return st;
+            const float* x = static_cast<const float*>(sn.vals[0].buf->p);
+            return L.type == MIMIR_LAYER_GELU ? mimir_gelu_bwd(ctx, x, g, d0, gn, a0)
+                                              : mimir_silu_bwd(ctx, x, g, d0, gn, a0);
+        }
+        default:  // RMSNorm, Softmax, LogSoftmax: the fallback at :9133-9140
+            if (gn != n0) return MIMIR_OK;
+            return grad_pass(s, nm(0), g, gn);
+    }
 }
 
 }  // namespace
@@ -382,8 +555,71 @@ int mimir_store_set_inputs(mimir_store* s, const char* const* fnames, const floa
 int mimir_store_run(mimir_store* s, const mimir_layer* layers, int32_t n_layers) {
     if (!s) return MIMIR_EINVAL;
     MIMIR_REQUIRE(s->ctx, n_layers >= 0 && (n_layers == 0 || layers), "mimir_store_run: invalid argument");
+    s->release_snaps();
     for (int32_t i = 0; i < n_layers; ++i)
-        if (int st = run_layer(s, layers[i])) return st;
+        if (int st = run_layer(s, layers[i], nullptr)) return st;
+    return MIMIR_OK;
+}
+
+int mimir_store_run_training(mimir_store* s, const mimir_layer* layers, int32_t n_layers) {
+    if (!s) return MIMIR_EINVAL;
+    MIMIR_REQUIRE(s->ctx, n_layers >= 0 && (n_layers == 0 || layers), "mimir_store_run_training: invalid argument");
+    s->release_snaps();
+    s->snaps.resize(static_cast<size_t>(n_layers));
+    for (int32_t i = 0; i < n_layers; ++i) {
+        if (int st = run_layer(s, layers[i], &s->snaps[i])) {
+            s->release_snaps();
+            return st;
+        }
+    }
+    return MIMIR_OK;
+}
+
+int mimir_store_backward(mimir_store* s, const mimir_layer* layers, int32_t n_layers, const float* loss_grad,
+                         int64_t n_grad) {
+    if (!s) return MIMIR_EINVAL;
+    MIMIR_REQUIRE(s->ctx, n_layers >= 0 && (n_layers == 0 || layers) && n_grad >= 0 && (n_grad == 0 || loss_grad),
+                  "mimir_store_backward: invalid argument");
+    // Model.cpp:7313-7317: a backward needs the training forward's state.
+    MIMIR_REQUIRE(s->ctx, static_cast<size_t>(n_layers) == s->snaps.size(),
+                  "mimir_store_backward: no training forward of these %d layers (run_training first)", n_layers);
+    s->release_grads();
+    Buf* b = nullptr;  // grad_store["x"] = loss_gradient (:7346)
+    if (int st = s->acquire(static_cast<size_t>(n_grad) * 4, &b)) return st;
+    if (n_grad > 0) {
+        if (int st = mimir_upload(s->ctx, b->p, loss_grad, static_cast<size_t>(n_grad) * 4)) {
+            s->discard(b);
+            return st;
+        }
+    }
+    ++b->refs;
+    s->grads.emplace("x", Slot{b, n_grad});
+    for (int32_t i = n_layers - 1; i >= 0; --i)
+        if (int st = backward_layer(s, layers[i], s->snaps[i])) return st;
+    return MIMIR_OK;
+}
+
+int mimir_store_grad_info(mimir_store* s, const char* name, void** dptr, int64_t* n) {
+    if (!s) return MIMIR_EINVAL;
+    MIMIR_REQUIRE(s->ctx, name && dptr && n, "mimir_store_grad_info: invalid argument");
+    auto it = s->grads.find(name);
+    MIMIR_REQUIRE(s->ctx, it != s->grads.end(), "mimir_store_grad_info: no gradient reached %s", name);
+    *dptr = it->second.buf->p;
+    *n = it->second.n;
+    return MIMIR_OK;
+}
+
+int mimir_store_grad_get(mimir_store* s, const char* name, float* host, int64_t cap, int64_t* n) {
+    if (!s) return MIMIR_EINVAL;
+    MIMIR_REQUIRE(s->ctx, name && n && cap >= 0, "mimir_store_grad_get: invalid argument");
+    auto it = s->grads.find(name);
+    MIMIR_REQUIRE(s->ctx, it != s->grads.end(), "mimir_store_grad_get: no gradient reached %s", name);
+    *n = it->second.n;
+    const int64_t k = cap < it->second.n ? cap : it->second.n;
+    if (k > 0) {
+        MIMIR_REQUIRE(s->ctx, host, "mimir_store_grad_get: null host buffer");
+        return mimir_download(s->ctx, host, it->second.buf->p, static_cast<size_t>(k) * 4);
+    }
     return MIMIR_OK;
 }
 

@@ -32,7 +32,7 @@ class Layer_C(Structure):
                 ("n_inputs", c_int32), ("output", c_char_p), ("weights", c_void_p),
                 ("weights_len", c_int64), ("eps", c_float), ("affine", c_int32), ("use_bias", c_int32),
                 ("in_features", c_int32), ("vocab_size", c_int32), ("embed_dim", c_int32),
-                ("padding_idx", c_int32), ("seq_len", c_int32)]
+                ("padding_idx", c_int32), ("seq_len", c_int32), ("grad_weights", c_void_p)]
 
 
 # name -> (restype, argtypes); mirrors include/mimir_hip.h one to one.
@@ -86,6 +86,10 @@ SIGNATURES = {
     "mimir_store_set_inputs": (c_int, [_P, POINTER(c_char_p), POINTER(c_void_p), POINTER(c_int64), c_int32,
                                        POINTER(c_char_p), POINTER(c_void_p), POINTER(c_int64), c_int32]),
     "mimir_store_run": (c_int, [_P, POINTER(Layer_C), c_int32]),
+    "mimir_store_run_training": (c_int, [_P, POINTER(Layer_C), c_int32]),
+    "mimir_store_backward": (c_int, [_P, POINTER(Layer_C), c_int32, _P, c_int64]),
+    "mimir_store_grad_info": (c_int, [_P, c_char_p, _PP, POINTER(c_int64)]),
+    "mimir_store_grad_get": (c_int, [_P, c_char_p, _P, c_int64, POINTER(c_int64)]),
 }
 
 _lib = None

@@ -314,6 +314,36 @@ class Store:
     def run(self, graph: "DeviceGraph"):
         self.ctx.check(self.ctx.lib.mimir_store_run(self.handle, graph.c_layers, len(graph.layers)))
 
+    def run_training(self, graph: "DeviceGraph"):
+        self.ctx.check(self.ctx.lib.mimir_store_run_training(self.handle, graph.c_layers, len(graph.layers)))
+
+    def backward(self, graph: "DeviceGraph", loss_grad):
+        g = np.ascontiguousarray(loss_grad, np.float32).ravel()
+        self.ctx.check(self.ctx.lib.mimir_store_backward(self.handle, graph.c_layers, len(graph.layers),
+                                                         g.ctypes.data_as(c_void_p), g.size))
+
+    def grad(self, name):
+        """The gradient that reached `name` in the last backward, or None."""
+        p, n = c_void_p(), ctypes.c_int64()
+        st = self.ctx.lib.mimir_store_grad_info(self.handle, name.encode(), byref(p), byref(n))
+        if st != 0:
+            return None
+        out = np.empty(n.value, np.float32)
+        got = ctypes.c_int64()
+        self.ctx.check(self.ctx.lib.mimir_store_grad_get(self.handle, name.encode(), out.ctypes.data_as(c_void_p),
+                                                         n.value, byref(got)))
+        return out
+
+    def train_step(self, graph: "DeviceGraph", fin, iin, loss_grad):
+        """Model::forwardPassNamed(training=true) then Model::backwardPass on
+        the device.  Returns (grads, input_grad): each layer's grad_weights
+        after the step (host copies, None for layers without weights) and the
+        gradient that reached "__input__" (None if none did)."""
+        self.set_inputs(fin, iin)
+        self.run_training(graph)
+        self.backward(graph, loss_grad)
+        return graph.grads(), self.grad("__input__")
+
     def forward_named(self, graph: "DeviceGraph", fin=None, iin=None):
         """Model::forwardPassNamed(fin, iin, training=false) on the device."""
         self.set_inputs(fin, iin)
@@ -323,20 +353,24 @@ class Store:
 
 class DeviceGraph:
     """A layer list (dicts with the reference Layer fields and host `weights`)
-    with its weight blocks uploaded once to the device."""
+    with its weight blocks uploaded once to the device, and a zeroed device
+    gradient block (Layer::grad_weights) per weighted layer."""
 
     def __init__(self, ctx: Context, layers):
         self.ctx = ctx
         self.layers = list(layers)
         self._keep = []
         self.weights = []
+        self.grad_bufs = []
         arr = (_lib.Layer_C * max(1, len(self.layers)))()
         for i, L in enumerate(self.layers):
             w = L.get("weights")
-            dw = None
+            dw = dg = None
             if w is not None and np.asarray(w).size > 0:
                 dw = ctx.to_device(np.ascontiguousarray(w, np.float32).ravel())
+                dg = ctx.to_device(np.zeros(dw.size, np.float32))
             self.weights.append(dw)
+            self.grad_bufs.append(dg)
             names = [n.encode() for n in L.get("inputs", [])]
             cnames = (ctypes.c_char_p * max(1, len(names)))(*names)
             name_b, out_b = L.get("name", "").encode(), L.get("output", "").encode()
@@ -346,11 +380,22 @@ class DeviceGraph:
                 dw.ptr if dw is not None else None, 0 if dw is None else dw.size,
                 float(L.get("eps", 1e-5)), int(L.get("affine", True)), int(L.get("use_bias", True)),
                 int(L.get("in_features", 0)), int(L.get("vocab_size", 0)), int(L.get("embed_dim", 0)),
-                int(L.get("padding_idx", -1)), int(L.get("seq_len", 0)))
+                int(L.get("padding_idx", -1)), int(L.get("seq_len", 0)),
+                dg.ptr if dg is not None else None)
         self.c_layers = arr
 
+    def grads(self):
+        """Host copies of the device grad_weights blocks (None where no weights)."""
+        return [None if d is None else d.numpy() for d in self.grad_bufs]
+
+    def zero_grads(self):
+        for d in self.grad_bufs:
+            if d is not None:
+                self.ctx.upload(d, np.zeros(d.size, np.float32))
+
     def close(self):
-        for d in self.weights:
+        for d in self.weights + self.grad_bufs:
             if d is not None:
                 d.free()
         self.weights = []
+        self.grad_bufs = []
