@@ -16,6 +16,7 @@
 //   mimir_hip::embedding_forward(_float_ids) Model.cpp:1152-1205 / 5301-5334 (inline there)
 //   mimir_hip::DeviceModel::forwardPassNamed Model.cpp:1352-1408, 4621-6824
 //                                            (device-resident TensorStore)
+//   mimir_hip::DeviceModel::backwardPass     Model.cpp:7307-9153
 //
 // The op templates take the reference's `Layer` (or anything with the same
 // fields: eps, affine, use_bias, in_features, vocab_size, embed_dim,
@@ -400,10 +401,12 @@ public:
         }
     }
 
+    // Model::forwardPassNamed (Model.cpp:1352-1408).  training=true keeps each
+    // layer's inputs on the device for backwardPass, as the reference's
+    // forward_state does (Dropout is then refused: its mask is random).
     std::vector<float> forwardPassNamed(const std::unordered_map<std::string, std::vector<float>>& fin,
                                         const std::unordered_map<std::string, std::vector<int>>& iin,
                                         bool training = false) {
-        if (training) throw std::runtime_error("DeviceModel: inference only (training=false)");
         std::vector<const char*> fn, in;
         std::vector<const float*> fd;
         std::vector<const int32_t*> id;
@@ -421,29 +424,12 @@ public:
         ctx_->check(mimir_store_set_inputs(store_, fn.data(), fd.data(), fs.data(), static_cast<int32_t>(fn.size()),
                                            in.data(), id.data(), is.data(), static_cast<int32_t>(in.size())),
                     "DeviceModel inputs");
-        std::vector<mimir_layer> ls(layers_->size());
-        std::vector<std::vector<const char*>> names(layers_->size());
-        for (size_t i = 0; i < layers_->size(); ++i) {
-            const LayerT& L = (*layers_)[i];
-            for (const auto& nm : L.inputs) names[i].push_back(nm.c_str());
-            mimir_layer& c = ls[i];
-            c.type = types_[i];
-            c.name = L.name.c_str();
-            c.inputs = names[i].data();
-            c.n_inputs = static_cast<int32_t>(names[i].size());
-            c.output = L.output.c_str();
-            c.weights = weights_[i].data();
-            c.weights_len = static_cast<int64_t>(weights_[i].size());
-            c.eps = L.eps;
-            c.affine = L.affine;
-            c.use_bias = L.use_bias;
-            c.in_features = L.in_features;
-            c.vocab_size = L.vocab_size;
-            c.embed_dim = L.embed_dim;
-            c.padding_idx = L.padding_idx;
-            c.seq_len = L.seq_len;
-        }
-        ctx_->check(mimir_store_run(store_, ls.data(), static_cast<int32_t>(ls.size())), "DeviceModel forward");
+        build_layers();
+        if (training)
+            ctx_->check(mimir_store_run_training(store_, ls_.data(), static_cast<int32_t>(ls_.size())),
+                        "DeviceModel forward (training)");
+        else
+            ctx_->check(mimir_store_run(store_, ls_.data(), static_cast<int32_t>(ls_.size())), "DeviceModel forward");
         int64_t n = 0;
         void* p = nullptr;
         ctx_->check(mimir_store_info(store_, "x", MIMIR_DTYPE_F32, &p, &n), "DeviceModel output");
@@ -451,6 +437,46 @@ public:
         ctx_->check(mimir_store_get(store_, "x", MIMIR_DTYPE_F32, out.data(), n, &n), "DeviceModel output");
         return out;
     }
+
+    // Model::backwardPass(loss_gradient) (Model.cpp:7307-9153) after a
+    // training forward.  Parameter gradients are added into the layers'
+    // grad_weights as the reference does (a vector of the wrong size is first
+    // reset to zeros, :7449-7451, :7751-7753), for the LayerNorm and Embedding
+    // layers whose branches produce them; the gradient that reached
+    // "__input__" is kept for getLastInputGradient().
+    void backwardPass(const std::vector<float>& loss_gradient, std::vector<LayerT>& layers) {
+        if (&layers != layers_ && layers.size() != layers_->size())
+            throw std::runtime_error("DeviceModel::backwardPass: not the model's layer list");
+        grads_.clear();
+        for (size_t i = 0; i < layers.size(); ++i) {
+            LayerT& L = layers[i];
+            const size_t wn = weights_[i].size();
+            if (wn && (types_[i] == MIMIR_LAYER_LAYERNORM || types_[i] == MIMIR_LAYER_EMBEDDING)) {
+                if (L.grad_weights.size() != wn) L.grad_weights.assign(wn, 0.0f);
+                grads_.emplace_back(*ctx_, L.grad_weights);
+            } else {
+                grads_.emplace_back(*ctx_, size_t(0));
+            }
+            ls_[i].grad_weights = grads_[i].size() ? grads_[i].data() : nullptr;
+        }
+        ctx_->check(mimir_store_backward(store_, ls_.data(), static_cast<int32_t>(ls_.size()), loss_gradient.data(),
+                                         static_cast<int64_t>(loss_gradient.size())),
+                    "DeviceModel backward");
+        for (size_t i = 0; i < layers.size(); ++i)
+            if (grads_[i].size()) layers[i].grad_weights = grads_[i].download();
+        has_input_grad_ = false;
+        input_grad_.clear();
+        void* p = nullptr;
+        int64_t n = 0;
+        if (mimir_store_grad_info(store_, "__input__", &p, &n) == MIMIR_OK) {
+            input_grad_.resize(static_cast<size_t>(n));
+            ctx_->check(mimir_store_grad_get(store_, "__input__", input_grad_.data(), n, &n), "DeviceModel input grad");
+            has_input_grad_ = true;
+        }
+    }
+
+    bool hasLastInputGradient() const { return has_input_grad_; }
+    const std::vector<float>& getLastInputGradient() const { return input_grad_; }
 
     mimir_store* store() const { return store_; }
 
@@ -467,11 +493,43 @@ private:
         return it == m.end() ? 0 : it->second;
     }
 
+    // The C descriptors of the layer list (names point into *layers_).
+    void build_layers() {
+        ls_.assign(layers_->size(), mimir_layer{});
+        names_.assign(layers_->size(), {});
+        for (size_t i = 0; i < layers_->size(); ++i) {
+            const LayerT& L = (*layers_)[i];
+            for (const auto& nm : L.inputs) names_[i].push_back(nm.c_str());
+            mimir_layer& c = ls_[i];
+            c.type = types_[i];
+            c.name = L.name.c_str();
+            c.inputs = names_[i].data();
+            c.n_inputs = static_cast<int32_t>(names_[i].size());
+            c.output = L.output.c_str();
+            c.weights = weights_[i].data();
+            c.weights_len = static_cast<int64_t>(weights_[i].size());
+            c.eps = L.eps;
+            c.affine = L.affine;
+            c.use_bias = L.use_bias;
+            c.in_features = L.in_features;
+            c.vocab_size = L.vocab_size;
+            c.embed_dim = L.embed_dim;
+            c.padding_idx = L.padding_idx;
+            c.seq_len = L.seq_len;
+            c.grad_weights = nullptr;
+        }
+    }
+
     Context* ctx_;
     const std::vector<LayerT>* layers_;
     mimir_store* store_ = nullptr;
     std::vector<int> types_;
     std::vector<DeviceBuffer<float>> weights_;
+    std::vector<DeviceBuffer<float>> grads_;
+    std::vector<mimir_layer> ls_;
+    std::vector<std::vector<const char*>> names_;
+    bool has_input_grad_ = false;
+    std::vector<float> input_grad_;
 };
 
 }  // namespace mimir_hip

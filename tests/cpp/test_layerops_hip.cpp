@@ -32,6 +32,7 @@ struct TestLayer {
     int embed_dim = 0;
     int padding_idx = -1;
     std::vector<float> weights;
+    std::vector<float> grad_weights;
     const float* getWeights() const { return weights.data(); }
     size_t getWeightsSize() const { return weights.size(); }
 };
@@ -266,6 +267,58 @@ int main() {
             e = me.forwardPassNamed({}, {});  // missing ids -> seq_len padding ids -> zeros
             CHECK(e.size() == 20);
             for (float v : e) CHECK_NEAR(v, 0.0f, 1e-6f);
+        }
+        // Training step: DeviceModel::forwardPassNamed(training=true) then
+        // backwardPass (Model.cpp:7307-9153), closed-form answers.
+        {
+            auto& c = mimir_hip::Context::instance();
+            // d(__input__) of x = __input__ * c is loss * c (Multiply branch, :7647-7665).
+            std::vector<TestLayer> mul(1);
+            mul[0].name = "m";
+            mul[0].type = "Multiply";
+            mul[0].inputs = {"__input__", "c"};
+            mul[0].output = "x";
+            mimir_hip::DeviceModel<TestLayer> mm(c, mul);
+            mm.forwardPassNamed({{"__input__", {1, 2}}, {"c", {3, 4}}}, {}, true);
+            mm.backwardPass({1, 1}, mul);
+            CHECK(mm.hasLastInputGradient());
+            CHECK(mm.getLastInputGradient() == std::vector<float>({3, 4}));
+            // LayerNorm over [1, 3]: xhat = [-1, 1] (up to eps), loss [1, 2]:
+            // dgamma = loss * xhat, dbeta = loss, dx = 0 (:7719-7821).
+            std::vector<TestLayer> ln(1);
+            ln[0].name = "ln";
+            ln[0].type = "LayerNorm";
+            ln[0].inputs = {"__input__"};
+            ln[0].output = "x";
+            ln[0].in_features = 2;
+            ln[0].weights = {1, 1, 0, 0};
+            mimir_hip::DeviceModel<TestLayer> ml(c, ln);
+            ml.forwardPassNamed({{"__input__", {1, 3}}}, {}, true);
+            ml.backwardPass({1, 2}, ln);
+            CHECK(ln[0].grad_weights.size() == 4);
+            CHECK_NEAR(ln[0].grad_weights[0], -1.0f, 1e-4f);
+            CHECK_NEAR(ln[0].grad_weights[1], 2.0f, 1e-4f);
+            CHECK_NEAR(ln[0].grad_weights[2], 1.0f, 1e-6f);
+            CHECK_NEAR(ln[0].grad_weights[3], 2.0f, 1e-6f);
+            CHECK_NEAR(ml.getLastInputGradient()[0], 0.0f, 1e-5f);
+            CHECK_NEAR(ml.getLastInputGradient()[1], 0.0f, 1e-5f);
+            ml.forwardPassNamed({{"__input__", {1, 3}}}, {}, true);  // grad_weights accumulate across steps
+            ml.backwardPass({1, 2}, ln);
+            CHECK_NEAR(ln[0].grad_weights[3], 4.0f, 1e-6f);
+            // Embedding scatter-add (:7429-7461): ids [1, 0, 2, 1], padding 0, dim 2.
+            std::vector<TestLayer> emb(1);
+            emb[0].name = "emb";
+            emb[0].type = "Embedding";
+            emb[0].inputs = {"ids"};
+            emb[0].output = "x";
+            emb[0].vocab_size = 3;
+            emb[0].embed_dim = 2;
+            emb[0].padding_idx = 0;
+            emb[0].weights.assign(6, 0.5f);
+            mimir_hip::DeviceModel<TestLayer> me(c, emb);
+            me.forwardPassNamed({}, {{"ids", {1, 0, 2, 1}}}, true);
+            me.backwardPass({1, 2, 3, 4, 5, 6, 7, 8}, emb);
+            CHECK(emb[0].grad_weights == std::vector<float>({0, 0, 8, 10, 5, 6}));
         }
     } catch (const std::exception& e) {
         std::fprintf(stderr, "FAIL: unexpected exception: %s\n", e.what());
