@@ -364,6 +364,54 @@ int mimir_store_backward(mimir_store* store, const mimir_layer* layers, int32_t 
 int mimir_store_grad_info(mimir_store* store, const char* name, void** dptr, int64_t* n);
 int mimir_store_grad_get(mimir_store* store, const char* name, float* host, int64_t cap, int64_t* n);
 
+/* ---------------------------------------------------------------------------
+ * SafeTensors checkpoints read straight into device memory: the reference's
+ * Mimir::Serialization::load_checkpoint for the SafeTensors format
+ * (Serialization.hpp:114; SafeTensorsReader.cpp).  The header is parsed
+ * with the reference's checks; tensor bytes go from the file to HBM through
+ * pinned staging buffers on the context's stream (reads overlap the DMA).
+ * ------------------------------------------------------------------------- */
+typedef struct mimir_safetensors mimir_safetensors;
+
+/* dtype codes, the reference's DType (Serialization.hpp:29-36). */
+#define MIMIR_ST_F32 0
+#define MIMIR_ST_F16 1
+#define MIMIR_ST_I32 2
+#define MIMIR_ST_I16 3
+#define MIMIR_ST_U16 4
+#define MIMIR_ST_U8 5
+
+/* Open and parse the header (SafeTensorsReader::parse_header, :52-166):
+ * 8-byte little-endian length (0 < len <= 100 MiB), JSON object of entries
+ * {dtype, shape, data_offsets} plus "__metadata__"; EINVAL with the
+ * reference's message for a missing / unknown dtype, missing shape or
+ * data_offsets, bad offsets or (end - begin) != prod(shape) * dtype size.
+ * ctx may be NULL to inspect a file without a device (no reads then);
+ * mimir_safetensors_error reports the message in that case. */
+int mimir_safetensors_open(mimir_ctx* ctx, const char* path, mimir_safetensors** out);
+int mimir_safetensors_close(mimir_safetensors* f);
+/* Number of tensor entries (metadata excluded), -1 for NULL. */
+int64_t mimir_safetensors_count(const mimir_safetensors* f);
+/* Entry i: name (valid until close), dtype code, up to max_dims dims of its
+ * shape, the number of dims and its byte size. */
+int mimir_safetensors_entry(const mimir_safetensors* f, int64_t i, const char** name, int32_t* dtype,
+                            int64_t* shape, int32_t max_dims, int32_t* ndims, int64_t* nbytes);
+/* Index of the entry named `name`, or -1. */
+int64_t mimir_safetensors_find(const mimir_safetensors* f, const char* name);
+/* The last error of this file (also in mimir_last_error when it has a ctx);
+ * with f == NULL, the message of this thread's last failed open. */
+const char* mimir_safetensors_error(const mimir_safetensors* f);
+/* Copy tensor `name`'s bytes into device memory (SafeTensorsReader::
+ * load_tensor_data, :168-216); EINVAL if they exceed dst_bytes.  Returns
+ * once the data is on the device. */
+int mimir_safetensors_read(mimir_safetensors* f, const char* name, void* dst_device, size_t dst_bytes);
+/* The weight loop of SafeTensorsReader::apply_tensors_to_model (:263-317):
+ * for every layer with a weight block (weights != NULL, weights_len > 0),
+ * tensor "<name>/weights" must have weights_len elements and is copied into
+ * the layer's DEVICE weights; a missing tensor is skipped, or EINVAL
+ * ("Missing tensor in strict mode: ...") when strict. */
+int mimir_safetensors_load_layers(mimir_safetensors* f, const mimir_layer* layers, int32_t n_layers, int strict);
+
 #ifdef __cplusplus
 }
 #endif

@@ -22,6 +22,7 @@ _P = c_void_p
 _PP = POINTER(c_void_p)
 
 DTYPE_F32, DTYPE_I32 = 0, 1
+ST_DTYPES = {0: "F32", 1: "F16", 2: "I32", 3: "I16", 4: "U16", 5: "U8"}  # MIMIR_ST_*
 LAYER_TYPES = {"LayerNorm": 1, "RMSNorm": 2, "Softmax": 3, "LogSoftmax": 4, "GELU": 5, "SiLU": 6,
                "Add": 7, "Multiply": 8, "Embedding": 9, "Identity": 10, "Dropout": 11}
 
@@ -87,6 +88,15 @@ SIGNATURES = {
                                        POINTER(c_char_p), POINTER(c_void_p), POINTER(c_int64), c_int32]),
     "mimir_store_run": (c_int, [_P, POINTER(Layer_C), c_int32]),
     "mimir_store_run_training": (c_int, [_P, POINTER(Layer_C), c_int32]),
+    "mimir_safetensors_open": (c_int, [_P, c_char_p, _PP]),
+    "mimir_safetensors_close": (c_int, [_P]),
+    "mimir_safetensors_count": (c_int64, [_P]),
+    "mimir_safetensors_entry": (c_int, [_P, c_int64, POINTER(c_char_p), POINTER(c_int32), POINTER(c_int64), c_int32,
+                                        POINTER(c_int32), POINTER(c_int64)]),
+    "mimir_safetensors_find": (c_int64, [_P, c_char_p]),
+    "mimir_safetensors_error": (c_char_p, [_P]),
+    "mimir_safetensors_read": (c_int, [_P, c_char_p, _P, c_size_t]),
+    "mimir_safetensors_load_layers": (c_int, [_P, POINTER(Layer_C), c_int32, c_int]),
     "mimir_store_backward": (c_int, [_P, POINTER(Layer_C), c_int32, _P, c_int64]),
     "mimir_store_grad_info": (c_int, [_P, c_char_p, _PP, POINTER(c_int64)]),
     "mimir_store_grad_get": (c_int, [_P, c_char_p, _P, c_int64, POINTER(c_int64)]),

@@ -399,3 +399,54 @@ class DeviceGraph:
                 d.free()
         self.weights = []
         self.grad_bufs = []
+
+
+class SafeTensors:
+    """A SafeTensors checkpoint (mimir_safetensors_*): header parsed on open
+    with the reference's checks; tensors read straight into device memory.
+    ctx may be None to inspect a file on a machine without a GPU."""
+
+    def __init__(self, ctx, path):
+        self.ctx = ctx
+        self.lib = _lib.load()
+        h = c_void_p()
+        st = self.lib.mimir_safetensors_open(ctx.handle if ctx is not None else None, str(path).encode(), byref(h))
+        if st != 0:
+            msg = self.lib.mimir_safetensors_error(None)
+            raise MimirError(st, (msg.decode() if msg else "") or f"cannot open {path}")
+        self.handle = h
+
+    def close(self):
+        if self.handle:
+            self.lib.mimir_safetensors_close(self.handle)
+            self.handle = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def entries(self):
+        """{name: (dtype string, shape tuple, nbytes)} in file order."""
+        out = {}
+        for i in range(self.lib.mimir_safetensors_count(self.handle)):
+            name = ctypes.c_char_p()
+            dt = ctypes.c_int32()
+            shape = (ctypes.c_int64 * 16)()
+            nd = ctypes.c_int32()
+            nb = ctypes.c_int64()
+            if self.lib.mimir_safetensors_entry(self.handle, i, byref(name), byref(dt), shape, 16, byref(nd),
+                                                byref(nb)) != 0:
+                raise MimirError(1, "mimir_safetensors_entry failed")
+            out[name.value.decode()] = (_lib.ST_DTYPES[dt.value], tuple(shape[k] for k in range(nd.value)), nb.value)
+        return out
+
+    def read(self, name, dst):
+        """Copy tensor `name` into the DeviceArray `dst` (its bytes as stored)."""
+        self.ctx.check(self.lib.mimir_safetensors_read(self.handle, name.encode(), _ptr(dst), dst.nbytes))
+
+    def load_graph(self, graph: "DeviceGraph", strict=False):
+        """apply_tensors_to_model's weight loop into the graph's device weights."""
+        self.ctx.check(self.lib.mimir_safetensors_load_layers(self.handle, graph.c_layers, len(graph.layers),
+                                                              int(bool(strict))))

@@ -48,6 +48,12 @@ def _load():
                       c_void_p, c_int64, POINTER(c_void_p), c_void_p, c_int64, POINTER(c_int64),
                       c_char_p, c_int32]
         b.restype = c_int32
+        sv = lib.ref_model_save_safetensors
+        sv.argtypes = [POINTER(_Spec), c_int32, c_char_p, c_char_p, c_int32]
+        sv.restype = c_int32
+        ld = lib.ref_model_load_safetensors
+        ld.argtypes = [POINTER(_Spec), c_int32, c_char_p, c_int32, POINTER(c_void_p), c_char_p, c_int32]
+        ld.restype = c_int32
         _lib = lib
     return _lib
 
@@ -118,3 +124,32 @@ def backward(layers, fin, iin, loss_grad, in_cap=1 << 24):
         raise RefModelError(err.value.decode(errors="replace"))
     assert n.value <= in_cap, "input gradient larger than in_cap"
     return grads, (None if n.value < 0 else ig[:n.value].copy())
+
+
+def save_safetensors(layers, path):
+    """The reference's save_checkpoint (SafeTensors) of a model with these layers."""
+    keep, args = _marshal(layers, {}, {})
+    err = ctypes.create_string_buffer(512)
+    st = _load().ref_model_save_safetensors(args[0], args[1], str(path).encode(), err, 512)
+    del keep
+    if st:
+        raise RefModelError(err.value.decode(errors="replace"))
+
+
+def load_safetensors(layers, path, strict=True):
+    """The reference's load_checkpoint (SafeTensors, weights only) into a model
+    with these layers; returns each layer's weight block afterwards (None for
+    layers without one).  Raises RefModelError with the reference's message."""
+    keep, args = _marshal(layers, {}, {})
+    outs = []
+    for L in layers:
+        w = L.get("weights")
+        pc = int(L.get("params_count", 0 if w is None else np.asarray(w).size))
+        outs.append(np.zeros(pc, np.float32) if pc > 0 else None)
+    ptrs = (c_void_p * max(1, len(layers)))(*[0 if a is None else a.ctypes.data for a in outs])
+    err = ctypes.create_string_buffer(512)
+    st = _load().ref_model_load_safetensors(args[0], args[1], str(path).encode(), int(bool(strict)), ptrs, err, 512)
+    del keep
+    if st:
+        raise RefModelError(err.value.decode(errors="replace"))
+    return outs

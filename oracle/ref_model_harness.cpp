@@ -1,8 +1,9 @@
 // ref_model_harness.cpp -- TEST INFRASTRUCTURE ONLY.
 //
 // Drives the reference's own runtime, Model::forwardPassNamed
-// (Model.cpp:1352-1408 -> forwardPassView, Model.cpp:4621-6824) and
-// Model::backwardPass (Model.cpp:7307-9153), on a layer
+// (Model.cpp:1352-1408 -> forwardPassView, Model.cpp:4621-6824),
+// Model::backwardPass (Model.cpp:7307-9153) and the SafeTensors
+// save_checkpoint / load_checkpoint (Serialization.cpp), on a layer
 // list described by plain C structs.  Compiled with the reference's sources
 // in place (oracle/Makefile, target `ref_model`) into
 // oracle/_ref/libmimir_ref_model.so; used only to pin the routing
@@ -12,6 +13,7 @@
 // through Model::getMutableLayers(), given weight blocks by
 // Model::allocateParams (Model.cpp:3156-3184) and filled from the spec.
 #include "Model.hpp"
+#include "Serialization/Serialization.hpp"
 
 #include <cstdint>
 #include <cstring>
@@ -142,6 +144,66 @@ int ref_model_backward(const ref_layer_spec* specs, int32_t n_layers, const char
             *in_n = static_cast<int64_t>(g.size());
             const size_t n = std::min(static_cast<size_t>(in_cap), g.size());
             if (n) std::memcpy(in_grad, g.data(), n * sizeof(float));
+        }
+        return 0;
+    } catch (const std::exception& e) {
+        copy_error(e, err, err_cap);
+        return 1;
+    }
+}
+
+// Mimir::Serialization::save_checkpoint (Serialization.cpp) of a model built
+// from the specs, SafeTensors format, the reference's default SaveOptions.
+int ref_model_save_safetensors(const ref_layer_spec* specs, int32_t n_layers, const char* path, char* err,
+                               int32_t err_cap) {
+    try {
+        Model m;
+        build_model(m, specs, n_layers);
+        Mimir::Serialization::SaveOptions o;
+        o.format = Mimir::Serialization::CheckpointFormat::SafeTensors;
+        o.include_git_info = false;
+        std::string e;
+        if (!Mimir::Serialization::save_checkpoint(m, path, o, &e)) {
+            if (err && err_cap > 0) {
+                std::strncpy(err, e.c_str(), static_cast<size_t>(err_cap) - 1);
+                err[err_cap - 1] = 0;
+            }
+            return 1;
+        }
+        return 0;
+    } catch (const std::exception& e) {
+        copy_error(e, err, err_cap);
+        return 1;
+    }
+}
+
+// Mimir::Serialization::load_checkpoint (SafeTensors, weights only: no
+// tokenizer / encoder / optimizer) into a model built from the specs; each
+// layer's weight block afterwards goes to weights_out[i] (params_count
+// floats, when non-null).  Returns 0, or 1 with the reference's message.
+int ref_model_load_safetensors(const ref_layer_spec* specs, int32_t n_layers, const char* path, int32_t strict,
+                               float* const* weights_out, char* err, int32_t err_cap) {
+    try {
+        Model m;
+        build_model(m, specs, n_layers);
+        Mimir::Serialization::LoadOptions o;
+        o.format = Mimir::Serialization::CheckpointFormat::SafeTensors;
+        o.strict_mode = strict != 0;
+        o.load_tokenizer = false;
+        o.load_encoder = false;
+        o.load_optimizer = false;
+        std::string e;
+        if (!Mimir::Serialization::load_checkpoint(m, path, o, &e)) {
+            if (err && err_cap > 0) {
+                std::strncpy(err, e.c_str(), static_cast<size_t>(err_cap) - 1);
+                err[err_cap - 1] = 0;
+            }
+            return 1;
+        }
+        auto& layers = m.getMutableLayers();
+        for (int32_t i = 0; i < n_layers; ++i) {
+            if (!weights_out || !weights_out[i] || specs[i].params_count <= 0) continue;
+            std::memcpy(weights_out[i], layers[i].getWeights(), static_cast<size_t>(specs[i].params_count) * 4);
         }
         return 0;
     } catch (const std::exception& e) {

@@ -212,3 +212,18 @@ def train_graphs():
                  dict(name="res", type="Add", inputs=["g", "__input__"], output="x")],
                 {"__input__": xs}, {}, r.standard_normal(32 * 4096).astype(np.float32)))
     return out
+
+
+def checkpoint_layers():
+    """The layers of the SafeTensors fixture tests/golden/ref_checkpoint.safetensors
+    (written by the reference's save_checkpoint from these weights)."""
+    r = _rng(0x5AFE)
+    return [
+        dict(name="tok", type="Embedding", inputs=["ids"], output="h", vocab_size=10, embed_dim=8,
+             weights=r.standard_normal(80).astype(np.float32)),
+        dict(name="ln", type="LayerNorm", inputs=["h"], output="n", in_features=8,
+             weights=np.concatenate([1 + 0.1 * r.standard_normal(8), 0.1 * r.standard_normal(8)]).astype(np.float32)),
+        dict(name="act", type="GELU", inputs=["n"], output="g"),
+        dict(name="rms", type="RMSNorm", inputs=["g"], output="x",
+             weights=(1 + 0.1 * r.standard_normal(24)).astype(np.float32)),
+    ]

@@ -174,7 +174,33 @@ def write_model_backward():
     print("wrote model_backward", len(outs), "arrays")
 
 
+def write_safetensors_fixture():
+    """tests/golden/ref_checkpoint.safetensors: Mimir::Serialization::
+    save_checkpoint (SafeTensors, default options) of checkpoint_layers()."""
+    sys.path.insert(0, os.path.join(REPO, "tests"))
+    import model_ref as MR
+    from _graphs import checkpoint_layers
+    if not MR.available():
+        sys.exit("oracle/_ref/libmimir_ref_model.so is not built: make -C oracle ref_model")
+    path = os.path.join(HERE, "ref_checkpoint.safetensors")
+    layers = checkpoint_layers()
+    MR.save_safetensors(layers, path)
+    data = open(path, "rb").read()
+    path_manifest = os.path.join(HERE, "MANIFEST.json")
+    manifest = json.load(open(path_manifest))
+    manifest["ref_checkpoint"] = {
+        "note": "Mimir::Serialization::save_checkpoint (SafeTensors, default SaveOptions, no git info) of "
+                "tests/_graphs.py checkpoint_layers(); weights: the layers' blocks as drawn there",
+        "file": {"bytes": len(data), "sha256": hashlib.sha256(data).hexdigest()},
+        "regenerated_inputs": {"tests/_graphs.py": "checkpoint_layers()"},
+    }
+    with open(path_manifest, "w") as f:
+        json.dump(manifest, f, indent=1, sort_keys=True)
+    print("wrote ref_checkpoint.safetensors", len(data), "bytes")
+
+
 if __name__ == "__main__":
     main()
     write_model_graphs()
     write_model_backward()
+    write_safetensors_fixture()
