@@ -384,6 +384,30 @@ def cpu_leg(which, reps):
             t = O.time_port(lambda: (a.copy(), a.copy()), reps)
             rec(key, t, 3 * a.nbytes, 8192, "port",
                 "full [8192x4096]: accumulate_grad into two absent names is two vector copies (Model.cpp:7552-7555)")
+        elif key == "cfg3_safetensors_ingest":
+            import struct
+            import tempfile
+            table, _ = G.cfg3_gather()
+            hdr = json.dumps({"tok/weights": {"dtype": "F32", "shape": list(table.shape),
+                                              "data_offsets": [0, table.nbytes]}}).encode()
+            with tempfile.TemporaryDirectory() as d:
+                path = os.path.join(d, "table.safetensors")
+                with open(path, "wb") as f:
+                    f.write(struct.pack("<Q", len(hdr)))
+                    f.write(hdr)
+                    f.write(table.tobytes())
+                sys.path.insert(0, os.path.join(REPO, "oracle"))
+                import model_ref as MR
+                if MR.available():
+                    layers = [dict(name="tok", type="Embedding", vocab_size=32000, embed_dim=4096,
+                                   weights=np.zeros(table.size, np.float32))]
+                    t = MR.time_safetensors_load(layers, path, reps)
+                    rec(key, t, table.nbytes, 32000, "reference",
+                        "Mimir::Serialization::load_checkpoint (SafeTensors, weights only) of the same file into "
+                        "host weight blocks, page cache warm")
+                else:
+                    t = O.time_port(lambda: np.fromfile(path, np.uint8, count=table.nbytes, offset=8 + len(hdr)), reps)
+                    rec(key, t, table.nbytes, 32000, "port", "sequential read of the tensor bytes into host memory")
         elif key == "cfg3_embedding_bwd":
             ids = G.cfg3_ids().ravel()[:4096].copy()
             dy = G.cfg3_embedding_grad()[:4096].copy()
@@ -394,6 +418,45 @@ def cpu_leg(which, reps):
             rec(key, t, ids.nbytes + dy.nbytes + 2 * u * 4096 * 4, 4096, "port",
                 f"first 4096 of 32768 tokens ({u} distinct ids), oracle embedding_bwd_i32 into a resident table")
     return out
+
+
+def time_ingest(ctx, reps=3):
+    """SafeTensors ingestion of the configs[3] embedding table (32000 x 4096
+    fp32, 500 MiB) from a file straight into device memory
+    (mimir_safetensors_read): the file is written to a temporary directory
+    first, then read `reps` times (page cache warm after the first); the
+    median read time gives GB/s.  Host-to-device bound (PCIe), not HBM."""
+    import struct
+    import tempfile
+    import time
+    table, _ = G.cfg3_gather()
+    hdr = json.dumps({"tok/weights": {"dtype": "F32", "shape": list(table.shape),
+                                      "data_offsets": [0, table.nbytes]}}).encode()
+    with tempfile.TemporaryDirectory() as d:
+        path = os.path.join(d, "table.safetensors")
+        with open(path, "wb") as f:
+            f.write(struct.pack("<Q", len(hdr)))
+            f.write(hdr)
+            f.write(table.tobytes())
+        dst = ctx.empty(table.shape)
+        try:
+            times = []
+            with M.SafeTensors(ctx, path) as f:
+                for _ in range(reps + 1):
+                    t0 = time.perf_counter()
+                    f.read("tok/weights", dst)
+                    ctx.sync()
+                    times.append(time.perf_counter() - t0)
+            ok = bool(np.array_equal(dst.numpy()[:4], table[:4]))
+        finally:
+            dst.free()
+    sec = float(np.median(times[1:]))
+    return {"op": "cfg3_safetensors_ingest", "config": 3,
+            "desc": "SafeTensors read of the embedding table [32000x4096] fp32 (500 MiB) file -> HBM",
+            "kernel": "pinned double-buffered pread + hipMemcpyAsync", "algorithmic_bytes": int(table.nbytes),
+            "us_per_launch": round(sec * 1e6, 1), "GB_s": round(table.nbytes / sec / 1e9, 2),
+            "bound": "host-to-device (PCIe) and the page cache, not HBM", "first_read_s": round(times[0], 4),
+            "reps": reps, "check": ok}
 
 
 def load_traffic(workload):
@@ -452,9 +515,17 @@ def main():
         if k == head.key:
             sweep.append(res)
             continue
+        if k == "cfg3_safetensors_ingest":
+            continue
         r = time_op(ctx, by_key[k], args.op_steps, 3)
         log(f"op {k}: {r['us_per_launch']} us/launch, {r['GB_s']} GB/s ({100 * r['frac_of_peak']:.1f}%)")
         sweep.append(r)
+    if args.ops == "all" or "cfg3_safetensors_ingest" in keys:
+        r = time_ingest(ctx)
+        log(f"op cfg3_safetensors_ingest: {r['us_per_launch']} us, {r['GB_s']} GB/s (first read {r['first_read_s']} s)")
+        sweep.append(r)
+        if "cfg3_safetensors_ingest" not in keys:
+            keys = keys + ["cfg3_safetensors_ingest"]
     ctx.close()
 
     cpu = {}

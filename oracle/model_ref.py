@@ -26,6 +26,23 @@ class RefModelError(RuntimeError):
     pass
 
 
+class _StdoutToStderr:
+    """The reference's Model logs to stdout (std::cout); while it runs, file
+    descriptor 1 points at stderr so a caller's stdout stays its own."""
+
+    def __enter__(self):
+        import sys
+        sys.stdout.flush()
+        self.saved = os.dup(1)
+        os.dup2(2, 1)
+        return self
+
+    def __exit__(self, *exc):
+        ctypes.CDLL(None).fflush(None)  # C stdio (and std::cout with it) before fd 1 returns
+        os.dup2(self.saved, 1)
+        os.close(self.saved)
+
+
 _lib = None
 
 
@@ -54,6 +71,9 @@ def _load():
         ld = lib.ref_model_load_safetensors
         ld.argtypes = [POINTER(_Spec), c_int32, c_char_p, c_int32, POINTER(c_void_p), c_char_p, c_int32]
         ld.restype = c_int32
+        tl = lib.ref_time_safetensors_load
+        tl.argtypes = [POINTER(_Spec), c_int32, c_char_p, c_int32]
+        tl.restype = ctypes.c_double
         _lib = lib
     return _lib
 
@@ -93,7 +113,8 @@ def forward_named(layers, fin=None, iin=None, out_cap=1 << 24):
     out = np.empty(out_cap, np.float32)
     n = c_int64(0)
     err = ctypes.create_string_buffer(512)
-    st = _load().ref_model_forward(*args, out.ctypes.data, out_cap, ctypes.byref(n), err, 512)
+    with _StdoutToStderr():
+        st = _load().ref_model_forward(*args, out.ctypes.data, out_cap, ctypes.byref(n), err, 512)
     del keep
     if st:
         raise RefModelError(err.value.decode(errors="replace"))
@@ -117,8 +138,9 @@ def backward(layers, fin, iin, loss_grad, in_cap=1 << 24):
     ig = np.empty(in_cap, np.float32)
     n = c_int64(0)
     err = ctypes.create_string_buffer(512)
-    st = _load().ref_model_backward(*args, g.ctypes.data, g.size, gp, ig.ctypes.data, in_cap,
-                                    ctypes.byref(n), err, 512)
+    with _StdoutToStderr():
+        st = _load().ref_model_backward(*args, g.ctypes.data, g.size, gp, ig.ctypes.data, in_cap,
+                                        ctypes.byref(n), err, 512)
     del keep
     if st:
         raise RefModelError(err.value.decode(errors="replace"))
@@ -130,7 +152,8 @@ def save_safetensors(layers, path):
     """The reference's save_checkpoint (SafeTensors) of a model with these layers."""
     keep, args = _marshal(layers, {}, {})
     err = ctypes.create_string_buffer(512)
-    st = _load().ref_model_save_safetensors(args[0], args[1], str(path).encode(), err, 512)
+    with _StdoutToStderr():
+        st = _load().ref_model_save_safetensors(args[0], args[1], str(path).encode(), err, 512)
     del keep
     if st:
         raise RefModelError(err.value.decode(errors="replace"))
@@ -148,8 +171,22 @@ def load_safetensors(layers, path, strict=True):
         outs.append(np.zeros(pc, np.float32) if pc > 0 else None)
     ptrs = (c_void_p * max(1, len(layers)))(*[0 if a is None else a.ctypes.data for a in outs])
     err = ctypes.create_string_buffer(512)
-    st = _load().ref_model_load_safetensors(args[0], args[1], str(path).encode(), int(bool(strict)), ptrs, err, 512)
+    with _StdoutToStderr():
+        st = _load().ref_model_load_safetensors(args[0], args[1], str(path).encode(), int(bool(strict)), ptrs, err,
+                                                512)
     del keep
     if st:
         raise RefModelError(err.value.decode(errors="replace"))
     return outs
+
+
+def time_safetensors_load(layers, path, reps=3):
+    """Median seconds of the reference's load_checkpoint (SafeTensors, weights
+    only) into a model built once with these layers (warm page cache)."""
+    keep, args = _marshal(layers, {}, {})
+    with _StdoutToStderr():
+        t = _load().ref_time_safetensors_load(args[0], args[1], str(path).encode(), int(reps))
+    del keep
+    if t < 0:
+        raise RefModelError("load_checkpoint failed")
+    return t

@@ -15,6 +15,8 @@
 #include "Model.hpp"
 #include "Serialization/Serialization.hpp"
 
+#include <algorithm>
+#include <chrono>
 #include <cstdint>
 #include <cstring>
 #include <sstream>
@@ -209,6 +211,32 @@ int ref_model_load_safetensors(const ref_layer_spec* specs, int32_t n_layers, co
     } catch (const std::exception& e) {
         copy_error(e, err, err_cap);
         return 1;
+    }
+}
+
+// Seconds per Mimir::Serialization::load_checkpoint (SafeTensors, weights
+// only) into a model built once from the specs: the median of `reps` timed
+// calls after one untimed call (page cache warm).  -1 on failure.
+double ref_time_safetensors_load(const ref_layer_spec* specs, int32_t n_layers, const char* path, int32_t reps) {
+    try {
+        Model m;
+        build_model(m, specs, n_layers);
+        Mimir::Serialization::LoadOptions o;
+        o.format = Mimir::Serialization::CheckpointFormat::SafeTensors;
+        o.load_tokenizer = false;
+        o.load_encoder = false;
+        o.load_optimizer = false;
+        std::vector<double> t;
+        for (int32_t r = 0; r <= reps; ++r) {
+            const auto t0 = std::chrono::steady_clock::now();
+            if (!Mimir::Serialization::load_checkpoint(m, path, o, nullptr)) return -1.0;
+            const auto t1 = std::chrono::steady_clock::now();
+            if (r > 0) t.push_back(std::chrono::duration<double>(t1 - t0).count());
+        }
+        std::sort(t.begin(), t.end());
+        return t.empty() ? -1.0 : t[t.size() / 2];
+    } catch (...) {
+        return -1.0;
     }
 }
 
