@@ -47,14 +47,22 @@ struct LongArgs {
     float eps;
     float* partial;  // [rows][nchunks][2]
     float* stats;    // [rows][2]
+    int reverse;     // this pass walks the chunks last to first
 };
+
+// Passes alternate direction: a pass starts where the previous one ended, so
+// the start of its walk is still in the 256 MiB Infinity Cache (MALL) and
+// only the part of the row beyond the cache comes again from HBM.
+__device__ __forceinline__ int64_t chunk_of(const LongArgs& a) {
+    return a.reverse ? a.nchunks - 1 - static_cast<int64_t>(blockIdx.x) : static_cast<int64_t>(blockIdx.x);
+}
 
 // Pass 1: one chunk's partial statistic.
 template <int S>
 __global__ __launch_bounds__(kBlock) void lr_partial(LongArgs a) {
     __shared__ float lds[2][kBlock / kWave];
     const int64_t row = blockIdx.y;
-    const int64_t chunk = blockIdx.x;
+    const int64_t chunk = chunk_of(a);
     const int64_t c4n = a.cols >> 2;
     const int64_t base = row * a.cols;
     f4 v[kChunkVec];
@@ -65,11 +73,11 @@ __global__ __launch_bounds__(kBlock) void lr_partial(LongArgs a) {
         ok[j] = c4 < c4n;
         if constexpr (S == kSumSqAdd) {
             if (ok[j]) {
-                v[j] = ld4<true>(a.x + base + 4 * c4) + ld4<true>(a.r + base + 4 * c4);
-                st4<true>(a.r_out + base + 4 * c4, v[j]);  // the updated residual
+                v[j] = ld4<false>(a.x + base + 4 * c4) + ld4<false>(a.r + base + 4 * c4);
+                st4<false>(a.r_out + base + 4 * c4, v[j]);  // the updated residual, re-read by the last pass
             }
         } else {
-            if (ok[j]) v[j] = ld4<true>(a.x + base + 4 * c4);
+            if (ok[j]) v[j] = ld4<false>(a.x + base + 4 * c4);  // kept in the caches for the next pass
         }
     }
     float p0 = 0.0f, p1 = 0.0f;
@@ -156,7 +164,7 @@ __device__ __forceinline__ float softmax_out(float xv, float m, float s) {
 template <int K, int MODE>
 __global__ __launch_bounds__(kBlock) void lr_apply(LongArgs a) {
     const int64_t row = blockIdx.y;
-    const int64_t chunk = blockIdx.x;
+    const int64_t chunk = chunk_of(a);
     const int64_t c4n = a.cols >> 2;
     const int64_t base = row * a.cols;
     const float s0 = a.stats[2 * row];
@@ -183,9 +191,13 @@ __global__ __launch_bounds__(kBlock) void lr_apply(LongArgs a) {
         } else if constexpr (K == 1 || K == 2) {
             o = v[j] / s0;
             if (a.g) {
+                if (c + 3 < a.w_len) {  // weights cover the whole vector: one 16-byte load
+                    o *= *reinterpret_cast<const f4*>(a.g + c);
+                } else {
 #pragma unroll
-                for (int k = 0; k < 4; ++k)
-                    if (c + k < a.w_len) o[k] *= a.g[c + k];
+                    for (int k = 0; k < 4; ++k)
+                        if (c + k < a.w_len) o[k] *= a.g[c + k];
+                }
             }
         } else {
 #pragma unroll
@@ -216,38 +228,42 @@ bool mimir::longrow_applies(int64_t rows, int64_t cols) {
 int mimir::longrow_norm(mimir_ctx* ctx, int kind, const float* x, const float* r, float* r_out,
                         const float* g, const float* b, int64_t w_len, float* y, int64_t rows, int64_t cols,
                         float eps) {
-    LongArgs a{x, r, r_out, g, b, w_len, y, 0, 0, 0, eps, nullptr, nullptr};
+    LongArgs a{x, r, r_out, g, b, w_len, y, 0, 0, 0, eps, nullptr, nullptr, 0};
     if (int st = setup(ctx, a, rows, cols)) return st;
     const dim3 grid(static_cast<unsigned>(a.nchunks), static_cast<unsigned>(rows));
     const unsigned nrows = static_cast<unsigned>(rows);
+    LongArgs fwd = a, rev = a;
+    rev.reverse = 1;
     if (kind == 0) {
-        lr_partial<kSumX><<<grid, kBlock, 0, ctx->stream>>>(a);
-        lr_combine<kSumX><<<nrows, kBlock, 0, ctx->stream>>>(a);
-        lr_partial<kSumDev><<<grid, kBlock, 0, ctx->stream>>>(a);
-        lr_combine<kSumDev><<<nrows, kBlock, 0, ctx->stream>>>(a);
-        lr_apply<0, 0><<<grid, kBlock, 0, ctx->stream>>>(a);
+        lr_partial<kSumX><<<grid, kBlock, 0, ctx->stream>>>(fwd);
+        lr_combine<kSumX><<<nrows, kBlock, 0, ctx->stream>>>(fwd);
+        lr_partial<kSumDev><<<grid, kBlock, 0, ctx->stream>>>(rev);
+        lr_combine<kSumDev><<<nrows, kBlock, 0, ctx->stream>>>(rev);
+        lr_apply<0, 0><<<grid, kBlock, 0, ctx->stream>>>(fwd);
     } else if (kind == 1) {
-        lr_partial<kSumSq><<<grid, kBlock, 0, ctx->stream>>>(a);
-        lr_combine<kSumSq><<<nrows, kBlock, 0, ctx->stream>>>(a);
-        lr_apply<1, 0><<<grid, kBlock, 0, ctx->stream>>>(a);
+        lr_partial<kSumSq><<<grid, kBlock, 0, ctx->stream>>>(fwd);
+        lr_combine<kSumSq><<<nrows, kBlock, 0, ctx->stream>>>(fwd);
+        lr_apply<1, 0><<<grid, kBlock, 0, ctx->stream>>>(rev);
     } else {
-        lr_partial<kSumSqAdd><<<grid, kBlock, 0, ctx->stream>>>(a);
-        lr_combine<kSumSqAdd><<<nrows, kBlock, 0, ctx->stream>>>(a);
-        lr_apply<2, 0><<<grid, kBlock, 0, ctx->stream>>>(a);
+        lr_partial<kSumSqAdd><<<grid, kBlock, 0, ctx->stream>>>(fwd);
+        lr_combine<kSumSqAdd><<<nrows, kBlock, 0, ctx->stream>>>(fwd);
+        lr_apply<2, 0><<<grid, kBlock, 0, ctx->stream>>>(rev);
     }
     return launched(ctx, "longrow_norm");
 }
 
 int mimir::longrow_softmax(mimir_ctx* ctx, int mode, const float* x, float* y, int64_t rows, int64_t cols) {
-    LongArgs a{x, nullptr, nullptr, nullptr, nullptr, 0, y, 0, 0, 0, 0.0f, nullptr, nullptr};
+    LongArgs a{x, nullptr, nullptr, nullptr, nullptr, 0, y, 0, 0, 0, 0.0f, nullptr, nullptr, 0};
     if (int st = setup(ctx, a, rows, cols)) return st;
     const dim3 grid(static_cast<unsigned>(a.nchunks), static_cast<unsigned>(rows));
+    LongArgs rev = a;
+    rev.reverse = 1;
     lr_partial<kSoftmax><<<grid, kBlock, 0, ctx->stream>>>(a);
     lr_combine<kSoftmax><<<static_cast<unsigned>(rows), kBlock, 0, ctx->stream>>>(a);
     switch (mode) {
-        case MIMIR_SOFTMAX_DIV_EPS: lr_apply<3, MIMIR_SOFTMAX_DIV_EPS><<<grid, kBlock, 0, ctx->stream>>>(a); break;
-        case MIMIR_SOFTMAX_MUL_INV: lr_apply<3, MIMIR_SOFTMAX_MUL_INV><<<grid, kBlock, 0, ctx->stream>>>(a); break;
-        default: lr_apply<3, MIMIR_SOFTMAX_LOG><<<grid, kBlock, 0, ctx->stream>>>(a); break;
+        case MIMIR_SOFTMAX_DIV_EPS: lr_apply<3, MIMIR_SOFTMAX_DIV_EPS><<<grid, kBlock, 0, ctx->stream>>>(rev); break;
+        case MIMIR_SOFTMAX_MUL_INV: lr_apply<3, MIMIR_SOFTMAX_MUL_INV><<<grid, kBlock, 0, ctx->stream>>>(rev); break;
+        default: lr_apply<3, MIMIR_SOFTMAX_LOG><<<grid, kBlock, 0, ctx->stream>>>(rev); break;
     }
     return launched(ctx, "longrow_softmax");
 }
