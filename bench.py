@@ -203,6 +203,38 @@ def build_ops():
                        f"{uniq3} distinct ids", "radix sort + embed_bwd_rows_vec",
                        32768 * 4 + 32768 * 4096 * f4 + 2 * uniq3 * 4096 * f4, 32768, "token rows", make_embb))
 
+    # The device-resident runtime (mimir_store_run): a residual block's chain
+    # of the path's layers at the configs[4] shape, routed by name as
+    # Model::forwardPassNamed does; a step is one run of the five layers.
+    class _Owned:
+        def __init__(self, *objs):
+            self.objs = objs
+
+        def free(self):
+            for o in self.objs:
+                o.close()
+
+    def make_block(ctx, nsets):
+        x, res = G.cfg4_add()
+        gate = G.cfg4_grad((8192, 4096), 11)
+        _, g, b, _ = G.cfg4_layernorm(rows=1)
+        layers = [dict(name="res_add", type="Add", inputs=["x", "res"], output="h"),
+                  dict(name="ln", type="LayerNorm", inputs=["h"], output="n", in_features=4096, eps=1e-5,
+                       weights=np.concatenate([g, b])),
+                  dict(name="act", type="GELU", inputs=["n"], output="g"),
+                  dict(name="gate", type="Multiply", inputs=["g", "gate"], output="m"),
+                  dict(name="silu", type="SiLU", inputs=["m"], output="y")]
+        graph = M.DeviceGraph(ctx, layers)
+        store = M.Store(ctx)
+        store.set_inputs({"x": x, "res": res, "gate": gate}, {})
+        store.run(graph)  # fills the buffer pool: later runs allocate nothing
+        return (lambda i: store.run(graph)), [[_Owned(store, graph)]]
+    blk = OpBench("cfg4_runtime_block", 4,
+                  "device-resident runtime: Add -> LayerNorm -> GELU -> Multiply -> SiLU on [8192x4096], routed by name",
+                  "mimir_store_run (5 kernels)", 12 * 8192 * 4096 * f4 + 2 * 4096 * f4, 8192, "rows", make_block)
+    blk.nsets = lambda: 1
+    ops.append(blk)
+
     # Calibration: a plain streaming copy of 512 MiB (mimir_copy), the
     # practical HBM ceiling and the yardstick for the FETCH/WRITE counters.
     def make_copy(ctx, nsets):
@@ -408,6 +440,24 @@ def cpu_leg(which, reps):
                 else:
                     t = O.time_port(lambda: np.fromfile(path, np.uint8, count=table.nbytes, offset=8 + len(hdr)), reps)
                     rec(key, t, table.nbytes, 32000, "port", "sequential read of the tensor bytes into host memory")
+        elif key == "cfg4_runtime_block":
+            rows = 1024
+            x, res = G.cfg4_add(rows=rows)
+            gate = G.cfg4_grad((8192, 4096), 11)[:rows]
+            _, g, b, _ = G.cfg4_layernorm(rows=1)
+            layers = [dict(name="res_add", type="Add", inputs=["x", "res"], output="h"),
+                      dict(name="ln", type="LayerNorm", inputs=["h"], output="n", in_features=4096, eps=1e-5,
+                           weights=np.concatenate([g, b])),
+                      dict(name="act", type="GELU", inputs=["n"], output="g"),
+                      dict(name="gate", type="Multiply", inputs=["g", "gate"], output="m"),
+                      dict(name="silu", type="SiLU", inputs=["m"], output="y")]
+            sys.path.insert(0, os.path.join(REPO, "oracle"))
+            import model_ref as MR
+            nb = 12 * x.nbytes + 2 * g.nbytes
+            if MR.available():
+                t = MR.time_forward_named(layers, {"x": x, "res": res, "gate": gate}, {}, reps)
+                rec(key, t, nb, rows, "reference",
+                    f"{rows} of 8192 rows: Model::forwardPassNamed of the same five layers (host tensor store)")
         elif key == "cfg3_embedding_bwd":
             ids = G.cfg3_ids().ravel()[:4096].copy()
             dy = G.cfg3_embedding_grad()[:4096].copy()

@@ -74,6 +74,10 @@ def _load():
         tl = lib.ref_time_safetensors_load
         tl.argtypes = [POINTER(_Spec), c_int32, c_char_p, c_int32]
         tl.restype = ctypes.c_double
+        tf = lib.ref_time_forward_named
+        tf.argtypes = [POINTER(_Spec), c_int32, POINTER(c_char_p), POINTER(c_void_p), POINTER(c_int64), c_int32,
+                       POINTER(c_char_p), POINTER(c_void_p), POINTER(c_int64), c_int32, c_int32]
+        tf.restype = ctypes.c_double
         _lib = lib
     return _lib
 
@@ -189,4 +193,16 @@ def time_safetensors_load(layers, path, reps=3):
     del keep
     if t < 0:
         raise RefModelError("load_checkpoint failed")
+    return t
+
+
+def time_forward_named(layers, fin=None, iin=None, reps=3):
+    """Median seconds of the reference's Model::forwardPassNamed (inference)
+    on a model built once with these layers."""
+    keep, args = _marshal(layers, fin, iin)
+    with _StdoutToStderr():
+        t = _load().ref_time_forward_named(*args, int(reps))
+    del keep
+    if t < 0:
+        raise RefModelError("forwardPassNamed failed")
     return t
