@@ -13,11 +13,19 @@
 //                order (per-thread strided sums, then the DPP/LDS tree), so
 //                the result does not depend on scheduling;
 //   3. apply   : per chunk, the elementwise normalisation with the row stats.
-// LayerNorm keeps the reference's two-pass variance: partial/combine for the
-// mean, then partial/combine of sum((x-mean)^2), then apply.  The extra reads
-// of x hit L2/MALL for rows that fit there and HBM otherwise: 3 (RMSNorm,
-// softmax) or 4 (LayerNorm) passes instead of 2.  Partials live in the
-// context's scratch buffer, reused in stream order.
+// LayerNorm's variance is two-pass within each chunk: the chunk is held in
+// registers, so its sum and its squared deviations about its own mean come
+// from one read.  The combine merges the chunks in float64 by the pairwise
+// formula of Chan, Golub and LeVeque (1979):
+//   M2 = sum_c M2_c + sum_c n_c (mean_c - mean)^2,
+// which equals the reference's sum((x - mean)^2) (LayerOps.hpp:296-303) up
+// to float rounding inside a chunk, without a second read of the row.  The
+// sums are taken of x - x0, x0 the row's first element (shifted data), and
+// the row mean reaches the apply pass as a float pair hi + lo, so a row whose
+// mean is large against its spread keeps its precision.  Every
+// op reads x twice (statistics, then apply) and writes y once; the second
+// read walks the row backwards so its first part comes from the MALL.
+// Partials live in the context's scratch buffer, reused in stream order.
 #include "common.hpp"
 #include "internal.hpp"
 
@@ -31,7 +39,7 @@ constexpr int kChunkVec = 4;                          // float4 per thread per c
 constexpr int64_t kChunk4 = kChunkVec * kBlock;       // float4 per chunk (1024)
 constexpr int64_t kChunkFloats = 4 * kChunk4;         // 4096 floats
 
-enum Stat { kSumX = 0, kSumSq = 1, kSumDev = 2, kSumSqAdd = 3, kSoftmax = 4 };
+enum Stat { kChan = 0, kSumSq = 1, kSumSqAdd = 3, kSoftmax = 4 };
 
 struct LongArgs {
     const float* x;
@@ -46,7 +54,7 @@ struct LongArgs {
     int64_t nchunks;
     float eps;
     float* partial;  // [rows][nchunks][2]
-    float* stats;    // [rows][2]
+    float* stats;    // [rows][4]
     int reverse;     // this pass walks the chunks last to first
 };
 
@@ -55,6 +63,27 @@ struct LongArgs {
 // only the part of the row beyond the cache comes again from HBM.
 __device__ __forceinline__ int64_t chunk_of(const LongArgs& a) {
     return a.reverse ? a.nchunks - 1 - static_cast<int64_t>(blockIdx.x) : static_cast<int64_t>(blockIdx.x);
+}
+
+// Number of floats in a chunk (the last one may be short).
+__device__ __forceinline__ float chunk_len(const LongArgs& a, int64_t chunk) {
+    const int64_t left = a.cols - chunk * kChunkFloats;
+    return static_cast<float>(left < kChunkFloats ? left : kChunkFloats);
+}
+
+// Sum of one double per thread over the workgroup, in a fixed tree order;
+// every thread gets the total.
+__device__ __forceinline__ double block_sum_f64(double v, double* lds) {
+    lds[threadIdx.x] = v;
+    __syncthreads();
+#pragma unroll
+    for (int h = kBlock / 2; h > 0; h >>= 1) {
+        if (static_cast<int>(threadIdx.x) < h) lds[threadIdx.x] += lds[threadIdx.x + h];
+        __syncthreads();
+    }
+    const double t = lds[0];
+    __syncthreads();  // lds is reused by the caller's next reduction
+    return t;
 }
 
 // Pass 1: one chunk's partial statistic.
@@ -96,19 +125,30 @@ __global__ __launch_bounds__(kBlock) void lr_partial(LongArgs a) {
         }
         p0 = m;
         p1 = block_sum<kBlock / kWave>(s, lds[1]);
-    } else {
-        const float mean = (S == kSumDev) ? a.stats[2 * row] : 0.0f;
+    } else if constexpr (S == kChan) {
+        const float x0 = a.x[base];  // the shift
         float s = 0.0f;
 #pragma unroll
         for (int j = 0; j < kChunkVec; ++j) {
             if (!ok[j]) continue;
-            if constexpr (S == kSumX) {
-                s += (v[j].x + v[j].y) + (v[j].z + v[j].w);
-            } else {
-                const f4 d = (S == kSumDev) ? v[j] - mean : v[j];
-                s += (d.x * d.x + d.y * d.y) + (d.z * d.z + d.w * d.w);
-            }
+            v[j] -= x0;
+            s += (v[j].x + v[j].y) + (v[j].z + v[j].w);
         }
+        p0 = block_sum<kBlock / kWave>(s, lds[0]);
+        const float mc = p0 / chunk_len(a, chunk);  // recomputed bit for bit by the combine
+        float q = 0.0f;
+#pragma unroll
+        for (int j = 0; j < kChunkVec; ++j) {
+            if (!ok[j]) continue;
+            const f4 d = v[j] - mc;
+            q += (d.x * d.x + d.y * d.y) + (d.z * d.z + d.w * d.w);
+        }
+        p1 = block_sum<kBlock / kWave>(q, lds[1]);
+    } else {
+        float s = 0.0f;
+#pragma unroll
+        for (int j = 0; j < kChunkVec; ++j)
+            if (ok[j]) s += (v[j].x * v[j].x + v[j].y * v[j].y) + (v[j].z * v[j].z + v[j].w * v[j].w);
         p0 = block_sum<kBlock / kWave>(s, lds[0]);
     }
     if (threadIdx.x == 0) {
@@ -119,7 +159,7 @@ __global__ __launch_bounds__(kBlock) void lr_partial(LongArgs a) {
 }
 
 // Pass 2: fold one row's chunk partials (fixed order) into its statistics.
-//   kSumX  -> stats = (mean, -)            kSumDev -> stats.y = 1/sqrt(var+eps)
+//   kChan  -> stats = (mean hi, mean lo, 1/sqrt(var+eps))
 //   kSumSq / kSumSqAdd -> stats = (rms, -) kSoftmax -> stats = (max, sum)
 template <int S>
 __global__ __launch_bounds__(kBlock) void lr_combine(LongArgs a) {
@@ -138,18 +178,33 @@ __global__ __launch_bounds__(kBlock) void lr_combine(LongArgs a) {
         }
         s = block_sum<kBlock / kWave>(s, lds[1]);
         if (threadIdx.x == 0) {
-            a.stats[2 * row] = m;
-            a.stats[2 * row + 1] = s;
+            a.stats[4 * row] = m;
+            a.stats[4 * row + 1] = s;
+        }
+    } else if constexpr (S == kChan) {
+        __shared__ double lds64[kBlock];
+        double s = 0.0;
+        for (int64_t c = threadIdx.x; c < a.nchunks; c += kBlock) s += static_cast<double>(p[2 * c]);
+        const double mean = block_sum_f64(s, lds64) / static_cast<double>(a.cols);
+        double m2 = 0.0;
+        for (int64_t c = threadIdx.x; c < a.nchunks; c += kBlock) {
+            const float nc = chunk_len(a, c);
+            const double d = static_cast<double>(p[2 * c] / nc) - mean;  // the chunk mean the partial used
+            m2 += static_cast<double>(p[2 * c + 1]) + static_cast<double>(nc) * d * d;
+        }
+        m2 = block_sum_f64(m2, lds64);
+        if (threadIdx.x == 0) {
+            const double mu = static_cast<double>(a.x[row * a.cols]) + mean;  // undo the shift
+            const float hi = static_cast<float>(mu);
+            a.stats[4 * row] = hi;
+            a.stats[4 * row + 1] = static_cast<float>(mu - static_cast<double>(hi));
+            a.stats[4 * row + 2] = 1.0f / sqrtf(static_cast<float>(m2 / static_cast<double>(a.cols)) + a.eps);
         }
     } else {
         float s = 0.0f;
         for (int64_t c = threadIdx.x; c < a.nchunks; c += kBlock) s += p[2 * c];
         s = block_sum<kBlock / kWave>(s, lds[0]);
-        if (threadIdx.x == 0) {
-            if constexpr (S == kSumX) a.stats[2 * row] = s / n;
-            else if constexpr (S == kSumDev) a.stats[2 * row + 1] = 1.0f / sqrtf(s / n + a.eps);
-            else a.stats[2 * row] = sqrtf(s / n + a.eps);
-        }
+        if (threadIdx.x == 0) a.stats[4 * row] = sqrtf(s / n + a.eps);
     }
 }
 
@@ -167,8 +222,9 @@ __global__ __launch_bounds__(kBlock) void lr_apply(LongArgs a) {
     const int64_t chunk = chunk_of(a);
     const int64_t c4n = a.cols >> 2;
     const int64_t base = row * a.cols;
-    const float s0 = a.stats[2 * row];
-    const float s1 = a.stats[2 * row + 1];
+    const float s0 = a.stats[4 * row];
+    const float s1 = a.stats[4 * row + 1];
+    const float s2 = a.stats[4 * row + 2];
     const float* src = (K == 2) ? a.r_out : a.x;  // add+RMSNorm re-reads the residual it wrote
     f4 v[kChunkVec];
 #pragma unroll
@@ -183,7 +239,7 @@ __global__ __launch_bounds__(kBlock) void lr_apply(LongArgs a) {
         const int64_t c = 4 * c4;
         f4 o;
         if constexpr (K == 0) {
-            o = (v[j] - s0) * s1;
+            o = ((v[j] - s0) - s1) * s2;
             if (a.g) {
                 o *= *reinterpret_cast<const f4*>(a.g + c);
                 if (a.b) o += *reinterpret_cast<const f4*>(a.b + c);
@@ -211,7 +267,7 @@ int setup(mimir_ctx* ctx, LongArgs& a, int64_t rows, int64_t cols) {
     a.rows = rows;
     a.cols = cols;
     a.nchunks = (cols + kChunkFloats - 1) / kChunkFloats;
-    const size_t bytes = sizeof(float) * (2 * static_cast<size_t>(rows) * a.nchunks + 2 * rows);
+    const size_t bytes = sizeof(float) * (2 * static_cast<size_t>(rows) * a.nchunks + 4 * rows);
     void* s = nullptr;
     if (int st = ensure_scratch(ctx, bytes, &s)) return st;
     a.partial = static_cast<float*>(s);
@@ -235,11 +291,9 @@ int mimir::longrow_norm(mimir_ctx* ctx, int kind, const float* x, const float* r
     LongArgs fwd = a, rev = a;
     rev.reverse = 1;
     if (kind == 0) {
-        lr_partial<kSumX><<<grid, kBlock, 0, ctx->stream>>>(fwd);
-        lr_combine<kSumX><<<nrows, kBlock, 0, ctx->stream>>>(fwd);
-        lr_partial<kSumDev><<<grid, kBlock, 0, ctx->stream>>>(rev);
-        lr_combine<kSumDev><<<nrows, kBlock, 0, ctx->stream>>>(rev);
-        lr_apply<0, 0><<<grid, kBlock, 0, ctx->stream>>>(fwd);
+        lr_partial<kChan><<<grid, kBlock, 0, ctx->stream>>>(fwd);
+        lr_combine<kChan><<<nrows, kBlock, 0, ctx->stream>>>(fwd);
+        lr_apply<0, 0><<<grid, kBlock, 0, ctx->stream>>>(rev);
     } else if (kind == 1) {
         lr_partial<kSumSq><<<grid, kBlock, 0, ctx->stream>>>(fwd);
         lr_combine<kSumSq><<<nrows, kBlock, 0, ctx->stream>>>(fwd);

@@ -367,6 +367,24 @@ def test_longrow_layernorm_rmsnorm(ctx, rows, cols):
     assert_close_or_nearer_exact(got, ref, X.rmsnorm(x, cols, g, wl, 1e-6), "long RMSNorm")
 
 
+def test_longrow_layernorm_offset_rows(ctx):
+    """Rows whose mean dwarfs their spread, and chunks of different means:
+    the per-chunk deviations and their float64 merge must still give the
+    two-pass variance."""
+    rows, cols = 3, 5 * 4096 * 4 + 4096
+    x = rng.standard_normal((rows, cols)).astype(np.float32)
+    x[0] = 1000.0 + 0.5 * x[0]
+    x[1, : cols // 2] += 40.0  # two halves with different means
+    x[2] = np.float32(3.25)  # constant row: variance 0, y = beta
+    g = (1 + 0.05 * rng.standard_normal(cols)).astype(np.float32)
+    b = (0.05 * rng.standard_normal(cols)).astype(np.float32)
+    got = run(ctx, lambda dx, dg, db, y: ctx.layernorm(dx, dg, db, y, rows, cols, 1e-5), x, g, b,
+              out_shape=x.shape)
+    assert_close_or_nearer_exact(got, O.layernorm(x, cols, g, b, 1e-5).reshape(x.shape),
+                                 X.layernorm(x, cols, g, b, 1e-5), "long LN, offset rows")
+    assert_bitexact(got[2], b, "constant row")
+
+
 def test_longrow_add_rmsnorm_inplace(ctx):
     rows, cols = 2, 3 * 4096 * 4 + 8
     x = rng.standard_normal((rows, cols), dtype=np.float32)
