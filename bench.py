@@ -15,7 +15,10 @@ Prints ONE JSON line on stdout (progress goes to stderr).  Besides the
 headline workload, `ops` lists every op of configs[0..4] measured the same
 way, and `cpu_baseline` times the reference's own CPU code (compiled from the
 reference sources into oracle/_ref) on the host, single-threaded as the
-reference ops are.
+reference ops are.  The same leg checks each op: one more launch on freshly
+uploaded inputs, compared with the CPU path's output on those inputs
+(`parity`: max |d|, max relative error, bit-exactness, pass under the
+path's tolerance).
 """
 from __future__ import annotations
 
@@ -49,10 +52,13 @@ class OpBench:
     """One op of one configuration: its inputs on the device (nsets copies)
     and a closure that launches it on set i."""
 
-    def __init__(self, key, config, desc, kernel, nbytes, rows, row_unit, make):
+    def __init__(self, key, config, desc, kernel, nbytes, rows, row_unit, make, outputs=None):
         self.key, self.config, self.desc, self.kernel = key, config, desc, kernel
         self.nbytes, self.rows, self.row_unit = nbytes, rows, row_unit
         self.make = make  # make(ctx, nsets) -> (step(i), buffers)
+        # outputs(buffers) -> {name: DeviceArray or ndarray}: what one launch
+        # on set 0 produced, for the parity check of the cpu_baseline leg
+        self.outputs = outputs
 
     def nsets(self):
         return max(2, min(MAX_SETS, math.ceil(MIN_FOOTPRINT / self.nbytes)))
@@ -74,6 +80,19 @@ def _replicate(ctx, host_arrays, nsets):
     return sets
 
 
+def block_layers():
+    """A residual block's chain of the path's layers at the configs[4] shape,
+    routed by name.  The result is named "x", the tensor
+    Model::forwardPassNamed returns."""
+    _, g, b, _ = G.cfg4_layernorm(rows=1)
+    return [dict(name="res_add", type="Add", inputs=["inp", "res"], output="h"),
+            dict(name="ln", type="LayerNorm", inputs=["h"], output="n", in_features=4096, eps=1e-5,
+                 weights=np.concatenate([g, b])),
+            dict(name="act", type="GELU", inputs=["n"], output="g"),
+            dict(name="gate", type="Multiply", inputs=["g", "gate"], output="m"),
+            dict(name="silu", type="SiLU", inputs=["m"], output="x")]
+
+
 def build_ops():
     ops = []
     f4 = 4
@@ -83,9 +102,9 @@ def build_ops():
             x, g, b, eps = gen()
             gb = _replicate(ctx, [g, b], 1)[0]
             sets = _replicate(ctx, [x, np.empty_like(x)], nsets)
-            return (lambda i: ctx.layernorm(sets[i][0], gb[0], gb[1], sets[i][1], rows, cols, eps)), sets
+            return (lambda i: ctx.layernorm(sets[i][0], gb[0], gb[1], sets[i][1], rows, cols, eps)), sets + [gb]
         return OpBench(key, cfg, f"LayerNorm fp32 [{rows}x{cols}]", "norm_rows_vec<Layer>",
-                       2 * rows * cols * f4 + 2 * cols * f4, rows, "rows", make)
+                       2 * rows * cols * f4 + 2 * cols * f4, rows, "rows", make, lambda s: {"y": s[0][1]})
 
     ops.append(ln_op("cfg0_layernorm", 0, G.cfg0_layernorm, 256, 512))
 
@@ -94,9 +113,10 @@ def build_ops():
         wd = _replicate(ctx, [w], 1)[0][0]
         sets = _replicate(ctx, [x, r, np.empty_like(x)], nsets)
         return (lambda i: ctx.add_rmsnorm(sets[i][0], sets[i][1], sets[i][1], wd, sets[i][2], 4096, 4096,
-                                          eps)), sets
+                                          eps)), sets + [[wd]]
     ops.append(OpBench("cfg1_add_rmsnorm", 1, "residual add + RMSNorm fp32 x,r [4096x4096] -> y, residual'",
-                       "norm_rows_vec<AddRms>", 4 * 4096 * 4096 * f4 + 4096 * f4, 4096, "rows", make_cfg1))
+                       "norm_rows_vec<AddRms>", 4 * 4096 * 4096 * f4 + 4096 * f4, 4096, "rows", make_cfg1,
+                       lambda s: {"y": s[0][2], "residual": s[0][1]}))
 
     def make_cfg2(ctx, nsets):
         s = G.cfg2_softmax().reshape(-1, 1024)
@@ -104,7 +124,7 @@ def build_ops():
         del s
         return (lambda i: ctx.softmax(sets[i][0], sets[i][1], 262144, 1024, M.SOFTMAX_DIV_EPS)), sets
     ops.append(OpBench("cfg2_softmax", 2, "causal row softmax fp32 [8x32x1024x1024]", "softmax_rows_vec",
-                       2 * 262144 * 1024 * f4, 262144, "rows", make_cfg2))
+                       2 * 262144 * 1024 * f4, 262144, "rows", make_cfg2, lambda s: {"y": s[0][1]}))
 
     def make_cfg3a(ctx, nsets):
         table, ids = G.cfg3_gather()
@@ -113,7 +133,8 @@ def build_ops():
         return (lambda i: ctx.embedding(sets[i][1], 32768, sets[i][0], 32000 * 4096, 32000, 4096, -1,
                                         sets[i][2])), sets
     ops.append(OpBench("cfg3_gather", 3, "token-embedding gather table [32000x4096] ids int32 [16x2048]",
-                       "embed_vec", 32768 * 4 + 2 * 32768 * 4096 * f4, 32768, "token rows", make_cfg3a))
+                       "embed_vec", 32768 * 4 + 2 * 32768 * 4096 * f4, 32768, "token rows", make_cfg3a,
+                       lambda s: {"y": s[0][2]}))
 
     def make_cfg3b(ctx, nsets):
         q, k, theta = G.cfg3_rope()
@@ -122,9 +143,10 @@ def build_ops():
         sets = _replicate(ctx, [q, k], nsets)
         del q, k
         return (lambda i: ctx.rope(sets[i][0], sets[i][0], 32, sets[i][1], sets[i][1], 32, 16, 2048, 128, 0,
-                                   cs[0], cs[1], 2048)), sets
+                                   cs[0], cs[1], 2048)), sets + [cs]
     ops.append(OpBench("cfg3_rope", 3, "RoPE q,k [16x2048x32x128] in place, one launch", "rope_vec",
-                       2 * 2 * 16 * 2048 * 32 * 128 * f4, 2 * 16 * 2048 * 32, "head rows", make_cfg3b))
+                       2 * 2 * 16 * 2048 * 32 * 128 * f4, 2 * 16 * 2048 * 32, "head rows", make_cfg3b,
+                       lambda s: {"q": s[0][0], "k": s[0][1]}))
 
     ops.append(ln_op("cfg4_layernorm", 4, G.cfg4_layernorm, 8192, 4096))
 
@@ -133,21 +155,22 @@ def build_ops():
         sets = _replicate(ctx, [a, np.empty_like(a)], nsets)
         return (lambda i: ctx.gelu(sets[i][0], sets[i][1], a.size)), sets
     ops.append(OpBench("cfg4_gelu", 4, "tanh-GELU fp32 [8192x11008]", "unary_vec<Gelu>",
-                       2 * 8192 * 11008 * f4, 8192, "rows", make_gelu))
+                       2 * 8192 * 11008 * f4, 8192, "rows", make_gelu, lambda s: {"y": s[0][1]}))
 
     def make_swiglu(ctx, nsets):
         g, u = G.cfg4_swiglu()
         sets = _replicate(ctx, [g, u, np.empty_like(g)], nsets)
         return (lambda i: ctx.silu_mul(sets[i][0], sets[i][1], sets[i][2], g.size)), sets
     ops.append(OpBench("cfg4_silu_mul", 4, "SiLU-gated product silu(gate)*up fp32 [8192x11008]",
-                       "binary_vec<SiluMul>", 3 * 8192 * 11008 * f4, 8192, "rows", make_swiglu))
+                       "binary_vec<SiluMul>", 3 * 8192 * 11008 * f4, 8192, "rows", make_swiglu,
+                       lambda s: {"y": s[0][2]}))
 
     def make_add(ctx, nsets):
         a, b = G.cfg4_add()
         sets = _replicate(ctx, [a, b, np.empty_like(a)], nsets)
         return (lambda i: ctx.add(sets[i][0], a.size, sets[i][1], b.size, sets[i][2])), sets
     ops.append(OpBench("cfg4_add", 4, "residual add fp32 [8192x4096]", "binary_vec<Add>",
-                       3 * 8192 * 4096 * f4, 8192, "rows", make_add))
+                       3 * 8192 * 4096 * f4, 8192, "rows", make_add, lambda s: {"y": s[0][2]}))
 
     # Backward of the same ops (Model::backwardPass branches, Model.cpp:7305-9153)
     # at the configs[3] / configs[4] shapes.
@@ -157,9 +180,10 @@ def build_ops():
         pd = _replicate(ctx, [g, np.zeros_like(g), np.zeros_like(b)], 1)[0]
         sets = _replicate(ctx, [x, dy, np.empty_like(x)], nsets)
         return (lambda i: ctx.layernorm_bwd(sets[i][0], sets[i][1], pd[0], sets[i][2], pd[1], pd[2], 8192, 4096,
-                                            eps)), sets
+                                            eps)), sets + [pd]
     ops.append(OpBench("cfg4_layernorm_bwd", 4, "LayerNorm backward fp32 [8192x4096]: dx, dgamma, dbeta",
-                       "ln_bwd_vec + slot sums", 3 * 8192 * 4096 * f4 + 5 * 4096 * f4, 8192, "rows", make_lnb))
+                       "ln_bwd_vec + slot sums", 3 * 8192 * 4096 * f4 + 5 * 4096 * f4, 8192, "rows", make_lnb,
+                       lambda s: {"dx": s[0][2], "dgamma": s[-1][1], "dbeta": s[-1][2]}))
 
     def make_act_bwd(fn_name):
         def make(ctx, nsets):
@@ -170,9 +194,9 @@ def build_ops():
             return (lambda i: fn(sets[i][0], sets[i][1], sets[i][2], a.size)), sets
         return make
     ops.append(OpBench("cfg4_gelu_bwd", 4, "GELU backward fp32 [8192x11008]", "dact_vec<DGelu>",
-                       3 * 8192 * 11008 * f4, 8192, "rows", make_act_bwd("gelu_bwd")))
+                       3 * 8192 * 11008 * f4, 8192, "rows", make_act_bwd("gelu_bwd"), lambda s: {"dx": s[0][2]}))
     ops.append(OpBench("cfg4_silu_bwd", 4, "SiLU backward fp32 [8192x11008]", "dact_vec<DSilu>",
-                       3 * 8192 * 11008 * f4, 8192, "rows", make_act_bwd("silu_bwd")))
+                       3 * 8192 * 11008 * f4, 8192, "rows", make_act_bwd("silu_bwd"), lambda s: {"dx": s[0][2]}))
 
     def make_mulb(ctx, nsets):
         g, u = G.cfg4_swiglu()
@@ -180,14 +204,14 @@ def build_ops():
         sets = _replicate(ctx, [g, u, dy, np.empty_like(g), np.empty_like(g)], nsets)
         return (lambda i: ctx.mul_bwd(sets[i][0], sets[i][1], sets[i][2], sets[i][3], sets[i][4], g.size)), sets
     ops.append(OpBench("cfg4_mul_bwd", 4, "Multiply backward fp32 [8192x11008]: da, db", "mul_bwd_vec",
-                       5 * 8192 * 11008 * f4, 8192, "rows", make_mulb))
+                       5 * 8192 * 11008 * f4, 8192, "rows", make_mulb, lambda s: {"da": s[0][3], "db": s[0][4]}))
 
     def make_addb(ctx, nsets):
         a, _ = G.cfg4_add()
         sets = _replicate(ctx, [a, np.empty_like(a), np.empty_like(a)], nsets)
         return (lambda i: ctx.add_bwd(sets[i][0], a.size, a.size, sets[i][1], sets[i][2])), sets
     ops.append(OpBench("cfg4_add_bwd", 4, "residual Add backward fp32 [8192x4096]: da, db", "add_bwd_vec",
-                       3 * 8192 * 4096 * f4, 8192, "rows", make_addb))
+                       3 * 8192 * 4096 * f4, 8192, "rows", make_addb, lambda s: {"da": s[0][1], "db": s[0][2]}))
 
     uniq3 = int(np.unique(G.cfg3_ids()).size)
 
@@ -201,7 +225,8 @@ def build_ops():
     ops.append(OpBench("cfg3_embedding_bwd", 3,
                        f"Embedding backward (scatter-add) ids int32 [16x2048] -> table grad [32000x4096], "
                        f"{uniq3} distinct ids", "radix sort + embed_bwd_rows_vec",
-                       32768 * 4 + 32768 * 4096 * f4 + 2 * uniq3 * 4096 * f4, 32768, "token rows", make_embb))
+                       32768 * 4 + 32768 * 4096 * f4 + 2 * uniq3 * 4096 * f4, 32768, "token rows", make_embb,
+                       lambda s: {"grad": s[-1][0]}))
 
     # The device-resident runtime (mimir_store_run): a residual block's chain
     # of the path's layers at the configs[4] shape, routed by name as
@@ -217,21 +242,16 @@ def build_ops():
     def make_block(ctx, nsets):
         x, res = G.cfg4_add()
         gate = G.cfg4_grad((8192, 4096), 11)
-        _, g, b, _ = G.cfg4_layernorm(rows=1)
-        layers = [dict(name="res_add", type="Add", inputs=["x", "res"], output="h"),
-                  dict(name="ln", type="LayerNorm", inputs=["h"], output="n", in_features=4096, eps=1e-5,
-                       weights=np.concatenate([g, b])),
-                  dict(name="act", type="GELU", inputs=["n"], output="g"),
-                  dict(name="gate", type="Multiply", inputs=["g", "gate"], output="m"),
-                  dict(name="silu", type="SiLU", inputs=["m"], output="y")]
+        layers = block_layers()
         graph = M.DeviceGraph(ctx, layers)
         store = M.Store(ctx)
-        store.set_inputs({"x": x, "res": res, "gate": gate}, {})
+        store.set_inputs({"inp": x, "res": res, "gate": gate}, {})
         store.run(graph)  # fills the buffer pool: later runs allocate nothing
         return (lambda i: store.run(graph)), [[_Owned(store, graph)]]
     blk = OpBench("cfg4_runtime_block", 4,
                   "device-resident runtime: Add -> LayerNorm -> GELU -> Multiply -> SiLU on [8192x4096], routed by name",
-                  "mimir_store_run (5 kernels)", 12 * 8192 * 4096 * f4 + 2 * 4096 * f4, 8192, "rows", make_block)
+                  "mimir_store_run (5 kernels)", 12 * 8192 * 4096 * f4 + 2 * 4096 * f4, 8192, "rows", make_block,
+                  lambda s: {"x": s[0][0].objs[0].get("x")})
     blk.nsets = lambda: 1
     ops.append(blk)
 
@@ -444,18 +464,12 @@ def cpu_leg(which, reps):
             rows = 1024
             x, res = G.cfg4_add(rows=rows)
             gate = G.cfg4_grad((8192, 4096), 11)[:rows]
-            _, g, b, _ = G.cfg4_layernorm(rows=1)
-            layers = [dict(name="res_add", type="Add", inputs=["x", "res"], output="h"),
-                      dict(name="ln", type="LayerNorm", inputs=["h"], output="n", in_features=4096, eps=1e-5,
-                           weights=np.concatenate([g, b])),
-                      dict(name="act", type="GELU", inputs=["n"], output="g"),
-                      dict(name="gate", type="Multiply", inputs=["g", "gate"], output="m"),
-                      dict(name="silu", type="SiLU", inputs=["m"], output="y")]
+            layers = block_layers()
             sys.path.insert(0, os.path.join(REPO, "oracle"))
             import model_ref as MR
-            nb = 12 * x.nbytes + 2 * g.nbytes
+            nb = 12 * x.nbytes + 2 * 4096 * 4
             if MR.available():
-                t = MR.time_forward_named(layers, {"x": x, "res": res, "gate": gate}, {}, reps)
+                t = MR.time_forward_named(layers, {"inp": x, "res": res, "gate": gate}, {}, reps)
                 rec(key, t, nb, rows, "reference",
                     f"{rows} of 8192 rows: Model::forwardPassNamed of the same five layers (host tensor store)")
         elif key == "cfg3_embedding_bwd":
@@ -467,6 +481,170 @@ def cpu_leg(which, reps):
             u = int(np.unique(ids).size)
             rec(key, t, ids.nbytes + dy.nbytes + 2 * u * 4096 * 4, 4096, "port",
                 f"first 4096 of 32768 tokens ({u} distinct ids), oracle embedding_bwd_i32 into a resident table")
+    return out
+
+
+def _agreement(got, ref, bitexact, scale=None):
+    """Max |d| and max |d|/|ref| of got against ref, and whether every element
+    meets the path's rule: NaN where ref is NaN, equal infinities, and
+    |d| <= max(1e-6, 1e-5 |ref|) elsewhere (or equal bits, for the byte-exact
+    ops).  For results that are float32 sums of many terms, `scale` is the sum
+    of the terms' magnitudes and replaces |ref| where larger: two summation
+    orders differ by ~u * scale however much the sum cancels."""
+    g = np.ascontiguousarray(got, np.float32).ravel()
+    r = np.ascontiguousarray(ref, np.float32).ravel()
+    assert g.size == r.size, f"{g.size} != {r.size}"
+    same_bits = bool(np.array_equal(g.view(np.uint32), r.view(np.uint32)))
+    nan_ok = bool(np.array_equal(np.isnan(g), np.isnan(r)))
+    inf_r = np.isinf(r)
+    inf_ok = bool(np.array_equal(g[inf_r], r[inf_r]))
+    fin = np.isfinite(r)
+    g64, r64 = g[fin].astype(np.float64), r[fin].astype(np.float64)
+    d = np.abs(g64 - r64)
+    nz = r64 != 0
+    mag = np.abs(r64) if scale is None else np.maximum(np.abs(r64), np.asarray(scale, np.float64).ravel()[fin])
+    within = bool(nan_ok and inf_ok and np.all(d <= np.maximum(1e-6, 1e-5 * mag)))
+    rule = ("bit-identical" if bitexact else
+            "|d| <= max(1e-6, 1e-5|ref|)" if scale is None else "|d| <= max(1e-6, 1e-5 max(|ref|, sum of |terms|))")
+    return {"elements": int(g.size), "max_abs": float(d.max()) if d.size else 0.0,
+            "max_rel": float((d[nz] / np.abs(r64[nz])).max()) if nz.any() else 0.0,
+            "bitexact": same_bits, "pass": same_bits if bitexact else within, "rule": rule}
+
+
+def parity_leg(ctx, by_key, which):
+    """Part of the cpu_baseline leg, as its checker: each op of `which` runs
+    once more on freshly uploaded inputs through the same launch closure the
+    timing used, and its output is compared with the CPU path's on the same
+    inputs -- the reference's own functions (oracle/_ref) where the reference
+    has one for the op, else the C restatement (oracle/lib).  Large configs
+    compare the leading rows the CPU sample covers."""
+    sys.path.insert(0, os.path.join(REPO, "oracle"))
+    import oracle as O
+    import model_ref as MR
+    have_ref = O.ref_available()
+    out = {}
+
+    def gpu_outputs(op, rows_like):
+        step, sets = op.make(ctx, 1)
+        try:
+            step(0)
+            ctx.sync()
+            got = {}
+            for name, dev in op.outputs(sets).items():
+                like = rows_like[name]
+                if isinstance(dev, np.ndarray):
+                    got[name] = dev.ravel()[:like.size].reshape(like.shape)
+                else:
+                    host = np.empty(like.shape, dev.dtype)
+                    ctx.download(host, dev)
+                    got[name] = host
+            return got
+        finally:
+            for bufs in sets:
+                for b in bufs:
+                    b.free()
+
+    def check(key, refs, vs, sample, exact=(), scales=None):
+        op = by_key[key]
+        got = gpu_outputs(op, refs)
+        scales = scales or {}
+        res = {n: _agreement(got[n], refs[n], n in exact, scales.get(n)) for n in refs}
+        out[key] = {"vs": vs, "sample": sample, "pass": all(r["pass"] for r in res.values()), "outputs": res}
+        log(f"parity {key}: {'pass' if out[key]['pass'] else 'FAIL'} vs {vs} "
+            + ", ".join(f"{n} max_abs {r['max_abs']:.3g}" for n, r in res.items()))
+
+    ref_or_port = "reference" if have_ref else "port"
+    for key in which:
+        if key not in by_key or by_key[key].outputs is None:
+            continue
+        if key in ("cfg0_layernorm", "cfg4_layernorm"):
+            x, g, b, eps = G.cfg0_layernorm() if key == "cfg0_layernorm" else G.cfg4_layernorm(rows=1024)
+            rows, cols = x.shape
+            y = (O.ref_layernorm(x, cols, np.concatenate([g, b]), eps=eps) if have_ref
+                 else O.layernorm(x, cols, g, b, eps))
+            check(key, {"y": y.reshape(x.shape)}, ref_or_port, f"first {rows} rows")
+        elif key == "cfg1_add_rmsnorm":
+            x, r, w, eps = G.cfg1_add_rmsnorm()
+            if have_ref:
+                h = O.ref_add(x, r).reshape(x.shape)
+                y = O.ref_rms_norm_rows(h, w, eps)
+            else:
+                y, h = O.add_rmsnorm(x, r, w, eps)
+            check(key, {"y": y, "residual": h}, ref_or_port, "full [4096x4096]", exact=("residual",))
+        elif key == "cfg2_softmax":
+            s = G.cfg2_softmax(batch=1, heads=4).reshape(-1, 1024)
+            y = O.ref_softmax_inplace(s) if have_ref else O.softmax_rows(s)
+            check(key, {"y": y}, ref_or_port, "first 4096 of 262144 rows")
+        elif key == "cfg3_gather":
+            table, ids = G.cfg3_gather()
+            ids = ids.ravel()[:4096].copy()
+            if MR.available():
+                layers = [dict(name="tok", type="Embedding", inputs=["ids"], output="y", vocab_size=32000,
+                               embed_dim=4096, weights=table.ravel())]
+                y = MR.forward_named(layers, {}, {"ids": ids}, out_cap=ids.size * 4096).reshape(-1, 4096)
+                vs = "reference (Model::forwardPassNamed, inline gather Model.cpp:1152-1205)"
+            else:
+                y, vs = O.embedding(ids, table, 32000, 4096, -1), "port"
+            check(key, {"y": y}, vs, "first 4096 of 32768 tokens", exact=("y",))
+        elif key == "cfg3_rope":
+            q, k, theta = G.cfg3_rope(batch=1)
+            c, s = O.rope_table(2048, 128, theta)
+            check(key, {"q": O.rope(q, c, s), "k": O.rope(k, c, s)}, "port (no reference RoPE exists)",
+                  "batch 1 of 16")
+        elif key == "cfg4_gelu":
+            a = G.cfg4_gelu(rows=512)
+            y = O.ref_gelu(a) if have_ref else O.gelu(a)
+            check(key, {"y": y.reshape(a.shape)}, ref_or_port, "first 512 of 8192 rows")
+        elif key == "cfg4_silu_mul":
+            g, u = G.cfg4_swiglu(rows=512)
+            y = O.ref_mul(O.ref_silu(g), u) if have_ref else O.silu_mul(g, u)
+            check(key, {"y": y.reshape(g.shape)}, ref_or_port, "first 512 of 8192 rows")
+        elif key == "cfg4_add":
+            a, b = G.cfg4_add()
+            y = O.ref_add(a, b) if have_ref else O.add(a, b)
+            check(key, {"y": y.reshape(a.shape)}, ref_or_port, "full [8192x4096]", exact=("y",))
+        elif key == "cfg4_layernorm_bwd":
+            x, g, b, eps = G.cfg4_layernorm()
+            dy = G.cfg4_grad(x.shape, 8)
+            dx, gp = O.layernorm_bwd(x, dy, 4096, g, True, eps)
+            # Magnitudes of the terms each result sums (float64): dgamma and
+            # dbeta add over 8192 rows; dx = inv/n (n dxh - sum dxh - xhat sum dxh xhat).
+            x64, dy64 = x.astype(np.float64), dy.astype(np.float64)
+            m = x64.mean(axis=1, keepdims=True)
+            inv = 1.0 / np.sqrt(((x64 - m) ** 2).mean(axis=1, keepdims=True) + eps)
+            xh = (x64 - m) * inv
+            dxh = dy64 * g
+            dx_scale = inv * (np.abs(dxh) + np.abs(dxh.mean(axis=1, keepdims=True))
+                              + np.abs(xh * (dxh * xh).mean(axis=1, keepdims=True)))
+            check(key, {"dx": dx.reshape(x.shape), "dgamma": gp[:4096], "dbeta": gp[4096:]}, "port",
+                  "full [8192x4096]", scales={"dx": dx_scale, "dgamma": np.abs(dy64 * xh).sum(axis=0),
+                                              "dbeta": np.abs(dy64).sum(axis=0)})
+        elif key in ("cfg4_gelu_bwd", "cfg4_silu_bwd"):
+            a = G.cfg4_gelu(rows=512)
+            dy = G.cfg4_grad((8192, 11008), 9)[:512]
+            fn = O.gelu_bwd if key == "cfg4_gelu_bwd" else O.silu_bwd
+            check(key, {"dx": fn(a, dy)}, "port", "first 512 of 8192 rows")
+        elif key == "cfg4_mul_bwd":
+            g, u = G.cfg4_swiglu(rows=512)
+            dy = G.cfg4_grad((8192, 11008), 10)[:512]
+            da, db = O.mul_bwd(g, u, dy)
+            check(key, {"da": da, "db": db}, "port", "first 512 of 8192 rows", exact=("da", "db"))
+        elif key == "cfg4_add_bwd":
+            a, _ = G.cfg4_add()
+            check(key, {"da": a, "db": a}, "port (accumulate_grad into absent names copies dy)",
+                  "full [8192x4096]", exact=("da", "db"))
+        elif key == "cfg3_embedding_bwd":
+            gt = O.embedding_bwd(G.cfg3_ids(), G.cfg3_embedding_grad(), np.zeros(32000 * 4096, np.float32),
+                                 32000, 4096, -1)
+            check(key, {"grad": gt}, "port", "full table [32000x4096], all 32768 tokens", exact=("grad",))
+        elif key == "cfg4_runtime_block" and MR.available():
+            rows = 1024
+            x, res = G.cfg4_add(rows=rows)
+            gate = G.cfg4_grad((8192, 4096), 11)[:rows]
+            layers = block_layers()
+            y = MR.forward_named(layers, {"inp": x, "res": res, "gate": gate}, {})
+            check(key, {"x": y}, "reference (Model::forwardPassNamed of the same five layers)",
+                  f"first {rows} of 8192 rows")
     return out
 
 
@@ -576,19 +754,26 @@ def main():
         sweep.append(r)
         if "cfg3_safetensors_ingest" not in keys:
             keys = keys + ["cfg3_safetensors_ingest"]
-    ctx.close()
 
-    cpu = {}
+    cpu, parity = {}, {}
     if args.cpu != "none":
+        which = [head.key] if args.cpu == "workload" else keys or [head.key]
         try:
-            cpu = cpu_leg([head.key] if args.cpu == "workload" else keys or [head.key], args.cpu_reps)
+            cpu = cpu_leg(which, args.cpu_reps)
         except Exception as e:  # the baseline is reported, never required
             log(f"cpu baseline unavailable: {e}")
+        try:
+            parity = parity_leg(ctx, by_key, which)
+        except Exception as e:
+            log(f"parity check unavailable: {e}")
+    ctx.close()
     for r in sweep:
         if r["op"] in cpu:
             r["cpu_GB_s"] = cpu[r["op"]]["value"]
             r["cpu_kind"] = cpu[r["op"]]["kind"]
             r["speedup_vs_cpu"] = round(r["GB_s"] / cpu[r["op"]]["value"], 1)
+        if r["op"] in parity:
+            r["parity"] = parity[r["op"]]
 
     traffic = load_traffic(head.key)
     host = {"cpu_model": cpu_model(), "nproc": os.cpu_count()}
@@ -634,6 +819,7 @@ def main():
         "cpu_baseline": None if cb is None else {
             "value": cb["value"], "unit": cb["unit"], "cores": cb["cores"], "kind": cb["kind"],
             "sample": cb["sample"], "rows_per_s": cb["rows_per_s"], **host},
+        "parity": parity.get(head.key),
         "ops": sweep,
     }
     print(json.dumps(line), flush=True)
