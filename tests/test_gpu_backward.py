@@ -296,6 +296,40 @@ def test_embedding_bwd_bitexact(ctx, vocab, dim, n, pad, float_ids):
             d.free()
 
 
+def _embedding_bwd_gpu(c, ids, dy, gt, vocab, dim, pad):
+    bi, bdy, bg = c.to_device(ids), c.to_device(dy), c.to_device(gt)
+    try:
+        c.embedding_bwd(bi, ids.size, bdy, bg, gt.size, vocab, dim, pad)
+        return bg.numpy()
+    finally:
+        for d in (bi, bdy, bg):
+            d.free()
+
+
+@pytest.mark.parametrize("case", ["262144 tokens", "long runs", "padding block"])
+def test_embedding_bwd_repeats(ctx, case):
+    """Many tokens per id: a 64-id table hit by 2^18 tokens (runs of ~4000,
+    padding and out-of-range ids mixed in), blocks of 4096 tokens of a single
+    id, and a block of padding only.  The adds stay in token order."""
+    vocab, dim, pad = 64, 8, -1
+    if case == "262144 tokens":
+        n = 64 * 4096
+        ids = rng.integers(-1, vocab + 1, n).astype(np.int32)
+    elif case == "long runs":
+        n = 3 * 4096 + 7
+        ids = np.full(n, 5, np.int32)
+        ids[4096:8192] = 7
+    else:
+        pad = 2
+        n = 2 * 4096 + 100
+        ids = rng.integers(0, vocab, n).astype(np.int32)
+        ids[4096:8192] = pad
+    dy = rng.standard_normal((n, dim)).astype(np.float32)
+    gt = rng.standard_normal(vocab * dim).astype(np.float32)
+    ref = O.embedding_bwd(ids, dy, gt, vocab, dim, pad)
+    assert_bitexact(_embedding_bwd_gpu(ctx, ids, dy, gt, vocab, dim, pad), ref, case)
+
+
 def test_embedding_bwd_unaligned_rows_and_errors(ctx):
     vocab, dim, n = 9, 5, 300
     ids = rng.integers(0, vocab, n).astype(np.int32)
