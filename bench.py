@@ -769,9 +769,12 @@ def main():
     ctx.close()
     for r in sweep:
         if r["op"] in cpu:
-            r["cpu_GB_s"] = cpu[r["op"]]["value"]
-            r["cpu_kind"] = cpu[r["op"]]["kind"]
-            r["speedup_vs_cpu"] = round(r["GB_s"] / cpu[r["op"]]["value"], 1)
+            c = cpu[r["op"]]
+            r["cpu_GB_s"] = c["value"]
+            r["cpu_kind"] = c["kind"]
+            r["cpu_us_sample"] = round(c["seconds"] * 1e6, 1)
+            r["cpu_sample"] = c["sample"]
+            r["speedup_vs_cpu"] = round(r["GB_s"] / c["value"], 1)
         if r["op"] in parity:
             r["parity"] = parity[r["op"]]
 
