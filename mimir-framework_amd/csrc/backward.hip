@@ -1004,6 +1004,14 @@ __global__ __launch_bounds__(kBlock) void embed_bwd_rows_scalar(const uint32_t* 
 
 size_t align256(size_t b) { return (b + 255) & ~size_t(255); }
 
+// The (id, token) sort.  Below rocPRIM's merge-sort limit (2^20 pairs) its
+// device radix sort is a block sort followed by merge passes; 8192-pair
+// blocks (512 threads x 16) need two passes at 32768 tokens.  Measured on
+// MI355X at configs[3] (32768 pairs, 15-bit keys): 28.4 us, against 33.2 us
+// for the default 1024-pair blocks (five passes), 40 us for 16384-pair
+// blocks and 60 us for onesweep.
+using EmbedSortConfig = rocprim::radix_sort_config<rocprim::default_config, rocprim::merge_sort_config<512, 512, 16>>;
+
 template <int MODE>
 int embed_bwd(mimir_ctx* ctx, const void* ids, int64_t n_ids, const float* dy, float* grad, int64_t table_len,
               int32_t vocab, int32_t dim, int32_t pad) {
@@ -1022,7 +1030,7 @@ int embed_bwd(mimir_ctx* ctx, const void* ids, int64_t n_ids, const float* dy, f
     unsigned end_bit = 1;
     while (end_bit < 32 && (static_cast<uint32_t>(vocab) >> end_bit) != 0) ++end_bit;
     size_t sort_bytes = 0;
-    hipError_t e = rocprim::radix_sort_pairs(nullptr, sort_bytes, static_cast<const uint32_t*>(nullptr),
+    hipError_t e = rocprim::radix_sort_pairs<EmbedSortConfig>(nullptr, sort_bytes, static_cast<const uint32_t*>(nullptr),
                                              static_cast<uint32_t*>(nullptr), static_cast<const uint32_t*>(nullptr),
                                              static_cast<uint32_t*>(nullptr), n, 0u, end_bit, ctx->stream);
     if (e != hipSuccess) return hip_fail(ctx, e, "radix_sort_pairs (size)");
@@ -1037,7 +1045,7 @@ int embed_bwd(mimir_ctx* ctx, const void* ids, int64_t n_ids, const float* dy, f
     void* temp = base + 4 * vec;
     embed_bwd_keys<MODE><<<(n + kBlock - 1) / kBlock, kBlock, 0, ctx->stream>>>(ids, n_ids, vocab, pad, keys, toks);
     if (int st = launched(ctx, "embed_bwd_keys")) return st;
-    e = rocprim::radix_sort_pairs(temp, sort_bytes, static_cast<const uint32_t*>(keys), skeys,
+    e = rocprim::radix_sort_pairs<EmbedSortConfig>(temp, sort_bytes, static_cast<const uint32_t*>(keys), skeys,
                                   static_cast<const uint32_t*>(toks), stoks, n, 0u, end_bit, ctx->stream);
     if (e != hipSuccess) return hip_fail(ctx, e, "radix_sort_pairs");
     if ((dim % 4) == 0 && aligned16(dy) && aligned16(grad)) {
