@@ -34,6 +34,8 @@
 #include <math.h>
 
 #include <rocprim/device/device_radix_sort.hpp>
+#include <rocprim/iterator/counting_iterator.hpp>
+#include <rocprim/iterator/transform_iterator.hpp>
 
 #pragma clang fp contract(off)
 
@@ -904,18 +906,21 @@ int ln_bwd_generic_run(mimir_ctx* ctx, LnBwdArgs a, float* dgamma, float* dbeta)
 // Embedding backward (Model.cpp:7429-7461)
 // ---------------------------------------------------------------------------
 
-// Sort keys: the id, or `vocab` (sorted last, skipped) for the padding id and
-// ids outside [0, vocab) (Model.cpp:7454-7455).
+// Sort key of token t: its id, or `vocab` (sorted last, skipped) for the
+// padding id and ids outside [0, vocab) (Model.cpp:7454-7455).  The sort
+// reads the keys through this (a transform iterator over the token index)
+// and the token indices from a counting iterator, so nothing is staged.
 template <int MODE>
-__global__ __launch_bounds__(kBlock) void embed_bwd_keys(const void* ids, int64_t n, int32_t vocab, int32_t pad,
-                                                         uint32_t* keys, uint32_t* toks) {
-    const int64_t t = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
-    if (t >= n) return;
-    const int32_t id = load_id<MODE>(ids, t);
-    const bool use = !(pad >= 0 && id == pad) && id >= 0 && id < vocab;
-    keys[t] = use ? static_cast<uint32_t>(id) : static_cast<uint32_t>(vocab);
-    toks[t] = static_cast<uint32_t>(t);
-}
+struct EmbedKey {
+    const void* ids;
+    int32_t vocab;
+    int32_t pad;
+    __device__ uint32_t operator()(int64_t t) const {
+        const int32_t id = load_id<MODE>(ids, t);
+        const bool use = !(pad >= 0 && id == pad) && id >= 0 && id < vocab;
+        return use ? static_cast<uint32_t>(id) : static_cast<uint32_t>(vocab);
+    }
+};
 
 // The end of the run of `id` that starts at sorted position i: each wave
 // checks 64 keys per step and takes the first mismatch from a ballot (the
@@ -1029,24 +1034,24 @@ int embed_bwd(mimir_ctx* ctx, const void* ids, int64_t n_ids, const float* dy, f
     const unsigned n = static_cast<unsigned>(n_ids);
     unsigned end_bit = 1;
     while (end_bit < 32 && (static_cast<uint32_t>(vocab) >> end_bit) != 0) ++end_bit;
+    const auto keys = rocprim::make_transform_iterator(rocprim::counting_iterator<int64_t>(0),
+                                                       EmbedKey<MODE>{ids, vocab, pad});
+    const rocprim::counting_iterator<uint32_t> toks(0);
     size_t sort_bytes = 0;
-    hipError_t e = rocprim::radix_sort_pairs<EmbedSortConfig>(nullptr, sort_bytes, static_cast<const uint32_t*>(nullptr),
-                                             static_cast<uint32_t*>(nullptr), static_cast<const uint32_t*>(nullptr),
-                                             static_cast<uint32_t*>(nullptr), n, 0u, end_bit, ctx->stream);
+    hipError_t e = rocprim::radix_sort_pairs<EmbedSortConfig>(nullptr, sort_bytes, keys,
+                                                              static_cast<uint32_t*>(nullptr), toks,
+                                                              static_cast<uint32_t*>(nullptr), n, 0u, end_bit,
+                                                              ctx->stream);
     if (e != hipSuccess) return hip_fail(ctx, e, "radix_sort_pairs (size)");
-    const size_t vec = align256(sizeof(uint32_t) * n);
+    const size_t vbytes = align256(sizeof(uint32_t) * n);
     void* s = nullptr;
-    if (int st = ensure_scratch(ctx, 4 * vec + align256(sort_bytes), &s)) return st;
+    if (int st = ensure_scratch(ctx, 2 * vbytes + align256(sort_bytes), &s)) return st;
     char* base = static_cast<char*>(s);
-    uint32_t* keys = reinterpret_cast<uint32_t*>(base);
-    uint32_t* toks = reinterpret_cast<uint32_t*>(base + vec);
-    uint32_t* skeys = reinterpret_cast<uint32_t*>(base + 2 * vec);
-    uint32_t* stoks = reinterpret_cast<uint32_t*>(base + 3 * vec);
-    void* temp = base + 4 * vec;
-    embed_bwd_keys<MODE><<<(n + kBlock - 1) / kBlock, kBlock, 0, ctx->stream>>>(ids, n_ids, vocab, pad, keys, toks);
-    if (int st = launched(ctx, "embed_bwd_keys")) return st;
-    e = rocprim::radix_sort_pairs<EmbedSortConfig>(temp, sort_bytes, static_cast<const uint32_t*>(keys), skeys,
-                                  static_cast<const uint32_t*>(toks), stoks, n, 0u, end_bit, ctx->stream);
+    uint32_t* skeys = reinterpret_cast<uint32_t*>(base);
+    uint32_t* stoks = reinterpret_cast<uint32_t*>(base + vbytes);
+    void* temp = base + 2 * vbytes;
+    e = rocprim::radix_sort_pairs<EmbedSortConfig>(temp, sort_bytes, keys, skeys, toks, stoks, n, 0u, end_bit,
+                                                   ctx->stream);
     if (e != hipSuccess) return hip_fail(ctx, e, "radix_sort_pairs");
     if ((dim % 4) == 0 && aligned16(dy) && aligned16(grad)) {
         // Measured on MI355X at dim 4096 (MIMIR_TUNE gather=256/512/1024 picks a
