@@ -22,10 +22,17 @@ def err_stats(got, ref):
     return float(d.max()), float(rel.max()), float((d / tol).max())
 
 
-def assert_close(got, ref, what="", rel=REL, abs_=ABS):
+def _nonempty(a, what, allow_empty):
+    # A comparison of nothing proves nothing: an empty result fails unless the
+    # test says an empty result is what it expects.
+    assert allow_empty or np.asarray(a).size > 0, f"{what}: nothing to compare (empty result)"
+
+
+def assert_close(got, ref, what="", rel=REL, abs_=ABS, allow_empty=False):
     got = np.asarray(got)
     ref = np.asarray(ref)
     assert got.shape == ref.shape, f"{what}: shape {got.shape} != {ref.shape}"
+    _nonempty(ref, what, allow_empty)
     g = got.astype(np.float64).ravel()
     r = ref.astype(np.float64).ravel()
     nan_r = np.isnan(r)
@@ -44,10 +51,11 @@ def assert_close(got, ref, what="", rel=REL, abs_=ABS):
             f"index {idx}: got {g[idx]!r} ref {r[idx]!r} (|d|={abs(g[idx]-r[idx]):.3g})")
 
 
-def assert_bitexact(got, ref, what=""):
+def assert_bitexact(got, ref, what="", allow_empty=False):
     got = np.ascontiguousarray(got)
     ref = np.ascontiguousarray(ref)
     assert got.shape == ref.shape, f"{what}: shape {got.shape} != {ref.shape}"
+    _nonempty(ref, what, allow_empty)
     gv = got.view(np.uint32) if got.dtype.itemsize == 4 else got.view(np.uint8)
     rv = ref.view(np.uint32) if ref.dtype.itemsize == 4 else ref.view(np.uint8)
     diff = np.flatnonzero(gv.ravel() != rv.ravel())
@@ -55,7 +63,7 @@ def assert_bitexact(got, ref, what=""):
                             f"got {got.ravel()[diff[0]]!r} ref {ref.ravel()[diff[0]]!r}")
 
 
-def assert_close_or_nearer_exact(got, ref, exact, what=""):
+def assert_close_or_nearer_exact(got, ref, exact, what="", allow_empty=False):
     """For reductions over long rows.  The reference sums in float32 one
     element at a time (LayerOps.hpp:291-303, 963-967; LayerOpsExt.hpp:357-361),
     whose rounding error grows like u*sqrt(n) and passes 1e-5 relative beyond
@@ -67,6 +75,7 @@ def assert_close_or_nearer_exact(got, ref, exact, what=""):
     r = np.asarray(ref, np.float64).ravel()
     e = np.asarray(exact, np.float64).ravel()
     assert got.shape == r.shape == e.shape, what
+    _nonempty(r, what, allow_empty)
     assert np.array_equal(np.isnan(got), np.isnan(r)), f"{what}: NaN pattern differs"
     inf_r = np.isinf(r)
     assert np.array_equal(got[inf_r], r[inf_r]), f"{what}: infinities differ"
@@ -82,7 +91,7 @@ def assert_close_or_nearer_exact(got, ref, exact, what=""):
                              f"ref {r[i]!r} exact {e[i]!r}")
 
 
-def assert_close_sum(got, ref, scale, what=""):
+def assert_close_sum(got, ref, scale, what="", allow_empty=False):
     """For results that are float32 sums (gradient accumulations over tokens):
     |got - ref| <= max(1e-6, 1e-5 * max(|ref|, scale)), scale = the sum of the
     magnitudes added into the element.  Two float32 summation orders differ
@@ -92,6 +101,7 @@ def assert_close_sum(got, ref, scale, what=""):
     ref = np.asarray(ref, np.float64).ravel()
     sc = np.zeros_like(ref) if scale is None else np.asarray(scale, np.float64).ravel()
     assert got.shape == ref.shape, f"{what}: shape {got.shape} != {ref.shape}"
+    _nonempty(ref, what, allow_empty)
     assert np.array_equal(np.isnan(got), np.isnan(ref)), f"{what}: NaN pattern differs"
     fin = np.isfinite(ref)
     d = np.abs(got[fin] - ref[fin])
