@@ -33,6 +33,10 @@ constexpr int kWavesPerBlock = kBlock / kWave;
 
 // TPT threads per token row (BS / TPT token rows per workgroup), one 16-byte
 // vector per thread per pass; rows wider than TPT vectors take several passes.
+// Table rows are loaded through the caches, output rows stored non-temporal:
+// a token that repeats an id already gathered in the same launch finds the
+// row in L2 or the Infinity Cache.  At configs[3] 37% of the tokens repeat an
+// id; measured on MI355X, 157 us against 172 us with non-temporal loads.
 template <int MODE, int TPT, int BS>
 __global__ __launch_bounds__(BS) void embed_vec(GatherArgs a) {
     const int t = threadIdx.x % TPT;
@@ -44,7 +48,7 @@ __global__ __launch_bounds__(BS) void embed_vec(GatherArgs a) {
     const u4* src = reinterpret_cast<const u4*>(a.table) + (copy ? static_cast<int64_t>(id) * dim4 : 0);
     u4* dst = reinterpret_cast<u4*>(a.y) + token * dim4;
     for (int64_t c = t; c < dim4; c += TPT)
-        __builtin_nontemporal_store(copy ? __builtin_nontemporal_load(src + c) : u4(0u), dst + c);
+        __builtin_nontemporal_store(copy ? src[c] : u4(0u), dst + c);
 }
 
 // Any dim / alignment: one wavefront per token, 32-bit words.
