@@ -58,6 +58,14 @@ void* mimir_ctx_stream(mimir_ctx* ctx);
 /* Cap on the bytes mimir_malloc may hold at once (0 = no cap).  Mirrors
  * MemoryGuard::setLimit (MemoryGuard.hpp:75-130): over the cap -> ENOMEM. */
 int mimir_ctx_set_alloc_limit(mimir_ctx* ctx, size_t bytes);
+/* Output store policy of the ops enqueued after this call.  0 (default):
+ * outputs are streamed to HBM with non-temporal stores, the fastest form
+ * for an op whose result is not read again soon.  1: plain stores, which
+ * leave the output in L2 / the Infinity Cache (256 MiB), so an op launched
+ * next that reads it finds much of it there -- a chain of layers.  The
+ * device-resident runtime (mimir_store_run) sets it for every layer but the
+ * last.  No counterpart in the reference (its ops run on host vectors). */
+int mimir_ctx_set_output_caching(mimir_ctx* ctx, int keep);
 /* Message for the last non-OK status returned on this context. */
 const char* mimir_last_error(const mimir_ctx* ctx);
 

@@ -27,13 +27,15 @@ struct GatherArgs {
     int32_t dim;
     int32_t pad;
     float* y;
+    int keep;  // y through the caches (mimir_ctx_set_output_caching)
 };
 
 constexpr int kWavesPerBlock = kBlock / kWave;
 
 // TPT threads per token row (BS / TPT token rows per workgroup), one 16-byte
 // vector per thread per pass; rows wider than TPT vectors take several passes.
-// Table rows are loaded through the caches, output rows stored non-temporal:
+// Table rows are loaded through the caches, output rows stored non-temporal
+// (unless the context keeps outputs cached for a consumer launched next):
 // a token that repeats an id already gathered in the same launch finds the
 // row in L2 or the Infinity Cache.  At configs[3] 37% of the tokens repeat an
 // id; measured on MI355X, 157 us against 172 us with non-temporal loads.
@@ -47,8 +49,11 @@ __global__ __launch_bounds__(BS) void embed_vec(GatherArgs a) {
     const int64_t dim4 = a.dim >> 2;
     const u4* src = reinterpret_cast<const u4*>(a.table) + (copy ? static_cast<int64_t>(id) * dim4 : 0);
     u4* dst = reinterpret_cast<u4*>(a.y) + token * dim4;
-    for (int64_t c = t; c < dim4; c += TPT)
-        __builtin_nontemporal_store(copy ? src[c] : u4(0u), dst + c);
+    for (int64_t c = t; c < dim4; c += TPT) {
+        const u4 v = copy ? src[c] : u4(0u);
+        if (a.keep) dst[c] = v;
+        else __builtin_nontemporal_store(v, dst + c);
+    }
 }
 
 // Any dim / alignment: one wavefront per token, 32-bit words.
@@ -78,7 +83,7 @@ int run(mimir_ctx* ctx, const void* ids, int64_t n_ids, const float* table, int6
     if (n_ids == 0) return MIMIR_OK;
     MIMIR_REQUIRE(ctx, ids && table && y, "Embedding: null tensor");
     MIMIR_ENTER(ctx);
-    const GatherArgs a{ids, n_ids, table, vocab, dim, pad, y};
+    const GatherArgs a{ids, n_ids, table, vocab, dim, pad, y, ctx->keep_outputs};
     unsigned blocks;
     if (!grid_for(n_ids, kWavesPerBlock, &blocks))
         return fail(ctx, MIMIR_EINVAL, "Embedding: %lld ids exceed the grid limit", (long long)n_ids);

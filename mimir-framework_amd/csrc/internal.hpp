@@ -22,6 +22,7 @@ struct mimir_ctx {
     std::unordered_map<void*, size_t> allocs;
     std::string last_error;
     mimir::Tuning tune;  // launch-shape override (MIMIR_TUNE), read at creation
+    int keep_outputs = 0;  // 1: ops store outputs through the caches (mimir_ctx_set_output_caching)
     // Scratch for the partial results of multi-workgroup row reductions
     // (longrow.hip); grows on demand, reused in stream order.
     void* scratch = nullptr;

@@ -56,6 +56,7 @@ struct LongArgs {
     float* partial;  // [rows][nchunks][2]
     float* stats;    // [rows][4]
     int reverse;     // this pass walks the chunks last to first
+    int keep;        // y through the caches (mimir_ctx_set_output_caching)
 };
 
 // Passes alternate direction: a pass starts where the previous one ended, so
@@ -259,7 +260,7 @@ __global__ __launch_bounds__(kBlock) void lr_apply(LongArgs a) {
 #pragma unroll
             for (int k = 0; k < 4; ++k) o[k] = softmax_out<MODE>(v[j][k], s0, s1);
         }
-        st4<true>(a.y + base + c, o);
+        st_out(a.y + base + c, o, a.keep);
     }
 }
 
@@ -284,7 +285,7 @@ bool mimir::longrow_applies(int64_t rows, int64_t cols) {
 int mimir::longrow_norm(mimir_ctx* ctx, int kind, const float* x, const float* r, float* r_out,
                         const float* g, const float* b, int64_t w_len, float* y, int64_t rows, int64_t cols,
                         float eps) {
-    LongArgs a{x, r, r_out, g, b, w_len, y, 0, 0, 0, eps, nullptr, nullptr, 0};
+    LongArgs a{x, r, r_out, g, b, w_len, y, 0, 0, 0, eps, nullptr, nullptr, 0, ctx->keep_outputs};
     if (int st = setup(ctx, a, rows, cols)) return st;
     const dim3 grid(static_cast<unsigned>(a.nchunks), static_cast<unsigned>(rows));
     const unsigned nrows = static_cast<unsigned>(rows);
@@ -307,7 +308,7 @@ int mimir::longrow_norm(mimir_ctx* ctx, int kind, const float* x, const float* r
 }
 
 int mimir::longrow_softmax(mimir_ctx* ctx, int mode, const float* x, float* y, int64_t rows, int64_t cols) {
-    LongArgs a{x, nullptr, nullptr, nullptr, nullptr, 0, y, 0, 0, 0, 0.0f, nullptr, nullptr, 0};
+    LongArgs a{x, nullptr, nullptr, nullptr, nullptr, 0, y, 0, 0, 0, 0.0f, nullptr, nullptr, 0, ctx->keep_outputs};
     if (int st = setup(ctx, a, rows, cols)) return st;
     const dim3 grid(static_cast<unsigned>(a.nchunks), static_cast<unsigned>(rows));
     LongArgs rev = a;

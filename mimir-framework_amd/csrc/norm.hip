@@ -39,6 +39,7 @@ struct NormArgs {
     int64_t cols;
     int64_t w_len;    // RMSNorm: weight applies to columns < w_len
     float eps;
+    int keep;         // y through the caches (mimir_ctx_set_output_caching); r_out is always streamed
 };
 
 // Scale by the RMSNorm weight where the column is below w_len.
@@ -125,7 +126,7 @@ __global__ __launch_bounds__(BS) void norm_rows_vec(NormArgs a) {
                     o *= *reinterpret_cast<const f4*>(a.g + 4 * c4);
                     if (a.b) o += *reinterpret_cast<const f4*>(a.b + 4 * c4);
                 }
-                st4<true>(a.y + base + 4 * c4, o);
+                st_out(a.y + base + 4 * c4, o, a.keep);
             }
         }
     } else {
@@ -140,7 +141,7 @@ __global__ __launch_bounds__(BS) void norm_rows_vec(NormArgs a) {
             if (c4 < c4n) {
                 f4 o = v[j] / rms;
                 if (a.g) o = rms_scale(o, a.g, a.w_len, 4 * c4);
-                st4<true>(a.y + base + 4 * c4, o);
+                st_out(a.y + base + 4 * c4, o, a.keep);
             }
         }
     }
@@ -248,7 +249,7 @@ int mimir_layernorm_fwd(mimir_ctx* ctx, const float* x, const float* gamma, cons
     if (groups == 0) return MIMIR_OK;
     MIMIR_REQUIRE(ctx, x && y, "LayerNorm: null tensor");
     MIMIR_ENTER(ctx);
-    NormArgs a{x, nullptr, nullptr, gamma, beta, y, groups, n, n, eps};
+    NormArgs a{x, nullptr, nullptr, gamma, beta, y, groups, n, n, eps, ctx->keep_outputs};
     return dispatch<Norm::Layer>(ctx, a);
 }
 
@@ -260,7 +261,8 @@ int mimir_rmsnorm_fwd(mimir_ctx* ctx, const float* x, const float* w, int64_t w_
     if (rows == 0) return MIMIR_OK;
     MIMIR_REQUIRE(ctx, x && y, "RMSNorm: null tensor");
     MIMIR_ENTER(ctx);
-    NormArgs a{x, nullptr, nullptr, (w && w_len > 0) ? w : nullptr, nullptr, y, rows, cols, w ? w_len : 0, eps};
+    NormArgs a{x, nullptr, nullptr, (w && w_len > 0) ? w : nullptr, nullptr, y, rows, cols, w ? w_len : 0, eps,
+               ctx->keep_outputs};
     return dispatch<Norm::Rms>(ctx, a);
 }
 
@@ -275,7 +277,7 @@ int mimir_add_rmsnorm_fwd(mimir_ctx* ctx, const float* x, const float* residual,
     MIMIR_REQUIRE(ctx, static_cast<const void*>(y) != static_cast<const void*>(residual_out),
                   "add+RMSNorm: y must not alias residual_out");
     MIMIR_ENTER(ctx);
-    NormArgs a{x, residual, residual_out, w, nullptr, y, rows, cols, w ? cols : 0, eps};
+    NormArgs a{x, residual, residual_out, w, nullptr, y, rows, cols, w ? cols : 0, eps, ctx->keep_outputs};
     return dispatch<Norm::AddRms>(ctx, a);
 }
 

@@ -37,6 +37,7 @@ struct RopeArgs {
     int64_t q_slots;      // q head rows * Q
     int64_t total_slots;  // (q + k head rows) * Q
     int64_t pos_offset;
+    int keep;  // outputs through the caches (mimir_ctx_set_output_caching)
 };
 
 __device__ __forceinline__ void rotate(f4& x0, f4& x1, f4 c, f4 s) {
@@ -77,8 +78,8 @@ __global__ __launch_bounds__(kBlock) void rope_vec(RopeArgs a) {
     for (int j = 0; j < PPT; ++j) {
         if (out[j]) {
             rotate(x0[j], x1[j], c[j], s[j]);
-            st4<true>(out[j], x0[j]);
-            st4<true>(out[j] + a.half, x1[j]);
+            st_out(out[j], x0[j], a.keep);
+            st_out(out[j] + a.half, x1[j], a.keep);
         }
     }
 }
@@ -169,7 +170,7 @@ int mimir_rope_fwd(mimir_ctx* ctx, const float* q, float* q_out, int64_t q_heads
     const int64_t half = head_dim / 2;
     RopeArgs a{q, q_out, k, k_out, cos_tab, sin_tab,
                static_cast<uint32_t>(qh ? qh : 1), static_cast<uint32_t>(kh ? kh : 1),
-               static_cast<uint32_t>(seq), static_cast<uint32_t>(half), 0, 0, pos_offset};
+               static_cast<uint32_t>(seq), static_cast<uint32_t>(half), 0, 0, pos_offset, ctx->keep_outputs};
     bool vec = (half % 4) == 0 && aligned16(cos_tab) && aligned16(sin_tab) &&
                (!q || (aligned16(q) && aligned16(q_out))) && (!k || (aligned16(k) && aligned16(k_out)));
     const int64_t Q = half / 4;

@@ -117,6 +117,12 @@ int mimir_ctx_set_stream(mimir_ctx* ctx, void* hip_stream) {
 
 void* mimir_ctx_stream(mimir_ctx* ctx) { return ctx ? static_cast<void*>(ctx->stream) : nullptr; }
 
+int mimir_ctx_set_output_caching(mimir_ctx* ctx, int keep) {
+    if (!ctx) return MIMIR_EINVAL;
+    ctx->keep_outputs = keep ? 1 : 0;
+    return MIMIR_OK;
+}
+
 int mimir_ctx_set_alloc_limit(mimir_ctx* ctx, size_t bytes) {
     if (!ctx) return MIMIR_EINVAL;
     ctx->alloc_limit = bytes;

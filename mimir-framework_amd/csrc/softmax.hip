@@ -28,6 +28,7 @@ struct SoftmaxArgs {
     float* y;
     int64_t rows;
     int64_t cols;
+    int keep;  // y through the caches (mimir_ctx_set_output_caching)
 };
 
 template <int MODE>
@@ -98,7 +99,7 @@ __global__ __launch_bounds__(BS) void softmax_rows_vec(SoftmaxArgs a) {
             f4 o;
 #pragma unroll
             for (int k = 0; k < 4; ++k) o[k] = finish<MODE>(v[j][k], e[j][k], m, sum, aux);
-            st4<true>(a.y + base + 4 * c4, o);
+            st_out(a.y + base + 4 * c4, o, a.keep);
         }
     }
 }
@@ -162,7 +163,7 @@ extern "C" int mimir_softmax_fwd(mimir_ctx* ctx, const float* x, float* y, int64
     if (rows == 0) return MIMIR_OK;
     MIMIR_REQUIRE(ctx, x && y, "Softmax: null tensor");
     MIMIR_ENTER(ctx);
-    const SoftmaxArgs a{x, y, rows, cols};
+    const SoftmaxArgs a{x, y, rows, cols, ctx->keep_outputs};
     switch (mode) {
         case MIMIR_SOFTMAX_DIV_EPS: return dispatch<MIMIR_SOFTMAX_DIV_EPS>(ctx, a);
         case MIMIR_SOFTMAX_MUL_INV: return dispatch<MIMIR_SOFTMAX_MUL_INV>(ctx, a);

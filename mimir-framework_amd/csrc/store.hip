@@ -552,12 +552,27 @@ int mimir_store_set_inputs(mimir_store* s, const char* const* fnames, const floa
     return MIMIR_OK;
 }
 
+// Every layer but the last stores its output through the caches, where the
+// layer after it (the usual reader) finds much of it in L2 / the Infinity
+// Cache; the last layer's output is streamed, and the context's own setting
+// (mimir_ctx_set_output_caching) is restored on the way out.
+struct ChainOutputs {
+    mimir_ctx* ctx;
+    int saved;
+    explicit ChainOutputs(mimir_ctx* c) : ctx(c), saved(c->keep_outputs) {}
+    void layer(int32_t i, int32_t n) { ctx->keep_outputs = i + 1 < n ? 1 : saved; }
+    ~ChainOutputs() { ctx->keep_outputs = saved; }
+};
+
 int mimir_store_run(mimir_store* s, const mimir_layer* layers, int32_t n_layers) {
     if (!s) return MIMIR_EINVAL;
     MIMIR_REQUIRE(s->ctx, n_layers >= 0 && (n_layers == 0 || layers), "mimir_store_run: invalid argument");
     s->release_snaps();
-    for (int32_t i = 0; i < n_layers; ++i)
+    ChainOutputs chain(s->ctx);
+    for (int32_t i = 0; i < n_layers; ++i) {
+        chain.layer(i, n_layers);
         if (int st = run_layer(s, layers[i], nullptr)) return st;
+    }
     return MIMIR_OK;
 }
 
@@ -566,7 +581,9 @@ int mimir_store_run_training(mimir_store* s, const mimir_layer* layers, int32_t 
     MIMIR_REQUIRE(s->ctx, n_layers >= 0 && (n_layers == 0 || layers), "mimir_store_run_training: invalid argument");
     s->release_snaps();
     s->snaps.resize(static_cast<size_t>(n_layers));
+    ChainOutputs chain(s->ctx);
     for (int32_t i = 0; i < n_layers; ++i) {
+        chain.layer(i, n_layers);
         if (int st = run_layer(s, layers[i], &s->snaps[i])) {
             s->release_snaps();
             return st;

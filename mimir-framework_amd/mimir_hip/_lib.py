@@ -43,6 +43,7 @@ SIGNATURES = {
     "mimir_ctx_set_stream": (c_int, [_P, _P]),
     "mimir_ctx_stream": (c_void_p, [_P]),
     "mimir_ctx_set_alloc_limit": (c_int, [_P, c_size_t]),
+    "mimir_ctx_set_output_caching": (c_int, [_P, c_int]),
     "mimir_last_error": (c_char_p, [_P]),
     "mimir_malloc": (c_int, [_P, c_size_t, _PP]),
     "mimir_free": (c_int, [_P, _P]),

@@ -147,6 +147,11 @@ class Context:
     def set_alloc_limit(self, nbytes):
         self.check(self.lib.mimir_ctx_set_alloc_limit(self.handle, nbytes))
 
+    def set_output_caching(self, keep):
+        """Ops enqueued next store their outputs through the caches (keep=True),
+        for a consumer launched right after, or stream them (False, default)."""
+        self.check(self.lib.mimir_ctx_set_output_caching(self.handle, 1 if keep else 0))
+
     # -- timing ---------------------------------------------------------
     def event(self):
         return Event(self)

@@ -418,3 +418,62 @@ def test_longrow_softmax_layer_whole_vector(ctx):
     ref = O.softmax_rows(x, M.SOFTMAX_MUL_INV)[0]
     assert_close_or_nearer_exact(got, ref, X.softmax(x, 1)[0], "whole-vector softmax")
     assert abs(got.sum(dtype=np.float64) - 1.0) < 1e-5
+
+
+# ---------------------------------------------------------------------------
+# Output store policy (mimir_ctx_set_output_caching): same bits either way
+# ---------------------------------------------------------------------------
+
+def test_output_caching_gives_the_same_bits(ctx):
+    """Every op's output with outputs kept in the caches equals the streamed
+    result bit for bit (only the store instruction differs)."""
+    rows, cols = 64, 4096
+    x = rng.standard_normal((rows, cols), dtype=np.float32)
+    r = rng.standard_normal((rows, cols), dtype=np.float32)
+    g = (1 + 0.05 * rng.standard_normal(cols)).astype(np.float32)
+    b = (0.05 * rng.standard_normal(cols)).astype(np.float32)
+    long_x = rng.standard_normal(1 << 17, dtype=np.float32)
+    table = rng.standard_normal((100, 256), dtype=np.float32)
+    ids = rng.integers(-2, 102, 300).astype(np.int32)
+    q = rng.standard_normal((2, 16, 4, 64), dtype=np.float32)
+    cos_t, sin_t = M.rope_table(16, 64)
+    dev = {k: ctx.to_device(v) for k, v in dict(x=x, r=r, g=g, b=b, long_x=long_x, table=table, ids=ids, q=q,
+                                                 c=cos_t, s=sin_t).items()}
+    outs = {}
+
+    def run_all(tag):
+        res = {}
+        y = ctx.empty(x.shape)
+        h = ctx.empty(x.shape)
+        yl = ctx.empty(long_x.shape)
+        ye = ctx.empty((ids.size, 256))
+        qo = ctx.empty(q.shape)
+        try:
+            ctx.layernorm(dev["x"], dev["g"], dev["b"], y, rows, cols, 1e-5); res["ln"] = y.numpy()
+            ctx.rmsnorm(dev["x"], dev["g"], cols, y, rows, cols, 1e-6); res["rms"] = y.numpy()
+            ctx.add_rmsnorm(dev["x"], dev["r"], h, dev["g"], y, rows, cols, 1e-6)
+            res["addrms_y"], res["addrms_h"] = y.numpy(), h.numpy()
+            ctx.softmax(dev["x"], y, rows, cols); res["softmax"] = y.numpy()
+            ctx.gelu(dev["x"], y, x.size); res["gelu"] = y.numpy()
+            ctx.silu_mul(dev["x"], dev["r"], y, x.size); res["silu_mul"] = y.numpy()
+            ctx.add(dev["x"], x.size, dev["r"], r.size, y); res["add"] = y.numpy()
+            ctx.add(dev["x"], x.size, dev["g"], cols, y); res["add_repeat"] = y.numpy()
+            ctx.layernorm(dev["long_x"], None, None, yl, 1, long_x.size, 1e-5); res["ln_long"] = yl.numpy()
+            ctx.softmax(dev["long_x"], yl, 1, long_x.size); res["softmax_long"] = yl.numpy()
+            ctx.embedding(dev["ids"], ids.size, dev["table"], table.size, 100, 256, -1, ye); res["gather"] = ye.numpy()
+            ctx.rope(dev["q"], qo, 4, None, None, 0, 2, 16, 64, 0, dev["c"], dev["s"], 16); res["rope"] = qo.numpy()
+        finally:
+            for a in (y, h, yl, ye, qo):
+                a.free()
+        outs[tag] = res
+
+    try:
+        run_all("streamed")
+        ctx.set_output_caching(True)
+        run_all("kept")
+    finally:
+        ctx.set_output_caching(False)
+        for a in dev.values():
+            a.free()
+    for k, v in outs["streamed"].items():
+        assert_bitexact(outs["kept"][k], v, f"{k}: kept vs streamed")
