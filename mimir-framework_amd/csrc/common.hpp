@@ -34,13 +34,16 @@ __device__ __forceinline__ void st4(float* p, f4 v) {
     else *reinterpret_cast<f4*>(p) = v;
 }
 
-// An op's output: streamed (non-temporal) unless `keep` (a uniform kernel
-// argument), in which case a plain store leaves the line in L2 / the
-// Infinity Cache for the op launched next.  Measured on MI355X, producer ->
-// consumer through a 128 MiB tensor: 79 us with kept outputs, 92 us
-// streamed; an op whose output is not read next is ~3% faster streamed.
-__device__ __forceinline__ void st_out(float* p, f4 v, int keep) {
-    if (keep) *reinterpret_cast<f4*>(p) = v;
+// An op's output: streamed (non-temporal) unless KEEP, in which case a plain
+// store leaves the line in L2 / the Infinity Cache for the op launched next.
+// Measured on MI355X, producer -> consumer through a 128 MiB tensor: 79 us
+// with kept outputs, 92 us streamed; an op whose output is not read next is
+// ~3% faster streamed.  KEEP is a template parameter, chosen per launch: a
+// run-time flag lets the compiler merge the two stores into one plain store
+// and drop the non-temporal hint.
+template <bool KEEP>
+__device__ __forceinline__ void st_out(float* p, f4 v) {
+    if constexpr (KEEP) *reinterpret_cast<f4*>(p) = v;
     else __builtin_nontemporal_store(v, reinterpret_cast<f4*>(p));
 }
 

@@ -70,8 +70,8 @@ __device__ __forceinline__ f4 map4(F f, f4 a, f4 b) {
     return f4{f(a.x, b.x), f(a.y, b.y), f(a.z, b.z), f(a.w, b.w)};
 }
 
-template <class F, int VPT>
-__global__ __launch_bounds__(kBlock) void unary_vec(const float* x, float* y, int64_t n4, F f, int keep) {
+template <class F, int VPT, bool KEEP>
+__global__ __launch_bounds__(kBlock) void unary_vec(const float* x, float* y, int64_t n4, F f) {
     const int64_t first = static_cast<int64_t>(blockIdx.x) * VPT * kBlock + threadIdx.x;
     f4 v[VPT];
 #pragma unroll
@@ -82,13 +82,13 @@ __global__ __launch_bounds__(kBlock) void unary_vec(const float* x, float* y, in
 #pragma unroll
     for (int j = 0; j < VPT; ++j) {
         const int64_t i = first + static_cast<int64_t>(j) * kBlock;
-        if (i < n4) st_out(y + 4 * i, map4(f, v[j]), keep);
+        if (i < n4) st_out<KEEP>(y + 4 * i, map4(f, v[j]));
     }
 }
 
-template <class F, int VPT>
+template <class F, int VPT, bool KEEP>
 __global__ __launch_bounds__(kBlock) void binary_vec(const float* a, const float* b, float* y,
-                                                     int64_t n4, F f, int keep) {
+                                                     int64_t n4, F f) {
     const int64_t first = static_cast<int64_t>(blockIdx.x) * VPT * kBlock + threadIdx.x;
     f4 va[VPT], vb[VPT];
 #pragma unroll
@@ -102,7 +102,7 @@ __global__ __launch_bounds__(kBlock) void binary_vec(const float* a, const float
 #pragma unroll
     for (int j = 0; j < VPT; ++j) {
         const int64_t i = first + static_cast<int64_t>(j) * kBlock;
-        if (i < n4) st_out(y + 4 * i, map4(f, va[j], vb[j]), keep);
+        if (i < n4) st_out<KEEP>(y + 4 * i, map4(f, va[j], vb[j]));
     }
 }
 
@@ -133,14 +133,15 @@ __global__ __launch_bounds__(kBlock) void add_scalar_kernel(const float* big, co
 // add_forward repeat broadcast, LayerOps.hpp:194-197: y[i] = big[i] + small[i % small_n],
 // as `rows` rows of small_n.  Each thread keeps its 16 bytes of `small` in
 // registers and walks the rows (blockIdx.y strided).
+template <bool KEEP>
 __global__ __launch_bounds__(kBlock) void add_repeat_vec(const float* big, const float* small,
-                                                         float* y, int64_t rows, int64_t small_n4, int keep) {
+                                                         float* y, int64_t rows, int64_t small_n4) {
     const int64_t c4 = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
     if (c4 >= small_n4) return;
     const f4 s = *reinterpret_cast<const f4*>(small + 4 * c4);
     for (int64_t r = blockIdx.y; r < rows; r += gridDim.y) {
         const int64_t i = r * small_n4 + c4;
-        st_out(y + 4 * i, ld4<true>(big + 4 * i) + s, keep);
+        st_out<KEEP>(y + 4 * i, ld4<true>(big + 4 * i) + s);
     }
 }
 
@@ -161,7 +162,8 @@ int launch_unary(mimir_ctx* ctx, const float* x, float* y, int64_t n4, F f, cons
     unsigned blocks;
     if (!grid_for(n4, static_cast<int64_t>(VPT) * kBlock, &blocks))
         return fail(ctx, MIMIR_EINVAL, "%s: n=%lld exceeds the grid limit", name, (long long)(4 * n4));
-    unary_vec<F, VPT><<<blocks, kBlock, 0, ctx->stream>>>(x, y, n4, f, ctx->keep_outputs);
+    if (ctx->keep_outputs) unary_vec<F, VPT, true><<<blocks, kBlock, 0, ctx->stream>>>(x, y, n4, f);
+    else unary_vec<F, VPT, false><<<blocks, kBlock, 0, ctx->stream>>>(x, y, n4, f);
     return launched(ctx, name);
 }
 
@@ -171,7 +173,8 @@ int launch_binary(mimir_ctx* ctx, const float* a, const float* b, float* y, int6
     unsigned blocks;
     if (!grid_for(n4, static_cast<int64_t>(VPT) * kBlock, &blocks))
         return fail(ctx, MIMIR_EINVAL, "%s: n=%lld exceeds the grid limit", name, (long long)(4 * n4));
-    binary_vec<F, VPT><<<blocks, kBlock, 0, ctx->stream>>>(a, b, y, n4, f, ctx->keep_outputs);
+    if (ctx->keep_outputs) binary_vec<F, VPT, true><<<blocks, kBlock, 0, ctx->stream>>>(a, b, y, n4, f);
+    else binary_vec<F, VPT, false><<<blocks, kBlock, 0, ctx->stream>>>(a, b, y, n4, f);
     return launched(ctx, name);
 }
 
@@ -299,7 +302,10 @@ int mimir_add_fwd(mimir_ctx* ctx, const float* a, int64_t na, const float* b, in
         // Enough rows per launch to give every CU work; each thread then strides rows.
         const int64_t want_y = (static_cast<int64_t>(2048) + bx - 1) / bx;
         const unsigned by = static_cast<unsigned>(rows < want_y ? rows : (want_y > 65535 ? 65535 : want_y));
-        add_repeat_vec<<<dim3(bx, by), kBlock, 0, ctx->stream>>>(big, small, y, rows, small_n4, ctx->keep_outputs);
+        if (ctx->keep_outputs)
+            add_repeat_vec<true><<<dim3(bx, by), kBlock, 0, ctx->stream>>>(big, small, y, rows, small_n4);
+        else
+            add_repeat_vec<false><<<dim3(bx, by), kBlock, 0, ctx->stream>>>(big, small, y, rows, small_n4);
         return launched(ctx, "add_repeat_vec");
     }
     add_repeat_scalar<<<stride_grid(big_n), kBlock, 0, ctx->stream>>>(big, small, y, big_n, small_n);

@@ -27,7 +27,6 @@ struct GatherArgs {
     int32_t dim;
     int32_t pad;
     float* y;
-    int keep;  // y through the caches (mimir_ctx_set_output_caching)
 };
 
 constexpr int kWavesPerBlock = kBlock / kWave;
@@ -35,11 +34,11 @@ constexpr int kWavesPerBlock = kBlock / kWave;
 // TPT threads per token row (BS / TPT token rows per workgroup), one 16-byte
 // vector per thread per pass; rows wider than TPT vectors take several passes.
 // Table rows are loaded through the caches, output rows stored non-temporal
-// (unless the context keeps outputs cached for a consumer launched next):
+// (unless KEEP: the context keeps outputs cached for a consumer launched next):
 // a token that repeats an id already gathered in the same launch finds the
 // row in L2 or the Infinity Cache.  At configs[3] 37% of the tokens repeat an
 // id; measured on MI355X, 157 us against 172 us with non-temporal loads.
-template <int MODE, int TPT, int BS>
+template <int MODE, int TPT, int BS, bool KEEP>
 __global__ __launch_bounds__(BS) void embed_vec(GatherArgs a) {
     const int t = threadIdx.x % TPT;
     const int64_t token = static_cast<int64_t>(blockIdx.x) * (BS / TPT) + threadIdx.x / TPT;
@@ -51,7 +50,7 @@ __global__ __launch_bounds__(BS) void embed_vec(GatherArgs a) {
     u4* dst = reinterpret_cast<u4*>(a.y) + token * dim4;
     for (int64_t c = t; c < dim4; c += TPT) {
         const u4 v = copy ? src[c] : u4(0u);
-        if (a.keep) dst[c] = v;
+        if constexpr (KEEP) dst[c] = v;
         else __builtin_nontemporal_store(v, dst + c);
     }
 }
@@ -70,6 +69,17 @@ __global__ __launch_bounds__(kBlock) void embed_scalar(GatherArgs a) {
     for (int64_t c = lane; c < a.dim; c += kWave) dst[c] = copy ? src[c] : 0u;
 }
 
+template <int MODE, bool KEEP>
+void launch_vec(int tpt, unsigned vb, hipStream_t stream, const GatherArgs& a) {
+    switch (tpt) {
+        case 64: embed_vec<MODE, 64, 256, KEEP><<<vb, 256, 0, stream>>>(a); break;
+        case 128: embed_vec<MODE, 128, 256, KEEP><<<vb, 256, 0, stream>>>(a); break;
+        case 256: embed_vec<MODE, 256, 256, KEEP><<<vb, 256, 0, stream>>>(a); break;
+        case 512: embed_vec<MODE, 512, 512, KEEP><<<vb, 512, 0, stream>>>(a); break;
+        default: embed_vec<MODE, 1024, 1024, KEEP><<<vb, 1024, 0, stream>>>(a); break;
+    }
+}
+
 template <int MODE>
 int run(mimir_ctx* ctx, const void* ids, int64_t n_ids, const float* table, int64_t table_len,
         int32_t vocab, int32_t dim, int32_t pad, float* y) {
@@ -83,7 +93,7 @@ int run(mimir_ctx* ctx, const void* ids, int64_t n_ids, const float* table, int6
     if (n_ids == 0) return MIMIR_OK;
     MIMIR_REQUIRE(ctx, ids && table && y, "Embedding: null tensor");
     MIMIR_ENTER(ctx);
-    const GatherArgs a{ids, n_ids, table, vocab, dim, pad, y, ctx->keep_outputs};
+    const GatherArgs a{ids, n_ids, table, vocab, dim, pad, y};
     unsigned blocks;
     if (!grid_for(n_ids, kWavesPerBlock, &blocks))
         return fail(ctx, MIMIR_EINVAL, "Embedding: %lld ids exceed the grid limit", (long long)n_ids);
@@ -96,13 +106,8 @@ int run(mimir_ctx* ctx, const void* ids, int64_t n_ids, const float* table, int6
         unsigned vb;
         if (!grid_for(n_ids, bs / tpt, &vb))
             return fail(ctx, MIMIR_EINVAL, "Embedding: %lld ids exceed the grid limit", (long long)n_ids);
-        switch (tpt) {
-            case 64: embed_vec<MODE, 64, 256><<<vb, 256, 0, ctx->stream>>>(a); break;
-            case 128: embed_vec<MODE, 128, 256><<<vb, 256, 0, ctx->stream>>>(a); break;
-            case 256: embed_vec<MODE, 256, 256><<<vb, 256, 0, ctx->stream>>>(a); break;
-            case 512: embed_vec<MODE, 512, 512><<<vb, 512, 0, ctx->stream>>>(a); break;
-            default: embed_vec<MODE, 1024, 1024><<<vb, 1024, 0, ctx->stream>>>(a); break;
-        }
+        if (ctx->keep_outputs) launch_vec<MODE, true>(tpt, vb, ctx->stream, a);
+        else launch_vec<MODE, false>(tpt, vb, ctx->stream, a);
         return launched(ctx, "embed_vec");
     }
     embed_scalar<MODE><<<blocks, kBlock, 0, ctx->stream>>>(a);

@@ -56,7 +56,6 @@ struct LongArgs {
     float* partial;  // [rows][nchunks][2]
     float* stats;    // [rows][4]
     int reverse;     // this pass walks the chunks last to first
-    int keep;        // y through the caches (mimir_ctx_set_output_caching)
 };
 
 // Passes alternate direction: a pass starts where the previous one ended, so
@@ -217,7 +216,8 @@ __device__ __forceinline__ float softmax_out(float xv, float m, float s) {
 }
 
 // Pass 3: normalise one chunk.  K: 0 LayerNorm, 1 RMSNorm, 2 add+RMSNorm, 3 softmax.
-template <int K, int MODE>
+// KEEP: y through the caches (mimir_ctx_set_output_caching).
+template <int K, int MODE, bool KEEP>
 __global__ __launch_bounds__(kBlock) void lr_apply(LongArgs a) {
     const int64_t row = blockIdx.y;
     const int64_t chunk = chunk_of(a);
@@ -260,7 +260,7 @@ __global__ __launch_bounds__(kBlock) void lr_apply(LongArgs a) {
 #pragma unroll
             for (int k = 0; k < 4; ++k) o[k] = softmax_out<MODE>(v[j][k], s0, s1);
         }
-        st_out(a.y + base + c, o, a.keep);
+        st_out<KEEP>(a.y + base + c, o);
     }
 }
 
@@ -282,10 +282,20 @@ bool mimir::longrow_applies(int64_t rows, int64_t cols) {
     return cols > 16384 && rows <= 256 && (cols + kChunkFloats - 1) / kChunkFloats <= 0x7fffffffLL;
 }
 
+namespace {
+
+template <int K, int MODE>
+void launch_apply(mimir_ctx* ctx, dim3 grid, const LongArgs& a) {
+    if (ctx->keep_outputs) lr_apply<K, MODE, true><<<grid, kBlock, 0, ctx->stream>>>(a);
+    else lr_apply<K, MODE, false><<<grid, kBlock, 0, ctx->stream>>>(a);
+}
+
+}  // namespace
+
 int mimir::longrow_norm(mimir_ctx* ctx, int kind, const float* x, const float* r, float* r_out,
                         const float* g, const float* b, int64_t w_len, float* y, int64_t rows, int64_t cols,
                         float eps) {
-    LongArgs a{x, r, r_out, g, b, w_len, y, 0, 0, 0, eps, nullptr, nullptr, 0, ctx->keep_outputs};
+    LongArgs a{x, r, r_out, g, b, w_len, y, 0, 0, 0, eps, nullptr, nullptr, 0};
     if (int st = setup(ctx, a, rows, cols)) return st;
     const dim3 grid(static_cast<unsigned>(a.nchunks), static_cast<unsigned>(rows));
     const unsigned nrows = static_cast<unsigned>(rows);
@@ -294,21 +304,21 @@ int mimir::longrow_norm(mimir_ctx* ctx, int kind, const float* x, const float* r
     if (kind == 0) {
         lr_partial<kChan><<<grid, kBlock, 0, ctx->stream>>>(fwd);
         lr_combine<kChan><<<nrows, kBlock, 0, ctx->stream>>>(fwd);
-        lr_apply<0, 0><<<grid, kBlock, 0, ctx->stream>>>(rev);
+        launch_apply<0, 0>(ctx, grid, rev);
     } else if (kind == 1) {
         lr_partial<kSumSq><<<grid, kBlock, 0, ctx->stream>>>(fwd);
         lr_combine<kSumSq><<<nrows, kBlock, 0, ctx->stream>>>(fwd);
-        lr_apply<1, 0><<<grid, kBlock, 0, ctx->stream>>>(rev);
+        launch_apply<1, 0>(ctx, grid, rev);
     } else {
         lr_partial<kSumSqAdd><<<grid, kBlock, 0, ctx->stream>>>(fwd);
         lr_combine<kSumSqAdd><<<nrows, kBlock, 0, ctx->stream>>>(fwd);
-        lr_apply<2, 0><<<grid, kBlock, 0, ctx->stream>>>(rev);
+        launch_apply<2, 0>(ctx, grid, rev);
     }
     return launched(ctx, "longrow_norm");
 }
 
 int mimir::longrow_softmax(mimir_ctx* ctx, int mode, const float* x, float* y, int64_t rows, int64_t cols) {
-    LongArgs a{x, nullptr, nullptr, nullptr, nullptr, 0, y, 0, 0, 0, 0.0f, nullptr, nullptr, 0, ctx->keep_outputs};
+    LongArgs a{x, nullptr, nullptr, nullptr, nullptr, 0, y, 0, 0, 0, 0.0f, nullptr, nullptr, 0};
     if (int st = setup(ctx, a, rows, cols)) return st;
     const dim3 grid(static_cast<unsigned>(a.nchunks), static_cast<unsigned>(rows));
     LongArgs rev = a;
@@ -316,9 +326,9 @@ int mimir::longrow_softmax(mimir_ctx* ctx, int mode, const float* x, float* y, i
     lr_partial<kSoftmax><<<grid, kBlock, 0, ctx->stream>>>(a);
     lr_combine<kSoftmax><<<static_cast<unsigned>(rows), kBlock, 0, ctx->stream>>>(a);
     switch (mode) {
-        case MIMIR_SOFTMAX_DIV_EPS: lr_apply<3, MIMIR_SOFTMAX_DIV_EPS><<<grid, kBlock, 0, ctx->stream>>>(rev); break;
-        case MIMIR_SOFTMAX_MUL_INV: lr_apply<3, MIMIR_SOFTMAX_MUL_INV><<<grid, kBlock, 0, ctx->stream>>>(rev); break;
-        default: lr_apply<3, MIMIR_SOFTMAX_LOG><<<grid, kBlock, 0, ctx->stream>>>(rev); break;
+        case MIMIR_SOFTMAX_DIV_EPS: launch_apply<3, MIMIR_SOFTMAX_DIV_EPS>(ctx, grid, rev); break;
+        case MIMIR_SOFTMAX_MUL_INV: launch_apply<3, MIMIR_SOFTMAX_MUL_INV>(ctx, grid, rev); break;
+        default: launch_apply<3, MIMIR_SOFTMAX_LOG>(ctx, grid, rev); break;
     }
     return launched(ctx, "longrow_softmax");
 }

@@ -39,7 +39,6 @@ struct NormArgs {
     int64_t cols;
     int64_t w_len;    // RMSNorm: weight applies to columns < w_len
     float eps;
-    int keep;         // y through the caches (mimir_ctx_set_output_caching); r_out is always streamed
 };
 
 // Scale by the RMSNorm weight where the column is below w_len.
@@ -55,7 +54,9 @@ __device__ __forceinline__ f4 rms_scale(f4 o, const float* w, int64_t w_len, int
     return o;
 }
 
-template <Norm K, int TPR, int VPT, int BS>
+// KEEP: y through the caches (mimir_ctx_set_output_caching); r_out is always
+// streamed (it is read by a later block, not the next op).
+template <Norm K, int TPR, int VPT, int BS, bool KEEP>
 __global__ __launch_bounds__(BS) void norm_rows_vec(NormArgs a) {
     constexpr int RPB = BS / TPR;  // rows per workgroup
     constexpr int NW = TPR / kWave;  // waves per row
@@ -126,7 +127,7 @@ __global__ __launch_bounds__(BS) void norm_rows_vec(NormArgs a) {
                     o *= *reinterpret_cast<const f4*>(a.g + 4 * c4);
                     if (a.b) o += *reinterpret_cast<const f4*>(a.b + 4 * c4);
                 }
-                st_out(a.y + base + 4 * c4, o, a.keep);
+                st_out<KEEP>(a.y + base + 4 * c4, o);
             }
         }
     } else {
@@ -141,7 +142,7 @@ __global__ __launch_bounds__(BS) void norm_rows_vec(NormArgs a) {
             if (c4 < c4n) {
                 f4 o = v[j] / rms;
                 if (a.g) o = rms_scale(o, a.g, a.w_len, 4 * c4);
-                st_out(a.y + base + 4 * c4, o, a.keep);
+                st_out<KEEP>(a.y + base + 4 * c4, o);
             }
         }
     }
@@ -207,7 +208,8 @@ int launch_vec(mimir_ctx* ctx, const NormArgs& a) {
     unsigned blocks;
     if (!grid_for(a.rows, BS / TPR, &blocks))
         return fail(ctx, MIMIR_EINVAL, "norm: %lld rows exceed the grid limit", (long long)a.rows);
-    norm_rows_vec<K, TPR, VPT, BS><<<blocks, BS, 0, ctx->stream>>>(a);
+    if (ctx->keep_outputs) norm_rows_vec<K, TPR, VPT, BS, true><<<blocks, BS, 0, ctx->stream>>>(a);
+    else norm_rows_vec<K, TPR, VPT, BS, false><<<blocks, BS, 0, ctx->stream>>>(a);
     return launched(ctx, "norm_rows_vec");
 }
 
@@ -249,7 +251,7 @@ int mimir_layernorm_fwd(mimir_ctx* ctx, const float* x, const float* gamma, cons
     if (groups == 0) return MIMIR_OK;
     MIMIR_REQUIRE(ctx, x && y, "LayerNorm: null tensor");
     MIMIR_ENTER(ctx);
-    NormArgs a{x, nullptr, nullptr, gamma, beta, y, groups, n, n, eps, ctx->keep_outputs};
+    NormArgs a{x, nullptr, nullptr, gamma, beta, y, groups, n, n, eps};
     return dispatch<Norm::Layer>(ctx, a);
 }
 
@@ -261,8 +263,7 @@ int mimir_rmsnorm_fwd(mimir_ctx* ctx, const float* x, const float* w, int64_t w_
     if (rows == 0) return MIMIR_OK;
     MIMIR_REQUIRE(ctx, x && y, "RMSNorm: null tensor");
     MIMIR_ENTER(ctx);
-    NormArgs a{x, nullptr, nullptr, (w && w_len > 0) ? w : nullptr, nullptr, y, rows, cols, w ? w_len : 0, eps,
-               ctx->keep_outputs};
+    NormArgs a{x, nullptr, nullptr, (w && w_len > 0) ? w : nullptr, nullptr, y, rows, cols, w ? w_len : 0, eps};
     return dispatch<Norm::Rms>(ctx, a);
 }
 
@@ -277,7 +278,7 @@ int mimir_add_rmsnorm_fwd(mimir_ctx* ctx, const float* x, const float* residual,
     MIMIR_REQUIRE(ctx, static_cast<const void*>(y) != static_cast<const void*>(residual_out),
                   "add+RMSNorm: y must not alias residual_out");
     MIMIR_ENTER(ctx);
-    NormArgs a{x, residual, residual_out, w, nullptr, y, rows, cols, w ? cols : 0, eps, ctx->keep_outputs};
+    NormArgs a{x, residual, residual_out, w, nullptr, y, rows, cols, w ? cols : 0, eps};
     return dispatch<Norm::AddRms>(ctx, a);
 }
 

@@ -37,7 +37,6 @@ struct RopeArgs {
     int64_t q_slots;      // q head rows * Q
     int64_t total_slots;  // (q + k head rows) * Q
     int64_t pos_offset;
-    int keep;  // outputs through the caches (mimir_ctx_set_output_caching)
 };
 
 __device__ __forceinline__ void rotate(f4& x0, f4& x1, f4 c, f4 s) {
@@ -47,7 +46,8 @@ __device__ __forceinline__ void rotate(f4& x0, f4& x1, f4 c, f4 s) {
     x1 = y1;
 }
 
-template <int LOG2Q, int PPT>
+// KEEP: outputs through the caches (mimir_ctx_set_output_caching).
+template <int LOG2Q, int PPT, bool KEEP>
 __global__ __launch_bounds__(kBlock) void rope_vec(RopeArgs a) {
     constexpr int Q = 1 << LOG2Q;
     const int64_t first = static_cast<int64_t>(blockIdx.x) * PPT * kBlock + threadIdx.x;
@@ -78,8 +78,8 @@ __global__ __launch_bounds__(kBlock) void rope_vec(RopeArgs a) {
     for (int j = 0; j < PPT; ++j) {
         if (out[j]) {
             rotate(x0[j], x1[j], c[j], s[j]);
-            st_out(out[j], x0[j], a.keep);
-            st_out(out[j] + a.half, x1[j], a.keep);
+            st_out<KEEP>(out[j], x0[j]);
+            st_out<KEEP>(out[j] + a.half, x1[j]);
         }
     }
 }
@@ -111,7 +111,8 @@ int launch_ppt(mimir_ctx* ctx, const RopeArgs& a) {
     unsigned blocks;
     if (!grid_for(a.total_slots, static_cast<int64_t>(PPT) * kBlock, &blocks))
         return fail(ctx, MIMIR_EINVAL, "RoPE: tensor exceeds the grid limit");
-    rope_vec<LOG2Q, PPT><<<blocks, kBlock, 0, ctx->stream>>>(a);
+    if (ctx->keep_outputs) rope_vec<LOG2Q, PPT, true><<<blocks, kBlock, 0, ctx->stream>>>(a);
+    else rope_vec<LOG2Q, PPT, false><<<blocks, kBlock, 0, ctx->stream>>>(a);
     return launched(ctx, "rope_vec");
 }
 
@@ -170,7 +171,7 @@ int mimir_rope_fwd(mimir_ctx* ctx, const float* q, float* q_out, int64_t q_heads
     const int64_t half = head_dim / 2;
     RopeArgs a{q, q_out, k, k_out, cos_tab, sin_tab,
                static_cast<uint32_t>(qh ? qh : 1), static_cast<uint32_t>(kh ? kh : 1),
-               static_cast<uint32_t>(seq), static_cast<uint32_t>(half), 0, 0, pos_offset, ctx->keep_outputs};
+               static_cast<uint32_t>(seq), static_cast<uint32_t>(half), 0, 0, pos_offset};
     bool vec = (half % 4) == 0 && aligned16(cos_tab) && aligned16(sin_tab) &&
                (!q || (aligned16(q) && aligned16(q_out))) && (!k || (aligned16(k) && aligned16(k_out)));
     const int64_t Q = half / 4;

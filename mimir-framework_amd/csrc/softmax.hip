@@ -28,7 +28,6 @@ struct SoftmaxArgs {
     float* y;
     int64_t rows;
     int64_t cols;
-    int keep;  // y through the caches (mimir_ctx_set_output_caching)
 };
 
 template <int MODE>
@@ -52,7 +51,8 @@ __device__ __forceinline__ void row_constants(float sum, float* s, float* aux) {
     }
 }
 
-template <int MODE, int TPR, int VPT, int BS>
+// KEEP: y through the caches (mimir_ctx_set_output_caching).
+template <int MODE, int TPR, int VPT, int BS, bool KEEP>
 __global__ __launch_bounds__(BS) void softmax_rows_vec(SoftmaxArgs a) {
     constexpr int RPB = BS / TPR;
     constexpr int NW = TPR / kWave;
@@ -99,7 +99,7 @@ __global__ __launch_bounds__(BS) void softmax_rows_vec(SoftmaxArgs a) {
             f4 o;
 #pragma unroll
             for (int k = 0; k < 4; ++k) o[k] = finish<MODE>(v[j][k], e[j][k], m, sum, aux);
-            st_out(a.y + base + 4 * c4, o, a.keep);
+            st_out<KEEP>(a.y + base + 4 * c4, o);
         }
     }
 }
@@ -129,7 +129,8 @@ int launch_vec(mimir_ctx* ctx, const SoftmaxArgs& a) {
     unsigned blocks;
     if (!grid_for(a.rows, BS / TPR, &blocks))
         return fail(ctx, MIMIR_EINVAL, "softmax: %lld rows exceed the grid limit", (long long)a.rows);
-    softmax_rows_vec<MODE, TPR, VPT, BS><<<blocks, BS, 0, ctx->stream>>>(a);
+    if (ctx->keep_outputs) softmax_rows_vec<MODE, TPR, VPT, BS, true><<<blocks, BS, 0, ctx->stream>>>(a);
+    else softmax_rows_vec<MODE, TPR, VPT, BS, false><<<blocks, BS, 0, ctx->stream>>>(a);
     return launched(ctx, "softmax_rows_vec");
 }
 
@@ -163,7 +164,7 @@ extern "C" int mimir_softmax_fwd(mimir_ctx* ctx, const float* x, float* y, int64
     if (rows == 0) return MIMIR_OK;
     MIMIR_REQUIRE(ctx, x && y, "Softmax: null tensor");
     MIMIR_ENTER(ctx);
-    const SoftmaxArgs a{x, y, rows, cols, ctx->keep_outputs};
+    const SoftmaxArgs a{x, y, rows, cols};
     switch (mode) {
         case MIMIR_SOFTMAX_DIV_EPS: return dispatch<MIMIR_SOFTMAX_DIV_EPS>(ctx, a);
         case MIMIR_SOFTMAX_MUL_INV: return dispatch<MIMIR_SOFTMAX_MUL_INV>(ctx, a);
