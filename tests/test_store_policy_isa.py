@@ -1,0 +1,58 @@
+"""The output store policy survives compilation.
+
+Every forward kernel is built twice, KEEP=false (outputs streamed with
+non-temporal stores, the fast form for an op whose result is not read next)
+and KEEP=true (plain stores that leave the output in L2 / the Infinity Cache
+for the next op of a chain).  Results are the same bits either way, so no
+numeric test can see a lost hint; this one compiles the kernel sources to
+gfx950 assembly and checks every 16-byte global store: `nt` in the streamed
+variants, plain in the kept ones (add+RMSNorm's residual output is streamed
+in both, since a later block reads it, not the next op)."""
+import os
+import re
+import shutil
+import subprocess
+
+import pytest
+
+CSRC = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "mimir-framework_amd", "csrc")
+HIPCC = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
+FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fno-gpu-flush-denormals-to-zero", "-Xclang",
+         "-target-feature", "-Xclang", "-packed-fp32-ops", "--cuda-device-only", "-S"]
+SOURCES = ["elementwise", "norm", "softmax", "gather", "rope", "longrow"]
+
+
+def _stores_by_kernel(asm):
+    stores, name = {}, None
+    for line in asm.splitlines():
+        m = re.match(r"^(_Z\S+):", line)
+        if m:
+            name = m.group(1)
+            stores[name] = []
+            continue
+        code = line.split(";")[0]
+        if name and "global_store_dwordx4" in code:
+            stores[name].append(bool(re.search(r"\bnt\b", code)))
+    return stores
+
+
+@pytest.mark.skipif(not os.path.exists(HIPCC), reason="hipcc not available")
+@pytest.mark.parametrize("src", SOURCES)
+def test_keep_variants_store_as_intended(src, tmp_path):
+    out = tmp_path / f"{src}.s"
+    r = subprocess.run([HIPCC, *FLAGS, "-o", str(out), os.path.join(CSRC, f"{src}.hip")],
+                       capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr[-2000:]
+    checked = 0
+    for name, nt in _stores_by_kernel(out.read_text()).items():
+        keep = "Lb1EEEv" in name
+        if not nt or not (keep or "Lb0EEEv" in name):
+            continue  # not a KEEP-templated kernel, or one without vector stores
+        checked += 1
+        if keep and "NormE2E" in name:  # add+RMSNorm: r_out streamed, y kept
+            assert nt.count(True) == nt.count(False), f"{name}: {nt}"
+        elif keep:
+            assert not any(nt), f"{name}: a kept output is stored non-temporal"
+        else:
+            assert all(nt), f"{name}: a streamed output lost its non-temporal hint"
+    assert checked >= 2, f"{src}: no KEEP variants found"
