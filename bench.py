@@ -255,6 +255,31 @@ def build_ops():
     blk.nsets = lambda: 1
     ops.append(blk)
 
+    # One device-resident training step of the same block: forwardPassNamed
+    # (training=true) then backwardPass with the loss gradient already in HBM
+    # (mimir_store_run_training + mimir_store_backward_dev).  Streams of
+    # [8192x4096]: forward 12; backward: loss-gradient copy 2, SiLU 3,
+    # Multiply 5, GELU 3, LayerNorm 3 (+ gamma, dgamma, dbeta), Add 3.
+    def make_block_train(ctx, nsets):
+        x, res = G.cfg4_add()
+        gate = G.cfg4_grad((8192, 4096), 11)
+        graph = M.DeviceGraph(ctx, block_layers())
+        store = M.Store(ctx)
+        store.set_inputs({"inp": x, "res": res, "gate": gate}, {})
+        lg = ctx.to_device(G.cfg4_grad((8192, 4096), 12))
+
+        def step(i):
+            store.run_training(graph)
+            store.backward(graph, lg)
+        step(0)  # fills the buffer pool: later steps allocate nothing
+        return step, [[_Owned(store, graph), lg]]
+    trn = OpBench("cfg4_runtime_block_train", 4,
+                  "device-resident training step of the same block on [8192x4096]: forward (training) + backward",
+                  "mimir_store_run_training + mimir_store_backward_dev (12 kernels)",
+                  31 * 8192 * 4096 * f4 + 7 * 4096 * f4, 8192, "rows", make_block_train)
+    trn.nsets = lambda: 1
+    ops.append(trn)
+
     # Calibration: a plain streaming copy of 512 MiB (mimir_copy), the
     # practical HBM ceiling and the yardstick for the FETCH/WRITE counters.
     def make_copy(ctx, nsets):
@@ -484,6 +509,18 @@ def cpu_leg(which, reps):
                 t = MR.time_forward_named(layers, {"inp": x, "res": res, "gate": gate}, {}, reps)
                 rec(key, t, nb, rows, "reference",
                     f"{rows} of 8192 rows: Model::forwardPassNamed of the same five layers (host tensor store)")
+        elif key == "cfg4_runtime_block_train":
+            rows = 256
+            x, res = G.cfg4_add(rows=rows)
+            gate = G.cfg4_grad((8192, 4096), 11)[:rows]
+            lg = G.cfg4_grad((8192, 4096), 12)[:rows]
+            sys.path.insert(0, os.path.join(REPO, "oracle"))
+            import model_ref as MR
+            if MR.available():
+                t = MR.time_train_step(block_layers(), {"inp": x, "res": res, "gate": gate}, {}, lg, reps)
+                rec(key, t, 31 * x.nbytes + 7 * 4096 * 4, rows, "reference",
+                    f"{rows} of 8192 rows: Model::forwardPassNamed(training=true) then Model::backwardPass of the "
+                    "same five layers (host tensor store)")
         elif key == "cfg3_embedding_bwd":
             ids = G.cfg3_ids().ravel()[:4096].copy()
             dy = G.cfg3_embedding_grad()[:4096].copy()
@@ -567,9 +604,16 @@ def parity_leg(ctx, by_key, which):
         log(f"parity {key}: {'pass' if out[key]['pass'] else 'FAIL'} vs {vs} "
             + ", ".join(f"{n} max_abs {r['max_abs']:.3g}" for n, r in res.items()))
 
+    def check_arrays(key, pairs, vs, sample):
+        """pairs: {name: (got, ref, scale or None)} computed by the caller."""
+        res = {n: _agreement(g, r, False, sc) for n, (g, r, sc) in pairs.items()}
+        out[key] = {"vs": vs, "sample": sample, "pass": all(r["pass"] for r in res.values()), "outputs": res}
+        log(f"parity {key}: {'pass' if out[key]['pass'] else 'FAIL'} vs {vs} "
+            + ", ".join(f"{n} max_abs {r['max_abs']:.3g}" for n, r in res.items()))
+
     ref_or_port = "reference" if have_ref else "port"
     for key in which:
-        if key not in by_key or by_key[key].outputs is None:
+        if key not in by_key or (by_key[key].outputs is None and key != "cfg4_runtime_block_train"):
             continue
         if key in ("cfg0_layernorm", "cfg4_layernorm"):
             x, g, b, eps = G.cfg0_layernorm() if key == "cfg0_layernorm" else G.cfg4_layernorm(rows=1024)
@@ -655,6 +699,44 @@ def parity_leg(ctx, by_key, which):
             gt = O.embedding_bwd(G.cfg3_ids(), G.cfg3_embedding_grad(), np.zeros(32000 * 4096, np.float32),
                                  32000, 4096, -1)
             check(key, {"grad": gt}, "port", "full table [32000x4096], all 32768 tokens", exact=("grad",))
+        elif key == "cfg4_runtime_block_train" and MR.available():
+            rows = 512
+            x, res = G.cfg4_add(rows=rows)
+            gate = G.cfg4_grad((8192, 4096), 11)[:rows]
+            lg = G.cfg4_grad((8192, 4096), 12)[:rows]
+            layers = block_layers()
+            r_grads, _ = MR.backward(layers, {"inp": x, "res": res, "gate": gate}, {}, lg)
+            ref = r_grads[1]  # the LayerNorm's [dgamma | dbeta]
+            graph = M.DeviceGraph(ctx, layers)
+            store = M.Store(ctx)
+            dlg = ctx.to_device(lg)
+            try:
+                store.set_inputs({"inp": x, "res": res, "gate": gate}, {})
+                store.run_training(graph)
+                store.backward(graph, dlg)
+                got = graph.grads()[1]
+            finally:
+                dlg.free()
+                store.close()
+                graph.close()
+            # Magnitudes each float32 sum adds (float64 chain of the block):
+            # dgamma = sum_rows dn*xhat, dbeta = sum_rows dn.
+            g64, b64 = (np.asarray(layers[1]["weights"][:4096], np.float64),
+                        np.asarray(layers[1]["weights"][4096:], np.float64))
+            h = x.astype(np.float64) + res
+            xh = (h - h.mean(axis=1, keepdims=True)) / np.sqrt(h.var(axis=1, keepdims=True) + 1e-5)
+            n = xh * g64 + b64
+            k = np.sqrt(np.float64(np.float32(2.0) / np.float32(3.14159265359)))
+            t = np.tanh(k * (n + 0.044715 * n ** 3))
+            gl = 0.5 * n * (1 + t)
+            m = gl * gate
+            s = 1 / (1 + np.exp(-m))
+            dm = lg * (s + m * s * (1 - s))
+            dn = dm * gate * (0.5 * (1 + t) + 0.5 * n * (1 - t * t) * k * (1 + 3 * 0.044715 * n * n))
+            scale = np.concatenate([np.abs(dn * xh).sum(axis=0), np.abs(dn).sum(axis=0)])
+            check_arrays(key, {"ln grad_weights": (got, ref, scale)},
+                         "reference (Model::backwardPass of the same five layers)",
+                         f"first {rows} of 8192 rows, the LayerNorm's [dgamma | dbeta] at the end of the chain")
         elif key == "cfg4_runtime_block" and MR.available():
             rows = 1024
             x, res = G.cfg4_add(rows=rows)

@@ -364,6 +364,12 @@ int mimir_store_run_training(mimir_store* store, const mimir_layer* layers, int3
  * reference skips with a warning are skipped. */
 int mimir_store_backward(mimir_store* store, const mimir_layer* layers, int32_t n_layers, const float* loss_grad,
                          int64_t n_grad);
+/* mimir_store_backward with loss_grad in device memory (n_grad floats,
+ * copied into the store like the host form's upload).  No counterpart in
+ * the reference, whose loss gradient is a host vector: for a device-resident
+ * training step whose loss gradient is computed on the GPU. */
+int mimir_store_backward_dev(mimir_store* store, const mimir_layer* layers, int32_t n_layers, const float* loss_grad,
+                             int64_t n_grad);
 
 /* A gradient of the last mimir_store_backward by tensor name ("__input__"
  * for Model::getLastInputGradient): device pointer and size, or a download

@@ -82,7 +82,9 @@ struct DSilu {
 };
 
 // dx = dy * f'(x), or dx += that (accumulate_grad into a present gradient).
-template <class F, bool ACC>
+// KEEP: dx through the caches (mimir_ctx_set_output_caching), as for every
+// *_vec kernel below with a KEEP parameter.
+template <class F, bool ACC, bool KEEP>
 __global__ __launch_bounds__(kBlock) void dact_vec(const float* x, const float* dy, float* dx, int64_t n4, F f) {
     const int64_t i = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
     if (i >= n4) return;
@@ -90,7 +92,7 @@ __global__ __launch_bounds__(kBlock) void dact_vec(const float* x, const float* 
     const f4 g = ld4<true>(dy + 4 * i);
     f4 o{g.x * f(xv.x), g.y * f(xv.y), g.z * f(xv.z), g.w * f(xv.w)};
     if constexpr (ACC) o = ld4<true>(dx + 4 * i) + o;
-    st4<true>(dx + 4 * i, o);
+    st_out<KEEP>(dx + 4 * i, o);
 }
 
 template <class F, bool ACC>
@@ -117,7 +119,8 @@ int run_dact(mimir_ctx* ctx, const float* x, const float* dy, float* dx, int64_t
             unsigned blocks;
             if (!grid_for(n4, kBlock, &blocks))
                 return fail(ctx, MIMIR_EINVAL, "%s: n=%lld exceeds the grid limit", name, (long long)n);
-            dact_vec<F, ACC><<<blocks, kBlock, 0, ctx->stream>>>(x, dy, dx, n4, f);
+            if (ctx->keep_outputs) dact_vec<F, ACC, true><<<blocks, kBlock, 0, ctx->stream>>>(x, dy, dx, n4, f);
+            else dact_vec<F, ACC, false><<<blocks, kBlock, 0, ctx->stream>>>(x, dy, dx, n4, f);
             if (int st = launched(ctx, name)) return st;
         }
         done = n4 * 4;
@@ -136,7 +139,7 @@ int run_dact(mimir_ctx* ctx, const float* x, const float* dy, float* dx, int64_t
 
 // g0 = dy*b and g1 = dy*a are formed before either is accumulated, as in
 // the reference, so da / db may alias dy (element for element).
-template <bool ACC_A, bool ACC_B>
+template <bool ACC_A, bool ACC_B, bool KEEP>
 __global__ __launch_bounds__(kBlock) void mul_bwd_vec(const float* a, const float* b, const float* dy, float* da,
                                                       float* db, int64_t n4) {
     const int64_t i = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
@@ -150,8 +153,8 @@ __global__ __launch_bounds__(kBlock) void mul_bwd_vec(const float* a, const floa
     if (db) {
         if constexpr (ACC_B) g1 = ld4<true>(db + 4 * i) + g1;
     }
-    if (da) st4<true>(da + 4 * i, g0);
-    if (db) st4<true>(db + 4 * i, g1);
+    if (da) st_out<KEEP>(da + 4 * i, g0);
+    if (db) st_out<KEEP>(db + 4 * i, g1);
 }
 
 // da == db (Multiply of a tensor with itself): the second accumulation adds
@@ -185,13 +188,13 @@ __global__ __launch_bounds__(kBlock) void mul_bwd_scalar(const float* a, const f
 }
 
 // dst = src or dst += src over n floats (accumulate_grad, Model.cpp:7329-7341).
-template <bool ACC>
+template <bool ACC, bool KEEP>
 __global__ __launch_bounds__(kBlock) void acc_vec(const float* src, float* dst, int64_t n4) {
     const int64_t i = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
     if (i >= n4) return;
     f4 o = ld4<true>(src + 4 * i);
     if constexpr (ACC) o = ld4<true>(dst + 4 * i) + o;
-    st4<true>(dst + 4 * i, o);
+    st_out<KEEP>(dst + 4 * i, o);
 }
 
 template <bool ACC>
@@ -205,13 +208,31 @@ __global__ __launch_bounds__(kBlock) void acc_scalar(const float* src, float* ds
 }
 
 // Equal sizes and no aliasing: da (+)= dy and db (+)= dy in one pass.
-template <bool ACC_A, bool ACC_B>
+template <bool ACC_A, bool ACC_B, bool KEEP>
 __global__ __launch_bounds__(kBlock) void add_bwd_vec(const float* dy, float* da, float* db, int64_t n4) {
     const int64_t i = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
     if (i >= n4) return;
     const f4 g = ld4<true>(dy + 4 * i);
-    if (da) st4<true>(da + 4 * i, ACC_A ? ld4<true>(da + 4 * i) + g : g);
-    if (db) st4<true>(db + 4 * i, ACC_B ? ld4<true>(db + 4 * i) + g : g);
+    if (da) st_out<KEEP>(da + 4 * i, ACC_A ? ld4<true>(da + 4 * i) + g : g);
+    if (db) st_out<KEEP>(db + 4 * i, ACC_B ? ld4<true>(db + 4 * i) + g : g);
+}
+
+template <bool KEEP>
+void launch_mul_bwd(mimir_ctx* ctx, unsigned blocks, bool A, bool B, const float* a, const float* b, const float* dy,
+                    float* da, float* db, int64_t n4) {
+    if (A && B) mul_bwd_vec<true, true, KEEP><<<blocks, kBlock, 0, ctx->stream>>>(a, b, dy, da, db, n4);
+    else if (A) mul_bwd_vec<true, false, KEEP><<<blocks, kBlock, 0, ctx->stream>>>(a, b, dy, da, db, n4);
+    else if (B) mul_bwd_vec<false, true, KEEP><<<blocks, kBlock, 0, ctx->stream>>>(a, b, dy, da, db, n4);
+    else mul_bwd_vec<false, false, KEEP><<<blocks, kBlock, 0, ctx->stream>>>(a, b, dy, da, db, n4);
+}
+
+template <bool KEEP>
+void launch_add_bwd(mimir_ctx* ctx, unsigned blocks, bool A, bool B, const float* dy, float* da, float* db,
+                    int64_t n4) {
+    if (A && B) add_bwd_vec<true, true, KEEP><<<blocks, kBlock, 0, ctx->stream>>>(dy, da, db, n4);
+    else if (A) add_bwd_vec<true, false, KEEP><<<blocks, kBlock, 0, ctx->stream>>>(dy, da, db, n4);
+    else if (B) add_bwd_vec<false, true, KEEP><<<blocks, kBlock, 0, ctx->stream>>>(dy, da, db, n4);
+    else add_bwd_vec<false, false, KEEP><<<blocks, kBlock, 0, ctx->stream>>>(dy, da, db, n4);
 }
 
 int accumulate(mimir_ctx* ctx, const float* src, float* dst, int64_t n, bool acc, const char* name) {
@@ -222,8 +243,11 @@ int accumulate(mimir_ctx* ctx, const float* src, float* dst, int64_t n, bool acc
             unsigned blocks;
             if (!grid_for(n4, kBlock, &blocks))
                 return fail(ctx, MIMIR_EINVAL, "%s: n=%lld exceeds the grid limit", name, (long long)n);
-            if (acc) acc_vec<true><<<blocks, kBlock, 0, ctx->stream>>>(src, dst, n4);
-            else acc_vec<false><<<blocks, kBlock, 0, ctx->stream>>>(src, dst, n4);
+            const bool k = ctx->keep_outputs != 0;
+            if (acc && k) acc_vec<true, true><<<blocks, kBlock, 0, ctx->stream>>>(src, dst, n4);
+            else if (acc) acc_vec<true, false><<<blocks, kBlock, 0, ctx->stream>>>(src, dst, n4);
+            else if (k) acc_vec<false, true><<<blocks, kBlock, 0, ctx->stream>>>(src, dst, n4);
+            else acc_vec<false, false><<<blocks, kBlock, 0, ctx->stream>>>(src, dst, n4);
             if (int st = launched(ctx, name)) return st;
         }
         done = n4 * 4;
@@ -651,7 +675,7 @@ __device__ __forceinline__ float hsum(f4 v) { return (v.x + v.y) + (v.z + v.w); 
 // The two reduction rounds of a row use separate LDS arrays, so each
 // array's reuse (next row) is separated from its reads by the other round's
 // barrier: no leading barriers are needed.
-template <int TPR, int VPT, int BS>
+template <int TPR, int VPT, int BS, bool KEEP>
 __global__ __launch_bounds__(BS) void ln_bwd_vec(LnBwdArgs a) {
     constexpr int RPB = BS / TPR;
     constexpr int NW = TPR / kWave;
@@ -730,7 +754,7 @@ __global__ __launch_bounds__(BS) void ln_bwd_vec(LnBwdArgs a) {
                 db[j] += gv[j];
                 f4 o = k * ((n * dxh - s1) - xh * s2);
                 if (a.acc) o = ld4<true>(a.dx + off + 4 * c4) + o;
-                st4<true>(a.dx + off + 4 * c4, o);
+                st_out<KEEP>(a.dx + off + 4 * c4, o);
             }
         }
 #pragma unroll
@@ -861,7 +885,8 @@ int launch_ln_bwd_vec(mimir_ctx* ctx, LnBwdArgs a, float* dgamma, float* dbeta) 
         a.part = static_cast<float*>(s);
         tmp = a.part + nslots * 2 * a.cols;
     }
-    ln_bwd_vec<TPR, VPT, BS><<<static_cast<unsigned>(grid), BS, 0, ctx->stream>>>(a);
+    if (ctx->keep_outputs) ln_bwd_vec<TPR, VPT, BS, true><<<static_cast<unsigned>(grid), BS, 0, ctx->stream>>>(a);
+    else ln_bwd_vec<TPR, VPT, BS, false><<<static_cast<unsigned>(grid), BS, 0, ctx->stream>>>(a);
     if (int st = launched(ctx, "ln_bwd_vec")) return st;
     if (!dgamma) return MIMIR_OK;
     // dbeta null: sum only the dgamma half.
@@ -1141,10 +1166,8 @@ int mimir_mul_bwd(mimir_ctx* ctx, const float* a, const float* b, const float* d
             unsigned blocks;
             if (!grid_for(n4, kBlock, &blocks))
                 return fail(ctx, MIMIR_EINVAL, "Multiply backward: n=%lld exceeds the grid limit", (long long)n);
-            if (A && B) mul_bwd_vec<true, true><<<blocks, kBlock, 0, ctx->stream>>>(a, b, dy, da, db, n4);
-            else if (A) mul_bwd_vec<true, false><<<blocks, kBlock, 0, ctx->stream>>>(a, b, dy, da, db, n4);
-            else if (B) mul_bwd_vec<false, true><<<blocks, kBlock, 0, ctx->stream>>>(a, b, dy, da, db, n4);
-            else mul_bwd_vec<false, false><<<blocks, kBlock, 0, ctx->stream>>>(a, b, dy, da, db, n4);
+            if (ctx->keep_outputs) launch_mul_bwd<true>(ctx, blocks, A, B, a, b, dy, da, db, n4);
+            else launch_mul_bwd<false>(ctx, blocks, A, B, a, b, dy, da, db, n4);
             if (int st = launched(ctx, "mul_bwd_vec")) return st;
         }
         done = n4 * 4;
@@ -1176,10 +1199,8 @@ int mimir_add_bwd(mimir_ctx* ctx, const float* dy, int64_t na, int64_t nb, float
             unsigned blocks;
             if (!grid_for(na / 4, kBlock, &blocks))
                 return fail(ctx, MIMIR_EINVAL, "Add backward: n=%lld exceeds the grid limit", (long long)na);
-            if (A && B) add_bwd_vec<true, true><<<blocks, kBlock, 0, ctx->stream>>>(dy, da, db, na / 4);
-            else if (A) add_bwd_vec<true, false><<<blocks, kBlock, 0, ctx->stream>>>(dy, da, db, na / 4);
-            else if (B) add_bwd_vec<false, true><<<blocks, kBlock, 0, ctx->stream>>>(dy, da, db, na / 4);
-            else add_bwd_vec<false, false><<<blocks, kBlock, 0, ctx->stream>>>(dy, da, db, na / 4);
+            if (ctx->keep_outputs) launch_add_bwd<true>(ctx, blocks, A, B, dy, da, db, na / 4);
+            else launch_add_bwd<false>(ctx, blocks, A, B, dy, da, db, na / 4);
             return launched(ctx, "add_bwd_vec");
         }
         // Aliased gradients: the second accumulation sees the first, as the

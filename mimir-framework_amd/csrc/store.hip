@@ -592,8 +592,12 @@ int mimir_store_run_training(mimir_store* s, const mimir_layer* layers, int32_t 
     return MIMIR_OK;
 }
 
-int mimir_store_backward(mimir_store* s, const mimir_layer* layers, int32_t n_layers, const float* loss_grad,
-                         int64_t n_grad) {
+namespace {
+
+// Model::backwardPass with the loss gradient on the host (the reference's
+// form) or already in device memory.
+int store_backward(mimir_store* s, const mimir_layer* layers, int32_t n_layers, const float* loss_grad,
+                   int64_t n_grad, bool device) {
     if (!s) return MIMIR_EINVAL;
     MIMIR_REQUIRE(s->ctx, n_layers >= 0 && (n_layers == 0 || layers) && n_grad >= 0 && (n_grad == 0 || loss_grad),
                   "mimir_store_backward: invalid argument");
@@ -601,19 +605,40 @@ int mimir_store_backward(mimir_store* s, const mimir_layer* layers, int32_t n_la
     MIMIR_REQUIRE(s->ctx, static_cast<size_t>(n_layers) == s->snaps.size(),
                   "mimir_store_backward: no training forward of these %d layers (run_training first)", n_layers);
     s->release_grads();
+    // Every layer's gradients but the first layer's (the model's input
+    // gradients, read back by the caller) feed the backward of the layer
+    // before it: they stay in the caches, as the forward's outputs do.
+    ChainOutputs chain(s->ctx);
+    chain.layer(0, n_layers + 1);
     Buf* b = nullptr;  // grad_store["x"] = loss_gradient (:7346)
     if (int st = s->acquire(static_cast<size_t>(n_grad) * 4, &b)) return st;
     if (n_grad > 0) {
-        if (int st = mimir_upload(s->ctx, b->p, loss_grad, static_cast<size_t>(n_grad) * 4)) {
+        const size_t bytes = static_cast<size_t>(n_grad) * 4;
+        const int st = device ? mimir_copy(s->ctx, b->p, loss_grad, bytes) : mimir_upload(s->ctx, b->p, loss_grad, bytes);
+        if (st) {
             s->discard(b);
             return st;
         }
     }
     ++b->refs;
     s->grads.emplace("x", Slot{b, n_grad});
-    for (int32_t i = n_layers - 1; i >= 0; --i)
+    for (int32_t i = n_layers - 1; i >= 0; --i) {
+        chain.layer(n_layers - 1 - i, n_layers);
         if (int st = backward_layer(s, layers[i], s->snaps[i])) return st;
+    }
     return MIMIR_OK;
+}
+
+}  // namespace
+
+int mimir_store_backward(mimir_store* s, const mimir_layer* layers, int32_t n_layers, const float* loss_grad,
+                         int64_t n_grad) {
+    return store_backward(s, layers, n_layers, loss_grad, n_grad, false);
+}
+
+int mimir_store_backward_dev(mimir_store* s, const mimir_layer* layers, int32_t n_layers, const float* loss_grad,
+                             int64_t n_grad) {
+    return store_backward(s, layers, n_layers, loss_grad, n_grad, true);
 }
 
 int mimir_store_grad_info(mimir_store* s, const char* name, void** dptr, int64_t* n) {

@@ -99,6 +99,7 @@ SIGNATURES = {
     "mimir_safetensors_read": (c_int, [_P, c_char_p, _P, c_size_t]),
     "mimir_safetensors_load_layers": (c_int, [_P, POINTER(Layer_C), c_int32, c_int]),
     "mimir_store_backward": (c_int, [_P, POINTER(Layer_C), c_int32, _P, c_int64]),
+    "mimir_store_backward_dev": (c_int, [_P, POINTER(Layer_C), c_int32, _P, c_int64]),
     "mimir_store_grad_info": (c_int, [_P, c_char_p, _PP, POINTER(c_int64)]),
     "mimir_store_grad_get": (c_int, [_P, c_char_p, _P, c_int64, POINTER(c_int64)]),
 }

@@ -323,6 +323,12 @@ class Store:
         self.ctx.check(self.ctx.lib.mimir_store_run_training(self.handle, graph.c_layers, len(graph.layers)))
 
     def backward(self, graph: "DeviceGraph", loss_grad):
+        """Model::backwardPass(loss_grad): a host array (the reference's form),
+        or a DeviceArray already on the GPU (mimir_store_backward_dev)."""
+        if isinstance(loss_grad, DeviceArray):
+            self.ctx.check(self.ctx.lib.mimir_store_backward_dev(self.handle, graph.c_layers, len(graph.layers),
+                                                                 c_void_p(loss_grad.ptr), loss_grad.size))
+            return
         g = np.ascontiguousarray(loss_grad, np.float32).ravel()
         self.ctx.check(self.ctx.lib.mimir_store_backward(self.handle, graph.c_layers, len(graph.layers),
                                                          g.ctypes.data_as(c_void_p), g.size))

@@ -78,6 +78,11 @@ def _load():
         tf.argtypes = [POINTER(_Spec), c_int32, POINTER(c_char_p), POINTER(c_void_p), POINTER(c_int64), c_int32,
                        POINTER(c_char_p), POINTER(c_void_p), POINTER(c_int64), c_int32, c_int32]
         tf.restype = ctypes.c_double
+        ts = lib.ref_time_train_step
+        ts.argtypes = [POINTER(_Spec), c_int32, POINTER(c_char_p), POINTER(c_void_p), POINTER(c_int64), c_int32,
+                       POINTER(c_char_p), POINTER(c_void_p), POINTER(c_int64), c_int32, c_void_p, c_int64,
+                       c_int32]
+        ts.restype = ctypes.c_double
         _lib = lib
     return _lib
 
@@ -193,6 +198,19 @@ def time_safetensors_load(layers, path, reps=3):
     del keep
     if t < 0:
         raise RefModelError("load_checkpoint failed")
+    return t
+
+
+def time_train_step(layers, fin, iin, loss_grad, reps=3):
+    """Median seconds of one reference training step (forwardPassNamed with
+    training=true, then backwardPass(loss_grad)) on a model built once."""
+    keep, args = _marshal(layers, fin, iin)
+    g = np.ascontiguousarray(loss_grad, np.float32).ravel()
+    with _StdoutToStderr():
+        t = _load().ref_time_train_step(*args, g.ctypes.data, g.size, int(reps))
+    del keep
+    if t < 0:
+        raise RefModelError("training step failed")
     return t
 
 

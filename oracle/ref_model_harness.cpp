@@ -243,6 +243,37 @@ double ref_time_forward_named(const ref_layer_spec* specs, int32_t n_layers, con
     }
 }
 
+// Seconds per training step -- Model::forwardPassNamed(training=true) then
+// Model::backwardPass(loss_grad) -- of a model built once from the specs:
+// the median of `reps` timed steps after one untimed step.  -1 when the
+// reference throws.
+double ref_time_train_step(const ref_layer_spec* specs, int32_t n_layers, const char* const* fnames,
+                           const float* const* fdata, const int64_t* fsizes, int32_t nf,
+                           const char* const* inames, const int32_t* const* idata, const int64_t* isizes,
+                           int32_t ni, const float* loss_grad, int64_t n_grad, int32_t reps) {
+    try {
+        Model m;
+        build_model(m, specs, n_layers);
+        std::unordered_map<std::string, std::vector<float>> fin;
+        std::unordered_map<std::string, std::vector<int>> iin;
+        for (int32_t i = 0; i < nf; ++i) fin[fnames[i]] = std::vector<float>(fdata[i], fdata[i] + fsizes[i]);
+        for (int32_t i = 0; i < ni; ++i) iin[inames[i]] = std::vector<int>(idata[i], idata[i] + isizes[i]);
+        const std::vector<float> lg(loss_grad, loss_grad + n_grad);
+        std::vector<double> t;
+        for (int32_t r = 0; r <= reps; ++r) {
+            const auto t0 = std::chrono::steady_clock::now();
+            m.forwardPassNamed(fin, iin, true);
+            m.backwardPass(lg);
+            const auto t1 = std::chrono::steady_clock::now();
+            if (r > 0) t.push_back(std::chrono::duration<double>(t1 - t0).count());
+        }
+        std::sort(t.begin(), t.end());
+        return t.empty() ? -1.0 : t[t.size() / 2];
+    } catch (...) {
+        return -1.0;
+    }
+}
+
 // Seconds per Mimir::Serialization::load_checkpoint (SafeTensors, weights
 // only) into a model built once from the specs: the median of `reps` timed
 // calls after one untimed call (page cache warm).  -1 on failure.

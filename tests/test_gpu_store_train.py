@@ -13,7 +13,7 @@ import pytest
 import mimir_hip as M
 import model_oracle as MO
 from _graphs import train_graphs
-from _parity import assert_close, assert_close_sum
+from _parity import assert_bitexact, assert_close, assert_close_sum
 
 pytestmark = pytest.mark.gpu
 
@@ -99,3 +99,33 @@ def test_train_step_allocates_nothing_on_repeat():
         store.close()
         graph.close()
         c.close()
+
+
+@pytest.mark.parametrize("case", train_graphs(), ids=lambda c: c[0])
+def test_device_loss_gradient_matches_host(ctx, case):
+    """mimir_store_backward_dev (loss gradient already on the GPU) gives the
+    same bits as the host form, for the input gradient and grad_weights."""
+    name, layers, fin, iin, lg = case
+    graph = M.DeviceGraph(ctx, layers)
+    store = M.Store(ctx)
+    dlg = ctx.to_device(np.ascontiguousarray(lg, np.float32).ravel())
+    try:
+        store.set_inputs(fin, iin)
+        store.run_training(graph)
+        store.backward(graph, lg)
+        host_grads, host_in = graph.grads(), store.grad("__input__")
+        graph.zero_grads()
+        store.set_inputs(fin, iin)  # the first step rebound names its layers write (e.g. "x")
+        store.run_training(graph)
+        store.backward(graph, dlg)
+        dev_grads, dev_in = graph.grads(), store.grad("__input__")
+        assert (host_in is None) == (dev_in is None)
+        if host_in is not None:
+            assert_bitexact(dev_in, host_in, f"{name} __input__ gradient")
+        for L, a, b in zip(layers, host_grads, dev_grads):
+            if a is not None:
+                assert_bitexact(b, a, f"{name} {L['name']} grad_weights")
+    finally:
+        dlg.free()
+        store.close()
+        graph.close()
