@@ -7,7 +7,10 @@ for the next op of a chain).  Results are the same bits either way, so no
 numeric test can see a lost hint; this one compiles the kernel sources to
 gfx950 assembly and checks every 16-byte global store: `nt` in the streamed
 variants, plain in the kept ones (add+RMSNorm's residual output is streamed
-in both, since a later block reads it, not the next op)."""
+in both, since a later block reads it, not the next op).  The backward
+kernels and the device copy take the same parameter; the LayerNorm
+backward's dgamma/dbeta slot partials are plain stores in both variants
+(the slot sums read them back next)."""
 import os
 import re
 import shutil
@@ -19,7 +22,9 @@ CSRC = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))),
 HIPCC = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
 FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fno-gpu-flush-denormals-to-zero", "-Xclang",
          "-target-feature", "-Xclang", "-packed-fp32-ops", "--cuda-device-only", "-S"]
-SOURCES = ["elementwise", "norm", "softmax", "gather", "rope", "longrow"]
+SOURCES = ["elementwise", "norm", "softmax", "gather", "rope", "longrow", "backward", "runtime"]
+# Kernels of backward.hip / runtime.hip whose last template parameter is KEEP.
+KEEP_KERNELS = ("dact_vec", "mul_bwd_vec", "add_bwd_vec", "acc_vec", "ln_bwd_vec", "copy16_kernel")
 
 
 def _stores_by_kernel(asm):
@@ -48,9 +53,13 @@ def test_keep_variants_store_as_intended(src, tmp_path):
         keep = "Lb1EEEv" in name
         if not nt or not (keep or "Lb0EEEv" in name):
             continue  # not a KEEP-templated kernel, or one without vector stores
+        if src in ("backward", "runtime") and not any(k in name for k in KEEP_KERNELS):
+            continue  # a bool template parameter that is not KEEP
         checked += 1
         if keep and "NormE2E" in name:  # add+RMSNorm: r_out streamed, y kept
             assert nt.count(True) == nt.count(False), f"{name}: {nt}"
+        elif "ln_bwd_vec" in name and not keep:  # dx streamed, slot partials plain
+            assert any(nt), f"{name}: dx lost its non-temporal hint"
         elif keep:
             assert not any(nt), f"{name}: a kept output is stored non-temporal"
         else:
