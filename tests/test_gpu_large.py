@@ -1,0 +1,89 @@
+"""Tensors of more than 2^31 elements (8 GiB of fp32 each): every index on
+the path is 64-bit.  The inputs are filled on the device (constants, with a
+few rows uploaded where values must differ), and the results are checked at
+the head, around element 2^31 and at the tail, against the oracle where a
+row is not constant.  Peak device memory: 24 GiB of the MI355X's 288."""
+import numpy as np
+import pytest
+
+import oracle as O
+from _parity import assert_bitexact, assert_close
+
+pytestmark = pytest.mark.gpu
+
+BIG = (1 << 31) + 4096  # elements: past the int32 range by one 4096-wide row
+
+
+def _slice(ctx, buf, start, n):
+    out = np.empty(n, np.float32)
+    ctx.download(out, buf.offset(start, (n,)))
+    return out
+
+
+def test_add_past_2_31(ctx):
+    a, b, y = ctx.empty(BIG), ctx.empty(BIG), ctx.empty(BIG)
+    try:
+        ctx.fill(a, 1.5)
+        ctx.fill(b, 2.25)
+        ctx.add(a, BIG, b, BIG, y)
+        for start in (0, (1 << 31) - 2048, BIG - 4096):
+            assert_bitexact(_slice(ctx, y, start, 4096), np.full(4096, 3.75, np.float32), f"add at {start}")
+    finally:
+        for d in (a, b, y):
+            d.free()
+
+
+def test_layernorm_rows_past_2_31(ctx):
+    cols = 4096
+    rows = BIG // cols  # 2^19 + 1 rows
+    x, y = ctx.empty((rows, cols)), ctx.empty((rows, cols))
+    rng = np.random.default_rng(31)
+    g = (1 + 0.05 * rng.standard_normal(cols)).astype(np.float32)
+    b = (0.05 * rng.standard_normal(cols)).astype(np.float32)
+    tail = rng.standard_normal((2, cols)).astype(np.float32)  # the last two rows differ
+    dg, db = ctx.to_device(g), ctx.to_device(b)
+    try:
+        ctx.fill(x, 0.75)
+        ctx.upload(x.offset((rows - 2) * cols, (2, cols)), tail)
+        ctx.layernorm(x, dg, db, y, rows, cols, 1e-5)
+        assert_bitexact(_slice(ctx, y, 0, cols), b, "constant row 0 -> beta")
+        assert_bitexact(_slice(ctx, y, (rows - 3) * cols, cols), b, "constant row before the tail -> beta")
+        got = _slice(ctx, y, (rows - 2) * cols, 2 * cols).reshape(2, cols)
+        assert_close(got, O.layernorm(tail, cols, g, b, 1e-5).reshape(2, cols), "last rows (past 2^31)")
+    finally:
+        for d in (x, y, dg, db):
+            d.free()
+
+
+def test_gather_output_past_2_31(ctx):
+    vocab, dim = 1000, 4096
+    n = BIG // dim  # output [n x 4096] past 2^31 elements
+    rng = np.random.default_rng(32)
+    table = rng.standard_normal((vocab, dim)).astype(np.float32)
+    ids = rng.integers(-1, vocab + 1, n).astype(np.int32)
+    dt, di, y = ctx.to_device(table), ctx.to_device(ids), ctx.empty((n, dim))
+    try:
+        ctx.embedding(di, n, dt, table.size, vocab, dim, -1, y)
+        for t in (0, n // 2, n - 2, n - 1):
+            want = table[ids[t]] if 0 <= ids[t] < vocab else np.zeros(dim, np.float32)
+            assert_bitexact(_slice(ctx, y, t * dim, dim), want, f"token {t}")
+    finally:
+        for d in (dt, di, y):
+            d.free()
+
+
+def test_softmax_rows_past_2_31(ctx):
+    cols = 1024
+    rows = BIG // cols
+    x, y = ctx.empty((rows, cols)), ctx.empty((rows, cols))
+    tail = (3 * np.random.default_rng(33).standard_normal((1, cols))).astype(np.float32)
+    try:
+        ctx.fill(x, -2.0)
+        ctx.upload(x.offset((rows - 1) * cols, (1, cols)), tail)
+        ctx.softmax(x, y, rows, cols)
+        flat = O.softmax_rows(np.full((1, cols), -2.0, np.float32))[0]
+        assert_close(_slice(ctx, y, 0, cols), flat, "constant row 0")
+        assert_close(_slice(ctx, y, (rows - 1) * cols, cols), O.softmax_rows(tail)[0], "last row (past 2^31)")
+    finally:
+        for d in (x, y):
+            d.free()
