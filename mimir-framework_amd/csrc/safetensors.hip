@@ -7,8 +7,11 @@
 // length, 0 < length <= 100 MiB, a JSON object of {dtype, shape,
 // data_offsets} entries plus "__metadata__", (end - begin) == prod(shape) *
 // dtype size), and a tensor's bytes go from the file to device memory through
-// two pinned staging buffers: while one chunk's DMA runs on the context's
-// stream, the next chunk is read from the file into the other buffer.
+// four pinned staging buffers: two threads read a pair of chunks from the file
+// while the previous pair's DMAs run on the context's stream.  Measured on
+// the MI355X box: one reader reaches ~22 GB/s from the page cache into a cold
+// buffer, pinned 8 MiB DMAs ~54 GB/s; one reader into two staging buffers
+// ingested ~40 GB/s, two readers leave the DMA as the bound.
 //
 // The JSON reader below accepts the subset a SafeTensors header is written
 // in (objects, arrays, strings with escapes, numbers, true/false/null); it
@@ -20,8 +23,11 @@
 #include <unistd.h>
 
 #include <cerrno>
+#include <condition_variable>
 #include <cstring>
 #include <memory>
+#include <mutex>
+#include <thread>
 #include <new>
 #include <string>
 #include <unordered_map>
@@ -303,6 +309,7 @@ struct Entry {
 };
 
 constexpr size_t kStageBytes = size_t(8) << 20;  // per staging buffer
+constexpr int kStages = 4;                       // two pairs: one being read, one in DMA
 
 // The message of this thread's last failed open (there is no handle then).
 thread_local std::string g_open_error;
@@ -316,8 +323,8 @@ struct mimir_safetensors {
     uint64_t data_offset = 0;
     std::vector<Entry> entries;
     std::unordered_map<std::string, size_t> index;
-    void* stage[2] = {nullptr, nullptr};  // pinned host memory, allocated on first read
-    hipEvent_t done[2] = {nullptr, nullptr};
+    void* stage[kStages] = {};  // pinned host memory, allocated on first read
+    hipEvent_t done[kStages] = {};
     std::string error;  // when there is no context to hold it
 };
 
@@ -393,6 +400,77 @@ int parse_header(mimir_safetensors* f, const char* path) {
     return MIMIR_OK;
 }
 
+// pread until n bytes are in dst (false on an error or end of file).
+bool read_full(int fd, char* dst, size_t n, off_t pos) {
+    size_t got = 0;
+    while (got < n) {
+        const ssize_t r = pread(fd, dst + got, n - got, pos + static_cast<off_t>(got));
+        if (r < 0 && errno == EINTR) continue;
+        if (r <= 0) return false;
+        got += static_cast<size_t>(r);
+    }
+    return true;
+}
+
+// A second reader: reads one chunk per job handed over by read_to_device.
+// Joined by its destructor on every path out of read_to_device.
+class Reader {
+  public:
+    explicit Reader(int fd) : fd_(fd), th_([this] { loop(); }) {}
+    ~Reader() {
+        {
+            std::lock_guard<std::mutex> l(m_);
+            quit_ = true;
+        }
+        cv_.notify_all();
+        th_.join();
+    }
+    void start(char* dst, size_t n, off_t pos) {
+        {
+            std::lock_guard<std::mutex> l(m_);
+            dst_ = dst;
+            n_ = n;
+            pos_ = pos;
+            pending_ = true;
+        }
+        cv_.notify_all();
+    }
+    bool wait() {  // the job's result
+        std::unique_lock<std::mutex> l(m_);
+        cv_.wait(l, [this] { return !pending_; });
+        return ok_;
+    }
+
+  private:
+    void loop() {
+        std::unique_lock<std::mutex> l(m_);
+        for (;;) {
+            cv_.wait(l, [this] { return pending_ || quit_; });
+            if (pending_) {
+                char* dst = dst_;
+                const size_t n = n_;
+                const off_t pos = pos_;
+                l.unlock();
+                const bool ok = read_full(fd_, dst, n, pos);
+                l.lock();
+                ok_ = ok;
+                pending_ = false;
+                cv_.notify_all();
+            } else {
+                return;  // quit, nothing pending
+            }
+        }
+    }
+    int fd_;
+    std::mutex m_;
+    std::condition_variable cv_;
+    char* dst_ = nullptr;
+    size_t n_ = 0;
+    off_t pos_ = 0;
+    bool pending_ = false, ok_ = true, quit_ = false;
+    std::thread th_;  // last: started once the members above exist
+};
+
 // SafeTensorsReader::load_tensor_data (:168-216), into device memory.
 int read_to_device(mimir_safetensors* f, const Entry& t, void* dst, size_t dst_bytes) {
     mimir_ctx* ctx = f->ctx;
@@ -400,7 +478,7 @@ int read_to_device(mimir_safetensors* f, const Entry& t, void* dst, size_t dst_b
     if (bytes > dst_bytes) return st_fail(f, ctx, MIMIR_EINVAL, "Buffer too small for tensor: " + t.name);  // :192-198
     if (bytes == 0) return MIMIR_OK;
     MIMIR_ENTER(ctx);
-    for (int i = 0; i < 2; ++i) {
+    for (int i = 0; i < kStages; ++i) {
         if (!f->stage[i]) {
             hipError_t e = hipHostMalloc(&f->stage[i], kStageBytes, hipHostMallocDefault);
             if (e != hipSuccess) {
@@ -416,41 +494,51 @@ int read_to_device(mimir_safetensors* f, const Entry& t, void* dst, size_t dst_b
             }
         }
     }
-    // Chunk k is read into stage[k % 2] once the DMA of chunk k-2 out of that
-    // buffer has finished; its own DMA then runs while chunk k+1 is read.
-    uint64_t off = 0;
-    bool used[2] = {false, false};
-    for (int k = 0; off < bytes; ++k) {
-        const int b = k & 1;
-        const size_t n = static_cast<size_t>(bytes - off < kStageBytes ? bytes - off : kStageBytes);
-        if (used[b]) {
-            hipError_t e = hipEventSynchronize(f->done[b]);
-            if (e != hipSuccess) return mimir::hip_fail(ctx, e, "hipEventSynchronize");
+    // Pair p is chunks 2p and 2p+1, read into stage[2p % 4] and
+    // stage[(2p+1) % 4] (this thread and the second reader) once the DMAs of
+    // pair p-2 out of those buffers have finished; its DMAs then run while
+    // pair p+1 is read.  A tensor of one or two chunks needs no second reader.
+    const uint64_t nchunks = (bytes + kStageBytes - 1) / kStageBytes;
+    std::unique_ptr<Reader> helper;
+    if (nchunks > 2) helper.reset(new Reader(f->fd));
+    bool used[kStages] = {};
+    auto wait_buffer = [&](int b) -> int {
+        if (!used[b]) return MIMIR_OK;
+        hipError_t e = hipEventSynchronize(f->done[b]);
+        return e == hipSuccess ? MIMIR_OK : mimir::hip_fail(ctx, e, "hipEventSynchronize");
+    };
+    auto fail_read = [&]() {
+        (void)hipStreamSynchronize(ctx->stream);  // earlier DMAs may still run out of the buffers
+        return st_fail(f, ctx, MIMIR_EINVAL, "Failed to read tensor data: " + t.name);  // :201-206
+    };
+    const off_t base = static_cast<off_t>(f->data_offset + t.begin);
+    for (uint64_t c = 0; c < nchunks; c += 2) {
+        const int b0 = static_cast<int>(c % kStages), b1 = static_cast<int>((c + 1) % kStages);
+        const uint64_t off0 = c * kStageBytes, off1 = off0 + kStageBytes;
+        const size_t n0 = static_cast<size_t>(bytes - off0 < kStageBytes ? bytes - off0 : kStageBytes);
+        const size_t n1 = off1 < bytes ? static_cast<size_t>(bytes - off1 < kStageBytes ? bytes - off1 : kStageBytes) : 0;
+        if (int st = wait_buffer(b0)) return st;
+        if (n1 > 0)
+            if (int st = wait_buffer(b1)) return st;
+        char* s0 = static_cast<char*>(f->stage[b0]);
+        char* s1 = static_cast<char*>(f->stage[b1]);
+        if (n1 > 0 && helper) helper->start(s1, n1, base + static_cast<off_t>(off1));
+        bool ok = read_full(f->fd, s0, n0, base + static_cast<off_t>(off0));
+        if (n1 > 0) ok = (helper ? helper->wait() : read_full(f->fd, s1, n1, base + static_cast<off_t>(off1))) && ok;
+        if (!ok) return fail_read();
+        for (int k = 0; k < (n1 > 0 ? 2 : 1); ++k) {
+            const int bk = k ? b1 : b0;
+            hipError_t e = hipMemcpyAsync(static_cast<char*>(dst) + (k ? off1 : off0), k ? s1 : s0, k ? n1 : n0,
+                                          hipMemcpyHostToDevice, ctx->stream);
+            if (e != hipSuccess) return mimir::hip_fail(ctx, e, "hipMemcpyAsync");
+            e = hipEventRecord(f->done[bk], ctx->stream);
+            if (e != hipSuccess) return mimir::hip_fail(ctx, e, "hipEventRecord");
+            used[bk] = true;
         }
-        size_t got = 0;
-        while (got < n) {
-            const ssize_t r = pread(f->fd, static_cast<char*>(f->stage[b]) + got, n - got,
-                                    static_cast<off_t>(f->data_offset + t.begin + off + got));
-            if (r < 0 && errno == EINTR) continue;
-            if (r <= 0) {
-                (void)hipStreamSynchronize(ctx->stream);  // the other buffer's DMA may still run
-                return st_fail(f, ctx, MIMIR_EINVAL, "Failed to read tensor data: " + t.name);  // :201-206
-            }
-            got += static_cast<size_t>(r);
-        }
-        hipError_t e = hipMemcpyAsync(static_cast<char*>(dst) + off, f->stage[b], n, hipMemcpyHostToDevice, ctx->stream);
-        if (e != hipSuccess) return mimir::hip_fail(ctx, e, "hipMemcpyAsync");
-        e = hipEventRecord(f->done[b], ctx->stream);
-        if (e != hipSuccess) return mimir::hip_fail(ctx, e, "hipEventRecord");
-        used[b] = true;
-        off += n;
     }
     // The staging buffers are reused by the next read: wait for the last DMAs.
-    for (int i = 0; i < 2; ++i) {
-        if (!used[i]) continue;
-        hipError_t e = hipEventSynchronize(f->done[i]);
-        if (e != hipSuccess) return mimir::hip_fail(ctx, e, "hipEventSynchronize");
-    }
+    for (int i = 0; i < kStages; ++i)
+        if (int st = wait_buffer(i)) return st;
     return MIMIR_OK;
 }
 
@@ -486,7 +574,7 @@ int mimir_safetensors_open(mimir_ctx* ctx, const char* path, mimir_safetensors**
 
 int mimir_safetensors_close(mimir_safetensors* f) {
     if (!f) return MIMIR_EINVAL;
-    for (int i = 0; i < 2; ++i) {
+    for (int i = 0; i < kStages; ++i) {
         if (f->done[i]) (void)hipEventDestroy(f->done[i]);
         if (f->stage[i]) (void)hipHostFree(f->stage[i]);
     }

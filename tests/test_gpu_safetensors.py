@@ -61,9 +61,12 @@ def test_strict_missing_and_size_mismatch(ctx, tmp_path):
         g.close()
 
 
-@pytest.mark.parametrize("nbytes", [4, 4 * 1000003, (8 << 20) * 4 + 12, (8 << 20) + 5])
+@pytest.mark.parametrize("nbytes", [4, 4 * 1000003, (8 << 20) + 5, (8 << 20) * 3, (8 << 20) * 4,
+                                    (8 << 20) * 4 + 12, (8 << 20) * 7 + 1])
 def test_read_multi_chunk_bitexact(ctx, tmp_path, nbytes):
-    # Reads cross the 8 MiB staging chunks (both buffers, odd tails).
+    # Reads cross the 8 MiB staging chunks: one or two chunks (one reader),
+    # three and more (two readers, pairs of chunks over four buffers), a pair
+    # whose second chunk is missing, ragged tails.
     rng = np.random.default_rng(nbytes)
     if nbytes % 4:
         a = rng.integers(0, 256, nbytes, dtype=np.uint8)
