@@ -560,7 +560,7 @@ struct ChainOutputs {
     mimir_ctx* ctx;
     int saved;
     explicit ChainOutputs(mimir_ctx* c) : ctx(c), saved(c->keep_outputs) {}
-    void layer(int32_t i, int32_t n) { ctx->keep_outputs = i + 1 < n ? 1 : saved; }
+    void layer(int32_t i, int32_t n) { ctx->keep_outputs = i + 1 < n && !ctx->tune.chain_streamed ? 1 : saved; }
     ~ChainOutputs() { ctx->keep_outputs = saved; }
 };
 
