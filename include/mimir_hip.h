@@ -400,6 +400,11 @@ typedef struct mimir_safetensors mimir_safetensors;
  * {dtype, shape, data_offsets} plus "__metadata__"; EINVAL with the
  * reference's message for a missing / unknown dtype, missing shape or
  * data_offsets, bad offsets or (end - begin) != prod(shape) * dtype size.
+ * JSON is read as the reference's nlohmann::json 3.11.2 reads it (strict
+ * syntax, well-formed UTF-8, a NUL between tokens ends the header, the last
+ * of duplicate keys); entries are visited and numbered in byte order of their
+ * names.  Refused where the reference's size arithmetic would wrap: negative
+ * or out-of-range sizes, and tensor data past the end of the file.
  * ctx may be NULL to inspect a file without a device (no reads then);
  * mimir_safetensors_error reports the message in that case. */
 int mimir_safetensors_open(mimir_ctx* ctx, const char* path, mimir_safetensors** out);

@@ -13,9 +13,15 @@
 // buffer, pinned 8 MiB DMAs ~54 GB/s; one reader into two staging buffers
 // ingested ~40 GB/s, two readers leave the DMA as the bound.
 //
-// The JSON reader below accepts the subset a SafeTensors header is written
-// in (objects, arrays, strings with escapes, numbers, true/false/null); it
-// is not a general-purpose JSON library.
+// The JSON reader below follows the library the reference parses headers
+// with (nlohmann::json 3.11.2, vendored as src/include/json.hpp) wherever a
+// header's outcome depends on it: RFC 8259 syntax with no comments, leading
+// zeros or trailing commas; strings must be well-formed UTF-8 with paired
+// surrogate escapes; a leading byte order mark is skipped; a NUL byte between
+// tokens ends the input (json.hpp:8885);
+// objects keep the last of duplicate keys and are visited in byte order of
+// their keys (std::map).  Nesting is limited to 512 levels (the library has
+// no limit).
 #include "internal.hpp"
 
 #include <fcntl.h>
@@ -25,6 +31,7 @@
 #include <cerrno>
 #include <condition_variable>
 #include <cstring>
+#include <map>
 #include <memory>
 #include <mutex>
 #include <thread>
@@ -56,12 +63,15 @@ public:
     JParser(const char* p, size_t n) : p_(p), end_(p + n) {}
 
     bool parse(JVal& out, std::string& err) {
+        if (end_ - p_ >= 3 && static_cast<unsigned char>(p_[0]) == 0xEF && static_cast<unsigned char>(p_[1]) == 0xBB &&
+            static_cast<unsigned char>(p_[2]) == 0xBF)
+            p_ += 3;  // a leading UTF-8 byte order mark is skipped (json.hpp, lexer::skip_bom)
         if (!value(out, 0)) {
             err = err_;
             return false;
         }
         ws();
-        if (p_ != end_) {
+        if (p_ != end_ && *p_ != '\0') {  // a NUL ends the input, as in json.hpp:8885-8888
             err = "trailing characters after the JSON value";
             return false;
         }
@@ -69,6 +79,27 @@ public:
     }
 
 private:
+    // After lead byte c (>= 0x80, already consumed): check the continuation
+    // bytes of a well-formed sequence (RFC 3629, section 4) and set seq_end_.
+    bool utf8_tail(unsigned char c) {
+        int n;
+        unsigned char lo = 0x80, hi = 0xBF;  // range of the first continuation byte
+        if (c >= 0xC2 && c <= 0xDF) n = 1;
+        else if (c == 0xE0) n = 2, lo = 0xA0;
+        else if ((c >= 0xE1 && c <= 0xEC) || c == 0xEE || c == 0xEF) n = 2;
+        else if (c == 0xED) n = 2, hi = 0x9F;
+        else if (c == 0xF0) n = 3, lo = 0x90;
+        else if (c >= 0xF1 && c <= 0xF3) n = 3;
+        else if (c == 0xF4) n = 3, hi = 0x8F;
+        else return false;
+        if (end_ - p_ < n) return false;
+        for (int i = 0; i < n; ++i) {
+            const unsigned char b = static_cast<unsigned char>(p_[i]);
+            if (b < (i ? 0x80 : lo) || b > (i ? 0xBF : hi)) return false;
+        }
+        seq_end_ = p_ + n;
+        return true;
+    }
     bool fail(const char* m) {
         if (err_.empty()) err_ = m;
         return false;
@@ -119,6 +150,12 @@ private:
         while (p_ < end_ && *p_ != '"') {
             const unsigned char c = static_cast<unsigned char>(*p_++);
             if (c < 0x20) return fail("control character in a string");
+            if (c >= 0x80) {  // a UTF-8 sequence, RFC 3629 well-formed
+                if (!utf8_tail(c)) return fail("ill-formed UTF-8 byte");
+                out.append(p_ - 1, seq_end_);
+                p_ = seq_end_;
+                continue;
+            }
             if (c != '\\') {
                 out += static_cast<char>(c);
                 continue;
@@ -143,6 +180,8 @@ private:
                         p_ += 2;
                         if (!hex4(lo) || lo < 0xDC00 || lo > 0xDFFF) return fail("bad surrogate pair");
                         cp = 0x10000 + ((cp - 0xD800) << 10) + (lo - 0xDC00);
+                    } else if (cp >= 0xDC00 && cp <= 0xDFFF) {
+                        return fail("lone low surrogate");
                     }
                     put_utf8(out, cp);
                     break;
@@ -163,6 +202,7 @@ private:
             ++p_;
         }
         if (p_ >= end_ || *p_ < '0' || *p_ > '9') return fail("bad number");
+        if (*p_ == '0' && p_ + 1 < end_ && p_[1] >= '0' && p_[1] <= '9') return fail("leading zero in a number");
         uint64_t u = 0;
         bool overflow = false;
         while (p_ < end_ && *p_ >= '0' && *p_ <= '9') {
@@ -190,7 +230,7 @@ private:
         return true;
     }
     bool value(JVal& v, int depth) {
-        if (depth > 64) return fail("JSON nested too deeply");
+        if (depth > 512) return fail("JSON nested too deeply");
         ws();
         if (p_ >= end_) return fail("unexpected end of JSON");
         const char c = *p_;
@@ -270,6 +310,7 @@ private:
 
     const char* p_;
     const char* end_;
+    const char* seq_end_ = nullptr;
     std::string err_;
 };
 
@@ -294,10 +335,36 @@ bool dtype_of(const std::string& s, int* code, size_t* size) {
     return false;
 }
 
-bool as_size(const JVal& v, uint64_t* out) {
-    if (v.kind != JVal::Num || !v.is_int || v.neg) return false;
-    *out = v.u;
-    return true;
+const char* kind_name(const JVal& v) {
+    switch (v.kind) {
+        case JVal::Null: return "null";
+        case JVal::Bool: return "boolean";
+        case JVal::Num: return "number";
+        case JVal::Str: return "string";
+        case JVal::Arr: return "array";
+        default: return "object";
+    }
+}
+
+// A header number read as a size, as the reference's json get<size_t>()
+// reads it (size_t is the library's unsigned number type, so
+// get_arithmetic_value, json.hpp:4607-4637 and :4683): unsigned integers as
+// they are, floats truncated toward zero.  NotNumber: any other kind,
+// booleans included (the reference throws a type error).  Wraps: a negative
+// integer, or a float outside (-1, 2^64): the reference's conversion wraps
+// modulo 2^64 (or is undefined for such floats); refused here.
+enum class SizeOf { Ok, NotNumber, Wraps };
+
+SizeOf as_size(const JVal& v, uint64_t* out) {
+    if (v.kind != JVal::Num) return SizeOf::NotNumber;
+    if (v.is_int) {
+        if (v.neg && v.u != 0) return SizeOf::Wraps;
+        *out = v.u;
+        return SizeOf::Ok;
+    }
+    if (!(v.num > -1.0 && v.num < 18446744073709551616.0)) return SizeOf::Wraps;
+    *out = v.num < 1.0 ? 0 : static_cast<uint64_t>(v.num);
+    return SizeOf::Ok;
 }
 
 struct Entry {
@@ -342,8 +409,9 @@ int parse_header(mimir_safetensors* f, const char* path) {
     if (pread(f->fd, len8, 8, 0) != 8) return st_fail(f, ctx, MIMIR_EINVAL, "Invalid header length");
     uint64_t hlen = 0;
     for (int i = 0; i < 8; ++i) hlen |= static_cast<uint64_t>(len8[i]) << (8 * i);  // :200-208
-    if (hlen == 0 || hlen > (uint64_t(100) << 20) || 8 + hlen > f->file_size)  // :68-74
+    if (hlen == 0 || hlen > (uint64_t(100) << 20))  // :68-74
         return st_fail(f, ctx, MIMIR_EINVAL, "Invalid header length");
+    if (8 + hlen > f->file_size) return st_fail(f, ctx, MIMIR_EINVAL, "Failed to read header");  // :77-85
     std::vector<char> text(hlen);
     if (pread(f->fd, text.data(), hlen, 8) != static_cast<ssize_t>(hlen))
         return st_fail(f, ctx, MIMIR_EINVAL, "Failed to read header");
@@ -351,17 +419,27 @@ int parse_header(mimir_safetensors* f, const char* path) {
     std::string err;
     if (!JParser(text.data(), text.size()).parse(root, err))
         return st_fail(f, ctx, MIMIR_EINVAL, std::string("Header parse error: ") + err + " in " + path);
-    if (root.kind != JVal::Obj) return st_fail(f, ctx, MIMIR_EINVAL, "Header parse error: not a JSON object");
     f->data_offset = 8 + hlen;  // :93
-    for (auto& kv : root.obj) {
+    // The reference iterates the parsed value with it.key() (:96): null and
+    // an empty array hold no entries; any other non-object throws.
+    const bool empty = root.kind == JVal::Null || (root.kind == JVal::Arr && root.arr.empty());
+    if (root.kind != JVal::Obj && !empty)
+        return st_fail(f, ctx, MIMIR_EINVAL, "Header parse error: cannot use key() for non-object iterators");
+    // Entries in key order, the last of duplicate keys (a std::map object).
+    std::map<std::string, const JVal*> by_name;
+    for (auto& kv : root.obj) by_name[kv.first] = &kv.second;
+    auto not_number = [&](const JVal& v) {
+        return st_fail(f, ctx, MIMIR_EINVAL, std::string("Header parse error: type must be number, but is ") +
+                                                 kind_name(v));
+    };
+    for (auto& kv : by_name) {
         if (kv.first == "__metadata__") continue;  // :97-99
         const std::string& name = kv.first;
-        const JVal& e = kv.second;
-        if (e.kind != JVal::Obj) return st_fail(f, ctx, MIMIR_EINVAL, "Header parse error: entry is not an object: " + name);
+        const JVal& e = *kv.second;
         const JVal* dt = nullptr;
         const JVal* shape = nullptr;
         const JVal* offs = nullptr;
-        for (auto& m : e.obj) {
+        for (auto& m : e.obj) {  // empty unless e is an object; the last of duplicate fields
             if (m.first == "dtype") dt = &m.second;
             else if (m.first == "shape") shape = &m.second;
             else if (m.first == "data_offsets") offs = &m.second;
@@ -370,27 +448,42 @@ int parse_header(mimir_safetensors* f, const char* path) {
         t.name = name;
         size_t esize = 0;
         if (!dt) return st_fail(f, ctx, MIMIR_EINVAL, "Missing dtype for tensor: " + name);  // :108-113
-        if (dt->kind != JVal::Str || !dtype_of(dt->s, &t.dtype, &esize))
+        if (dt->kind != JVal::Str)
             return st_fail(f, ctx, MIMIR_EINVAL,
-                           "Header parse error: Unknown dtype string: " + (dt->kind == JVal::Str ? dt->s : "?"));
+                           std::string("Header parse error: type must be string, but is ") + kind_name(*dt));
+        if (!dtype_of(dt->s, &t.dtype, &esize))
+            return st_fail(f, ctx, MIMIR_EINVAL, "Header parse error: Unknown dtype string: " + dt->s);
         if (!shape) return st_fail(f, ctx, MIMIR_EINVAL, "Missing shape for tensor: " + name);  // :117-122
-        if (shape->kind != JVal::Arr) return st_fail(f, ctx, MIMIR_EINVAL, "Header parse error: bad shape for " + name);
+        if (shape->kind != JVal::Arr)
+            return st_fail(f, ctx, MIMIR_EINVAL,
+                           std::string("Header parse error: type must be array, but is ") + kind_name(*shape));
         uint64_t count = 1;
+        bool overflow = false;
         for (const JVal& d : shape->arr) {
-            uint64_t dim;
-            if (!as_size(d, &dim)) return st_fail(f, ctx, MIMIR_EINVAL, "Header parse error: bad shape for " + name);
-            if (dim && count > UINT64_MAX / dim)
-                return st_fail(f, ctx, MIMIR_EINVAL, "Size mismatch for tensor: " + name);
+            uint64_t dim = 0;
+            const SizeOf k = as_size(d, &dim);
+            if (k == SizeOf::NotNumber) return not_number(d);
+            if (k == SizeOf::Wraps)
+                return st_fail(f, ctx, MIMIR_EINVAL, "Header parse error: negative or out-of-range dimension for " + name);
+            if (dim && count > UINT64_MAX / dim) overflow = true;
             count *= dim;
             t.shape.push_back(static_cast<int64_t>(dim));
         }
         if (!offs) return st_fail(f, ctx, MIMIR_EINVAL, "Missing data_offsets for tensor: " + name);  // :126-131
-        if (offs->kind != JVal::Arr || offs->arr.size() != 2 || !as_size(offs->arr[0], &t.begin) ||
-            !as_size(offs->arr[1], &t.end))  // :132-137
+        if (offs->kind != JVal::Arr || offs->arr.size() != 2)  // :132-137
             return st_fail(f, ctx, MIMIR_EINVAL, "Invalid data_offsets for tensor: " + name);
-        // :142-153; also refuse ranges that run past the end of the file,
-        // which the reference only finds when the read comes up short.
-        if (t.end < t.begin || count > UINT64_MAX / esize || t.end - t.begin != count * esize)
+        uint64_t* ends[2] = {&t.begin, &t.end};
+        for (int i = 0; i < 2; ++i) {
+            const SizeOf k = as_size(offs->arr[i], ends[i]);
+            if (k == SizeOf::NotNumber) return not_number(offs->arr[i]);
+            if (k == SizeOf::Wraps)
+                return st_fail(f, ctx, MIMIR_EINVAL, "Header parse error: negative or out-of-range offset for " + name);
+        }
+        // :142-153, without the wrap-around of the reference's size_t
+        // arithmetic (a product past 2^64 or end < begin is a mismatch); also
+        // refuse ranges that run past the end of the file, which the
+        // reference only finds when the read comes up short.
+        if (overflow || t.end < t.begin || count > UINT64_MAX / esize || t.end - t.begin != count * esize)
             return st_fail(f, ctx, MIMIR_EINVAL, "Size mismatch for tensor: " + name);
         if (t.end > f->file_size - f->data_offset)
             return st_fail(f, ctx, MIMIR_EINVAL, "Tensor data past the end of the file: " + name);

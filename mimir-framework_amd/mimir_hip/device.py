@@ -439,7 +439,8 @@ class SafeTensors:
         self.close()
 
     def entries(self):
-        """{name: (dtype string, shape tuple, nbytes)} in file order."""
+        """{name: (dtype string, shape tuple, nbytes)} in byte order of the names
+        (the order in which the reference visits them)."""
         out = {}
         for i in range(self.lib.mimir_safetensors_count(self.handle)):
             name = ctypes.c_char_p()
