@@ -111,3 +111,31 @@ def assert_close_sum(got, ref, scale, what="", allow_empty=False):
         idx = np.flatnonzero(fin)[np.argmax(d / tol)]
         raise AssertionError(f"{what}: {int(bad.sum())} of {fin.sum()} elements out of tolerance; worst at "
                              f"{idx}: got {got[idx]!r} ref {ref[idx]!r} scale {sc[idx]:.3g}")
+
+
+def assert_close_normwise(got, ref, what="", rel=REL, abs_=ABS, allow_empty=False):
+    """|got - ref| <= max(abs_, rel * max|ref|) for every element: the error
+    measured against the size of the whole result rather than of each element.
+    For composed layer graphs, where an element near zero can come out of a
+    cancellation (LayerNorm's x - mean on offset data, an Add of opposite
+    signs) and carry the rounding error of the larger values it came from;
+    the routing mistakes such a test is for (a wrong input, broadcast or
+    in-place binding) move the result by a large fraction of its size."""
+    got = np.asarray(got)
+    ref = np.asarray(ref)
+    assert got.shape == ref.shape, f"{what}: shape {got.shape} != {ref.shape}"
+    _nonempty(ref, what, allow_empty)
+    g = got.astype(np.float64).ravel()
+    r = ref.astype(np.float64).ravel()
+    assert np.array_equal(np.isnan(g), np.isnan(r)), f"{what}: NaN pattern differs"
+    inf_r = np.isinf(r)
+    assert np.array_equal(g[inf_r], r[inf_r]) and not np.isinf(g[~inf_r]).any(), f"{what}: infinities differ"
+    fin = np.isfinite(r)
+    if not fin.any():
+        return
+    tol = max(abs_, rel * float(np.abs(r[fin]).max()))
+    d = np.abs(g[fin] - r[fin])
+    if (d > tol).any():
+        idx = np.flatnonzero(fin)[np.argmax(d)]
+        raise AssertionError(f"{what}: {int((d > tol).sum())} of {fin.sum()} elements beyond {tol:.3g}; worst at "
+                             f"flat index {idx}: got {g[idx]!r} ref {r[idx]!r} (|d|={abs(g[idx] - r[idx]):.3g})")
