@@ -172,6 +172,35 @@ def build_ops():
     ops.append(OpBench("cfg4_add", 4, "residual add fp32 [8192x4096]", "binary_vec<Add>",
                        3 * 8192 * 4096 * f4, 8192, "rows", make_add, lambda s: {"y": s[0][2]}))
 
+    # The reference's Softmax and RMSNorm layers, and LayerNorm with
+    # in_features unset, normalise their whole input as one row
+    # (LayerOps.hpp:276, :325-361; LayerOpsExt.hpp:345-378): the configs[4]
+    # activation [8192x4096] is then one row of 2^25 floats, cut into chunks
+    # over the whole GPU (partial, combine, apply).
+    def make_whole(kind):
+        def make(ctx, nsets):
+            x, _, _, eps = G.cfg4_layernorm()
+            w = G.cfg4_layernorm(rows=1)[1]  # an RMSNorm weight block of in_features = 4096
+            wd = _replicate(ctx, [w], 1)[0][0]
+            sets = _replicate(ctx, [x, np.empty_like(x)], nsets)
+            n = x.size
+            del x
+            if kind == "softmax":
+                return (lambda i: ctx.softmax(sets[i][0], sets[i][1], 1, n, M.SOFTMAX_MUL_INV)), sets + [[wd]]
+            if kind == "rmsnorm":
+                return (lambda i: ctx.rmsnorm(sets[i][0], wd, w.size, sets[i][1], 1, n, eps)), sets + [[wd]]
+            return (lambda i: ctx.layernorm(sets[i][0], None, None, sets[i][1], 1, n, eps)), sets + [[wd]]
+        return make
+    for kind, desc, kern, extra in (
+            ("softmax", "Softmax layer over the configs[4] activation as one row of 2^25 fp32",
+             "lr_partial<Softmax> + lr_combine + lr_apply", 0),
+            ("rmsnorm", "RMSNorm layer (weights 4096) over the configs[4] activation as one row of 2^25 fp32",
+             "lr_partial<SumSq> + lr_combine + lr_apply", 4096 * f4),
+            ("layernorm", "LayerNorm layer (in_features unset, no weight block) over the configs[4] activation "
+             "as one row of 2^25 fp32", "lr_partial<Chan> + lr_combine + lr_apply", 0)):
+        ops.append(OpBench(f"cfg4_{kind}_whole", 4, desc, kern, 2 * 8192 * 4096 * f4 + extra, 1, "rows",
+                           make_whole(kind), lambda s: {"y": s[0][1]}))
+
     # Backward of the same ops (Model::backwardPass branches, Model.cpp:7305-9153)
     # at the configs[3] / configs[4] shapes.
     def make_lnb(ctx, nsets):
@@ -359,6 +388,42 @@ def cpu_model():
     return platform.processor() or "unknown"
 
 
+def _whole_inputs(key):
+    """(kind, flat x, RMSNorm weights, eps, reference fn, port fn, float64 exact fn) of a
+    cfg4_*_whole op: the reference's own layer function, the C restatement,
+    and the float64 value of the same formula."""
+    sys.path.insert(0, os.path.join(REPO, "oracle"))
+    import oracle as O
+    kind = key[len("cfg4_"):-len("_whole")]
+    x, _, _, eps = G.cfg4_layernorm()
+    x = x.ravel()
+    w = G.cfg4_layernorm(rows=1)[1]
+    if kind == "softmax":  # LayerOps::softmax_forward, the Model's Softmax layer
+        ref = lambda: O.ref_softmax_forward(x)
+        port = lambda: O.softmax_rows(x.reshape(1, -1), O.SOFTMAX_MUL_INV).ravel()
+
+        def exact():
+            e = np.exp(x.astype(np.float64) - float(x.max()))
+            return e / e.sum()
+    elif kind == "rmsnorm":  # LayerOpsExt rms_norm over the whole vector, weight i while i < 4096
+        ref = lambda: O.ref_rms_norm_forward(x, w, eps=eps)
+        port = lambda: O.rmsnorm_whole(x, w, eps)
+
+        def exact():
+            x64 = x.astype(np.float64)
+            y = x64 / np.sqrt(np.mean(x64 * x64) + eps)
+            y[:w.size] *= w
+            return y
+    else:  # LayerOps::layernorm_forward, normalized_size = the whole input, no weight block
+        ref = lambda: O.ref_layernorm(x, 0, None, eps=eps)
+        port = lambda: O.layernorm(x, x.size, None, None, eps)
+
+        def exact():
+            x64 = x.astype(np.float64)
+            return (x64 - x64.mean()) / np.sqrt(x64.var() + eps)
+    return kind, x, w, eps, ref, port, exact
+
+
 def cpu_leg(which, reps):
     sys.path.insert(0, os.path.join(REPO, "oracle"))
     import oracle as O
@@ -521,6 +586,14 @@ def cpu_leg(which, reps):
                 rec(key, t, 31 * x.nbytes + 7 * 4096 * 4, rows, "reference",
                     f"{rows} of 8192 rows: Model::forwardPassNamed(training=true) then Model::backwardPass of the "
                     "same five layers (host tensor store)")
+        elif key.endswith("_whole"):
+            kind, x, w, eps, ref, port, _ = _whole_inputs(key)
+            nb = 2 * x.nbytes + (w.nbytes if kind == "rmsnorm" else 0)
+            if have_ref:
+                rec(key, O.time_port(ref, reps), nb, 1, "reference",
+                    f"the full 2^25-element row through the reference's {kind} layer function, median of {reps}")
+            else:
+                rec(key, O.time_port(port, reps), nb, 1, "port", f"the full 2^25-element row, oracle, median of {reps}")
         elif key == "cfg3_embedding_bwd":
             ids = G.cfg3_ids().ravel()[:4096].copy()
             dy = G.cfg3_embedding_grad()[:4096].copy()
@@ -533,13 +606,17 @@ def cpu_leg(which, reps):
     return out
 
 
-def _agreement(got, ref, bitexact, scale=None):
+def _agreement(got, ref, bitexact, scale=None, exact=None):
     """Max |d| and max |d|/|ref| of got against ref, and whether every element
     meets the path's rule: NaN where ref is NaN, equal infinities, and
     |d| <= max(1e-6, 1e-5 |ref|) elsewhere (or equal bits, for the byte-exact
     ops).  For results that are float32 sums of many terms, `scale` is the sum
     of the terms' magnitudes and replaces |ref| where larger: two summation
-    orders differ by ~u * scale however much the sum cancels."""
+    orders differ by ~u * scale however much the sum cancels.  With `exact`
+    (the float64 value), an element outside the tolerance of ref also passes
+    when it is within tolerance of exact and nearer to it than ref is: the
+    reference's sequential float32 sums over very long rows carry errors of
+    ~u*sqrt(n), beyond 1e-5 relative past ~10^4 terms."""
     g = np.ascontiguousarray(got, np.float32).ravel()
     r = np.ascontiguousarray(ref, np.float32).ravel()
     assert g.size == r.size, f"{g.size} != {r.size}"
@@ -553,10 +630,17 @@ def _agreement(got, ref, bitexact, scale=None):
     nz = r64 != 0
     mag = np.abs(r64) if scale is None else np.maximum(np.abs(r64), np.asarray(scale, np.float64).ravel()[fin])
     # An empty comparison proves nothing and does not pass.
-    within = bool(g.size > 0 and nan_ok and inf_ok and np.all(d <= np.maximum(1e-6, 1e-5 * mag)))
+    ok = d <= np.maximum(1e-6, 1e-5 * mag)
+    if exact is not None:
+        e64 = np.asarray(exact, np.float64).ravel()[fin]
+        de = np.abs(g64 - e64)
+        ok |= (de <= np.maximum(1e-6, 1e-5 * np.abs(e64))) & (de < np.abs(r64 - e64))
+    within = bool(g.size > 0 and nan_ok and inf_ok and np.all(ok))
     same_bits = same_bits and g.size > 0
     rule = ("bit-identical" if bitexact else
             "|d| <= max(1e-6, 1e-5|ref|)" if scale is None else "|d| <= max(1e-6, 1e-5 max(|ref|, sum of |terms|))")
+    if exact is not None:
+        rule += ", or within that of the float64 value and nearer to it than ref"
     return {"elements": int(g.size), "max_abs": float(d.max()) if d.size else 0.0,
             "max_rel": float((d[nz] / np.abs(r64[nz])).max()) if nz.any() else 0.0,
             "bitexact": same_bits, "pass": same_bits if bitexact else within, "rule": rule}
@@ -595,11 +679,12 @@ def parity_leg(ctx, by_key, which):
                 for b in bufs:
                     b.free()
 
-    def check(key, refs, vs, sample, exact=(), scales=None):
+    def check(key, refs, vs, sample, exact=(), scales=None, nearer=None):
         op = by_key[key]
         got = gpu_outputs(op, refs)
         scales = scales or {}
-        res = {n: _agreement(got[n], refs[n], n in exact, scales.get(n)) for n in refs}
+        nearer = nearer or {}
+        res = {n: _agreement(got[n], refs[n], n in exact, scales.get(n), nearer.get(n)) for n in refs}
         out[key] = {"vs": vs, "sample": sample, "pass": all(r["pass"] for r in res.values()), "outputs": res}
         log(f"parity {key}: {'pass' if out[key]['pass'] else 'FAIL'} vs {vs} "
             + ", ".join(f"{n} max_abs {r['max_abs']:.3g}" for n, r in res.items()))
@@ -695,6 +780,12 @@ def parity_leg(ctx, by_key, which):
             a, _ = G.cfg4_add()
             check(key, {"da": a, "db": a}, "port (accumulate_grad into absent names copies dy)",
                   "full [8192x4096]", exact=("da", "db"))
+        elif key.endswith("_whole"):
+            kind, x, _, _, ref, port, exact = _whole_inputs(key)
+            y = ref() if have_ref else port()
+            shape = (8192, 4096)
+            check(key, {"y": y.reshape(shape)}, ref_or_port, "the full 2^25-element row",
+                  nearer={"y": exact().reshape(shape)})
         elif key == "cfg3_embedding_bwd":
             gt = O.embedding_bwd(G.cfg3_ids(), G.cfg3_embedding_grad(), np.zeros(32000 * 4096, np.float32),
                                  32000, 4096, -1)

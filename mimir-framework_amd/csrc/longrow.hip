@@ -9,9 +9,10 @@
 // 256-thread workgroup each:
 //   1. partial : per chunk, the partial statistic (sum, sum of squares,
 //                sum of squared deviations, or softmax's (max, sum of exp));
-//   2. combine : one workgroup per row folds the chunk partials in a fixed
-//                order (per-thread strided sums, then the DPP/LDS tree), so
-//                the result does not depend on scheduling;
+//   2. combine : one 1024-thread workgroup per row folds the chunk partials
+//                in a fixed order (per-thread strided sums with eight loads in
+//                flight, then the DPP/LDS tree), so the result does not
+//                depend on scheduling;
 //   3. apply   : per chunk, the elementwise normalisation with the row stats.
 // LayerNorm's variance is two-pass within each chunk: the chunk is held in
 // registers, so its sum and its squared deviations about its own mean come
@@ -24,7 +25,8 @@
 // the row mean reaches the apply pass as a float pair hi + lo, so a row whose
 // mean is large against its spread keeps its precision.  Every
 // op reads x twice (statistics, then apply) and writes y once; the second
-// read walks the row backwards so its first part comes from the MALL.
+// read walks the row backwards, so that its first part can come from the MALL
+// (measured: the apply streams at the HBM rate whatever the row size).
 // Partials live in the context's scratch buffer, reused in stream order.
 #include "common.hpp"
 #include "internal.hpp"
@@ -71,13 +73,14 @@ __device__ __forceinline__ float chunk_len(const LongArgs& a, int64_t chunk) {
     return static_cast<float>(left < kChunkFloats ? left : kChunkFloats);
 }
 
-// Sum of one double per thread over the workgroup, in a fixed tree order;
-// every thread gets the total.
+// Sum of one double per thread over a workgroup of BS threads, in a fixed
+// tree order; every thread gets the total.
+template <int BS>
 __device__ __forceinline__ double block_sum_f64(double v, double* lds) {
     lds[threadIdx.x] = v;
     __syncthreads();
 #pragma unroll
-    for (int h = kBlock / 2; h > 0; h >>= 1) {
+    for (int h = BS / 2; h > 0; h >>= 1) {
         if (static_cast<int>(threadIdx.x) < h) lds[threadIdx.x] += lds[threadIdx.x + h];
         __syncthreads();
     }
@@ -161,38 +164,63 @@ __global__ __launch_bounds__(kBlock) void lr_partial(LongArgs a) {
 // Pass 2: fold one row's chunk partials (fixed order) into its statistics.
 //   kChan  -> stats = (mean hi, mean lo, 1/sqrt(var+eps))
 //   kSumSq / kSumSqAdd -> stats = (rms, -) kSoftmax -> stats = (max, sum)
+// Thread t folds chunks t, t + kCombine, t + 2*kCombine, ... in that order,
+// then the workgroup tree adds the threads; kCombineU partials per thread are
+// loaded before the first is folded, so a row of up to kCombine*kCombineU
+// chunks (32M floats) costs one memory round trip per pass instead of one
+// per chunk.
+constexpr int kCombine = 1024;
+constexpr int kCombineU = 8;
+
 template <int S>
-__global__ __launch_bounds__(kBlock) void lr_combine(LongArgs a) {
-    __shared__ float lds[2][kBlock / kWave];
+__global__ __launch_bounds__(kCombine) void lr_combine(LongArgs a) {
+    constexpr int NW = kCombine / kWave;
+    __shared__ float lds[2][NW];
     const int64_t row = blockIdx.x;
-    const float* p = a.partial + 2 * row * a.nchunks;
+    const float2* p = reinterpret_cast<const float2*>(a.partial) + row * a.nchunks;
+    const int64_t nc = a.nchunks;
+    // f(chunk, partial) for this thread's chunks, in chunk order.
+    auto each = [&](auto&& f) {
+        for (int64_t c0 = threadIdx.x; c0 < nc; c0 += static_cast<int64_t>(kCombine) * kCombineU) {
+            float2 v[kCombineU];
+#pragma unroll
+            for (int u = 0; u < kCombineU; ++u) {
+                const int64_t c = c0 + static_cast<int64_t>(u) * kCombine;
+                if (c < nc) v[u] = p[c];
+            }
+#pragma unroll
+            for (int u = 0; u < kCombineU; ++u) {
+                const int64_t c = c0 + static_cast<int64_t>(u) * kCombine;
+                if (c < nc) f(c, v[u]);
+            }
+        }
+    };
     const float n = static_cast<float>(a.cols);
     if constexpr (S == kSoftmax) {
         float m = -INFINITY;
-        for (int64_t c = threadIdx.x; c < a.nchunks; c += kBlock) m = fmaxf(m, p[2 * c]);
-        m = block_max<kBlock / kWave>(m, lds[0]);
+        each([&](int64_t, float2 q) { m = fmaxf(m, q.x); });
+        m = block_max<NW>(m, lds[0]);
         float s = 0.0f;
-        for (int64_t c = threadIdx.x; c < a.nchunks; c += kBlock) {
-            const float mc = p[2 * c];
-            if (mc != -INFINITY) s += p[2 * c + 1] * expf(mc - m);
-        }
-        s = block_sum<kBlock / kWave>(s, lds[1]);
+        each([&](int64_t, float2 q) {
+            if (q.x != -INFINITY) s += q.y * expf(q.x - m);
+        });
+        s = block_sum<NW>(s, lds[1]);
         if (threadIdx.x == 0) {
             a.stats[4 * row] = m;
             a.stats[4 * row + 1] = s;
         }
     } else if constexpr (S == kChan) {
-        __shared__ double lds64[kBlock];
+        __shared__ double lds64[kCombine];
         double s = 0.0;
-        for (int64_t c = threadIdx.x; c < a.nchunks; c += kBlock) s += static_cast<double>(p[2 * c]);
-        const double mean = block_sum_f64(s, lds64) / static_cast<double>(a.cols);
+        each([&](int64_t, float2 q) { s += static_cast<double>(q.x); });
+        const double mean = block_sum_f64<kCombine>(s, lds64) / static_cast<double>(a.cols);
         double m2 = 0.0;
-        for (int64_t c = threadIdx.x; c < a.nchunks; c += kBlock) {
-            const float nc = chunk_len(a, c);
-            const double d = static_cast<double>(p[2 * c] / nc) - mean;  // the chunk mean the partial used
-            m2 += static_cast<double>(p[2 * c + 1]) + static_cast<double>(nc) * d * d;
-        }
-        m2 = block_sum_f64(m2, lds64);
+        each([&](int64_t c, float2 q) {
+            const float ncl = chunk_len(a, c);
+            const double d = static_cast<double>(q.x / ncl) - mean;  // the chunk mean the partial used
+            m2 += static_cast<double>(q.y) + static_cast<double>(ncl) * d * d;
+        });
+        m2 = block_sum_f64<kCombine>(m2, lds64);
         if (threadIdx.x == 0) {
             const double mu = static_cast<double>(a.x[row * a.cols]) + mean;  // undo the shift
             const float hi = static_cast<float>(mu);
@@ -202,8 +230,8 @@ __global__ __launch_bounds__(kBlock) void lr_combine(LongArgs a) {
         }
     } else {
         float s = 0.0f;
-        for (int64_t c = threadIdx.x; c < a.nchunks; c += kBlock) s += p[2 * c];
-        s = block_sum<kBlock / kWave>(s, lds[0]);
+        each([&](int64_t, float2 q) { s += q.x; });
+        s = block_sum<NW>(s, lds[0]);
         if (threadIdx.x == 0) a.stats[4 * row] = sqrtf(s / n + a.eps);
     }
 }
@@ -303,15 +331,15 @@ int mimir::longrow_norm(mimir_ctx* ctx, int kind, const float* x, const float* r
     rev.reverse = 1;
     if (kind == 0) {
         lr_partial<kChan><<<grid, kBlock, 0, ctx->stream>>>(fwd);
-        lr_combine<kChan><<<nrows, kBlock, 0, ctx->stream>>>(fwd);
+        lr_combine<kChan><<<nrows, kCombine, 0, ctx->stream>>>(fwd);
         launch_apply<0, 0>(ctx, grid, rev);
     } else if (kind == 1) {
         lr_partial<kSumSq><<<grid, kBlock, 0, ctx->stream>>>(fwd);
-        lr_combine<kSumSq><<<nrows, kBlock, 0, ctx->stream>>>(fwd);
+        lr_combine<kSumSq><<<nrows, kCombine, 0, ctx->stream>>>(fwd);
         launch_apply<1, 0>(ctx, grid, rev);
     } else {
         lr_partial<kSumSqAdd><<<grid, kBlock, 0, ctx->stream>>>(fwd);
-        lr_combine<kSumSqAdd><<<nrows, kBlock, 0, ctx->stream>>>(fwd);
+        lr_combine<kSumSqAdd><<<nrows, kCombine, 0, ctx->stream>>>(fwd);
         launch_apply<2, 0>(ctx, grid, rev);
     }
     return launched(ctx, "longrow_norm");
@@ -324,7 +352,7 @@ int mimir::longrow_softmax(mimir_ctx* ctx, int mode, const float* x, float* y, i
     LongArgs rev = a;
     rev.reverse = 1;
     lr_partial<kSoftmax><<<grid, kBlock, 0, ctx->stream>>>(a);
-    lr_combine<kSoftmax><<<static_cast<unsigned>(rows), kBlock, 0, ctx->stream>>>(a);
+    lr_combine<kSoftmax><<<static_cast<unsigned>(rows), kCombine, 0, ctx->stream>>>(a);
     switch (mode) {
         case MIMIR_SOFTMAX_DIV_EPS: launch_apply<3, MIMIR_SOFTMAX_DIV_EPS>(ctx, grid, rev); break;
         case MIMIR_SOFTMAX_MUL_INV: launch_apply<3, MIMIR_SOFTMAX_MUL_INV>(ctx, grid, rev); break;

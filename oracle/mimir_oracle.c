@@ -16,7 +16,15 @@
 #define ORACLE_OK 0
 #define ORACLE_EINVAL 1
 
-/* LayerOps.hpp:264-319 */
+/* LayerOps.hpp:264-319.  The reference's two sums carry `#pragma omp simd
+ * reduction(+:...)` (:290, :297), which lets the compiler split them into
+ * vector-lane partial sums; they are taken here in index order.  The two agree
+ * within the path's tolerance at the row widths the tests pin against
+ * oracle/_ref (tests/test_oracle_vs_reference.py, up to 3000 per group); over
+ * whole-vector rows of millions of floats neither is near the float64 value
+ * (2^25 normal floats: the reference 1e-2 off, index order 0.2), and the HIP
+ * path is held to the reference's compiled output and to the float64 value
+ * instead. */
 int oracle_layernorm(const float* x, int64_t N, int64_t in_features,
                      const float* gamma, const float* beta, float eps, float* y) {
     /* LayerOps.hpp:276-280: normalized = in_features > 0 ? in_features : N,
