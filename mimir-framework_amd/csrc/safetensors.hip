@@ -600,9 +600,15 @@ int read_to_device(mimir_safetensors* f, const Entry& t, void* dst, size_t dst_b
         hipError_t e = hipEventSynchronize(f->done[b]);
         return e == hipSuccess ? MIMIR_OK : mimir::hip_fail(ctx, e, "hipEventSynchronize");
     };
+    // Every exit waits for the DMAs already queued: they read the staging
+    // buffers, which the next read of this file refills (its `used` flags
+    // start clear).
+    auto drain = [&](int st) {
+        (void)hipStreamSynchronize(ctx->stream);
+        return st;
+    };
     auto fail_read = [&]() {
-        (void)hipStreamSynchronize(ctx->stream);  // earlier DMAs may still run out of the buffers
-        return st_fail(f, ctx, MIMIR_EINVAL, "Failed to read tensor data: " + t.name);  // :201-206
+        return drain(st_fail(f, ctx, MIMIR_EINVAL, "Failed to read tensor data: " + t.name));  // :201-206
     };
     const off_t base = static_cast<off_t>(f->data_offset + t.begin);
     for (uint64_t c = 0; c < nchunks; c += 2) {
@@ -610,9 +616,9 @@ int read_to_device(mimir_safetensors* f, const Entry& t, void* dst, size_t dst_b
         const uint64_t off0 = c * kStageBytes, off1 = off0 + kStageBytes;
         const size_t n0 = static_cast<size_t>(bytes - off0 < kStageBytes ? bytes - off0 : kStageBytes);
         const size_t n1 = off1 < bytes ? static_cast<size_t>(bytes - off1 < kStageBytes ? bytes - off1 : kStageBytes) : 0;
-        if (int st = wait_buffer(b0)) return st;
+        if (int st = wait_buffer(b0)) return drain(st);
         if (n1 > 0)
-            if (int st = wait_buffer(b1)) return st;
+            if (int st = wait_buffer(b1)) return drain(st);
         char* s0 = static_cast<char*>(f->stage[b0]);
         char* s1 = static_cast<char*>(f->stage[b1]);
         if (n1 > 0 && helper) helper->start(s1, n1, base + static_cast<off_t>(off1));
@@ -623,15 +629,15 @@ int read_to_device(mimir_safetensors* f, const Entry& t, void* dst, size_t dst_b
             const int bk = k ? b1 : b0;
             hipError_t e = hipMemcpyAsync(static_cast<char*>(dst) + (k ? off1 : off0), k ? s1 : s0, k ? n1 : n0,
                                           hipMemcpyHostToDevice, ctx->stream);
-            if (e != hipSuccess) return mimir::hip_fail(ctx, e, "hipMemcpyAsync");
+            if (e != hipSuccess) return drain(mimir::hip_fail(ctx, e, "hipMemcpyAsync"));
             e = hipEventRecord(f->done[bk], ctx->stream);
-            if (e != hipSuccess) return mimir::hip_fail(ctx, e, "hipEventRecord");
+            if (e != hipSuccess) return drain(mimir::hip_fail(ctx, e, "hipEventRecord"));
             used[bk] = true;
         }
     }
     // The staging buffers are reused by the next read: wait for the last DMAs.
     for (int i = 0; i < kStages; ++i)
-        if (int st = wait_buffer(i)) return st;
+        if (int st = wait_buffer(i)) return drain(st);
     return MIMIR_OK;
 }
 
