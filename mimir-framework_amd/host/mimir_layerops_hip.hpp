@@ -32,6 +32,7 @@
 
 #include <cstddef>
 #include <cstdint>
+#include <mutex>
 #include <stdexcept>
 #include <string>
 #include <unordered_map>
@@ -51,6 +52,10 @@ private:
 
 // One device + stream.  Context::instance() is the process-wide default,
 // created on first use (as the reference's static compute engines are).
+// The host-vector mirrors below all use it, each holding lock() for its
+// whole call (uploads, launch, download), so host threads may call them at
+// the same time; a caller that wants its threads to overlap on the GPU gives
+// each thread a Context of its own and uses the device:: functions.
 class Context {
 public:
     explicit Context(int device = 0) {
@@ -70,6 +75,7 @@ public:
     }
 
     mimir_ctx* get() const { return ctx_; }
+    std::unique_lock<std::mutex> lock() { return std::unique_lock<std::mutex>(m_); }
 
     // MIMIR_EINVAL -> std::runtime_error (the reference's convention); others -> Error.
     void check(int st, const char* what) const {
@@ -82,6 +88,7 @@ public:
 
 private:
     mimir_ctx* ctx_ = nullptr;
+    std::mutex m_;
 };
 
 // Owning device buffer of T.
@@ -207,6 +214,7 @@ std::vector<float> layernorm_forward(const std::vector<float>& input, const Laye
                                      bool training = true) {
     (void)training;
     Context& c = Context::instance();
+    const auto held = c.lock();  // buffers below are freed before it is released
     const int64_t N = static_cast<int64_t>(input.size());
     const int64_t n = layer.in_features > 0 ? layer.in_features : N;
     if (n <= 0 || (N % n) != 0) throw std::runtime_error("LayerNorm: invalid normalized_size");
@@ -229,6 +237,7 @@ std::vector<float> layernorm_forward(const std::vector<float>& input, const Laye
 template <class LayerT>
 std::vector<float> softmax_forward(const std::vector<float>& input, const LayerT& layer) {
     Context& c = Context::instance();
+    const auto held = c.lock();  // buffers below are freed before it is released
     const bool log = layer.type_enum == decltype(layer.type_enum)::LogSoftmax;
     return detail::run1(c, input, input.size(), [&](const float* x, float* y) {
         device::softmax(c, x, y, 1, static_cast<int64_t>(input.size()),
@@ -238,6 +247,7 @@ std::vector<float> softmax_forward(const std::vector<float>& input, const LayerT
 
 inline void softmax_inplace(std::vector<float>& x, int seq_len, int dim) {
     Context& c = Context::instance();
+    const auto held = c.lock();  // buffers below are freed before it is released
     x = detail::run1(c, x, x.size(), [&](const float* in, float* y) {
         device::softmax(c, in, y, seq_len, dim, MIMIR_SOFTMAX_DIV_EPS);
     });
@@ -245,6 +255,7 @@ inline void softmax_inplace(std::vector<float>& x, int seq_len, int dim) {
 
 inline std::vector<float> gelu_forward(const std::vector<float>& input) {
     Context& c = Context::instance();
+    const auto held = c.lock();  // buffers below are freed before it is released
     return detail::run1(c, input, input.size(), [&](const float* x, float* y) {
         device::gelu(c, x, y, static_cast<int64_t>(input.size()));
     });
@@ -252,6 +263,7 @@ inline std::vector<float> gelu_forward(const std::vector<float>& input) {
 
 inline std::vector<float> silu_forward(const std::vector<float>& input) {
     Context& c = Context::instance();
+    const auto held = c.lock();  // buffers below are freed before it is released
     return detail::run1(c, input, input.size(), [&](const float* x, float* y) {
         device::silu(c, x, y, static_cast<int64_t>(input.size()));
     });
@@ -260,6 +272,7 @@ inline std::vector<float> silu_forward(const std::vector<float>& input) {
 inline std::vector<float> add_forward(const std::vector<float>& input1, const std::vector<float>& input2) {
     if (input1.empty() || input2.empty()) throw std::runtime_error("Add: inputs must be non-empty");
     Context& c = Context::instance();
+    const auto held = c.lock();  // buffers below are freed before it is released
     const size_t out_n = input1.size() > input2.size() ? input1.size() : input2.size();
     return detail::run2(c, input1, input2, out_n, [&](const float* a, const float* b, float* y) {
         device::add(c, a, static_cast<int64_t>(input1.size()), b, static_cast<int64_t>(input2.size()), y);
@@ -270,6 +283,7 @@ inline std::vector<float> multiply_forward(const std::vector<float>& input1,
                                            const std::vector<float>& input2) {
     if (input1.size() != input2.size()) throw std::runtime_error("Multiply: input sizes must match");
     Context& c = Context::instance();
+    const auto held = c.lock();  // buffers below are freed before it is released
     return detail::run2(c, input1, input2, input1.size(), [&](const float* a, const float* b, float* y) {
         device::mul(c, a, static_cast<int64_t>(input1.size()), b, static_cast<int64_t>(input2.size()), y);
     });
@@ -279,6 +293,7 @@ inline std::vector<float> multiply_forward(const std::vector<float>& input1,
 inline std::vector<float> silu_mul_forward(const std::vector<float>& gate, const std::vector<float>& up) {
     if (gate.size() != up.size()) throw std::runtime_error("Multiply: input sizes must match");
     Context& c = Context::instance();
+    const auto held = c.lock();  // buffers below are freed before it is released
     return detail::run2(c, gate, up, gate.size(), [&](const float* g, const float* u, float* y) {
         device::silu_mul(c, g, u, y, static_cast<int64_t>(gate.size()));
     });
@@ -291,6 +306,7 @@ namespace LayerOpsExt {
 template <class LayerT>
 std::vector<float> rms_norm_forward(const std::vector<float>& input, const LayerT& layer) {
     Context& c = Context::instance();
+    const auto held = c.lock();  // buffers below are freed before it is released
     if (input.empty()) return {};
     const float* w = layer.getWeights();
     const size_t wn = (layer.affine && w) ? layer.getWeightsSize() : 0;
@@ -308,6 +324,7 @@ namespace Normalization {
 inline void rms_norm(std::vector<float>& data, const std::vector<float>& gamma, int normalized_size,
                      float eps = 1e-6f) {
     Context& c = Context::instance();
+    const auto held = c.lock();  // buffers below are freed before it is released
     if (normalized_size <= 0 || gamma.size() < static_cast<size_t>(normalized_size))
         throw std::runtime_error("rms_norm: invalid normalized_size");
     const int64_t rows = static_cast<int64_t>(data.size()) / normalized_size;
@@ -323,6 +340,7 @@ inline void rms_norm(std::vector<float>& data, const std::vector<float>& gamma, 
 template <class LayerT>
 std::vector<float> embedding_forward(const std::vector<int>& ids, const LayerT& layer) {
     Context& c = Context::instance();
+    const auto held = c.lock();  // buffers below are freed before it is released
     const int32_t vocab = layer.vocab_size > 1 ? layer.vocab_size : 1;
     const int32_t dim = layer.embed_dim > 1 ? layer.embed_dim : 1;
     const float* w = layer.getWeights();
@@ -344,6 +362,7 @@ std::vector<float> embedding_forward(const std::vector<int>& ids, const LayerT& 
 template <class LayerT>
 std::vector<float> embedding_forward_float_ids(const std::vector<float>& x, const LayerT& layer) {
     Context& c = Context::instance();
+    const auto held = c.lock();  // buffers below are freed before it is released
     const int32_t vocab = layer.vocab_size > 1 ? layer.vocab_size : 1;
     const int32_t dim = layer.embed_dim > 1 ? layer.embed_dim : 1;
     const float* w = layer.getWeights();

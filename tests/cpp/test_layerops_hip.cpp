@@ -5,9 +5,11 @@
 // reference's CTest programs.  Run by tests/test_gpu_cpp_adapter.py.
 #include "mimir_layerops_hip.hpp"
 
+#include <atomic>
 #include <cmath>
 #include <cstdio>
 #include <string>
+#include <thread>
 #include <unordered_map>
 #include <vector>
 
@@ -319,6 +321,40 @@ int main() {
             me.forwardPassNamed({}, {{"ids", {1, 0, 2, 1}}}, true);
             me.backwardPass({1, 2, 3, 4, 5, 6, 7, 8}, emb);
             CHECK(emb[0].grad_weights == std::vector<float>({0, 0, 8, 10, 5, 6}));
+        }
+        {
+            // The host-vector mirrors share Context::instance() and hold its
+            // lock per call: four host threads calling them at once must get
+            // what one thread gets.
+            TestLayer ln;
+            ln.in_features = 256;
+            ln.weights.resize(512);
+            for (int i = 0; i < 512; ++i) ln.weights[i] = i < 256 ? 1.0f + 0.001f * i : 0.01f * (i - 256);
+            std::vector<float> xs(64 * 256);
+            for (size_t i = 0; i < xs.size(); ++i) xs[i] = std::sin(0.37f * static_cast<float>(i)) * 3.0f;
+            const std::vector<float> want_ln = mimir_hip::LayerOps::layernorm_forward(xs, ln);
+            std::vector<float> want_sm = xs;
+            mimir_hip::LayerOps::softmax_inplace(want_sm, 64, 256);
+            const std::vector<float> want_add = mimir_hip::LayerOps::add_forward(xs, want_ln);
+            std::atomic<int> bad{0};
+            std::vector<std::thread> pool;
+            for (int t = 0; t < 4; ++t)
+                pool.emplace_back([&] {
+                    try {
+                        for (int k = 0; k < 25; ++k) {
+                            if (mimir_hip::LayerOps::layernorm_forward(xs, ln) != want_ln) ++bad;
+                            std::vector<float> sm = xs;
+                            mimir_hip::LayerOps::softmax_inplace(sm, 64, 256);
+                            if (sm != want_sm) ++bad;
+                            if (mimir_hip::LayerOps::add_forward(xs, want_ln) != want_add) ++bad;
+                        }
+                    } catch (const std::exception& e) {
+                        std::fprintf(stderr, "FAIL: thread exception: %s\n", e.what());
+                        ++bad;
+                    }
+                });
+            for (auto& th : pool) th.join();
+            CHECK(bad.load() == 0);
         }
     } catch (const std::exception& e) {
         std::fprintf(stderr, "FAIL: unexpected exception: %s\n", e.what());
