@@ -1,5 +1,5 @@
-"""Tensors of more than 2^31 elements (8 GiB of fp32 each): every index on
-the path is 64-bit.  The inputs are filled on the device (constants, with a
+"""Tensors of more than 2^31 elements (8 GiB of fp32 each), forward and
+backward: every index on the path is 64-bit.  The inputs are filled on the device (constants, with a
 few rows uploaded where values must differ), and the results are checked at
 the head, around element 2^31 and at the tail, against the oracle where a
 row is not constant.  Peak device memory: 24 GiB of the MI355X's 288."""
@@ -86,4 +86,74 @@ def test_softmax_rows_past_2_31(ctx):
         assert_close(_slice(ctx, y, (rows - 1) * cols, cols), O.softmax_rows(tail)[0], "last row (past 2^31)")
     finally:
         for d in (x, y):
+            d.free()
+
+
+def test_gelu_bwd_past_2_31(ctx):
+    x, dy, dx = ctx.empty(BIG), ctx.empty(BIG), ctx.empty(BIG)
+    try:
+        ctx.fill(x, 0.75)
+        ctx.fill(dy, 2.0)
+        tail = np.random.default_rng(34).standard_normal(4096).astype(np.float32)
+        ctx.upload(x.offset(BIG - 4096, (4096,)), tail)
+        ctx.gelu_bwd(x, dy, dx, BIG)
+        one = O.gelu_bwd(np.full(4096, 0.75, np.float32), np.full(4096, 2.0, np.float32))
+        for start in (0, (1 << 31) - 4096):  # the random tail starts at element 2^31
+            assert_close(_slice(ctx, dx, start, 4096), one, f"gelu_bwd at {start}")
+        assert_close(_slice(ctx, dx, BIG - 4096, 4096), O.gelu_bwd(tail, np.full(4096, 2.0, np.float32)),
+                     "gelu_bwd tail (past 2^31)")
+    finally:
+        for d in (x, dy, dx):
+            d.free()
+
+
+def test_add_bwd_past_2_31(ctx):
+    dy, da, db = ctx.empty(BIG), ctx.empty(BIG), ctx.empty(BIG)
+    try:
+        ctx.fill(dy, 1.25)
+        ctx.add_bwd(dy, BIG, BIG, da, db)
+        want = np.full(4096, 1.25, np.float32)
+        for start in (0, (1 << 31) - 2048, BIG - 4096):
+            assert_bitexact(_slice(ctx, da, start, 4096), want, f"da at {start}")
+            assert_bitexact(_slice(ctx, db, start, 4096), want, f"db at {start}")
+    finally:
+        for d in (dy, da, db):
+            d.free()
+
+
+def test_layernorm_bwd_rows_past_2_31(ctx):
+    """Constant rows of x with a constant dy (x - mean = 0: those rows add
+    nothing to dgamma, and 0.5 each to dbeta), then two random rows at the
+    end, past element 2^31.  dx of a constant row and of the last rows, and
+    dgamma / dbeta, are held to the oracle.  eps = 1 keeps 1/sqrt(var + eps)
+    of the constant rows at 1, so their dx is not an amplified rounding
+    difference."""
+    cols = 4096
+    rows = BIG // cols  # 2^19 + 1 rows
+    x, dy, dx = ctx.empty((rows, cols)), ctx.empty((rows, cols)), ctx.empty((rows, cols))
+    rng = np.random.default_rng(35)
+    g = (1 + 0.05 * rng.standard_normal(cols)).astype(np.float32)
+    xt = rng.standard_normal((2, cols)).astype(np.float32)
+    dyt = rng.standard_normal((2, cols)).astype(np.float32)
+    dg_, dgam, dbet = ctx.to_device(g), ctx.to_device(np.zeros(cols, np.float32)), ctx.to_device(
+        np.zeros(cols, np.float32))
+    try:
+        ctx.fill(x, 0.75)
+        ctx.fill(dy, 0.5)
+        ctx.upload(x.offset((rows - 2) * cols, (2, cols)), xt)
+        ctx.upload(dy.offset((rows - 2) * cols, (2, cols)), dyt)
+        ctx.layernorm_bwd(x, dy, dg_, dx, dgam, dbet, rows, cols, 1.0)
+        const_dx, _ = O.layernorm_bwd(np.full(cols, 0.75, np.float32), np.full(cols, 0.5, np.float32), cols, g,
+                                      has_bias=True, eps=1.0)
+        assert_close(_slice(ctx, dx, 0, cols), const_dx, "dx of constant row 0")
+        assert_close(_slice(ctx, dx, (rows - 3) * cols, cols), const_dx, "dx of the constant row before the tail")
+        want_dx, gp = O.layernorm_bwd(xt, dyt, cols, g, has_bias=True, eps=1.0)
+        got = _slice(ctx, dx, (rows - 2) * cols, 2 * cols)
+        assert_close(got, want_dx.ravel(), "dx of the last rows (past 2^31)")
+        # dgamma: only the tail rows contribute; dbeta: (rows - 2) * 0.5 + the tail's dy
+        assert_close(dgam.numpy(), gp[:cols], "dgamma")
+        want_db = np.float64(rows - 2) * 0.5 + dyt.astype(np.float64).sum(0)
+        assert_close(dbet.numpy(), want_db.astype(np.float32), "dbeta")
+    finally:
+        for d in (x, dy, dx, dg_, dgam, dbet):
             d.free()
