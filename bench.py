@@ -242,20 +242,26 @@ def build_ops():
     ops.append(OpBench("cfg4_add_bwd", 4, "residual Add backward fp32 [8192x4096]: da, db", "add_bwd_vec",
                        3 * 8192 * 4096 * f4, 8192, "rows", make_addb, lambda s: {"da": s[0][1], "db": s[0][2]}))
 
-    uniq3 = int(np.unique(G.cfg3_ids()).size)
-
-    def make_embb(ctx, nsets):
-        ids = G.cfg3_ids()
-        dy = G.cfg3_embedding_grad()
-        gt = _replicate(ctx, [np.zeros(32000 * 4096, np.float32)], 1)[0][0]
-        sets = _replicate(ctx, [ids, dy], nsets)
-        return (lambda i: ctx.embedding_bwd(sets[i][0], ids.size, sets[i][1], gt, 32000 * 4096, 32000, 4096, -1)), \
-            sets + [[gt]]
-    ops.append(OpBench("cfg3_embedding_bwd", 3,
-                       f"Embedding backward (scatter-add) ids int32 [16x2048] -> table grad [32000x4096], "
-                       f"{uniq3} distinct ids", "radix sort + embed_bwd_rows_vec",
-                       32768 * 4 + 32768 * 4096 * f4 + 2 * uniq3 * 4096 * f4, 32768, "token rows", make_embb,
-                       lambda s: {"grad": s[-1][0]}))
+    # Embedding backward on the configs[3] ids (uniform), and on ids as text
+    # has them (Zipf, s = 1: the most frequent id is ~9% of the tokens).
+    def make_embb(ids_fn):
+        def make(ctx, nsets):
+            ids = ids_fn()
+            dy = G.cfg3_embedding_grad()
+            gt = _replicate(ctx, [np.zeros(32000 * 4096, np.float32)], 1)[0][0]
+            sets = _replicate(ctx, [ids, dy], nsets)
+            return (lambda i: ctx.embedding_bwd(sets[i][0], ids.size, sets[i][1], gt, 32000 * 4096, 32000, 4096,
+                                                -1)), sets + [[gt]]
+        return make
+    for key, ids_fn, what in (("cfg3_embedding_bwd", G.cfg3_ids, "ids int32 [16x2048]"),
+                              ("cfg3_embedding_bwd_zipf", G.cfg3_ids_zipf, "Zipf(1.0) ids int32 [16x2048]")):
+        ids_ = ids_fn()
+        u = int(np.unique(ids_).size)
+        top = int(np.bincount(ids_.ravel()).max())
+        ops.append(OpBench(key, 3, f"Embedding backward (scatter-add) {what} -> table grad [32000x4096], "
+                           f"{u} distinct ids, longest run {top}", "radix sort + embed_bwd_long_runs + embed_bwd_rows_vec",
+                           32768 * 4 + 32768 * 4096 * f4 + 2 * u * 4096 * f4, 32768, "token rows", make_embb(ids_fn),
+                           lambda s: {"grad": s[-1][0]}))
 
     # The device-resident runtime (mimir_store_run): a residual block's chain
     # of the path's layers at the configs[4] shape, routed by name as
@@ -594,8 +600,8 @@ def cpu_leg(which, reps):
                     f"the full 2^25-element row through the reference's {kind} layer function, median of {reps}")
             else:
                 rec(key, O.time_port(port, reps), nb, 1, "port", f"the full 2^25-element row, oracle, median of {reps}")
-        elif key == "cfg3_embedding_bwd":
-            ids = G.cfg3_ids().ravel()[:4096].copy()
+        elif key in ("cfg3_embedding_bwd", "cfg3_embedding_bwd_zipf"):
+            ids = (G.cfg3_ids() if key == "cfg3_embedding_bwd" else G.cfg3_ids_zipf()).ravel()[:4096].copy()
             dy = G.cfg3_embedding_grad()[:4096].copy()
             gt = np.zeros(32000 * 4096, np.float32)
             fn = O._oracle().oracle_embedding_bwd_i32
@@ -786,9 +792,9 @@ def parity_leg(ctx, by_key, which):
             shape = (8192, 4096)
             check(key, {"y": y.reshape(shape)}, ref_or_port, "the full 2^25-element row",
                   nearer={"y": exact().reshape(shape)})
-        elif key == "cfg3_embedding_bwd":
-            gt = O.embedding_bwd(G.cfg3_ids(), G.cfg3_embedding_grad(), np.zeros(32000 * 4096, np.float32),
-                                 32000, 4096, -1)
+        elif key in ("cfg3_embedding_bwd", "cfg3_embedding_bwd_zipf"):
+            ids = G.cfg3_ids() if key == "cfg3_embedding_bwd" else G.cfg3_ids_zipf()
+            gt = O.embedding_bwd(ids, G.cfg3_embedding_grad(), np.zeros(32000 * 4096, np.float32), 32000, 4096, -1)
             check(key, {"grad": gt}, "port", "full table [32000x4096], all 32768 tokens", exact=("grad",))
         elif key == "cfg4_runtime_block_train" and MR.available():
             rows = 512

@@ -962,6 +962,97 @@ __device__ __forceinline__ int64_t run_end(const uint32_t* keys, int64_t i, int6
     }
 }
 
+// Runs of at least kLongRun tokens (a frequent id) go to embed_bwd_long_runs,
+// which spreads each over kLongSlices one-wave workgroups by columns; a wave
+// then has few enough lanes to keep kLongBatch tokens of loads in flight.
+// Shorter runs stay with embed_bwd_rows_vec, one token's loads at a time.
+constexpr int kLongRun = 32;
+constexpr int kLongSlices = 16;
+constexpr int kLongBatch = 32;
+
+// The end of the run of `id` in the sorted keys, given a position j inside
+// it: the first position after j whose key differs, or n.  Each step the 64
+// lanes probe 64 evenly spaced positions of the range still open; since the
+// keys are sorted the probes that still hold `id` form a prefix, and the end
+// lies after the last of them and no later than the next probe -- log64 of
+// the span steps (3 for 32768 keys).  Must be reached by all 64 lanes.
+__device__ __forceinline__ int64_t run_end_search(const uint32_t* keys, int64_t j, int64_t n, uint32_t id) {
+    const int lane = threadIdx.x & (kWave - 1);
+    int64_t lo = j + 1, hi = n;  // keys[lo - 1] == id; the end is in [lo, hi]
+    while (lo < hi) {
+        const int64_t span = hi - lo;
+        const int64_t step = (span + kWave - 1) / kWave;
+        const int64_t q = lo + lane * step;
+        const unsigned long long m = __ballot(q < hi && keys[q] == id);
+        const int64_t cnt = __popcll(m);
+        if (cnt == 0) return lo;
+        const int64_t next = lo + cnt * step;  // the first probe past the run, or past hi
+        lo = lo + (cnt - 1) * step + 1;
+        if (next < hi) hi = next;
+    }
+    return lo;
+}
+
+// Long runs: workgroup (m, o) takes the run holding sorted position
+// m*kLongRun if that is the run's first multiple of kLongRun (so each long
+// run is taken once), and its o-th slice of 16-byte columns.  Each column
+// still adds the run's dy rows in token order onto the gradient row, so the
+// sums are the same bits as one workgroup walking the run.
+// Few of these one-wave workgroups do work (most exit at once), each on its
+// own CU: two waves per SIMD is the occupancy to plan for, and a scheduling
+// barrier keeps all kLongBatch loads of a batch in flight (without it the
+// compiler may trade most of them for registers).
+__global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1, 2))) void embed_bwd_long_runs(
+    const uint32_t* keys, const uint32_t* toks, int64_t n, uint32_t vocab, const float* dy, float* grad,
+    int64_t dim4) {
+    const int64_t p = static_cast<int64_t>(blockIdx.x) * kLongRun;
+    if (p >= n) return;
+    const uint32_t id = keys[p];
+    const uint32_t before = p >= kLongRun ? keys[p - kLongRun] : ~0u;  // loaded with id: one round trip
+    if (id >= vocab || before == id) return;  // not the run's first multiple of kLongRun
+    // One ballot over positions p - 15 .. p + 15 (lanes 0..30): the head is
+    // the first of them holding id (it is among p - 15 .. p), and the run is
+    // long when position head + 15 (at most p + 15) still holds it.
+    const int lane = threadIdx.x;
+    const int64_t slice = blockIdx.y;
+    const int64_t q = p - (kLongRun - 1) + lane;
+    const unsigned long long m = __ballot(lane < 2 * kLongRun - 1 && q >= 0 && q < n && keys[q] == id);
+    const int first = __builtin_ctzll(m);
+    if (first + kLongRun - 1 >= 2 * kLongRun - 1 || !((m >> (first + kLongRun - 1)) & 1ull)) return;
+    const int64_t head = p - (kLongRun - 1) + first;
+    const int64_t end = run_end_search(keys, head + kLongRun - 1, n, id);
+    const int64_t w = (dim4 + kLongSlices - 1) / kLongSlices;
+    const int64_t c1 = (slice + 1) * w < dim4 ? (slice + 1) * w : dim4;
+    const f4* src = reinterpret_cast<const f4*>(dy);
+    f4* g = reinterpret_cast<f4*>(grad) + static_cast<int64_t>(id) * dim4;
+    for (int64_t c = slice * w + lane; c < c1; c += kWave) {
+        f4 acc = __builtin_nontemporal_load(g + c);
+        int64_t j = head;
+        // The token indices of a batch are loaded while the previous batch's
+        // rows are in flight, so a batch costs one memory round trip.
+        uint32_t t[kLongBatch];
+        if (j + kLongBatch <= end) {
+#pragma unroll
+            for (int u = 0; u < kLongBatch; ++u) t[u] = toks[j + u];
+        }
+        for (; j + kLongBatch <= end; j += kLongBatch) {
+            f4 v[kLongBatch];
+#pragma unroll
+            for (int u = 0; u < kLongBatch; ++u)
+                v[u] = __builtin_nontemporal_load(src + static_cast<int64_t>(t[u]) * dim4 + c);
+            if (j + 2 * kLongBatch <= end) {
+#pragma unroll
+                for (int u = 0; u < kLongBatch; ++u) t[u] = toks[j + kLongBatch + u];
+            }
+            __builtin_amdgcn_sched_barrier(0);  // every load of the batch is issued before the first add
+#pragma unroll
+            for (int u = 0; u < kLongBatch; ++u) acc += v[u];
+        }
+        for (; j < end; ++j) acc += __builtin_nontemporal_load(src + static_cast<int64_t>(toks[j]) * dim4 + c);
+        __builtin_nontemporal_store(acc, g + c);
+    }
+}
+
 // One workgroup per sorted position; the first position of each id's run
 // adds the run's dy rows (token order, the sort is stable) onto the id's
 // gradient row.  Non-head positions leave at once.  Each thread owns CPT
@@ -969,10 +1060,13 @@ __device__ __forceinline__ int64_t run_end(const uint32_t* keys, int64_t i, int6
 // first token's row and the gradient row are requested before the run's
 // end is known, so a run of one (the common case) waits for two memory
 // round trips, not four.
+// With skip_long, runs of kLongRun tokens or more are left to
+// embed_bwd_long_runs (sorted keys: the run is that long when the key
+// kLongRun - 1 positions on is still the same).
 template <int TPT, int CPT>
 __global__ __launch_bounds__(TPT) void embed_bwd_rows_vec(const uint32_t* keys, const uint32_t* toks, int64_t n,
                                                           uint32_t vocab, const float* dy, float* grad,
-                                                          int64_t dim4) {
+                                                          int64_t dim4, int skip_long) {
     const int64_t i = blockIdx.x;
     const uint32_t id = keys[i];
     const uint32_t t0 = toks[i];
@@ -992,12 +1086,14 @@ __global__ __launch_bounds__(TPT) void embed_bwd_rows_vec(const uint32_t* keys, 
     };
     int64_t c0 = threadIdx.x;
     load_group(c0);
+    if (skip_long && i + kLongRun <= n && keys[i + kLongRun - 1] == id) return;  // the same for the workgroup
     // Every lane of the wave takes part in the ballots of run_end.
     const int64_t end = run_end(keys, i, n, id);
     while (c0 < dim4) {
 #pragma unroll
         for (int k = 0; k < CPT; ++k) acc[k] += v[k];
-        for (int64_t j = i + 1; j < end; ++j) {
+        int64_t j = i + 1;
+        for (; j < end; ++j) {
             const int64_t row = static_cast<int64_t>(toks[j]) * dim4;
 #pragma unroll
             for (int k = 0; k < CPT; ++k) {
@@ -1069,6 +1165,8 @@ int embed_bwd(mimir_ctx* ctx, const void* ids, int64_t n_ids, const float* dy, f
                                                               ctx->stream);
     if (e != hipSuccess) return hip_fail(ctx, e, "radix_sort_pairs (size)");
     const size_t vbytes = align256(sizeof(uint32_t) * n);
+    const bool vec = (dim % 4) == 0 && aligned16(dy) && aligned16(grad);
+    const bool long_runs = vec && n_ids >= kLongRun;
     void* s = nullptr;
     if (int st = ensure_scratch(ctx, 2 * vbytes + align256(sort_bytes), &s)) return st;
     char* base = static_cast<char*>(s);
@@ -1078,19 +1176,25 @@ int embed_bwd(mimir_ctx* ctx, const void* ids, int64_t n_ids, const float* dy, f
     e = rocprim::radix_sort_pairs<EmbedSortConfig>(temp, sort_bytes, keys, skeys, toks, stoks, n, 0u, end_bit,
                                                    ctx->stream);
     if (e != hipSuccess) return hip_fail(ctx, e, "radix_sort_pairs");
-    if ((dim % 4) == 0 && aligned16(dy) && aligned16(grad)) {
+    if (vec) {
+        const uint32_t v = static_cast<uint32_t>(vocab);
+        const int64_t dim4 = dim / 4;
+        if (long_runs) {
+            const dim3 lgrid(static_cast<unsigned>((n_ids + kLongRun - 1) / kLongRun), kLongSlices);
+            embed_bwd_long_runs<<<lgrid, kWave, 0, ctx->stream>>>(skeys, stoks, n_ids, v, dy, grad, dim4);
+            if (int st = launched(ctx, "embed_bwd_long_runs")) return st;
+        }
+        const int skip = long_runs ? 1 : 0;
         // Measured on MI355X at dim 4096 (MIMIR_TUNE gather=256/512/1024 picks a
         // variant): one 16-byte column per thread in 1024-thread workgroups
         // is fastest, 2-4 columns per thread in smaller ones ~2-4% slower.
-        const uint32_t v = static_cast<uint32_t>(vocab);
-        const int64_t dim4 = dim / 4;
         const int tpt = ctx->tune.gather_tpt ? ctx->tune.gather_tpt : (dim4 >= 1024 ? 1024 : dim4 >= 512 ? 512 : 256);
         if (tpt == 256)
-            embed_bwd_rows_vec<256, 4><<<n, 256, 0, ctx->stream>>>(skeys, stoks, n_ids, v, dy, grad, dim / 4);
+            embed_bwd_rows_vec<256, 4><<<n, 256, 0, ctx->stream>>>(skeys, stoks, n_ids, v, dy, grad, dim4, skip);
         else if (tpt == 512)
-            embed_bwd_rows_vec<512, 2><<<n, 512, 0, ctx->stream>>>(skeys, stoks, n_ids, v, dy, grad, dim / 4);
+            embed_bwd_rows_vec<512, 2><<<n, 512, 0, ctx->stream>>>(skeys, stoks, n_ids, v, dy, grad, dim4, skip);
         else
-            embed_bwd_rows_vec<1024, 1><<<n, 1024, 0, ctx->stream>>>(skeys, stoks, n_ids, v, dy, grad, dim / 4);
+            embed_bwd_rows_vec<1024, 1><<<n, 1024, 0, ctx->stream>>>(skeys, stoks, n_ids, v, dy, grad, dim4, skip);
         return launched(ctx, "embed_bwd_rows_vec");
     }
     embed_bwd_rows_scalar<<<n, kBlock, 0, ctx->stream>>>(skeys, stoks, n_ids, static_cast<uint32_t>(vocab), dy,

@@ -107,3 +107,13 @@ def cfg3_embedding_grad(batch=16, seq=2048, dim=4096):
 
 def cfg3_ids(batch=16, seq=2048, vocab=32000):
     return ids(3, 1, (batch, seq), vocab)
+
+
+def cfg3_ids_zipf(batch=16, seq=2048, vocab=32000, s=1.0):
+    """Token ids as text has them: the id of frequency rank r drawn with
+    probability proportional to r^-s (Zipf), ranks mapped to ids by a fixed
+    permutation.  At s = 1 the most frequent id is ~9% of the tokens."""
+    g = rng(3, 5)
+    p = np.arange(1, vocab + 1, dtype=np.float64) ** -s
+    ranks = g.choice(vocab, size=(batch, seq), p=p / p.sum())
+    return g.permutation(vocab).astype(np.int32)[ranks]

@@ -330,6 +330,29 @@ def test_embedding_bwd_repeats(ctx, case):
     assert_bitexact(_embedding_bwd_gpu(ctx, ids, dy, gt, vocab, dim, pad), ref, case)
 
 
+@pytest.mark.parametrize("case", ["zipf ids, dim 4096", "runs around the long-run threshold, dim 132"])
+def test_embedding_bwd_long_runs(ctx, case):
+    """Runs of 32 tokens or more are summed by column slices of the gradient
+    row on 16 workgroups; every column still adds its dy rows in token order,
+    so the result is the oracle's bit for bit.  Zipf(1.0) ids are what a text
+    batch looks like (the top id is ~9% of the tokens); the second case puts
+    runs of 1, 31, 32, 33, 63, 64, 65 and 200 tokens next to each other, with
+    33 16-byte columns per row (uneven slices, the last one partial)."""
+    if case.startswith("zipf"):
+        vocab, dim, n = 2000, 4096, 8192
+        r = np.arange(1, vocab + 1, dtype=np.float64) ** -1.0
+        ids = rng.choice(vocab, n, p=r / r.sum()).astype(np.int32)
+    else:
+        vocab, dim = 40, 132
+        ids = np.concatenate([np.full(k, i, np.int32) for i, k in enumerate([1, 31, 32, 33, 63, 64, 65, 200, 3])])
+        ids = rng.permutation(ids)
+        n = ids.size
+    dy = rng.standard_normal((n, dim)).astype(np.float32)
+    gt = rng.standard_normal(vocab * dim).astype(np.float32)
+    ref = O.embedding_bwd(ids, dy, gt, vocab, dim, -1)
+    assert_bitexact(_embedding_bwd_gpu(ctx, ids, dy, gt, vocab, dim, -1), ref, case)
+
+
 def test_embedding_bwd_unaligned_rows_and_errors(ctx):
     vocab, dim, n = 9, 5, 300
     ids = rng.integers(0, vocab, n).astype(np.int32)
