@@ -93,6 +93,10 @@ bool longrow_applies(int64_t rows, int64_t cols);
 int longrow_norm(mimir_ctx* ctx, int kind, const float* x, const float* r, float* r_out, const float* g,
                  const float* b, int64_t w_len, float* y, int64_t rows, int64_t cols, float eps);
 int longrow_softmax(mimir_ctx* ctx, int mode, const float* x, float* y, int64_t rows, int64_t cols);
+// LayerNorm backward of such rows (the forward's statistics, then two more
+// passes); dgamma / dbeta are added onto, as the reference's grad_weights.
+int longrow_ln_bwd(mimir_ctx* ctx, const float* x, const float* dy, const float* gamma, float* dx, float* dgamma,
+                   float* dbeta, int64_t rows, int64_t cols, float eps, int accumulate);
 
 // Embedding gather with an id mode (gather.hip); used by the C ABI and the
 // device-resident runtime (store.hip).

@@ -360,3 +360,168 @@ int mimir::longrow_softmax(mimir_ctx* ctx, int mode, const float* x, float* y, i
     }
     return launched(ctx, "longrow_softmax");
 }
+
+// ---------------------------------------------------------------------------
+// LayerNorm backward over long rows (Model.cpp:7719-7821 with a group of the
+// whole input, or of more than 16384 floats): the row statistics come from
+// the forward's passes (lr_partial / lr_combine<kChan>), then
+//   lr_bwd_partial : per chunk, sum(dxh) and sum(dxh * xh), dxh = dy * gamma;
+//   lr_bwd_combine : per row, their totals, added in float64 in chunk order;
+//   lr_bwd_apply   : per chunk, dx = inv_std/n * ((n*dxh - S1) - xh*S2) for
+//                    every row in order, and the chunk's columns of dgamma
+//                    (+= sum over rows of dy*xh) and dbeta (+= sum of dy),
+//                    each column owned by one thread: no slots, no atomics.
+// ---------------------------------------------------------------------------
+namespace {
+
+struct LongBwdArgs {
+    const float* x;
+    const float* dy;
+    const float* g;  // gamma, or null (no affine transform)
+    float* dx;
+    float* dgamma;   // += ; null: not wanted
+    float* dbeta;    // += ; null: not wanted
+    int64_t rows;
+    int64_t cols;
+    int64_t nchunks;
+    const float* stats;  // [rows][4]: mean hi, mean lo, inv_std
+    float* partial;      // [rows][nchunks][2]
+    float* sums;         // [rows][2]: S1, S2
+    int acc;             // dx += instead of dx =
+    int params16;        // dgamma / dbeta 16-byte aligned: vector read-modify-writes
+};
+
+__device__ __forceinline__ float sum4(f4 v) { return (v.x + v.y) + (v.z + v.w); }
+
+__global__ __launch_bounds__(kBlock) void lr_bwd_partial(LongBwdArgs a) {
+    __shared__ float lds[2][kBlock / kWave];
+    const int64_t row = blockIdx.y;
+    const int64_t chunk = blockIdx.x;
+    const int64_t c4n = a.cols >> 2;
+    const int64_t base = row * a.cols;
+    const float m0 = a.stats[4 * row], m1 = a.stats[4 * row + 1], inv = a.stats[4 * row + 2];
+    float p = 0.0f, q = 0.0f;
+#pragma unroll
+    for (int j = 0; j < kChunkVec; ++j) {
+        const int64_t c4 = chunk * kChunk4 + static_cast<int64_t>(j) * kBlock + threadIdx.x;
+        if (c4 < c4n) {
+            const f4 xv = ld4<false>(a.x + base + 4 * c4);  // kept in the caches for the apply pass
+            const f4 gv = ld4<false>(a.dy + base + 4 * c4);
+            const f4 dxh = a.g ? gv * *reinterpret_cast<const f4*>(a.g + 4 * c4) : gv;
+            const f4 xh = ((xv - m0) - m1) * inv;
+            p += sum4(dxh);
+            q += sum4(dxh * xh);
+        }
+    }
+    p = block_sum<kBlock / kWave>(p, lds[0]);
+    q = block_sum<kBlock / kWave>(q, lds[1]);
+    if (threadIdx.x == 0) {
+        a.partial[2 * (row * a.nchunks + chunk)] = p;
+        a.partial[2 * (row * a.nchunks + chunk) + 1] = q;
+    }
+}
+
+__global__ __launch_bounds__(kCombine) void lr_bwd_combine(LongBwdArgs a) {
+    __shared__ double lds64[kCombine];
+    const int64_t row = blockIdx.x;
+    const float2* p = reinterpret_cast<const float2*>(a.partial) + row * a.nchunks;
+    double s = 0.0, t = 0.0;
+    for (int64_t c0 = threadIdx.x; c0 < a.nchunks; c0 += static_cast<int64_t>(kCombine) * kCombineU) {
+        float2 v[kCombineU];
+#pragma unroll
+        for (int u = 0; u < kCombineU; ++u) {
+            const int64_t c = c0 + static_cast<int64_t>(u) * kCombine;
+            if (c < a.nchunks) v[u] = p[c];
+        }
+#pragma unroll
+        for (int u = 0; u < kCombineU; ++u) {
+            if (c0 + static_cast<int64_t>(u) * kCombine < a.nchunks) {
+                s += static_cast<double>(v[u].x);
+                t += static_cast<double>(v[u].y);
+            }
+        }
+    }
+    s = block_sum_f64<kCombine>(s, lds64);
+    t = block_sum_f64<kCombine>(t, lds64);
+    if (threadIdx.x == 0) {
+        a.sums[2 * row] = static_cast<float>(s);
+        a.sums[2 * row + 1] = static_cast<float>(t);
+    }
+}
+
+template <bool KEEP>
+__global__ __launch_bounds__(kBlock) void lr_bwd_apply(LongBwdArgs a) {
+    const int64_t chunk = blockIdx.x;
+    const int64_t c4n = a.cols >> 2;
+    const float n = static_cast<float>(a.cols);
+    const float invF = 1.0f / n;
+    f4 gm[kChunkVec], dg[kChunkVec], db[kChunkVec];
+#pragma unroll
+    for (int j = 0; j < kChunkVec; ++j) {
+        const int64_t c4 = chunk * kChunk4 + static_cast<int64_t>(j) * kBlock + threadIdx.x;
+        gm[j] = (a.g && c4 < c4n) ? *reinterpret_cast<const f4*>(a.g + 4 * c4) : f4(1.0f);
+        dg[j] = f4(0.0f);
+        db[j] = f4(0.0f);
+    }
+    for (int64_t row = 0; row < a.rows; ++row) {
+        const int64_t base = row * a.cols;
+        const float m0 = a.stats[4 * row], m1 = a.stats[4 * row + 1], inv = a.stats[4 * row + 2];
+        const float S1 = a.sums[2 * row], S2 = a.sums[2 * row + 1];
+        const float k = inv * invF;
+#pragma unroll
+        for (int j = 0; j < kChunkVec; ++j) {
+            const int64_t c4 = chunk * kChunk4 + static_cast<int64_t>(j) * kBlock + threadIdx.x;
+            if (c4 >= c4n) continue;
+            const f4 xv = ld4<true>(a.x + base + 4 * c4);
+            const f4 gv = ld4<true>(a.dy + base + 4 * c4);
+            const f4 xh = ((xv - m0) - m1) * inv;
+            const f4 dxh = gv * gm[j];
+            dg[j] += gv * xh;
+            db[j] += gv;
+            f4 o = k * ((n * dxh - S1) - xh * S2);
+            if (a.acc) o = ld4<true>(a.dx + base + 4 * c4) + o;
+            st_out<KEEP>(a.dx + base + 4 * c4, o);
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < kChunkVec; ++j) {
+        const int64_t c4 = chunk * kChunk4 + static_cast<int64_t>(j) * kBlock + threadIdx.x;
+        if (c4 >= c4n) continue;
+        if (a.params16) {
+            if (a.dgamma) *reinterpret_cast<f4*>(a.dgamma + 4 * c4) += dg[j];
+            if (a.dbeta) *reinterpret_cast<f4*>(a.dbeta + 4 * c4) += db[j];
+            continue;
+        }
+        for (int e = 0; e < 4; ++e) {
+            if (a.dgamma) a.dgamma[4 * c4 + e] += dg[j][e];
+            if (a.dbeta) a.dbeta[4 * c4 + e] += db[j][e];
+        }
+    }
+}
+
+}  // namespace
+
+int mimir::longrow_ln_bwd(mimir_ctx* ctx, const float* x, const float* dy, const float* gamma, float* dx,
+                          float* dgamma, float* dbeta, int64_t rows, int64_t cols, float eps, int accumulate) {
+    LongArgs a{x, nullptr, nullptr, nullptr, nullptr, 0, nullptr, 0, 0, 0, eps, nullptr, nullptr, 0};
+    a.rows = rows;
+    a.cols = cols;
+    a.nchunks = (cols + kChunkFloats - 1) / kChunkFloats;
+    // partials [rows][nchunks][2] (the statistics pass's, then this pass's),
+    // stats [rows][4], sums [rows][2]
+    const size_t bytes = sizeof(float) * (2 * static_cast<size_t>(rows) * a.nchunks + 6 * rows);
+    void* s = nullptr;
+    if (int st = ensure_scratch(ctx, bytes, &s)) return st;
+    a.partial = static_cast<float*>(s);
+    a.stats = a.partial + 2 * rows * a.nchunks;
+    const dim3 grid(static_cast<unsigned>(a.nchunks), static_cast<unsigned>(rows));
+    lr_partial<kChan><<<grid, kBlock, 0, ctx->stream>>>(a);
+    lr_combine<kChan><<<static_cast<unsigned>(rows), kCombine, 0, ctx->stream>>>(a);
+    LongBwdArgs b{x, dy, gamma, dx, dgamma, dbeta, rows, cols, a.nchunks, a.stats, a.partial,
+                  a.stats + 4 * rows, accumulate ? 1 : 0, aligned16(dgamma) && aligned16(dbeta) ? 1 : 0};
+    lr_bwd_partial<<<grid, kBlock, 0, ctx->stream>>>(b);
+    lr_bwd_combine<<<static_cast<unsigned>(rows), kCombine, 0, ctx->stream>>>(b);
+    if (ctx->keep_outputs) lr_bwd_apply<true><<<static_cast<unsigned>(a.nchunks), kBlock, 0, ctx->stream>>>(b);
+    else lr_bwd_apply<false><<<static_cast<unsigned>(a.nchunks), kBlock, 0, ctx->stream>>>(b);
+    return launched(ctx, "longrow_ln_bwd");
+}

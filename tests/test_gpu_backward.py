@@ -368,3 +368,56 @@ def test_embedding_bwd_unaligned_rows_and_errors(ctx):
     finally:
         for d in (bi, bdy, bg):
             d.free()
+
+
+def _ln_bwd_exact(x, dy, g, eps):
+    """float64 LayerNorm backward of rows of x: (dx, sum over rows of dy*xh, sum of dy)."""
+    x64, dy64 = x.astype(np.float64), dy.astype(np.float64)
+    mu = x64.mean(1, keepdims=True)
+    sig = np.sqrt(((x64 - mu) ** 2).mean(1, keepdims=True) + eps)
+    xh = (x64 - mu) / sig
+    dxh = dy64 * (1.0 if g is None else g.astype(np.float64))
+    dx = (dxh - dxh.mean(1, keepdims=True) - xh * (dxh * xh).mean(1, keepdims=True)) / sig
+    return dx, (dy64 * xh).sum(0), dy64.sum(0)
+
+
+@pytest.mark.parametrize("rows,cols,affine,acc,shift", [(1, 1 << 20, True, False, 0), (3, 20004, False, True, 0),
+                                                        (2, 65536, True, True, 0), (2, 20000, True, False, 1)])
+def test_layernorm_bwd_long_rows(ctx, rows, cols, affine, acc, shift):
+    """Rows wider than one workgroup takes (a LayerNorm with in_features unset
+    normalises the whole input): the chunked path.  Offset rows (mean 3), the
+    reference's sequential sums against the float64 value: dx within tolerance
+    of the oracle or nearer the float64 value than it; dgamma / dbeta (added
+    onto random values) and the accumulated dx within tolerance.  shift=1
+    puts dgamma / dbeta one float off 16-byte alignment (scalar updates)."""
+    r = np.random.default_rng(cols + rows)
+    x = (3 + r.standard_normal((rows, cols))).astype(np.float32)
+    dy = r.standard_normal((rows, cols)).astype(np.float32)
+    g = (1 + 0.1 * r.standard_normal(cols)).astype(np.float32) if affine else None
+    dx0 = r.standard_normal((rows, cols)).astype(np.float32) if acc else np.zeros((rows, cols), np.float32)
+    gp0 = r.standard_normal(2 * cols).astype(np.float32)
+    bx, bdy, bdx = ctx.to_device(x), ctx.to_device(dy), ctx.to_device(dx0)
+    bg = ctx.to_device(g) if affine else None
+    keep = []
+
+    def params(v):
+        full = ctx.to_device(np.concatenate([np.zeros(shift, np.float32), v]))
+        keep.append(full)
+        return full.offset(shift, (cols,)) if shift else full
+    bdg = params(gp0[:cols].copy()) if affine else None
+    bdb = params(gp0[cols:].copy()) if affine else None
+    try:
+        ctx.layernorm_bwd(bx, bdy, bg, bdx, bdg, bdb, rows, cols, 1e-5, accumulate=acc)
+        got = bdx.numpy()
+        ref, gp = O.layernorm_bwd(x, dy, cols, g, has_bias=affine, eps=1e-5,
+                                  grad_params=gp0 if affine else None)
+        ex_dx, ex_dg, ex_db = _ln_bwd_exact(x, dy, g, 1e-5)
+        assert_close_or_nearer_exact(got, dx0 + ref.reshape(rows, cols), dx0.astype(np.float64) + ex_dx,
+                                     "dx accumulated" if acc else "dx")
+        if affine:
+            assert_close(bdg.numpy(), (gp0[:cols] + ex_dg).astype(np.float32), "dgamma")
+            assert_close(bdb.numpy(), (gp0[cols:] + ex_db).astype(np.float32), "dbeta")
+    finally:
+        for d in [bx, bdy, bdx, bg] + keep:
+            if d is not None:
+                d.free()
