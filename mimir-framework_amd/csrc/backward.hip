@@ -1220,7 +1220,7 @@ int mimir_layernorm_bwd(mimir_ctx* ctx, const float* x, const float* dy, const f
     const int64_t c4 = n / 4;
     const bool vec = (n % 4) == 0 && aligned16(x) && aligned16(dy) && aligned16(dx) && (!gamma || aligned16(gamma));
     // A few rows too wide for one workgroup: chunked over the whole GPU.
-    if (vec && longrow_applies(groups, n))
+    if (vec && groups <= kLongBwdRows && longrow_applies(groups, n))
         return longrow_ln_bwd(ctx, x, dy, gamma, dx, dgamma, dbeta, groups, n, eps, accumulate);
     if (vec) {
         const RowShape over = ctx->tune.lnbwd;

@@ -86,15 +86,17 @@ inline bool grid_for(int64_t units, int64_t per_block, unsigned* blocks) {
 // the work already enqueued, which may still read the old buffer.
 int ensure_scratch(mimir_ctx* ctx, size_t bytes, void** out);
 
-// Rows too long for one workgroup's registers, few of them: split each row
-// over many workgroups (longrow.hip).  `kind`: 0 LayerNorm, 1 RMSNorm,
+// Rows too long for one workgroup's registers: split each row over many
+// workgroups (longrow.hip).  `kind`: 0 LayerNorm, 1 RMSNorm,
 // 2 add + RMSNorm; softmax `mode` as in mimir_softmax_fwd.
 bool longrow_applies(int64_t rows, int64_t cols);
 int longrow_norm(mimir_ctx* ctx, int kind, const float* x, const float* r, float* r_out, const float* g,
                  const float* b, int64_t w_len, float* y, int64_t rows, int64_t cols, float eps);
 int longrow_softmax(mimir_ctx* ctx, int mode, const float* x, float* y, int64_t rows, int64_t cols);
-// LayerNorm backward of such rows (the forward's statistics, then two more
-// passes); dgamma / dbeta are added onto, as the reference's grad_weights.
+// LayerNorm backward of up to kLongBwdRows such rows (the forward's
+// statistics, then two more passes); dgamma / dbeta are added onto, as the
+// reference's grad_weights.
+constexpr int64_t kLongBwdRows = 16;
 int longrow_ln_bwd(mimir_ctx* ctx, const float* x, const float* dy, const float* gamma, float* dx, float* dgamma,
                    float* dbeta, int64_t rows, int64_t cols, float eps, int accumulate);
 

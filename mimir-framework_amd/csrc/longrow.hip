@@ -306,8 +306,10 @@ int setup(mimir_ctx* ctx, LongArgs& a, int64_t rows, int64_t cols) {
 
 }  // namespace
 
+// Rows wider than a register-resident workgroup takes, however many: the
+// grid is chunks x rows (rows up to 65535, the grid's y limit used here).
 bool mimir::longrow_applies(int64_t rows, int64_t cols) {
-    return cols > 16384 && rows <= 256 && (cols + kChunkFloats - 1) / kChunkFloats <= 0x7fffffffLL;
+    return cols > 16384 && rows <= 65535 && (cols + kChunkFloats - 1) / kChunkFloats <= 0x7fffffffLL;
 }
 
 namespace {
@@ -362,8 +364,10 @@ int mimir::longrow_softmax(mimir_ctx* ctx, int mode, const float* x, float* y, i
 }
 
 // ---------------------------------------------------------------------------
-// LayerNorm backward over long rows (Model.cpp:7719-7821 with a group of the
-// whole input, or of more than 16384 floats): the row statistics come from
+// LayerNorm backward over a few long rows (Model.cpp:7719-7821 with a group of
+// the whole input, or of more than 16384 floats; at most kLongBwdRows rows,
+// since the apply pass walks every row in each chunk's workgroup): the row
+// statistics come from
 // the forward's passes (lr_partial / lr_combine<kChan>), then
 //   lr_bwd_partial : per chunk, sum(dxh) and sum(dxh * xh), dxh = dy * gamma;
 //   lr_bwd_combine : per row, their totals, added in float64 in chunk order;

@@ -352,7 +352,8 @@ def test_rope_qk(ctx, B, S, H, Hk, D):
 # Long rows split over many workgroups (longrow.hip)
 # ---------------------------------------------------------------------------
 
-@pytest.mark.parametrize("rows,cols", [(1, 1 << 20), (3, 65536), (2, 20004), (1, 4097 * 4), (2, 20001)])
+@pytest.mark.parametrize("rows,cols", [(1, 1 << 20), (3, 65536), (2, 20004), (1, 4097 * 4), (2, 20001),
+                                       (300, 20004)])
 def test_longrow_layernorm_rmsnorm(ctx, rows, cols):
     x = (rng.standard_normal((rows, cols), dtype=np.float32) * 1.3 + 0.2)
     g = (1 + 0.05 * rng.standard_normal(cols)).astype(np.float32)
@@ -410,6 +411,15 @@ def test_longrow_softmax_with_masked_chunks(ctx, mode):
     got = run(ctx, lambda dx, y: ctx.softmax(dx, y, rows, cols, mode), s, out_shape=s.shape)
     assert_close_or_nearer_exact(got, O.softmax_rows(s, mode), X.softmax(s, mode), f"long softmax {mode}")
     assert np.isnan(got[1]).all() and np.isnan(got[2]).all()
+
+
+@pytest.mark.parametrize("mode", [M.SOFTMAX_DIV_EPS, M.SOFTMAX_LOG])
+def test_longrow_softmax_many_rows(ctx, mode):
+    """Many wide rows (a vocabulary-sized log-softmax): chunks x rows."""
+    rows, cols = 300, 20004
+    s = (3 * rng.standard_normal((rows, cols))).astype(np.float32)
+    got = run(ctx, lambda dx, y: ctx.softmax(dx, y, rows, cols, mode), s, out_shape=s.shape)
+    assert_close_or_nearer_exact(got, O.softmax_rows(s, mode), X.softmax(s, mode), f"wide softmax {mode}")
 
 
 def test_longrow_softmax_layer_whole_vector(ctx):
