@@ -348,7 +348,7 @@ __global__ __launch_bounds__(kSumLanes * kWave) void sum_slots4(const float* par
 // rows in order.  (Folding that second level into this kernel with an
 // arrival counter needs a device-scope release per block, which on this
 // GPU writes back the XCD's L2 each time and costs far more than a launch.)
-constexpr int kGroups = 16;
+constexpr int kGroups = kSlotGroups;
 
 template <int U>
 __global__ __launch_bounds__(kBlock) void slot_groups4(const float* part, int64_t nslots, int64_t stride,
@@ -1219,9 +1219,18 @@ int mimir_layernorm_bwd(mimir_ctx* ctx, const float* x, const float* dy, const f
     LnBwdArgs a{x, dy, gamma, dx, nullptr, nullptr, groups, n, eps, accumulate ? 1 : 0};
     const int64_t c4 = n / 4;
     const bool vec = (n % 4) == 0 && aligned16(x) && aligned16(dy) && aligned16(dx) && (!gamma || aligned16(gamma));
-    // A few rows too wide for one workgroup: chunked over the whole GPU.
-    if (vec && groups <= kLongBwdRows && longrow_applies(groups, n))
-        return longrow_ln_bwd(ctx, x, dy, gamma, dx, dgamma, dbeta, groups, n, eps, accumulate);
+    // Rows too wide for one workgroup: chunked over the whole GPU; with more
+    // than one group of rows, dgamma / dbeta come from per-group slots.
+    if (vec && longrow_applies(groups, n)) {
+        float* slots = nullptr;
+        float* tmp = nullptr;
+        int64_t nslots = 0;
+        if (int st = longrow_ln_bwd(ctx, x, dy, gamma, dx, dgamma, dbeta, groups, n, eps, accumulate, &slots,
+                                    &nslots, &tmp))
+            return st;
+        if (!slots) return MIMIR_OK;
+        return launch_sum_slots(ctx, slots, nslots, 2 * n, dbeta ? 2 * n : n, dgamma, dbeta, n, true, tmp);
+    }
     if (vec) {
         const RowShape over = ctx->tune.lnbwd;
         const RowShape s = shape_fits(over, c4) ? over : default_norm_shape(c4);

@@ -93,12 +93,19 @@ bool longrow_applies(int64_t rows, int64_t cols);
 int longrow_norm(mimir_ctx* ctx, int kind, const float* x, const float* r, float* r_out, const float* g,
                  const float* b, int64_t w_len, float* y, int64_t rows, int64_t cols, float eps);
 int longrow_softmax(mimir_ctx* ctx, int mode, const float* x, float* y, int64_t rows, int64_t cols);
-// LayerNorm backward of up to kLongBwdRows such rows (the forward's
-// statistics, then two more passes); dgamma / dbeta are added onto, as the
-// reference's grad_weights.
+// Second-level groups of the slot sums (backward.hip launch_sum_slots): its
+// `tmp` holds kSlotGroups rows of the summed width.
+constexpr int kSlotGroups = 16;
+// LayerNorm backward of such rows (the forward's statistics, then two more
+// passes); dgamma / dbeta are added onto, as the reference's grad_weights.
+// The apply pass takes kLongBwdRows rows per workgroup: with more rows than
+// that and dgamma wanted, it leaves one slot of column sums per row group,
+// [*nslots][2*cols] at *slots with room for the slot sums at *tmp, for the
+// caller to add into dgamma / dbeta; else *slots is null.
 constexpr int64_t kLongBwdRows = 16;
 int longrow_ln_bwd(mimir_ctx* ctx, const float* x, const float* dy, const float* gamma, float* dx, float* dgamma,
-                   float* dbeta, int64_t rows, int64_t cols, float eps, int accumulate);
+                   float* dbeta, int64_t rows, int64_t cols, float eps, int accumulate, float** slots,
+                   int64_t* nslots, float** tmp);
 
 // Embedding gather with an id mode (gather.hip); used by the C ABI and the
 // device-resident runtime (store.hip).

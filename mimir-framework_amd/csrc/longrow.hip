@@ -364,17 +364,17 @@ int mimir::longrow_softmax(mimir_ctx* ctx, int mode, const float* x, float* y, i
 }
 
 // ---------------------------------------------------------------------------
-// LayerNorm backward over a few long rows (Model.cpp:7719-7821 with a group of
-// the whole input, or of more than 16384 floats; at most kLongBwdRows rows,
-// since the apply pass walks every row in each chunk's workgroup): the row
-// statistics come from
+// LayerNorm backward over long rows (Model.cpp:7719-7821 with a group of the
+// whole input, or of more than 16384 floats): the row statistics come from
 // the forward's passes (lr_partial / lr_combine<kChan>), then
 //   lr_bwd_partial : per chunk, sum(dxh) and sum(dxh * xh), dxh = dy * gamma;
 //   lr_bwd_combine : per row, their totals, added in float64 in chunk order;
-//   lr_bwd_apply   : per chunk, dx = inv_std/n * ((n*dxh - S1) - xh*S2) for
-//                    every row in order, and the chunk's columns of dgamma
-//                    (+= sum over rows of dy*xh) and dbeta (+= sum of dy),
-//                    each column owned by one thread: no slots, no atomics.
+//   lr_bwd_apply   : per (chunk, group of kLongBwdRows rows), dx =
+//                    inv_std/n * ((n*dxh - S1) - xh*S2) for its rows in
+//                    order, and the chunk's column sums of dy*xh and dy over
+//                    those rows, each column owned by one thread: added into
+//                    dgamma / dbeta when there is one group, else written to
+//                    the group's slot for the caller's slot sums.
 // ---------------------------------------------------------------------------
 namespace {
 
@@ -393,6 +393,7 @@ struct LongBwdArgs {
     float* sums;         // [rows][2]: S1, S2
     int acc;             // dx += instead of dx =
     int params16;        // dgamma / dbeta 16-byte aligned: vector read-modify-writes
+    float* slots;        // [groups][2*cols] column sums per row group, or null (add into dgamma / dbeta)
 };
 
 __device__ __forceinline__ float sum4(f4 v) { return (v.x + v.y) + (v.z + v.w); }
@@ -467,7 +468,9 @@ __global__ __launch_bounds__(kBlock) void lr_bwd_apply(LongBwdArgs a) {
         dg[j] = f4(0.0f);
         db[j] = f4(0.0f);
     }
-    for (int64_t row = 0; row < a.rows; ++row) {
+    const int64_t r0 = static_cast<int64_t>(blockIdx.y) * kLongBwdRows;
+    const int64_t r1 = r0 + kLongBwdRows < a.rows ? r0 + kLongBwdRows : a.rows;
+    for (int64_t row = r0; row < r1; ++row) {
         const int64_t base = row * a.cols;
         const float m0 = a.stats[4 * row], m1 = a.stats[4 * row + 1], inv = a.stats[4 * row + 2];
         const float S1 = a.sums[2 * row], S2 = a.sums[2 * row + 1];
@@ -486,6 +489,17 @@ __global__ __launch_bounds__(kBlock) void lr_bwd_apply(LongBwdArgs a) {
             if (a.acc) o = ld4<true>(a.dx + base + 4 * c4) + o;
             st_out<KEEP>(a.dx + base + 4 * c4, o);
         }
+    }
+    if (a.slots) {  // this row group's slot: dgamma sums, then dbeta sums (16-byte aligned)
+        f4* sg = reinterpret_cast<f4*>(a.slots + static_cast<int64_t>(blockIdx.y) * 2 * a.cols);
+#pragma unroll
+        for (int j = 0; j < kChunkVec; ++j) {
+            const int64_t c4 = chunk * kChunk4 + static_cast<int64_t>(j) * kBlock + threadIdx.x;
+            if (c4 >= c4n) continue;
+            sg[c4] = dg[j];
+            sg[c4n + c4] = db[j];
+        }
+        return;
     }
 #pragma unroll
     for (int j = 0; j < kChunkVec; ++j) {
@@ -506,26 +520,43 @@ __global__ __launch_bounds__(kBlock) void lr_bwd_apply(LongBwdArgs a) {
 }  // namespace
 
 int mimir::longrow_ln_bwd(mimir_ctx* ctx, const float* x, const float* dy, const float* gamma, float* dx,
-                          float* dgamma, float* dbeta, int64_t rows, int64_t cols, float eps, int accumulate) {
+                          float* dgamma, float* dbeta, int64_t rows, int64_t cols, float eps, int accumulate,
+                          float** slots, int64_t* nslots, float** tmp) {
+    const int64_t groups = (rows + kLongBwdRows - 1) / kLongBwdRows;
+    const bool use_slots = groups > 1 && dgamma;
+    *slots = nullptr;
+    *nslots = 0;
+    *tmp = nullptr;
     LongArgs a{x, nullptr, nullptr, nullptr, nullptr, 0, nullptr, 0, 0, 0, eps, nullptr, nullptr, 0};
     a.rows = rows;
     a.cols = cols;
     a.nchunks = (cols + kChunkFloats - 1) / kChunkFloats;
     // partials [rows][nchunks][2] (the statistics pass's, then this pass's),
-    // stats [rows][4], sums [rows][2]
-    const size_t bytes = sizeof(float) * (2 * static_cast<size_t>(rows) * a.nchunks + 6 * rows);
+    // stats [rows][4], sums [rows][2]; then, with slots, [groups][2*cols] and
+    // the slot sums' [kSlotGroups][2*cols], each 256-byte aligned.
+    const size_t head = (sizeof(float) * (2 * static_cast<size_t>(rows) * a.nchunks + 6 * rows) + 255) & ~size_t(255);
+    const size_t slot_bytes = use_slots ? sizeof(float) * static_cast<size_t>(groups) * 2 * cols : 0;
+    const size_t tmp_bytes = use_slots ? sizeof(float) * static_cast<size_t>(kSlotGroups) * 2 * cols : 0;
     void* s = nullptr;
-    if (int st = ensure_scratch(ctx, bytes, &s)) return st;
+    if (int st = ensure_scratch(ctx, head + slot_bytes + tmp_bytes, &s)) return st;
     a.partial = static_cast<float*>(s);
     a.stats = a.partial + 2 * rows * a.nchunks;
+    float* slot_base = use_slots ? reinterpret_cast<float*>(static_cast<char*>(s) + head) : nullptr;
     const dim3 grid(static_cast<unsigned>(a.nchunks), static_cast<unsigned>(rows));
     lr_partial<kChan><<<grid, kBlock, 0, ctx->stream>>>(a);
     lr_combine<kChan><<<static_cast<unsigned>(rows), kCombine, 0, ctx->stream>>>(a);
     LongBwdArgs b{x, dy, gamma, dx, dgamma, dbeta, rows, cols, a.nchunks, a.stats, a.partial,
-                  a.stats + 4 * rows, accumulate ? 1 : 0, aligned16(dgamma) && aligned16(dbeta) ? 1 : 0};
+                  a.stats + 4 * rows, accumulate ? 1 : 0, aligned16(dgamma) && aligned16(dbeta) ? 1 : 0, slot_base};
     lr_bwd_partial<<<grid, kBlock, 0, ctx->stream>>>(b);
     lr_bwd_combine<<<static_cast<unsigned>(rows), kCombine, 0, ctx->stream>>>(b);
-    if (ctx->keep_outputs) lr_bwd_apply<true><<<static_cast<unsigned>(a.nchunks), kBlock, 0, ctx->stream>>>(b);
-    else lr_bwd_apply<false><<<static_cast<unsigned>(a.nchunks), kBlock, 0, ctx->stream>>>(b);
-    return launched(ctx, "longrow_ln_bwd");
+    const dim3 agrid(static_cast<unsigned>(a.nchunks), static_cast<unsigned>(groups));
+    if (ctx->keep_outputs) lr_bwd_apply<true><<<agrid, kBlock, 0, ctx->stream>>>(b);
+    else lr_bwd_apply<false><<<agrid, kBlock, 0, ctx->stream>>>(b);
+    if (int st = launched(ctx, "longrow_ln_bwd")) return st;
+    if (use_slots) {
+        *slots = slot_base;
+        *nslots = groups;
+        *tmp = reinterpret_cast<float*>(reinterpret_cast<char*>(slot_base) + slot_bytes);
+    }
+    return MIMIR_OK;
 }
