@@ -9,8 +9,9 @@ gfx950 assembly and checks every 16-byte global store: `nt` in the streamed
 variants, plain in the kept ones (add+RMSNorm's residual output is streamed
 in both, since a later block reads it, not the next op).  The backward
 kernels and the device copy take the same parameter; the LayerNorm
-backward's dgamma/dbeta slot partials are plain stores in both variants
-(the slot sums read them back next)."""
+backward's dgamma/dbeta slot partials (ln_bwd_vec, and lr_bwd_apply over
+long rows, which also adds into dgamma / dbeta in place) are plain stores
+in both variants (the slot sums read them back next)."""
 import os
 import re
 import shutil
@@ -58,7 +59,7 @@ def test_keep_variants_store_as_intended(src, tmp_path):
         checked += 1
         if keep and "NormE2E" in name:  # add+RMSNorm: r_out streamed, y kept
             assert nt.count(True) == nt.count(False), f"{name}: {nt}"
-        elif "ln_bwd_vec" in name and not keep:  # dx streamed, slot partials plain
+        elif ("ln_bwd_vec" in name or "lr_bwd_apply" in name) and not keep:  # dx streamed, slot partials plain
             assert any(nt), f"{name}: dx lost its non-temporal hint"
         elif keep:
             assert not any(nt), f"{name}: a kept output is stored non-temporal"
