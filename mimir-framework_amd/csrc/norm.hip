@@ -213,6 +213,80 @@ int launch_vec(mimir_ctx* ctx, const NormArgs& a) {
     return launched(ctx, "norm_rows_vec");
 }
 
+// Rows the vector kernels cannot take (a width that is not a multiple of 4,
+// so rows start off 16-byte alignment, or unaligned pointers), up to
+// kBlock*VPT floats: the same register-resident scheme with 4-byte columns.
+// One kBlock-thread workgroup per row; thread t holds columns t, t+kBlock,
+// ...; one read of the row, two reductions (LayerNorm) or one (RMSNorm).
+template <Norm K, int VPT, bool KEEP>
+__global__ __launch_bounds__(kBlock) void norm_rows_scalar(NormArgs a) {
+    constexpr int NW = kBlock / kWave;
+    __shared__ float lds[2][NW];
+    const int t = threadIdx.x;
+    const int64_t base = static_cast<int64_t>(blockIdx.x) * a.cols;
+    float v[VPT];
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) {
+        const int64_t c = static_cast<int64_t>(j) * kBlock + t;
+        v[j] = c < a.cols ? __builtin_nontemporal_load(a.x + base + c) : 0.0f;
+    }
+    const float n = static_cast<float>(a.cols);
+    auto put = [&](int64_t c, float o) {
+        if constexpr (KEEP) a.y[base + c] = o;
+        else __builtin_nontemporal_store(o, a.y + base + c);
+    };
+    if constexpr (K == Norm::Layer) {
+        float s = 0.0f;
+#pragma unroll
+        for (int j = 0; j < VPT; ++j) s += v[j];
+        const float mean = row_sum<NW, false>(s, lds[0], 0) / n;
+        float q = 0.0f;
+#pragma unroll
+        for (int j = 0; j < VPT; ++j) {
+            if (static_cast<int64_t>(j) * kBlock + t < a.cols) {
+                const float d = v[j] - mean;
+                q += d * d;
+            }
+        }
+        const float var = row_sum<NW, false>(q, lds[1], 0) / n;
+        const float inv_std = 1.0f / sqrtf(var + a.eps);
+#pragma unroll
+        for (int j = 0; j < VPT; ++j) {
+            const int64_t c = static_cast<int64_t>(j) * kBlock + t;
+            if (c < a.cols) {
+                float o = (v[j] - mean) * inv_std;
+                if (a.g) {
+                    o *= a.g[c];
+                    if (a.b) o += a.b[c];
+                }
+                put(c, o);
+            }
+        }
+    } else {
+        float q = 0.0f;
+#pragma unroll
+        for (int j = 0; j < VPT; ++j) q += v[j] * v[j];
+        const float rms = sqrtf(row_sum<NW, false>(q, lds[0], 0) / n + a.eps);
+#pragma unroll
+        for (int j = 0; j < VPT; ++j) {
+            const int64_t c = static_cast<int64_t>(j) * kBlock + t;
+            if (c < a.cols) {
+                float o = v[j] / rms;
+                if (a.g && c < a.w_len) o *= a.g[c];
+                put(c, o);
+            }
+        }
+    }
+}
+
+template <Norm K, int VPT>
+int launch_scalar(mimir_ctx* ctx, const NormArgs& a) {
+    const unsigned grid = static_cast<unsigned>(a.rows);
+    if (ctx->keep_outputs) norm_rows_scalar<K, VPT, true><<<grid, kBlock, 0, ctx->stream>>>(a);
+    else norm_rows_scalar<K, VPT, false><<<grid, kBlock, 0, ctx->stream>>>(a);
+    return launched(ctx, "norm_rows_scalar");
+}
+
 template <Norm K>
 int dispatch(mimir_ctx* ctx, const NormArgs& a) {
     bool vec = (a.cols % 4) == 0 && aligned16(a.x) && aligned16(a.y) &&
@@ -234,6 +308,11 @@ int dispatch(mimir_ctx* ctx, const NormArgs& a) {
     }
     if (a.rows > 0x7fffffffLL)
         return fail(ctx, MIMIR_EINVAL, "norm: %lld rows exceed the grid limit", (long long)a.rows);
+    if constexpr (K != Norm::AddRms) {
+        if (!vec && a.cols <= 4 * kBlock) return launch_scalar<K, 4>(ctx, a);
+        if (!vec && a.cols <= 8 * kBlock) return launch_scalar<K, 8>(ctx, a);
+        if (!vec && a.cols <= 16 * kBlock) return launch_scalar<K, 16>(ctx, a);
+    }
     norm_rows_generic<K><<<static_cast<unsigned>(a.rows), kBlock, 0, ctx->stream>>>(a);
     return launched(ctx, "norm_rows_generic");
 }

@@ -124,6 +124,55 @@ __global__ __launch_bounds__(kBlock) void softmax_rows_generic(SoftmaxArgs a) {
     }
 }
 
+// Rows the vector kernel cannot take (a width that is not a multiple of 4,
+// or unaligned pointers), up to kBlock*VPT floats: the row held in registers
+// with 4-byte columns, one kBlock-thread workgroup per row -- one read of
+// the row, and the same max / sum / finish as softmax_rows_generic.
+template <int MODE, int VPT, bool KEEP>
+__global__ __launch_bounds__(kBlock) void softmax_rows_scalar(SoftmaxArgs a) {
+    constexpr int NW = kBlock / kWave;
+    __shared__ float lds[2][NW];
+    const int t = threadIdx.x;
+    const int64_t base = static_cast<int64_t>(blockIdx.x) * a.cols;
+    float v[VPT], e[VPT];
+    float m = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) {
+        const int64_t c = static_cast<int64_t>(j) * kBlock + t;
+        v[j] = c < a.cols ? __builtin_nontemporal_load(a.x + base + c) : 0.0f;
+        if (c < a.cols) m = fmaxf(m, v[j]);
+    }
+    m = block_max<NW>(m, lds[0]);
+    float s = 0.0f;
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) {
+        e[j] = 0.0f;
+        if (static_cast<int64_t>(j) * kBlock + t < a.cols) {
+            e[j] = expf(v[j] - m);
+            s += e[j];
+        }
+    }
+    float sum, aux;
+    row_constants<MODE>(block_sum<NW>(s, lds[1]), &sum, &aux);
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) {
+        const int64_t c = static_cast<int64_t>(j) * kBlock + t;
+        if (c < a.cols) {
+            const float o = finish<MODE>(v[j], e[j], m, sum, aux);
+            if constexpr (KEEP) a.y[base + c] = o;
+            else __builtin_nontemporal_store(o, a.y + base + c);
+        }
+    }
+}
+
+template <int MODE, int VPT>
+int launch_scalar(mimir_ctx* ctx, const SoftmaxArgs& a) {
+    const unsigned grid = static_cast<unsigned>(a.rows);
+    if (ctx->keep_outputs) softmax_rows_scalar<MODE, VPT, true><<<grid, kBlock, 0, ctx->stream>>>(a);
+    else softmax_rows_scalar<MODE, VPT, false><<<grid, kBlock, 0, ctx->stream>>>(a);
+    return launched(ctx, "softmax_rows_scalar");
+}
+
 template <int MODE, int TPR, int VPT, int BS>
 int launch_vec(mimir_ctx* ctx, const SoftmaxArgs& a) {
     unsigned blocks;
@@ -137,7 +186,8 @@ int launch_vec(mimir_ctx* ctx, const SoftmaxArgs& a) {
 template <int MODE>
 int dispatch(mimir_ctx* ctx, const SoftmaxArgs& a) {
     const int64_t c4 = a.cols / 4;
-    if ((a.cols % 4) == 0 && aligned16(a.x) && aligned16(a.y)) {
+    const bool vec = (a.cols % 4) == 0 && aligned16(a.x) && aligned16(a.y);
+    if (vec) {
         const RowShape s = shape_fits(ctx->tune.softmax, c4) ? ctx->tune.softmax : default_softmax_shape(c4);
 #define MIMIR_SOFTMAX_CASE(T, V, B) \
         if (s.tpr == T && s.vpt == V && s.bs == B) return launch_vec<MODE, T, V, B>(ctx, a);
@@ -147,6 +197,9 @@ int dispatch(mimir_ctx* ctx, const SoftmaxArgs& a) {
     }
     if (a.rows > 0x7fffffffLL)
         return fail(ctx, MIMIR_EINVAL, "softmax: %lld rows exceed the grid limit", (long long)a.rows);
+    if (!vec && a.cols <= 4 * kBlock) return launch_scalar<MODE, 4>(ctx, a);
+    if (!vec && a.cols <= 8 * kBlock) return launch_scalar<MODE, 8>(ctx, a);
+    if (!vec && a.cols <= 16 * kBlock) return launch_scalar<MODE, 16>(ctx, a);
     softmax_rows_generic<MODE><<<static_cast<unsigned>(a.rows), kBlock, 0, ctx->stream>>>(a);
     return launched(ctx, "softmax_rows_generic");
 }

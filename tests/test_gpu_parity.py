@@ -487,3 +487,31 @@ def test_output_caching_gives_the_same_bits(ctx):
             a.free()
     for k, v in outs["streamed"].items():
         assert_bitexact(outs["kept"][k], v, f"{k}: kept vs streamed")
+
+
+@pytest.mark.parametrize("cols", [1023, 2047, 4095])
+def test_odd_widths_register_resident(ctx, cols):
+    """Widths that are not a multiple of 4 (rows start off 16-byte alignment)
+    take the 4-byte-column kernels (norm_rows_scalar, softmax_rows_scalar):
+    LayerNorm, RMSNorm with a weight block shorter than the row, and softmax
+    with a masked column, an all -inf row (NaN, as the reference) and a NaN
+    row, against the oracle (softmax: within tolerance of it or nearer the
+    float64 value, since LogSoftmax's small outputs cancel (x - max) against
+    log(sum) and carry the reference's sequential-sum error)."""
+    rows = 9
+    x = (0.7 + 1.3 * rng.standard_normal((rows, cols))).astype(np.float32)
+    g = (1 + 0.05 * rng.standard_normal(cols)).astype(np.float32)
+    b = (0.05 * rng.standard_normal(cols)).astype(np.float32)
+    got = run(ctx, lambda dx, dg, db, y: ctx.layernorm(dx, dg, db, y, rows, cols, 1e-5), x, g, b, out_shape=x.shape)
+    assert_close(got, O.layernorm(x, cols, g, b, 1e-5).reshape(x.shape), f"LN cols={cols}")
+    wl = cols // 2
+    got = run(ctx, lambda dx, dw, y: ctx.rmsnorm(dx, dw, wl, y, rows, cols, 1e-6), x, g, out_shape=x.shape)
+    ref = np.stack([O.rmsnorm_whole(x[i], g[:wl], 1e-6) for i in range(rows)])
+    assert_close(got, ref, f"RMSNorm cols={cols}")
+    s = (3 * x).astype(np.float32)
+    s[1, 5] = -np.inf
+    s[2, :] = -np.inf
+    s[3, cols // 2] = np.nan
+    for mode in (M.SOFTMAX_DIV_EPS, M.SOFTMAX_MUL_INV, M.SOFTMAX_LOG):
+        got = run(ctx, lambda dx, y: ctx.softmax(dx, y, rows, cols, mode), s, out_shape=s.shape)
+        assert_close_or_nearer_exact(got, O.softmax_rows(s, mode), X.softmax(s, mode), f"softmax cols={cols} mode {mode}")
