@@ -1,5 +1,5 @@
-// longrow.hip -- row reductions split over many workgroups, for a few very
-// long rows.
+// longrow.hip -- row reductions split over many workgroups, for rows too
+// long for one workgroup's registers (more than 16384 floats).
 //
 // The reference's RMSNorm and Softmax layers normalise the whole input as one
 // row (LayerOpsExt.hpp:345-378, LayerOps.hpp:325-361), and so does LayerNorm

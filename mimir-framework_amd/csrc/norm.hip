@@ -5,10 +5,12 @@
 // so every load instruction of a wave covers 1 KiB of contiguous row.  Each
 // input byte crosses HBM once: the row is loaded, reduced (DPP wave
 // reductions, LDS only to combine the waves of one row) and written from
-// registers.  A few rows too wide for that register budget are split over
-// many workgroups (longrow.hip); other wide rows, and rows whose width is not
-// a multiple of 4 or whose buffers are not 16-byte aligned, take the generic
-// kernel: one workgroup per row, scalar strided passes.
+// registers.  Rows too wide for that register budget are split over many
+// workgroups (longrow.hip).  Rows whose width is not a multiple of 4 or whose
+// buffers are not 16-byte aligned are held in registers with 4-byte columns
+// up to 4096 floats (norm_rows_scalar); what remains (add + RMSNorm on such
+// rows, wider unaligned rows) takes the generic kernel: one workgroup per
+// row, scalar strided passes.
 //
 // Arithmetic follows the reference step by step:
 //   LayerNorm  LayerOps::layernorm_forward, LayerOps.hpp:264-319
@@ -301,7 +303,7 @@ int dispatch(mimir_ctx* ctx, const NormArgs& a) {
         if (s.tpr == T && s.vpt == V && s.bs == B) return launch_vec<K, T, V, B>(ctx, a);
         MIMIR_ROW_SHAPES(MIMIR_NORM_CASE)
 #undef MIMIR_NORM_CASE
-        // A few rows too wide for one workgroup's registers: split each row.
+        // Rows too wide for one workgroup's registers: split each row.
         if (longrow_applies(a.rows, a.cols))
             return longrow_norm(ctx, K == Norm::Layer ? 0 : (K == Norm::Rms ? 1 : 2), a.x, a.r, a.r_out, a.g, a.b,
                                 a.w_len, a.y, a.rows, a.cols, a.eps);

@@ -3,10 +3,11 @@
 // Same row layout as norm.hip (rows.hpp): TPR threads hold the row in VGPRs
 // as 16-byte vectors;
 // the row max and the sum of exponentials are wave-uniform DPP reductions, so
-// each element is read from HBM once and written once.  A few rows too wide
-// for the register budget are split over many workgroups (longrow.hip);
-// other wide or unaligned rows take one workgroup per row with three strided
-// passes.
+// each element is read from HBM once and written once.  Rows too wide for
+// the register budget are split over many workgroups (longrow.hip); rows of
+// a width that is not a multiple of 4, or unaligned, are held in registers
+// with 4-byte columns up to 4096 floats (softmax_rows_scalar); wider
+// unaligned rows take one workgroup per row with three strided passes.
 //
 // Arithmetic (per row): m = max_j x[j]; e[j] = expf(x[j] - m); s = sum e[j];
 //   MIMIR_SOFTMAX_DIV_EPS  y = e / (s + 1e-9f)    LayerOps::softmax_inplace,
