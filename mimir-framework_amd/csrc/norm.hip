@@ -8,9 +8,8 @@
 // registers.  Rows too wide for that register budget are split over many
 // workgroups (longrow.hip).  Rows whose width is not a multiple of 4 or whose
 // buffers are not 16-byte aligned are held in registers with 4-byte columns
-// up to 4096 floats (norm_rows_scalar); what remains (add + RMSNorm on such
-// rows, wider unaligned rows) takes the generic kernel: one workgroup per
-// row, scalar strided passes.
+// up to 4096 floats (norm_rows_scalar); wider unaligned rows take the generic
+// kernel: one workgroup per row, scalar strided passes.
 //
 // Arithmetic follows the reference step by step:
 //   LayerNorm  LayerOps::layernorm_forward, LayerOps.hpp:264-319
@@ -219,7 +218,8 @@ int launch_vec(mimir_ctx* ctx, const NormArgs& a) {
 // so rows start off 16-byte alignment, or unaligned pointers), up to
 // kBlock*VPT floats: the same register-resident scheme with 4-byte columns.
 // One kBlock-thread workgroup per row; thread t holds columns t, t+kBlock,
-// ...; one read of the row, two reductions (LayerNorm) or one (RMSNorm).
+// ...; one read of the row (and of the residual for add + RMSNorm, whose
+// sum is written once), two reductions (LayerNorm) or one (RMSNorm).
 template <Norm K, int VPT, bool KEEP>
 __global__ __launch_bounds__(kBlock) void norm_rows_scalar(NormArgs a) {
     constexpr int NW = kBlock / kWave;
@@ -231,6 +231,20 @@ __global__ __launch_bounds__(kBlock) void norm_rows_scalar(NormArgs a) {
     for (int j = 0; j < VPT; ++j) {
         const int64_t c = static_cast<int64_t>(j) * kBlock + t;
         v[j] = c < a.cols ? __builtin_nontemporal_load(a.x + base + c) : 0.0f;
+    }
+    if constexpr (K == Norm::AddRms) {  // h = x + residual (one IEEE add, as add_forward), streamed out
+        float rr[VPT];
+#pragma unroll
+        for (int j = 0; j < VPT; ++j) {
+            const int64_t c = static_cast<int64_t>(j) * kBlock + t;
+            rr[j] = c < a.cols ? __builtin_nontemporal_load(a.r + base + c) : 0.0f;
+        }
+#pragma unroll
+        for (int j = 0; j < VPT; ++j) {
+            const int64_t c = static_cast<int64_t>(j) * kBlock + t;
+            v[j] = v[j] + rr[j];
+            if (c < a.cols) __builtin_nontemporal_store(v[j], a.r_out + base + c);
+        }
     }
     const float n = static_cast<float>(a.cols);
     auto put = [&](int64_t c, float o) {
@@ -310,11 +324,9 @@ int dispatch(mimir_ctx* ctx, const NormArgs& a) {
     }
     if (a.rows > 0x7fffffffLL)
         return fail(ctx, MIMIR_EINVAL, "norm: %lld rows exceed the grid limit", (long long)a.rows);
-    if constexpr (K != Norm::AddRms) {
-        if (!vec && a.cols <= 4 * kBlock) return launch_scalar<K, 4>(ctx, a);
-        if (!vec && a.cols <= 8 * kBlock) return launch_scalar<K, 8>(ctx, a);
-        if (!vec && a.cols <= 16 * kBlock) return launch_scalar<K, 16>(ctx, a);
-    }
+    if (!vec && a.cols <= 4 * kBlock) return launch_scalar<K, 4>(ctx, a);
+    if (!vec && a.cols <= 8 * kBlock) return launch_scalar<K, 8>(ctx, a);
+    if (!vec && a.cols <= 16 * kBlock) return launch_scalar<K, 16>(ctx, a);
     norm_rows_generic<K><<<static_cast<unsigned>(a.rows), kBlock, 0, ctx->stream>>>(a);
     return launched(ctx, "norm_rows_generic");
 }

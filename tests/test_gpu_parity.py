@@ -493,21 +493,35 @@ def test_output_caching_gives_the_same_bits(ctx):
 def test_odd_widths_register_resident(ctx, cols):
     """Widths that are not a multiple of 4 (rows start off 16-byte alignment)
     take the 4-byte-column kernels (norm_rows_scalar, softmax_rows_scalar):
-    LayerNorm, RMSNorm with a weight block shorter than the row, and softmax
+    LayerNorm, RMSNorm with a weight block shorter than the row, add + RMSNorm
+    with the residual updated in place (bit-exact), and softmax
     with a masked column, an all -inf row (NaN, as the reference) and a NaN
-    row, against the oracle (softmax: within tolerance of it or nearer the
-    float64 value, since LogSoftmax's small outputs cancel (x - max) against
-    log(sum) and carry the reference's sequential-sum error)."""
+    row: within tolerance of the oracle or nearer the float64 value, since
+    the reference's sequential float sums over ~4000 terms carry ~1e-6 of
+    error into outputs near zero (LayerNorm's mean, LogSoftmax's log(sum))."""
     rows = 9
     x = (0.7 + 1.3 * rng.standard_normal((rows, cols))).astype(np.float32)
     g = (1 + 0.05 * rng.standard_normal(cols)).astype(np.float32)
     b = (0.05 * rng.standard_normal(cols)).astype(np.float32)
     got = run(ctx, lambda dx, dg, db, y: ctx.layernorm(dx, dg, db, y, rows, cols, 1e-5), x, g, b, out_shape=x.shape)
-    assert_close(got, O.layernorm(x, cols, g, b, 1e-5).reshape(x.shape), f"LN cols={cols}")
+    assert_close_or_nearer_exact(got, O.layernorm(x, cols, g, b, 1e-5).reshape(x.shape),
+                                 X.layernorm(x, cols, g, b, 1e-5), f"LN cols={cols}")
     wl = cols // 2
     got = run(ctx, lambda dx, dw, y: ctx.rmsnorm(dx, dw, wl, y, rows, cols, 1e-6), x, g, out_shape=x.shape)
     ref = np.stack([O.rmsnorm_whole(x[i], g[:wl], 1e-6) for i in range(rows)])
-    assert_close(got, ref, f"RMSNorm cols={cols}")
+    assert_close_or_nearer_exact(got, ref, X.rmsnorm(x, cols, g, wl, 1e-6), f"RMSNorm cols={cols}")
+    r = rng.standard_normal((rows, cols)).astype(np.float32)
+    y_ref, h_ref = O.add_rmsnorm(x, r, g, 1e-6)
+    dx, dr, dw, dy = ctx.to_device(x), ctx.to_device(r), ctx.to_device(g), ctx.empty((rows, cols))
+    try:
+        ctx.add_rmsnorm(dx, dr, dr, dw, dy, rows, cols, 1e-6)  # residual updated in place
+        assert_bitexact(dr.numpy(), h_ref.reshape(rows, cols), f"add+RMSNorm residual cols={cols}")
+        assert_close_or_nearer_exact(dy.numpy(), y_ref.reshape(rows, cols),
+                                     X.rmsnorm(h_ref.reshape(rows, cols), cols, g, cols, 1e-6),
+                                     f"add+RMSNorm cols={cols}")
+    finally:
+        for d in (dx, dr, dw, dy):
+            d.free()
     s = (3 * x).astype(np.float32)
     s[1, 5] = -np.inf
     s[2, :] = -np.inf
