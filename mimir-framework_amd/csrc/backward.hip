@@ -20,7 +20,11 @@
 //                            sums in registers over the rows it visits and
 //                            writes them once; sum_slots adds the slots in a
 //                            fixed order into grad_weights
-//   ln_stats_generic, ln_bwd_params_part, ln_bwd_generic  any width / alignment
+//   ln_bwd_scalar            the same with 4-byte columns: rows up to 4096
+//                            floats that are not 16-byte aligned or whose
+//                            width is not a multiple of 4
+//   ln_stats_generic, ln_bwd_params_part, ln_bwd_generic  any other width /
+//                            alignment
 //   embed_bwd_*              scatter-add of dy rows into the gradient table:
 //                            (id, token) pairs are sorted by id (stable radix
 //                            sort), then one workgroup per distinct id adds
@@ -797,6 +801,126 @@ __global__ __launch_bounds__(BS) void ln_bwd_vec(LnBwdArgs a) {
     }
 }
 
+// Rows of up to 4096 floats whose 16-byte vectors do not line up (a width
+// that is not a multiple of 4, or an unaligned pointer): ln_bwd_vec's scheme
+// with 4-byte columns c = j*TPR + t, TPR threads per row and kBlock/TPR rows
+// per workgroup (one wave per row up to 1024 floats: no barrier in the row
+// sums, and four rows' loads in flight per workgroup).  Each row is read
+// once; a thread reads dy[c] before it writes dx[c], so dx may alias dy.
+template <int TPR, int VPT, bool KEEP>
+__global__ __launch_bounds__(kBlock) void ln_bwd_scalar(LnBwdArgs a) {
+    constexpr int RPB = kBlock / TPR;
+    constexpr int NW = TPR / kWave;
+    __shared__ float lds[4][kBlock / kWave];
+    const int t = threadIdx.x % TPR;
+    const int sub = threadIdx.x / TPR;
+    const float n = static_cast<float>(a.cols);
+    const float invF = 1.0f / n;  // Model.cpp:7799
+    float gm[VPT], dg[VPT], db[VPT];
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) {
+        const int64_t c = static_cast<int64_t>(j) * TPR + t;
+        gm[j] = (a.g && c < a.cols) ? a.g[c] : 1.0f;
+        dg[j] = 0.0f;
+        db[j] = 0.0f;
+    }
+    const int64_t step = static_cast<int64_t>(gridDim.x) * RPB;
+    // Row group `b`'s x and dy for this thread (zeros past the end).
+    auto load_rows = [&](int64_t b, float* xo, float* go) {
+        const int64_t r = b + sub;
+        const int64_t l = r < a.rows ? a.cols : 0;
+#pragma unroll
+        for (int j = 0; j < VPT; ++j) {
+            const int64_t c = static_cast<int64_t>(j) * TPR + t;
+            const bool ok = c < l;
+            xo[j] = ok ? __builtin_nontemporal_load(a.x + r * a.cols + c) : 0.0f;
+            go[j] = ok ? __builtin_nontemporal_load(a.dy + r * a.cols + c) : 0.0f;
+        }
+    };
+    float xv[VPT], gv[VPT];
+    load_rows(static_cast<int64_t>(blockIdx.x) * RPB, xv, gv);
+    for (int64_t base = static_cast<int64_t>(blockIdx.x) * RPB; base < a.rows; base += step) {
+        const int64_t row = base + sub;
+        const int64_t lim = row < a.rows ? a.cols : 0;  // past-end rows join the barriers only
+        const int64_t off = row * a.cols;
+        float xn[VPT], gn[VPT];
+        load_rows(base + step, xn, gn);  // the next group's loads in flight during the reductions
+        float s = 0.0f, s1 = 0.0f;
+#pragma unroll
+        for (int j = 0; j < VPT; ++j) {
+            s += xv[j];
+            s1 += gv[j] * gm[j];
+        }
+        row_sum2<NW>(s, s1, lds[0], lds[1], sub);
+        const float mean = s / n;  // :7765-7768
+        float q = 0.0f, p2 = 0.0f;
+#pragma unroll
+        for (int j = 0; j < VPT; ++j) {
+            if (static_cast<int64_t>(j) * TPR + t < lim) {
+                const float d = xv[j] - mean;
+                q += d * d;
+                p2 += gv[j] * gm[j] * d;
+            }
+        }
+        row_sum2<NW>(q, p2, lds[2], lds[3], sub);
+        const float var = q / n;                          // :7770-7776
+        const float inv_std = 1.0f / sqrtf(var + a.eps);  // :7777
+        const float s2 = p2 * inv_std;
+        const float k = inv_std * invF;
+#pragma unroll
+        for (int j = 0; j < VPT; ++j) {  // :7783-7805
+            const int64_t c = static_cast<int64_t>(j) * TPR + t;
+            if (c < lim) {
+                const float xh = (xv[j] - mean) * inv_std;
+                const float dxh = gv[j] * gm[j];
+                dg[j] += gv[j] * xh;
+                db[j] += gv[j];
+                float o = k * ((n * dxh - s1) - xh * s2);
+                if (a.acc) o = a.dx[off + c] + o;
+                if constexpr (KEEP) a.dx[off + c] = o;
+                else __builtin_nontemporal_store(o, a.dx + off + c);
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < VPT; ++j) {
+            xv[j] = xn[j];
+            gv[j] = gn[j];
+        }
+    }
+    if (!a.part) return;
+    // One slot per workgroup: the sub-rows' sums are added in sub-row order
+    // through LDS, then written once.
+    float* p = a.part + static_cast<int64_t>(blockIdx.x) * 2 * a.cols;
+    if constexpr (RPB > 1) {
+        __shared__ float comb[2 * TPR * VPT];
+        for (int r = 0; r < RPB; ++r) {
+            if (sub == r) {
+#pragma unroll
+                for (int j = 0; j < VPT; ++j) {
+                    const int i = j * TPR + t;
+                    comb[i] = r == 0 ? dg[j] : comb[i] + dg[j];
+                    comb[TPR * VPT + i] = r == 0 ? db[j] : comb[TPR * VPT + i] + db[j];
+                }
+            }
+            __syncthreads();
+        }
+        if (sub != 0) return;
+#pragma unroll
+        for (int j = 0; j < VPT; ++j) {
+            dg[j] = comb[j * TPR + t];
+            db[j] = comb[TPR * VPT + j * TPR + t];
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < VPT; ++j) {
+        const int64_t c = static_cast<int64_t>(j) * TPR + t;
+        if (c < a.cols) {
+            p[c] = dg[j];
+            p[a.cols + c] = db[j];
+        }
+    }
+}
+
 // Any width / alignment: one workgroup per row, strided passes (the re-reads
 // of a row hit L2).  Three kernels, so that dx may overwrite dy: the row
 // statistics (mean, inv_std) first, then the parameter gradients (which read
@@ -870,10 +994,13 @@ __global__ __launch_bounds__(kBlock) void ln_bwd_params_part(LnBwdArgs a, int64_
     p[a.cols + c] = sb;
 }
 
-template <int TPR, int VPT, int BS>
-int launch_ln_bwd_vec(mimir_ctx* ctx, LnBwdArgs a, float* dgamma, float* dbeta) {
-    constexpr int RPB = BS / TPR;
-    const int64_t groups = (a.rows + RPB - 1) / RPB;
+// The persistent grid of the register-resident kernels: `groups` row groups
+// on at most 512 workgroups (or the tuned count), one dgamma | dbeta slot per
+// workgroup, then the slots' deterministic sum.  `run(grid, a)` launches the
+// kernel with a.part set.
+template <class Run>
+int ln_bwd_persistent(mimir_ctx* ctx, LnBwdArgs a, int64_t groups, float* dgamma, float* dbeta, const char* name,
+                      Run run) {
     int64_t grid = ctx->tune.lnbwd_grid > 0 ? ctx->tune.lnbwd_grid : 512;
     if (grid > groups) grid = groups;
     const int64_t nslots = grid;
@@ -885,13 +1012,33 @@ int launch_ln_bwd_vec(mimir_ctx* ctx, LnBwdArgs a, float* dgamma, float* dbeta) 
         a.part = static_cast<float*>(s);
         tmp = a.part + nslots * 2 * a.cols;
     }
-    if (ctx->keep_outputs) ln_bwd_vec<TPR, VPT, BS, true><<<static_cast<unsigned>(grid), BS, 0, ctx->stream>>>(a);
-    else ln_bwd_vec<TPR, VPT, BS, false><<<static_cast<unsigned>(grid), BS, 0, ctx->stream>>>(a);
-    if (int st = launched(ctx, "ln_bwd_vec")) return st;
+    run(static_cast<unsigned>(grid), a);
+    if (int st = launched(ctx, name)) return st;
     if (!dgamma) return MIMIR_OK;
     // dbeta null: sum only the dgamma half.
     return launch_sum_slots(ctx, a.part, nslots, 2 * a.cols, dbeta ? 2 * a.cols : a.cols, dgamma, dbeta, a.cols,
                             true, tmp);
+}
+
+template <int TPR, int VPT, int BS>
+int launch_ln_bwd_vec(mimir_ctx* ctx, LnBwdArgs a, float* dgamma, float* dbeta) {
+    constexpr int RPB = BS / TPR;
+    return ln_bwd_persistent(ctx, a, (a.rows + RPB - 1) / RPB, dgamma, dbeta, "ln_bwd_vec",
+                             [ctx](unsigned grid, const LnBwdArgs& la) {
+                                 if (ctx->keep_outputs) ln_bwd_vec<TPR, VPT, BS, true><<<grid, BS, 0, ctx->stream>>>(la);
+                                 else ln_bwd_vec<TPR, VPT, BS, false><<<grid, BS, 0, ctx->stream>>>(la);
+                             });
+}
+
+template <int TPR, int VPT>
+int launch_ln_bwd_scalar(mimir_ctx* ctx, LnBwdArgs a, float* dgamma, float* dbeta) {
+    constexpr int RPB = kBlock / TPR;
+    return ln_bwd_persistent(ctx, a, (a.rows + RPB - 1) / RPB, dgamma, dbeta, "ln_bwd_scalar",
+                             [ctx](unsigned grid, const LnBwdArgs& la) {
+                                 if (ctx->keep_outputs)
+                                     ln_bwd_scalar<TPR, VPT, true><<<grid, kBlock, 0, ctx->stream>>>(la);
+                                 else ln_bwd_scalar<TPR, VPT, false><<<grid, kBlock, 0, ctx->stream>>>(la);
+                             });
 }
 
 int ln_bwd_generic_run(mimir_ctx* ctx, LnBwdArgs a, float* dgamma, float* dbeta) {
@@ -1239,6 +1386,10 @@ int mimir_layernorm_bwd(mimir_ctx* ctx, const float* x, const float* dy, const f
         MIMIR_ROW_SHAPES(MIMIR_LNBWD_CASE)
 #undef MIMIR_LNBWD_CASE
     }
+    if (!vec && n <= 256) return launch_ln_bwd_scalar<64, 4>(ctx, a, dgamma, dbeta);
+    if (!vec && n <= 1024) return launch_ln_bwd_scalar<64, 16>(ctx, a, dgamma, dbeta);
+    if (!vec && n <= 2048) return launch_ln_bwd_scalar<128, 16>(ctx, a, dgamma, dbeta);
+    if (!vec && n <= 4096) return launch_ln_bwd_scalar<256, 16>(ctx, a, dgamma, dbeta);
     return ln_bwd_generic_run(ctx, a, dgamma, dbeta);
 }
 

@@ -33,7 +33,8 @@ def dev(ctx, a, offset=0):
 # LayerNorm
 # ---------------------------------------------------------------------------
 
-@pytest.mark.parametrize("cols", [1, 3, 4, 64, 100, 256, 512, 1000, 1024, 2048, 4096, 4100, 8192, 20000])
+@pytest.mark.parametrize("cols", [1, 3, 4, 64, 100, 256, 512, 1000, 1023, 1024, 2047, 2048, 4095, 4096, 4099, 4100,
+                                  8192, 20000])
 @pytest.mark.parametrize("affine", ["gb", "g", "none"])
 def test_layernorm_bwd(ctx, cols, affine):
     rows = 37 if cols <= 4096 else 5
@@ -74,9 +75,11 @@ def test_layernorm_bwd(ctx, cols, affine):
                 b.free()
 
 
-@pytest.mark.parametrize("rows,cols", [(8192, 4096), (3000, 512), (1025, 64), (70000, 16)])
+@pytest.mark.parametrize("rows,cols", [(8192, 4096), (3000, 512), (1025, 64), (70000, 16), (8192, 4095), (3000, 1023),
+                                       (70000, 17)])
 def test_layernorm_bwd_many_rows(ctx, rows, cols):
-    # Many rows per persistent-grid slot: dgamma / dbeta sums over thousands of tokens.
+    # Many rows per persistent-grid slot: dgamma / dbeta sums over thousands of
+    # tokens (odd widths: the 4-byte-column kernel).
     x = rng.standard_normal((rows, cols), dtype=np.float32)
     dy = rng.standard_normal((rows, cols), dtype=np.float32)
     g = (1 + 0.02 * rng.standard_normal(cols)).astype(np.float32)
@@ -109,11 +112,11 @@ def test_layernorm_bwd_unaligned_and_inplace(ctx):
     (bx, vx), (bd, vd), (bg, vg) = dev(ctx, x, 1), dev(ctx, dy, 1), dev(ctx, g, 1)
     dgb, dbb = ctx.to_device(np.zeros(cols, np.float32)), ctx.to_device(np.zeros(cols, np.float32))
     try:
-        ctx.layernorm_bwd(vx, vd, vg, vd, dgb, dbb, rows, cols, 1e-5)  # unaligned (generic), dx over dy
+        ctx.layernorm_bwd(vx, vd, vg, vd, dgb, dbb, rows, cols, 1e-5)  # unaligned (4-byte columns), dx over dy
         _, _, _, (sg, sb), dxs = X.layernorm_bwd(x, dy, cols, g, 1e-5)
         assert_close_sum(vd.numpy().ravel(), dx_ref, dxs, "dx unaligned in place")
-        assert_close_sum(dgb.numpy(), gp_ref[:cols], sg, "dgamma generic")
-        assert_close_sum(dbb.numpy(), gp_ref[cols:], sb, "dbeta generic")
+        assert_close_sum(dgb.numpy(), gp_ref[:cols], sg, "dgamma unaligned")
+        assert_close_sum(dbb.numpy(), gp_ref[cols:], sb, "dbeta unaligned")
         # Aligned (register-resident rows), dx over dy as well.
         (ax, avx), (ad, avd), (ag, avg) = dev(ctx, x), dev(ctx, dy), dev(ctx, g)
         ctx.upload(dgb, np.zeros(cols, np.float32))
