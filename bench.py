@@ -11,10 +11,12 @@ idle state the host uploads left them in.  Time is taken with HIP events
 recorded on the context's stream around exactly K steps, between two stream
 synchronisations.
 
-Prints ONE JSON line on stdout (progress goes to stderr).  Besides the
-headline workload, `ops` lists every op of configs[0..4] measured the same
-way, and `cpu_baseline` times the reference's own CPU code (compiled from the
-reference sources into oracle/_ref) on the host, single-threaded as the
+Prints ONE compact JSON line on stdout (under 4 KB; progress goes to
+stderr).  Besides the headline workload, `ops` summarises every op of
+configs[0..4] measured the same way as [us per launch, GB/s, fraction of
+peak, parity pass, HBM traffic over algorithmic bytes]; the full per-op
+records go to `--full-out`.  `cpu_baseline` times the reference's own
+CPU code (compiled from the reference sources into oracle/_ref) on the host, single-threaded as the
 reference ops are.  The same leg checks each op: one more launch on freshly
 uploaded inputs, compared with the CPU path's output on those inputs
 (`parity`: max |d|, max relative error, bit-exactness, pass under the
@@ -42,6 +44,7 @@ PEAK_GBS = 8000.0  # MI355X HBM3E
 MALL_BYTES = 256 << 20
 MIN_FOOTPRINT = 5 * MALL_BYTES  # rotate buffer sets until one pass covers 1.25 GiB
 MAX_SETS = 32
+STDOUT_LIMIT = 4000  # the JSON line on stdout stays well inside the driver's tail
 
 
 def log(*a):
@@ -787,11 +790,18 @@ def parity_leg(ctx, by_key, which):
             check(key, {"da": a, "db": a}, "port (accumulate_grad into absent names copies dy)",
                   "full [8192x4096]", exact=("da", "db"))
         elif key.endswith("_whole"):
+            # At 2^25 terms the reference's sequential float32 sums are
+            # themselves off by up to a few percent, so the device is held to
+            # the float64 value of the reference's formula and the
+            # reference's own distance from it is reported beside.
             kind, x, _, _, ref, port, exact = _whole_inputs(key)
-            y = ref() if have_ref else port()
             shape = (8192, 4096)
-            check(key, {"y": y.reshape(shape)}, ref_or_port, "the full 2^25-element row",
-                  nearer={"y": exact().reshape(shape)})
+            e = exact().reshape(shape)
+            check(key, {"y": e}, "float64 value of the reference formula", "the full 2^25-element row")
+            y = (ref() if have_ref else port()).reshape(shape)
+            err = _agreement(y, e, False)
+            out[key]["reference_error_vs_float64"] = {
+                "of": ref_or_port, "max_abs": err["max_abs"], "max_rel": err["max_rel"]}
         elif key in ("cfg3_embedding_bwd", "cfg3_embedding_bwd_zipf"):
             ids = G.cfg3_ids() if key == "cfg3_embedding_bwd" else G.cfg3_ids_zipf()
             gt = O.embedding_bwd(ids, G.cfg3_embedding_grad(), np.zeros(32000 * 4096, np.float32), 32000, 4096, -1)
@@ -904,6 +914,8 @@ def main():
     ap.add_argument("--ops", default="all", help="'all', 'none', or a comma list of op keys")
     ap.add_argument("--cpu", default="all", help="'all', 'workload' or 'none'")
     ap.add_argument("--cpu-reps", type=int, default=3)
+    ap.add_argument("--full-out", default=os.path.join("gpurun_out", "bench_full.json"),
+                    help="file for the full per-op records ('' for none); stdout carries a summary")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -977,6 +989,15 @@ def main():
         if r["op"] in parity:
             r["parity"] = parity[r["op"]]
 
+    for r in sweep:
+        t = load_traffic(r["op"])
+        if t is not None:
+            r["traffic_bytes"] = t["traffic_bytes"]
+            r["traffic_over_algorithmic"] = t["traffic_over_algorithmic"]
+            for k in ("distinct_row_bytes", "distinct_row_GB_s_at_profiled_time"):
+                if k in t:
+                    r[k] = t[k]
+
     traffic = load_traffic(head.key)
     host = {"cpu_model": cpu_model(), "nproc": os.cpu_count()}
     cb = cpu.get(head.key)
@@ -1021,10 +1042,36 @@ def main():
         "cpu_baseline": None if cb is None else {
             "value": cb["value"], "unit": cb["unit"], "cores": cb["cores"], "kind": cb["kind"],
             "sample": cb["sample"], "rows_per_s": cb["rows_per_s"], **host},
-        "parity": parity.get(head.key),
-        "ops": sweep,
+        "parity": compact_parity(parity.get(head.key)),
+        "ops_fields": ["us_per_launch", "GB_s", "frac_of_peak", "parity_pass", "traffic_over_algorithmic"],
+        "ops": {r["op"]: [r["us_per_launch"], r["GB_s"], r.get("frac_of_peak"),
+                          r["parity"]["pass"] if "parity" in r else None,
+                          r.get("traffic_over_algorithmic")] for r in sweep},
     }
-    print(json.dumps(line), flush=True)
+    full = dict(line, parity=parity.get(head.key), ops=sweep)
+    out = args.full_out
+    if out:
+        os.makedirs(os.path.dirname(os.path.abspath(out)), exist_ok=True)
+        with open(out, "w") as f:
+            json.dump(full, f, indent=1)
+        line["full_records"] = os.path.relpath(os.path.abspath(out), REPO)
+        log(f"full per-op records written to {out}")
+    text = json.dumps(line, separators=(",", ":"))
+    if len(text) > STDOUT_LIMIT:
+        # The driver keeps the tail of stdout; a line it cannot parse whole
+        # loses the measurement.  The per-op summary goes first.
+        line.pop("ops")
+        text = json.dumps(line, separators=(",", ":"))
+    print(text, flush=True)
+
+
+def compact_parity(p):
+    """The headline's parity record without the per-output rule strings."""
+    if p is None:
+        return None
+    return {"vs": p["vs"], "sample": p["sample"], "pass": p["pass"],
+            "outputs": {n: {k: o[k] for k in ("max_abs", "max_rel", "bitexact", "pass")}
+                        for n, o in p["outputs"].items()}}
 
 
 if __name__ == "__main__":

@@ -165,6 +165,27 @@ int mimir_add_fwd(mimir_ctx* ctx, const float* a, int64_t na, const float* b, in
 int mimir_mul_fwd(mimir_ctx* ctx, const float* a, int64_t na, const float* b, int64_t nb,
                   float* y);
 
+/* Branch merge operations: the reference's MergeOperation (Layers.hpp:72-80). */
+#define MIMIR_MERGE_ADD 0
+#define MIMIR_MERGE_MULTIPLY 1
+#define MIMIR_MERGE_CONCATENATE 2
+#define MIMIR_MERGE_MAX 3
+#define MIMIR_MERGE_AVERAGE 4
+#define MIMIR_MERGE_GATED 5
+#define MIMIR_MERGE_ATTENTION_WEIGHTED 6
+/* Model::computeBranchMerge(branch1 = a, branch2 = b, output = y, merge_op),
+ * Model.cpp:4344-4479, the training-mode residual merge.  y holds na floats
+ * (na + nb for CONCATENATE: a then b).  ADD, and GATED / ATTENTION_WEIGHTED
+ * (the reference's default branch, copy then +=): a[i] + b[i]; MULTIPLY:
+ * a[i] * b[i]; AVERAGE: (a[i] + b[i]) * 0.5f; MAX: for i below na rounded
+ * down to a multiple of 8, the AVX2 body's vmaxps (a[i] > b[i] ? a[i] :
+ * b[i]), past it the scalar tail's std::max (a[i] < b[i] ? b[i] : a[i]) --
+ * the two differ only for NaN and signed zeros.  Bit-identical to the
+ * reference.  The reference reads b past its end when nb < na; that is
+ * EINVAL here. */
+int mimir_branch_merge_fwd(mimir_ctx* ctx, const float* a, int64_t na, const float* b, int64_t nb,
+                           float* y, int merge_op);
+
 /* ---------------------------------------------------------------------------
  * Embedding gather and rotary position embedding
  * ------------------------------------------------------------------------- */
@@ -315,7 +336,18 @@ typedef struct mimir_layer {
     float* grad_weights;        /* DEVICE, weights_len floats, or NULL: the layer's
                                    Layer::grad_weights for mimir_store_backward
                                    (added to, as the reference adds into it) */
+    /* Branch fields (Layers.hpp:214-219), read by mimir_store_run_training
+     * only, as forwardPassView reads them only with training=true
+     * (Model.cpp:4729-4732, 6676-6685).  Zero-initialised = no branch. */
+    int32_t branch_type;              /* Layer::branch_type (BranchType, Layers.hpp:59-69) */
+    int32_t merge_op;                 /* Layer::merge_op, a MIMIR_MERGE_* value */
+    const int32_t* branch_sources;    /* host array, Layer::branch_sources */
+    int32_t n_branch_sources;
 } mimir_layer;
+
+/* BranchType values (Layers.hpp:59-69) that the runtime acts on. */
+#define MIMIR_BRANCH_NONE 0
+#define MIMIR_BRANCH_RESIDUAL 1
 
 int mimir_store_create(mimir_ctx* ctx, mimir_store** out);
 int mimir_store_destroy(mimir_store* store);
@@ -348,7 +380,15 @@ int mimir_store_run(mimir_store* store, const mimir_layer* layers, int32_t n_lay
  * mimir_store_backward.  The store never writes a tensor in place, so the
  * snapshots are references to its buffers, not copies.  Dropout is refused
  * (its training form draws a random mask).  The snapshots live until the
- * next run, set_inputs or clear. */
+ * next run, set_inputs or clear.
+ * Residual merges (Model.cpp:6676-6685 -> executeBranchComputation :4550-4582):
+ * after a layer with branch_type RESIDUAL and a branch source s (its first
+ * entry) with 0 <= s <= the layer's index, the layer's output is replaced by
+ * mimir_branch_merge_fwd(output, the output layer s produced in this run,
+ * merge_op) under the same name; that merged tensor is also what a later
+ * merge reads as this layer's output.  Other sources merge nothing, as in
+ * the reference.  The backward ignores merges, as Model::backwardPass does
+ * (backpropThroughBranch, Model.cpp:4584-4613, is never called). */
 int mimir_store_run_training(mimir_store* store, const mimir_layer* layers, int32_t n_layers);
 
 /* Model::backwardPass(loss_gradient), Model.cpp:7307-9153, over the layers of

@@ -60,6 +60,20 @@ struct Add {
 struct Mul {
     __device__ float operator()(float a, float b) const { return a * b; }
 };
+// computeBranchMerge AVERAGE, Model.cpp:4434-4460: (a + b) * 0.5f, two roundings.
+struct Average {
+    __device__ float operator()(float a, float b) const { return (a + b) * 0.5f; }
+};
+// computeBranchMerge MAX, Model.cpp:4408-4432.  The AVX2 body's vmaxps
+// returns its second operand unless the first is greater (so b for a NaN on
+// either side and for equal zeros); the scalar tail's std::max(a, b) returns
+// a unless a < b.
+struct MaxBody {
+    __device__ float operator()(float a, float b) const { return a > b ? a : b; }
+};
+struct MaxTail {
+    __device__ float operator()(float a, float b) const { return a < b ? b : a; }
+};
 
 template <class F>
 __device__ __forceinline__ f4 map4(F f, f4 a) {
@@ -310,6 +324,42 @@ int mimir_add_fwd(mimir_ctx* ctx, const float* a, int64_t na, const float* b, in
     }
     add_repeat_scalar<<<stride_grid(big_n), kBlock, 0, ctx->stream>>>(big, small, y, big_n, small_n);
     return launched(ctx, "add_repeat_scalar");
+}
+
+int mimir_branch_merge_fwd(mimir_ctx* ctx, const float* a, int64_t na, const float* b, int64_t nb,
+                           float* y, int merge_op) {
+    if (!ctx) return MIMIR_EINVAL;
+    MIMIR_REQUIRE(ctx, na >= 0 && nb >= 0, "branch merge: negative size");
+    MIMIR_REQUIRE(ctx, merge_op >= MIMIR_MERGE_ADD && merge_op <= MIMIR_MERGE_ATTENTION_WEIGHTED,
+                  "branch merge: unknown merge operation %d", merge_op);
+    if (merge_op == MIMIR_MERGE_CONCATENATE) {  // Model.cpp:4462-4468: a then b
+        MIMIR_REQUIRE(ctx, (na == 0 || (a && y)) && (nb == 0 || (b && y)), "branch merge: null tensor");
+        if (na > 0)
+            if (int st = mimir_copy(ctx, y, a, static_cast<size_t>(na) * 4)) return st;
+        return nb > 0 ? mimir_copy(ctx, y + na, b, static_cast<size_t>(nb) * 4) : MIMIR_OK;
+    }
+    // Every other operation reads branch2[i] for i < branch1.size().
+    MIMIR_REQUIRE(ctx, nb >= na,
+                  "branch merge: the source branch has %lld floats, fewer than the %lld it is merged with",
+                  (long long)nb, (long long)na);
+    if (na == 0) return MIMIR_OK;
+    MIMIR_REQUIRE(ctx, a && b && y, "branch merge: null tensor");
+    MIMIR_ENTER(ctx);
+    switch (merge_op) {
+        case MIMIR_MERGE_MULTIPLY:
+            return run_binary(ctx, a, b, y, na, Mul{}, "merge_mul");
+        case MIMIR_MERGE_AVERAGE:
+            return run_binary(ctx, a, b, y, na, Average{}, "merge_average");
+        case MIMIR_MERGE_MAX: {
+            const int64_t body = na / 8 * 8;  // the 8-wide AVX2 loop, then the tail
+            if (body > 0)
+                if (int st = run_binary(ctx, a, b, y, body, MaxBody{}, "merge_max")) return st;
+            return na > body ? run_binary(ctx, a + body, b + body, y + body, na - body, MaxTail{}, "merge_max")
+                             : MIMIR_OK;
+        }
+        default:  // ADD (:4355-4380); GATED, ATTENTION_WEIGHTED: copy then += (:4470-4477)
+            return run_binary(ctx, a, b, y, na, Add{}, "merge_add");
+    }
 }
 
 int mimir_mul_fwd(mimir_ctx* ctx, const float* a, int64_t na, const float* b, int64_t nb,

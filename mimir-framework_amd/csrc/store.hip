@@ -66,6 +66,10 @@ struct mimir_store {
     std::unordered_map<std::string, Slot> f32;
     std::unordered_map<std::string, Slot> i32;
     std::vector<Snap> snaps;                      // last mimir_store_run_training
+    // The outputs of that run's layers that a residual merge reads
+    // (forwardPassView's all_layer_outputs, Model.cpp:4734-4737, 6676-6678):
+    // held by reference, as the snapshots are; empty slots elsewhere.
+    std::vector<Slot> outs;
     std::unordered_map<std::string, Slot> grads;  // last mimir_store_backward
     std::vector<std::unique_ptr<Buf>> bufs;
     std::multimap<size_t, Buf*> free_bufs;  // capacity -> idle buffer
@@ -118,6 +122,8 @@ struct mimir_store {
         for (auto& sn : snaps)
             for (auto& v : sn.vals) release(v.buf);
         snaps.clear();
+        for (auto& o : outs) release(o.buf);
+        outs.clear();
     }
 
     void release_grads() {
@@ -576,15 +582,72 @@ int mimir_store_run(mimir_store* s, const mimir_layer* layers, int32_t n_layers)
     return MIMIR_OK;
 }
 
+namespace {
+
+// The source layer of layer i's residual merge, or -1 when the layer merges
+// nothing: executeBranchComputation (Model.cpp:4550-4582) merges only for
+// BranchType::RESIDUAL with a first branch source inside all_layer_outputs,
+// which at layer i holds the outputs of layers 0..i.
+int merge_source(const mimir_layer& L, int32_t i) {
+    if (L.branch_type != MIMIR_BRANCH_RESIDUAL || L.n_branch_sources <= 0 || !L.branch_sources) return -1;
+    const int32_t src = L.branch_sources[0];
+    return src >= 0 && src <= i ? src : -1;
+}
+
+// After layer i of a training run: keep its output when a merge reads it,
+// and merge it with its source's output when it is a residual layer
+// (Model.cpp:6676-6685).  The merged tensor replaces the output under the
+// same name, and is what a later merge reads as layer i's output.
+int after_training_layer(mimir_store* s, const mimir_layer* layers, int32_t i, const std::vector<bool>& kept) {
+    const mimir_layer& L = layers[i];
+    const std::string out_name = (L.output && *L.output) ? L.output : "x";
+    const Slot o = s->f32.at(out_name);
+    const int src = merge_source(L, i);
+    if (src >= 0) {
+        const Slot b = src == i ? o : s->outs[src];
+        const int64_t n = L.merge_op == MIMIR_MERGE_CONCATENATE ? o.n + b.n : o.n;
+        Buf* mb = nullptr;
+        if (int st = s->acquire(static_cast<size_t>(n) * 4, &mb)) return st;
+        const int st = mimir_branch_merge_fwd(s->ctx, static_cast<const float*>(o.buf->p), o.n,
+                                              static_cast<const float*>(b.buf->p), b.n,
+                                              static_cast<float*>(mb->p), L.merge_op);
+        if (st != MIMIR_OK) {
+            s->discard(mb);
+            return fail(s->ctx, st, "%s (layer %s, merged with layer %d)", mimir_last_error(s->ctx), layer_name(L),
+                        src);
+        }
+        s->bind(MIMIR_DTYPE_F32, out_name, mb, n);
+    }
+    if (kept[i]) {
+        const Slot m = s->f32.at(out_name);
+        ++m.buf->refs;
+        s->outs[i] = m;
+    }
+    return MIMIR_OK;
+}
+
+}  // namespace
+
 int mimir_store_run_training(mimir_store* s, const mimir_layer* layers, int32_t n_layers) {
     if (!s) return MIMIR_EINVAL;
     MIMIR_REQUIRE(s->ctx, n_layers >= 0 && (n_layers == 0 || layers), "mimir_store_run_training: invalid argument");
     s->release_snaps();
     s->snaps.resize(static_cast<size_t>(n_layers));
+    // Layers whose outputs a later (or their own) residual merge reads.
+    std::vector<bool> kept(static_cast<size_t>(n_layers), false);
+    bool merges = false;
+    for (int32_t i = 0; i < n_layers; ++i) {
+        const int src = merge_source(layers[i], i);
+        if (src >= 0 && src < i) kept[src] = true;
+        merges = merges || src >= 0;
+    }
+    if (merges) s->outs.resize(static_cast<size_t>(n_layers));
     ChainOutputs chain(s->ctx);
     for (int32_t i = 0; i < n_layers; ++i) {
         chain.layer(i, n_layers);
-        if (int st = run_layer(s, layers[i], &s->snaps[i])) {
+        int st = run_layer(s, layers[i], &s->snaps[i]);
+        if (st == MIMIR_OK && merges) st = after_training_layer(s, layers, i, kept);
+        if (st != MIMIR_OK) {
             s->release_snaps();
             return st;
         }

@@ -383,9 +383,12 @@ std::vector<float> embedding_forward_float_ids(const std::vector<float>& x, cons
 // ---------------------------------------------------------------------------
 // Device-resident runtime: Model::forwardPassNamed (Model.cpp:1352-1408,
 // forwardPassView Model.cpp:4621-6824) over a reference layer list, with every
-// activation held in HBM by a mimir_store and only "x" downloaded.  Inference
-// only.  Layer types: LayerNorm, RMSNorm, Softmax, LogSoftmax, GELU, SiLU,
-// Add, Multiply, Embedding, Identity, Dropout (others throw at construction).
+// activation held in HBM by a mimir_store and only "x" downloaded, and the
+// training step's Model::backwardPass over the same store.  A training
+// forward applies the layers' residual merges (Layer::branch_type RESIDUAL
+// with branch_sources, Model.cpp:6676-6685) as the reference does.  Layer
+// types: LayerNorm, RMSNorm, Softmax, LogSoftmax, GELU, SiLU, Add, Multiply,
+// Embedding, Identity, Dropout (others throw at construction).
 // ---------------------------------------------------------------------------
 template <class LayerT>
 class DeviceModel {
@@ -536,6 +539,12 @@ private:
             c.padding_idx = L.padding_idx;
             c.seq_len = L.seq_len;
             c.grad_weights = nullptr;
+            // Branch fields, read by training forwards (Layers.hpp:214-219).
+            c.branch_type = static_cast<int32_t>(L.branch_type);
+            c.merge_op = static_cast<int32_t>(L.merge_op);
+            static_assert(sizeof(L.branch_sources[0]) == sizeof(int32_t), "Layer::branch_sources is int");
+            c.branch_sources = reinterpret_cast<const int32_t*>(L.branch_sources.data());
+            c.n_branch_sources = static_cast<int32_t>(L.branch_sources.size());
         }
     }
 

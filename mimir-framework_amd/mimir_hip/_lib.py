@@ -25,6 +25,37 @@ DTYPE_F32, DTYPE_I32 = 0, 1
 ST_DTYPES = {0: "F32", 1: "F16", 2: "I32", 3: "I16", 4: "U16", 5: "U8"}  # MIMIR_ST_*
 LAYER_TYPES = {"LayerNorm": 1, "RMSNorm": 2, "Softmax": 3, "LogSoftmax": 4, "GELU": 5, "SiLU": 6,
                "Add": 7, "Multiply": 8, "Embedding": 9, "Identity": 10, "Dropout": 11}
+# The reference's BranchType and MergeOperation (Layers.hpp:59-80), in order.
+BRANCH_TYPES = ("NONE", "RESIDUAL", "SKIP_CONNECTION", "DENSE_CONNECTION", "ATTENTION_BRANCH", "MULTI_SCALE",
+                "GATE", "SPLIT", "MERGE")
+MERGE_OPS = ("ADD", "MULTIPLY", "CONCATENATE", "MAX", "AVERAGE", "GATED", "ATTENTION_WEIGHTED")
+
+
+def detect_branch_type(name):
+    """(branch_type, merge_op) as Layer::detectBranchType (Layers.hpp:260-304)
+    sets them from a layer's name; Model::push calls it for every layer
+    (Model.cpp:3145).  merge_op keeps its default, ADD, where the reference
+    does not set it."""
+    def has(*w):
+        return all(x in name for x in w)
+    if has("residual") or has("shortcut") or has("skip"):
+        return "RESIDUAL", "ADD"
+    if has("concat"):
+        return "SKIP_CONNECTION", "CONCATENATE"
+    if has("dense", "connect"):
+        return "DENSE_CONNECTION", "CONCATENATE"
+    if has("attention", "branch"):
+        return "ATTENTION_BRANCH", "ATTENTION_WEIGHTED"
+    if has("inception") or has("multiscale"):
+        return "MULTI_SCALE", "CONCATENATE"
+    if has("gate"):
+        return "GATE", "GATED"
+    if has("split"):
+        return "SPLIT", "ADD"
+    if has("merge") or has("fusion"):
+        op = "ADD" if has("add") else "MULTIPLY" if has("mul") else "CONCATENATE" if has("concat") else "ADD"
+        return "MERGE", op
+    return "NONE", "ADD"
 
 
 class Layer_C(Structure):
@@ -33,7 +64,9 @@ class Layer_C(Structure):
                 ("n_inputs", c_int32), ("output", c_char_p), ("weights", c_void_p),
                 ("weights_len", c_int64), ("eps", c_float), ("affine", c_int32), ("use_bias", c_int32),
                 ("in_features", c_int32), ("vocab_size", c_int32), ("embed_dim", c_int32),
-                ("padding_idx", c_int32), ("seq_len", c_int32), ("grad_weights", c_void_p)]
+                ("padding_idx", c_int32), ("seq_len", c_int32), ("grad_weights", c_void_p),
+                ("branch_type", c_int32), ("merge_op", c_int32), ("branch_sources", POINTER(c_int32)),
+                ("n_branch_sources", c_int32)]
 
 
 # name -> (restype, argtypes); mirrors include/mimir_hip.h one to one.
@@ -66,6 +99,7 @@ SIGNATURES = {
     "mimir_gelu_mul_fwd": (c_int, [_P, _P, _P, _P, c_int64]),
     "mimir_add_fwd": (c_int, [_P, _P, c_int64, _P, c_int64, _P]),
     "mimir_mul_fwd": (c_int, [_P, _P, c_int64, _P, c_int64, _P]),
+    "mimir_branch_merge_fwd": (c_int, [_P, _P, c_int64, _P, c_int64, _P, c_int]),
     "mimir_embedding_fwd": (c_int, [_P, _P, c_int64, _P, c_int64, c_int32, c_int32, c_int32, _P]),
     "mimir_embedding_f32ids_fwd": (c_int, [_P, _P, c_int64, _P, c_int64, c_int32, c_int32, c_int32,
                                            _P]),

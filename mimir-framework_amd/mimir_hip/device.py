@@ -191,6 +191,11 @@ class Context:
     def mul(self, a, na, b, nb, y):
         self.check(self.lib.mimir_mul_fwd(self.handle, _ptr(a), na, _ptr(b), nb, _ptr(y)))
 
+    def branch_merge(self, a, na, b, nb, y, merge_op):
+        """merge_op: a MergeOperation name ("ADD", "MAX", ...) or its code."""
+        op = _lib.MERGE_OPS.index(merge_op) if isinstance(merge_op, str) else int(merge_op)
+        self.check(self.lib.mimir_branch_merge_fwd(self.handle, _ptr(a), na, _ptr(b), nb, _ptr(y), op))
+
     def embedding(self, ids, n_ids, table, table_len, vocab, dim, padding_idx, y, float_ids=False):
         fn = self.lib.mimir_embedding_f32ids_fwd if float_ids else self.lib.mimir_embedding_fwd
         self.check(fn(self.handle, _ptr(ids), n_ids, _ptr(table), table_len, vocab, dim,
@@ -355,11 +360,23 @@ class Store:
         self.backward(graph, loss_grad)
         return graph.grads(), self.grad("__input__")
 
-    def forward_named(self, graph: "DeviceGraph", fin=None, iin=None):
-        """Model::forwardPassNamed(fin, iin, training=false) on the device."""
+    def forward_named(self, graph: "DeviceGraph", fin=None, iin=None, training=False):
+        """Model::forwardPassNamed(fin, iin, training) on the device (the
+        training form keeps the backward's snapshots and applies the
+        layers' residual merges)."""
         self.set_inputs(fin, iin)
-        self.run(graph)
+        (self.run_training if training else self.run)(graph)
         return self.get("x")
+
+
+def branch_fields(L):
+    """(branch_type, merge_op) codes of a layer dict: what Model::push's
+    detectBranchType gives its name, unless the dict sets "branch_type" or
+    "merge_op" (names of BranchType / MergeOperation) as a caller may set the
+    Layer fields afterwards."""
+    bt, mop = _lib.detect_branch_type(L.get("name", ""))
+    bt, mop = L.get("branch_type", bt), L.get("merge_op", mop)
+    return _lib.BRANCH_TYPES.index(bt), _lib.MERGE_OPS.index(mop)
 
 
 class DeviceGraph:
@@ -385,14 +402,17 @@ class DeviceGraph:
             names = [n.encode() for n in L.get("inputs", [])]
             cnames = (ctypes.c_char_p * max(1, len(names)))(*names)
             name_b, out_b = L.get("name", "").encode(), L.get("output", "").encode()
-            self._keep += [cnames, name_b, out_b]
+            bt, mop = branch_fields(L)
+            srcs = list(L.get("branch_sources", []))
+            csrcs = (ctypes.c_int32 * max(1, len(srcs)))(*srcs)
+            self._keep += [cnames, name_b, out_b, csrcs]
             arr[i] = _lib.Layer_C(
                 _lib.LAYER_TYPES.get(L["type"], -1), name_b, cnames, len(names), out_b,
                 dw.ptr if dw is not None else None, 0 if dw is None else dw.size,
                 float(L.get("eps", 1e-5)), int(L.get("affine", True)), int(L.get("use_bias", True)),
                 int(L.get("in_features", 0)), int(L.get("vocab_size", 0)), int(L.get("embed_dim", 0)),
                 int(L.get("padding_idx", -1)), int(L.get("seq_len", 0)),
-                dg.ptr if dg is not None else None)
+                dg.ptr if dg is not None else None, bt, mop, csrcs, len(srcs))
         self.c_layers = arr
 
     def grads(self):

@@ -15,6 +15,12 @@ Follows brit45/mimir-framework Model.cpp:
                                       name); else "Missing input tensor"
   dispatch               :4891-...   per layer type (the op functions of oracle.py)
   output                 :6655,6674  stored under layer.output or "x"
+  residual merge         :6676-6685  training only: each layer's output is
+                                      kept (all_layer_outputs); a RESIDUAL
+                                      layer with a branch source merges its
+                                      output with that layer's
+                                      (executeBranchComputation :4550-4582,
+                                      computeBranchMerge :4344-4479)
   result                 :6823       the float tensor "x"
 The encoder's "mag"/"mod" injection (:4670-4700) belongs to the tokenizer /
 encoder subsystem and is not restated: graphs here pass such tensors by name.
@@ -104,9 +110,52 @@ def _apply(L, ins):
     raise ModelError(f"unsupported layer type {t}")
 
 
-def forward_named(layers, fin=None, iin=None):
-    """Model::forwardPassNamed(fin, iin, training=false) for the layer types
-    in SUPPORTED.  Returns the float32 "x" output."""
+def detect_branch_type(name):
+    """Layer::detectBranchType (Layers.hpp:260-304), which Model::push runs on
+    every layer's name (Model.cpp:3145): (branch_type, merge_op); merge_op
+    keeps its default ADD where the reference leaves it."""
+    def has(*w):
+        return all(x in name for x in w)
+    if has("residual") or has("shortcut") or has("skip"):
+        return "RESIDUAL", "ADD"
+    if has("concat"):
+        return "SKIP_CONNECTION", "CONCATENATE"
+    if has("dense", "connect"):
+        return "DENSE_CONNECTION", "CONCATENATE"
+    if has("attention", "branch"):
+        return "ATTENTION_BRANCH", "ATTENTION_WEIGHTED"
+    if has("inception") or has("multiscale"):
+        return "MULTI_SCALE", "CONCATENATE"
+    if has("gate"):
+        return "GATE", "GATED"
+    if has("split"):
+        return "SPLIT", "ADD"
+    if has("merge") or has("fusion"):
+        return "MERGE", ("ADD" if has("add") else "MULTIPLY" if has("mul") else
+                         "CONCATENATE" if has("concat") else "ADD")
+    return "NONE", "ADD"
+
+
+def merge_of(L, i):
+    """(source layer, merge_op) of layer i's residual merge, or None:
+    executeBranchComputation (Model.cpp:4550-4582) merges only a RESIDUAL
+    layer whose first branch source indexes all_layer_outputs, which holds
+    layers 0..i at that point."""
+    bt, mop = detect_branch_type(L.get("name", ""))
+    bt, mop = L.get("branch_type", bt), L.get("merge_op", mop)
+    srcs = L.get("branch_sources", [])
+    if bt != "RESIDUAL" or not srcs or not 0 <= srcs[0] <= i:
+        return None
+    return srcs[0], mop
+
+
+def forward_named(layers, fin=None, iin=None, training=False):
+    """Model::forwardPassNamed(fin, iin, training) for the layer types in
+    SUPPORTED.  Returns the float32 "x" output.  The training form applies
+    the residual merges (and refuses Dropout, whose training form draws a
+    random mask)."""
+    if training:
+        return _forward_snap(layers, fin, iin)[0]
     fin = {k: np.ascontiguousarray(v, np.float32).ravel() for k, v in (fin or {}).items()}
     iin = {k: np.ascontiguousarray(v, np.int32).ravel() for k, v in (iin or {}).items()}
     x0 = fin.get("x", fin.get("__input__", np.zeros(0, np.float32)))
@@ -149,7 +198,10 @@ _SIZES_ONLY = ("Add", "Identity")
 
 def _forward_snap(layers, fin, iin):
     """forward_named with the per-layer input snapshots the reference keeps in
-    training mode (Model.cpp:4858-4878): (values or None, sizes)."""
+    training mode (Model.cpp:4858-4878): (values or None, sizes), and the
+    residual merges of the training form.  The backward then ignores the
+    merges, as Model::backwardPass does: backpropThroughBranch
+    (Model.cpp:4584-4613) is never called."""
     fin = {k: np.ascontiguousarray(v, np.float32).ravel() for k, v in (fin or {}).items()}
     iin = {k: np.ascontiguousarray(v, np.int32).ravel() for k, v in (iin or {}).items()}
     x0 = fin.get("x", fin.get("__input__", np.zeros(0, np.float32)))
@@ -160,6 +212,7 @@ def _forward_snap(layers, fin, iin):
             istore[alias] = iin["seq"]
     fstore.update(fin)
     snaps = []
+    outs = []
     for L in layers:
         if L["type"] not in BACKWARD_SUPPORTED:
             raise ModelError(f"unsupported layer type {L['type']} for backward")
@@ -179,7 +232,16 @@ def _forward_snap(layers, fin, iin):
             raise ModelError(f"Missing input tensor: {name}")
         vals = None if L["type"] in _SIZES_ONLY else [a.copy() for a in ins]
         snaps.append((vals, [a.size for a in ins]))
-        fstore[L.get("output") or "x"] = np.asarray(_apply(L, ins), np.float32).ravel()
+        out = L.get("output") or "x"
+        fstore[out] = np.asarray(_apply(L, ins), np.float32).ravel()
+        outs.append(fstore[out])  # all_layer_outputs (Model.cpp:6676-6678)
+        m = merge_of(L, len(outs) - 1)
+        if m is not None:  # Model.cpp:6681-6685
+            try:
+                outs[-1] = O.branch_merge(outs[-1], outs[m[0]], m[1])
+            except O.OracleError as e:
+                raise ModelError(str(e)) from e
+            fstore[out] = outs[-1]
     return fstore["x"].copy(), snaps
 
 

@@ -19,7 +19,13 @@ class _Spec(Structure):
                 ("params_count", c_int64), ("weights", c_void_p), ("eps", c_float),
                 ("affine", c_int32), ("use_bias", c_int32), ("in_features", c_int32),
                 ("vocab_size", c_int32), ("embed_dim", c_int32), ("padding_idx", c_int32),
-                ("seq_len", c_int32)]
+                ("seq_len", c_int32), ("branch_type", c_int32), ("merge_op", c_int32),
+                ("branch_sources", POINTER(c_int32)), ("n_branch_sources", c_int32)]
+
+# The reference's BranchType and MergeOperation (Layers.hpp:59-80), in order.
+BRANCH_TYPES = ("NONE", "RESIDUAL", "SKIP_CONNECTION", "DENSE_CONNECTION", "ATTENTION_BRANCH", "MULTI_SCALE",
+                "GATE", "SPLIT", "MERGE")
+MERGE_OPS = ("ADD", "MULTIPLY", "CONCATENATE", "MAX", "AVERAGE", "GATED", "ATTENTION_WEIGHTED")
 
 
 class RefModelError(RuntimeError):
@@ -57,7 +63,7 @@ def _load():
         f = lib.ref_model_forward
         f.argtypes = [POINTER(_Spec), c_int32, POINTER(c_char_p), POINTER(c_void_p), POINTER(c_int64),
                       c_int32, POINTER(c_char_p), POINTER(c_void_p), POINTER(c_int64), c_int32,
-                      c_void_p, c_int64, POINTER(c_int64), c_char_p, c_int32]
+                      c_void_p, c_int64, POINTER(c_int64), c_char_p, c_int32, c_int32]
         f.restype = c_int32
         b = lib.ref_model_backward
         b.argtypes = [POINTER(_Spec), c_int32, POINTER(c_char_p), POINTER(c_void_p), POINTER(c_int64),
@@ -95,14 +101,18 @@ def _marshal(layers, fin, iin):
     for i, L in enumerate(layers):
         w = L.get("weights")
         w = None if w is None else np.ascontiguousarray(w, np.float32)
-        keep.append(w)
+        srcs = (c_int32 * max(1, len(L.get("branch_sources", []))))(*L.get("branch_sources", []))
+        keep += [w, srcs]
         specs[i] = _Spec(L["name"].encode(), L["type"].encode(), ",".join(L.get("inputs", [])).encode(),
                          L.get("output", "").encode(), int(L.get("params_count", 0 if w is None else w.size)),
                          None if w is None else w.ctypes.data, float(L.get("eps", 1e-5)),
                          int(L.get("affine", True)), int(L.get("use_bias", True)),
                          int(L.get("in_features", 0)), int(L.get("vocab_size", 0)),
                          int(L.get("embed_dim", 0)), int(L.get("padding_idx", -1)),
-                         int(L.get("seq_len", 0)))
+                         int(L.get("seq_len", 0)),
+                         BRANCH_TYPES.index(L["branch_type"]) if "branch_type" in L else -1,
+                         MERGE_OPS.index(L["merge_op"]) if "merge_op" in L else -1,
+                         srcs, len(L.get("branch_sources", [])))
     fa = {k: np.ascontiguousarray(v, np.float32).ravel() for k, v in fin.items()}
     ia = {k: np.ascontiguousarray(v, np.int32).ravel() for k, v in iin.items()}
     keep += list(fa.values()) + list(ia.values())
@@ -115,15 +125,17 @@ def _marshal(layers, fin, iin):
     return keep, (specs, len(layers), fn, fd, fs, len(fa), inn, idd, isz, len(ia))
 
 
-def forward_named(layers, fin=None, iin=None, out_cap=1 << 24):
+def forward_named(layers, fin=None, iin=None, out_cap=1 << 24, training=False):
     """layers: list of dicts (see oracle.model_oracle.Layer fields); fin/iin:
-    {name: float32 / int32 array}.  Returns the float32 "x" output."""
+    {name: float32 / int32 array}.  Returns the float32 "x" output of
+    forwardPassNamed(fin, iin, training)."""
     keep, args = _marshal(layers, fin, iin)
     out = np.empty(out_cap, np.float32)
     n = c_int64(0)
     err = ctypes.create_string_buffer(512)
     with _StdoutToStderr():
-        st = _load().ref_model_forward(*args, out.ctypes.data, out_cap, ctypes.byref(n), err, 512)
+        st = _load().ref_model_forward(*args, out.ctypes.data, out_cap, ctypes.byref(n), err, 512,
+                                       int(bool(training)))
     del keep
     if st:
         raise RefModelError(err.value.decode(errors="replace"))

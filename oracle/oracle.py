@@ -183,6 +183,41 @@ def mul(a, b):
     return y
 
 
+MERGE_OPS = ("ADD", "MULTIPLY", "CONCATENATE", "MAX", "AVERAGE", "GATED", "ATTENTION_WEIGHTED")
+
+
+def branch_merge(b1, b2, op):
+    """Model::computeBranchMerge(branch1, branch2, output, merge_op) with the
+    hardware path the reference takes on an AVX2 host (Model.cpp:4344-4479):
+    output has branch1's size (both, for CONCATENATE) and reads branch2[i]
+    for i < branch1.size().  ADD (:4355-4380), and the default branch that
+    GATED / ATTENTION_WEIGHTED take (copy, then +=, :4470-4477): b1 + b2.
+    MULTIPLY (:4382-4406): b1 * b2.  AVERAGE (:4434-4460): (b1 + b2) * 0.5f.
+    MAX (:4408-4432): the 8-wide _mm256_max_ps loop over the largest multiple
+    of 8 (b1 > b2 ? b1 : b2), then the std::max tail (b1 < b2 ? b2 : b1).
+    CONCATENATE (:4462-4468): b1 then b2.  Each element is one or two IEEE
+    float32 operations, which numpy float32 arithmetic performs exactly so.
+    Raises OracleError where the reference would read past branch2's end."""
+    a = _f32(b1).ravel()
+    b = _f32(b2).ravel()
+    op = MERGE_OPS[op] if not isinstance(op, str) else op
+    if op == "CONCATENATE":
+        return np.concatenate([a, b])
+    if b.size < a.size:
+        raise OracleError("branch merge: branch2 shorter than branch1 (read out of bounds in the reference)")
+    b = b[:a.size]
+    with np.errstate(all="ignore"):
+        if op == "MULTIPLY":
+            return a * b
+        if op == "AVERAGE":
+            return (a + b) * np.float32(0.5)
+        if op == "MAX":
+            body = a.size // 8 * 8
+            return np.concatenate([np.where(a[:body] > b[:body], a[:body], b[:body]),
+                                   np.where(a[body:] < b[body:], b[body:], a[body:])])
+        return a + b
+
+
 def softmax_rows(x, mode=SOFTMAX_DIV_EPS):
     x = _f32(x)
     if x.ndim == 1:

@@ -41,6 +41,12 @@ struct ref_layer_spec {
     int32_t embed_dim;
     int32_t padding_idx;
     int32_t seq_len;
+    // Branch fields (Layers.hpp:214-219), set after Model::push's
+    // detectBranchType: -1 keeps what it derived from the name.
+    int32_t branch_type;
+    int32_t merge_op;
+    const int32_t* branch_sources;
+    int32_t n_branch_sources;
 };
 
 // Layers from the specs, weights copied into the blocks allocateParams made.
@@ -66,6 +72,9 @@ static void build_model(Model& m, const ref_layer_spec* specs, int32_t n_layers)
         L.embed_dim = s.embed_dim;
         L.padding_idx = s.padding_idx;
         L.seq_len = s.seq_len;
+        if (s.branch_type >= 0) L.branch_type = static_cast<BranchType>(s.branch_type);
+        if (s.merge_op >= 0) L.merge_op = static_cast<MergeOperation>(s.merge_op);
+        L.branch_sources.assign(s.branch_sources, s.branch_sources + (s.branch_sources ? s.n_branch_sources : 0));
     }
     m.allocateParams();
     for (int32_t i = 0; i < n_layers; ++i) {
@@ -97,16 +106,18 @@ static std::vector<float> run_forward(Model& m, const char* const* fnames, const
 
 // Named inputs: nf float tensors and ni int tensors.  Writes at most out_cap
 // floats of the returned "x" to out and its size to *out_n.  Returns 0, or 1
-// when the reference throws (message copied to err).
+// when the reference throws (message copied to err).  `training` is
+// forwardPassNamed's flag (the training form applies residual merges).
 int ref_model_forward(const ref_layer_spec* specs, int32_t n_layers, const char* const* fnames,
                       const float* const* fdata, const int64_t* fsizes, int32_t nf,
                       const char* const* inames, const int32_t* const* idata, const int64_t* isizes,
                       int32_t ni, float* out, int64_t out_cap, int64_t* out_n, char* err,
-                      int32_t err_cap) {
+                      int32_t err_cap, int32_t training) {
     try {
         Model m;
         build_model(m, specs, n_layers);
-        const std::vector<float> y = run_forward(m, fnames, fdata, fsizes, nf, inames, idata, isizes, ni, false);
+        const std::vector<float> y =
+            run_forward(m, fnames, fdata, fsizes, nf, inames, idata, isizes, ni, training != 0);
         *out_n = static_cast<int64_t>(y.size());
         const size_t n = std::min(static_cast<size_t>(out_cap), y.size());
         if (n) std::memcpy(out, y.data(), n * sizeof(float));

@@ -214,6 +214,100 @@ def train_graphs():
     return out
 
 
+# Training graphs with residual merges (forwardPassView with training=true,
+# Model.cpp:6676-6685 -> executeBranchComputation :4550-4582 ->
+# computeBranchMerge :4344-4479): (name, layers, float_inputs, int_inputs).
+# A layer merges when its branch type is RESIDUAL (from its name, as
+# Model::push's detectBranchType sets it, or set explicitly) and its first
+# branch source is a layer at or before it.  The loss gradient is drawn by
+# the caller at the training output's size.
+MERGE_OPS = ("ADD", "MULTIPLY", "CONCATENATE", "MAX", "AVERAGE", "GATED", "ATTENTION_WEIGHTED")
+
+
+def merge_graphs():
+    out = []
+    # Tests/test_runtime_residual_merge.cpp:9-47 exactly.
+    out.append(("residual_merge_kat",
+                [dict(name="skip", type="Identity", inputs=["x"], output="skip"),
+                 dict(name="my_residual", type="Multiply", inputs=["x", "scale"], output="x",
+                      branch_sources=[0], merge_op="ADD")],
+                {"x": [1.0, 2.0], "scale": [2.0, 3.0]}, {}))
+
+    # Every merge operation on a ragged length (the MAX body and its tail),
+    # with NaN, infinities and signed zeros on both sides of the merge, so
+    # MAX's two forms (vmaxps, std::max) are told apart.
+    specials = np.array([np.nan, 1.0, -0.0, 0.0, np.inf, -np.inf, 2.0, np.nan, -3.0, 0.0, -0.0, np.nan, 5.0],
+                        np.float32)
+    other = np.array([1.0, np.nan, 0.0, -0.0, -np.inf, 7.0, np.nan, np.nan, -3.0, -0.0, 0.0, 4.0, np.nan],
+                     np.float32)
+    for op in MERGE_OPS:
+        out.append((f"merge_{op.lower()}_specials",
+                    [dict(name="src", type="Identity", inputs=["b"], output="skipped"),
+                     dict(name="block_residual", type="Identity", inputs=["a"], output="x",
+                          branch_sources=[0], merge_op=op)],
+                    {"a": specials, "b": other}, {}))
+
+    r = _rng(21)
+    rows, d = 6, 40
+    x = (1.3 * r.standard_normal(rows * d) + 0.3).astype(np.float32)
+    ln_w = np.concatenate([1 + 0.1 * r.standard_normal(d), 0.1 * r.standard_normal(d)]).astype(np.float32)
+    for op in MERGE_OPS:
+        # A pre-norm block whose GELU output is merged with the LayerNorm
+        # input's producer, then used downstream (so the merge changes the
+        # gradient's inputs, not its routing).
+        out.append((f"block_{op.lower()}",
+                    [dict(name="inp", type="SiLU", inputs=["__input__"], output="h"),
+                     dict(name="ln", type="LayerNorm", inputs=["h"], output="n", in_features=d, weights=ln_w),
+                     dict(name="ffn_residual", type="GELU", inputs=["n"], output="g",
+                          branch_sources=[0], merge_op=op),
+                     dict(name="head", type="LayerNorm", inputs=["g"], output="x", in_features=d if op !=
+                          "CONCATENATE" else 0, affine=False)],
+                    {"__input__": x}, {}))
+
+    # Sources: the layer itself (merged with its own output), a later layer
+    # and a negative index (no merge), a longer source (its head is read), a
+    # RESIDUAL type set on a neutral name, a GATE-typed layer with a source
+    # (no merge: only RESIDUAL merges), and a chain where a merged output is
+    # itself a later merge's source.
+    r = _rng(22)
+    v = r.standard_normal(24).astype(np.float32)
+    long_src = r.standard_normal(48).astype(np.float32)
+    out.append(("self_later_negative",
+                [dict(name="a_shortcut", type="GELU", inputs=["v"], output="a", branch_sources=[0]),
+                 dict(name="b_skip", type="SiLU", inputs=["a"], output="b", branch_sources=[2]),
+                 dict(name="c_residual", type="GELU", inputs=["b"], output="c", branch_sources=[-1]),
+                 dict(name="d", type="Add", inputs=["c", "a"], output="x")],
+                {"v": v}, {}))
+    out.append(("longer_source_and_chain",
+                [dict(name="wide", type="GELU", inputs=["w"], output="w2"),
+                 dict(name="plain", type="SiLU", inputs=["v"], output="p", branch_type="RESIDUAL",
+                      branch_sources=[0], merge_op="AVERAGE"),
+                 dict(name="gate", type="GELU", inputs=["p"], output="q", branch_sources=[1]),
+                 dict(name="chain_residual", type="Multiply", inputs=["q", "v"], output="x",
+                      branch_sources=[1], merge_op="MAX")],
+                {"v": v, "w": long_src}, {}))
+    # A merge into a name read later by its old value's consumers: the
+    # merged tensor replaces the name, the source is the value layer s made.
+    out.append(("rebound_source",
+                [dict(name="s", type="GELU", inputs=["x"], output="h"),
+                 dict(name="rebind", type="SiLU", inputs=["x"], output="h"),
+                 dict(name="h_residual", type="Identity", inputs=["x"], output="x",
+                      branch_sources=[0], merge_op="MULTIPLY"),
+                 dict(name="sum", type="Add", inputs=["x", "h"], output="x")],
+                {"x": v}, {}))
+    return out
+
+
+def merge_error_graphs():
+    """A merge whose source is shorter than the layer's output: the
+    reference reads past the source's end (undefined behaviour), the device
+    and the restatement refuse it."""
+    return [("short_source",
+             [dict(name="s", type="Identity", inputs=["short"], output="s"),
+              dict(name="r_residual", type="GELU", inputs=["x"], output="x", branch_sources=[0])],
+             {"x": np.ones(8, np.float32), "short": np.ones(5, np.float32)}, {})]
+
+
 def checkpoint_layers():
     """The layers of the SafeTensors fixture tests/golden/ref_checkpoint.safetensors
     (written by the reference's save_checkpoint from these weights)."""

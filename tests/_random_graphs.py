@@ -28,7 +28,16 @@ _WEIGHTS = {"LayerNorm": 3, "RMSNorm": 2, "Softmax": 1, "LogSoftmax": 1, "GELU":
             "Multiply": 2, "Embedding": 1, "Identity": 1, "Dropout": 1}
 
 
-def random_graph(seed, training=False):
+MERGE_OPS = ("ADD", "MULTIPLY", "CONCATENATE", "MAX", "AVERAGE", "GATED", "ATTENTION_WEIGHTED")
+
+
+def random_graph(seed, training=False, merges=False):
+    """merges=True (training graphs): about a third of the layers also carry a
+    residual merge (Model.cpp:6676-6685) -- RESIDUAL from a "_residual" /
+    "_skip" / "_shortcut" name or set explicitly, a source drawn among the
+    layers so far (or an index that merges nothing), any merge operation.
+    A source must hold at least as many floats as the layer's output, or the
+    reference reads past its end; CONCATENATE accepts any source."""
     rng = np.random.default_rng(seed)
     types = BACKWARD_TYPES if training else FORWARD_TYPES
     p = np.array([_WEIGHTS[t] for t in types], float)
@@ -60,6 +69,7 @@ def random_graph(seed, training=False):
     n_layers = int(rng.integers(1, 7))
     bad_at = int(rng.integers(0, n_layers)) if broken else -1
     layers = []
+    out_sizes = []  # each layer's output size after its merge
 
     def pick(exclude=()):
         names = [k for k in sizes if k not in exclude]
@@ -154,6 +164,26 @@ def random_graph(seed, training=False):
         if out in int_sizes:  # keep int-store names out of the float store
             out = "x"
             L["output"] = "x"
+        if merges and rng.random() < 0.35:
+            i_l = len(layers)
+            op = str(rng.choice(MERGE_OPS))
+            # Earlier layers with room enough, and the layer itself (always valid).
+            ok = [j for j in range(i_l) if op == "CONCATENATE" or out_sizes[j] >= out_size] + [i_l]
+            r = rng.random()
+            src = int(rng.choice(ok)) if r < 0.85 else int(rng.choice([i_l + 1, -1, i_l + 5]))
+            kind = rng.random()
+            if kind < 0.5:
+                L["name"] += str(rng.choice(["_residual", "_skip", "_shortcut"]))
+            elif kind < 0.8:
+                L["branch_type"] = "RESIDUAL"
+            else:  # a source on a layer whose type does not merge
+                L["branch_type"] = str(rng.choice(["GATE", "NONE", "SPLIT"]))
+            L["branch_sources"] = [src]
+            L["merge_op"] = op
+            merging = L.get("branch_type", "RESIDUAL") == "RESIDUAL" and 0 <= src <= i_l
+            if merging and op == "CONCATENATE":
+                out_size += out_size if src == i_l else out_sizes[src]
         sizes[out] = out_size
+        out_sizes.append(out_size)
         layers.append(L)
     return (f"seed{seed}", layers, fin, iin)

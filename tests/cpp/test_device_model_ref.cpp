@@ -1,0 +1,169 @@
+// test_device_model_ref.cpp -- the C++ adapter's DeviceModel instantiated on
+// the reference's own `struct Layer` (Layers.hpp:86-309), whose weights live
+// in the blocks Model::allocateParams hands out (Layer::getWeights through
+// the weight_block), run on the GPU beside the reference's own
+// Model::forwardPassNamed / Model::backwardPass on the same layers.
+//
+// Built by oracle/Makefile (target `adapter_ref`, only where the reference
+// tree is present) against the reference headers and the reference runtime
+// compiled in place (oracle/_ref/libmimir_ref_model.so); run by
+// tests/test_gpu_cpp_adapter.py.  Standalone main() returning 0 / 1, like
+// the reference's CTest programs.
+#include "Model.hpp"
+#include "mimir_layerops_hip.hpp"
+
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+namespace {
+
+int failures = 0;
+
+#define CHECK(cond)                                                                   \
+    do {                                                                              \
+        if (!(cond)) {                                                                \
+            std::fprintf(stderr, "FAIL %s:%d: %s\n", __FILE__, __LINE__, #cond);      \
+            ++failures;                                                               \
+        }                                                                             \
+    } while (0)
+
+using FMap = std::unordered_map<std::string, std::vector<float>>;
+using IMap = std::unordered_map<std::string, std::vector<int>>;
+
+bool same_bits(const std::vector<float>& a, const std::vector<float>& b) {
+    return a.size() == b.size() && (a.empty() || std::memcmp(a.data(), b.data(), a.size() * 4) == 0);
+}
+
+// |a - b| <= max(1e-6, 1e-5 |b|) elementwise.
+bool close(const std::vector<float>& a, const std::vector<float>& b) {
+    if (a.size() != b.size()) return false;
+    for (size_t i = 0; i < a.size(); ++i)
+        if (!(std::fabs(a[i] - b[i]) <= std::fmax(1e-6f, 1e-5f * std::fabs(b[i])))) return false;
+    return true;
+}
+
+// Tests/test_runtime_residual_merge.cpp:9-47: layer 1 (named "my_residual",
+// so Model::push's detectBranchType makes it RESIDUAL) merges its output with
+// layer 0's by ADD, in training forwards only.
+void residual_merge_kat(mimir_hip::Context& c) {
+    Model m;
+    m.push("skip", "Identity", 0);
+    m.push("my_residual", "Multiply", 0);
+    auto& layers = m.getMutableLayers();
+    layers[0].inputs = {"x"};
+    layers[0].output = "skip";
+    layers[1].inputs = {"x", "scale"};
+    layers[1].output = "x";
+    CHECK(layers[1].branch_type == BranchType::RESIDUAL);
+    layers[1].branch_sources = {0};
+    layers[1].merge_op = MergeOperation::ADD;
+    m.allocateParams();
+    const FMap fin{{"x", {1.0f, 2.0f}}, {"scale", {2.0f, 3.0f}}};
+
+    const std::vector<float> ref_train = m.forwardPassNamed(fin, IMap{}, true);
+    const std::vector<float> ref_inf = m.forwardPassNamed(fin, IMap{}, false);
+    CHECK(same_bits(ref_train, {3.0f, 8.0f}));
+    CHECK(same_bits(ref_inf, {2.0f, 6.0f}));
+
+    mimir_hip::DeviceModel<Layer> dm(c, m.getLayers());
+    CHECK(same_bits(dm.forwardPassNamed(fin, IMap{}, true), ref_train));
+    CHECK(same_bits(dm.forwardPassNamed(fin, IMap{}, false), ref_inf));
+
+    // Every merge operation through the Layer field, against the reference.
+    const MergeOperation ops[] = {MergeOperation::ADD, MergeOperation::MULTIPLY, MergeOperation::CONCATENATE,
+                                  MergeOperation::MAX, MergeOperation::AVERAGE, MergeOperation::GATED,
+                                  MergeOperation::ATTENTION_WEIGHTED};
+    const FMap fin9{{"x", {1, -2, 3, -4, 5, -6, 7, -8, 0.5f}}, {"scale", {2, 3, -1, 0, 1, 1, -2, 2, 3}}};
+    for (MergeOperation op : ops) {
+        layers[1].merge_op = op;
+        const std::vector<float> want = m.forwardPassNamed(fin9, IMap{}, true);
+        CHECK(same_bits(dm.forwardPassNamed(fin9, IMap{}, true), want));
+    }
+}
+
+// A LayerNorm whose gamma | beta come from the reference's weight block, then
+// a residual GELU ("block_residual", source: the LayerNorm), then an Add:
+// forward in both modes, and a training step whose gradients (grad_weights,
+// the "__input__" gradient) must equal the reference's.  The reference's
+// backward ignores the merge (backpropThroughBranch is never called), and so
+// must the device's.
+void weight_block_and_backward(mimir_hip::Context& c) {
+    const int rows = 3, feat = 8;
+    Model m;
+    m.push("ln", "LayerNorm", 2 * feat);
+    m.push("block_residual", "GELU", 0);
+    m.push("out", "Add", 0);
+    auto& layers = m.getMutableLayers();
+    layers[0].inputs = {"__input__"};
+    layers[0].output = "h";
+    layers[0].in_features = feat;
+    layers[1].inputs = {"h"};
+    layers[1].output = "g";
+    layers[1].branch_sources = {0};
+    layers[2].inputs = {"g", "bias"};
+    layers[2].output = "x";
+    m.allocateParams();
+    float* w = layers[0].getWeights();
+    CHECK(w != nullptr && layers[0].getWeightsSize() == 2 * feat);
+    for (int i = 0; i < feat; ++i) {
+        w[i] = 1.0f + 0.05f * static_cast<float>(i);
+        w[feat + i] = 0.01f * static_cast<float>(i) - 0.03f;
+    }
+    std::vector<float> x(rows * feat), bias(feat), loss(rows * feat);
+    for (size_t i = 0; i < x.size(); ++i) {
+        x[i] = std::sin(0.7f * static_cast<float>(i)) * 2.0f + 0.25f;
+        loss[i] = std::cos(0.3f * static_cast<float>(i));
+    }
+    for (int i = 0; i < feat; ++i) bias[i] = 0.1f * static_cast<float>(i);
+    const FMap fin{{"__input__", x}, {"bias", bias}};
+
+    mimir_hip::DeviceModel<Layer> dm(c, m.getLayers());
+    const std::vector<float> ref_inf = m.forwardPassNamed(fin, IMap{}, false);
+    CHECK(close(dm.forwardPassNamed(fin, IMap{}, false), ref_inf));
+
+    const std::vector<float> ref_train = m.forwardPassNamed(fin, IMap{}, true);
+    m.backwardPass(loss);
+    const std::vector<float> ref_gw = m.getLayers()[0].grad_weights;
+    CHECK(m.hasLastInputGradient());
+    const std::vector<float> ref_gin = m.getLastInputGradient();
+    CHECK(!close(ref_train, ref_inf));  // the merge changed the training output
+
+    std::vector<Layer> dev_layers = m.getLayers();  // grad_weights start from the reference's zeros
+    for (auto& L : dev_layers) std::fill(L.grad_weights.begin(), L.grad_weights.end(), 0.0f);
+    mimir_hip::DeviceModel<Layer> dt(c, dev_layers);
+    CHECK(close(dt.forwardPassNamed(fin, IMap{}, true), ref_train));
+    dt.backwardPass(loss, dev_layers);
+    CHECK(dt.hasLastInputGradient());
+    // Float32 sums over rows: held at 1e-5 of the summed magnitudes' scale.
+    auto close_sum = [](const std::vector<float>& a, const std::vector<float>& b, float scale) {
+        if (a.size() != b.size()) return false;
+        for (size_t i = 0; i < a.size(); ++i)
+            if (!(std::fabs(a[i] - b[i]) <= std::fmax(1e-6f, 1e-5f * scale))) return false;
+        return true;
+    };
+    CHECK(close_sum(dev_layers[0].grad_weights, ref_gw, 8.0f));
+    CHECK(close_sum(dt.getLastInputGradient(), ref_gin, 8.0f));
+}
+
+}  // namespace
+
+int main() {
+    try {
+        auto& c = mimir_hip::Context::instance();
+        residual_merge_kat(c);
+        weight_block_and_backward(c);
+    } catch (const std::exception& e) {
+        std::fprintf(stderr, "FAIL: exception %s\n", e.what());
+        return 1;
+    }
+    if (failures) {
+        std::fprintf(stderr, "%d check(s) failed\n", failures);
+        return 1;
+    }
+    std::printf("DeviceModel<Layer> matches the reference Model: all checks passed\n");
+    return 0;
+}

@@ -18,6 +18,8 @@ namespace {
 // The fields of the reference's `struct Layer` (Layers.hpp:86-309) the
 // adapter reads; weights live in a plain vector as with weight_block == nullptr.
 enum class LayerType { Softmax, LogSoftmax, Other };
+enum class BranchType { NONE, RESIDUAL };
+enum class MergeOperation { ADD, MULTIPLY, CONCATENATE, MAX, AVERAGE };
 
 struct TestLayer {
     std::string name;
@@ -35,6 +37,9 @@ struct TestLayer {
     int padding_idx = -1;
     std::vector<float> weights;
     std::vector<float> grad_weights;
+    BranchType branch_type = BranchType::NONE;
+    MergeOperation merge_op = MergeOperation::ADD;
+    std::vector<int> branch_sources;
     const float* getWeights() const { return weights.data(); }
     size_t getWeightsSize() const { return weights.size(); }
 };

@@ -81,6 +81,12 @@ def test_activations_closed_form():
     assert_close(O.silu(x), x64 / (1 + np.exp(-x64)), "SiLU")
     u = rng.standard_normal(x.size).astype(np.float32)
     assert_close(O.silu_mul(x, u), x64 / (1 + np.exp(-x64)) * u, "SiLU*up")
+    u64 = u.astype(np.float64)
+    assert_close(O.gelu_mul(x, u), gelu64 * u64, "GELU*up")
+    with pytest.raises(AssertionError):  # dropped cubic term in the gate
+        assert_close(O.gelu_mul(x, u), x64 * 0.5 * (1 + np.tanh(k * x64)) * u64)
+    with pytest.raises(AssertionError):  # the gate's GELU applied to up instead
+        assert_close(O.gelu_mul(x, u), x64 * u64 * 0.5 * (1 + np.tanh(k * (u64 + 0.044715 * u64 ** 3))))
 
 
 # ---------------------------------------------------------------------------

@@ -105,3 +105,19 @@ def test_gelu_silu_dense_grid():
                         rng.standard_normal(100000, dtype=np.float32)])
     assert_close(O.gelu(x), O.ref_gelu(x), "gelu")
     assert_close(O.silu(x), O.ref_silu(x), "silu")
+
+
+def test_gated_products_are_the_reference_compositions():
+    """oracle_gelu_mul and oracle_silu_mul restate the two reference calls a
+    gated product is made of: multiply_forward(gelu_forward(gate), up) and
+    multiply_forward(silu_forward(gate), up) (LayerOps.hpp:556-568, 570-581,
+    205-230), on the dense grid, the specials and normals."""
+    g = np.concatenate([np.linspace(-12, 12, 200001, dtype=np.float32), SPECIALS,
+                        rng.standard_normal(100000, dtype=np.float32)])
+    u = np.concatenate([rng.standard_normal(200001).astype(np.float32) * 3, SPECIALS[::-1],
+                        rng.standard_normal(100000, dtype=np.float32)])
+    assert_close(O.gelu_mul(g, u), O.ref_mul(O.ref_gelu(g), u), "gelu*up")
+    assert_close(O.silu_mul(g, u), O.ref_mul(O.ref_silu(g), u), "silu*up")
+    # The gate and the up operand are not interchangeable.
+    with pytest.raises(AssertionError):
+        assert_close(O.gelu_mul(u, g), O.ref_mul(O.ref_gelu(g), u))
