@@ -391,8 +391,31 @@ int mimir_store_run(mimir_store* store, const mimir_layer* layers, int32_t n_lay
  * (backpropThroughBranch, Model.cpp:4584-4613, is never called). */
 int mimir_store_run_training(mimir_store* store, const mimir_layer* layers, int32_t n_layers);
 
+/* The int-ids forward, Model::forwardPassView(const std::vector<int>&
+ * input_ids, bool training) (Model.cpp:1030-1349; Model::forwardPass(ids)
+ * :1026-1028), the Lua Mimir.Model.forward path.  set_input_ids is its input
+ * setup: both stores cleared, the ids (host data) stored as the int tensors
+ * "x" and "__input__" (:1046-1049). */
+int mimir_store_set_input_ids(mimir_store* store, const int32_t* ids, int64_t n);
+/* Its layer loop (:1143-1346).  An Embedding reads its first input from the
+ * int store and gathers the ids as ints (EINVAL "Int tensor not found: <name>"
+ * when absent; no padding fallback); every other layer reads float inputs
+ * (EINVAL "Tensor not found: <name>").  The int path's switch is narrower
+ * than forwardPassView(float)'s: of this path's types it runs LayerNorm,
+ * GELU, Softmax, LogSoftmax, Dropout, Add and Embedding, and refuses RMSNorm,
+ * SiLU, Multiply and Identity with the reference's strict-mode error
+ * "forwardPass(int): layer type not supported in int path: <type>"
+ * (:1311-1319); an Add with one input is "Add requires 2 inputs" (:1285).
+ * Outputs go to layer.output or "x"; with layers, the result must be the
+ * float tensor "x" (EINVAL "Tensor not found: x" otherwise, :1348).
+ * training=1 keeps the snapshots mimir_store_backward needs (Dropout is then
+ * refused, as in mimir_store_run_training); the int path has no residual
+ * merges. */
+int mimir_store_run_ids(mimir_store* store, const mimir_layer* layers, int32_t n_layers, int training);
+
 /* Model::backwardPass(loss_gradient), Model.cpp:7307-9153, over the layers of
- * the last mimir_store_run_training (the same array): the gradient map starts
+ * the last mimir_store_run_training or training mimir_store_run_ids (the
+ * same array): the gradient map starts
  * as {"x": loss_grad} (n_grad host floats) and each layer, last to first,
  * routes its output's gradient to its inputs with the branches of the
  * mimir_*_bwd entry points and accumulate_grad's copy-or-add (an input named

@@ -160,9 +160,28 @@ int put_host(mimir_store* s, int dtype, const std::string& name, const void* hos
 
 const char* layer_name(const mimir_layer& L) { return L.name ? L.name : "?"; }
 
+const char* type_name(int32_t t) {
+    switch (t) {
+        case MIMIR_LAYER_LAYERNORM: return "LayerNorm";
+        case MIMIR_LAYER_RMSNORM: return "RMSNorm";
+        case MIMIR_LAYER_SOFTMAX: return "Softmax";
+        case MIMIR_LAYER_LOGSOFTMAX: return "LogSoftmax";
+        case MIMIR_LAYER_GELU: return "GELU";
+        case MIMIR_LAYER_SILU: return "SiLU";
+        case MIMIR_LAYER_ADD: return "Add";
+        case MIMIR_LAYER_MULTIPLY: return "Multiply";
+        case MIMIR_LAYER_EMBEDDING: return "Embedding";
+        case MIMIR_LAYER_IDENTITY: return "Identity";
+        case MIMIR_LAYER_DROPOUT: return "Dropout";
+        default: return "?";
+    }
+}
+
 // One layer of Model::forwardPassView's loop (Model.cpp:4795-6680); with
-// `snap`, the training form that keeps the layer's inputs.
-int run_layer(mimir_store* s, const mimir_layer& L, Snap* snap) {
+// `snap`, the training form that keeps the layer's inputs.  `ids_path`: the
+// loop of the int-ids forward instead (Model.cpp:1143-1346), whose routing
+// and layer switch are narrower (see mimir_store_run_ids).
+int run_layer(mimir_store* s, const mimir_layer& L, Snap* snap, bool ids_path = false) {
     mimir_ctx* ctx = s->ctx;
     static const char* const kDefaultInput[] = {"x"};
     const char* const* names = L.n_inputs > 0 ? L.inputs : kDefaultInput;
@@ -180,8 +199,27 @@ int run_layer(mimir_store* s, const mimir_layer& L, Snap* snap) {
     };
     std::vector<In> in;
     in.reserve(n_in);
-    for (int k = 0; k < n_in; ++k) {
+    // The int path's Embedding reads only its first input, from the int store
+    // ("Int tensor not found", Model.cpp:1148 -> :936-948); every other layer
+    // reads float inputs ("Tensor not found", :1214-1215 -> :918-930), with no
+    // int fallback.
+    const int n_read = (ids_path && L.type == MIMIR_LAYER_EMBEDDING) ? 1 : n_in;
+    for (int k = 0; k < n_read; ++k) {
         const std::string name = names[k] ? names[k] : "";
+        if (ids_path) {
+            if (L.type == MIMIR_LAYER_EMBEDDING) {
+                auto iti = s->i32.find(name);
+                if (iti == s->i32.end())
+                    return fail(ctx, MIMIR_EINVAL, "Int tensor not found: %s (layer %s)", name.c_str(), layer_name(L));
+                in.push_back(In{iti->second.buf->p, iti->second.n, true, iti->second.buf});
+            } else {
+                auto itf = s->f32.find(name);
+                if (itf == s->f32.end())
+                    return fail(ctx, MIMIR_EINVAL, "Tensor not found: %s (layer %s)", name.c_str(), layer_name(L));
+                in.push_back(In{itf->second.buf->p, itf->second.n, false, itf->second.buf});
+            }
+            continue;
+        }
         auto itf = s->f32.find(name);
         if (itf != s->f32.end()) {
             in.push_back(In{itf->second.buf->p, itf->second.n, false, itf->second.buf});
@@ -222,6 +260,22 @@ int run_layer(mimir_store* s, const mimir_layer& L, Snap* snap) {
                 snap->vals.push_back(Slot{v.buf, v.n});
                 snap->ids_i32.push_back(v.ids_i32);
             }
+        }
+    }
+
+    if (ids_path) {  // the int path's reduced switch, Model.cpp:1242-1321 (strict mode)
+        switch (L.type) {
+            case MIMIR_LAYER_RMSNORM:
+            case MIMIR_LAYER_SILU:
+            case MIMIR_LAYER_MULTIPLY:
+            case MIMIR_LAYER_IDENTITY:
+                return fail(ctx, MIMIR_EINVAL, "forwardPass(int): layer type not supported in int path: %s (layer %s)",
+                            type_name(L.type), layer_name(L));
+            case MIMIR_LAYER_ADD:  // :1285
+                if (n_in < 2) return fail(ctx, MIMIR_EINVAL, "Add requires 2 inputs (layer %s)", layer_name(L));
+                break;
+            default:
+                break;
         }
     }
 
@@ -314,8 +368,10 @@ int run_layer(mimir_store* s, const mimir_layer& L, Snap* snap) {
                 st = fail(ctx, MIMIR_EINVAL, "Embedding: weights not initialized (layer %s)", layer_name(L));
                 break;
             }
-            st = embedding_launch(ctx, in[0].p, in[0].ids_i32 ? kIdsI32AsF32 : kIdsF32, N, L.weights,
-                                  L.weights_len, L.vocab_size, L.embed_dim, L.padding_idx, y);
+            // The int path gathers the ids as ints (Model.cpp:1194-1203); the
+            // float path reads int-store ids through a float cast.
+            st = embedding_launch(ctx, in[0].p, ids_path ? kIdsI32 : in[0].ids_i32 ? kIdsI32AsF32 : kIdsF32, N,
+                                  L.weights, L.weights_len, L.vocab_size, L.embed_dim, L.padding_idx, y);
             break;
     }
     if (st != MIMIR_OK) {
@@ -578,6 +634,38 @@ int mimir_store_run(mimir_store* s, const mimir_layer* layers, int32_t n_layers)
     for (int32_t i = 0; i < n_layers; ++i) {
         chain.layer(i, n_layers);
         if (int st = run_layer(s, layers[i], nullptr)) return st;
+    }
+    return MIMIR_OK;
+}
+
+int mimir_store_set_input_ids(mimir_store* s, const int32_t* ids, int64_t n) {
+    if (!s) return MIMIR_EINVAL;
+    MIMIR_REQUIRE(s->ctx, n >= 0 && (n == 0 || ids), "mimir_store_set_input_ids: invalid argument");
+    s->clear();  // Model.cpp:1046-1049
+    if (int st = put_host(s, MIMIR_DTYPE_I32, "x", ids, n)) return st;
+    const Slot xs = s->i32.at("x");
+    s->bind(MIMIR_DTYPE_I32, "__input__", xs.buf, xs.n);
+    return MIMIR_OK;
+}
+
+int mimir_store_run_ids(mimir_store* s, const mimir_layer* layers, int32_t n_layers, int training) {
+    if (!s) return MIMIR_EINVAL;
+    MIMIR_REQUIRE(s->ctx, n_layers >= 0 && (n_layers == 0 || layers), "mimir_store_run_ids: invalid argument");
+    s->release_snaps();
+    if (training) s->snaps.resize(static_cast<size_t>(n_layers));
+    ChainOutputs chain(s->ctx);
+    for (int32_t i = 0; i < n_layers; ++i) {
+        chain.layer(i, n_layers);
+        if (int st = run_layer(s, layers[i], training ? &s->snaps[i] : nullptr, true)) {
+            s->release_snaps();
+            return st;
+        }
+    }
+    // Model.cpp:1348: the result is the float tensor "x" (no layers: an empty
+    // result, :1033-1037).
+    if (n_layers > 0 && s->f32.find("x") == s->f32.end()) {
+        s->release_snaps();
+        return fail(s->ctx, MIMIR_EINVAL, "Tensor not found: x");
     }
     return MIMIR_OK;
 }

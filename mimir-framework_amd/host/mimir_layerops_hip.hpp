@@ -460,6 +460,27 @@ public:
         return out;
     }
 
+    // Model::forwardPass(const std::vector<int>& input_ids, training)
+    // (Model.cpp:1026-1349), the int-ids forward: the ids are the int
+    // tensors "x" and "__input__"; Embedding layers gather them as ints and
+    // the reduced layer switch of that path applies (RMSNorm, SiLU, Multiply
+    // and Identity throw).  The reference's default is training=true.
+    std::vector<float> forwardPass(const std::vector<int>& input_ids, bool training = true) {
+        ctx_->check(mimir_store_set_input_ids(store_, reinterpret_cast<const int32_t*>(input_ids.data()),
+                                              static_cast<int64_t>(input_ids.size())),
+                    "DeviceModel ids");
+        build_layers();
+        ctx_->check(mimir_store_run_ids(store_, ls_.data(), static_cast<int32_t>(ls_.size()), training ? 1 : 0),
+                    "DeviceModel forward (int ids)");
+        if (ls_.empty()) return {};
+        int64_t n = 0;
+        void* p = nullptr;
+        ctx_->check(mimir_store_info(store_, "x", MIMIR_DTYPE_F32, &p, &n), "DeviceModel output");
+        std::vector<float> out(static_cast<size_t>(n));
+        ctx_->check(mimir_store_get(store_, "x", MIMIR_DTYPE_F32, out.data(), n, &n), "DeviceModel output");
+        return out;
+    }
+
     // Model::backwardPass(loss_gradient) (Model.cpp:7307-9153) after a
     // training forward.  Parameter gradients are added into the layers'
     // grad_weights as the reference does (a vector of the wrong size is first

@@ -123,6 +123,8 @@ SIGNATURES = {
                                        POINTER(c_char_p), POINTER(c_void_p), POINTER(c_int64), c_int32]),
     "mimir_store_run": (c_int, [_P, POINTER(Layer_C), c_int32]),
     "mimir_store_run_training": (c_int, [_P, POINTER(Layer_C), c_int32]),
+    "mimir_store_set_input_ids": (c_int, [_P, _P, c_int64]),
+    "mimir_store_run_ids": (c_int, [_P, POINTER(Layer_C), c_int32, c_int]),
     "mimir_safetensors_open": (c_int, [_P, c_char_p, _PP]),
     "mimir_safetensors_close": (c_int, [_P]),
     "mimir_safetensors_count": (c_int64, [_P]),

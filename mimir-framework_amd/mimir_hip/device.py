@@ -360,6 +360,29 @@ class Store:
         self.backward(graph, loss_grad)
         return graph.grads(), self.grad("__input__")
 
+    def set_input_ids(self, ids):
+        ids = np.ascontiguousarray(ids, np.int32).ravel()
+        self.ctx.check(self.ctx.lib.mimir_store_set_input_ids(self.handle, ids.ctypes.data_as(c_void_p), ids.size))
+
+    def run_ids(self, graph: "DeviceGraph", training=True):
+        self.ctx.check(self.ctx.lib.mimir_store_run_ids(self.handle, graph.c_layers, len(graph.layers),
+                                                        int(bool(training))))
+
+    def forward_ids(self, graph: "DeviceGraph", ids, training=True):
+        """Model::forwardPass(const std::vector<int>& ids, training) on the
+        device (the reference's default is training=true).  Returns the float
+        "x" output (empty for a graph without layers)."""
+        self.set_input_ids(ids)
+        self.run_ids(graph, training)
+        return self.get("x") if graph.layers else np.zeros(0, np.float32)
+
+    def train_step_ids(self, graph: "DeviceGraph", ids, loss_grad):
+        """forwardPass(ids, training=true) then Model::backwardPass."""
+        self.set_input_ids(ids)
+        self.run_ids(graph, True)
+        self.backward(graph, loss_grad)
+        return graph.grads(), self.grad("__input__")
+
     def forward_named(self, graph: "DeviceGraph", fin=None, iin=None, training=False):
         """Model::forwardPassNamed(fin, iin, training) on the device (the
         training form keeps the backward's snapshots and applies the

@@ -260,6 +260,11 @@ def backward_named(layers, fin, iin, loss_grad, scales=False):
     gradient onto its own output gradient (numpy in-place ops on the same
     array reproduce this)."""
     _, snaps = _forward_snap(layers, fin, iin)
+    return _backward(layers, snaps, loss_grad, scales)
+
+
+def _backward(layers, snaps, loss_grad, scales):
+    """Model::backwardPass over the snapshots of a training forward."""
     grads = []
     for L in layers:
         w = L.get("weights")
@@ -371,3 +376,71 @@ def backward_named(layers, fin, iin, loss_grad, scales=False):
     if scales:
         return grads, (None if gin is None else gin.copy()), mags
     return grads, (None if gin is None else gin.copy())
+
+
+# ---------------------------------------------------------------------------
+# The int-ids forward, Model::forwardPassView(const std::vector<int>&,
+# training) (Model.cpp:1030-1349), reached by Model::forwardPass(ids)
+# (:1026-1028) and the Lua Mimir.Model.forward.
+# ---------------------------------------------------------------------------
+
+# The int path's switch (Model.cpp:1242-1321) for the types of this path; the
+# others (RMSNorm, SiLU, Multiply, Identity) hit its strict-mode default.
+INT_PATH_TYPES = ("LayerNorm", "GELU", "Softmax", "LogSoftmax", "Dropout", "Add", "Embedding")
+
+
+def _forward_ids_snap(layers, ids, training):
+    ids = np.ascontiguousarray(ids, np.int32).ravel()
+    if not layers:  # :1033-1037: no layers -> an empty result
+        return np.zeros(0, np.float32), []
+    istore = {"x": ids, "__input__": ids}  # :1046-1049
+    fstore = {}
+    snaps = []
+    for L in layers:
+        names = L.get("inputs") or ["x"]
+        t = L["type"]
+        if t == "Embedding":  # :1145-1205
+            if names[0] not in istore:
+                raise ModelError(f"Int tensor not found: {names[0]}")
+            v = istore[names[0]]
+            snaps.append(([v.astype(np.float32)], [v.size]))  # ids snapshotted as floats (:1160-1165)
+            w = L.get("weights")
+            vocab = max(1, L.get("vocab_size", 0))
+            dim = max(1, L.get("embed_dim", 0))
+            if w is None or np.asarray(w).size == 0:
+                raise ModelError("Embedding: weights not initialized")
+            if np.asarray(w).size < vocab * dim:
+                raise ModelError("Embedding: invalid weight size")
+            out = O.embedding(v, np.asarray(w, np.float32), vocab, dim, L.get("padding_idx", -1)).ravel()
+        else:
+            ins = []
+            for name in names:
+                if name not in fstore:
+                    raise ModelError(f"Tensor not found: {name}")
+                ins.append(fstore[name])
+            snaps.append((None if t in _SIZES_ONLY else [a.copy() for a in ins], [a.size for a in ins]))
+            if t not in INT_PATH_TYPES:
+                raise ModelError(f"forwardPass(int): layer type not supported in int path: {t}")
+            if t == "Add" and len(ins) < 2:
+                raise ModelError("Add requires 2 inputs")
+            if t == "Dropout" and training:
+                raise ModelError("Dropout: its training form draws a random mask")
+            out = np.asarray(_apply(L, ins), np.float32).ravel()
+        fstore[L.get("output") or "x"] = out
+    if "x" not in fstore:  # :1348 getTensor("x")
+        raise ModelError("Tensor not found: x")
+    return fstore["x"].copy(), snaps
+
+
+def forward_ids(layers, ids, training=True):
+    """Model::forwardPass(const std::vector<int>& ids, training): the float
+    "x" result (the reference's default is training=true; the int path has
+    no residual merges)."""
+    return _forward_ids_snap(layers, ids, training)[0]
+
+
+def backward_ids(layers, ids, loss_grad, scales=False):
+    """forwardPass(ids, training=true) then Model::backwardPass(loss_grad), as
+    backward_named returns it."""
+    _, snaps = _forward_ids_snap(layers, ids, True)
+    return _backward(layers, snaps, loss_grad, scales)

@@ -71,6 +71,10 @@ def _load():
                       c_void_p, c_int64, POINTER(c_void_p), c_void_p, c_int64, POINTER(c_int64),
                       c_char_p, c_int32]
         b.restype = c_int32
+        fi = lib.ref_model_forward_ids
+        fi.argtypes = [POINTER(_Spec), c_int32, c_void_p, c_int64, c_int32, c_void_p, c_int64, POINTER(c_int64),
+                       c_void_p, c_int64, POINTER(c_void_p), c_void_p, c_int64, POINTER(c_int64), c_char_p, c_int32]
+        fi.restype = c_int32
         sv = lib.ref_model_save_safetensors
         sv.argtypes = [POINTER(_Spec), c_int32, c_char_p, c_char_p, c_int32]
         sv.restype = c_int32
@@ -167,6 +171,41 @@ def backward(layers, fin, iin, loss_grad, in_cap=1 << 24):
         raise RefModelError(err.value.decode(errors="replace"))
     assert n.value <= in_cap, "input gradient larger than in_cap"
     return grads, (None if n.value < 0 else ig[:n.value].copy())
+
+
+def forward_ids(layers, ids, training=True, loss_grad=None, out_cap=1 << 24, in_cap=1 << 24):
+    """Model::forwardPass(const std::vector<int>& ids, training) (the
+    reference's default is training=true).  Returns the float32 output; with
+    loss_grad (a training forward), also (grads, input_grad) of the
+    backwardPass that follows, as backward() returns them."""
+    keep, args = _marshal(layers, {}, {})
+    ids = np.ascontiguousarray(ids, np.int32).ravel()
+    out = np.empty(out_cap, np.float32)
+    n = c_int64(0)
+    grads, gp, ig, lg = [], None, None, None
+    if loss_grad is not None:
+        lg = np.ascontiguousarray(loss_grad, np.float32).ravel()
+        for L in layers:
+            w = L.get("weights")
+            pc = int(L.get("params_count", 0 if w is None else np.asarray(w).size))
+            grads.append(np.zeros(pc, np.float32) if pc > 0 else None)
+        gp = (c_void_p * max(1, len(layers)))(*[0 if a is None else a.ctypes.data for a in grads])
+        ig = np.empty(in_cap, np.float32)
+    n_in = c_int64(0)
+    err = ctypes.create_string_buffer(512)
+    with _StdoutToStderr():
+        st = _load().ref_model_forward_ids(args[0], args[1], ids.ctypes.data, ids.size, int(bool(training)),
+                                           out.ctypes.data, out_cap, ctypes.byref(n),
+                                           None if lg is None else lg.ctypes.data, 0 if lg is None else lg.size,
+                                           gp, None if ig is None else ig.ctypes.data, in_cap, ctypes.byref(n_in),
+                                           err, 512)
+    del keep
+    if st:
+        raise RefModelError(err.value.decode(errors="replace"))
+    y = out[:n.value].copy()
+    if loss_grad is None:
+        return y
+    return y, (grads, None if n_in.value < 0 else ig[:n_in.value].copy())
 
 
 def save_safetensors(layers, path):

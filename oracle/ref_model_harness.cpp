@@ -165,6 +165,48 @@ int ref_model_backward(const ref_layer_spec* specs, int32_t n_layers, const char
     }
 }
 
+// The int-ids forward, Model::forwardPass(const std::vector<int>&, training)
+// (Model.cpp:1026-1349).  Writes at most out_cap floats of the result to out
+// and its size to *out_n.  With loss_grad non-null, a training forward is
+// followed by Model::backwardPass(loss_grad): grad_weights to grads_out[i],
+// the "__input__" gradient to in_grad (*in_n = -1 when none reached it), as
+// ref_model_backward.  Returns 0, or 1 when the reference throws.
+int ref_model_forward_ids(const ref_layer_spec* specs, int32_t n_layers, const int32_t* ids, int64_t n_ids,
+                          int32_t training, float* out, int64_t out_cap, int64_t* out_n, const float* loss_grad,
+                          int64_t n_grad, float* const* grads_out, float* in_grad, int64_t in_cap, int64_t* in_n,
+                          char* err, int32_t err_cap) {
+    try {
+        Model m;
+        build_model(m, specs, n_layers);
+        const std::vector<int> v(ids, ids + n_ids);
+        const std::vector<float> y = m.forwardPass(v, training != 0);
+        *out_n = static_cast<int64_t>(y.size());
+        const size_t n = std::min(static_cast<size_t>(out_cap), y.size());
+        if (n) std::memcpy(out, y.data(), n * sizeof(float));
+        if (loss_grad) {
+            m.backwardPass(std::vector<float>(loss_grad, loss_grad + n_grad));
+            const auto& layers = m.getLayers();
+            for (int32_t i = 0; i < n_layers; ++i) {
+                if (!grads_out || !grads_out[i]) continue;
+                const size_t pc = static_cast<size_t>(specs[i].params_count);
+                const std::vector<float>& g = layers[i].grad_weights;
+                for (size_t k = 0; k < pc; ++k) grads_out[i][k] = k < g.size() ? g[k] : 0.0f;
+            }
+            *in_n = -1;
+            if (m.hasLastInputGradient()) {
+                const std::vector<float>& g = m.getLastInputGradient();
+                *in_n = static_cast<int64_t>(g.size());
+                const size_t k = std::min(static_cast<size_t>(in_cap), g.size());
+                if (k) std::memcpy(in_grad, g.data(), k * sizeof(float));
+            }
+        }
+        return 0;
+    } catch (const std::exception& e) {
+        copy_error(e, err, err_cap);
+        return 1;
+    }
+}
+
 // Mimir::Serialization::save_checkpoint (Serialization.cpp) of a model built
 // from the specs, SafeTensors format, the reference's default SaveOptions.
 int ref_model_save_safetensors(const ref_layer_spec* specs, int32_t n_layers, const char* path, char* err,

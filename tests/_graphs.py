@@ -308,6 +308,59 @@ def merge_error_graphs():
              {"x": np.ones(8, np.float32), "short": np.ones(5, np.float32)}, {})]
 
 
+# Graphs for the int-ids forward, Model::forwardPass(const std::vector<int>&
+# ids, training) (Model.cpp:1026-1349): (name, layers, ids).  The first ones
+# run; ids_error_graphs() hold the cases the reference throws on.
+def ids_graphs():
+    out = []
+    r = _rng(31)
+    vocab, d, seq = 20, 16, 12
+    table = (0.5 * r.standard_normal(vocab * d)).astype(np.float32)
+    ln_w = np.concatenate([1 + 0.1 * r.standard_normal(d), 0.1 * r.standard_normal(d)]).astype(np.float32)
+    ids = r.integers(-2, vocab + 3, seq).astype(np.int32)
+    ids[:3] = 4  # a repeated row: its gradient sums in token order
+    ids[5] = 1   # the padding id
+    emb = dict(name="tok", type="Embedding", inputs=["x"], output="h", vocab_size=vocab, embed_dim=d,
+               padding_idx=1, weights=table)
+    out.append(("ids_block",
+                [emb,
+                 dict(name="ln", type="LayerNorm", inputs=["h"], output="n", in_features=d, weights=ln_w),
+                 dict(name="act", type="GELU", inputs=["n"], output="g"),
+                 dict(name="res", type="Add", inputs=["g", "h"], output="a"),
+                 dict(name="head", type="LogSoftmax", inputs=["a"], output="x")], ids))
+    out.append(("ids_default_names",
+                [dict(emb, inputs=[], output="x"),
+                 dict(name="act", type="GELU"),
+                 dict(name="drop", type="Dropout"),
+                 dict(name="sm", type="Softmax")], ids))
+    out.append(("ids_input_alias_and_broadcast",
+                [dict(emb, inputs=["__input__"], output="e"),
+                 dict(name="ln", type="LayerNorm", inputs=["e"], output="n", in_features=0, affine=False),
+                 dict(name="bias", type="Add", inputs=["n", "n"], output="x")], ids))
+    big = np.array([0, 3, (1 << 24) + 1, -(1 << 24) - 3, 2**31 - 1, -2**31, 7], np.int32)
+    out.append(("ids_extreme_values", [dict(emb, output="x")], big))
+    out.append(("ids_empty", [dict(emb, output="x")], np.zeros(0, np.int32)))
+    out.append(("no_layers", [], ids))
+    return out
+
+
+def ids_error_graphs():
+    r = _rng(32)
+    table = r.standard_normal(5 * 4).astype(np.float32)
+    emb = dict(name="tok", type="Embedding", inputs=["x"], output="h", vocab_size=5, embed_dim=4, weights=table)
+    ids = np.array([1, 2, 3], np.int32)
+    out = []
+    for t in ("RMSNorm", "SiLU", "Multiply", "Identity"):  # the int path's strict default (:1311-1319)
+        L = dict(name="op", type=t, inputs=["h"] + (["h"] if t == "Multiply" else []), output="x")
+        out.append((f"ids_refuses_{t.lower()}", [emb, L], ids))
+    out.append(("ids_missing_int_tensor", [dict(emb, inputs=["ids"])], ids))
+    out.append(("ids_float_input_not_in_float_store", [emb, dict(name="g", type="GELU", inputs=["x"])], ids))
+    out.append(("ids_no_x_result", [emb], ids))
+    out.append(("ids_add_one_input", [emb, dict(name="a", type="Add", inputs=["h"], output="x")], ids))
+    out.append(("ids_table_too_small", [dict(emb, weights=table[:19], output="x")], ids))
+    return out
+
+
 def checkpoint_layers():
     """The layers of the SafeTensors fixture tests/golden/ref_checkpoint.safetensors
     (written by the reference's save_checkpoint from these weights)."""

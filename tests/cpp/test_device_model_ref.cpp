@@ -149,6 +149,50 @@ void weight_block_and_backward(mimir_hip::Context& c) {
     CHECK(close_sum(dt.getLastInputGradient(), ref_gin, 8.0f));
 }
 
+// Model::forwardPass(const std::vector<int>&, training) through the
+// reference Layer list: a gather, LayerNorm and Add graph in both modes, and
+// the int path's refusal of a Multiply (Model.cpp:1311-1319).
+void int_ids_forward(mimir_hip::Context& c) {
+    const int vocab = 10, dim = 8;
+    Model m;
+    m.push("tok", "Embedding", vocab * dim);
+    m.push("ln", "LayerNorm", 2 * dim);
+    m.push("res", "Add", 0);
+    auto& layers = m.getMutableLayers();
+    layers[0].inputs = {"x"};
+    layers[0].output = "h";
+    layers[0].vocab_size = vocab;
+    layers[0].embed_dim = dim;
+    layers[0].padding_idx = 2;
+    layers[1].inputs = {"h"};
+    layers[1].output = "n";
+    layers[1].in_features = dim;
+    layers[2].inputs = {"n", "h"};
+    layers[2].output = "x";
+    m.allocateParams();
+    float* w = layers[0].getWeights();
+    for (int i = 0; i < vocab * dim; ++i) w[i] = std::sin(0.1f * static_cast<float>(i));
+    float* g = layers[1].getWeights();
+    for (int i = 0; i < dim; ++i) {
+        g[i] = 1.0f + 0.1f * static_cast<float>(i);
+        g[dim + i] = 0.05f * static_cast<float>(i);
+    }
+    const std::vector<int> ids = {3, 2, 9, -1, 10, 3, 0};
+    mimir_hip::DeviceModel<Layer> dm(c, m.getLayers());
+    for (bool training : {false, true}) {
+        const std::vector<float> want = m.forwardPass(ids, training);
+        CHECK(close(dm.forwardPass(ids, training), want));
+    }
+    m.push("bad", "Multiply", 0);
+    auto& l2 = m.getMutableLayers();
+    l2[3].inputs = {"x", "x"};
+    mimir_hip::DeviceModel<Layer> dbad(c, m.getLayers());
+    bool ref_threw = false, dev_threw = false;
+    try { m.forwardPass(ids, false); } catch (const std::exception&) { ref_threw = true; }
+    try { dbad.forwardPass(ids, false); } catch (const std::exception&) { dev_threw = true; }
+    CHECK(ref_threw && dev_threw);
+}
+
 }  // namespace
 
 int main() {
@@ -156,6 +200,7 @@ int main() {
         auto& c = mimir_hip::Context::instance();
         residual_merge_kat(c);
         weight_block_and_backward(c);
+        int_ids_forward(c);
     } catch (const std::exception& e) {
         std::fprintf(stderr, "FAIL: exception %s\n", e.what());
         return 1;

@@ -107,9 +107,10 @@ def test_store_merge_backward_matches_reference(ctx, graph):
     graph = M.DeviceGraph(ctx, layers)
     store = M.Store(ctx)
     try:
-        grads, gin = store.train_step(graph, fin, iin, lg)
-        # A repeated step reuses every buffer and gives the same input gradient.
-        _, gin2 = store.train_step(graph, fin, iin, lg)
+        _, gin = store.train_step(graph, fin, iin, lg)
+        # A repeated step reuses every buffer, gives the same input gradient
+        # and adds the same parameter gradients again.
+        grads, gin2 = store.train_step(graph, fin, iin, lg)
     finally:
         store.close()
         graph.close()
