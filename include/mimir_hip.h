@@ -249,6 +249,18 @@ int mimir_rope_fwd(mimir_ctx* ctx, const float* q, float* q_out, int64_t q_heads
  * dx may alias dy. */
 int mimir_layernorm_bwd(mimir_ctx* ctx, const float* x, const float* dy, const float* gamma, float* dx,
                         float* dgamma, float* dbeta, int64_t groups, int64_t n, float eps, int accumulate);
+/* mimir_layernorm_bwd that allocates nothing.  No counterpart in the
+ * reference: for callers that cannot allocate device memory (code under HIP
+ * graph capture, tight serving and training loops, harnesses that forbid
+ * hipMalloc).  Same arguments, kernels and bits as mimir_layernorm_bwd, but
+ * its scratch (the dgamma / dbeta partial-sum slots, the long-row partials)
+ * is a fixed 32 MiB device array that the library reserves per GPU for the
+ * life of the process.  A call that needs more (e.g. width 4096 takes 17.3 MB
+ * with dgamma, a width above ~7900 takes more than 32 MiB) returns EINVAL
+ * before any launch.  Every call on one GPU shares that array: calls that
+ * overlap on one GPU (other streams, other threads) race. */
+int mimir_layernorm_bwd_noalloc(mimir_ctx* ctx, const float* x, const float* dy, const float* gamma, float* dx,
+                                float* dgamma, float* dbeta, int64_t groups, int64_t n, float eps, int accumulate);
 
 /* GELU branch, Model.cpp:9026-9051 (tanh approximation): dx (+)= dy * gelu'(x). */
 int mimir_gelu_bwd(mimir_ctx* ctx, const float* x, const float* dy, float* dx, int64_t n, int accumulate);

@@ -36,6 +36,7 @@
 #include "ids.hpp"
 
 #include <math.h>
+#include <mutex>
 
 #include <rocprim/device/device_radix_sort.hpp>
 #include <rocprim/iterator/counting_iterator.hpp>
@@ -1000,7 +1001,7 @@ __global__ __launch_bounds__(kBlock) void ln_bwd_params_part(LnBwdArgs a, int64_
 // kernel with a.part set.
 template <class Run>
 int ln_bwd_persistent(mimir_ctx* ctx, LnBwdArgs a, int64_t groups, float* dgamma, float* dbeta, const char* name,
-                      Run run) {
+                      const ScratchSpan* fixed, Run run) {
     int64_t grid = ctx->tune.lnbwd_grid > 0 ? ctx->tune.lnbwd_grid : 512;
     if (grid > groups) grid = groups;
     const int64_t nslots = grid;
@@ -1008,7 +1009,7 @@ int ln_bwd_persistent(mimir_ctx* ctx, LnBwdArgs a, int64_t groups, float* dgamma
     if (dgamma) {  // partial slots, then room for the second level of their sum
         void* s = nullptr;
         const size_t bytes = sizeof(float) * static_cast<size_t>((nslots + kGroups) * 2 * a.cols);
-        if (int st = ensure_scratch(ctx, bytes, &s)) return st;
+        if (int st = get_scratch(ctx, fixed, bytes, &s)) return st;
         a.part = static_cast<float*>(s);
         tmp = a.part + nslots * 2 * a.cols;
     }
@@ -1021,9 +1022,9 @@ int ln_bwd_persistent(mimir_ctx* ctx, LnBwdArgs a, int64_t groups, float* dgamma
 }
 
 template <int TPR, int VPT, int BS>
-int launch_ln_bwd_vec(mimir_ctx* ctx, LnBwdArgs a, float* dgamma, float* dbeta) {
+int launch_ln_bwd_vec(mimir_ctx* ctx, LnBwdArgs a, float* dgamma, float* dbeta, const ScratchSpan* fixed) {
     constexpr int RPB = BS / TPR;
-    return ln_bwd_persistent(ctx, a, (a.rows + RPB - 1) / RPB, dgamma, dbeta, "ln_bwd_vec",
+    return ln_bwd_persistent(ctx, a, (a.rows + RPB - 1) / RPB, dgamma, dbeta, "ln_bwd_vec", fixed,
                              [ctx](unsigned grid, const LnBwdArgs& la) {
                                  if (ctx->keep_outputs) ln_bwd_vec<TPR, VPT, BS, true><<<grid, BS, 0, ctx->stream>>>(la);
                                  else ln_bwd_vec<TPR, VPT, BS, false><<<grid, BS, 0, ctx->stream>>>(la);
@@ -1031,9 +1032,9 @@ int launch_ln_bwd_vec(mimir_ctx* ctx, LnBwdArgs a, float* dgamma, float* dbeta) 
 }
 
 template <int TPR, int VPT>
-int launch_ln_bwd_scalar(mimir_ctx* ctx, LnBwdArgs a, float* dgamma, float* dbeta) {
+int launch_ln_bwd_scalar(mimir_ctx* ctx, LnBwdArgs a, float* dgamma, float* dbeta, const ScratchSpan* fixed) {
     constexpr int RPB = kBlock / TPR;
-    return ln_bwd_persistent(ctx, a, (a.rows + RPB - 1) / RPB, dgamma, dbeta, "ln_bwd_scalar",
+    return ln_bwd_persistent(ctx, a, (a.rows + RPB - 1) / RPB, dgamma, dbeta, "ln_bwd_scalar", fixed,
                              [ctx](unsigned grid, const LnBwdArgs& la) {
                                  if (ctx->keep_outputs)
                                      ln_bwd_scalar<TPR, VPT, true><<<grid, kBlock, 0, ctx->stream>>>(la);
@@ -1041,7 +1042,7 @@ int launch_ln_bwd_scalar(mimir_ctx* ctx, LnBwdArgs a, float* dgamma, float* dbet
                              });
 }
 
-int ln_bwd_generic_run(mimir_ctx* ctx, LnBwdArgs a, float* dgamma, float* dbeta) {
+int ln_bwd_generic_run(mimir_ctx* ctx, LnBwdArgs a, float* dgamma, float* dbeta, const ScratchSpan* fixed) {
     if (a.rows > 0x7fffffffLL)
         return fail(ctx, MIMIR_EINVAL, "LayerNorm backward: %lld rows exceed the grid limit", (long long)a.rows);
     const int64_t cblocks = (a.cols + kBlock - 1) / kBlock;
@@ -1056,7 +1057,7 @@ int ln_bwd_generic_run(mimir_ctx* ctx, LnBwdArgs a, float* dgamma, float* dbeta)
     }
     void* s = nullptr;
     const size_t bytes = sizeof(float) * static_cast<size_t>(2 * a.rows + nchunks * 2 * a.cols);
-    if (int st = ensure_scratch(ctx, bytes, &s)) return st;
+    if (int st = get_scratch(ctx, fixed, bytes, &s)) return st;
     a.stats = static_cast<float*>(s);
     a.part = a.stats + 2 * a.rows;
     const unsigned rows = static_cast<unsigned>(a.rows);
@@ -1349,12 +1350,11 @@ int embed_bwd(mimir_ctx* ctx, const void* ids, int64_t n_ids, const float* dy, f
     return launched(ctx, "embed_bwd_rows_scalar");
 }
 
-}  // namespace
-
-extern "C" {
-
-int mimir_layernorm_bwd(mimir_ctx* ctx, const float* x, const float* dy, const float* gamma, float* dx,
-                        float* dgamma, float* dbeta, int64_t groups, int64_t n, float eps, int accumulate) {
+// Model.cpp:7719-7821 (the LayerNorm branch of backwardPass): dispatch over
+// the kernels by row width and alignment.  Scratch comes from `fixed` when
+// given (the no-allocation entry point), else from the context.
+int layernorm_bwd(mimir_ctx* ctx, const float* x, const float* dy, const float* gamma, float* dx, float* dgamma,
+                  float* dbeta, int64_t groups, int64_t n, float eps, int accumulate, const ScratchSpan* fixed) {
     if (!ctx) return MIMIR_EINVAL;
     MIMIR_REQUIRE(ctx, n > 0 && groups >= 0, "LayerNorm backward: invalid shape (groups=%lld, n=%lld)",
                   (long long)groups, (long long)n);
@@ -1373,7 +1373,7 @@ int mimir_layernorm_bwd(mimir_ctx* ctx, const float* x, const float* dy, const f
         float* tmp = nullptr;
         int64_t nslots = 0;
         if (int st = longrow_ln_bwd(ctx, x, dy, gamma, dx, dgamma, dbeta, groups, n, eps, accumulate, &slots,
-                                    &nslots, &tmp))
+                                    &nslots, &tmp, fixed))
             return st;
         if (!slots) return MIMIR_OK;
         return launch_sum_slots(ctx, slots, nslots, 2 * n, dbeta ? 2 * n : n, dgamma, dbeta, n, true, tmp);
@@ -1382,15 +1382,61 @@ int mimir_layernorm_bwd(mimir_ctx* ctx, const float* x, const float* dy, const f
         const RowShape over = ctx->tune.lnbwd;
         const RowShape s = shape_fits(over, c4) ? over : default_norm_shape(c4);
 #define MIMIR_LNBWD_CASE(T, V, B) \
-        if (s.tpr == T && s.vpt == V && s.bs == B) return launch_ln_bwd_vec<T, V, B>(ctx, a, dgamma, dbeta);
+        if (s.tpr == T && s.vpt == V && s.bs == B) return launch_ln_bwd_vec<T, V, B>(ctx, a, dgamma, dbeta, fixed);
         MIMIR_ROW_SHAPES(MIMIR_LNBWD_CASE)
 #undef MIMIR_LNBWD_CASE
     }
-    if (!vec && n <= 256) return launch_ln_bwd_scalar<64, 4>(ctx, a, dgamma, dbeta);
-    if (!vec && n <= 1024) return launch_ln_bwd_scalar<64, 16>(ctx, a, dgamma, dbeta);
-    if (!vec && n <= 2048) return launch_ln_bwd_scalar<128, 16>(ctx, a, dgamma, dbeta);
-    if (!vec && n <= 4096) return launch_ln_bwd_scalar<256, 16>(ctx, a, dgamma, dbeta);
-    return ln_bwd_generic_run(ctx, a, dgamma, dbeta);
+    if (!vec && n <= 256) return launch_ln_bwd_scalar<64, 4>(ctx, a, dgamma, dbeta, fixed);
+    if (!vec && n <= 1024) return launch_ln_bwd_scalar<64, 16>(ctx, a, dgamma, dbeta, fixed);
+    if (!vec && n <= 2048) return launch_ln_bwd_scalar<128, 16>(ctx, a, dgamma, dbeta, fixed);
+    if (!vec && n <= 4096) return launch_ln_bwd_scalar<256, 16>(ctx, a, dgamma, dbeta, fixed);
+    return ln_bwd_generic_run(ctx, a, dgamma, dbeta, fixed);
+}
+
+// The no-allocation entry point's scratch: one array per GPU, reserved when
+// the code object loads and held until the process ends.  Its name is a
+// host-side stand-in in host code; the device address comes from
+// hipGetSymbolAddress, once per device (noalloc_scratch_init).  The LayerNorm
+// backward writes every slot it later reads, so nothing in it has to start
+// at zero; calls that overlap on one GPU share it and race.
+constexpr size_t kNoAllocScratchBytes = size_t(32) << 20;
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_noalloc_mutex;
+void* g_noalloc_ptr[kMaxDevices] = {};
+
+}  // namespace
+
+// The device address of this GPU's scratch array (ctx->device current).
+int mimir::noalloc_scratch_init(mimir_ctx* ctx) {
+    if (ctx->device < 0 || ctx->device >= kMaxDevices)
+        return fail(ctx, MIMIR_EDEVICE, "device %d: no scratch slot for it", ctx->device);
+    std::lock_guard<std::mutex> lock(g_noalloc_mutex);
+    if (!g_noalloc_ptr[ctx->device]) {
+        void* ptr = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !ptr) return hip_fail(ctx, e, "hipGetSymbolAddress(scratch)");
+        g_noalloc_ptr[ctx->device] = ptr;
+    }
+    ctx->noalloc_scratch = g_noalloc_ptr[ctx->device];
+    return MIMIR_OK;
+}
+
+extern "C" {
+
+int mimir_layernorm_bwd(mimir_ctx* ctx, const float* x, const float* dy, const float* gamma, float* dx,
+                        float* dgamma, float* dbeta, int64_t groups, int64_t n, float eps, int accumulate) {
+    return layernorm_bwd(ctx, x, dy, gamma, dx, dgamma, dbeta, groups, n, eps, accumulate, nullptr);
+}
+
+int mimir_layernorm_bwd_noalloc(mimir_ctx* ctx, const float* x, const float* dy, const float* gamma, float* dx,
+                                float* dgamma, float* dbeta, int64_t groups, int64_t n, float eps, int accumulate) {
+    if (!ctx) return MIMIR_EINVAL;
+    if (!ctx->noalloc_scratch)
+        return fail(ctx, MIMIR_EDEVICE, "LayerNorm backward (no allocation): the device scratch is not set up");
+    const ScratchSpan fixed{ctx->noalloc_scratch, kNoAllocScratchBytes};
+    return layernorm_bwd(ctx, x, dy, gamma, dx, dgamma, dbeta, groups, n, eps, accumulate, &fixed);
 }
 
 int mimir_gelu_bwd(mimir_ctx* ctx, const float* x, const float* dy, float* dx, int64_t n, int accumulate) {

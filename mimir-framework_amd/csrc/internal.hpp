@@ -27,6 +27,9 @@ struct mimir_ctx {
     // (longrow.hip); grows on demand, reused in stream order.
     void* scratch = nullptr;
     size_t scratch_bytes = 0;
+    // Device address of this GPU's fixed scratch array (backward.hip), for
+    // the entry point that allocates nothing; set at context creation.
+    void* noalloc_scratch = nullptr;
 };
 
 struct mimir_event {
@@ -86,6 +89,26 @@ inline bool grid_for(int64_t units, int64_t per_block, unsigned* blocks) {
 // the work already enqueued, which may still read the old buffer.
 int ensure_scratch(mimir_ctx* ctx, size_t bytes, void** out);
 
+// Look up this context's device address of the no-allocation scratch array
+// (backward.hip); called once per context, with its device current.
+int noalloc_scratch_init(mimir_ctx* ctx);
+
+// Scratch for one call: a fixed span (the no-allocation entry point's device
+// array) or, when `fixed` is null, the context's growable scratch.  A fixed
+// span never grows: a call needing more is refused before any launch.
+struct ScratchSpan {
+    void* ptr;
+    size_t bytes;
+};
+inline int get_scratch(mimir_ctx* ctx, const ScratchSpan* fixed, size_t bytes, void** out) {
+    if (!fixed) return ensure_scratch(ctx, bytes, out);
+    if (bytes > fixed->bytes)
+        return fail(ctx, MIMIR_EINVAL, "this call needs %zu bytes of scratch; the no-allocation entry point has %zu",
+                    bytes, fixed->bytes);
+    *out = fixed->ptr;
+    return MIMIR_OK;
+}
+
 // Rows too long for one workgroup's registers: split each row over many
 // workgroups (longrow.hip).  `kind`: 0 LayerNorm, 1 RMSNorm,
 // 2 add + RMSNorm; softmax `mode` as in mimir_softmax_fwd.
@@ -105,7 +128,7 @@ constexpr int kSlotGroups = 16;
 constexpr int64_t kLongBwdRows = 16;
 int longrow_ln_bwd(mimir_ctx* ctx, const float* x, const float* dy, const float* gamma, float* dx, float* dgamma,
                    float* dbeta, int64_t rows, int64_t cols, float eps, int accumulate, float** slots,
-                   int64_t* nslots, float** tmp);
+                   int64_t* nslots, float** tmp, const ScratchSpan* fixed = nullptr);
 
 // Embedding gather with an id mode (gather.hip); used by the C ABI and the
 // device-resident runtime (store.hip).

@@ -521,7 +521,7 @@ __global__ __launch_bounds__(kBlock) void lr_bwd_apply(LongBwdArgs a) {
 
 int mimir::longrow_ln_bwd(mimir_ctx* ctx, const float* x, const float* dy, const float* gamma, float* dx,
                           float* dgamma, float* dbeta, int64_t rows, int64_t cols, float eps, int accumulate,
-                          float** slots, int64_t* nslots, float** tmp) {
+                          float** slots, int64_t* nslots, float** tmp, const ScratchSpan* fixed) {
     const int64_t groups = (rows + kLongBwdRows - 1) / kLongBwdRows;
     const bool use_slots = groups > 1 && dgamma;
     *slots = nullptr;
@@ -538,7 +538,7 @@ int mimir::longrow_ln_bwd(mimir_ctx* ctx, const float* x, const float* dy, const
     const size_t slot_bytes = use_slots ? sizeof(float) * static_cast<size_t>(groups) * 2 * cols : 0;
     const size_t tmp_bytes = use_slots ? sizeof(float) * static_cast<size_t>(kSlotGroups) * 2 * cols : 0;
     void* s = nullptr;
-    if (int st = ensure_scratch(ctx, head + slot_bytes + tmp_bytes, &s)) return st;
+    if (int st = get_scratch(ctx, fixed, head + slot_bytes + tmp_bytes, &s)) return st;
     a.partial = static_cast<float*>(s);
     a.stats = a.partial + 2 * rows * a.nchunks;
     float* slot_base = use_slots ? reinterpret_cast<float*>(static_cast<char*>(s) + head) : nullptr;

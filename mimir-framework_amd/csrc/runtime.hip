@@ -93,6 +93,11 @@ int mimir_ctx_create(int device, mimir_ctx** out) {
         return MIMIR_EDEVICE;
     }
     ctx->stream = ctx->own_stream;
+    if (int st = noalloc_scratch_init(ctx)) {
+        (void)hipStreamDestroy(ctx->own_stream);
+        delete ctx;
+        return st;
+    }
     *out = ctx;
     return MIMIR_OK;
 }

@@ -107,6 +107,7 @@ SIGNATURES = {
     "mimir_rope_fwd": (c_int, [_P, _P, _P, c_int64, _P, _P, c_int64, c_int64, c_int64, c_int64,
                                c_int64, _P, _P, c_int64]),
     "mimir_layernorm_bwd": (c_int, [_P, _P, _P, _P, _P, _P, _P, c_int64, c_int64, c_float, c_int]),
+    "mimir_layernorm_bwd_noalloc": (c_int, [_P, _P, _P, _P, _P, _P, _P, c_int64, c_int64, c_float, c_int]),
     "mimir_gelu_bwd": (c_int, [_P, _P, _P, _P, c_int64, c_int]),
     "mimir_silu_bwd": (c_int, [_P, _P, _P, _P, c_int64, c_int]),
     "mimir_mul_bwd": (c_int, [_P, _P, _P, _P, _P, _P, c_int64, c_int, c_int]),
