@@ -27,10 +27,13 @@
 //                            alignment
 //   embed_bwd_*              scatter-add of dy rows into the gradient table:
 //                            (id, token) pairs are sorted by id (stable radix
-//                            sort), then one workgroup per distinct id adds
-//                            its tokens' rows in token order -- the same
-//                            sequence of float adds as the reference, so the
-//                            result is bit-identical and deterministic.
+//                            sort); an id with fewer than 32 tokens has its
+//                            rows added in token order by one workgroup --
+//                            the reference's sequence of float adds, bit for
+//                            bit -- and a more frequent id's rows are summed
+//                            in 32-token segments in parallel, then the
+//                            segments in order (deterministic, the
+//                            reference's sum to float32 rounding).
 #include "common.hpp"
 #include "internal.hpp"
 #include "ids.hpp"
@@ -1110,13 +1113,18 @@ __device__ __forceinline__ int64_t run_end(const uint32_t* keys, int64_t i, int6
     }
 }
 
-// Runs of at least kLongRun tokens (a frequent id) go to embed_bwd_long_runs,
-// which spreads each over kLongSlices one-wave workgroups by columns; a wave
-// then has few enough lanes to keep kLongBatch tokens of loads in flight.
-// Shorter runs stay with embed_bwd_rows_vec, one token's loads at a time.
+// Runs of at least kLongRun tokens (a frequent id) are summed in two levels
+// instead of one token after another: the run's positions are cut at the
+// multiples of kLongRun, embed_bwd_seg_partial sums each segment's dy rows
+// (token order) into a slot of partial rows, all segments at once, and
+// embed_bwd_seg_combine adds the run's slots in order onto the gradient row.
+// The result is deterministic; it is the reference's sequential sum
+// regrouped, so it agrees with it to the rounding of a float32 sum (the
+// path's tolerance for sums), not bit for bit.  Shorter runs stay with
+// embed_bwd_rows_vec, which adds in token order (bit-exact).
 constexpr int kLongRun = 32;
 constexpr int kLongSlices = 16;
-constexpr int kLongBatch = 32;
+constexpr int kLongBatch = 16;
 
 // The end of the run of `id` in the sorted keys, given a position j inside
 // it: the first position after j whose key differs, or n.  Each step the 64
@@ -1141,86 +1149,129 @@ __device__ __forceinline__ int64_t run_end_search(const uint32_t* keys, int64_t 
     return lo;
 }
 
-// Long runs: workgroup (m, o) takes the run holding sorted position
-// m*kLongRun if that is the run's first multiple of kLongRun (so each long
-// run is taken once), and its o-th slice of 16-byte columns.  Each column
-// still adds the run's dy rows in token order onto the gradient row, so the
-// sums are the same bits as one workgroup walking the run.
-// Few of these one-wave workgroups do work (most exit at once), each on its
-// own CU: two waves per SIMD is the occupancy to plan for, and a scheduling
-// barrier keeps all kLongBatch loads of a batch in flight (without it the
-// compiler may trade most of them for registers).
-__global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(1, 2))) void embed_bwd_long_runs(
-    const uint32_t* keys, const uint32_t* toks, int64_t n, uint32_t vocab, const float* dy, float* grad,
-    int64_t dim4) {
-    const int64_t p = static_cast<int64_t>(blockIdx.x) * kLongRun;
+// The long run through sorted position p = m * kLongRun, seen from p: its
+// key, whether p is the run's first multiple of kLongRun (`first`), its head
+// (valid when `first`) and end.  `is_long` when it has kLongRun tokens or
+// more.  One ballot over positions p - kLongRun + 1 .. p finds the head of a
+// run that starts there; a run through p - kLongRun as well is long.  Must
+// be reached by all 64 lanes of the wave.
+struct LongRun {
+    uint32_t id;
+    bool first;
+    bool is_long;
+    int64_t head;
+    int64_t end;
+};
+__device__ __forceinline__ LongRun long_run_at(const uint32_t* keys, int64_t p, int64_t n, uint32_t vocab) {
+    LongRun r{keys[p], false, false, p, p + 1};
+    const uint32_t before = p >= kLongRun ? keys[p - kLongRun] : ~0u;  // loaded with the key: one round trip
+    if (r.id >= vocab) return r;
+    r.first = before != r.id;
+    const int lane = threadIdx.x & (kWave - 1);
+    if (r.first) {
+        const int64_t q = p - (kLongRun - 1) + lane;
+        const unsigned long long m = __ballot(lane < kLongRun && q >= 0 && keys[q] == r.id);
+        r.head = p - (kLongRun - 1) + __builtin_ctzll(m);  // lane kLongRun - 1 (position p) always matches
+    }
+    r.end = run_end_search(keys, p, n, r.id);
+    r.is_long = !r.first || r.end - r.head >= kLongRun;
+    return r;
+}
+
+// First level: workgroup (m, o) of position p = m * kLongRun in a long run
+// sums the dy rows of its segment, positions p .. min(p + kLongRun, end) - 1
+// (and head .. p - 1 before them when p is the run's first multiple), in
+// token order, into partial slot m, for its o-th block of kSegCols 16-byte
+// columns (one per thread).  Each thread requests kSegRows tokens' rows
+// before adding the first.
+constexpr int kSegCols = 256;
+constexpr int kSegRows = 16;
+__global__ __launch_bounds__(kSegCols) void embed_bwd_seg_partial(const uint32_t* keys, const uint32_t* toks,
+                                                                  int64_t n, uint32_t vocab, const float* dy,
+                                                                  float* part, int64_t dim4) {
+    const int64_t m = blockIdx.x;
+    const int64_t p = m * kLongRun;
     if (p >= n) return;
-    const uint32_t id = keys[p];
-    const uint32_t before = p >= kLongRun ? keys[p - kLongRun] : ~0u;  // loaded with id: one round trip
-    if (id >= vocab || before == id) return;  // not the run's first multiple of kLongRun
-    // One ballot over positions p - 15 .. p + 15 (lanes 0..30): the head is
-    // the first of them holding id (it is among p - 15 .. p), and the run is
-    // long when position head + 15 (at most p + 15) still holds it.
-    const int lane = threadIdx.x;
-    const int64_t slice = blockIdx.y;
-    const int64_t q = p - (kLongRun - 1) + lane;
-    const unsigned long long m = __ballot(lane < 2 * kLongRun - 1 && q >= 0 && q < n && keys[q] == id);
-    const int first = __builtin_ctzll(m);
-    if (first + kLongRun - 1 >= 2 * kLongRun - 1 || !((m >> (first + kLongRun - 1)) & 1ull)) return;
-    const int64_t head = p - (kLongRun - 1) + first;
-    const int64_t end = run_end_search(keys, head + kLongRun - 1, n, id);
+    const LongRun r = long_run_at(keys, p, n, vocab);
+    if (!r.is_long) return;
+    const int64_t c = static_cast<int64_t>(blockIdx.y) * kSegCols + threadIdx.x;
+    if (c >= dim4) return;  // after the ballots of long_run_at
+    const int64_t s0 = r.first ? r.head : p;
+    const int64_t s1 = p + kLongRun < r.end ? p + kLongRun : r.end;
+    const f4* src = reinterpret_cast<const f4*>(dy);
+    f4 acc;
+    bool started = false;
+    for (int64_t j = s0; j < s1; j += kSegRows) {
+        f4 v[kSegRows];
+#pragma unroll
+        for (int u = 0; u < kSegRows; ++u)
+            if (j + u < s1) v[u] = __builtin_nontemporal_load(src + static_cast<int64_t>(toks[j + u]) * dim4 + c);
+        __builtin_amdgcn_sched_barrier(0);  // the batch's loads are all issued before the first add
+#pragma unroll
+        for (int u = 0; u < kSegRows; ++u) {
+            if (j + u < s1) {
+                acc = started ? acc + v[u] : v[u];
+                started = true;
+            }
+        }
+    }
+    reinterpret_cast<f4*>(part)[m * dim4 + c] = acc;
+}
+
+// Second level: the workgroup at the run's first multiple of kLongRun adds
+// the run's partial slots, in order, onto the id's gradient row; each of its
+// kLongSlices waves takes a slice of the 16-byte columns and keeps
+// kLongBatch slots' loads in flight.
+__global__ __launch_bounds__(kWave * kLongSlices) void embed_bwd_seg_combine(
+    const uint32_t* keys, int64_t n, uint32_t vocab, const float* part, float* grad, int64_t dim4) {
+    const int64_t m0 = blockIdx.x;
+    const int64_t p = m0 * kLongRun;
+    if (p >= n) return;
+    const LongRun r = long_run_at(keys, p, n, vocab);
+    if (!r.first || !r.is_long) return;
+    const int64_t m1 = (r.end - 1) / kLongRun + 1;  // slots m0 .. m1 - 1
+    const int lane = threadIdx.x & (kWave - 1);
+    const int64_t slice = threadIdx.x / kWave;
     const int64_t w = (dim4 + kLongSlices - 1) / kLongSlices;
     const int64_t c1 = (slice + 1) * w < dim4 ? (slice + 1) * w : dim4;
-    const f4* src = reinterpret_cast<const f4*>(dy);
-    f4* g = reinterpret_cast<f4*>(grad) + static_cast<int64_t>(id) * dim4;
+    const f4* src = reinterpret_cast<const f4*>(part);
+    f4* g = reinterpret_cast<f4*>(grad) + static_cast<int64_t>(r.id) * dim4;
     for (int64_t c = slice * w + lane; c < c1; c += kWave) {
         f4 acc = __builtin_nontemporal_load(g + c);
-        int64_t j = head;
-        // The token indices of a batch are loaded while the previous batch's
-        // rows are in flight, so a batch costs one memory round trip.
-        uint32_t t[kLongBatch];
-        if (j + kLongBatch <= end) {
-#pragma unroll
-            for (int u = 0; u < kLongBatch; ++u) t[u] = toks[j + u];
-        }
-        for (; j + kLongBatch <= end; j += kLongBatch) {
+        int64_t j = m0;
+        for (; j + kLongBatch <= m1; j += kLongBatch) {
             f4 v[kLongBatch];
 #pragma unroll
-            for (int u = 0; u < kLongBatch; ++u)
-                v[u] = __builtin_nontemporal_load(src + static_cast<int64_t>(t[u]) * dim4 + c);
-            if (j + 2 * kLongBatch <= end) {
-#pragma unroll
-                for (int u = 0; u < kLongBatch; ++u) t[u] = toks[j + kLongBatch + u];
-            }
-            __builtin_amdgcn_sched_barrier(0);  // every load of the batch is issued before the first add
+            for (int u = 0; u < kLongBatch; ++u) v[u] = src[(j + u) * dim4 + c];
+            __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (int u = 0; u < kLongBatch; ++u) acc += v[u];
         }
-        for (; j < end; ++j) acc += __builtin_nontemporal_load(src + static_cast<int64_t>(toks[j]) * dim4 + c);
+        for (; j < m1; ++j) acc += src[j * dim4 + c];
         __builtin_nontemporal_store(acc, g + c);
     }
 }
 
-// One workgroup per sorted position; the first position of each id's run
-// adds the run's dy rows (token order, the sort is stable) onto the id's
-// gradient row.  Non-head positions leave at once.  Each thread owns CPT
-// 16-byte columns TPT apart and issues all of a token's loads together; the
-// first token's row and the gradient row are requested before the run's
-// end is known, so a run of one (the common case) waits for two memory
-// round trips, not four.
-// With skip_long, runs of kLongRun tokens or more are left to
-// embed_bwd_long_runs (sorted keys: the run is that long when the key
-// kLongRun - 1 positions on is still the same).
+// One workgroup per sorted position.  The first position of each id's run
+// of fewer than kLongRun tokens (every run without `long_runs`) adds the
+// run's dy rows (token order, the sort is stable) onto the id's gradient row;
+// every other position leaves at once.  Each thread owns CPT 16-byte columns
+// TPT apart.  The first token's row and the gradient row are requested
+// before the run's end is known, so a run of one (the common case) waits for
+// two memory round trips; the rest of a run is loaded kRunBatch tokens at a
+// time, then added in token order.  Most workgroups leave at once, so the
+// kernel is kept small in registers: two 1024-thread workgroups fit a CU.
+constexpr int kRunBatch = 4;
 template <int TPT, int CPT>
 __global__ __launch_bounds__(TPT) void embed_bwd_rows_vec(const uint32_t* keys, const uint32_t* toks, int64_t n,
-                                                          uint32_t vocab, const float* dy, float* grad,
-                                                          int64_t dim4, int skip_long) {
+                                                          uint32_t vocab, const float* dy, float* grad, int64_t dim4,
+                                                          int long_runs) {
     const int64_t i = blockIdx.x;
     const uint32_t id = keys[i];
     const uint32_t t0 = toks[i];
-    if (id >= vocab || (i > 0 && keys[i - 1] == id)) return;
-    f4* g = reinterpret_cast<f4*>(grad) + static_cast<int64_t>(id) * dim4;
+    if (id >= vocab || (i > 0 && keys[i - 1] == id)) return;  // not a run's head
     const f4* src = reinterpret_cast<const f4*>(dy);
+    f4* g = reinterpret_cast<f4*>(grad) + static_cast<int64_t>(id) * dim4;
     f4 acc[CPT], v[CPT];
     auto load_group = [&](int64_t c0) {
 #pragma unroll
@@ -1234,22 +1285,33 @@ __global__ __launch_bounds__(TPT) void embed_bwd_rows_vec(const uint32_t* keys, 
     };
     int64_t c0 = threadIdx.x;
     load_group(c0);
-    if (skip_long && i + kLongRun <= n && keys[i + kLongRun - 1] == id) return;  // the same for the workgroup
+    if (long_runs && i + kLongRun <= n && keys[i + kLongRun - 1] == id) return;  // a long run: segments
     // Every lane of the wave takes part in the ballots of run_end.
     const int64_t end = run_end(keys, i, n, id);
     while (c0 < dim4) {
 #pragma unroll
         for (int k = 0; k < CPT; ++k) acc[k] += v[k];
-        int64_t j = i + 1;
-        for (; j < end; ++j) {
-            const int64_t row = static_cast<int64_t>(toks[j]) * dim4;
+        for (int64_t j = i + 1; j < end; j += kRunBatch) {
+            f4 w[kRunBatch][CPT];
 #pragma unroll
-            for (int k = 0; k < CPT; ++k) {
-                const int64_t c = c0 + static_cast<int64_t>(k) * TPT;
-                if (c < dim4) v[k] = __builtin_nontemporal_load(src + row + c);
+            for (int u = 0; u < kRunBatch; ++u) {
+                if (j + u < end) {
+                    const int64_t row = static_cast<int64_t>(toks[j + u]) * dim4;
+#pragma unroll
+                    for (int k = 0; k < CPT; ++k) {
+                        const int64_t c = c0 + static_cast<int64_t>(k) * TPT;
+                        if (c < dim4) w[u][k] = __builtin_nontemporal_load(src + row + c);
+                    }
+                }
             }
+            __builtin_amdgcn_sched_barrier(0);  // the batch's loads are all issued before the first add
 #pragma unroll
-            for (int k = 0; k < CPT; ++k) acc[k] += v[k];
+            for (int u = 0; u < kRunBatch; ++u) {
+                if (j + u < end) {
+#pragma unroll
+                    for (int k = 0; k < CPT; ++k) acc[k] += w[u][k];
+                }
+            }
         }
 #pragma unroll
         for (int k = 0; k < CPT; ++k) {
@@ -1315,35 +1377,44 @@ int embed_bwd(mimir_ctx* ctx, const void* ids, int64_t n_ids, const float* dy, f
     const size_t vbytes = align256(sizeof(uint32_t) * n);
     const bool vec = (dim % 4) == 0 && aligned16(dy) && aligned16(grad);
     const bool long_runs = vec && n_ids >= kLongRun;
+    // Partial rows of the long runs' segments: one slot per kLongRun positions.
+    const int64_t nslots = (n_ids + kLongRun - 1) / kLongRun;
+    const size_t part_bytes = long_runs ? align256(sizeof(float) * static_cast<size_t>(nslots) * dim) : 0;
     void* s = nullptr;
-    if (int st = ensure_scratch(ctx, 2 * vbytes + align256(sort_bytes), &s)) return st;
+    if (int st = ensure_scratch(ctx, 2 * vbytes + part_bytes + align256(sort_bytes), &s)) return st;
     char* base = static_cast<char*>(s);
     uint32_t* skeys = reinterpret_cast<uint32_t*>(base);
     uint32_t* stoks = reinterpret_cast<uint32_t*>(base + vbytes);
-    void* temp = base + 2 * vbytes;
+    float* part = reinterpret_cast<float*>(base + 2 * vbytes);
+    void* temp = base + 2 * vbytes + part_bytes;
     e = rocprim::radix_sort_pairs<EmbedSortConfig>(temp, sort_bytes, keys, skeys, toks, stoks, n, 0u, end_bit,
                                                    ctx->stream);
     if (e != hipSuccess) return hip_fail(ctx, e, "radix_sort_pairs");
     if (vec) {
         const uint32_t v = static_cast<uint32_t>(vocab);
         const int64_t dim4 = dim / 4;
+        const int lr = long_runs ? 1 : 0;
         if (long_runs) {
-            const dim3 lgrid(static_cast<unsigned>((n_ids + kLongRun - 1) / kLongRun), kLongSlices);
-            embed_bwd_long_runs<<<lgrid, kWave, 0, ctx->stream>>>(skeys, stoks, n_ids, v, dy, grad, dim4);
-            if (int st = launched(ctx, "embed_bwd_long_runs")) return st;
+            const dim3 pgrid(static_cast<unsigned>(nslots), static_cast<unsigned>((dim4 + kSegCols - 1) / kSegCols));
+            embed_bwd_seg_partial<<<pgrid, kSegCols, 0, ctx->stream>>>(skeys, stoks, n_ids, v, dy, part, dim4);
+            if (int st = launched(ctx, "embed_bwd_seg_partial")) return st;
         }
-        const int skip = long_runs ? 1 : 0;
         // Measured on MI355X at dim 4096 (MIMIR_TUNE gather=256/512/1024 picks a
         // variant): one 16-byte column per thread in 1024-thread workgroups
         // is fastest, 2-4 columns per thread in smaller ones ~2-4% slower.
         const int tpt = ctx->tune.gather_tpt ? ctx->tune.gather_tpt : (dim4 >= 1024 ? 1024 : dim4 >= 512 ? 512 : 256);
         if (tpt == 256)
-            embed_bwd_rows_vec<256, 4><<<n, 256, 0, ctx->stream>>>(skeys, stoks, n_ids, v, dy, grad, dim4, skip);
+            embed_bwd_rows_vec<256, 4><<<n, 256, 0, ctx->stream>>>(skeys, stoks, n_ids, v, dy, grad, dim4, lr);
         else if (tpt == 512)
-            embed_bwd_rows_vec<512, 2><<<n, 512, 0, ctx->stream>>>(skeys, stoks, n_ids, v, dy, grad, dim4, skip);
+            embed_bwd_rows_vec<512, 2><<<n, 512, 0, ctx->stream>>>(skeys, stoks, n_ids, v, dy, grad, dim4, lr);
         else
-            embed_bwd_rows_vec<1024, 1><<<n, 1024, 0, ctx->stream>>>(skeys, stoks, n_ids, v, dy, grad, dim4, skip);
-        return launched(ctx, "embed_bwd_rows_vec");
+            embed_bwd_rows_vec<1024, 1><<<n, 1024, 0, ctx->stream>>>(skeys, stoks, n_ids, v, dy, grad, dim4, lr);
+        if (int st = launched(ctx, "embed_bwd_rows_vec")) return st;
+        if (!long_runs) return MIMIR_OK;
+        // The long runs' segment partials are complete (stream order): add them.
+        embed_bwd_seg_combine<<<static_cast<unsigned>(nslots), kWave * kLongSlices, 0, ctx->stream>>>(
+            skeys, n_ids, v, part, grad, dim4);
+        return launched(ctx, "embed_bwd_seg_combine");
     }
     embed_bwd_rows_scalar<<<n, kBlock, 0, ctx->stream>>>(skeys, stoks, n_ids, static_cast<uint32_t>(vocab), dy,
                                                          grad, dim);

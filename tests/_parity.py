@@ -139,3 +139,24 @@ def assert_close_normwise(got, ref, what="", rel=REL, abs_=ABS, allow_empty=Fals
         idx = np.flatnonzero(fin)[np.argmax(d)]
         raise AssertionError(f"{what}: {int((d > tol).sum())} of {fin.sum()} elements beyond {tol:.3g}; worst at "
                              f"flat index {idx}: got {g[idx]!r} ref {r[idx]!r} (|d|={abs(g[idx] - r[idx]):.3g})")
+
+
+# The device sums the dy rows of an id with at least this many tokens in
+# 32-token segments, then the segments in order: deterministic, and the
+# reference's token-order sum to float32 rounding.  Rarer ids keep the
+# reference's sequence of adds.
+EMBED_LONG_RUN = 32
+
+
+def assert_embedding_scatter(got, ref, counts, scale, what=""):
+    """Embedding backward (a scatter-add into the gradient table, [vocab, dim]):
+    rows of ids with fewer than EMBED_LONG_RUN tokens must equal ref bit for
+    bit; rows of more frequent ids are float32 sums held to assert_close_sum
+    with `scale` (|gradient row| + the sum of the |dy| rows added)."""
+    got = np.asarray(got, np.float32).reshape(counts.size, -1)
+    ref = np.asarray(ref, np.float32).reshape(counts.size, -1)
+    short = counts < EMBED_LONG_RUN
+    assert_bitexact(got[short], ref[short], what + " (ids with fewer than 32 tokens)", allow_empty=True)
+    if (~short).any():
+        sc = np.asarray(scale, np.float64).reshape(counts.size, -1)
+        assert_close_sum(got[~short], ref[~short], sc[~short], what + " (frequent ids, segment sums)")
