@@ -88,7 +88,11 @@ class LayerOps:
         n = layer.in_features if layer.in_features > 0 else N
         if n <= 0 or N % n:
             raise RuntimeError("LayerNorm: invalid normalized_size")
-        w = _f32(layer.getWeights()) if layer.affine else None
+        # LayerOps.hpp:284-285: affine reads getWeights(), which is null for a
+        # layer without a weight block -- then there is no affine transform.
+        # A block shorter than gamma | beta is read out of bounds by the
+        # reference; it is refused here.
+        w = _f32(layer.getWeights()) if layer.affine and layer.getWeightsSize() > 0 else None
         gamma = beta = None
         if w is not None:
             need = 2 * n if layer.use_bias else n
