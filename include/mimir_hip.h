@@ -226,6 +226,25 @@ int mimir_rope_fwd(mimir_ctx* ctx, const float* q, float* q_out, int64_t q_heads
                    int64_t pos_offset, const float* cos_tab, const float* sin_tab,
                    int64_t table_rows);
 
+/* The attention core with the softmax fused between QK^T and PV: replaces
+ * steps 3-5 of LayerOps::self_attention_forward (LayerOps.hpp:1045-1089,
+ * called by the SelfAttention / MultiHeadAttention layers, Model.cpp:
+ * 5904-5934 and :1291-1310) and the same core of cross_attention_forward
+ * (:1163-1209).  For each of `batch` independent sequences, head h and query i:
+ *   s_j = (Q_i . K_j) * scale, j in [0, kv_len); causal: keys j > i excluded
+ *   out_i = sum_j exp(s_j - max) V_j / (sum_j exp(s_j - max) + 1e-9)
+ * Query i of sequence b is row b*q_len + i of q (stride ld_q floats) and of
+ * out (stride ld_out); key j is row b*kv_len + j of k and v (stride ld_kv),
+ * so q / k / v may be the three column blocks of one fused QKV buffer
+ * (ld = 3 * heads * head_dim).  Head h owns columns [h*head_dim,
+ * (h+1)*head_dim).  The reference's scale is 1.0f / sqrtf(head_dim).
+ * head_dim <= 128.  fp32 throughout (fp32 matrix-core products), no score
+ * matrix in memory.  out must not overlap q, k or v.  kv_len == 0 gives zeros;
+ * batch == 0 or q_len == 0 is a no-op.  Device pointers, stream order. */
+int mimir_attention_fwd(mimir_ctx* ctx, const float* q, int64_t ld_q, const float* k, const float* v,
+                        int64_t ld_kv, float* out, int64_t ld_out, int64_t batch, int64_t q_len,
+                        int64_t kv_len, int64_t heads, int64_t head_dim, float scale, int causal);
+
 /* ---------------------------------------------------------------------------
  * Backward of the path's ops: the branches of the reference's
  * Model::backwardPass (Model.cpp:7305-9153).  Device pointers, stream order.

@@ -1,0 +1,414 @@
+// attention.hip -- the attention core softmax(Q K^T * scale) V with the
+// softmax fused between the two products, fp32 on the gfx950 matrix cores.
+//
+// Reference: the core of LayerOps::self_attention_forward (LayerOps.hpp:
+// 1045-1089) and cross_attention_forward (:1163-1209), which materialise one
+// score row per query (s = dot * scale; causal j > i masked to -1e9; max from
+// -1e30; e = exp(s - max); p = e / (sum + 1e-9); out = sum_j p_j V_j).  Here
+// no score row is ever stored: each workgroup streams K / V tiles through LDS
+// and keeps a running max / sum per query ("online softmax"; Milakov and
+// Gimelshein 2018, as used by FlashAttention, Dao et al. 2022), rescaling its
+// partial output when the max grows, and divides by (sum + 1e-9) at the end.
+//
+// Matrix-core mapping.  v_mfma_f32_32x32x2_f32 computes D[32x32] += A[32x2] *
+// B[2x32]; lane l supplies A[l%32][l/32] and B[l/32][l%32] and receives
+// D[8*(r/4) + 4*(l/32) + r%4][l%32] in accumulator register r (r = 0..15).
+// - Scores: S^T = K Q^T, keys as rows, queries as columns.  A = K (row = the
+//   key, k index = one head dimension), B = Q^T, so lane l owns query l%32 and
+//   16 of the 32 keys of the tile.  The head dimensions are split between the
+//   two lane halves: at step s the half h = l/32 supplies dimension
+//   h*DP/2 + s, so each lane reads four steps of K with one 16-byte LDS read
+//   and holds its query's DP/2 Q values in registers for the whole kernel.
+// - Softmax: per lane over its 16 keys; the running max is shared with the
+//   other half (lane l ^ 32, same query) once per tile.
+// - Output: O^T = V^T P^T.  The accumulator register r of S^T already holds
+//   P^T[key(r, h)][query] in the layout of the B operand when the MFMA's two
+//   k-slots are the keys key(r, 0), key(r, 1), key(r, h) = 8*(r/4) + 4h + r%4,
+//   so the probabilities feed the second product without a lane exchange.
+//   The A operand row i of dimension block db is head dimension (DP/32)*i + db,
+//   so a lane reads its DP/32 values of one V row with one LDS read, and its
+//   output rows come out as DP/32 consecutive dimensions (one 16-byte store
+//   for DP = 128).
+//
+// Workgroup: 4 waves, 32 queries each (128 queries of one (sequence, head)),
+// K / V tiles of 32 keys double-buffered in LDS (one barrier per tile), the
+// next tile's global loads in flight while the current one is computed.
+// Causal: a workgroup stops at its last query's diagonal, a wave skips the
+// tiles past its own diagonal and masks inside the diagonal tile only.
+// Grid: the query blocks of one (sequence, head) are placed on one XCD (the
+// hardware deals workgroups to the 8 XCDs round-robin), so K and V are fetched
+// once into that XCD's L2 and re-read from there; heavier (later, causal)
+// query blocks start first.
+#include "common.hpp"
+#include "internal.hpp"
+
+#include <math.h>
+
+using namespace mimir;
+
+namespace {
+
+typedef float f16v __attribute__((ext_vector_type(16)));
+typedef float f2 __attribute__((ext_vector_type(2)));
+
+constexpr int kQPerWave = 32;
+constexpr int kWaves = 4;
+constexpr int kQPerBlock = kQPerWave * kWaves;  // 128
+constexpr int kKeyTile = 32;
+constexpr int kThreads = kWaves * kWave;        // 256
+constexpr int kXcds = 8;
+
+struct AttnArgs {
+    const float* q;
+    const float* k;
+    const float* v;
+    float* out;
+    int64_t ld_q, ld_kv, ld_out;  // row strides (floats)
+    int32_t q_len, kv_len, heads, head_dim;
+    int32_t n_qblocks;            // ceil(q_len / 128)
+    uint32_t total_blocks;        // batch * heads * n_qblocks
+    float scale;                  // applied to the dot products, as the reference does
+    int32_t causal;
+};
+
+// LDS layout of one buffer: K tile [32][DP + 4] (the pad staggers the rows
+// across banks for the column-wise reads), then V tile [32][DP].
+template <int DP>
+struct Lds {
+    static constexpr int kLd = DP + 4;
+    static constexpr int vLd = DP;
+    static constexpr int kFloats = kKeyTile * kLd;
+    static constexpr int buf = kFloats + kKeyTile * vLd;
+    static constexpr int f4PerRow = DP / 4;
+    static constexpr int loads = kKeyTile * f4PerRow / kThreads;  // float4 per thread per operand
+    static_assert(loads >= 1 && kKeyTile * f4PerRow == loads * kThreads, "tile / block mismatch");
+};
+
+// 4 floats of a row at column c (a multiple of 4), zero past `valid` columns.
+// VEC: head_dim, the strides and the base pointers are 16-byte multiples.
+template <bool VEC>
+__device__ __forceinline__ f4 load4(const float* row, int c, int valid) {
+    if constexpr (VEC) {
+        if (c < valid) return *reinterpret_cast<const f4*>(row + c);
+        return f4{0.f, 0.f, 0.f, 0.f};
+    } else {
+        f4 r;
+        r.x = c + 0 < valid ? row[c + 0] : 0.f;
+        r.y = c + 1 < valid ? row[c + 1] : 0.f;
+        r.z = c + 2 < valid ? row[c + 2] : 0.f;
+        r.w = c + 3 < valid ? row[c + 3] : 0.f;
+        return r;
+    }
+}
+
+// Scalar-path tile load: four loads from clamped, always valid columns
+// (< head_dim); the caller clamps the row below kv_len.  What lies outside
+// the tile's valid rows / columns is replaced by zeros when the values are
+// written to LDS (zero_outside).
+__device__ __forceinline__ f4 load4_clamped(const float* row, int c, int head_dim) {
+    f4 r;
+    r.x = row[min(c + 0, head_dim - 1)];
+    r.y = row[min(c + 1, head_dim - 1)];
+    r.z = row[min(c + 2, head_dim - 1)];
+    r.w = row[min(c + 3, head_dim - 1)];
+    return r;
+}
+
+// Word 3 of a raw (stride 0) buffer descriptor on gfx9-family GPUs: 32-bit
+// data format, no swizzle; out-of-range offsets return zeros.
+constexpr int kBufferWord3 = 0x00020000;
+
+__device__ __forceinline__ f4 zero_outside(f4 x, bool row_ok, int c, int head_dim) {
+    x.x = row_ok && c + 0 < head_dim ? x.x : 0.f;
+    x.y = row_ok && c + 1 < head_dim ? x.y : 0.f;
+    x.z = row_ok && c + 2 < head_dim ? x.z : 0.f;
+    x.w = row_ok && c + 3 < head_dim ? x.w : 0.f;
+    return x;
+}
+
+// Workgroup -> (sequence * heads + head, query block).  Consecutive logical
+// indices share a (sequence, head); they are given to one XCD when the grid
+// divides evenly.  Within a (sequence, head) the last query block comes first.
+__device__ __forceinline__ void block_coords(const AttnArgs& a, uint32_t bid, uint32_t* bh, int* qb) {
+    uint32_t logical = bid;
+    if (a.total_blocks % kXcds == 0) logical = (bid % kXcds) * (a.total_blocks / kXcds) + bid / kXcds;
+    *bh = logical / static_cast<uint32_t>(a.n_qblocks);
+    *qb = a.n_qblocks - 1 - static_cast<int>(logical % static_cast<uint32_t>(a.n_qblocks));
+}
+
+template <int DP, bool VEC>
+__global__ __launch_bounds__(kThreads, 2) void attention_fwd_mfma(AttnArgs a) {
+    using L = Lds<DP>;
+    constexpr int kSteps = DP / 2;   // MFMA k-steps over the head dimension
+    constexpr int kHalf = DP / 2;    // dimensions per lane half
+    constexpr int kDb = DP / 32;     // output dimension blocks
+    __shared__ __attribute__((aligned(16))) float lds[2 * L::buf];
+
+    uint32_t bh;
+    int qb;
+    block_coords(a, blockIdx.x, &bh, &qb);
+    const int64_t b = bh / static_cast<uint32_t>(a.heads);
+    const int64_t hd_off = static_cast<int64_t>(bh % static_cast<uint32_t>(a.heads)) * a.head_dim;
+    const float* qbase = a.q + b * a.q_len * a.ld_q + hd_off;
+    const float* kbase = a.k + b * a.kv_len * a.ld_kv + hd_off;
+    const float* vbase = a.v + b * a.kv_len * a.ld_kv + hd_off;
+    float* obase = a.out + b * a.q_len * a.ld_out + hd_off;
+
+    const int tid = threadIdx.x;
+    const int wave = tid / kWave;
+    const int lane = tid % kWave;
+    const int li = lane % 32;  // query column / MFMA row index
+    const int hf = lane / 32;  // lane half
+    const int q0 = qb * kQPerBlock;
+    const int qw0 = q0 + wave * kQPerWave;
+    const int my_q = qw0 + li;
+
+    // Tiles this workgroup streams, and the ones this wave computes.
+    int key_end = a.kv_len;
+    int wave_key_end = a.kv_len;
+    if (a.causal) {
+        key_end = min(key_end, min(q0 + kQPerBlock, a.q_len));
+        wave_key_end = min(wave_key_end, min(qw0 + kQPerWave, a.q_len));
+    }
+    if (qw0 >= a.q_len) wave_key_end = 0;
+    const int n_tiles = (key_end + kKeyTile - 1) / kKeyTile;
+    const int wave_tiles = (wave_key_end + kKeyTile - 1) / kKeyTile;
+
+    // This lane's Q values: query my_q, dimensions hf*kHalf + [0, kHalf).
+    float qreg[kHalf];
+    {
+        const float* qrow = qbase + static_cast<int64_t>(min(my_q, a.q_len - 1)) * a.ld_q;
+        const int valid = my_q < a.q_len ? a.head_dim : 0;
+#pragma unroll
+        for (int j = 0; j < kHalf / 4; ++j) {
+            const f4 t = load4<VEC>(qrow, hf * kHalf + 4 * j, valid);
+            qreg[4 * j + 0] = t.x;
+            qreg[4 * j + 1] = t.y;
+            qreg[4 * j + 2] = t.z;
+            qreg[4 * j + 3] = t.w;
+        }
+    }
+
+    // Cooperative tile load: thread tid moves float4 number tid + 256*r of
+    // each operand (row = key within the tile, column group c).  VEC: buffer
+    // loads through a descriptor based at the tile's first row whose range
+    // ends after the sequence's last row, so rows past kv_len read as zeros
+    // without a memory access; the per-thread byte offsets are loop
+    // invariants (no address registers recycled while the loads are in
+    // flight).  Columns are clamped below head_dim (never past the row).
+    f4 kst[L::loads], vst[L::loads];
+    uint32_t voff[L::loads];
+    if constexpr (VEC) {
+#pragma unroll
+        for (int r = 0; r < L::loads; ++r) {
+            const int f = tid + r * kThreads;
+            const int row = f / L::f4PerRow;
+            const int c = min(4 * (f % L::f4PerRow), a.head_dim - 4);
+            voff[r] = static_cast<uint32_t>((row * a.ld_kv + c) * 4);
+        }
+    }
+    auto fetch = [&](int tile) {
+        if constexpr (VEC) {
+            const int64_t first = static_cast<int64_t>(tile) * kKeyTile * a.ld_kv;
+            const int rows = min(kKeyTile, a.kv_len - tile * kKeyTile);
+            const int bytes = static_cast<int>(rows * a.ld_kv * 4);
+            const __amdgpu_buffer_rsrc_t kr =
+                __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(kbase + first), 0, bytes, kBufferWord3);
+            const __amdgpu_buffer_rsrc_t vr =
+                __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(vbase + first), 0, bytes, kBufferWord3);
+#pragma unroll
+            for (int r = 0; r < L::loads; ++r) {
+                kst[r] = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(kr, voff[r], 0, 0));
+                vst[r] = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(vr, voff[r], 0, 0));
+            }
+        } else {
+#pragma unroll
+            for (int r = 0; r < L::loads; ++r) {
+                const int f = tid + r * kThreads;
+                const int row = f / L::f4PerRow;
+                const int c = 4 * (f % L::f4PerRow);
+                const int64_t off = static_cast<int64_t>(min(tile * kKeyTile + row, a.kv_len - 1)) * a.ld_kv;
+                kst[r] = load4_clamped(kbase + off, c, a.head_dim);
+                vst[r] = load4_clamped(vbase + off, c, a.head_dim);
+            }
+        }
+    };
+    auto stash = [&](int tile, int buf) {
+        float* kl = lds + buf * L::buf;
+        float* vl = kl + L::kFloats;
+#pragma unroll
+        for (int r = 0; r < L::loads; ++r) {
+            const int f = tid + r * kThreads;
+            const int row = f / L::f4PerRow;
+            const int c = 4 * (f % L::f4PerRow);
+            const bool row_ok = tile * kKeyTile + row < a.kv_len;
+            *reinterpret_cast<f4*>(kl + row * L::kLd + c) = zero_outside(kst[r], row_ok, c, a.head_dim);
+            *reinterpret_cast<f4*>(vl + row * L::vLd + c) = zero_outside(vst[r], row_ok, c, a.head_dim);
+        }
+    };
+
+    f16v o[kDb];
+#pragma unroll
+    for (int d = 0; d < kDb; ++d) o[d] = f16v{};
+    float m_run = -1e30f;  // the reference's initial max (LayerOps.hpp:1052)
+    float l_run = 0.f;     // this half's share of the running sum
+    constexpr float kLog2e = 1.4426950408889634f;
+
+    if (n_tiles > 0) {
+        fetch(0);
+        stash(0, 0);
+    }
+    __syncthreads();
+    for (int t = 0; t < n_tiles; ++t) {
+        const int buf = t & 1;
+        fetch(min(t + 1, n_tiles - 1));  // the last iteration refetches into the idle buffer
+        if (t < wave_tiles) {
+            const float* kl = lds + buf * L::buf;
+            const float* vl = kl + L::kFloats;
+            // S^T = K Q^T over the head dimension.
+            f16v s = f16v{};
+            const float* krow = kl + li * L::kLd + hf * kHalf;
+#pragma unroll
+            for (int j = 0; j < kSteps / 4; ++j) {
+                const f4 kv = *reinterpret_cast<const f4*>(krow + 4 * j);
+                s = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.x, qreg[4 * j + 0], s, 0, 0, 0);
+                s = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.y, qreg[4 * j + 1], s, 0, 0, 0);
+                s = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.z, qreg[4 * j + 2], s, 0, 0, 0);
+                s = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.w, qreg[4 * j + 3], s, 0, 0, 0);
+            }
+            // Scores, mask, tile max (the masked ones do not enter it, :1054-1057).
+            const int key0 = t * kKeyTile + 4 * hf;
+            const bool need_mask = (t + 1) * kKeyTile > a.kv_len || (a.causal && (t + 1) * kKeyTile - 1 > qw0);
+            float tmax = -1e30f;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                s[r] *= a.scale;
+                if (need_mask) {
+                    const int key = key0 + 8 * (r / 4) + (r % 4);
+                    const bool masked = key >= a.kv_len || (a.causal && key > my_q);
+                    s[r] = masked ? -INFINITY : s[r];
+                }
+                tmax = fmaxf(tmax, s[r]);
+            }
+            tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
+            const float m_new = fmaxf(m_run, tmax);
+            const float alpha = __builtin_amdgcn_exp2f((m_run - m_new) * kLog2e);
+            m_run = m_new;
+            float psum = 0.f;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                s[r] = __builtin_amdgcn_exp2f((s[r] - m_new) * kLog2e);  // exp2(-inf) = 0: masked keys
+                psum += s[r];
+            }
+            l_run = l_run * alpha + psum;
+#pragma unroll
+            for (int d = 0; d < kDb; ++d) o[d] *= alpha;
+            // O^T += V^T P^T: k-slot h of step r is key(r, h) = 8*(r/4) + 4h + r%4.
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const float* vrow = vl + (8 * (r / 4) + 4 * hf + (r % 4)) * L::vLd + kDb * li;
+                if constexpr (kDb == 4) {
+                    const f4 vv = *reinterpret_cast<const f4*>(vrow);
+                    o[0] = __builtin_amdgcn_mfma_f32_32x32x2f32(vv.x, s[r], o[0], 0, 0, 0);
+                    o[1] = __builtin_amdgcn_mfma_f32_32x32x2f32(vv.y, s[r], o[1], 0, 0, 0);
+                    o[2] = __builtin_amdgcn_mfma_f32_32x32x2f32(vv.z, s[r], o[2], 0, 0, 0);
+                    o[3] = __builtin_amdgcn_mfma_f32_32x32x2f32(vv.w, s[r], o[3], 0, 0, 0);
+                } else if constexpr (kDb == 2) {
+                    const f2 vv = *reinterpret_cast<const f2*>(vrow);
+                    o[0] = __builtin_amdgcn_mfma_f32_32x32x2f32(vv.x, s[r], o[0], 0, 0, 0);
+                    o[1] = __builtin_amdgcn_mfma_f32_32x32x2f32(vv.y, s[r], o[1], 0, 0, 0);
+                } else {
+                    o[0] = __builtin_amdgcn_mfma_f32_32x32x2f32(vrow[0], s[r], o[0], 0, 0, 0);
+                }
+            }
+        }
+        stash(min(t + 1, n_tiles - 1), buf ^ 1);
+        __syncthreads();
+    }
+
+    // out = O / (sum + 1e-9) (LayerOps.hpp:1076-1079), rows of DP/32 dims.
+    if (my_q < a.q_len) {
+        const float l_tot = l_run + __shfl_xor(l_run, 32);
+        const float inv = 1.0f / (l_tot + 1e-9f);
+        float* orow = obase + static_cast<int64_t>(my_q) * a.ld_out;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int d0 = kDb * (8 * (r / 4) + 4 * hf + (r % 4));
+            if (d0 >= a.head_dim) continue;
+            if constexpr (kDb == 4) {
+                const f4 val{o[0][r] * inv, o[1][r] * inv, o[2][r] * inv, o[3][r] * inv};
+                if constexpr (VEC) {
+                    *reinterpret_cast<f4*>(orow + d0) = val;
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        if (d0 + e < a.head_dim) orow[d0 + e] = val[e];
+                }
+            } else if constexpr (kDb == 2) {
+                orow[d0] = o[0][r] * inv;
+                if (d0 + 1 < a.head_dim) orow[d0 + 1] = o[1][r] * inv;
+            } else {
+                orow[d0] = o[0][r] * inv;
+            }
+        }
+    }
+}
+
+template <int DP>
+int launch(mimir_ctx* ctx, const AttnArgs& a, bool vec) {
+    if (vec) attention_fwd_mfma<DP, true><<<a.total_blocks, kThreads, 0, ctx->stream>>>(a);
+    else attention_fwd_mfma<DP, false><<<a.total_blocks, kThreads, 0, ctx->stream>>>(a);
+    return launched(ctx, "attention_fwd_mfma");
+}
+
+}  // namespace
+
+extern "C" {
+
+int mimir_attention_fwd(mimir_ctx* ctx, const float* q, int64_t ld_q, const float* k, const float* v,
+                        int64_t ld_kv, float* out, int64_t ld_out, int64_t batch, int64_t q_len,
+                        int64_t kv_len, int64_t heads, int64_t head_dim, float scale, int causal) {
+    if (!ctx) return MIMIR_EINVAL;
+    MIMIR_REQUIRE(ctx, batch >= 0 && q_len >= 0 && kv_len >= 0 && heads >= 1 && head_dim >= 1,
+                  "attention: invalid shape (batch=%lld q_len=%lld kv_len=%lld heads=%lld head_dim=%lld)",
+                  (long long)batch, (long long)q_len, (long long)kv_len, (long long)heads, (long long)head_dim);
+    MIMIR_REQUIRE(ctx, head_dim <= 128, "attention: head_dim %lld > 128 is not supported", (long long)head_dim);
+    const int64_t width = heads * head_dim;
+    MIMIR_REQUIRE(ctx, ld_q >= width && ld_kv >= width && ld_out >= width,
+                  "attention: row strides (%lld, %lld, %lld) below heads * head_dim = %lld", (long long)ld_q,
+                  (long long)ld_kv, (long long)ld_out, (long long)width);
+    MIMIR_REQUIRE(ctx, q_len < (int64_t{1} << 30) && kv_len < (int64_t{1} << 30) && heads < (int64_t{1} << 30),
+                  "attention: sequence or head count too large");
+    if (batch == 0 || q_len == 0) return MIMIR_OK;
+    MIMIR_REQUIRE(ctx, q && out && (kv_len == 0 || (k && v)), "attention: null pointer");
+    const int64_t nqb = (q_len + kQPerBlock - 1) / kQPerBlock;
+    MIMIR_REQUIRE(ctx, batch * heads * nqb <= INT32_MAX, "attention: grid of %lld workgroups exceeds the limit",
+                  (long long)(batch * heads * nqb));
+    if (int st = enter(ctx)) return st;
+    AttnArgs a;
+    a.q = q;
+    a.k = kv_len ? k : q;  // never read when kv_len == 0
+    a.v = kv_len ? v : q;
+    a.out = out;
+    a.ld_q = ld_q;
+    a.ld_kv = ld_kv;
+    a.ld_out = ld_out;
+    a.q_len = static_cast<int32_t>(q_len);
+    a.kv_len = static_cast<int32_t>(kv_len);
+    a.heads = static_cast<int32_t>(heads);
+    a.head_dim = static_cast<int32_t>(head_dim);
+    a.n_qblocks = static_cast<int32_t>(nqb);
+    a.total_blocks = static_cast<uint32_t>(batch * heads * nqb);
+    a.scale = scale;
+    a.causal = causal ? 1 : 0;
+    // The vector path's buffer descriptors span one 32-row tile: 32 rows of
+    // ld_kv floats must stay below 2^31 bytes.
+    const bool vec = head_dim % 4 == 0 && ld_q % 4 == 0 && ld_kv % 4 == 0 && ld_out % 4 == 0 && aligned16(q) &&
+                     aligned16(a.k) && aligned16(a.v) && aligned16(out) &&
+                     ld_kv < (int64_t{1} << 31) / (4 * kKeyTile);
+    if (head_dim <= 32) return launch<32>(ctx, a, vec);
+    if (head_dim <= 64) return launch<64>(ctx, a, vec);
+    return launch<128>(ctx, a, vec);
+}
+
+}  // extern "C"

@@ -106,6 +106,8 @@ SIGNATURES = {
     "mimir_rope_table": (c_int, [c_int64, c_int64, c_double, _P, _P]),
     "mimir_rope_fwd": (c_int, [_P, _P, _P, c_int64, _P, _P, c_int64, c_int64, c_int64, c_int64,
                                c_int64, _P, _P, c_int64]),
+    "mimir_attention_fwd": (c_int, [_P, _P, c_int64, _P, _P, c_int64, _P, c_int64, c_int64, c_int64, c_int64,
+                                    c_int64, c_int64, c_float, c_int]),
     "mimir_layernorm_bwd": (c_int, [_P, _P, _P, _P, _P, _P, _P, c_int64, c_int64, c_float, c_int]),
     "mimir_layernorm_bwd_noalloc": (c_int, [_P, _P, _P, _P, _P, _P, _P, c_int64, c_int64, c_float, c_int]),
     "mimir_gelu_bwd": (c_int, [_P, _P, _P, _P, c_int64, c_int]),

@@ -207,6 +207,17 @@ class Context:
                                            _ptr(k_out), k_heads, batch, seq, head_dim, pos_offset,
                                            _ptr(cos_tab), _ptr(sin_tab), table_rows))
 
+    def attention(self, q, k, v, out, batch, q_len, kv_len, heads, head_dim, causal=False, scale=None,
+                  ld_q=None, ld_kv=None, ld_out=None):
+        """mimir_attention_fwd: softmax(Q K^T * scale, causal) V per head; the
+        row strides default to heads * head_dim (separate Q / K / V / out)."""
+        width = heads * head_dim
+        if scale is None:
+            scale = float(np.float32(1.0) / np.sqrt(np.float32(head_dim)))  # LayerOps.hpp:1047
+        self.check(self.lib.mimir_attention_fwd(self.handle, _ptr(q), ld_q or width, _ptr(k), _ptr(v),
+                                                ld_kv or width, _ptr(out), ld_out or width, batch, q_len,
+                                                kv_len, heads, head_dim, float(scale), int(bool(causal))))
+
     # -- backward (Model::backwardPass branches) -------------------------------
 
     def layernorm_bwd(self, x, dy, gamma, dx, dgamma, dbeta, groups, n, eps, accumulate=False):

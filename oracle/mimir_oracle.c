@@ -441,3 +441,73 @@ int oracle_embedding_bwd_f32(const float* ids, int64_t n_ids, const float* dy, f
     }
     return ORACLE_OK;
 }
+
+/* The attention core of LayerOps::self_attention_forward, LayerOps.hpp:1045-1089
+ * (between the QKV projection and the output projection; the same core is
+ * cross_attention_forward's, :1163-1209, with kv_len keys) for `batch`
+ * independent sequences.  Query i of sequence b reads its Q row at
+ * (b*q_len + i)*ld_q and writes its output row at (b*q_len + i)*ld_out; key j
+ * reads K and V rows at (b*kv_len + j)*ld_kv.  Head h owns columns
+ * [h*head_dim, (h+1)*head_dim).  Per head and query i:
+ *   s_j = (sum_k Q[i][k] K[j][k]) * scale      (k in index order, :1059-1065)
+ *   masked (causal, j > i): s_j = -1e9, not taken into the max (:1054-1057)
+ *   max starts at -1e30 (:1052); e_j = expf(s_j - max); sum in j order (:1069-1075)
+ *   p_j = e_j * (1 / (sum + 1e-9f)) (:1076-1079)
+ *   out[i][k] = sum_j p_j V[j][k], j in index order (:1081-1088).
+ * The reference as compiled (g++ -O3 -mfma; C++ keeps GCC's default
+ * -ffp-contract=fast) fuses the weighted-sum step acc += p*V into one fused
+ * multiply-add and keeps the score dot product as a multiply then an add;
+ * fmaf in the PV loop restates that, and the two agree bit for bit on the
+ * tests' shapes (tests/test_oracle_attention.py). */
+int oracle_attention(const float* q, int64_t ld_q, const float* k, const float* v, int64_t ld_kv,
+                     float* out, int64_t ld_out, int64_t batch, int64_t q_len, int64_t kv_len,
+                     int64_t heads, int64_t head_dim, float scale, int causal) {
+    const int64_t width = heads * head_dim;
+    if (batch < 0 || q_len < 0 || kv_len < 0 || heads <= 0 || head_dim <= 0 || ld_q < width ||
+        ld_kv < width || ld_out < width)
+        return ORACLE_EINVAL;
+    if (batch == 0 || q_len == 0) return ORACLE_OK;
+    float* row = (float*)malloc((size_t)(kv_len > 0 ? kv_len : 1) * sizeof(float));
+    if (!row) return ORACLE_EINVAL;
+    for (int64_t b = 0; b < batch; ++b) {
+        const float* qb = q + b * q_len * ld_q;
+        const float* kb = k + b * kv_len * ld_kv;
+        const float* vb = v + b * kv_len * ld_kv;
+        float* ob = out + b * q_len * ld_out;
+        for (int64_t h = 0; h < heads; ++h) {
+            const int64_t off = h * head_dim;
+            for (int64_t i = 0; i < q_len; ++i) {
+                const float* qi = qb + i * ld_q + off;
+                float max_val = -1e30f;
+                for (int64_t j = 0; j < kv_len; ++j) {
+                    if (causal && j > i) {
+                        row[j] = -1e9f;
+                        continue;
+                    }
+                    const float* kj = kb + j * ld_kv + off;
+                    float dot = 0.0f;
+                    for (int64_t d = 0; d < head_dim; ++d) dot += qi[d] * kj[d];
+                    const float s = dot * scale;
+                    row[j] = s;
+                    if (s > max_val) max_val = s;
+                }
+                float sum = 0.0f;
+                for (int64_t j = 0; j < kv_len; ++j) {
+                    const float e = expf(row[j] - max_val);
+                    row[j] = e;
+                    sum += e;
+                }
+                const float inv_sum = 1.0f / (sum + 1e-9f);
+                for (int64_t j = 0; j < kv_len; ++j) row[j] *= inv_sum;
+                float* oi = ob + i * ld_out + off;
+                for (int64_t d = 0; d < head_dim; ++d) {
+                    float acc = 0.0f;
+                    for (int64_t j = 0; j < kv_len; ++j) acc = fmaf(row[j], vb[j * ld_kv + off + d], acc);
+                    oi[d] = acc;
+                }
+            }
+        }
+    }
+    free(row);
+    return ORACLE_OK;
+}

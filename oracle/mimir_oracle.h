@@ -28,6 +28,10 @@
  *                           in place (oracle/_ref), on graphs of these layers;
  *                           float64 derivatives of the forward closed forms;
  *                           brute-force scatter-add for the embedding.
+ *   oracle_attention        the reference's LayerOps::self_attention_forward,
+ *                           compiled in place, with one-hot inputs and an
+ *                           identity output projection (bit-exact); float64
+ *                           softmax attention; closed-form special cases.
  */
 #ifndef MIMIR_ORACLE_H
 #define MIMIR_ORACLE_H
@@ -139,6 +143,19 @@ int oracle_embedding_bwd_i32(const int32_t* ids, int64_t n_ids, const float* dy,
                              int32_t padding_idx);
 int oracle_embedding_bwd_f32(const float* ids, int64_t n_ids, const float* dy, float* grad_table,
                              int64_t table_len, int32_t vocab, int32_t dim, int32_t padding_idx);
+
+/* ---- Attention core (the softmax between QK^T and PV) ---- */
+
+/* The core of LayerOps::self_attention_forward (LayerOps.hpp:1045-1089) and
+ * cross_attention_forward (:1163-1209): softmax(Q K^T * scale, causal mask
+ * j > i) V over `batch` independent sequences of q_len queries and kv_len
+ * keys.  Q rows have stride ld_q, K and V rows stride ld_kv (so Q, K, V may be
+ * the column blocks of one fused QKV buffer), output rows stride ld_out; head
+ * h owns columns [h*head_dim, (h+1)*head_dim).  The reference's scale is
+ * 1.0f / sqrtf((float) head_dim) (:1047). */
+int oracle_attention(const float* q, int64_t ld_q, const float* k, const float* v, int64_t ld_kv,
+                     float* out, int64_t ld_out, int64_t batch, int64_t q_len, int64_t kv_len,
+                     int64_t heads, int64_t head_dim, float scale, int causal);
 
 #ifdef __cplusplus
 }

@@ -71,6 +71,8 @@ def _oracle():
             "oracle_add_bwd_small": [P, c_int64, c_int64, P],
             "oracle_embedding_bwd_i32": [P, c_int64, P, P, c_int64, c_int32, c_int32, c_int32],
             "oracle_embedding_bwd_f32": [P, c_int64, P, P, c_int64, c_int32, c_int32, c_int32],
+            "oracle_attention": [P, c_int64, P, P, c_int64, P, c_int64, c_int64, c_int64, c_int64,
+                                 c_int64, c_int64, c_float, c_int32],
         }
         for name, args in sig.items():
             fn = getattr(lib, name)
@@ -101,6 +103,8 @@ def _ref():
             "ref_softmax_forward": [P, c_int64, c_int32, P],
             "ref_gelu": [P, c_int64, P],
             "ref_silu": [P, c_int64, P],
+            "ref_self_attention": [P, P, P, c_int32, c_int32, c_int32, c_int32, c_int32, P],
+            "ref_cross_attention": [P, P, P, P, P, c_int32, c_int32, c_int32, c_int32, c_int32, P],
         }
         for name, args in sig.items():
             fn = getattr(lib, name)
@@ -375,6 +379,34 @@ def embedding_bwd(ids, dy, grad_table, vocab, dim, padding_idx=-1):
     return gt
 
 
+def attention_scale(head_dim):
+    """1.0f / std::sqrt((float) head_dim), LayerOps.hpp:1047 (both IEEE, correctly rounded)."""
+    return float(np.float32(1.0) / np.sqrt(np.float32(head_dim)))
+
+
+def attention(q, k, v, heads, causal=False, scale=None):
+    """The attention core of self_attention_forward / cross_attention_forward
+    (oracle_attention).  q: [batch, q_len, width] (or [q_len, width]); k, v:
+    [batch, kv_len, width]; width = heads * head_dim.  Returns [batch, q_len,
+    width] (or [q_len, width])."""
+    squeeze = np.ndim(q) == 2
+    q, k, v = (np.asarray(a, np.float32) for a in (q, k, v))
+    if squeeze:
+        q, k, v = q[None], k[None], v[None]
+    batch, q_len, width = q.shape
+    kv_len = k.shape[1]
+    if k.shape != (batch, kv_len, width) or v.shape != k.shape or width % heads:
+        raise OracleError("attention: shape mismatch")
+    head_dim = width // heads
+    if scale is None:
+        scale = attention_scale(head_dim)
+    q, k, v = _f32(q), _f32(k), _f32(v)
+    y = np.empty((batch, q_len, width), np.float32)
+    _check(_oracle().oracle_attention(_p(q), width, _p(k), _p(v), width, _p(y), width, batch, q_len,
+                                      kv_len, heads, head_dim, scale, int(causal)), "attention")
+    return y[0] if squeeze else y
+
+
 # --------------------------------------------------------------------------
 # The reference's own functions (compiled in place)
 # --------------------------------------------------------------------------
@@ -450,6 +482,31 @@ def ref_silu(x):
     y = np.empty_like(x)
     _check(_ref().ref_silu(_p(x), x.size, _p(y)), "ref_silu")
     return y
+
+
+def ref_self_attention(x, qkv_weight, out_weight, seq_len, embed_dim, num_heads, causal=False,
+                       multihead=False):
+    """LayerOps::self_attention_forward (or multihead_attention_forward)."""
+    x, wq, wo = _f32(x).ravel(), _f32(qkv_weight).ravel(), _f32(out_weight).ravel()
+    if x.size != seq_len * embed_dim or wq.size != 3 * embed_dim * embed_dim or wo.size != embed_dim ** 2:
+        raise OracleError("ref_self_attention: size mismatch")
+    y = np.empty(seq_len * embed_dim, np.float32)
+    _check(_ref().ref_self_attention(_p(x), _p(wq), _p(wo), seq_len, embed_dim, num_heads, int(causal),
+                                     int(multihead), _p(y)), "ref_self_attention")
+    return y.reshape(seq_len, embed_dim)
+
+
+def ref_cross_attention(xq, xkv, q_weight, kv_weight, out_weight, query_len, kv_len, embed_dim, num_heads,
+                        causal=False):
+    """LayerOps::cross_attention_forward."""
+    a = [_f32(t).ravel() for t in (xq, xkv, q_weight, kv_weight, out_weight)]
+    e = embed_dim
+    if [t.size for t in a] != [query_len * e, kv_len * e, e * e, 2 * e * e, e * e]:
+        raise OracleError("ref_cross_attention: size mismatch")
+    y = np.empty(query_len * e, np.float32)
+    _check(_ref().ref_cross_attention(*[_p(t) for t in a], query_len, kv_len, e, num_heads, int(causal),
+                                      _p(y)), "ref_cross_attention")
+    return y.reshape(query_len, e)
 
 
 # --------------------------------------------------------------------------

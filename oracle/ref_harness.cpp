@@ -136,6 +136,46 @@ int ref_silu(const float* x, int64_t n, float* y) {
     }
 }
 
+// LayerOps::self_attention_forward, LayerOps.hpp:1004-1097: input [seq, embed],
+// qkv_weight [embed, 3 embed], out_weight [embed, embed].  `multihead` calls
+// LayerOps::multihead_attention_forward (:1100-1113) instead.
+int ref_self_attention(const float* input, const float* qkv_weight, const float* out_weight,
+                       int32_t seq_len, int32_t embed_dim, int32_t num_heads, int32_t causal,
+                       int32_t multihead, float* y) {
+    try {
+        const int64_t e = embed_dim;
+        const std::vector<float> x = vec(input, static_cast<int64_t>(seq_len) * e);
+        const std::vector<float> wq = vec(qkv_weight, 3 * e * e), wo = vec(out_weight, e * e);
+        return put(multihead ? LayerOps::multihead_attention_forward(x, wq, wo, seq_len, embed_dim,
+                                                                     num_heads, causal != 0)
+                             : LayerOps::self_attention_forward(x, wq, wo, seq_len, embed_dim,
+                                                                num_heads, causal != 0),
+                   y);
+    } catch (...) {
+        return 1;
+    }
+}
+
+// LayerOps::cross_attention_forward, LayerOps.hpp:1116-1216: query_input
+// [query_len, embed], kv_input [kv_len, embed], q_weight [embed, embed],
+// kv_weight [embed, 2 embed], out_weight [embed, embed].
+int ref_cross_attention(const float* query_input, const float* kv_input, const float* q_weight,
+                        const float* kv_weight, const float* out_weight, int32_t query_len,
+                        int32_t kv_len, int32_t embed_dim, int32_t num_heads, int32_t causal,
+                        float* y) {
+    try {
+        const int64_t e = embed_dim;
+        return put(LayerOps::cross_attention_forward(
+                       vec(query_input, static_cast<int64_t>(query_len) * e),
+                       vec(kv_input, static_cast<int64_t>(kv_len) * e), vec(q_weight, e * e),
+                       vec(kv_weight, 2 * e * e), vec(out_weight, e * e), query_len, kv_len,
+                       embed_dim, num_heads, causal != 0),
+                   y);
+    } catch (...) {
+        return 1;
+    }
+}
+
 // ---------------------------------------------------------------------------
 // CPU baseline timing: the inputs are turned into std::vector once, then only
 // the reference call(s) of the path are timed (including the output vector

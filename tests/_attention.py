@@ -1,0 +1,106 @@
+"""Attention cases shared by the CPU pin tests (tests/test_oracle_attention.py),
+the golden writer (tests/golden/make_golden.py) and the GPU parity tests.
+
+The reference's attention functions (LayerOps::self_attention_forward,
+LayerOps.hpp:1004-1097; cross_attention_forward, :1116-1216) wrap the core in
+two projections.  With one-hot input rows (row m = e_(m mod E)) and an
+identity output projection both projections are exact in float32 (each output
+is one product 1*w plus products 0*w), so the reference's output IS its
+attention core on Q / K / V = the selected rows of the projection weights."""
+import numpy as np
+
+# (seq_len, embed_dim, num_heads): head_dim = embed_dim / num_heads.
+SELF_CASES = [(1, 8, 1), (8, 8, 1), (5, 16, 2), (24, 32, 4), (33, 32, 1), (64, 64, 2), (100, 128, 1),
+              (130, 96, 3), (40, 48, 3), (70, 80, 1)]
+# (query_len, kv_len, embed_dim, num_heads)
+CROSS_CASES = [(1, 7, 8, 1), (9, 4, 16, 2), (40, 65, 64, 2), (33, 100, 128, 1)]
+
+
+def one_hot_rows(n, e):
+    x = np.zeros((n, e), np.float32)
+    x[np.arange(n), np.arange(n) % e] = 1.0
+    return x
+
+
+def self_case(seq, e, amp, seed):
+    """(input, qkv_weight, q, k, v): q/k/v are the rows the one-hot input selects."""
+    rng = np.random.default_rng(seed)
+    w = (amp * rng.standard_normal((e, 3 * e))).astype(np.float32)
+    x = one_hot_rows(seq, e)
+    rows = w[np.arange(seq) % e]
+    return x, w, rows[:, :e].copy(), rows[:, e:2 * e].copy(), rows[:, 2 * e:].copy()
+
+
+def cross_case(q_len, kv_len, e, amp, seed):
+    """(xq, xkv, q_weight, kv_weight, q, k, v)."""
+    rng = np.random.default_rng(seed)
+    wq = (amp * rng.standard_normal((e, e))).astype(np.float32)
+    wkv = (amp * rng.standard_normal((e, 2 * e))).astype(np.float32)
+    xq, xkv = one_hot_rows(q_len, e), one_hot_rows(kv_len, e)
+    q = wq[np.arange(q_len) % e].copy()
+    kv = wkv[np.arange(kv_len) % e]
+    return xq, xkv, wq, wkv, q, kv[:, :e].copy(), kv[:, e:].copy()
+
+
+U32 = 2.0 ** -24  # float32 unit roundoff
+
+
+def attention64(q, k, v, heads, causal, scale):
+    """float64 softmax attention: (out, mag, cond).
+    mag  = sum_j p_j |v_j|: the scale of the float32 rounding of the weighted
+           sum (the sum-aware tolerance of tests/_parity.py);
+    cond = u * sqrt(head_dim) * sum_j p_j A_j (|v_j| + |out|), A_j = scale *
+           sum_k |q_k k_k|: the first-order effect on the output of rounding
+           the float32 scores (d out / d s_j = p_j (v_j - out), |ds_j| ~ u
+           sqrt(D) A_j for a D-term float32 dot product).  The restatement
+           pinned to the reference stays within a quarter of it even where
+           the scores reach +-50 (tests/test_oracle_attention.py).
+    q: [.., q_len, width]."""
+    q, k, v = (np.asarray(a, np.float64) for a in (q, k, v))
+    squeeze = q.ndim == 2
+    if squeeze:
+        q, k, v = q[None], k[None], v[None]
+    b, lq, width = q.shape
+    lk = k.shape[1]
+    hd = width // heads
+    sc = float(np.float32(scale))
+    out = np.zeros((b, lq, width))
+    mag = np.zeros((b, lq, width))
+    cond = np.zeros((b, lq, width))
+    mask = np.arange(lk)[None, :] > np.arange(lq)[:, None]
+    for h in range(heads):
+        sl = slice(h * hd, (h + 1) * hd)
+        s = np.einsum("bid,bjd->bij", q[..., sl], k[..., sl]) * sc
+        a = np.einsum("bid,bjd->bij", np.abs(q[..., sl]), np.abs(k[..., sl])) * abs(sc)
+        if causal:
+            s = np.where(mask[None], -np.inf, s)
+        s = s - s.max(axis=2, keepdims=True) if lk else s
+        p = np.exp(s)
+        p /= np.maximum(p.sum(axis=2, keepdims=True), 1e-300)
+        out[..., sl] = np.einsum("bij,bjd->bid", p, v[..., sl])
+        mag[..., sl] = np.einsum("bij,bjd->bid", p, np.abs(v[..., sl]))
+        pa = p * a
+        cond[..., sl] = (np.einsum("bij,bjd->bid", pa, np.abs(v[..., sl])) +
+                         pa.sum(axis=2)[..., None] * np.abs(out[..., sl])) * (U32 * np.sqrt(hd))
+    if squeeze:
+        return out[0], mag[0], cond[0]
+    return out, mag, cond
+
+
+def assert_attention_close(got, ref, mag, cond, what=""):
+    """|got - ref| <= max(1e-6, 1e-5 * max(|ref|, mag)) + cond (attention64)."""
+    got = np.asarray(got, np.float64).ravel()
+    ref = np.asarray(ref, np.float64).ravel()
+    mag = np.asarray(mag, np.float64).ravel()
+    cond = np.asarray(cond, np.float64).ravel()
+    assert got.shape == ref.shape, f"{what}: shape {got.shape} != {ref.shape}"
+    assert ref.size, f"{what}: empty"
+    assert np.array_equal(np.isnan(got), np.isnan(ref)), f"{what}: NaN pattern differs"
+    fin = np.isfinite(ref)
+    d = np.abs(got[fin] - ref[fin])
+    tol = np.maximum(1e-6, 1e-5 * np.maximum(np.abs(ref[fin]), mag[fin])) + cond[fin]
+    bad = d > tol
+    if bad.any():
+        idx = np.flatnonzero(fin)[np.argmax(d / tol)]
+        raise AssertionError(f"{what}: {int(bad.sum())} of {fin.sum()} elements out of tolerance; worst at {idx}: "
+                             f"got {got[idx]!r} ref {ref[idx]!r} mag {mag[idx]:.3g} cond {cond[idx]:.3g}")

@@ -9,7 +9,7 @@ data, so parity stays pinned to the reference where the reference tree is
 absent (the GPU box, a fresh clone).  Inputs drawn from mimir_hip.datagen are
 not stored; their SHA-256 is, and the tests regenerate and check them.
 
-Run from the repository root:  python tests/golden/make_golden.py
+Run from the repository root:  python tests/golden/make_golden.py [fixture ...]
 """
 import hashlib
 import json
@@ -199,8 +199,44 @@ def write_safetensors_fixture():
     print("wrote ref_checkpoint.safetensors", len(data), "bytes")
 
 
+def write_attention():
+    """attention.npz: LayerOps::self_attention_forward (LayerOps.hpp:1004-1097)
+    and cross_attention_forward (:1116-1216) on the one-hot cases of
+    tests/_attention.py, in both mask modes.  The Q / K / V those cases select
+    are regenerated by the tests; the outputs are stored."""
+    sys.path.insert(0, os.path.join(REPO, "tests"))
+    from _attention import CROSS_CASES, SELF_CASES, cross_case, self_case
+    if not O.ref_available():
+        sys.exit("oracle/_ref/libmimir_ref.so is not built: make -C oracle ref")
+    outs = {}
+    for seq, e, heads in SELF_CASES:
+        x, w, q, k, v = self_case(seq, e, 1.5, seq * 1000 + e)
+        for causal in (0, 1):
+            outs[f"self_{seq}_{e}_{heads}_{causal}"] = O.ref_self_attention(
+                x, w, np.eye(e, dtype=np.float32), seq, e, heads, bool(causal))
+    for lq, lk, e, heads in CROSS_CASES:
+        xq, xkv, wq, wkv, q, k, v = cross_case(lq, lk, e, 1.2, lq * 7 + lk)
+        for causal in (0, 1):
+            outs[f"cross_{lq}_{lk}_{e}_{heads}_{causal}"] = O.ref_cross_attention(
+                xq, xkv, wq, wkv, np.eye(e, dtype=np.float32), lq, lk, e, heads, bool(causal))
+    np.savez_compressed(os.path.join(HERE, "attention.npz"), **outs)
+    path = os.path.join(HERE, "MANIFEST.json")
+    manifest = json.load(open(path))
+    manifest["attention"] = {
+        "note": "LayerOps::self_attention_forward / cross_attention_forward (LayerOps.hpp:1004-1216) with "
+                "one-hot inputs and an identity output projection: the attention core on the selected rows",
+        "arrays": {k: {"shape": list(v.shape), "dtype": str(v.dtype), "sha256": sha(v)} for k, v in outs.items()},
+        "regenerated_inputs": {"tests/_attention.py": "self_case / cross_case"},
+    }
+    with open(path, "w") as f:
+        json.dump(manifest, f, indent=1, sort_keys=True)
+    print("wrote attention", len(outs), "arrays")
+
+
+WRITERS = {"ops": lambda: main(), "model_graphs": write_model_graphs, "model_backward": write_model_backward,
+           "safetensors": write_safetensors_fixture, "attention": write_attention}
+
 if __name__ == "__main__":
-    main()
-    write_model_graphs()
-    write_model_backward()
-    write_safetensors_fixture()
+    # No argument: every fixture; else only the named ones (e.g. `attention`).
+    for name in (sys.argv[1:] or list(WRITERS)):
+        WRITERS[name]()
