@@ -41,6 +41,7 @@ from mimir_hip import datagen as G  # noqa: E402
 
 METRIC = "achieved HBM GB/s (% of MI355X peak) + rows/s per fused layer op vs host CPU"
 PEAK_GBS = 8000.0  # MI355X HBM3E
+PEAK_F32_MFMA_TFLOPS = 157.3  # MI355X dense fp32 matrix-core peak
 MALL_BYTES = 256 << 20
 MIN_FOOTPRINT = 5 * MALL_BYTES  # rotate buffer sets until one pass covers 1.25 GiB
 MAX_SETS = 32
@@ -55,9 +56,12 @@ class OpBench:
     """One op of one configuration: its inputs on the device (nsets copies)
     and a closure that launches it on set i."""
 
-    def __init__(self, key, config, desc, kernel, nbytes, rows, row_unit, make, outputs=None):
+    def __init__(self, key, config, desc, kernel, nbytes, rows, row_unit, make, outputs=None, flops=None):
         self.key, self.config, self.desc, self.kernel = key, config, desc, kernel
         self.nbytes, self.rows, self.row_unit = nbytes, rows, row_unit
+        # Matrix-core ops: algorithmic flops per launch (the roofline is the
+        # fp32 MFMA peak, not HBM).
+        self.flops = flops
         self.make = make  # make(ctx, nsets) -> (step(i), buffers)
         # outputs(buffers) -> {name: DeviceArray or ndarray}: what one launch
         # on set 0 produced, for the parity check of the cpu_baseline leg
@@ -94,6 +98,18 @@ def block_layers():
             dict(name="act", type="GELU", inputs=["n"], output="g"),
             dict(name="gate", type="Multiply", inputs=["g", "gate"], output="m"),
             dict(name="silu", type="SiLU", inputs=["m"], output="x")]
+
+
+def attention_flops(batch, heads, q_len, kv_len, head_dim, causal):
+    """Algorithmic flops of the attention core: 2*head_dim for each visible
+    (query, key) pair in QK^T and again in PV (the softmax's exponentials are
+    not counted).  Causal: query i sees min(i + 1, kv_len) keys."""
+    if causal:
+        i = np.arange(q_len)
+        pairs = int(np.minimum(i + 1, kv_len).sum())
+    else:
+        pairs = q_len * kv_len
+    return 4 * head_dim * pairs * batch * heads
 
 
 def build_ops(rows_override=None):
@@ -134,6 +150,25 @@ def build_ops(rows_override=None):
         return (lambda i: ctx.softmax(sets[i][0], sets[i][1], 262144, 1024, M.SOFTMAX_DIV_EPS)), sets
     ops.append(OpBench("cfg2_softmax", 2, "causal row softmax fp32 [8x32x1024x1024]", "softmax_rows_vec",
                        2 * 262144 * 1024 * f4, 262144, "rows", make_cfg2, lambda s: {"y": s[0][1]}))
+
+    # The attention core at configs[2]'s shape (8 sequences x 32 heads x 1024
+    # tokens, causal), head_dim 128, on a fused [8192 x 12288] QKV buffer: the
+    # softmax of configs[2] fused between QK^T and PV (matrix-core bound).
+    ab, al, ah, ad = 8, 1024, 32, 128
+    aw = ah * ad
+
+    def make_attention(ctx, nsets):
+        qkv = G.attention_qkv(ab, al, ah, ad)
+        sets = _replicate(ctx, [qkv, np.empty((ab * al, aw), np.float32)], nsets)
+        del qkv
+        return (lambda i: ctx.attention(sets[i][0], sets[i][0].offset(aw), sets[i][0].offset(2 * aw), sets[i][1],
+                                        ab, al, al, ah, ad, True, ld_q=3 * aw, ld_kv=3 * aw)), sets
+    ops.append(OpBench("f4_attention", 2,
+                       f"fused causal attention core fp32 [{ab} seq x {ah} heads x {al} tokens, head_dim {ad}], "
+                       f"fused QKV [{ab * al}x{3 * aw}] -> out [{ab * al}x{aw}]",
+                       "attention_fwd_mfma<128>", 4 * ab * al * aw * f4, ab * ah * al, "query rows",
+                       make_attention, lambda s: {"out": s[0][1]},
+                       flops=attention_flops(ab, ah, al, al, ad, True)))
 
     def make_cfg3a(ctx, nsets):
         table, ids = G.cfg3_gather()
@@ -379,13 +414,19 @@ def time_op(ctx, op, steps, warmup, spin_s=0.25):
                 b.free()
     us = ms * 1e3 / steps
     gbs = op.nbytes / (us * 1e-6) / 1e9
-    return {
+    rec = {
         "op": op.key, "config": op.config, "desc": op.desc, "kernel": op.kernel,
         "algorithmic_bytes": op.nbytes, "us_per_launch": round(us, 3), "GB_s": round(gbs, 1),
         "frac_of_peak": round(gbs / PEAK_GBS, 4), "rows_per_s": round(op.rows / (us * 1e-6), 1),
         "row_unit": op.row_unit, "launches": steps, "buffer_sets": nsets,
         "footprint_MiB": round(nsets * op.nbytes / 2**20, 1),
     }
+    if op.flops:
+        tf = op.flops / (us * 1e-6) / 1e12
+        rec.update({"bound": "mfma", "algorithmic_flops": op.flops, "TFLOP_s": round(tf, 2),
+                    "frac_of_peak": round(tf / PEAK_F32_MFMA_TFLOPS, 4), "peak": PEAK_F32_MFMA_TFLOPS,
+                    "peak_unit": "TFLOP/s (dense fp32 MFMA)", "frac_of_hbm_peak": round(gbs / PEAK_GBS, 4)})
+    return rec
 
 
 # ---------------------------------------------------------------------------
@@ -610,6 +651,18 @@ def cpu_leg(which, reps):
                     f"the full 2^25-element row through the reference's {kind} layer function, median of {reps}")
             else:
                 rec(key, O.time_port(port, reps), nb, 1, "port", f"the full 2^25-element row, oracle, median of {reps}")
+        elif key == "f4_attention":
+            # One (sequence, head) of the workload through the restatement of
+            # the reference core (LayerOps.hpp:1045-1089, single-threaded as
+            # the reference's core loops are); throughput in core flops.
+            qkv = G.attention_qkv(1, 1024, 32, 128)
+            q, k, v = (np.ascontiguousarray(qkv[:, i * 4096:i * 4096 + 128]) for i in range(3))
+            t = O.time_port(lambda: O.attention(q, k, v, 1, True), reps)
+            fl = attention_flops(1, 1, 1024, 1024, 128, True)
+            out[key] = {"value": round(fl / t / 1e9, 3), "unit": "GFLOP/s", "seconds": round(t, 6),
+                        "rows_per_s": round(1024 / t, 1), "cores": 1, "kind": "port",
+                        "sample": "1 of 256 (sequence, head) pairs: 1024 causal queries, head_dim 128, "
+                                  f"oracle_attention (bit-exact to the reference core), median of {reps}"}
         elif key in ("cfg3_embedding_bwd", "cfg3_embedding_bwd_zipf"):
             ids = (G.cfg3_ids() if key == "cfg3_embedding_bwd" else G.cfg3_ids_zipf()).ravel()[:4096].copy()
             dy = G.cfg3_embedding_grad()[:4096].copy()
@@ -829,6 +882,30 @@ def parity_leg(ctx, by_key, which):
                         "pass": all(r["pass"] for r in res.values()), "outputs": res}
             log(f"parity {key}: {'pass' if out[key]['pass'] else 'FAIL'} vs port "
                 + ", ".join(f"{n} max_abs {r['max_abs']:.3g}" for n, r in res.items()))
+        elif key == "f4_attention":
+            # Sampled (sequence, head) pairs of the full launch against the
+            # restatement (pinned bit-exact to the reference core) with the
+            # attention tolerance: 1e-5 of sum_j p_j |v_j| plus the propagated
+            # rounding of the float32 scores, twice (both sides round).
+            qkv = G.attention_qkv(8, 1024, 32, 128)
+            got = gpu_outputs(by_key[key], {"out": np.empty((8192, 4096), np.float32)})["out"]
+            res = {}
+            for bi, h in ((0, 0), (3, 17), (7, 31)):
+                rows = slice(bi * 1024, (bi + 1) * 1024)
+                q, k, v = (np.ascontiguousarray(qkv[rows, i * 4096 + h * 128:i * 4096 + (h + 1) * 128])
+                           for i in range(3))
+                ref = O.attention(q, k, v, 1, True)
+                _, mag, cond = O.attention_float64(q, k, v, 1, True, O.attention_scale(128))
+                res[f"out (seq {bi}, head {h})"] = _agreement(got[rows, h * 128:(h + 1) * 128], ref, False,
+                                                              mag + 2 * cond / 1e-5)
+            res["out (first query of every head)"] = _agreement(
+                got.reshape(8, 1024, 4096)[:, 0], qkv.reshape(8, 1024, 12288)[:, 0, 8192:], True)
+            out[key] = {"vs": "port (oracle_attention, bit-exact to the reference's self_attention_forward core)",
+                        "sample": "3 of 256 (sequence, head) pairs in full, and every head's first query "
+                                  "(one visible key: V's row exactly)",
+                        "pass": all(r["pass"] for r in res.values()), "outputs": res}
+            log(f"parity {key}: {'pass' if out[key]['pass'] else 'FAIL'} vs port "
+                + ", ".join(f"{n} max_abs {r['max_abs']:.3g}" for n, r in res.items()))
         elif key == "cfg4_runtime_block_train" and MR.available():
             rows = 512
             x, res = G.cfg4_add(rows=rows)
@@ -1009,11 +1086,15 @@ def main():
     for r in sweep:
         if r["op"] in cpu:
             c = cpu[r["op"]]
-            r["cpu_GB_s"] = c["value"]
             r["cpu_kind"] = c["kind"]
             r["cpu_us_sample"] = round(c["seconds"] * 1e6, 1)
             r["cpu_sample"] = c["sample"]
-            r["speedup_vs_cpu"] = round(r["GB_s"] / c["value"], 1)
+            if c["unit"] == "GFLOP/s":
+                r["cpu_GFLOP_s"] = c["value"]
+                r["speedup_vs_cpu"] = round(r["TFLOP_s"] * 1e3 / c["value"], 1)
+            else:
+                r["cpu_GB_s"] = c["value"]
+                r["speedup_vs_cpu"] = round(r["GB_s"] / c["value"], 1)
         if r["op"] in parity:
             r["parity"] = parity[r["op"]]
 
@@ -1054,7 +1135,17 @@ def main():
         },
         "rows_per_s": res["rows_per_s"],
         "frac_of_peak": res["frac_of_peak"],
-        "roofline": {
+        "roofline": ({
+            "bound": "mfma",
+            "kernel": head.kernel,
+            "achieved": res["TFLOP_s"],
+            "peak": PEAK_F32_MFMA_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": res["frac_of_peak"],
+            "traffic": None if traffic is None else traffic.get("traffic_bytes"),
+            "algorithmic_flops": head.flops,
+            "algorithmic_bytes": head.nbytes,
+        } if head.flops else {
             "bound": "hbm",
             "kernel": head.kernel,
             "achieved": res["GB_s"],
@@ -1066,7 +1157,7 @@ def main():
             "copy_same_bytes": {"GB_s": same["GB_s"], "frac": same["frac_of_peak"],
                                 "us_per_launch": same["us_per_launch"]},
             "frac_of_copy": round(res["GB_s"] / same["GB_s"], 4),
-        },
+        }),
         "cpu_baseline": None if cb is None else {
             "value": cb["value"], "unit": cb["unit"], "cores": cb["cores"], "kind": cb["kind"],
             "sample": cb["sample"], "rows_per_s": cb["rows_per_s"], **host},
@@ -1074,7 +1165,12 @@ def main():
         "ops_fields": ["us_per_launch", "GB_s", "frac_of_peak", "parity_pass", "traffic_over_algorithmic"],
         "ops": {r["op"]: [r["us_per_launch"], r["GB_s"], r.get("frac_of_peak"),
                           r["parity"]["pass"] if "parity" in r else None,
-                          r.get("traffic_over_algorithmic")] for r in sweep},
+                          r.get("traffic_over_algorithmic")] for r in sweep if r.get("bound") != "mfma"},
+        "mfma_ops_fields": ["us_per_launch", "TFLOP_s", "frac_of_fp32_mfma_peak", "parity_pass",
+                            "cpu_GFLOP_s"],
+        "mfma_ops": {r["op"]: [r["us_per_launch"], r["TFLOP_s"], r["frac_of_peak"],
+                               r["parity"]["pass"] if "parity" in r else None, r.get("cpu_GFLOP_s")]
+                     for r in sweep if r.get("bound") == "mfma"},
     }
     full = dict(line, parity=parity.get(head.key), ops=sweep)
     out = args.full_out

@@ -9,6 +9,8 @@
 // and keeps a running max / sum per query ("online softmax"; Milakov and
 // Gimelshein 2018, as used by FlashAttention, Dao et al. 2022), rescaling its
 // partial output when the max grows, and divides by (sum + 1e-9) at the end.
+// Q is multiplied by scale * log2(e) once, so the scores come out of the
+// matrix core in base-2 units and each probability is one v_exp_f32.
 //
 // Matrix-core mapping.  v_mfma_f32_32x32x2_f32 computes D[32x32] += A[32x2] *
 // B[2x32]; lane l supplies A[l%32][l/32] and B[l/32][l%32] and receives
@@ -30,15 +32,25 @@
 //   output rows come out as DP/32 consecutive dimensions (one 16-byte store
 //   for DP = 128).
 //
-// Workgroup: 4 waves, 32 queries each (128 queries of one (sequence, head)),
-// K / V tiles of 32 keys double-buffered in LDS (one barrier per tile), the
-// next tile's global loads in flight while the current one is computed.
+// Pipeline.  A wave issues its instructions in order, and a v_mfma holds the
+// matrix pipe for 64 cycles, so the softmax's vector work only overlaps the
+// matrix core if it sits between independent MFMAs.  Iteration t therefore
+// computes the scores of tile t+1 (S_next = K_{t+1} Q^T) interleaved
+// instruction by instruction with the softmax of tile t (whose scores came
+// from iteration t-1), then O += V_t^T P_t.  K runs one tile ahead of V: LDS
+// holds a K ring and a V ring of two tiles each; iteration t reads K_{t+1}
+// and V_t and refills the slots of K_t and V_{t-1} with K_{t+2} and V_{t+1},
+// whose global loads were issued at the start of the iteration, then one
+// barrier.
+//
+// Workgroup: 4 waves, 32 queries each (128 queries of one (sequence, head)).
 // Causal: a workgroup stops at its last query's diagonal, a wave skips the
-// tiles past its own diagonal and masks inside the diagonal tile only.
-// Grid: the query blocks of one (sequence, head) are placed on one XCD (the
-// hardware deals workgroups to the 8 XCDs round-robin), so K and V are fetched
-// once into that XCD's L2 and re-read from there; heavier (later, causal)
-// query blocks start first.
+// tiles past its own diagonal and masks inside its last tile only (the
+// diagonal, or the sequence's ragged end).
+// Grid: the hardware deals workgroups to the 8 XCDs round-robin.  When the
+// (sequence, head) count divides by 8, each XCD owns an eighth of them (their
+// K and V stay in that XCD's L2) and runs its query blocks longest first
+// across all of its heads, so the short causal blocks fill the tail.
 #include "common.hpp"
 #include "internal.hpp"
 
@@ -57,6 +69,7 @@ constexpr int kQPerBlock = kQPerWave * kWaves;  // 128
 constexpr int kKeyTile = 32;
 constexpr int kThreads = kWaves * kWave;        // 256
 constexpr int kXcds = 8;
+constexpr float kLog2e = 1.4426950408889634f;
 
 struct AttnArgs {
     const float* q;
@@ -67,20 +80,22 @@ struct AttnArgs {
     int32_t q_len, kv_len, heads, head_dim;
     int32_t n_qblocks;            // ceil(q_len / 128)
     uint32_t total_blocks;        // batch * heads * n_qblocks
-    float scale;                  // applied to the dot products, as the reference does
+    float qscale;                 // scale * log2(e), applied to Q
     int32_t causal;
 };
 
-// LDS layout of one buffer: K tile [32][DP + 4] (the pad staggers the rows
-// across banks for the column-wise reads), then V tile [32][DP].
+// LDS: the K ring [2][32][DP + 4] (the pad staggers the rows across banks for
+// the column-wise reads), then the V ring [2][32][DP].
 template <int DP>
 struct Lds {
     static constexpr int kLd = DP + 4;
     static constexpr int vLd = DP;
-    static constexpr int kFloats = kKeyTile * kLd;
-    static constexpr int buf = kFloats + kKeyTile * vLd;
+    static constexpr int kTile = kKeyTile * kLd;
+    static constexpr int vTile = kKeyTile * vLd;
+    static constexpr int vRing = 2 * kTile;
+    static constexpr int total = 2 * kTile + 2 * vTile;
     static constexpr int f4PerRow = DP / 4;
-    static constexpr int loads = kKeyTile * f4PerRow / kThreads;  // float4 per thread per operand
+    static constexpr int loads = kKeyTile * f4PerRow / kThreads;  // float4 per thread per tile
     static_assert(loads >= 1 && kKeyTile * f4PerRow == loads * kThreads, "tile / block mismatch");
 };
 
@@ -126,23 +141,25 @@ __device__ __forceinline__ f4 zero_outside(f4 x, bool row_ok, int c, int head_di
     return x;
 }
 
-// Workgroup -> (sequence * heads + head, query block).  Consecutive logical
-// indices share a (sequence, head); they are given to one XCD when the grid
-// divides evenly.  Within a (sequence, head) the last query block comes first.
+// Workgroup -> (sequence * heads + head, query block): see the file comment.
 __device__ __forceinline__ void block_coords(const AttnArgs& a, uint32_t bid, uint32_t* bh, int* qb) {
-    uint32_t logical = bid;
-    if (a.total_blocks % kXcds == 0) logical = (bid % kXcds) * (a.total_blocks / kXcds) + bid / kXcds;
-    *bh = logical / static_cast<uint32_t>(a.n_qblocks);
-    *qb = a.n_qblocks - 1 - static_cast<int>(logical % static_cast<uint32_t>(a.n_qblocks));
+    const uint32_t n_bh = a.total_blocks / static_cast<uint32_t>(a.n_qblocks);
+    uint32_t first = 0, owned = n_bh, idx = bid;
+    if (n_bh % kXcds == 0) {
+        owned = n_bh / kXcds;
+        first = (bid % kXcds) * owned;
+        idx = bid / kXcds;
+    }
+    *qb = a.n_qblocks - 1 - static_cast<int>(idx / owned);
+    *bh = first + idx % owned;
 }
 
 template <int DP, bool VEC>
 __global__ __launch_bounds__(kThreads, 2) void attention_fwd_mfma(AttnArgs a) {
     using L = Lds<DP>;
-    constexpr int kSteps = DP / 2;   // MFMA k-steps over the head dimension
-    constexpr int kHalf = DP / 2;    // dimensions per lane half
-    constexpr int kDb = DP / 32;     // output dimension blocks
-    __shared__ __attribute__((aligned(16))) float lds[2 * L::buf];
+    constexpr int kHalf = DP / 2;  // dimensions per lane half = MFMA k-steps of S
+    constexpr int kDb = DP / 32;   // output dimension blocks
+    __shared__ __attribute__((aligned(16))) float lds[L::total];
 
     uint32_t bh;
     int qb;
@@ -173,8 +190,12 @@ __global__ __launch_bounds__(kThreads, 2) void attention_fwd_mfma(AttnArgs a) {
     if (qw0 >= a.q_len) wave_key_end = 0;
     const int n_tiles = (key_end + kKeyTile - 1) / kKeyTile;
     const int wave_tiles = (wave_key_end + kKeyTile - 1) / kKeyTile;
+    // Keys of this lane's query: the rest of its last tile is masked
+    // (causal: key > query; all: key >= kv_len).
+    const int lane_key_end = min(a.kv_len, a.causal ? my_q + 1 : a.kv_len);
 
-    // This lane's Q values: query my_q, dimensions hf*kHalf + [0, kHalf).
+    // This lane's Q values, times scale*log2(e): query my_q, dimensions
+    // hf*kHalf + [0, kHalf).
     float qreg[kHalf];
     {
         const float* qrow = qbase + static_cast<int64_t>(min(my_q, a.q_len - 1)) * a.ld_q;
@@ -182,17 +203,17 @@ __global__ __launch_bounds__(kThreads, 2) void attention_fwd_mfma(AttnArgs a) {
 #pragma unroll
         for (int j = 0; j < kHalf / 4; ++j) {
             const f4 t = load4<VEC>(qrow, hf * kHalf + 4 * j, valid);
-            qreg[4 * j + 0] = t.x;
-            qreg[4 * j + 1] = t.y;
-            qreg[4 * j + 2] = t.z;
-            qreg[4 * j + 3] = t.w;
+            qreg[4 * j + 0] = t.x * a.qscale;
+            qreg[4 * j + 1] = t.y * a.qscale;
+            qreg[4 * j + 2] = t.z * a.qscale;
+            qreg[4 * j + 3] = t.w * a.qscale;
         }
     }
 
-    // Cooperative tile load: thread tid moves float4 number tid + 256*r of
-    // each operand (row = key within the tile, column group c).  VEC: buffer
-    // loads through a descriptor based at the tile's first row whose range
-    // ends after the sequence's last row, so rows past kv_len read as zeros
+    // Cooperative tile load: thread tid moves float4 number tid + 256*r of a
+    // tile (row = key within the tile, column group c).  VEC: buffer loads
+    // through a descriptor based at the tile's first row whose range ends
+    // after the sequence's last row, so rows past kv_len read as zeros
     // without a memory access; the per-thread byte offsets are loop
     // invariants (no address registers recycled while the loads are in
     // flight).  Columns are clamped below head_dim (never past the row).
@@ -207,20 +228,16 @@ __global__ __launch_bounds__(kThreads, 2) void attention_fwd_mfma(AttnArgs a) {
             voff[r] = static_cast<uint32_t>((row * a.ld_kv + c) * 4);
         }
     }
-    auto fetch = [&](int tile) {
+    auto fetch = [&](const float* base, int tile, f4* dst) {
         if constexpr (VEC) {
             const int64_t first = static_cast<int64_t>(tile) * kKeyTile * a.ld_kv;
             const int rows = min(kKeyTile, a.kv_len - tile * kKeyTile);
             const int bytes = static_cast<int>(rows * a.ld_kv * 4);
-            const __amdgpu_buffer_rsrc_t kr =
-                __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(kbase + first), 0, bytes, kBufferWord3);
-            const __amdgpu_buffer_rsrc_t vr =
-                __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(vbase + first), 0, bytes, kBufferWord3);
+            const __amdgpu_buffer_rsrc_t rs =
+                __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base + first), 0, bytes, kBufferWord3);
 #pragma unroll
-            for (int r = 0; r < L::loads; ++r) {
-                kst[r] = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(kr, voff[r], 0, 0));
-                vst[r] = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(vr, voff[r], 0, 0));
-            }
+            for (int r = 0; r < L::loads; ++r)
+                dst[r] = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(rs, voff[r], 0, 0));
         } else {
 #pragma unroll
             for (int r = 0; r < L::loads; ++r) {
@@ -228,101 +245,132 @@ __global__ __launch_bounds__(kThreads, 2) void attention_fwd_mfma(AttnArgs a) {
                 const int row = f / L::f4PerRow;
                 const int c = 4 * (f % L::f4PerRow);
                 const int64_t off = static_cast<int64_t>(min(tile * kKeyTile + row, a.kv_len - 1)) * a.ld_kv;
-                kst[r] = load4_clamped(kbase + off, c, a.head_dim);
-                vst[r] = load4_clamped(vbase + off, c, a.head_dim);
+                dst[r] = load4_clamped(base + off, c, a.head_dim);
             }
         }
     };
-    auto stash = [&](int tile, int buf) {
-        float* kl = lds + buf * L::buf;
-        float* vl = kl + L::kFloats;
+    auto stash = [&](const f4* src, int tile, float* dst, int ld) {
 #pragma unroll
         for (int r = 0; r < L::loads; ++r) {
             const int f = tid + r * kThreads;
             const int row = f / L::f4PerRow;
             const int c = 4 * (f % L::f4PerRow);
             const bool row_ok = tile * kKeyTile + row < a.kv_len;
-            *reinterpret_cast<f4*>(kl + row * L::kLd + c) = zero_outside(kst[r], row_ok, c, a.head_dim);
-            *reinterpret_cast<f4*>(vl + row * L::vLd + c) = zero_outside(vst[r], row_ok, c, a.head_dim);
+            *reinterpret_cast<f4*>(dst + row * ld + c) = zero_outside(src[r], row_ok, c, a.head_dim);
         }
+    };
+    float* const kring = lds;
+    float* const vring = lds + L::vRing;
+
+    // S^T = K Q^T over the head dimension, K from ring slot `slot`.
+    auto scores = [&](int slot) {
+        f16v s = f16v{};
+        const float* krow = kring + slot * L::kTile + li * L::kLd + hf * kHalf;
+#pragma unroll
+        for (int j = 0; j < kHalf / 4; ++j) {
+            const f4 kv = *reinterpret_cast<const f4*>(krow + 4 * j);
+            s = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.x, qreg[4 * j + 0], s, 0, 0, 0);
+            s = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.y, qreg[4 * j + 1], s, 0, 0, 0);
+            s = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.z, qreg[4 * j + 2], s, 0, 0, 0);
+            s = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.w, qreg[4 * j + 3], s, 0, 0, 0);
+        }
+        return s;
     };
 
     f16v o[kDb];
 #pragma unroll
     for (int d = 0; d < kDb; ++d) o[d] = f16v{};
-    float m_run = -1e30f;  // the reference's initial max (LayerOps.hpp:1052)
+    float m_run = -1e30f;  // running max (base-2 units); the reference starts at -1e30 (LayerOps.hpp:1052)
     float l_run = 0.f;     // this half's share of the running sum
-    constexpr float kLog2e = 1.4426950408889634f;
 
-    if (n_tiles > 0) {
-        fetch(0);
-        stash(0, 0);
-    }
-    __syncthreads();
-    for (int t = 0; t < n_tiles; ++t) {
-        const int buf = t & 1;
-        fetch(min(t + 1, n_tiles - 1));  // the last iteration refetches into the idle buffer
-        if (t < wave_tiles) {
-            const float* kl = lds + buf * L::buf;
-            const float* vl = kl + L::kFloats;
-            // S^T = K Q^T over the head dimension.
-            f16v s = f16v{};
-            const float* krow = kl + li * L::kLd + hf * kHalf;
+    // Online softmax of one tile's scores (in place: s becomes P), rescale of
+    // O and the running sum, then O^T += V^T P^T with V from ring slot
+    // `slot`.  mask: keys at or past lane_key_end are excluded.
+    auto softmax_pv = [&](f16v& s, int slot, bool mask, int key0) {
+        if (mask) {
+            const int lim = lane_key_end - key0 - 4 * hf;
 #pragma unroll
-            for (int j = 0; j < kSteps / 4; ++j) {
-                const f4 kv = *reinterpret_cast<const f4*>(krow + 4 * j);
-                s = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.x, qreg[4 * j + 0], s, 0, 0, 0);
-                s = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.y, qreg[4 * j + 1], s, 0, 0, 0);
-                s = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.z, qreg[4 * j + 2], s, 0, 0, 0);
-                s = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.w, qreg[4 * j + 3], s, 0, 0, 0);
-            }
-            // Scores, mask, tile max (the masked ones do not enter it, :1054-1057).
-            const int key0 = t * kKeyTile + 4 * hf;
-            const bool need_mask = (t + 1) * kKeyTile > a.kv_len || (a.causal && (t + 1) * kKeyTile - 1 > qw0);
-            float tmax = -1e30f;
+            for (int r = 0; r < 16; ++r) s[r] = 8 * (r / 4) + (r % 4) < lim ? s[r] : -INFINITY;
+        }
+        float tmax = fmaxf(fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3])), fmaxf(fmaxf(s[4], s[5]), fmaxf(s[6], s[7])));
+        tmax = fmaxf(tmax, fmaxf(fmaxf(fmaxf(s[8], s[9]), fmaxf(s[10], s[11])),
+                                 fmaxf(fmaxf(s[12], s[13]), fmaxf(s[14], s[15]))));
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
+        const float m_new = fmaxf(m_run, tmax);
+        const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+        m_run = m_new;
+        float psum = 0.f;
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                s[r] *= a.scale;
-                if (need_mask) {
-                    const int key = key0 + 8 * (r / 4) + (r % 4);
-                    const bool masked = key >= a.kv_len || (a.causal && key > my_q);
-                    s[r] = masked ? -INFINITY : s[r];
-                }
-                tmax = fmaxf(tmax, s[r]);
-            }
-            tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
-            const float m_new = fmaxf(m_run, tmax);
-            const float alpha = __builtin_amdgcn_exp2f((m_run - m_new) * kLog2e);
-            m_run = m_new;
-            float psum = 0.f;
+        for (int r = 0; r < 16; ++r) {
+            s[r] = __builtin_amdgcn_exp2f(s[r] - m_new);  // exp2(-inf) = 0: masked keys
+            psum += s[r];
+        }
+        l_run = l_run * alpha + psum;
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                s[r] = __builtin_amdgcn_exp2f((s[r] - m_new) * kLog2e);  // exp2(-inf) = 0: masked keys
-                psum += s[r];
-            }
-            l_run = l_run * alpha + psum;
+        for (int d = 0; d < kDb; ++d) o[d] *= alpha;
+        const float* vl = vring + slot * L::vTile;
+        // k-slot h of step r is key(r, h) = 8*(r/4) + 4h + r%4.
 #pragma unroll
-            for (int d = 0; d < kDb; ++d) o[d] *= alpha;
-            // O^T += V^T P^T: k-slot h of step r is key(r, h) = 8*(r/4) + 4h + r%4.
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const float* vrow = vl + (8 * (r / 4) + 4 * hf + (r % 4)) * L::vLd + kDb * li;
-                if constexpr (kDb == 4) {
-                    const f4 vv = *reinterpret_cast<const f4*>(vrow);
-                    o[0] = __builtin_amdgcn_mfma_f32_32x32x2f32(vv.x, s[r], o[0], 0, 0, 0);
-                    o[1] = __builtin_amdgcn_mfma_f32_32x32x2f32(vv.y, s[r], o[1], 0, 0, 0);
-                    o[2] = __builtin_amdgcn_mfma_f32_32x32x2f32(vv.z, s[r], o[2], 0, 0, 0);
-                    o[3] = __builtin_amdgcn_mfma_f32_32x32x2f32(vv.w, s[r], o[3], 0, 0, 0);
-                } else if constexpr (kDb == 2) {
-                    const f2 vv = *reinterpret_cast<const f2*>(vrow);
-                    o[0] = __builtin_amdgcn_mfma_f32_32x32x2f32(vv.x, s[r], o[0], 0, 0, 0);
-                    o[1] = __builtin_amdgcn_mfma_f32_32x32x2f32(vv.y, s[r], o[1], 0, 0, 0);
-                } else {
-                    o[0] = __builtin_amdgcn_mfma_f32_32x32x2f32(vrow[0], s[r], o[0], 0, 0, 0);
-                }
+        for (int r = 0; r < 16; ++r) {
+            const float* vrow = vl + (8 * (r / 4) + 4 * hf + (r % 4)) * L::vLd + kDb * li;
+            if constexpr (kDb == 4) {
+                const f4 vv = *reinterpret_cast<const f4*>(vrow);
+                o[0] = __builtin_amdgcn_mfma_f32_32x32x2f32(vv.x, s[r], o[0], 0, 0, 0);
+                o[1] = __builtin_amdgcn_mfma_f32_32x32x2f32(vv.y, s[r], o[1], 0, 0, 0);
+                o[2] = __builtin_amdgcn_mfma_f32_32x32x2f32(vv.z, s[r], o[2], 0, 0, 0);
+                o[3] = __builtin_amdgcn_mfma_f32_32x32x2f32(vv.w, s[r], o[3], 0, 0, 0);
+            } else if constexpr (kDb == 2) {
+                const f2 vv = *reinterpret_cast<const f2*>(vrow);
+                o[0] = __builtin_amdgcn_mfma_f32_32x32x2f32(vv.x, s[r], o[0], 0, 0, 0);
+                o[1] = __builtin_amdgcn_mfma_f32_32x32x2f32(vv.y, s[r], o[1], 0, 0, 0);
+            } else {
+                o[0] = __builtin_amdgcn_mfma_f32_32x32x2f32(vrow[0], s[r], o[0], 0, 0, 0);
             }
         }
-        stash(min(t + 1, n_tiles - 1), buf ^ 1);
+    };
+
+    // Prologue: K_0, V_0 and K_1 in LDS, S_0 computed.
+    if (n_tiles > 0) {
+        fetch(kbase, 0, kst);
+        fetch(vbase, 0, vst);
+        stash(kst, 0, kring, L::kLd);
+        stash(vst, 0, vring, L::vLd);
+    }
+    if (n_tiles > 1) {
+        fetch(kbase, 1, kst);
+        stash(kst, 1, kring + L::kTile, L::kLd);
+    }
+    __syncthreads();
+    f16v s_cur = f16v{};
+    if (wave_tiles > 0) s_cur = scores(0);
+    // Iteration 0 refills K_0's slot: every wave must have read it first
+    // (later refills are ordered by the previous iteration's barrier).
+    __syncthreads();
+
+    for (int t = 0; t < n_tiles; ++t) {
+        // Global loads of K_{t+2} and V_{t+1} (clamped to the last tile; the
+        // slots they fill are not read again once they would be past it).
+        fetch(kbase, min(t + 2, n_tiles - 1), kst);
+        fetch(vbase, min(t + 1, n_tiles - 1), vst);
+        if (t + 1 < wave_tiles) {
+            // S_{t+1} interleaved with the softmax of S_t; a tile before the
+            // wave's last one is never masked.
+            const f16v s_next = scores((t + 1) & 1);
+            softmax_pv(s_cur, t & 1, false, t * kKeyTile);
+#pragma unroll
+            for (int i = 0; i < kHalf / 4; ++i) {
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one LDS read (K)
+                __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);  // four score MFMAs
+                __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);  // six softmax VALU ops
+            }
+            s_cur = s_next;
+        } else if (t < wave_tiles) {
+            const bool mask = (t + 1) * kKeyTile > a.kv_len || (a.causal && (t + 1) * kKeyTile - 1 > qw0);
+            if (mask) softmax_pv(s_cur, t & 1, true, t * kKeyTile);
+            else softmax_pv(s_cur, t & 1, false, t * kKeyTile);
+        }
+        stash(kst, min(t + 2, n_tiles - 1), kring + (t & 1) * L::kTile, L::kLd);
+        stash(vst, min(t + 1, n_tiles - 1), vring + ((t + 1) & 1) * L::vTile, L::vLd);
         __syncthreads();
     }
 
@@ -379,6 +427,7 @@ int mimir_attention_fwd(mimir_ctx* ctx, const float* q, int64_t ld_q, const floa
                   (long long)ld_kv, (long long)ld_out, (long long)width);
     MIMIR_REQUIRE(ctx, q_len < (int64_t{1} << 30) && kv_len < (int64_t{1} << 30) && heads < (int64_t{1} << 30),
                   "attention: sequence or head count too large");
+    MIMIR_REQUIRE(ctx, std::isfinite(scale), "attention: scale must be finite");
     if (batch == 0 || q_len == 0) return MIMIR_OK;
     MIMIR_REQUIRE(ctx, q && out && (kv_len == 0 || (k && v)), "attention: null pointer");
     const int64_t nqb = (q_len + kQPerBlock - 1) / kQPerBlock;
@@ -399,7 +448,7 @@ int mimir_attention_fwd(mimir_ctx* ctx, const float* q, int64_t ld_q, const floa
     a.head_dim = static_cast<int32_t>(head_dim);
     a.n_qblocks = static_cast<int32_t>(nqb);
     a.total_blocks = static_cast<uint32_t>(batch * heads * nqb);
-    a.scale = scale;
+    a.qscale = scale * kLog2e;
     a.causal = causal ? 1 : 0;
     // The vector path's buffer descriptors span one 32-row tile: 32 rows of
     // ld_kv floats must stay below 2^31 bytes.

@@ -97,6 +97,14 @@ def cfg4_add(rows=8192, cols=4096):
 # embedding's scaled by 0.01 like a small loss gradient)
 # --------------------------------------------------------------------------
 
+def attention_qkv(batch=8, seq=1024, heads=32, head_dim=128):
+    """The fused QKV buffer of the attention benchmark: [batch*seq, 3*E]
+    (E = heads*head_dim) N(0,1), Q | K | V column blocks -- the layout of
+    self_attention_forward's projection output (LayerOps.hpp:1031-1043) --
+    at configs[2]'s attention shape (8 sequences x 32 heads x 1024 tokens)."""
+    return normal(2, 6, (batch * seq, 3 * heads * head_dim))
+
+
 def cfg4_grad(shape, tensor=8):
     return normal(4, tensor, shape)
 

@@ -407,6 +407,51 @@ def attention(q, k, v, heads, causal=False, scale=None):
     return y[0] if squeeze else y
 
 
+U32 = 2.0 ** -24  # float32 unit roundoff
+
+
+def attention_float64(q, k, v, heads, causal, scale):
+    """float64 softmax attention and the scales of its float32 rounding:
+    (out, mag, cond), all shaped like q ([.., q_len, width]).
+    mag  = sum_j p_j |v_j|: the scale of the float32 rounding of the weighted
+           sum (two summation orders differ by ~u * mag);
+    cond = u * sqrt(head_dim) * sum_j p_j A_j (|v_j| + |out|), A_j = scale *
+           sum_k |q_k k_k|: the first-order effect on the output of rounding
+           the float32 scores (d out / d s_j = p_j (v_j - out); a D-term
+           float32 dot product is off by ~u sqrt(D) A_j).
+    The path's tolerance for attention is max(1e-6, 1e-5 * max(|ref|, mag))
+    + cond."""
+    q, k, v = (np.asarray(a, np.float64) for a in (q, k, v))
+    squeeze = q.ndim == 2
+    if squeeze:
+        q, k, v = q[None], k[None], v[None]
+    b, lq, width = q.shape
+    lk = k.shape[1]
+    hd = width // heads
+    sc = float(np.float32(scale))
+    out = np.zeros((b, lq, width))
+    mag = np.zeros((b, lq, width))
+    cond = np.zeros((b, lq, width))
+    mask = np.arange(lk)[None, :] > np.arange(lq)[:, None]
+    for h in range(heads):
+        sl = slice(h * hd, (h + 1) * hd)
+        s = np.einsum("bid,bjd->bij", q[..., sl], k[..., sl]) * sc
+        a = np.einsum("bid,bjd->bij", np.abs(q[..., sl]), np.abs(k[..., sl])) * abs(sc)
+        if causal:
+            s = np.where(mask[None], -np.inf, s)
+        s = s - s.max(axis=2, keepdims=True) if lk else s
+        p = np.exp(s)
+        p /= np.maximum(p.sum(axis=2, keepdims=True), 1e-300)
+        out[..., sl] = np.einsum("bij,bjd->bid", p, v[..., sl])
+        mag[..., sl] = np.einsum("bij,bjd->bid", p, np.abs(v[..., sl]))
+        pa = p * a
+        cond[..., sl] = (np.einsum("bij,bjd->bid", pa, np.abs(v[..., sl])) +
+                         pa.sum(axis=2)[..., None] * np.abs(out[..., sl])) * (U32 * np.sqrt(hd))
+    if squeeze:
+        return out[0], mag[0], cond[0]
+    return out, mag, cond
+
+
 # --------------------------------------------------------------------------
 # The reference's own functions (compiled in place)
 # --------------------------------------------------------------------------

@@ -9,6 +9,8 @@ is one product 1*w plus products 0*w), so the reference's output IS its
 attention core on Q / K / V = the selected rows of the projection weights."""
 import numpy as np
 
+import oracle as O
+
 # (seq_len, embed_dim, num_heads): head_dim = embed_dim / num_heads.
 SELF_CASES = [(1, 8, 1), (8, 8, 1), (5, 16, 2), (24, 32, 4), (33, 32, 1), (64, 64, 2), (100, 128, 1),
               (130, 96, 3), (40, 48, 3), (70, 80, 1)]
@@ -42,49 +44,12 @@ def cross_case(q_len, kv_len, e, amp, seed):
     return xq, xkv, wq, wkv, q, kv[:, :e].copy(), kv[:, e:].copy()
 
 
-U32 = 2.0 ** -24  # float32 unit roundoff
-
-
 def attention64(q, k, v, heads, causal, scale):
-    """float64 softmax attention: (out, mag, cond).
-    mag  = sum_j p_j |v_j|: the scale of the float32 rounding of the weighted
-           sum (the sum-aware tolerance of tests/_parity.py);
-    cond = u * sqrt(head_dim) * sum_j p_j A_j (|v_j| + |out|), A_j = scale *
-           sum_k |q_k k_k|: the first-order effect on the output of rounding
-           the float32 scores (d out / d s_j = p_j (v_j - out), |ds_j| ~ u
-           sqrt(D) A_j for a D-term float32 dot product).  The restatement
-           pinned to the reference stays within a quarter of it even where
-           the scores reach +-50 (tests/test_oracle_attention.py).
-    q: [.., q_len, width]."""
-    q, k, v = (np.asarray(a, np.float64) for a in (q, k, v))
-    squeeze = q.ndim == 2
-    if squeeze:
-        q, k, v = q[None], k[None], v[None]
-    b, lq, width = q.shape
-    lk = k.shape[1]
-    hd = width // heads
-    sc = float(np.float32(scale))
-    out = np.zeros((b, lq, width))
-    mag = np.zeros((b, lq, width))
-    cond = np.zeros((b, lq, width))
-    mask = np.arange(lk)[None, :] > np.arange(lq)[:, None]
-    for h in range(heads):
-        sl = slice(h * hd, (h + 1) * hd)
-        s = np.einsum("bid,bjd->bij", q[..., sl], k[..., sl]) * sc
-        a = np.einsum("bid,bjd->bij", np.abs(q[..., sl]), np.abs(k[..., sl])) * abs(sc)
-        if causal:
-            s = np.where(mask[None], -np.inf, s)
-        s = s - s.max(axis=2, keepdims=True) if lk else s
-        p = np.exp(s)
-        p /= np.maximum(p.sum(axis=2, keepdims=True), 1e-300)
-        out[..., sl] = np.einsum("bij,bjd->bid", p, v[..., sl])
-        mag[..., sl] = np.einsum("bij,bjd->bid", p, np.abs(v[..., sl]))
-        pa = p * a
-        cond[..., sl] = (np.einsum("bij,bjd->bid", pa, np.abs(v[..., sl])) +
-                         pa.sum(axis=2)[..., None] * np.abs(out[..., sl])) * (U32 * np.sqrt(hd))
-    if squeeze:
-        return out[0], mag[0], cond[0]
-    return out, mag, cond
+    """float64 softmax attention: (out, mag, cond) -- oracle.attention_float64,
+    whose cond term (the propagated rounding of the float32 scores) the
+    restatement pinned to the reference stays within a quarter of even where
+    the scores reach +-50 (tests/test_oracle_attention.py)."""
+    return O.attention_float64(q, k, v, heads, causal, scale)
 
 
 def assert_attention_close(got, ref, mag, cond, what=""):
