@@ -30,6 +30,7 @@
 
 #include <mimir_hip.h>
 
+#include <cmath>
 #include <cstddef>
 #include <cstdint>
 #include <mutex>
@@ -178,6 +179,14 @@ inline void rope(Context& c, const float* q, float* q_out, int64_t q_heads, cons
             "RoPE");
 }
 
+inline void attention(Context& c, const float* q, int64_t ld_q, const float* k, const float* v, int64_t ld_kv,
+                      float* out, int64_t ld_out, int64_t batch, int64_t q_len, int64_t kv_len, int64_t heads,
+                      int64_t head_dim, float scale, bool causal) {
+    c.check(mimir_attention_fwd(c.get(), q, ld_q, k, v, ld_kv, out, ld_out, batch, q_len, kv_len, heads,
+                                head_dim, scale, causal ? 1 : 0),
+            "Attention");
+}
+
 }  // namespace device
 
 namespace detail {
@@ -296,6 +305,49 @@ inline std::vector<float> silu_mul_forward(const std::vector<float>& gate, const
     const auto held = c.lock();  // buffers below are freed before it is released
     return detail::run2(c, gate, up, gate.size(), [&](const float* g, const float* u, float* y) {
         device::silu_mul(c, g, u, y, static_cast<int64_t>(gate.size()));
+    });
+}
+
+// Steps 2-5 of self_attention_forward (LayerOps.hpp:1028-1089) on the QKV
+// projection's output qkv [seq_len x 3*embed_dim] (Q | K | V column blocks):
+// returns the attended heads [seq_len x embed_dim] that the reference then
+// multiplies by out_weight (:1094).  The split copies are not made: Q, K and
+// V are read in place through the row stride.  Same checks and messages.
+inline std::vector<float> attention_core(const std::vector<float>& qkv, int seq_len, int embed_dim,
+                                         int num_heads = 1, bool causal = false) {
+    if (num_heads <= 0 || embed_dim % num_heads != 0)
+        throw std::runtime_error("SelfAttention: embed_dim must be divisible by num_heads");
+    if (seq_len < 0 || qkv.size() != static_cast<size_t>(seq_len) * 3 * static_cast<size_t>(embed_dim))
+        throw std::runtime_error("SelfAttention: input size mismatch");
+    const int head_dim = embed_dim / num_heads;
+    Context& c = Context::instance();
+    const auto held = c.lock();  // buffers below are freed before it is released
+    return detail::run1(c, qkv, static_cast<size_t>(seq_len) * embed_dim, [&](const float* d, float* y) {
+        device::attention(c, d, 3 * embed_dim, d + embed_dim, d + 2 * embed_dim, 3 * embed_dim, y, embed_dim, 1,
+                          seq_len, seq_len, num_heads, head_dim, 1.0f / std::sqrt(static_cast<float>(head_dim)),
+                          causal);
+    });
+}
+
+// The core of cross_attention_forward (LayerOps.hpp:1163-1209) on its
+// projections: Q [query_len x embed_dim] and KV [kv_len x 2*embed_dim]
+// (K | V column blocks).  Returns [query_len x embed_dim].
+inline std::vector<float> cross_attention_core(const std::vector<float>& Q, const std::vector<float>& KV,
+                                               int query_len, int kv_len, int embed_dim, int num_heads = 1,
+                                               bool causal = false) {
+    if (num_heads <= 0 || embed_dim % num_heads != 0)
+        throw std::runtime_error("CrossAttention: embed_dim must be divisible by num_heads");
+    if (query_len <= 0 || kv_len <= 0 || embed_dim <= 0)
+        throw std::runtime_error("CrossAttention: invalid dimensions");
+    if (Q.size() != static_cast<size_t>(query_len) * embed_dim ||
+        KV.size() != static_cast<size_t>(kv_len) * 2 * embed_dim)
+        throw std::runtime_error("CrossAttention: input size mismatch");
+    const int head_dim = embed_dim / num_heads;
+    Context& c = Context::instance();
+    const auto held = c.lock();  // buffers below are freed before it is released
+    return detail::run2(c, Q, KV, Q.size(), [&](const float* q, const float* kv, float* y) {
+        device::attention(c, q, embed_dim, kv, kv + embed_dim, 2 * embed_dim, y, embed_dim, 1, query_len, kv_len,
+                          num_heads, head_dim, 1.0f / std::sqrt(static_cast<float>(head_dim)), causal);
     });
 }
 

@@ -11,6 +11,9 @@ entry points (brit45/mimir-framework):
 * ``gelu_forward`` / ``silu_forward``  LayerOps.hpp:556-581
 * ``add_forward`` / ``multiply_forward``  LayerOps.hpp:142-230
 * ``embedding_forward``   the inline gather of Model.cpp:1152-1205 / 5301-5334
+* ``attention_core``      steps 2-5 of self_attention_forward, LayerOps.hpp:1028-1089,
+                          on the QKV projection's output (the softmax fused into QK^T / PV)
+* ``cross_attention_core`` the same core of cross_attention_forward, :1163-1209
 
 Inputs and outputs are host numpy vectors, so every call uploads, runs the
 HIP kernel and downloads (the PCIe-inclusive path the reference's callers
@@ -185,3 +188,34 @@ class LayerOps:
             d_ids.free()
             d_tab.free()
             y.free()
+
+    def attention_core(self, qkv, seq_len, embed_dim, num_heads=1, causal=False):
+        """Steps 2-5 of self_attention_forward on qkv [seq_len x 3*embed_dim]
+        (Q | K | V column blocks): the attended heads [seq_len x embed_dim],
+        flat, that the reference multiplies by out_weight."""
+        x = _f32(qkv)
+        if num_heads <= 0 or embed_dim % num_heads:
+            raise RuntimeError("SelfAttention: embed_dim must be divisible by num_heads")
+        if seq_len < 0 or x.size != seq_len * 3 * embed_dim:
+            raise RuntimeError("SelfAttention: input size mismatch")
+        hd = embed_dim // num_heads
+        e = embed_dim
+        return self._run(lambda d, y: self.ctx.attention(d, d.offset(e), d.offset(2 * e), y, 1, seq_len, seq_len,
+                                                         num_heads, hd, causal, ld_q=3 * e, ld_kv=3 * e),
+                         x, out_size=seq_len * e)
+
+    def cross_attention_core(self, Q, KV, query_len, kv_len, embed_dim, num_heads=1, causal=False):
+        """The core of cross_attention_forward on Q [query_len x E] and
+        KV [kv_len x 2E] (K | V column blocks)."""
+        q, kv = _f32(Q), _f32(KV)
+        if num_heads <= 0 or embed_dim % num_heads:
+            raise RuntimeError("CrossAttention: embed_dim must be divisible by num_heads")
+        if query_len <= 0 or kv_len <= 0 or embed_dim <= 0:
+            raise RuntimeError("CrossAttention: invalid dimensions")
+        if q.size != query_len * embed_dim or kv.size != kv_len * 2 * embed_dim:
+            raise RuntimeError("CrossAttention: input size mismatch")
+        e = embed_dim
+        return self._run(lambda dq, dkv, y: self.ctx.attention(dq, dkv, dkv.offset(e), y, 1, query_len, kv_len,
+                                                               num_heads, e // num_heads, causal, ld_q=e,
+                                                               ld_kv=2 * e),
+                         q, kv, out_size=query_len * e)

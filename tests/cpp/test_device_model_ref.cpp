@@ -8,7 +8,9 @@
 // tree is present) against the reference headers and the reference runtime
 // compiled in place (oracle/_ref/libmimir_ref_model.so); run by
 // tests/test_gpu_cpp_adapter.py.  Standalone main() returning 0 / 1, like
-// the reference's CTest programs.
+// the reference's CTest programs.  Also the attention core's binding inside
+// the reference's own self_attention_forward / cross_attention_forward.
+#include "LayerOps.hpp"
 #include "Model.hpp"
 #include "mimir_layerops_hip.hpp"
 
@@ -193,6 +195,61 @@ void int_ids_forward(mimir_hip::Context& c) {
     CHECK(ref_threw && dev_threw);
 }
 
+// LayerOps::self_attention_forward / cross_attention_forward (LayerOps.hpp:
+// 1004-1097, 1116-1216) at their own call shape: the reference computes the
+// projections, the adapter's attention_core / cross_attention_core replaces
+// steps 2-5 (the softmax fused into QK^T and PV on the device), and the
+// reference's output projection follows.  Held normwise at 1e-4 of the
+// largest output: the core's element-wise parity is tests/test_gpu_attention.py;
+// this checks the binding (layouts, strides, scale, mask) at the call site.
+void attention_at_call_site() {
+    const int seq = 100, e = 64, heads = 4;
+    std::vector<float> x(seq * e), wqkv(3 * e * e), wout(e * e);
+    for (size_t i = 0; i < x.size(); ++i) x[i] = std::sin(0.37f * static_cast<float>(i)) * 1.3f;
+    for (size_t i = 0; i < wqkv.size(); ++i) wqkv[i] = std::cos(0.11f * static_cast<float>(i) + 0.5f) * 0.2f;
+    for (size_t i = 0; i < wout.size(); ++i) wout[i] = std::sin(0.23f * static_cast<float>(i) + 1.0f) * 0.15f;
+    auto normwise = [](const std::vector<float>& a, const std::vector<float>& b) {
+        if (a.size() != b.size() || b.empty()) return false;
+        float m = 0.f;
+        for (float v : b) m = std::fmax(m, std::fabs(v));
+        for (size_t i = 0; i < a.size(); ++i)
+            if (!(std::fabs(a[i] - b[i]) <= 1e-6f + 1e-4f * m)) return false;
+        return true;
+    };
+    for (bool causal : {false, true}) {
+        const std::vector<float> ref = LayerOps::self_attention_forward(x, wqkv, wout, seq, e, heads, causal);
+        std::vector<float> qkv, out;
+        LayerOps::matmul(x, wqkv, qkv, seq, e, 3 * e);
+        const std::vector<float> att = mimir_hip::LayerOps::attention_core(qkv, seq, e, heads, causal);
+        LayerOps::matmul(att, wout, out, seq, e, e);
+        CHECK(normwise(out, ref));
+    }
+    // Cross attention: 37 queries over 90 keys.
+    const int lq = 37, lk = 90;
+    std::vector<float> xq(lq * e), xkv(lk * e), wq(e * e), wkv(2 * e * e);
+    for (size_t i = 0; i < xq.size(); ++i) xq[i] = std::cos(0.29f * static_cast<float>(i));
+    for (size_t i = 0; i < xkv.size(); ++i) xkv[i] = std::sin(0.17f * static_cast<float>(i) + 0.3f);
+    for (size_t i = 0; i < wq.size(); ++i) wq[i] = std::sin(0.07f * static_cast<float>(i)) * 0.25f;
+    for (size_t i = 0; i < wkv.size(); ++i) wkv[i] = std::cos(0.05f * static_cast<float>(i) + 0.2f) * 0.2f;
+    for (bool causal : {false, true}) {
+        const std::vector<float> ref =
+            LayerOps::cross_attention_forward(xq, xkv, wq, wkv, wout, lq, lk, e, heads, causal);
+        std::vector<float> q, kv, out;
+        LayerOps::matmul(xq, wq, q, lq, e, e);
+        LayerOps::matmul(xkv, wkv, kv, lk, e, 2 * e);
+        const std::vector<float> att = mimir_hip::LayerOps::cross_attention_core(q, kv, lq, lk, e, heads, causal);
+        LayerOps::matmul(att, wout, out, lq, e, e);
+        CHECK(normwise(out, ref));
+    }
+    // The reference's refusal, with its message.
+    std::string ref_msg, dev_msg;
+    try { LayerOps::self_attention_forward(x, wqkv, wout, seq, e, 5, false); } catch (const std::exception& ex) { ref_msg = ex.what(); }
+    std::vector<float> qkv;
+    LayerOps::matmul(x, wqkv, qkv, seq, e, 3 * e);
+    try { mimir_hip::LayerOps::attention_core(qkv, seq, e, 5, false); } catch (const std::exception& ex) { dev_msg = ex.what(); }
+    CHECK(!ref_msg.empty() && ref_msg == dev_msg);
+}
+
 }  // namespace
 
 int main() {
@@ -201,6 +258,7 @@ int main() {
         residual_merge_kat(c);
         weight_block_and_backward(c);
         int_ids_forward(c);
+        attention_at_call_site();
     } catch (const std::exception& e) {
         std::fprintf(stderr, "FAIL: exception %s\n", e.what());
         return 1;

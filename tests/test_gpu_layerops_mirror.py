@@ -113,3 +113,38 @@ def test_embedding_forward_bitexact(ops, float_ids):
     assert_bitexact(ops.embedding_forward(arg, L), O.embedding(arg, table, vocab, dim, 4).ravel(), "gather")
     with pytest.raises(RuntimeError):  # Model.cpp:1181-1182
         ops.embedding_forward(ids, M.Layer(type="Embedding", vocab_size=vocab, embed_dim=dim, weights=table[:-1]))
+
+
+@pytest.mark.parametrize("seq,e,heads", [(40, 64, 2), (130, 96, 3), (1, 16, 1)])
+@pytest.mark.parametrize("causal", [False, True])
+def test_attention_core(ops, seq, e, heads, causal):
+    """attention_core on the QKV projection, against the reference's own
+    self_attention_forward fed one-hot inputs and an identity output
+    projection (both projections exact: its output is the core itself)."""
+    from _attention import assert_attention_close, attention64, self_case
+    x, w, q, k, v = self_case(seq, e, 1.5, seq + e)
+    ref = O.ref_self_attention(x, w, np.eye(e, dtype=np.float32), seq, e, heads, causal)
+    qkv = np.concatenate([q, k, v], axis=1)
+    got = ops.attention_core(qkv, seq, e, heads, causal).reshape(seq, e)
+    _, mag, cond = attention64(q, k, v, heads, causal, O.attention_scale(e // heads))
+    assert_attention_close(got, ref, mag, 2 * cond, "attention_core")
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_cross_attention_core(ops, causal):
+    from _attention import assert_attention_close, attention64, cross_case
+    lq, lk, e, heads = 40, 65, 64, 2
+    xq, xkv, wq, wkv, q, k, v = cross_case(lq, lk, e, 1.2, 9)
+    ref = O.ref_cross_attention(xq, xkv, wq, wkv, np.eye(e, dtype=np.float32), lq, lk, e, heads, causal)
+    got = ops.cross_attention_core(q, np.concatenate([k, v], axis=1), lq, lk, e, heads, causal).reshape(lq, e)
+    _, mag, cond = attention64(q, k, v, heads, causal, O.attention_scale(e // heads))
+    assert_attention_close(got, ref, mag, 2 * cond, "cross_attention_core")
+
+
+def test_attention_core_errors(ops):
+    with pytest.raises(RuntimeError, match="embed_dim must be divisible by num_heads"):
+        ops.attention_core(np.zeros(4 * 36, np.float32), 4, 12, 5)
+    with pytest.raises(RuntimeError, match="input size mismatch"):
+        ops.attention_core(np.zeros(10, np.float32), 4, 12, 2)
+    with pytest.raises(RuntimeError, match="invalid dimensions"):
+        ops.cross_attention_core(np.zeros(0, np.float32), np.zeros(24, np.float32), 0, 1, 12, 2)
