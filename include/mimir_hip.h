@@ -245,6 +245,30 @@ int mimir_attention_fwd(mimir_ctx* ctx, const float* q, int64_t ld_q, const floa
                         int64_t ld_kv, float* out, int64_t ld_out, int64_t batch, int64_t q_len,
                         int64_t kv_len, int64_t heads, int64_t head_dim, float scale, int causal);
 
+/* The SelfAttention / MultiHeadAttention layer: LayerOps::self_attention_forward
+ * (LayerOps.hpp:1004-1097; MultiHeadAttention calls it, :1100-1113), as
+ * Model.cpp:5904-5934 dispatches it.  input [seq_len x embed_dim]; weights =
+ * the layer's block [qkv_weight (embed_dim x 3 embed_dim) | out_weight
+ * (embed_dim x embed_dim)], row-major as the reference's matmul reads them,
+ * at least 4 embed_dim^2 floats (the reference reads past a shorter block; it
+ * is refused here); out [seq_len x embed_dim].  The projections are fp32
+ * library GEMMs, the core is mimir_attention_fwd with the reference's
+ * scale 1/sqrtf(head_dim).  head_dim <= 128.  Uses the context's scratch
+ * (4 seq_len embed_dim floats).  out must not overlap input or weights. */
+int mimir_self_attention_fwd(mimir_ctx* ctx, const float* input, int64_t seq_len, int64_t embed_dim,
+                             int64_t num_heads, int causal, const float* weights, int64_t weights_len,
+                             float* out);
+
+/* The CrossAttention layer: LayerOps::cross_attention_forward
+ * (LayerOps.hpp:1116-1216) as Model.cpp:5936-5990 dispatches it.
+ * query_input [query_len x embed_dim], kv_input [kv_len x embed_dim];
+ * weights = [q_weight (E x E) | kv_weight (E x 2E) | out_weight (E x E)],
+ * at least 4 E^2 floats; out [query_len x embed_dim].  Scratch: 2 (query_len
+ * + kv_len) E floats. */
+int mimir_cross_attention_fwd(mimir_ctx* ctx, const float* query_input, int64_t query_len,
+                              const float* kv_input, int64_t kv_len, int64_t embed_dim, int64_t num_heads,
+                              int causal, const float* weights, int64_t weights_len, float* out);
+
 /* ---------------------------------------------------------------------------
  * Backward of the path's ops: the branches of the reference's
  * Model::backwardPass (Model.cpp:7305-9153).  Device pointers, stream order.

@@ -56,6 +56,8 @@
 
 #include <math.h>
 
+#include <cmath>
+
 using namespace mimir;
 
 namespace {
@@ -458,6 +460,65 @@ int mimir_attention_fwd(mimir_ctx* ctx, const float* q, int64_t ld_q, const floa
     if (head_dim <= 32) return launch<32>(ctx, a, vec);
     if (head_dim <= 64) return launch<64>(ctx, a, vec);
     return launch<128>(ctx, a, vec);
+}
+
+// The attention layers (Model.cpp:5904-5934, 5936-5990): the projections as
+// library GEMMs (gemm.hip), the fused core between them on the projection's
+// output in place (no split copies).  Scratch: the projections' outputs and
+// the attended heads, reused in stream order.
+int mimir_self_attention_fwd(mimir_ctx* ctx, const float* input, int64_t seq_len, int64_t embed_dim,
+                             int64_t num_heads, int causal, const float* weights, int64_t weights_len, float* out) {
+    if (!ctx) return MIMIR_EINVAL;
+    MIMIR_REQUIRE(ctx, embed_dim >= 1 && num_heads >= 1 && embed_dim % num_heads == 0,
+                  "SelfAttention: embed_dim must be divisible by num_heads");
+    MIMIR_REQUIRE(ctx, seq_len >= 0, "SelfAttention: input size mismatch");
+    const int64_t e = embed_dim;
+    MIMIR_REQUIRE(ctx, weights_len >= 4 * e * e, "SelfAttention: weight block of %lld floats, %lld needed",
+                  (long long)weights_len, (long long)(4 * e * e));
+    MIMIR_REQUIRE(ctx, e / num_heads <= 128, "attention: head_dim %lld > 128 is not supported",
+                  (long long)(e / num_heads));
+    if (seq_len == 0) return MIMIR_OK;
+    MIMIR_REQUIRE(ctx, input && weights && out, "SelfAttention: null pointer");
+    MIMIR_ENTER(ctx);
+    void* s = nullptr;
+    if (int st = ensure_scratch(ctx, sizeof(float) * static_cast<size_t>(seq_len) * 4 * e, &s)) return st;
+    float* qkv = static_cast<float*>(s);  // [seq, 3E]: Q | K | V
+    float* att = qkv + seq_len * 3 * e;   // [seq, E]
+    const int64_t hd = e / num_heads;
+    if (int st = gemm_f32(ctx, seq_len, 3 * e, e, input, e, weights, 3 * e, qkv, 3 * e)) return st;  // :1027-1028
+    if (int st = mimir_attention_fwd(ctx, qkv, 3 * e, qkv + e, qkv + 2 * e, 3 * e, att, e, 1, seq_len, seq_len,
+                                     num_heads, hd, 1.0f / std::sqrt(static_cast<float>(hd)), causal))
+        return st;
+    return gemm_f32(ctx, seq_len, e, e, att, e, weights + 3 * e * e, e, out, e);  // :1093-1094
+}
+
+int mimir_cross_attention_fwd(mimir_ctx* ctx, const float* query_input, int64_t query_len, const float* kv_input,
+                              int64_t kv_len, int64_t embed_dim, int64_t num_heads, int causal,
+                              const float* weights, int64_t weights_len, float* out) {
+    if (!ctx) return MIMIR_EINVAL;
+    MIMIR_REQUIRE(ctx, embed_dim >= 1 && num_heads >= 1 && embed_dim % num_heads == 0,
+                  "CrossAttention: embed_dim must be divisible by num_heads");
+    MIMIR_REQUIRE(ctx, query_len > 0 && kv_len > 0, "CrossAttention: invalid dimensions");
+    const int64_t e = embed_dim;
+    MIMIR_REQUIRE(ctx, weights_len >= 4 * e * e, "CrossAttention: weight block of %lld floats, %lld needed",
+                  (long long)weights_len, (long long)(4 * e * e));
+    MIMIR_REQUIRE(ctx, e / num_heads <= 128, "attention: head_dim %lld > 128 is not supported",
+                  (long long)(e / num_heads));
+    MIMIR_REQUIRE(ctx, query_input && kv_input && weights && out, "CrossAttention: null pointer");
+    MIMIR_ENTER(ctx);
+    void* s = nullptr;
+    if (int st = ensure_scratch(ctx, sizeof(float) * static_cast<size_t>(2 * query_len + 2 * kv_len) * e, &s))
+        return st;
+    float* qp = static_cast<float*>(s);  // [query_len, E]
+    float* kv = qp + query_len * e;      // [kv_len, 2E]: K | V
+    float* att = kv + kv_len * 2 * e;    // [query_len, E]
+    const int64_t hd = e / num_heads;
+    if (int st = gemm_f32(ctx, query_len, e, e, query_input, e, weights, e, qp, e)) return st;  // :1146-1147
+    if (int st = gemm_f32(ctx, kv_len, 2 * e, e, kv_input, e, weights + e * e, 2 * e, kv, 2 * e)) return st;
+    if (int st = mimir_attention_fwd(ctx, qp, e, kv, kv + e, 2 * e, att, e, 1, query_len, kv_len, num_heads, hd,
+                                     1.0f / std::sqrt(static_cast<float>(hd)), causal))
+        return st;
+    return gemm_f32(ctx, query_len, e, e, att, e, weights + 3 * e * e, e, out, e);  // :1213-1214
 }
 
 }  // extern "C"

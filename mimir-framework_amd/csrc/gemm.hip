@@ -1,0 +1,63 @@
+// gemm.hip -- the plain fp32 matrix products around the attention core (the
+// QKV and output projections of the attention layers), through rocBLAS on
+// the context's stream.  These are library GEMMs: the path's own kernel is
+// the fused core between them (attention.hip).
+//
+// The reference computes them with LayerOps::matmul (LayerOps.hpp:977-1001):
+// row-major C[M x N] = A[M x K] * B[K x N] in float32.  rocBLAS is
+// column-major, so the row-major product is taken as C^T = B^T A^T, which is
+// the same memory.  rocBLAS's default math mode keeps fp32 arithmetic (no
+// reduced-precision inner products).
+#include "internal.hpp"
+
+#include <rocblas/rocblas.h>
+
+namespace {
+
+rocblas_handle handle_of(mimir_ctx* ctx, int* st) {
+    if (!ctx->blas) {
+        rocblas_handle h = nullptr;
+        if (rocblas_create_handle(&h) != rocblas_status_success) {
+            *st = mimir::fail(ctx, MIMIR_EDEVICE, "rocblas_create_handle failed");
+            return nullptr;
+        }
+        ctx->blas = h;
+    }
+    rocblas_handle h = static_cast<rocblas_handle>(ctx->blas);
+    if (rocblas_set_stream(h, ctx->stream) != rocblas_status_success) {
+        *st = mimir::fail(ctx, MIMIR_EDEVICE, "rocblas_set_stream failed");
+        return nullptr;
+    }
+    *st = MIMIR_OK;
+    return h;
+}
+
+}  // namespace
+
+namespace mimir {
+
+int gemm_f32(mimir_ctx* ctx, int64_t M, int64_t N, int64_t K, const float* A, int64_t lda, const float* B,
+             int64_t ldb, float* C, int64_t ldc) {
+    if (M == 0 || N == 0) return MIMIR_OK;
+    const int64_t lim = INT32_MAX;
+    if (M > lim || N > lim || K > lim || lda > lim || ldb > lim || ldc > lim)
+        return fail(ctx, MIMIR_EINVAL, "matrix product: dimensions exceed the 32-bit library limit");
+    int st = MIMIR_OK;
+    rocblas_handle h = handle_of(ctx, &st);
+    if (!h) return st;
+    const float one = 1.0f, zero = 0.0f;
+    // K == 0: C = 0 (beta = 0 with an empty sum).
+    const rocblas_status s =
+        rocblas_sgemm(h, rocblas_operation_none, rocblas_operation_none, static_cast<rocblas_int>(N),
+                      static_cast<rocblas_int>(M), static_cast<rocblas_int>(K), &one, B, static_cast<rocblas_int>(ldb),
+                      A, static_cast<rocblas_int>(lda), &zero, C, static_cast<rocblas_int>(ldc));
+    if (s != rocblas_status_success) return fail(ctx, MIMIR_EDEVICE, "rocblas_sgemm failed (status %d)", (int)s);
+    return MIMIR_OK;
+}
+
+void gemm_release(mimir_ctx* ctx) {
+    if (ctx->blas) (void)rocblas_destroy_handle(static_cast<rocblas_handle>(ctx->blas));
+    ctx->blas = nullptr;
+}
+
+}  // namespace mimir

@@ -30,6 +30,9 @@ struct mimir_ctx {
     // Device address of this GPU's fixed scratch array (backward.hip), for
     // the entry point that allocates nothing; set at context creation.
     void* noalloc_scratch = nullptr;
+    // rocBLAS handle for the attention layers' projections (gemm.hip),
+    // created on first use.
+    void* blas = nullptr;
 };
 
 struct mimir_event {
@@ -88,6 +91,12 @@ inline bool grid_for(int64_t units, int64_t per_block, unsigned* blocks) {
 // Context scratch of at least `bytes` (runtime.hip).  Growing it waits for
 // the work already enqueued, which may still read the old buffer.
 int ensure_scratch(mimir_ctx* ctx, size_t bytes, void** out);
+
+// Row-major fp32 C[M x N] = A[M x K] * B[K x N] on the context's stream
+// (rocBLAS; gemm.hip), and the release of its handle at context teardown.
+int gemm_f32(mimir_ctx* ctx, int64_t M, int64_t N, int64_t K, const float* A, int64_t lda, const float* B,
+             int64_t ldb, float* C, int64_t ldc);
+void gemm_release(mimir_ctx* ctx);
 
 // Look up this context's device address of the no-allocation scratch array
 // (backward.hip); called once per context, with its device current.

@@ -107,6 +107,7 @@ int mimir_ctx_destroy(mimir_ctx* ctx) {
     int st = enter(ctx);
     if (st == MIMIR_OK) {
         (void)hipStreamSynchronize(ctx->stream);
+        gemm_release(ctx);
         for (auto& kv : ctx->allocs) (void)hipFree(kv.first);
         if (ctx->scratch) (void)hipFree(ctx->scratch);
         (void)hipStreamDestroy(ctx->own_stream);

@@ -218,6 +218,17 @@ class Context:
                                                 ld_kv or width, _ptr(out), ld_out or width, batch, q_len,
                                                 kv_len, heads, head_dim, float(scale), int(bool(causal))))
 
+    def self_attention(self, x, seq_len, embed_dim, num_heads, causal, weights, weights_len, out):
+        """mimir_self_attention_fwd: the SelfAttention layer on device buffers."""
+        self.check(self.lib.mimir_self_attention_fwd(self.handle, _ptr(x), seq_len, embed_dim, num_heads,
+                                                     int(bool(causal)), _ptr(weights), weights_len, _ptr(out)))
+
+    def cross_attention(self, xq, query_len, xkv, kv_len, embed_dim, num_heads, causal, weights, weights_len, out):
+        """mimir_cross_attention_fwd: the CrossAttention layer on device buffers."""
+        self.check(self.lib.mimir_cross_attention_fwd(self.handle, _ptr(xq), query_len, _ptr(xkv), kv_len, embed_dim,
+                                                      num_heads, int(bool(causal)), _ptr(weights), weights_len,
+                                                      _ptr(out)))
+
     # -- backward (Model::backwardPass branches) -------------------------------
 
     def layernorm_bwd(self, x, dy, gamma, dx, dgamma, dbeta, groups, n, eps, accumulate=False):

@@ -206,3 +206,61 @@ def test_full_size_properties(ctx):
         assert_attention_close(got[bi:bi + 1, :, sl], want, mag, cond, f"full size b{bi} h{h} vs float64")
         assert_attention_close(got[bi:bi + 1, :, sl], O.attention(qs, ks, vs, 1, True), mag, 2 * cond,
                                f"b{bi} h{h} vs oracle")
+
+
+@pytest.mark.parametrize("seq,e,heads", [(1, 16, 2), (50, 64, 4), (130, 96, 3), (64, 128, 1), (300, 256, 2)])
+@pytest.mark.parametrize("causal", [False, True])
+def test_self_attention_layer(ctx, seq, e, heads, causal):
+    """mimir_self_attention_fwd (projections + fused core) against the
+    compiled reference's self_attention_forward with random weights and
+    float64, under the whole-layer tolerance (tests/_attention.py)."""
+    from _attention import assert_within, attention_layer64, layer_case
+    x, w = layer_case(seq, e, seq * 7 + e, 1.5)
+    wqkv, wout = w[:3 * e * e].reshape(e, 3 * e), w[3 * e * e:].reshape(e, e)
+    print(f"self attention layer seq={seq} e={e} h={heads} causal={causal}", flush=True)
+    dx, dw, dy = ctx.to_device(x), ctx.to_device(w), ctx.empty((seq, e))
+    try:
+        ctx.self_attention(dx, seq, e, heads, causal, dw, w.size, dy)
+        got = dy.numpy()
+    finally:
+        for d in (dx, dw, dy):
+            d.free()
+    want, tol = attention_layer64(x, wqkv, wout, heads, causal)
+    assert_within(got, want, tol, "layer vs float64")
+    assert_within(got, O.ref_self_attention(x, wqkv, wout, seq, e, heads, causal), 2 * tol, "layer vs reference")
+
+
+@pytest.mark.parametrize("lq,lk,e,heads", [(37, 90, 64, 4), (200, 33, 128, 2), (1, 1, 32, 1)])
+@pytest.mark.parametrize("causal", [False, True])
+def test_cross_attention_layer(ctx, lq, lk, e, heads, causal):
+    from _attention import assert_within, cross_attention_layer64
+    r = np.random.default_rng(lq + lk + e)
+    xq = r.standard_normal((lq, e)).astype(np.float32)
+    xkv = r.standard_normal((lk, e)).astype(np.float32)
+    wq, wkv, wout = ((r.standard_normal(s) / np.sqrt(e)).astype(np.float32) for s in ((e, e), (e, 2 * e), (e, e)))
+    w = np.concatenate([wq.ravel(), wkv.ravel(), wout.ravel()])
+    print(f"cross attention layer lq={lq} lk={lk} e={e} h={heads} causal={causal}", flush=True)
+    dq, dkv, dw, dy = ctx.to_device(xq), ctx.to_device(xkv), ctx.to_device(w), ctx.empty((lq, e))
+    try:
+        ctx.cross_attention(dq, lq, dkv, lk, e, heads, causal, dw, w.size, dy)
+        got = dy.numpy()
+    finally:
+        for d in (dq, dkv, dw, dy):
+            d.free()
+    want, tol = cross_attention_layer64(xq, xkv, wq, wkv, wout, heads, causal)
+    assert_within(got, want, tol, "cross layer vs float64")
+    assert_within(got, O.ref_cross_attention(xq, xkv, wq, wkv, wout, lq, lk, e, heads, causal), 2 * tol,
+                  "cross layer vs reference")
+
+
+def test_attention_layer_refusals(ctx):
+    b = ctx.empty(4096)
+    try:
+        with pytest.raises(M.MimirError, match="divisible by num_heads"):
+            ctx.self_attention(b, 4, 12, 5, False, b, 4096, b)
+        with pytest.raises(M.MimirError, match="weight block"):
+            ctx.self_attention(b, 4, 16, 2, False, b, 4 * 16 * 16 - 1, b)
+        with pytest.raises(M.MimirError, match="invalid dimensions"):
+            ctx.cross_attention(b, 0, b, 3, 16, 2, False, b, 4096, b)
+    finally:
+        b.free()

@@ -148,3 +148,38 @@ def test_oracle_reproduces_golden_fixture():
             assert_bitexact(got, gold[f"cross_{lq}_{lk}_{e}_{heads}_{causal}"])
             n += 1
     assert n == len(gold)
+
+
+@needs_ref
+@pytest.mark.parametrize("seq,e,heads", [(50, 64, 4), (130, 96, 3), (64, 128, 1)])
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("amp", [1.0, 2.5])
+def test_layer_tolerance_model(seq, e, heads, causal, amp):
+    """The whole-layer tolerance (projections, core, output projection; see
+    tests/_attention.py attention_layer64): the compiled reference's own
+    self_attention_forward with random weights stays within a quarter of it
+    against float64, and a planted mistake (no 1/sqrt(d) scale) does not."""
+    from _attention import assert_within, attention_layer64, layer_case
+    x, w = layer_case(seq, e, seq * 3 + e, amp)
+    wqkv, wout = w[:3 * e * e].reshape(e, 3 * e), w[3 * e * e:].reshape(e, e)
+    want, tol = attention_layer64(x, wqkv, wout, heads, causal)
+    ref = O.ref_self_attention(x, wqkv, wout, seq, e, heads, causal)
+    assert_within(ref, want, tol / 4, "reference vs float64")
+    qkv = x.astype(np.float64) @ wqkv
+    att = O.attention(qkv[:, :e], qkv[:, e:2 * e], qkv[:, 2 * e:], heads, causal, scale=1.0)
+    with pytest.raises(AssertionError):
+        assert_within(att.astype(np.float64) @ wout, want, tol, "no scale")
+
+
+@needs_ref
+@pytest.mark.parametrize("causal", [False, True])
+def test_cross_layer_tolerance_model(causal):
+    from _attention import assert_within, cross_attention_layer64
+    r = np.random.default_rng(4)
+    lq, lk, e, heads = 37, 90, 64, 4
+    xq = r.standard_normal((lq, e)).astype(np.float32)
+    xkv = r.standard_normal((lk, e)).astype(np.float32)
+    wq, wkv, wout = ((r.standard_normal(s) / np.sqrt(e)).astype(np.float32) for s in ((e, e), (e, 2 * e), (e, e)))
+    want, tol = cross_attention_layer64(xq, xkv, wq, wkv, wout, heads, causal)
+    ref = O.ref_cross_attention(xq, xkv, wq, wkv, wout, lq, lk, e, heads, causal)
+    assert_within(ref, want, tol / 4, "reference vs float64")
