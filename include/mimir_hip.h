@@ -368,6 +368,12 @@ typedef struct mimir_store mimir_store;
 #define MIMIR_LAYER_EMBEDDING 9  /* inline gather, Model.cpp:5301-5334 */
 #define MIMIR_LAYER_IDENTITY 10  /* LayerOps::identity_forward */
 #define MIMIR_LAYER_DROPOUT 11   /* LayerOps::dropout_forward at inference: identity */
+/* The attention layers (Model.cpp:5904-5990): projections + the fused core,
+ * mimir_self_attention_fwd / mimir_cross_attention_fwd.  Forward only: a
+ * backward that reaches one returns EINVAL. */
+#define MIMIR_LAYER_SELF_ATTENTION 12      /* LayerOps::self_attention_forward */
+#define MIMIR_LAYER_MULTIHEAD_ATTENTION 13 /* LayerOps::multihead_attention_forward (the same) */
+#define MIMIR_LAYER_CROSS_ATTENTION 14     /* LayerOps::cross_attention_forward (inputs: query, key_value) */
 
 /* One layer: the fields of the reference's `Layer` (Layers.hpp:86-309) this
  * path reads.  `weights` is a DEVICE pointer to the layer's weight block
@@ -398,6 +404,10 @@ typedef struct mimir_layer {
     int32_t merge_op;                 /* Layer::merge_op, a MIMIR_MERGE_* value */
     const int32_t* branch_sources;    /* host array, Layer::branch_sources */
     int32_t n_branch_sources;
+    /* Attention fields (Layers.hpp:174-178), read by the attention layers. */
+    int32_t num_heads;                /* Layer::num_heads (the reference's default is 8) */
+    int32_t head_dim;                 /* Layer::head_dim (CrossAttention: embed_dim = head_dim * num_heads when 0) */
+    int32_t causal;                   /* Layer::causal */
 } mimir_layer;
 
 /* BranchType values (Layers.hpp:59-69) that the runtime acts on. */

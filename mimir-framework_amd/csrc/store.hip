@@ -173,6 +173,9 @@ const char* type_name(int32_t t) {
         case MIMIR_LAYER_EMBEDDING: return "Embedding";
         case MIMIR_LAYER_IDENTITY: return "Identity";
         case MIMIR_LAYER_DROPOUT: return "Dropout";
+        case MIMIR_LAYER_SELF_ATTENTION: return "SelfAttention";
+        case MIMIR_LAYER_MULTIHEAD_ATTENTION: return "MultiHeadAttention";
+        case MIMIR_LAYER_CROSS_ATTENTION: return "CrossAttention";
         default: return "?";
     }
 }
@@ -269,6 +272,7 @@ int run_layer(mimir_store* s, const mimir_layer& L, Snap* snap, bool ids_path = 
             case MIMIR_LAYER_SILU:
             case MIMIR_LAYER_MULTIPLY:
             case MIMIR_LAYER_IDENTITY:
+            case MIMIR_LAYER_CROSS_ATTENTION:
                 return fail(ctx, MIMIR_EINVAL, "forwardPass(int): layer type not supported in int path: %s (layer %s)",
                             type_name(L.type), layer_name(L));
             case MIMIR_LAYER_ADD:  // :1285
@@ -309,6 +313,45 @@ int run_layer(mimir_store* s, const mimir_layer& L, Snap* snap, bool ids_path = 
         case MIMIR_LAYER_EMBEDDING: {
             const int64_t dim = L.embed_dim > 1 ? L.embed_dim : 1;
             out_n = N * dim;
+            break;
+        }
+        case MIMIR_LAYER_SELF_ATTENTION:
+        case MIMIR_LAYER_MULTIHEAD_ATTENTION: {  // Model.cpp:5904-5934 (int path :1291-1310)
+            if (!L.weights || L.weights_len <= 0)
+                return fail(ctx, MIMIR_EINVAL, "Attention: weights not initialized. Call allocateParams() first. "
+                            "(layer %s)", layer_name(L));
+            const int64_t seq = L.seq_len > 0 ? L.seq_len : 1;
+            const int64_t e = L.embed_dim > 0 ? L.embed_dim : N;
+            const int64_t heads = L.num_heads > 0 ? L.num_heads : 1;
+            if (e <= 0 || e % heads != 0)  // LayerOps.hpp:1013-1015
+                return fail(ctx, MIMIR_EINVAL, "SelfAttention: embed_dim must be divisible by num_heads (layer %s)",
+                            layer_name(L));
+            if (N != seq * e)  // :1021-1023
+                return fail(ctx, MIMIR_EINVAL, "SelfAttention: input size mismatch (layer %s)", layer_name(L));
+            out_n = seq * e;
+            break;
+        }
+        case MIMIR_LAYER_CROSS_ATTENTION: {  // Model.cpp:5936-5990
+            if (n_in < 2)
+                return fail(ctx, MIMIR_EINVAL, "CrossAttention requires 2 inputs (query, key_value), got %d", n_in);
+            if (!L.weights || L.weights_len <= 0)
+                return fail(ctx, MIMIR_EINVAL, "CrossAttention: weights not initialized. Call allocateParams() "
+                            "first. (layer %s)", layer_name(L));
+            const int64_t heads = L.num_heads > 0 ? L.num_heads : 1;
+            int64_t e = L.embed_dim;
+            if (e <= 0 && L.head_dim > 0) e = static_cast<int64_t>(L.head_dim) * heads;
+            if (e <= 0)
+                return fail(ctx, MIMIR_EINVAL, "CrossAttention: embed_dim must be configured (set layer.embed_dim "
+                            "or head_dim*num_heads) (layer %s)", layer_name(L));
+            if (in[0].n % e != 0)
+                return fail(ctx, MIMIR_EINVAL, "CrossAttention: query input size must be divisible by embed_dim "
+                            "(layer %s)", layer_name(L));
+            if (in[1].n % e != 0)
+                return fail(ctx, MIMIR_EINVAL, "CrossAttention: key/value input size must be divisible by "
+                            "embed_dim (layer %s)", layer_name(L));
+            if (in[0].n == 0 || in[1].n == 0)
+                return fail(ctx, MIMIR_EINVAL, "CrossAttention: invalid sequence lengths (layer %s)", layer_name(L));
+            out_n = in[0].n;
             break;
         }
         default:
@@ -373,6 +416,21 @@ int run_layer(mimir_store* s, const mimir_layer& L, Snap* snap, bool ids_path = 
             st = embedding_launch(ctx, in[0].p, ids_path ? kIdsI32 : in[0].ids_i32 ? kIdsI32AsF32 : kIdsF32, N,
                                   L.weights, L.weights_len, L.vocab_size, L.embed_dim, L.padding_idx, y);
             break;
+        case MIMIR_LAYER_SELF_ATTENTION:
+        case MIMIR_LAYER_MULTIHEAD_ATTENTION: {
+            const int64_t seq = L.seq_len > 0 ? L.seq_len : 1;
+            const int64_t e = L.embed_dim > 0 ? L.embed_dim : N;
+            st = mimir_self_attention_fwd(ctx, x, seq, e, L.num_heads > 0 ? L.num_heads : 1, L.causal, L.weights,
+                                          L.weights_len, y);
+            break;
+        }
+        case MIMIR_LAYER_CROSS_ATTENTION: {
+            const int64_t heads = L.num_heads > 0 ? L.num_heads : 1;
+            const int64_t e = L.embed_dim > 0 ? L.embed_dim : static_cast<int64_t>(L.head_dim) * heads;
+            st = mimir_cross_attention_fwd(ctx, x, in[0].n / e, static_cast<const float*>(in[1].p), in[1].n / e, e,
+                                           heads, L.causal, L.weights, L.weights_len, y);
+            break;
+        }
     }
     if (st != MIMIR_OK) {
         s->discard(ob);
@@ -502,6 +560,11 @@ int backward_layer(mimir_store* s, const mimir_layer& L, const Snap& sn) {
             return L.type == MIMIR_LAYER_GELU ? mimir_gelu_bwd(ctx, x, g, d0, gn, a0)
                                               : mimir_silu_bwd(ctx, x, g, d0, gn, a0);
         }
+        case MIMIR_LAYER_SELF_ATTENTION:
+        case MIMIR_LAYER_MULTIHEAD_ATTENTION:
+        case MIMIR_LAYER_CROSS_ATTENTION:  // Model.cpp:8034-8127 -> backward_self_attention (:6847) & co.
+            return fail(ctx, MIMIR_EINVAL, "%s backward is not on this path (layer %s)", type_name(L.type),
+                        layer_name(L));
         default:  // RMSNorm, Softmax, LogSoftmax: the fallback at :9133-9140
             if (gn != n0) return MIMIR_OK;
             return grad_pass(s, nm(0), g, gn);

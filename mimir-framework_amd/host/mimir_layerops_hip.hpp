@@ -583,7 +583,10 @@ private:
             {"GELU", MIMIR_LAYER_GELU},           {"SiLU", MIMIR_LAYER_SILU},
             {"Add", MIMIR_LAYER_ADD},             {"Multiply", MIMIR_LAYER_MULTIPLY},
             {"Embedding", MIMIR_LAYER_EMBEDDING}, {"Identity", MIMIR_LAYER_IDENTITY},
-            {"Dropout", MIMIR_LAYER_DROPOUT}};
+            {"Dropout", MIMIR_LAYER_DROPOUT},
+            {"SelfAttention", MIMIR_LAYER_SELF_ATTENTION},
+            {"MultiHeadAttention", MIMIR_LAYER_MULTIHEAD_ATTENTION},
+            {"CrossAttention", MIMIR_LAYER_CROSS_ATTENTION}};
         auto it = m.find(t);
         return it == m.end() ? 0 : it->second;
     }
@@ -618,6 +621,10 @@ private:
             static_assert(sizeof(L.branch_sources[0]) == sizeof(int32_t), "Layer::branch_sources is int");
             c.branch_sources = reinterpret_cast<const int32_t*>(L.branch_sources.data());
             c.n_branch_sources = static_cast<int32_t>(L.branch_sources.size());
+            // Attention fields (Layers.hpp:174-178).
+            c.num_heads = L.num_heads;
+            c.head_dim = L.head_dim;
+            c.causal = L.causal ? 1 : 0;
         }
     }
 

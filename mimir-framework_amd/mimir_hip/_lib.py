@@ -24,7 +24,8 @@ _PP = POINTER(c_void_p)
 DTYPE_F32, DTYPE_I32 = 0, 1
 ST_DTYPES = {0: "F32", 1: "F16", 2: "I32", 3: "I16", 4: "U16", 5: "U8"}  # MIMIR_ST_*
 LAYER_TYPES = {"LayerNorm": 1, "RMSNorm": 2, "Softmax": 3, "LogSoftmax": 4, "GELU": 5, "SiLU": 6,
-               "Add": 7, "Multiply": 8, "Embedding": 9, "Identity": 10, "Dropout": 11}
+               "Add": 7, "Multiply": 8, "Embedding": 9, "Identity": 10, "Dropout": 11,
+               "SelfAttention": 12, "MultiHeadAttention": 13, "CrossAttention": 14}
 # The reference's BranchType and MergeOperation (Layers.hpp:59-80), in order.
 BRANCH_TYPES = ("NONE", "RESIDUAL", "SKIP_CONNECTION", "DENSE_CONNECTION", "ATTENTION_BRANCH", "MULTI_SCALE",
                 "GATE", "SPLIT", "MERGE")
@@ -66,7 +67,7 @@ class Layer_C(Structure):
                 ("in_features", c_int32), ("vocab_size", c_int32), ("embed_dim", c_int32),
                 ("padding_idx", c_int32), ("seq_len", c_int32), ("grad_weights", c_void_p),
                 ("branch_type", c_int32), ("merge_op", c_int32), ("branch_sources", POINTER(c_int32)),
-                ("n_branch_sources", c_int32)]
+                ("n_branch_sources", c_int32), ("num_heads", c_int32), ("head_dim", c_int32), ("causal", c_int32)]
 
 
 # name -> (restype, argtypes); mirrors include/mimir_hip.h one to one.

@@ -457,7 +457,8 @@ class DeviceGraph:
                 float(L.get("eps", 1e-5)), int(L.get("affine", True)), int(L.get("use_bias", True)),
                 int(L.get("in_features", 0)), int(L.get("vocab_size", 0)), int(L.get("embed_dim", 0)),
                 int(L.get("padding_idx", -1)), int(L.get("seq_len", 0)),
-                dg.ptr if dg is not None else None, bt, mop, csrcs, len(srcs))
+                dg.ptr if dg is not None else None, bt, mop, csrcs, len(srcs),
+                int(L.get("num_heads", 8)), int(L.get("head_dim", 0)), int(bool(L.get("causal", False))))
         self.c_layers = arr
 
     def grads(self):

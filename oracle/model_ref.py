@@ -20,7 +20,8 @@ class _Spec(Structure):
                 ("affine", c_int32), ("use_bias", c_int32), ("in_features", c_int32),
                 ("vocab_size", c_int32), ("embed_dim", c_int32), ("padding_idx", c_int32),
                 ("seq_len", c_int32), ("branch_type", c_int32), ("merge_op", c_int32),
-                ("branch_sources", POINTER(c_int32)), ("n_branch_sources", c_int32)]
+                ("branch_sources", POINTER(c_int32)), ("n_branch_sources", c_int32),
+                ("num_heads", c_int32), ("head_dim", c_int32), ("causal", c_int32)]
 
 # The reference's BranchType and MergeOperation (Layers.hpp:59-80), in order.
 BRANCH_TYPES = ("NONE", "RESIDUAL", "SKIP_CONNECTION", "DENSE_CONNECTION", "ATTENTION_BRANCH", "MULTI_SCALE",
@@ -116,7 +117,8 @@ def _marshal(layers, fin, iin):
                          int(L.get("seq_len", 0)),
                          BRANCH_TYPES.index(L["branch_type"]) if "branch_type" in L else -1,
                          MERGE_OPS.index(L["merge_op"]) if "merge_op" in L else -1,
-                         srcs, len(L.get("branch_sources", [])))
+                         srcs, len(L.get("branch_sources", [])),
+                         int(L.get("num_heads", 8)), int(L.get("head_dim", 0)), int(bool(L.get("causal", False))))
     fa = {k: np.ascontiguousarray(v, np.float32).ravel() for k, v in fin.items()}
     ia = {k: np.ascontiguousarray(v, np.int32).ravel() for k, v in iin.items()}
     keep += list(fa.values()) + list(ia.values())

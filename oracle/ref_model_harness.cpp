@@ -47,6 +47,10 @@ struct ref_layer_spec {
     int32_t merge_op;
     const int32_t* branch_sources;
     int32_t n_branch_sources;
+    // Attention fields (Layers.hpp:174-178).
+    int32_t num_heads;
+    int32_t head_dim;
+    int32_t causal;
 };
 
 // Layers from the specs, weights copied into the blocks allocateParams made.
@@ -75,6 +79,9 @@ static void build_model(Model& m, const ref_layer_spec* specs, int32_t n_layers)
         if (s.branch_type >= 0) L.branch_type = static_cast<BranchType>(s.branch_type);
         if (s.merge_op >= 0) L.merge_op = static_cast<MergeOperation>(s.merge_op);
         L.branch_sources.assign(s.branch_sources, s.branch_sources + (s.branch_sources ? s.n_branch_sources : 0));
+        L.num_heads = s.num_heads;
+        L.head_dim = s.head_dim;
+        L.causal = s.causal != 0;
     }
     m.allocateParams();
     for (int32_t i = 0; i < n_layers; ++i) {

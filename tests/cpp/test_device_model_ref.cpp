@@ -250,6 +250,49 @@ void attention_at_call_site() {
     CHECK(!ref_msg.empty() && ref_msg == dev_msg);
 }
 
+// DeviceModel<Layer> on a pre-norm attention block of reference Layers
+// (LayerNorm -> SelfAttention -> Add), beside Model::forwardPassNamed.
+// Normwise at 1e-4: each layer's element-wise parity is tested on its own.
+void attention_block_model(mimir_hip::Context& c) {
+    const int seq = 24, e = 32, heads = 4;
+    Model m;
+    m.push("ln", "LayerNorm", 2 * e);
+    m.push("attn", "SelfAttention", 4 * e * e);
+    m.push("res", "Add", 0);
+    auto& layers = m.getMutableLayers();
+    layers[0].inputs = {"inp"};
+    layers[0].output = "h";
+    layers[0].in_features = e;
+    layers[1].inputs = {"h"};
+    layers[1].output = "a";
+    layers[1].seq_len = seq;
+    layers[1].embed_dim = e;
+    layers[1].num_heads = heads;
+    layers[1].causal = true;
+    layers[2].inputs = {"a", "inp"};
+    layers[2].output = "x";
+    m.allocateParams();
+    float* g = layers[0].getWeights();
+    for (int i = 0; i < e; ++i) {
+        g[i] = 1.0f + 0.03f * static_cast<float>(i % 7);
+        g[e + i] = 0.01f * static_cast<float>(i % 5);
+    }
+    float* w = layers[1].getWeights();
+    CHECK(w != nullptr && layers[1].getWeightsSize() >= static_cast<size_t>(4 * e * e));
+    for (int i = 0; i < 4 * e * e; ++i) w[i] = std::sin(0.013f * static_cast<float>(i) + 0.4f) * 0.18f;
+    std::vector<float> x(seq * e);
+    for (size_t i = 0; i < x.size(); ++i) x[i] = std::cos(0.21f * static_cast<float>(i)) * 1.1f;
+    const FMap fin{{"inp", x}};
+    const std::vector<float> ref = m.forwardPassNamed(fin, IMap{}, false);
+    mimir_hip::DeviceModel<Layer> dm(c, m.getLayers());
+    const std::vector<float> got = dm.forwardPassNamed(fin, IMap{}, false);
+    float mx = 0.f;
+    for (float v : ref) mx = std::fmax(mx, std::fabs(v));
+    bool ok = got.size() == ref.size() && !ref.empty();
+    for (size_t i = 0; ok && i < ref.size(); ++i) ok = std::fabs(got[i] - ref[i]) <= 1e-6f + 1e-4f * mx;
+    CHECK(ok);
+}
+
 }  // namespace
 
 int main() {
@@ -259,6 +302,7 @@ int main() {
         weight_block_and_backward(c);
         int_ids_forward(c);
         attention_at_call_site();
+        attention_block_model(c);
     } catch (const std::exception& e) {
         std::fprintf(stderr, "FAIL: exception %s\n", e.what());
         return 1;

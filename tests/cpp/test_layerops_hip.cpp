@@ -40,6 +40,9 @@ struct TestLayer {
     BranchType branch_type = BranchType::NONE;
     MergeOperation merge_op = MergeOperation::ADD;
     std::vector<int> branch_sources;
+    int num_heads = 8;  // Layers.hpp:175
+    int head_dim = 0;
+    bool causal = false;
     const float* getWeights() const { return weights.data(); }
     size_t getWeightsSize() const { return weights.size(); }
 };
