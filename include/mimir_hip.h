@@ -238,7 +238,8 @@ int mimir_rope_fwd(mimir_ctx* ctx, const float* q, float* q_out, int64_t q_heads
  * so q / k / v may be the three column blocks of one fused QKV buffer
  * (ld = 3 * heads * head_dim).  Head h owns columns [h*head_dim,
  * (h+1)*head_dim).  The reference's scale is 1.0f / sqrtf(head_dim).
- * head_dim <= 128.  fp32 throughout (fp32 matrix-core products), no score
+ * head_dim <= 2048 (above 128 a plain fp32 vector kernel runs instead of the
+ * matrix-core one).  fp32 throughout (fp32 matrix-core products), no score
  * matrix in memory.  out must not overlap q, k or v.  kv_len == 0 gives zeros;
  * batch == 0 or q_len == 0 is a no-op.  Device pointers, stream order. */
 int mimir_attention_fwd(mimir_ctx* ctx, const float* q, int64_t ld_q, const float* k, const float* v,
@@ -253,7 +254,7 @@ int mimir_attention_fwd(mimir_ctx* ctx, const float* q, int64_t ld_q, const floa
  * at least 4 embed_dim^2 floats (the reference reads past a shorter block; it
  * is refused here); out [seq_len x embed_dim].  The projections are fp32
  * library GEMMs, the core is mimir_attention_fwd with the reference's
- * scale 1/sqrtf(head_dim).  head_dim <= 128.  Uses the context's scratch
+ * scale 1/sqrtf(head_dim).  head_dim <= 2048.  Uses the context's scratch
  * (4 seq_len embed_dim floats).  out must not overlap input or weights. */
 int mimir_self_attention_fwd(mimir_ctx* ctx, const float* input, int64_t seq_len, int64_t embed_dim,
                              int64_t num_heads, int causal, const float* weights, int64_t weights_len,

@@ -404,6 +404,72 @@ __global__ __launch_bounds__(kThreads, 2) void attention_fwd_mfma(AttnArgs a) {
     }
 }
 
+// Heads wider than 128 (up to 2048): one wave per query, the head's
+// dimensions spread over the lanes (CH per lane, lane + 64 c), each score a
+// DPP wave sum, the same online softmax (base-2 scores, running max and
+// sum) and the same division by (sum + 1e-9).  Plain fp32 vector code: the
+// reference accepts any head size, the matrix-core kernel's register layout
+// stops at 128.  Keys are read row by row through L2 by all four waves of a
+// workgroup (four queries).
+constexpr int kGenericWaves = 4;
+template <int CH>
+__global__ __launch_bounds__(kGenericWaves * kWave) void attention_fwd_generic(AttnArgs a) {
+    const int lane = threadIdx.x % kWave;
+    const int64_t qi = static_cast<int64_t>(blockIdx.y) * kGenericWaves + threadIdx.x / kWave;
+    if (qi >= a.q_len) return;  // whole waves leave: no barrier below
+    const uint32_t bh = blockIdx.x;
+    const int64_t b = bh / static_cast<uint32_t>(a.heads);
+    const int64_t hd_off = static_cast<int64_t>(bh % static_cast<uint32_t>(a.heads)) * a.head_dim;
+    const float* qrow = a.q + (b * a.q_len + qi) * a.ld_q + hd_off;
+    const float* kb = a.k + b * a.kv_len * a.ld_kv + hd_off;
+    const float* vb = a.v + b * a.kv_len * a.ld_kv + hd_off;
+    float q[CH], acc[CH];
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+        const int d = lane + c * kWave;
+        q[c] = d < a.head_dim ? qrow[d] * a.qscale : 0.f;
+        acc[c] = 0.f;
+    }
+    const int64_t key_end = a.causal ? (qi + 1 < a.kv_len ? qi + 1 : a.kv_len) : a.kv_len;
+    float m_run = -1e30f, l_run = 0.f;
+    for (int64_t j = 0; j < key_end; ++j) {
+        const float* krow = kb + j * a.ld_kv;
+        const float* vrow = vb + j * a.ld_kv;
+        float part = 0.f;
+#pragma unroll
+        for (int c = 0; c < CH; ++c) {
+            const int d = lane + c * kWave;
+            if (d < a.head_dim) part += q[c] * krow[d];
+        }
+        const float s = wave_sum(part);  // wave-uniform
+        const float m_new = fmaxf(m_run, s);
+        const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+        const float p = __builtin_amdgcn_exp2f(s - m_new);
+        m_run = m_new;
+        l_run = l_run * alpha + p;
+#pragma unroll
+        for (int c = 0; c < CH; ++c) {
+            const int d = lane + c * kWave;
+            acc[c] = acc[c] * alpha + (d < a.head_dim ? p * vrow[d] : 0.f);
+        }
+    }
+    const float inv = 1.0f / (l_run + 1e-9f);
+    float* orow = a.out + (b * a.q_len + qi) * a.ld_out + hd_off;
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+        const int d = lane + c * kWave;
+        if (d < a.head_dim) orow[d] = acc[c] * inv;
+    }
+}
+
+template <int CH>
+int launch_generic(mimir_ctx* ctx, const AttnArgs& a, int64_t batch, int64_t heads) {
+    const dim3 grid(static_cast<unsigned>(batch * heads),
+                    static_cast<unsigned>((a.q_len + kGenericWaves - 1) / kGenericWaves));
+    attention_fwd_generic<CH><<<grid, kGenericWaves * kWave, 0, ctx->stream>>>(a);
+    return launched(ctx, "attention_fwd_generic");
+}
+
 template <int DP>
 int launch(mimir_ctx* ctx, const AttnArgs& a, bool vec) {
     if (vec) attention_fwd_mfma<DP, true><<<a.total_blocks, kThreads, 0, ctx->stream>>>(a);
@@ -422,7 +488,7 @@ int mimir_attention_fwd(mimir_ctx* ctx, const float* q, int64_t ld_q, const floa
     MIMIR_REQUIRE(ctx, batch >= 0 && q_len >= 0 && kv_len >= 0 && heads >= 1 && head_dim >= 1,
                   "attention: invalid shape (batch=%lld q_len=%lld kv_len=%lld heads=%lld head_dim=%lld)",
                   (long long)batch, (long long)q_len, (long long)kv_len, (long long)heads, (long long)head_dim);
-    MIMIR_REQUIRE(ctx, head_dim <= 128, "attention: head_dim %lld > 128 is not supported", (long long)head_dim);
+    MIMIR_REQUIRE(ctx, head_dim <= 2048, "attention: head_dim %lld > 2048 is not supported", (long long)head_dim);
     const int64_t width = heads * head_dim;
     MIMIR_REQUIRE(ctx, ld_q >= width && ld_kv >= width && ld_out >= width,
                   "attention: row strides (%lld, %lld, %lld) below heads * head_dim = %lld", (long long)ld_q,
@@ -459,7 +525,13 @@ int mimir_attention_fwd(mimir_ctx* ctx, const float* q, int64_t ld_q, const floa
                      ld_kv < (int64_t{1} << 31) / (4 * kKeyTile);
     if (head_dim <= 32) return launch<32>(ctx, a, vec);
     if (head_dim <= 64) return launch<64>(ctx, a, vec);
-    return launch<128>(ctx, a, vec);
+    if (head_dim <= 128) return launch<128>(ctx, a, vec);
+    MIMIR_REQUIRE(ctx, batch * heads <= INT32_MAX && (q_len + kGenericWaves - 1) / kGenericWaves <= 65535,
+                  "attention: grid exceeds the limit of the wide-head kernel");
+    if (head_dim <= 256) return launch_generic<4>(ctx, a, batch, heads);
+    if (head_dim <= 512) return launch_generic<8>(ctx, a, batch, heads);
+    if (head_dim <= 1024) return launch_generic<16>(ctx, a, batch, heads);
+    return launch_generic<32>(ctx, a, batch, heads);
 }
 
 // The attention layers (Model.cpp:5904-5934, 5936-5990): the projections as
@@ -475,7 +547,7 @@ int mimir_self_attention_fwd(mimir_ctx* ctx, const float* input, int64_t seq_len
     const int64_t e = embed_dim;
     MIMIR_REQUIRE(ctx, weights_len >= 4 * e * e, "SelfAttention: weight block of %lld floats, %lld needed",
                   (long long)weights_len, (long long)(4 * e * e));
-    MIMIR_REQUIRE(ctx, e / num_heads <= 128, "attention: head_dim %lld > 128 is not supported",
+    MIMIR_REQUIRE(ctx, e / num_heads <= 2048, "attention: head_dim %lld > 2048 is not supported",
                   (long long)(e / num_heads));
     if (seq_len == 0) return MIMIR_OK;
     MIMIR_REQUIRE(ctx, input && weights && out, "SelfAttention: null pointer");
@@ -502,7 +574,7 @@ int mimir_cross_attention_fwd(mimir_ctx* ctx, const float* query_input, int64_t 
     const int64_t e = embed_dim;
     MIMIR_REQUIRE(ctx, weights_len >= 4 * e * e, "CrossAttention: weight block of %lld floats, %lld needed",
                   (long long)weights_len, (long long)(4 * e * e));
-    MIMIR_REQUIRE(ctx, e / num_heads <= 128, "attention: head_dim %lld > 128 is not supported",
+    MIMIR_REQUIRE(ctx, e / num_heads <= 2048, "attention: head_dim %lld > 2048 is not supported",
                   (long long)(e / num_heads));
     MIMIR_REQUIRE(ctx, query_input && kv_input && weights && out, "CrossAttention: null pointer");
     MIMIR_ENTER(ctx);

@@ -178,7 +178,7 @@ def test_invalid_arguments(ctx):
     q = ctx.empty(1024)
     try:
         with pytest.raises(M.MimirError, match="head_dim"):
-            ctx.attention(q, q, q, q, 1, 2, 2, 1, 256)
+            ctx.attention(q, q, q, q, 1, 2, 2, 1, 4096)
         with pytest.raises(M.MimirError, match="row strides"):
             ctx.attention(q, q, q, q, 1, 2, 2, 2, 16, ld_q=16)
         with pytest.raises(M.MimirError, match="invalid shape"):
@@ -264,3 +264,14 @@ def test_attention_layer_refusals(ctx):
             ctx.cross_attention(b, 0, b, 3, 16, 2, False, b, 4096, b)
     finally:
         b.free()
+
+
+@pytest.mark.parametrize("b,lq,lk,heads,hd", [(1, 40, 40, 2, 160), (2, 33, 70, 1, 256), (1, 20, 20, 1, 200),
+                                               (1, 9, 9, 2, 512), (1, 5, 7, 1, 1000)])
+@pytest.mark.parametrize("causal", [False, True])
+def test_wide_heads(ctx, b, lq, lk, heads, hd, causal):
+    """Heads wider than 128 (the plain fp32 vector kernel): the reference
+    accepts any head size."""
+    q, k, v = rand_qkv(hd + lq, b, lq, lk, heads * hd)
+    print(f"attention wide b={b} lq={lq} lk={lk} h={heads} d={hd} causal={causal}", flush=True)
+    check(gpu_attention(ctx, q, k, v, heads, causal), q, k, v, heads, causal, f"wide d{hd}")
