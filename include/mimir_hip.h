@@ -270,6 +270,49 @@ int mimir_cross_attention_fwd(mimir_ctx* ctx, const float* query_input, int64_t 
                               const float* kv_input, int64_t kv_len, int64_t embed_dim, int64_t num_heads,
                               int causal, const float* weights, int64_t weights_len, float* out);
 
+/* Backward of the attention core: the per-head part of the reference's
+ * backward_self_attention / backward_cross_attention (Model.cpp:6892-7028,
+ * 7122-7246).  From q, k, v (laid out as for mimir_attention_fwd) and dout,
+ * the gradient of the core's output (ld_dout), writes
+ *   dv = P^T dout,  dq = scale dS k,  dk = scale dS^T q,
+ *   dS = P (dout v^T - rowsum(P * (dout v^T))), 0 on masked keys,
+ * with P the core's probabilities (causal j > i masked to -1e9, max from
+ * -1e30, p = e / (sum + 1e-9)).  dq rows have ld_dq, dk and dv rows ld_dkv
+ * (dk and dv may be column blocks of one buffer, as the reference's dqkv).
+ * Overwrites dq / dk / dv.  P and dS are materialised per group of heads
+ * in the context's scratch (2 q_len kv_len floats per head, groups capped at
+ * 1 GiB, one head at least); the products are fp32 library GEMMs, the row
+ * passes (mask + softmax, softmax backward) hand-written kernels.
+ * kv_len == 0: dq = 0.  Outputs must not overlap the inputs. */
+int mimir_attention_bwd(mimir_ctx* ctx, const float* q, int64_t ld_q, const float* k, const float* v,
+                        int64_t ld_kv, const float* dout, int64_t ld_dout, float* dq, int64_t ld_dq, float* dk,
+                        float* dv, int64_t ld_dkv, int64_t batch, int64_t q_len, int64_t kv_len, int64_t heads,
+                        int64_t head_dim, float scale, int causal);
+
+/* backward_self_attention (Model.cpp:6847-7062), as Model::backwardPass's
+ * SelfAttention / MultiHeadAttention branch calls it (:8034-8072): input
+ * [seq_len x E] (the layer's forward input), grad_out [seq_len x E], the
+ * weight block as for mimir_self_attention_fwd.  Adds dWqkv / dWout into
+ * grad_weights (same layout as weights; skipped when NULL) and writes the
+ * input gradient dx = dqkv Wqkv^T to grad_input, or adds it there when
+ * accumulate (accumulate_grad's add).  grad_input may be grad_out itself
+ * (it is written last).  Scratch: 8 seq_len E floats plus the core's. */
+int mimir_self_attention_bwd(mimir_ctx* ctx, const float* input, const float* grad_out, int64_t seq_len,
+                             int64_t embed_dim, int64_t num_heads, int causal, const float* weights,
+                             int64_t weights_len, float* grad_weights, float* grad_input, int accumulate);
+
+/* backward_cross_attention (Model.cpp:7068-7300), as the CrossAttention
+ * branch calls it (:8074-8130): adds dWq / dWkv / dWout into grad_weights
+ * (skipped when NULL), then writes (or, with the accumulate flags, adds) the
+ * query gradient into grad_query and after it the key/value gradient into
+ * grad_kv; either may be grad_out's buffer and the two may be one buffer
+ * (inputs that share a name).  Scratch: 4 (query_len + kv_len) E floats plus
+ * the core's. */
+int mimir_cross_attention_bwd(mimir_ctx* ctx, const float* query_input, int64_t query_len, const float* kv_input,
+                              int64_t kv_len, const float* grad_out, int64_t embed_dim, int64_t num_heads,
+                              int causal, const float* weights, int64_t weights_len, float* grad_weights,
+                              float* grad_query, int accumulate_query, float* grad_kv, int accumulate_kv);
+
 /* ---------------------------------------------------------------------------
  * Backward of the path's ops: the branches of the reference's
  * Model::backwardPass (Model.cpp:7305-9153).  Device pointers, stream order.
@@ -370,8 +413,9 @@ typedef struct mimir_store mimir_store;
 #define MIMIR_LAYER_IDENTITY 10  /* LayerOps::identity_forward */
 #define MIMIR_LAYER_DROPOUT 11   /* LayerOps::dropout_forward at inference: identity */
 /* The attention layers (Model.cpp:5904-5990): projections + the fused core,
- * mimir_self_attention_fwd / mimir_cross_attention_fwd.  Forward only: a
- * backward that reaches one returns EINVAL. */
+ * mimir_self_attention_fwd / mimir_cross_attention_fwd; in
+ * mimir_store_backward, mimir_self_attention_bwd / mimir_cross_attention_bwd
+ * (Model.cpp:8034-8130). */
 #define MIMIR_LAYER_SELF_ATTENTION 12      /* LayerOps::self_attention_forward */
 #define MIMIR_LAYER_MULTIHEAD_ATTENTION 13 /* LayerOps::multihead_attention_forward (the same) */
 #define MIMIR_LAYER_CROSS_ATTENTION 14     /* LayerOps::cross_attention_forward (inputs: query, key_value) */

@@ -38,20 +38,34 @@ namespace mimir {
 
 int gemm_f32(mimir_ctx* ctx, int64_t M, int64_t N, int64_t K, const float* A, int64_t lda, const float* B,
              int64_t ldb, float* C, int64_t ldc) {
-    if (M == 0 || N == 0) return MIMIR_OK;
+    return gemm_f32_ex(ctx, false, false, M, N, K, 1.0f, A, lda, 0, B, ldb, 0, 0.0f, C, ldc, 0, 1);
+}
+
+int gemm_f32_ex(mimir_ctx* ctx, bool trans_a, bool trans_b, int64_t M, int64_t N, int64_t K, float alpha,
+                const float* A, int64_t lda, int64_t stride_a, const float* B, int64_t ldb, int64_t stride_b,
+                float beta, float* C, int64_t ldc, int64_t stride_c, int64_t batch) {
+    if (M == 0 || N == 0 || batch == 0) return MIMIR_OK;
     const int64_t lim = INT32_MAX;
-    if (M > lim || N > lim || K > lim || lda > lim || ldb > lim || ldc > lim)
+    if (M > lim || N > lim || K > lim || lda > lim || ldb > lim || ldc > lim || batch > lim)
         return fail(ctx, MIMIR_EINVAL, "matrix product: dimensions exceed the 32-bit library limit");
     int st = MIMIR_OK;
     rocblas_handle h = handle_of(ctx, &st);
     if (!h) return st;
-    const float one = 1.0f, zero = 0.0f;
-    // K == 0: C = 0 (beta = 0 with an empty sum).
-    const rocblas_status s =
-        rocblas_sgemm(h, rocblas_operation_none, rocblas_operation_none, static_cast<rocblas_int>(N),
-                      static_cast<rocblas_int>(M), static_cast<rocblas_int>(K), &one, B, static_cast<rocblas_int>(ldb),
-                      A, static_cast<rocblas_int>(lda), &zero, C, static_cast<rocblas_int>(ldc));
-    if (s != rocblas_status_success) return fail(ctx, MIMIR_EDEVICE, "rocblas_sgemm failed (status %d)", (int)s);
+    // Row-major C = op(A) op(B) is column-major C^T = op(B)^T op(A)^T: the
+    // operands swap and each keeps its own transpose flag.  K == 0 with
+    // beta == 0 gives C = 0 (an empty sum).
+    const rocblas_operation ob = trans_b ? rocblas_operation_transpose : rocblas_operation_none;
+    const rocblas_operation oa = trans_a ? rocblas_operation_transpose : rocblas_operation_none;
+    const auto n32 = static_cast<rocblas_int>(N), m32 = static_cast<rocblas_int>(M), k32 = static_cast<rocblas_int>(K);
+    rocblas_status s;
+    if (batch == 1)
+        s = rocblas_sgemm(h, ob, oa, n32, m32, k32, &alpha, B, static_cast<rocblas_int>(ldb), A,
+                          static_cast<rocblas_int>(lda), &beta, C, static_cast<rocblas_int>(ldc));
+    else
+        s = rocblas_sgemm_strided_batched(h, ob, oa, n32, m32, k32, &alpha, B, static_cast<rocblas_int>(ldb),
+                                          stride_b, A, static_cast<rocblas_int>(lda), stride_a, &beta, C,
+                                          static_cast<rocblas_int>(ldc), stride_c, static_cast<rocblas_int>(batch));
+    if (s != rocblas_status_success) return fail(ctx, MIMIR_EDEVICE, "rocBLAS sgemm failed (status %d)", (int)s);
     return MIMIR_OK;
 }
 

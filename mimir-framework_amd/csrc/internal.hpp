@@ -96,6 +96,12 @@ int ensure_scratch(mimir_ctx* ctx, size_t bytes, void** out);
 // (rocBLAS; gemm.hip), and the release of its handle at context teardown.
 int gemm_f32(mimir_ctx* ctx, int64_t M, int64_t N, int64_t K, const float* A, int64_t lda, const float* B,
              int64_t ldb, float* C, int64_t ldc);
+// The general form: row-major C = alpha op(A) op(B) + beta C over `batch`
+// products whose operands sit `stride_*` floats apart; op(A) is M x K (A
+// stored K x M when trans_a), op(B) is K x N (B stored N x K when trans_b).
+int gemm_f32_ex(mimir_ctx* ctx, bool trans_a, bool trans_b, int64_t M, int64_t N, int64_t K, float alpha,
+                const float* A, int64_t lda, int64_t stride_a, const float* B, int64_t ldb, int64_t stride_b,
+                float beta, float* C, int64_t ldc, int64_t stride_c, int64_t batch);
 void gemm_release(mimir_ctx* ctx);
 
 // Look up this context's device address of the no-allocation scratch array

@@ -561,10 +561,38 @@ int backward_layer(mimir_store* s, const mimir_layer& L, const Snap& sn) {
                                               : mimir_silu_bwd(ctx, x, g, d0, gn, a0);
         }
         case MIMIR_LAYER_SELF_ATTENTION:
-        case MIMIR_LAYER_MULTIHEAD_ATTENTION:
-        case MIMIR_LAYER_CROSS_ATTENTION:  // Model.cpp:8034-8127 -> backward_self_attention (:6847) & co.
-            return fail(ctx, MIMIR_EINVAL, "%s backward is not on this path (layer %s)", type_name(L.type),
-                        layer_name(L));
+        case MIMIR_LAYER_MULTIHEAD_ATTENTION: {  // :8034-8072 -> backward_self_attention (:6847-7062)
+            if (sn.vals.empty()) return MIMIR_OK;
+            const Slot& x = sn.vals[0];
+            const int64_t seq = L.seq_len > 0 ? L.seq_len : 1;
+            const int64_t e = L.embed_dim > 0 ? L.embed_dim : (x.n % seq == 0 ? x.n / seq : x.n);
+            const int64_t heads = L.num_heads > 1 ? L.num_heads : 1;
+            if (!L.weights || L.weights_len < 4 * e * e) return MIMIR_OK;  // "weights invalid": skipped
+            // backward_self_attention's own refusals (:6860-6863): "failed", skipped
+            if (e <= 0 || e % heads != 0 || x.n != seq * e || gn != seq * e) return MIMIR_OK;
+            if (int st = grad_dst(s, nm(0), x.n, &d0, &a0)) return st;
+            return mimir_self_attention_bwd(ctx, static_cast<const float*>(x.buf->p), g, seq, e, heads, L.causal,
+                                            L.weights, L.weights_len, L.grad_weights, d0, a0);
+        }
+        case MIMIR_LAYER_CROSS_ATTENTION: {  // :8074-8130 -> backward_cross_attention (:7068-7300)
+            if (sn.vals.size() < 2) return MIMIR_OK;  // "need 2 inputs": skipped
+            const Slot& xq = sn.vals[0];
+            const Slot& xkv = sn.vals[1];
+            const int64_t heads = L.num_heads > 1 ? L.num_heads : 1;
+            int64_t e = L.embed_dim;
+            if (e <= 0 && L.head_dim > 0) e = static_cast<int64_t>(L.head_dim) * heads;
+            if (e <= 0 || e % heads != 0) return MIMIR_OK;          // "invalid embed_dim": skipped
+            if (xq.n % e != 0 || xkv.n % e != 0) return MIMIR_OK;   // "input size mismatch": skipped
+            const int64_t lq = xq.n / e, lk = xkv.n / e;
+            if (gn != lq * e) return MIMIR_OK;                      // "grad size mismatch": skipped
+            if (!L.weights || L.weights_len < 4 * e * e) return MIMIR_OK;
+            if (lq <= 0 || lk <= 0) return MIMIR_OK;                // backward_cross_attention's refusal
+            if (int st = grad_dst(s, nm(0), xq.n, &d0, &a0)) return st;
+            if (int st = grad_dst(s, nm(1), xkv.n, &d1, &a1)) return st;
+            return mimir_cross_attention_bwd(ctx, static_cast<const float*>(xq.buf->p), lq,
+                                             static_cast<const float*>(xkv.buf->p), lk, g, e, heads, L.causal,
+                                             L.weights, L.weights_len, L.grad_weights, d0, a0, d1, a1);
+        }
         default:  // RMSNorm, Softmax, LogSoftmax: the fallback at :9133-9140
             if (gn != n0) return MIMIR_OK;
             return grad_pass(s, nm(0), g, gn);

@@ -111,6 +111,11 @@ SIGNATURES = {
                                     c_int64, c_int64, c_float, c_int]),
     "mimir_self_attention_fwd": (c_int, [_P, _P, c_int64, c_int64, c_int64, c_int, _P, c_int64, _P]),
     "mimir_cross_attention_fwd": (c_int, [_P, _P, c_int64, _P, c_int64, c_int64, c_int64, c_int, _P, c_int64, _P]),
+    "mimir_attention_bwd": (c_int, [_P, _P, c_int64, _P, _P, c_int64, _P, c_int64, _P, c_int64, _P, _P, c_int64,
+                                    c_int64, c_int64, c_int64, c_int64, c_int64, c_float, c_int]),
+    "mimir_self_attention_bwd": (c_int, [_P, _P, _P, c_int64, c_int64, c_int64, c_int, _P, c_int64, _P, _P, c_int]),
+    "mimir_cross_attention_bwd": (c_int, [_P, _P, c_int64, _P, c_int64, _P, c_int64, c_int64, c_int, _P, c_int64, _P,
+                                          _P, c_int, _P, c_int]),
     "mimir_layernorm_bwd": (c_int, [_P, _P, _P, _P, _P, _P, _P, c_int64, c_int64, c_float, c_int]),
     "mimir_layernorm_bwd_noalloc": (c_int, [_P, _P, _P, _P, _P, _P, _P, c_int64, c_int64, c_float, c_int]),
     "mimir_gelu_bwd": (c_int, [_P, _P, _P, _P, c_int64, c_int]),

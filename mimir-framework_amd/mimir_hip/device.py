@@ -231,6 +231,34 @@ class Context:
 
     # -- backward (Model::backwardPass branches) -------------------------------
 
+    def attention_bwd(self, q, k, v, dout, dq, dk, dv, batch, q_len, kv_len, heads, head_dim, causal=False,
+                      scale=None, ld_q=None, ld_kv=None, ld_dout=None, ld_dq=None, ld_dkv=None):
+        """mimir_attention_bwd: dq / dk / dv of the attention core from dout,
+        strides as for attention() (default heads * head_dim)."""
+        width = heads * head_dim
+        if scale is None:
+            scale = float(np.float32(1.0) / np.sqrt(np.float32(head_dim)))
+        self.check(self.lib.mimir_attention_bwd(self.handle, _ptr(q), ld_q or width, _ptr(k), _ptr(v), ld_kv or width,
+                                                _ptr(dout), ld_dout or width, _ptr(dq), ld_dq or width, _ptr(dk),
+                                                _ptr(dv), ld_dkv or width, batch, q_len, kv_len, heads, head_dim,
+                                                float(scale), int(bool(causal))))
+
+    def self_attention_bwd(self, x, dy, seq_len, embed_dim, num_heads, causal, weights, weights_len, grad_weights,
+                           dx, accumulate=False):
+        """mimir_self_attention_bwd: backward_self_attention on device buffers
+        (grad_weights may be None)."""
+        self.check(self.lib.mimir_self_attention_bwd(self.handle, _ptr(x), _ptr(dy), seq_len, embed_dim, num_heads,
+                                                     int(bool(causal)), _ptr(weights), weights_len,
+                                                     _ptr(grad_weights), _ptr(dx), int(bool(accumulate))))
+
+    def cross_attention_bwd(self, xq, query_len, xkv, kv_len, dy, embed_dim, num_heads, causal, weights, weights_len,
+                            grad_weights, dxq, dxkv, acc_q=False, acc_kv=False):
+        """mimir_cross_attention_bwd: backward_cross_attention on device buffers."""
+        self.check(self.lib.mimir_cross_attention_bwd(self.handle, _ptr(xq), query_len, _ptr(xkv), kv_len, _ptr(dy),
+                                                      embed_dim, num_heads, int(bool(causal)), _ptr(weights),
+                                                      weights_len, _ptr(grad_weights), _ptr(dxq), int(bool(acc_q)),
+                                                      _ptr(dxkv), int(bool(acc_kv))))
+
     def layernorm_bwd(self, x, dy, gamma, dx, dgamma, dbeta, groups, n, eps, accumulate=False):
         self.check(self.lib.mimir_layernorm_bwd(self.handle, _ptr(x), _ptr(dy), _ptr(gamma), _ptr(dx),
                                                 _ptr(dgamma), _ptr(dbeta), groups, n, eps,

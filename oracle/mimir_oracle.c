@@ -511,3 +511,119 @@ int oracle_attention(const float* q, int64_t ld_q, const float* k, const float* 
     free(row);
     return ORACLE_OK;
 }
+
+/* The per-head core of backward_self_attention (Model.cpp:6892-7028) and
+ * backward_cross_attention (:7122-7246), over `batch` sequences laid out as
+ * for oracle_attention; dout is the gradient of the attended heads (the
+ * reference's dAtt).  Per head, in the reference's loop order:
+ *   P[i][j]: s = (sum_k q_ik k_jk) * scale, masked (causal, j > i) -1e9;
+ *            max from -1e30 over every j; e = expf(s - max), sum in j order;
+ *            p = e * (1 / (sum + 1e-9f))                       (:6892-6920)
+ *   dv[j][k] = 0 + sum_i P[i][j] dout[i][k]  (i in order)       (:6967-6977)
+ *   dP[i][j] = sum_k dout[i][k] v[j][k]                         (:6979-6989)
+ *   dot_i = sum_j dP[i][j] P[i][j] (softmax_row_dot, :6841-6845)
+ *   dS[i][j] = masked ? 0 : (dP[i][j] - dot_i) * P[i][j]        (:6991-7005)
+ *   dq[i][k] = 0 + (sum_j dS[i][j] k[j][k]) * scale              (:7007-7016)
+ *   dk[j][k] = 0 + (sum_i dS[i][j] q[i][k]) * scale              (:7018-7028)
+ * dq rows stride ld_dq, dk / dv rows stride ld_dkv.
+ * The reference's runtime as compiled (g++ -O2 -mfma, C++'s default
+ * -ffp-contract=fast) fuses every one of these multiply-accumulate loops --
+ * the score dot as well, unlike the -O3 build of LayerOps' forward -- into
+ * fused multiply-adds; fmaf restates that.  Of the 64 fused / unfused
+ * combinations only this one matches Model::backwardPass bit for bit
+ * (tests/test_oracle_attention_bwd.py). */
+int oracle_attention_bwd(const float* q, int64_t ld_q, const float* k, const float* v, int64_t ld_kv,
+                         const float* dout, int64_t ld_dout, float* dq, int64_t ld_dq, float* dk, float* dv,
+                         int64_t ld_dkv, int64_t batch, int64_t q_len, int64_t kv_len, int64_t heads,
+                         int64_t head_dim, float scale, int causal) {
+    const int64_t width = heads * head_dim;
+    if (batch < 0 || q_len < 0 || kv_len < 0 || heads <= 0 || head_dim <= 0 || ld_q < width ||
+        ld_kv < width || ld_dout < width || ld_dq < width || ld_dkv < width)
+        return ORACLE_EINVAL;
+    if (batch == 0 || q_len == 0) return ORACLE_OK;
+    const size_t tt = (size_t)q_len * (size_t)(kv_len > 0 ? kv_len : 1);
+    float* P = (float*)malloc(tt * sizeof(float));
+    float* dP = (float*)malloc(tt * sizeof(float));
+    float* dS = (float*)malloc(tt * sizeof(float));
+    if (!P || !dP || !dS) {
+        free(P);
+        free(dP);
+        free(dS);
+        return ORACLE_EINVAL;
+    }
+    for (int64_t b = 0; b < batch; ++b) {
+        const float* qb = q + b * q_len * ld_q;
+        const float* kb = k + b * kv_len * ld_kv;
+        const float* vb = v + b * kv_len * ld_kv;
+        const float* ob = dout + b * q_len * ld_dout;
+        float* dqb = dq + b * q_len * ld_dq;
+        float* dkb = dk + b * kv_len * ld_dkv;
+        float* dvb = dv + b * kv_len * ld_dkv;
+        for (int64_t h = 0; h < heads; ++h) {
+            const int64_t off = h * head_dim;
+            for (int64_t i = 0; i < q_len; ++i) {
+                float* pr = P + i * kv_len;
+                float maxv = -1e30f;
+                for (int64_t j = 0; j < kv_len; ++j) {
+                    float s = -1e9f;
+                    if (!(causal && j > i)) {
+                        float dot = 0.0f;
+                        for (int64_t d = 0; d < head_dim; ++d)
+                            dot = fmaf(qb[i * ld_q + off + d], kb[j * ld_kv + off + d], dot);
+                        s = dot * scale;
+                    }
+                    pr[j] = s;
+                    if (s > maxv) maxv = s;
+                }
+                float sum = 0.0f;
+                for (int64_t j = 0; j < kv_len; ++j) {
+                    const float e = expf(pr[j] - maxv);
+                    pr[j] = e;
+                    sum += e;
+                }
+                const float inv = 1.0f / (sum + 1e-9f);
+                for (int64_t j = 0; j < kv_len; ++j) pr[j] *= inv;
+            }
+            for (int64_t j = 0; j < kv_len; ++j)
+                for (int64_t d = 0; d < head_dim; ++d) {
+                    float sum = 0.0f;
+                    for (int64_t i = 0; i < q_len; ++i)
+                        sum = fmaf(P[i * kv_len + j], ob[i * ld_dout + off + d], sum);
+                    dvb[j * ld_dkv + off + d] = 0.0f + sum;
+                }
+            for (int64_t i = 0; i < q_len; ++i)
+                for (int64_t j = 0; j < kv_len; ++j) {
+                    float sum = 0.0f;
+                    for (int64_t d = 0; d < head_dim; ++d)
+                        sum = fmaf(ob[i * ld_dout + off + d], vb[j * ld_kv + off + d], sum);
+                    dP[i * kv_len + j] = sum;
+                }
+            for (int64_t i = 0; i < q_len; ++i) {
+                const float* pr = P + i * kv_len;
+                const float* dpr = dP + i * kv_len;
+                float dot = 0.0f;
+                for (int64_t j = 0; j < kv_len; ++j) dot = fmaf(dpr[j], pr[j], dot);
+                for (int64_t j = 0; j < kv_len; ++j)
+                    dS[i * kv_len + j] = (causal && j > i) ? 0.0f : (dpr[j] - dot) * pr[j];
+            }
+            for (int64_t i = 0; i < q_len; ++i)
+                for (int64_t d = 0; d < head_dim; ++d) {
+                    float sum = 0.0f;
+                    for (int64_t j = 0; j < kv_len; ++j)
+                        sum = fmaf(dS[i * kv_len + j], kb[j * ld_kv + off + d], sum);
+                    dqb[i * ld_dq + off + d] = 0.0f + sum * scale;
+                }
+            for (int64_t j = 0; j < kv_len; ++j)
+                for (int64_t d = 0; d < head_dim; ++d) {
+                    float sum = 0.0f;
+                    for (int64_t i = 0; i < q_len; ++i)
+                        sum = fmaf(dS[i * kv_len + j], qb[i * ld_q + off + d], sum);
+                    dkb[j * ld_dkv + off + d] = 0.0f + sum * scale;
+                }
+        }
+    }
+    free(P);
+    free(dP);
+    free(dS);
+    return ORACLE_OK;
+}

@@ -157,6 +157,15 @@ int oracle_attention(const float* q, int64_t ld_q, const float* k, const float* 
                      float* out, int64_t ld_out, int64_t batch, int64_t q_len, int64_t kv_len,
                      int64_t heads, int64_t head_dim, float scale, int causal);
 
+/* The per-head core of the reference's backward_self_attention /
+ * backward_cross_attention (Model.cpp:6892-7028, 7122-7246): from q, k, v
+ * (laid out as for oracle_attention) and dout, the gradient of the attended
+ * heads, writes dq (rows ld_dq), dk and dv (rows ld_dkv). */
+int oracle_attention_bwd(const float* q, int64_t ld_q, const float* k, const float* v, int64_t ld_kv,
+                         const float* dout, int64_t ld_dout, float* dq, int64_t ld_dq, float* dk, float* dv,
+                         int64_t ld_dkv, int64_t batch, int64_t q_len, int64_t kv_len, int64_t heads,
+                         int64_t head_dim, float scale, int causal);
+
 #ifdef __cplusplus
 }
 #endif

@@ -73,6 +73,8 @@ def _oracle():
             "oracle_embedding_bwd_f32": [P, c_int64, P, P, c_int64, c_int32, c_int32, c_int32],
             "oracle_attention": [P, c_int64, P, P, c_int64, P, c_int64, c_int64, c_int64, c_int64,
                                  c_int64, c_int64, c_float, c_int32],
+            "oracle_attention_bwd": [P, c_int64, P, P, c_int64, P, c_int64, P, c_int64, P, P, c_int64,
+                                     c_int64, c_int64, c_int64, c_int64, c_int64, c_float, c_int32],
         }
         for name, args in sig.items():
             fn = getattr(lib, name)
@@ -405,6 +407,34 @@ def attention(q, k, v, heads, causal=False, scale=None):
     _check(_oracle().oracle_attention(_p(q), width, _p(k), _p(v), width, _p(y), width, batch, q_len,
                                       kv_len, heads, head_dim, scale, int(causal)), "attention")
     return y[0] if squeeze else y
+
+
+def attention_bwd(q, k, v, dout, heads, causal=False, scale=None):
+    """The per-head core of backward_self_attention / backward_cross_attention
+    (oracle_attention_bwd): (dq, dk, dv) from q [.., q_len, width], k / v
+    [.., kv_len, width] and dout (the gradient of the attended heads, shaped
+    like q)."""
+    squeeze = np.ndim(q) == 2
+    q, k, v, dout = (np.asarray(a, np.float32) for a in (q, k, v, dout))
+    if squeeze:
+        q, k, v, dout = q[None], k[None], v[None], dout[None]
+    batch, q_len, width = q.shape
+    kv_len = k.shape[1]
+    if k.shape != (batch, kv_len, width) or v.shape != k.shape or dout.shape != q.shape or width % heads:
+        raise OracleError("attention_bwd: shape mismatch")
+    head_dim = width // heads
+    if scale is None:
+        scale = attention_scale(head_dim)
+    q, k, v, dout = _f32(q), _f32(k), _f32(v), _f32(dout)
+    dq = np.empty_like(q)
+    dk = np.empty_like(k)
+    dv = np.empty_like(v)
+    _check(_oracle().oracle_attention_bwd(_p(q), width, _p(k), _p(v), width, _p(dout), width, _p(dq), width,
+                                          _p(dk), _p(dv), width, batch, q_len, kv_len, heads, head_dim, scale,
+                                          int(causal)), "attention_bwd")
+    if squeeze:
+        return dq[0], dk[0], dv[0]
+    return dq, dk, dv
 
 
 U32 = 2.0 ** -24  # float32 unit roundoff

@@ -7,10 +7,10 @@ reference's own compiled Model::forwardPassNamed (oracle/_ref):
 - a pre-norm residual block (LayerNorm -> SelfAttention -> Add -> LayerNorm
   -> GELU), held normwise to 1e-4 of its largest output (each layer's
   element-wise parity is tested on its own);
-- the reference's refusals, with its messages; the int-ids forward, which
-  runs SelfAttention and refuses CrossAttention as the reference does; and
-  a backward that reaches an attention layer, which is refused (its gradient
-  is not on this path)."""
+- the reference's refusals, with its messages; and the int-ids forward,
+  which runs SelfAttention and refuses CrossAttention as the reference does.
+The training step through these layers is tested in
+tests/test_gpu_attention_bwd.py."""
 import numpy as np
 import pytest
 
@@ -106,18 +106,5 @@ def test_attention_in_int_ids_path(ctx, store):
     try:
         with pytest.raises(M.MimirError, match="not supported in int path: CrossAttention"):
             store.forward_ids(g, ids, training=False)
-    finally:
-        g.close()
-
-
-def test_attention_backward_is_refused(ctx, store):
-    name, layers, fin, iin = block_graph(seq=8, e=32, heads=2)
-    fin = {"inp": fin["inp"][:8 * 32]}
-    g = M.DeviceGraph(ctx, layers)
-    try:
-        store.set_inputs(fin, iin)
-        store.run_training(g)  # the forward runs
-        with pytest.raises(M.MimirError, match="SelfAttention backward is not on this path"):
-            store.backward(g, np.ones(8 * 32, np.float32))
     finally:
         g.close()
