@@ -112,6 +112,14 @@ def attention_flops(batch, heads, q_len, kv_len, head_dim, causal):
     return 4 * head_dim * pairs * batch * heads
 
 
+def attention_bwd_flops(batch, heads, q_len, kv_len, head_dim, causal):
+    """Algorithmic flops of the attention core's backward: the five products
+    of backward_self_attention (S = QK^T, dP = dO V^T, dV = P^T dO,
+    dQ = dS K, dK = dS^T Q) over the visible (query, key) pairs, 2*head_dim
+    each (the masked pairs contribute nothing)."""
+    return attention_flops(batch, heads, q_len, kv_len, head_dim, causal) // 4 * 10
+
+
 def build_ops(rows_override=None):
     """Every op of the sweep.  rows_override (bench --rows) changes the row
     count of the configs[1] add + RMSNorm and configs[4] LayerNorm ops only,
@@ -169,6 +177,23 @@ def build_ops(rows_override=None):
                        "attention_fwd_mfma<128>", 4 * ab * al * aw * f4, ab * ah * al, "query rows",
                        make_attention, lambda s: {"out": s[0][1]},
                        flops=attention_flops(ab, ah, al, al, ad, True)))
+
+    def make_attention_bwd(ctx, nsets):
+        qkv = G.attention_qkv(ab, al, ah, ad)
+        sets = _replicate(ctx, [qkv, G.attention_dout(ab, al, ah, ad), np.empty_like(qkv)], nsets)
+        del qkv
+
+        def step(i):
+            x, do, g = sets[i]
+            ctx.attention_bwd(x, x.offset(aw), x.offset(2 * aw), do, g, g.offset(aw), g.offset(2 * aw), ab, al, al,
+                              ah, ad, True, ld_q=3 * aw, ld_kv=3 * aw, ld_dout=aw, ld_dq=3 * aw, ld_dkv=3 * aw)
+        return step, sets
+    ops.append(OpBench("f4_attention_bwd", 2,
+                       f"attention core backward fp32 [{ab} seq x {ah} heads x {al} tokens, head_dim {ad}, causal]: "
+                       f"QKV [{ab * al}x{3 * aw}] + dout [{ab * al}x{aw}] -> dQKV [{ab * al}x{3 * aw}]",
+                       "rocBLAS sgemm (5 per head group) + attn_probs_kernel<16> + attn_dsoftmax_kernel<16>",
+                       7 * ab * al * aw * f4, ab * ah * al, "query rows", make_attention_bwd,
+                       lambda s: {"dqkv": s[0][2]}, flops=attention_bwd_flops(ab, ah, al, al, ad, True)))
 
     def make_cfg3a(ctx, nsets):
         table, ids = G.cfg3_gather()
@@ -663,6 +688,19 @@ def cpu_leg(which, reps):
                         "rows_per_s": round(1024 / t, 1), "cores": 1, "kind": "port",
                         "sample": "1 of 256 (sequence, head) pairs: 1024 causal queries, head_dim 128, "
                                   f"oracle_attention (bit-exact to the reference core), median of {reps}"}
+        elif key == "f4_attention_bwd":
+            # One (sequence, head) through the restatement of the reference's
+            # backward core (Model.cpp:6892-7028, single-threaded as there).
+            qkv = G.attention_qkv(1, 1024, 32, 128)
+            q, k, v = (np.ascontiguousarray(qkv[:, i * 4096:i * 4096 + 128]) for i in range(3))
+            do = np.ascontiguousarray(G.attention_dout(1, 1024, 32, 128)[:, :128])
+            t = O.time_port(lambda: O.attention_bwd(q, k, v, do, 1, True), reps)
+            fl = attention_bwd_flops(1, 1, 1024, 1024, 128, True)
+            out[key] = {"value": round(fl / t / 1e9, 3), "unit": "GFLOP/s", "seconds": round(t, 6),
+                        "rows_per_s": round(1024 / t, 1), "cores": 1, "kind": "port",
+                        "sample": "1 of 256 (sequence, head) pairs: 1024 causal queries, head_dim 128, "
+                                  f"oracle_attention_bwd (bit-exact to the reference's backward core), median of "
+                                  f"{reps}"}
         elif key in ("cfg3_embedding_bwd", "cfg3_embedding_bwd_zipf"):
             ids = (G.cfg3_ids() if key == "cfg3_embedding_bwd" else G.cfg3_ids_zipf()).ravel()[:4096].copy()
             dy = G.cfg3_embedding_grad()[:4096].copy()
@@ -903,6 +941,37 @@ def parity_leg(ctx, by_key, which):
             out[key] = {"vs": "port (oracle_attention, bit-exact to the reference's self_attention_forward core)",
                         "sample": "3 of 256 (sequence, head) pairs in full, and every head's first query "
                                   "(one visible key: V's row exactly)",
+                        "pass": all(r["pass"] for r in res.values()), "outputs": res}
+            log(f"parity {key}: {'pass' if out[key]['pass'] else 'FAIL'} vs port "
+                + ", ".join(f"{n} max_abs {r['max_abs']:.3g}" for n, r in res.items()))
+        elif key == "f4_attention_bwd":
+            # Two (sequence, head) pairs of the full launch against the
+            # restatement (bit-exact to the reference's backward core), each
+            # element within twice the float64 model's first-order bound (both
+            # sides round); every head's first query: dq is exactly 0 (one
+            # visible key, so its dS row is 0).
+            sys.path.insert(0, os.path.join(REPO, "tests"))
+            from _attention import attention_bwd64
+            qkv = G.attention_qkv(8, 1024, 32, 128)
+            dout = G.attention_dout(8, 1024, 32, 128)
+            got = gpu_outputs(by_key[key], {"dqkv": np.empty((8192, 12288), np.float32)})["dqkv"]
+            res = {}
+            for bi, h in ((0, 0), (7, 31)):
+                rows = slice(bi * 1024, (bi + 1) * 1024)
+                q, k, v = (np.ascontiguousarray(qkv[rows, i * 4096 + h * 128:i * 4096 + (h + 1) * 128])
+                           for i in range(3))
+                do = np.ascontiguousarray(dout[rows, h * 128:(h + 1) * 128])
+                ref = O.attention_bwd(q, k, v, do, 1, True)
+                _, tol = attention_bwd64(q, k, v, do, 1, True, O.attention_scale(128))
+                for j, name in enumerate(("dq", "dk", "dv")):
+                    cols = slice(j * 4096 + h * 128, j * 4096 + (h + 1) * 128)
+                    res[f"{name} (seq {bi}, head {h})"] = _agreement(got[rows, cols], ref[j], False,
+                                                                     2 * tol[j] / 1e-5)
+            res["dq (first query of every sequence and head)"] = _agreement(
+                got.reshape(8, 1024, 12288)[:, 0, :4096], np.zeros((8, 4096), np.float32), True)
+            out[key] = {"vs": "port (oracle_attention_bwd, bit-exact to the reference's backward core)",
+                        "sample": "2 of 256 (sequence, head) pairs in full (dq, dk, dv), and every head's "
+                                  "first-query dq (exactly 0)",
                         "pass": all(r["pass"] for r in res.values()), "outputs": res}
             log(f"parity {key}: {'pass' if out[key]['pass'] else 'FAIL'} vs port "
                 + ", ".join(f"{n} max_abs {r['max_abs']:.3g}" for n, r in res.items()))

@@ -281,8 +281,10 @@ int mimir_cross_attention_fwd(mimir_ctx* ctx, const float* query_input, int64_t 
  * (dk and dv may be column blocks of one buffer, as the reference's dqkv).
  * Overwrites dq / dk / dv.  P and dS are materialised per group of heads
  * in the context's scratch (2 q_len kv_len floats per head, groups capped at
- * 1 GiB, one head at least); the products are fp32 library GEMMs, the row
- * passes (mask + softmax, softmax backward) hand-written kernels.
+ * 1 GiB, one head at least), beside K^T and V^T of one sequence (2 kv_len
+ * heads head_dim floats); the products are fp32 library GEMMs, the row
+ * passes (mask + softmax, softmax backward) and the transposes hand-written
+ * kernels.
  * kv_len == 0: dq = 0.  Outputs must not overlap the inputs. */
 int mimir_attention_bwd(mimir_ctx* ctx, const float* q, int64_t ld_q, const float* k, const float* v,
                         int64_t ld_kv, const float* dout, int64_t ld_dout, float* dq, int64_t ld_dq, float* dk,

@@ -133,6 +133,30 @@ __global__ __launch_bounds__(kBlock) void zero_rows_kernel(float* __restrict__ y
         y[(t / cols) * ld + t % cols] = 0.0f;
 }
 
+// dst[c][r] = src[r][c] for a [rows x cols] block of rows ld_src apart; dst
+// is [cols x rows] dense.  32 x 32 tiles through LDS (one padding column so
+// the transposed reads hit distinct banks).
+constexpr int kTile = 32;
+__global__ __launch_bounds__(kTile * 8) void transpose_kernel(const float* __restrict__ src, int64_t ld_src,
+                                                              int64_t rows, int64_t cols, float* __restrict__ dst) {
+    __shared__ float t[kTile][kTile + 1];
+    const int64_t c0 = static_cast<int64_t>(blockIdx.x) * kTile, r0 = static_cast<int64_t>(blockIdx.y) * kTile;
+    const int tx = threadIdx.x % kTile, ty = threadIdx.x / kTile;
+    for (int i = ty; i < kTile; i += 8)
+        if (r0 + i < rows && c0 + tx < cols) t[i][tx] = src[(r0 + i) * ld_src + c0 + tx];
+    __syncthreads();
+    for (int i = ty; i < kTile; i += 8)
+        if (c0 + i < cols && r0 + tx < rows) dst[(c0 + i) * rows + r0 + tx] = t[tx][i];
+}
+
+int transpose(mimir_ctx* ctx, const float* src, int64_t ld_src, int64_t rows, int64_t cols, float* dst) {
+    const int64_t gx = (cols + kTile - 1) / kTile, gy = (rows + kTile - 1) / kTile;
+    if (gx > INT32_MAX || gy > 65535) return fail(ctx, MIMIR_EINVAL, "attention backward: transpose grid too large");
+    transpose_kernel<<<dim3(static_cast<unsigned>(gx), static_cast<unsigned>(gy)), kTile * 8, 0, ctx->stream>>>(
+        src, ld_src, rows, cols, dst);
+    return launched(ctx, "transpose_kernel");
+}
+
 int zero_rows(mimir_ctx* ctx, float* y, int64_t rows, int64_t cols, int64_t ld) {
     if (rows == 0 || cols == 0) return MIMIR_OK;
     unsigned blocks = 0;
@@ -203,7 +227,7 @@ int64_t heads_per_group(const mimir_ctx* ctx, const CoreBwd& a) {
     return std::max<int64_t>(1, hc);
 }
 int64_t work_floats(const mimir_ctx* ctx, const CoreBwd& a) {
-    return 2 * heads_per_group(ctx, a) * a.q_len * a.kv_len;
+    return 2 * heads_per_group(ctx, a) * a.q_len * a.kv_len + 2 * a.heads * a.head_dim * a.kv_len;
 }
 
 int core_bwd(mimir_ctx* ctx, const CoreBwd& a, float* work) {
@@ -218,8 +242,15 @@ int core_bwd(mimir_ctx* ctx, const CoreBwd& a, float* work) {
         return MIMIR_OK;
     }
     const int64_t hc = heads_per_group(ctx, a);
+    const int64_t width = a.heads * D;
     float* P = work;
     float* G = work + hc * TT;
+    // K^T and V^T of one sequence, [width x kv_len]: with the head dimension
+    // as rows, the score products S = Q K^T and dP = dO V^T are plain (NN)
+    // products, which the library runs about twice as fast as the
+    // transposed-operand form on these shapes.
+    float* KT = G + hc * TT;
+    float* VT = KT + width * Tk;
     for (int64_t b = 0; b < a.batch; ++b) {
         const float* qb = a.q + b * Tq * a.ld_q;
         const float* kb = a.k + b * Tk * a.ld_kv;
@@ -229,13 +260,15 @@ int core_bwd(mimir_ctx* ctx, const CoreBwd& a, float* work) {
         float* dkb = a.dk + b * Tk * a.ld_dkv;
         float* dvb = a.dv + b * Tk * a.ld_dkv;
         float* attb = a.att ? a.att + b * Tq * a.ld_att : nullptr;
+        if (int st = transpose(ctx, kb, a.ld_kv, Tk, width, KT)) return st;
+        if (int st = transpose(ctx, vb, a.ld_kv, Tk, width, VT)) return st;
         for (int64_t h0 = 0; h0 < a.heads; h0 += hc) {
             const int64_t n = std::min(hc, a.heads - h0), off = h0 * D;
             const int64_t rows = n * Tq;
             const auto q32 = static_cast<int32_t>(Tq), k32 = static_cast<int32_t>(Tk);
             // S = scale Q K^T, then P = softmax(mask(S)) in place (:6892-6920)
-            if (int st = gemm_f32_ex(ctx, false, true, Tq, Tk, D, a.scale, qb + off, a.ld_q, D, kb + off, a.ld_kv, D,
-                                     0.0f, P, Tk, TT, n))
+            if (int st = gemm_f32_ex(ctx, false, false, Tq, Tk, D, a.scale, qb + off, a.ld_q, D, KT + off * Tk, Tk,
+                                     D * Tk, 0.0f, P, Tk, TT, n))
                 return st;
             if (int st = probs(ctx, P, rows, q32, k32, a.causal)) return st;
             if (attb)  // attended = P V (:6922-6930)
@@ -243,8 +276,8 @@ int core_bwd(mimir_ctx* ctx, const CoreBwd& a, float* work) {
                                          attb + off, a.ld_att, D, n))
                     return st;
             // dP = dO V^T (:6979-6989), then dS in place (:6991-7005)
-            if (int st = gemm_f32_ex(ctx, false, true, Tq, Tk, D, 1.0f, ob + off, a.ld_dout, D, vb + off, a.ld_kv, D,
-                                     0.0f, G, Tk, TT, n))
+            if (int st = gemm_f32_ex(ctx, false, false, Tq, Tk, D, 1.0f, ob + off, a.ld_dout, D, VT + off * Tk, Tk,
+                                     D * Tk, 0.0f, G, Tk, TT, n))
                 return st;
             if (int st = dsoftmax(ctx, P, G, rows, q32, k32, a.causal)) return st;
             // dV = P^T dO (:6967-6977)

@@ -440,7 +440,8 @@ std::vector<float> embedding_forward_float_ids(const std::vector<float>& x, cons
 // forward applies the layers' residual merges (Layer::branch_type RESIDUAL
 // with branch_sources, Model.cpp:6676-6685) as the reference does.  Layer
 // types: LayerNorm, RMSNorm, Softmax, LogSoftmax, GELU, SiLU, Add, Multiply,
-// Embedding, Identity, Dropout (others throw at construction).
+// Embedding, Identity, Dropout, SelfAttention, MultiHeadAttention,
+// CrossAttention (others throw at construction).
 // ---------------------------------------------------------------------------
 template <class LayerT>
 class DeviceModel {
@@ -536,9 +537,9 @@ public:
     // Model::backwardPass(loss_gradient) (Model.cpp:7307-9153) after a
     // training forward.  Parameter gradients are added into the layers'
     // grad_weights as the reference does (a vector of the wrong size is first
-    // reset to zeros, :7449-7451, :7751-7753), for the LayerNorm and Embedding
-    // layers whose branches produce them; the gradient that reached
-    // "__input__" is kept for getLastInputGradient().
+    // reset to zeros, :7448-7450, :7751-7753, :8057-8059, :8110-8112), for the
+    // LayerNorm, Embedding and attention layers whose branches produce them;
+    // the gradient that reached "__input__" is kept for getLastInputGradient().
     void backwardPass(const std::vector<float>& loss_gradient, std::vector<LayerT>& layers) {
         if (&layers != layers_ && layers.size() != layers_->size())
             throw std::runtime_error("DeviceModel::backwardPass: not the model's layer list");
@@ -546,7 +547,7 @@ public:
         for (size_t i = 0; i < layers.size(); ++i) {
             LayerT& L = layers[i];
             const size_t wn = weights_[i].size();
-            if (wn && (types_[i] == MIMIR_LAYER_LAYERNORM || types_[i] == MIMIR_LAYER_EMBEDDING)) {
+            if (wn && has_param_grads(types_[i])) {
                 if (L.grad_weights.size() != wn) L.grad_weights.assign(wn, 0.0f);
                 grads_.emplace_back(*ctx_, L.grad_weights);
             } else {
@@ -576,6 +577,11 @@ public:
     mimir_store* store() const { return store_; }
 
 private:
+    static bool has_param_grads(int t) {
+        return t == MIMIR_LAYER_LAYERNORM || t == MIMIR_LAYER_EMBEDDING || t == MIMIR_LAYER_SELF_ATTENTION ||
+               t == MIMIR_LAYER_MULTIHEAD_ATTENTION || t == MIMIR_LAYER_CROSS_ATTENTION;
+    }
+
     static int type_of(const std::string& t) {
         static const std::unordered_map<std::string, int> m = {
             {"LayerNorm", MIMIR_LAYER_LAYERNORM}, {"RMSNorm", MIMIR_LAYER_RMSNORM},

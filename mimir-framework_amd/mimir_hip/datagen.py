@@ -105,6 +105,12 @@ def attention_qkv(batch=8, seq=1024, heads=32, head_dim=128):
     return normal(2, 6, (batch * seq, 3 * heads * head_dim))
 
 
+def attention_dout(batch=8, seq=1024, heads=32, head_dim=128):
+    """The gradient of the attended heads for the attention backward
+    benchmark: [batch*seq, E] N(0,1)."""
+    return normal(2, 7, (batch * seq, heads * head_dim))
+
+
 def cfg4_grad(shape, tensor=8):
     return normal(4, tensor, shape)
 

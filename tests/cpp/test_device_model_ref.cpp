@@ -251,8 +251,10 @@ void attention_at_call_site() {
 }
 
 // DeviceModel<Layer> on a pre-norm attention block of reference Layers
-// (LayerNorm -> SelfAttention -> Add), beside Model::forwardPassNamed.
-// Normwise at 1e-4: each layer's element-wise parity is tested on its own.
+// (LayerNorm -> SelfAttention -> Add), beside Model::forwardPassNamed, then a
+// training step beside Model::backwardPass (the input gradient gathers the
+// LayerNorm's and the Add's contributions).  Normwise at 1e-4: each layer's
+// element-wise parity is tested on its own.
 void attention_block_model(mimir_hip::Context& c) {
     const int seq = 24, e = 32, heads = 4;
     Model m;
@@ -260,7 +262,7 @@ void attention_block_model(mimir_hip::Context& c) {
     m.push("attn", "SelfAttention", 4 * e * e);
     m.push("res", "Add", 0);
     auto& layers = m.getMutableLayers();
-    layers[0].inputs = {"inp"};
+    layers[0].inputs = {"__input__"};
     layers[0].output = "h";
     layers[0].in_features = e;
     layers[1].inputs = {"h"};
@@ -269,7 +271,7 @@ void attention_block_model(mimir_hip::Context& c) {
     layers[1].embed_dim = e;
     layers[1].num_heads = heads;
     layers[1].causal = true;
-    layers[2].inputs = {"a", "inp"};
+    layers[2].inputs = {"a", "__input__"};
     layers[2].output = "x";
     m.allocateParams();
     float* g = layers[0].getWeights();
@@ -282,15 +284,32 @@ void attention_block_model(mimir_hip::Context& c) {
     for (int i = 0; i < 4 * e * e; ++i) w[i] = std::sin(0.013f * static_cast<float>(i) + 0.4f) * 0.18f;
     std::vector<float> x(seq * e);
     for (size_t i = 0; i < x.size(); ++i) x[i] = std::cos(0.21f * static_cast<float>(i)) * 1.1f;
-    const FMap fin{{"inp", x}};
+    const FMap fin{{"__input__", x}};
+    auto normwise = [](const std::vector<float>& got, const std::vector<float>& ref) {
+        float mx = 0.f;
+        for (float v : ref) mx = std::fmax(mx, std::fabs(v));
+        bool ok = got.size() == ref.size() && !ref.empty();
+        for (size_t i = 0; ok && i < ref.size(); ++i) ok = std::fabs(got[i] - ref[i]) <= 1e-6f + 1e-4f * mx;
+        return ok;
+    };
     const std::vector<float> ref = m.forwardPassNamed(fin, IMap{}, false);
     mimir_hip::DeviceModel<Layer> dm(c, m.getLayers());
-    const std::vector<float> got = dm.forwardPassNamed(fin, IMap{}, false);
-    float mx = 0.f;
-    for (float v : ref) mx = std::fmax(mx, std::fabs(v));
-    bool ok = got.size() == ref.size() && !ref.empty();
-    for (size_t i = 0; ok && i < ref.size(); ++i) ok = std::fabs(got[i] - ref[i]) <= 1e-6f + 1e-4f * mx;
-    CHECK(ok);
+    CHECK(normwise(dm.forwardPassNamed(fin, IMap{}, false), ref));
+
+    std::vector<float> loss(seq * e);
+    for (size_t i = 0; i < loss.size(); ++i) loss[i] = std::sin(0.37f * static_cast<float>(i)) + 0.2f;
+    m.forwardPassNamed(fin, IMap{}, true);
+    m.backwardPass(loss);
+    CHECK(m.hasLastInputGradient());
+    std::vector<Layer> dev_layers = m.getLayers();  // grad_weights start from zeros, as the reference's did
+    for (auto& L : dev_layers) std::fill(L.grad_weights.begin(), L.grad_weights.end(), 0.0f);
+    mimir_hip::DeviceModel<Layer> dt(c, dev_layers);
+    dt.forwardPassNamed(fin, IMap{}, true);
+    dt.backwardPass(loss, dev_layers);
+    CHECK(dt.hasLastInputGradient());
+    CHECK(normwise(dt.getLastInputGradient(), m.getLastInputGradient()));
+    CHECK(normwise(dev_layers[0].grad_weights, m.getLayers()[0].grad_weights));  // LayerNorm dgamma | dbeta
+    CHECK(normwise(dev_layers[1].grad_weights, m.getLayers()[1].grad_weights));  // dWqkv | dWout
 }
 
 }  // namespace

@@ -102,12 +102,16 @@ def check_core(got, q, k, v, dout, heads, causal, what, oracle=True):
 
 # (batch, q_len, kv_len, heads, head_dim, causal, amp): the softmax kernels'
 # register forms (kv_len <= 256, <= 1024, <= 4096) and the streamed form
-# (> 4096), self and cross shapes, causal rows past the last key.
+# (> 4096), self and cross shapes, causal rows past the last key, head_dim
+# above 128.
 CORE = [(1, 64, 64, 2, 32, True, 1.0), (1, 64, 64, 2, 32, False, 1.0), (3, 33, 33, 3, 20, True, 1.0),
         (1, 37, 90, 4, 16, False, 1.0), (1, 90, 37, 1, 64, True, 2.0), (1, 128, 128, 1, 128, True, 3.0),
         (1, 300, 300, 2, 48, True, 1.0), (1, 17, 1500, 2, 40, False, 1.0), (1, 5, 5000, 1, 32, True, 1.0),
         (1, 5, 5000, 1, 32, False, 1.0), (1, 1, 1, 1, 8, True, 1.0), (1, 1, 7, 3, 8, False, 1.0),
-        (2, 257, 257, 1, 200, True, 1.0)]
+        (2, 257, 257, 1, 200, True, 1.0),
+        # longer causal rows and cross shapes with keys past every query
+        (1, 600, 600, 2, 32, True, 1.0), (1, 1000, 1000, 1, 64, True, 1.0), (1, 700, 300, 1, 32, True, 1.0),
+        (1, 300, 700, 1, 32, True, 1.0), (2, 520, 520, 2, 16, True, 2.0)]
 
 
 @pytest.mark.parametrize("case", CORE, ids=lambda c: "x".join(map(str, c[:6])))
