@@ -157,3 +157,55 @@ def test_layernorm_bwd_rows_past_2_31(ctx):
     finally:
         for d in (x, dy, dx, dg_, dgam, dbet):
             d.free()
+
+
+def test_attention_past_2_31(ctx):
+    """The attention core, forward and backward, on a fused QKV buffer of
+    more than 2^31 floats (172 sequences x 1024 tokens x 32 heads of 128,
+    causal): the last sequence lies wholly past element 2^31 of the QKV and
+    dQKV buffers and is held to float64 (two heads forward, one backward);
+    the first, constant sequence to its closed form (every probability
+    row averages one value of V)."""
+    from _attention import assert_attention_close, assert_bwd_close, attention64, attention_bwd64
+    b, seq, heads, hd = 172, 1024, 32, 128
+    w = heads * hd
+    rows = b * seq
+    assert (rows - seq) * 3 * w > 1 << 31
+    r = np.random.default_rng(41)
+    last = (0.5 * r.standard_normal((seq, 3 * w))).astype(np.float32)
+    last_dout = r.standard_normal((seq, w)).astype(np.float32)
+    qkv, out = ctx.empty((rows, 3 * w)), ctx.empty((rows, w))
+    dout, g = ctx.empty((rows, w)), ctx.empty((rows, 3 * w))
+    try:
+        ctx.fill(qkv, 0.25)
+        ctx.upload(qkv.offset((rows - seq) * 3 * w, (seq, 3 * w)), last)
+        print("attention forward past 2^31", flush=True)
+        ctx.attention(qkv, qkv.offset(w), qkv.offset(2 * w), out, b, seq, seq, heads, hd, True, ld_q=3 * w,
+                      ld_kv=3 * w)
+        assert_close(_slice(ctx, out, 0, seq * w), np.full(seq * w, 0.25, np.float32), "constant first sequence")
+        got = _slice(ctx, out, (rows - seq) * w, seq * w).reshape(seq, w)
+        parts = [np.ascontiguousarray(last[:, i * w:(i + 1) * w]) for i in range(3)]
+        for h in (0, heads - 1):
+            sl = slice(h * hd, (h + 1) * hd)
+            q, k, v = (np.ascontiguousarray(p[:, sl]) for p in parts)
+            want, mag, cond = attention64(q, k, v, 1, True, O.attention_scale(hd))
+            assert_attention_close(got[:, sl], want, mag, cond, f"last sequence head {h}")
+        ctx.fill(dout, 0.5)
+        ctx.upload(dout.offset((rows - seq) * w, (seq, w)), last_dout)
+        print("attention backward past 2^31", flush=True)
+        ctx.attention_bwd(qkv, qkv.offset(w), qkv.offset(2 * w), dout, g, g.offset(w), g.offset(2 * w), b, seq, seq,
+                          heads, hd, True, ld_q=3 * w, ld_kv=3 * w, ld_dout=w, ld_dq=3 * w, ld_dkv=3 * w)
+        tail = _slice(ctx, g, (rows - seq) * 3 * w, seq * 3 * w).reshape(seq, 3 * w)
+        q, k, v = (np.ascontiguousarray(p[:, :hd]) for p in parts)
+        want, tol = attention_bwd64(q, k, v, last_dout[:, :hd], 1, True, O.attention_scale(hd))
+        for j, name in enumerate(("dq", "dk", "dv")):
+            assert_bwd_close(tail[:, j * w:j * w + hd], want[j], tol[j], f"last sequence head 0 {name}")
+        # The constant first sequence: dv_j = 0.5 * sum_{i >= j} 1 / (i + 1)
+        # (P is 1/(i+1) on the visible keys), dq and dk vanish up to rounding.
+        head = _slice(ctx, g, 0, seq * 3 * w).reshape(seq, 3 * w)
+        dv_want = 0.5 * np.cumsum((1.0 / np.arange(1, seq + 1))[::-1])[::-1]
+        assert_close(head[:, 2 * w], dv_want.astype(np.float32), "constant first sequence dv", rel=1e-4)
+        assert np.abs(head[:, :2 * w]).max() < 1e-5, "constant first sequence dq / dk"
+    finally:
+        for d in (qkv, out, dout, g):
+            d.free()
