@@ -251,6 +251,13 @@ int core_bwd(mimir_ctx* ctx, const CoreBwd& a, float* work) {
     // transposed-operand form on these shapes.
     float* KT = G + hc * TT;
     float* VT = KT + width * Tk;
+    // Causal: the products may run over nblk blocks of bs queries (or keys),
+    // so the key columns past a query block's diagonal -- masked, P = dS = 0
+    // there -- are not multiplied ((nblk + 1) / (2 nblk) of the full work).
+    const int64_t want_blk = ctx->tune.attn_bwd_blocks > 0 ? ctx->tune.attn_bwd_blocks : 1;
+    const int64_t nblk = a.causal ? std::max<int64_t>(1, std::min<int64_t>(want_blk, Tq / 256)) : 1;
+    const int64_t bs = nblk > 1 ? ((Tq + nblk - 1) / nblk + 63) / 64 * 64 : std::max(Tq, Tk);
+    auto live = [&](int64_t q1) { return a.causal ? std::min(q1, Tk) : Tk; };  // keys queries < q1 see
     for (int64_t b = 0; b < a.batch; ++b) {
         const float* qb = a.q + b * Tq * a.ld_q;
         const float* kb = a.k + b * Tk * a.ld_kv;
@@ -266,31 +273,58 @@ int core_bwd(mimir_ctx* ctx, const CoreBwd& a, float* work) {
             const int64_t n = std::min(hc, a.heads - h0), off = h0 * D;
             const int64_t rows = n * Tq;
             const auto q32 = static_cast<int32_t>(Tq), k32 = static_cast<int32_t>(Tk);
-            // S = scale Q K^T, then P = softmax(mask(S)) in place (:6892-6920)
-            if (int st = gemm_f32_ex(ctx, false, false, Tq, Tk, D, a.scale, qb + off, a.ld_q, D, KT + off * Tk, Tk,
-                                     D * Tk, 0.0f, P, Tk, TT, n))
-                return st;
-            if (int st = probs(ctx, P, rows, q32, k32, a.causal)) return st;
-            if (attb)  // attended = P V (:6922-6930)
-                if (int st = gemm_f32_ex(ctx, false, false, Tq, D, Tk, 1.0f, P, Tk, TT, vb + off, a.ld_kv, D, 0.0f,
-                                         attb + off, a.ld_att, D, n))
+            // Row-blocked products (S, attended, dP, dQ): query block [q0, q1)
+            // reads keys [0, live(q1)).
+            for (int64_t q0 = 0; q0 < Tq; q0 += bs) {
+                const int64_t m = std::min(bs, Tq - q0), kl = live(q0 + m);
+                // S = scale Q K^T (:6892-6905)
+                if (int st = gemm_f32_ex(ctx, false, false, m, kl, D, a.scale, qb + q0 * a.ld_q + off, a.ld_q, D,
+                                         KT + off * Tk, Tk, D * Tk, 0.0f, P + q0 * Tk, Tk, TT, n))
                     return st;
-            // dP = dO V^T (:6979-6989), then dS in place (:6991-7005)
-            if (int st = gemm_f32_ex(ctx, false, false, Tq, Tk, D, 1.0f, ob + off, a.ld_dout, D, VT + off * Tk, Tk,
-                                     D * Tk, 0.0f, G, Tk, TT, n))
-                return st;
+            }
+            // P = softmax(mask(S)) in place (:6906-6920); every key column is
+            // written (0 where masked), so the key-blocked products below may
+            // read whole columns of a block.
+            if (int st = probs(ctx, P, rows, q32, k32, a.causal)) return st;
+            for (int64_t q0 = 0; q0 < Tq; q0 += bs) {
+                const int64_t m = std::min(bs, Tq - q0), kl = live(q0 + m);
+                if (attb)  // attended = P V (:6922-6930)
+                    if (int st = gemm_f32_ex(ctx, false, false, m, D, kl, 1.0f, P + q0 * Tk, Tk, TT, vb + off, a.ld_kv,
+                                             D, 0.0f, attb + q0 * a.ld_att + off, a.ld_att, D, n))
+                        return st;
+                // dP = dO V^T (:6979-6989)
+                if (int st = gemm_f32_ex(ctx, false, false, m, kl, D, 1.0f, ob + q0 * a.ld_dout + off, a.ld_dout, D,
+                                         VT + off * Tk, Tk, D * Tk, 0.0f, G + q0 * Tk, Tk, TT, n))
+                    return st;
+            }
+            // dS in place (:6991-7005), every key column written as for P
             if (int st = dsoftmax(ctx, P, G, rows, q32, k32, a.causal)) return st;
-            // dV = P^T dO (:6967-6977)
-            if (int st = gemm_f32_ex(ctx, true, false, Tk, D, Tq, 1.0f, P, Tk, TT, ob + off, a.ld_dout, D, 0.0f,
-                                     dvb + off, a.ld_dkv, D, n))
-                return st;
-            // dQ = scale dS K (:7007-7016), dK = scale dS^T Q (:7018-7028)
-            if (int st = gemm_f32_ex(ctx, false, false, Tq, D, Tk, a.scale, G, Tk, TT, kb + off, a.ld_kv, D, 0.0f,
-                                     dqb + off, a.ld_dq, D, n))
-                return st;
-            if (int st = gemm_f32_ex(ctx, true, false, Tk, D, Tq, a.scale, G, Tk, TT, qb + off, a.ld_q, D, 0.0f,
-                                     dkb + off, a.ld_dkv, D, n))
-                return st;
+            for (int64_t q0 = 0; q0 < Tq; q0 += bs) {  // dQ = scale dS K (:7007-7016)
+                const int64_t m = std::min(bs, Tq - q0), kl = live(q0 + m);
+                if (int st = gemm_f32_ex(ctx, false, false, m, D, kl, a.scale, G + q0 * Tk, Tk, TT, kb + off, a.ld_kv,
+                                         D, 0.0f, dqb + q0 * a.ld_dq + off, a.ld_dq, D, n))
+                    return st;
+            }
+            // Key-blocked products (dV, dK): key block [k0, k1) is seen by
+            // queries [first(k0), Tq); a block no query sees gets zeros.
+            for (int64_t k0 = 0; k0 < Tk; k0 += bs) {
+                const int64_t m = std::min(bs, Tk - k0), qs = a.causal ? k0 : 0;
+                if (qs >= Tq) {
+                    if (int st = zero_rows(ctx, dvb + k0 * a.ld_dkv + off, m, n * D, a.ld_dkv)) return st;
+                    if (int st = zero_rows(ctx, dkb + k0 * a.ld_dkv + off, m, n * D, a.ld_dkv)) return st;
+                    continue;
+                }
+                // dV = P^T dO (:6967-6977)
+                if (int st = gemm_f32_ex(ctx, true, false, m, D, Tq - qs, 1.0f, P + qs * Tk + k0, Tk, TT,
+                                         ob + qs * a.ld_dout + off, a.ld_dout, D, 0.0f, dvb + k0 * a.ld_dkv + off,
+                                         a.ld_dkv, D, n))
+                    return st;
+                // dK = scale dS^T Q (:7018-7028)
+                if (int st = gemm_f32_ex(ctx, true, false, m, D, Tq - qs, a.scale, G + qs * Tk + k0, Tk, TT,
+                                         qb + qs * a.ld_q + off, a.ld_q, D, 0.0f, dkb + k0 * a.ld_dkv + off, a.ld_dkv,
+                                         D, n))
+                    return st;
+            }
         }
     }
     return MIMIR_OK;

@@ -46,7 +46,7 @@ struct RowShape {
 
 // Tuning override, read once per context from MIMIR_TUNE, e.g.
 //   MIMIR_TUNE="norm=1024x1x1024,layernorm=512x2x512,softmax=64x4x64,ew=1,gather=1024,rope=1,
-//               lnbwd=512x2x512,lnbwd_grid=512,chain=0,attnbwd_heads=4"
+//               lnbwd=512x2x512,lnbwd_grid=512,chain=0,attnbwd_heads=4,attnbwd_blocks=2"
 // Each entry selects among the compiled variants above; an entry that does
 // not fit a call (row too wide for it) is ignored for that call.  Unset, the
 // measured defaults apply.  Used for sweeps; results are identical.
@@ -61,6 +61,7 @@ struct Tuning {
     int lnbwd_grid = 0;       // its persistent grid (workgroups)
     int chain_streamed = 0;   // chain=0: the runtime streams every layer's output (no kept outputs)
     int attn_bwd_heads = 0;   // heads per group of the attention backward (0: what 1 GiB of P / dS holds)
+    int attn_bwd_blocks = 0;  // causal attention backward: query / key blocks of the products (0: default)
 };
 
 inline bool parse_shape(const char* v, RowShape* s) {
@@ -98,6 +99,7 @@ inline Tuning read_tuning() {
         else if (!std::strcmp(k, "lnbwd_grid")) t.lnbwd_grid = std::atoi(v);
         else if (!std::strcmp(k, "chain")) t.chain_streamed = std::atoi(v) == 0;
         else if (!std::strcmp(k, "attnbwd_heads")) t.attn_bwd_heads = std::atoi(v);
+        else if (!std::strcmp(k, "attnbwd_blocks")) t.attn_bwd_blocks = std::atoi(v);
     }
     return t;
 }

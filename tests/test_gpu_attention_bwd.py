@@ -130,22 +130,40 @@ def test_core_backward_fused_layout(ctx, causal):
     check_core(gpu_core_bwd(ctx, q, k, v, dout, 4, causal, fused=True), q, k, v, dout, 4, causal, "fused")
 
 
-@pytest.mark.parametrize("group", [1, 2])
-def test_core_backward_head_groups(group):
-    """Heads processed in groups (the scratch cap; forced small here through
-    the tuning override) give the same gradients as one group."""
+def _tuned_context(tune):
     old = os.environ.get("MIMIR_TUNE")
-    os.environ["MIMIR_TUNE"] = f"attnbwd_heads={group}"
+    os.environ["MIMIR_TUNE"] = tune
     try:
-        c = M.Context(0)
+        return M.Context(0)
     finally:
         if old is None:
             del os.environ["MIMIR_TUNE"]
         else:
             os.environ["MIMIR_TUNE"] = old
+
+
+@pytest.mark.parametrize("group", [1, 2])
+def test_core_backward_head_groups(group):
+    """Heads processed in groups (the scratch cap; forced small here through
+    the tuning override) give the same gradients as one group."""
+    c = _tuned_context(f"attnbwd_heads={group}")
     try:
         q, k, v, dout = rand_core(12, 2, 50, 60, 5 * 16, 1.0)
         check_core(gpu_core_bwd(c, q, k, v, dout, 5, True), q, k, v, dout, 5, True, f"groups of {group}")
+    finally:
+        c.close()
+
+
+@pytest.mark.parametrize("blocks", [2, 3, 4])
+@pytest.mark.parametrize("lq,lk", [(1000, 1000), (700, 300), (520, 900)])
+def test_core_backward_causal_blocks(blocks, lq, lk):
+    """The causal products over query / key blocks (a tuning override; one
+    block is the default): ragged last blocks, cross shapes, and key blocks
+    that no query sees (zeroed)."""
+    c = _tuned_context(f"attnbwd_blocks={blocks}")
+    try:
+        q, k, v, dout = rand_core(lq + lk + blocks, 1, lq, lk, 2 * 32, 1.0)
+        check_core(gpu_core_bwd(c, q, k, v, dout, 2, True), q, k, v, dout, 2, True, f"{blocks} blocks")
     finally:
         c.close()
 
