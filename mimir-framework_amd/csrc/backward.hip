@@ -1263,10 +1263,9 @@ __global__ __launch_bounds__(kWave * kLongSlices) void embed_bwd_seg_combine(
 // kernel is kept small in registers: two 1024-thread workgroups fit a CU.
 constexpr int kRunBatch = 4;
 template <int TPT, int CPT>
-__global__ __launch_bounds__(TPT) void embed_bwd_rows_vec(const uint32_t* keys, const uint32_t* toks, int64_t n,
-                                                          uint32_t vocab, const float* dy, float* grad, int64_t dim4,
-                                                          int long_runs) {
-    const int64_t i = blockIdx.x;
+__device__ __forceinline__ void embed_rows_position(int64_t i, const uint32_t* keys, const uint32_t* toks, int64_t n,
+                                                    uint32_t vocab, const float* dy, float* grad, int64_t dim4,
+                                                    int long_runs) {
     const uint32_t id = keys[i];
     const uint32_t t0 = toks[i];
     if (id >= vocab || (i > 0 && keys[i - 1] == id)) return;  // not a run's head
@@ -1320,6 +1319,62 @@ __global__ __launch_bounds__(TPT) void embed_bwd_rows_vec(const uint32_t* keys, 
         }
         c0 += static_cast<int64_t>(TPT) * CPT;
         if (c0 < dim4) load_group(c0);
+    }
+}
+
+template <int TPT, int CPT>
+__global__ __launch_bounds__(TPT) void embed_bwd_rows_vec(const uint32_t* keys, const uint32_t* toks, int64_t n,
+                                                          uint32_t vocab, const float* dy, float* grad, int64_t dim4,
+                                                          int long_runs) {
+    embed_rows_position<TPT, CPT>(blockIdx.x, keys, toks, n, vocab, dy, grad, dim4, long_runs);
+}
+
+// The rows kernel and the long runs' first level in one launch, so the two
+// independent streams overlap: blocks [0, nslots) are the segments of
+// embed_bwd_seg_partial (dispatched first, so the long segments start before
+// the short rows), blocks [nslots, nslots + n) embed_bwd_rows_vec's sorted
+// positions,
+// each 1024-thread block summing its segment's rows over whole 16-byte
+// columns with kMergedSegRows tokens' loads in flight.  The segment path is
+// kept small enough that the kernel stays at 64 registers, so two
+// 1024-thread workgroups still fit a CU (the rows path's turnover needs
+// them); its sums are embed_bwd_seg_partial's, in the same token order, bit
+// for bit.
+constexpr int kMergedSegRows = 8;
+__global__ __launch_bounds__(1024, 8) void embed_bwd_rows_seg(const uint32_t* keys, const uint32_t* toks, int64_t n,
+                                                               uint32_t vocab, const float* dy, float* grad,
+                                                               float* part, int64_t dim4) {
+    const int64_t nslots = (n + kLongRun - 1) / kLongRun;
+    if (blockIdx.x >= nslots) {
+        embed_rows_position<1024, 1>(blockIdx.x - nslots, keys, toks, n, vocab, dy, grad, dim4, 1);
+        return;
+    }
+    const int64_t m = blockIdx.x;
+    const int64_t p = m * kLongRun;
+    if (p >= n) return;
+    const LongRun r = long_run_at(keys, p, n, vocab);
+    if (!r.is_long) return;
+    const int64_t s0 = r.first ? r.head : p;
+    const int64_t s1 = p + kLongRun < r.end ? p + kLongRun : r.end;
+    const f4* src = reinterpret_cast<const f4*>(dy);
+    for (int64_t c = threadIdx.x; c < dim4; c += 1024) {
+        f4 acc;
+        bool started = false;
+        for (int64_t j = s0; j < s1; j += kMergedSegRows) {
+            f4 v[kMergedSegRows];
+#pragma unroll
+            for (int u = 0; u < kMergedSegRows; ++u)
+                if (j + u < s1) v[u] = __builtin_nontemporal_load(src + static_cast<int64_t>(toks[j + u]) * dim4 + c);
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int u = 0; u < kMergedSegRows; ++u) {
+                if (j + u < s1) {
+                    acc = started ? acc + v[u] : v[u];
+                    started = true;
+                }
+            }
+        }
+        reinterpret_cast<f4*>(part)[m * dim4 + c] = acc;
     }
 }
 
@@ -1394,22 +1449,31 @@ int embed_bwd(mimir_ctx* ctx, const void* ids, int64_t n_ids, const float* dy, f
         const uint32_t v = static_cast<uint32_t>(vocab);
         const int64_t dim4 = dim / 4;
         const int lr = long_runs ? 1 : 0;
-        if (long_runs) {
-            const dim3 pgrid(static_cast<unsigned>(nslots), static_cast<unsigned>((dim4 + kSegCols - 1) / kSegCols));
-            embed_bwd_seg_partial<<<pgrid, kSegCols, 0, ctx->stream>>>(skeys, stoks, n_ids, v, dy, part, dim4);
-            if (int st = launched(ctx, "embed_bwd_seg_partial")) return st;
-        }
         // Measured on MI355X at dim 4096 (MIMIR_TUNE gather=256/512/1024 picks a
         // variant): one 16-byte column per thread in 1024-thread workgroups
         // is fastest, 2-4 columns per thread in smaller ones ~2-4% slower.
         const int tpt = ctx->tune.gather_tpt ? ctx->tune.gather_tpt : (dim4 >= 1024 ? 1024 : dim4 >= 512 ? 512 : 256);
-        if (tpt == 256)
-            embed_bwd_rows_vec<256, 4><<<n, 256, 0, ctx->stream>>>(skeys, stoks, n_ids, v, dy, grad, dim4, lr);
-        else if (tpt == 512)
-            embed_bwd_rows_vec<512, 2><<<n, 512, 0, ctx->stream>>>(skeys, stoks, n_ids, v, dy, grad, dim4, lr);
-        else
-            embed_bwd_rows_vec<1024, 1><<<n, 1024, 0, ctx->stream>>>(skeys, stoks, n_ids, v, dy, grad, dim4, lr);
-        if (int st = launched(ctx, "embed_bwd_rows_vec")) return st;
+        const bool merged = long_runs && tpt == 1024 && n_ids + nslots <= 0x7fffffffLL &&
+                            ctx->tune.embed_bwd_merged != 0;
+        if (merged) {
+            embed_bwd_rows_seg<<<static_cast<unsigned>(n_ids + nslots), 1024, 0, ctx->stream>>>(skeys, stoks, n_ids,
+                                                                                             v, dy, grad, part, dim4);
+            if (int st = launched(ctx, "embed_bwd_rows_seg")) return st;
+        } else {
+            if (long_runs) {
+                const dim3 pgrid(static_cast<unsigned>(nslots),
+                                 static_cast<unsigned>((dim4 + kSegCols - 1) / kSegCols));
+                embed_bwd_seg_partial<<<pgrid, kSegCols, 0, ctx->stream>>>(skeys, stoks, n_ids, v, dy, part, dim4);
+                if (int st = launched(ctx, "embed_bwd_seg_partial")) return st;
+            }
+            if (tpt == 256)
+                embed_bwd_rows_vec<256, 4><<<n, 256, 0, ctx->stream>>>(skeys, stoks, n_ids, v, dy, grad, dim4, lr);
+            else if (tpt == 512)
+                embed_bwd_rows_vec<512, 2><<<n, 512, 0, ctx->stream>>>(skeys, stoks, n_ids, v, dy, grad, dim4, lr);
+            else
+                embed_bwd_rows_vec<1024, 1><<<n, 1024, 0, ctx->stream>>>(skeys, stoks, n_ids, v, dy, grad, dim4, lr);
+            if (int st = launched(ctx, "embed_bwd_rows_vec")) return st;
+        }
         if (!long_runs) return MIMIR_OK;
         // The long runs' segment partials are complete (stream order): add them.
         embed_bwd_seg_combine<<<static_cast<unsigned>(nslots), kWave * kLongSlices, 0, ctx->stream>>>(

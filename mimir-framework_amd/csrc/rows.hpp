@@ -62,6 +62,7 @@ struct Tuning {
     int chain_streamed = 0;   // chain=0: the runtime streams every layer's output (no kept outputs)
     int attn_bwd_heads = 0;   // heads per group of the attention backward (0: what 1 GiB of P / dS holds)
     int attn_bwd_blocks = 0;  // causal attention backward: query / key blocks of the products (0: default)
+    int embed_bwd_merged = -1;  // embedding backward: rows + segment partials in one launch (1) or two (0)
 };
 
 inline bool parse_shape(const char* v, RowShape* s) {
@@ -100,6 +101,7 @@ inline Tuning read_tuning() {
         else if (!std::strcmp(k, "chain")) t.chain_streamed = std::atoi(v) == 0;
         else if (!std::strcmp(k, "attnbwd_heads")) t.attn_bwd_heads = std::atoi(v);
         else if (!std::strcmp(k, "attnbwd_blocks")) t.attn_bwd_blocks = std::atoi(v);
+        else if (!std::strcmp(k, "embmerge")) t.embed_bwd_merged = std::atoi(v);
     }
     return t;
 }
