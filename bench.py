@@ -87,6 +87,28 @@ def _replicate(ctx, host_arrays, nsets):
     return sets
 
 
+def small_stack(blocks=4, seq=128, e=256, heads=4):
+    """A small transformer stack for the launch-bound runtime measurement:
+    `blocks` pre-norm half-blocks (LayerNorm -> SelfAttention -> Add ->
+    LayerNorm -> GELU) on [seq x e], 5 layers each, reading "inp" and
+    leaving "x".  Returns (layers, float inputs)."""
+    r = G.rng(5, 0)
+    layers, cur = [], "inp"
+    for b in range(blocks):
+        g = np.concatenate([1 + 0.05 * r.standard_normal(e), 0.05 * r.standard_normal(e)]).astype(np.float32)
+        w = (r.standard_normal(4 * e * e) / np.sqrt(e)).astype(np.float32)
+        out = "x" if b == blocks - 1 else f"h{b}"
+        layers += [dict(name=f"ln{b}", type="LayerNorm", inputs=[cur], output=f"n{b}", in_features=e, weights=g),
+                   dict(name=f"attn{b}", type="SelfAttention", inputs=[f"n{b}"], output=f"a{b}", seq_len=seq,
+                        embed_dim=e, num_heads=heads, causal=True, weights=w),
+                   dict(name=f"res{b}", type="Add", inputs=[f"a{b}", cur], output=f"r{b}"),
+                   dict(name=f"ln2_{b}", type="LayerNorm", inputs=[f"r{b}"], output=f"m{b}", in_features=e,
+                        weights=g),
+                   dict(name=f"act{b}", type="GELU", inputs=[f"m{b}"], output=out)]
+        cur = out
+    return layers, {"inp": r.standard_normal(seq * e).astype(np.float32)}
+
+
 def block_layers():
     """A residual block's chain of the path's layers at the configs[4] shape,
     routed by name.  The result is named "x", the tensor
@@ -385,6 +407,31 @@ def build_ops(rows_override=None):
     trn.nsets = lambda: 1
     ops.append(trn)
 
+    # Launch-bound: the small stack through the runtime, eager (a launch per
+    # kernel: 4 blocks x (2 LayerNorm, 3 GEMMs + the core, Add, GELU)) and as
+    # one captured graph replayed (mimir_store_capture / _graph_launch).
+    def make_stack(captured):
+        def make(ctx, nsets):
+            layers, fin = small_stack()
+            graph = M.DeviceGraph(ctx, layers)
+            store = M.Store(ctx)
+            if captured:
+                sg = store.capture(graph, fin, {})
+                return (lambda i: sg.launch()), [[_Owned(sg, store, graph)]]
+            store.set_inputs(fin, {})
+            store.run(graph)  # fills the pool, the scratch and the library workspace
+            return (lambda i: store.run(graph)), [[_Owned(store, graph)]]
+        return make
+    sl, _ = small_stack()
+    for key, captured in (("f1_stack_eager", False), ("f1_stack_graph", True)):
+        op = OpBench(key, -1, f"runtime forward of a small transformer stack ({len(sl)} layers, [128x256], 4 "
+                     f"causal attention blocks), {'one captured graph launch' if captured else 'eager launches'}",
+                     "mimir_store_graph_launch" if captured else "mimir_store_run", 128 * 256 * f4, 128, "rows",
+                     make_stack(captured))
+        op.nsets = lambda: 1
+        op.bound = "launch"
+        ops.append(op)
+
     # Calibration: a plain streaming copy of 512 MiB (mimir_copy), the
     # practical HBM ceiling and the yardstick for the FETCH/WRITE counters.
     def make_copy(ctx, nsets):
@@ -446,7 +493,9 @@ def time_op(ctx, op, steps, warmup, spin_s=0.25):
         "row_unit": op.row_unit, "launches": steps, "buffer_sets": nsets,
         "footprint_MiB": round(nsets * op.nbytes / 2**20, 1),
     }
-    if op.flops:
+    if getattr(op, "bound", None) == "launch":
+        rec.update({"bound": "launch", "GB_s": None, "frac_of_peak": None})
+    elif op.flops:
         tf = op.flops / (us * 1e-6) / 1e12
         rec.update({"bound": "mfma", "algorithmic_flops": op.flops, "TFLOP_s": round(tf, 2),
                     "frac_of_peak": round(tf / PEAK_F32_MFMA_TFLOPS, 4), "peak": PEAK_F32_MFMA_TFLOPS,
@@ -1104,6 +1153,8 @@ def main():
     if args.workload not in by_key:
         sys.exit(f"unknown workload {args.workload}; choose from {sorted(by_key)}")
     head = by_key[args.workload]
+    if getattr(head, "bound", None) == "launch":
+        sys.exit(f"{args.workload} is launch-bound (it is timed in the sweep, not as the metric's workload)")
 
     ctx = M.Context(0)
     log(f"workload {head.key}: {head.desc}")
@@ -1131,7 +1182,10 @@ def main():
         if k == "cfg3_safetensors_ingest":
             continue
         r = time_op(ctx, by_key[k], args.op_steps, 3)
-        log(f"op {k}: {r['us_per_launch']} us/launch, {r['GB_s']} GB/s ({100 * r['frac_of_peak']:.1f}%)")
+        if r.get("bound") == "launch":
+            log(f"op {k}: {r['us_per_launch']} us/launch (launch-bound)")
+        else:
+            log(f"op {k}: {r['us_per_launch']} us/launch, {r['GB_s']} GB/s ({100 * r['frac_of_peak']:.1f}%)")
         sweep.append(r)
     if args.ops == "all" or "cfg3_safetensors_ingest" in keys:
         r = time_ingest(ctx)
@@ -1234,13 +1288,18 @@ def main():
         "ops_fields": ["us_per_launch", "GB_s", "frac_of_peak", "parity_pass", "traffic_over_algorithmic"],
         "ops": {r["op"]: [r["us_per_launch"], r["GB_s"], r.get("frac_of_peak"),
                           r["parity"]["pass"] if "parity" in r else None,
-                          r.get("traffic_over_algorithmic")] for r in sweep if r.get("bound") != "mfma"},
+                          r.get("traffic_over_algorithmic")] for r in sweep if r.get("bound") not in ("mfma", "launch")},
         "mfma_ops_fields": ["us_per_launch", "TFLOP_s", "frac_of_fp32_mfma_peak", "parity_pass",
                             "cpu_GFLOP_s"],
         "mfma_ops": {r["op"]: [r["us_per_launch"], r["TFLOP_s"], r["frac_of_peak"],
                                r["parity"]["pass"] if "parity" in r else None, r.get("cpu_GFLOP_s")]
                      for r in sweep if r.get("bound") == "mfma"},
     }
+    stack = {r["op"]: r["us_per_launch"] for r in sweep if r.get("bound") == "launch"}
+    if "f1_stack_eager" in stack and "f1_stack_graph" in stack:
+        line["runtime_graph"] = {"layers": 20, "eager_us": stack["f1_stack_eager"],
+                                 "graph_us": stack["f1_stack_graph"],
+                                 "speedup": round(stack["f1_stack_eager"] / stack["f1_stack_graph"], 2)}
     full = dict(line, parity=parity.get(head.key), ops=sweep)
     out = args.full_out
     if out:

@@ -546,6 +546,48 @@ int mimir_store_backward(mimir_store* store, const mimir_layer* layers, int32_t 
 int mimir_store_backward_dev(mimir_store* store, const mimir_layer* layers, int32_t n_layers, const float* loss_grad,
                              int64_t n_grad);
 
+/* ---------------------------------------------------------------------------
+ * Captured forwards: a mimir_store_run recorded once as a HIP graph and
+ * replayed with one launch.  No counterpart in the reference, whose layers
+ * run one host call after another: for callers that run the same graph of
+ * small layers many times (serving, evaluation loops), where launching the
+ * kernels one by one costs more than running them.
+ *
+ *   mimir_store_set_inputs(store, ...);        // the tensors the graph reads
+ *   mimir_store_capture(store, layers, n, &g); // runs once eagerly (so every
+ *                                              // buffer exists), then records
+ *                                              // the same run and launches it
+ *   for (...) {
+ *       mimir_store_graph_set_input(g, "x", MIMIR_DTYPE_F32, host, n);
+ *       mimir_store_graph_launch(g);
+ *       mimir_store_graph_get(g, "x", MIMIR_DTYPE_F32, out, cap, &n_out);
+ *   }
+ *   mimir_store_graph_destroy(g);
+ *
+ * The graph holds every buffer its run uses (its inputs are the tensors
+ * bound at capture, its outputs the bindings the run left), so the store may
+ * run other work between launches; they are ordered on the context's
+ * stream.  While any graph is alive the context keeps the scratch and
+ * library workspace addresses it captured (growing either allocates a new
+ * one beside the old).  Inference runs only (mimir_store_run).  The
+ * context's stream must not be the null stream.  Destroying the store
+ * destroys its graphs.
+ * ------------------------------------------------------------------------- */
+typedef struct mimir_store_graph mimir_store_graph;
+
+int mimir_store_capture(mimir_store* store, const mimir_layer* layers, int32_t n_layers, mimir_store_graph** out);
+/* Replay on the context's stream (asynchronous). */
+int mimir_store_graph_launch(mimir_store_graph* graph);
+/* Write n host elements into the input `name` (bound when the graph was
+ * captured; EINVAL for another name or size). */
+int mimir_store_graph_set_input(mimir_store_graph* graph, const char* name, int dtype, const void* host,
+                                int64_t n);
+/* Download a tensor the graph's run left bound (at most cap elements; *n
+ * gets its size).  Waits for the launches before it. */
+int mimir_store_graph_get(mimir_store_graph* graph, const char* name, int dtype, void* host, int64_t cap,
+                          int64_t* n);
+int mimir_store_graph_destroy(mimir_store_graph* graph);
+
 /* A gradient of the last mimir_store_backward by tensor name ("__input__"
  * for Model::getLastInputGradient): device pointer and size, or a download
  * of at most cap floats (*n = its size).  EINVAL when no gradient reached

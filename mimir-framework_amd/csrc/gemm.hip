@@ -1,7 +1,9 @@
 // gemm.hip -- the plain fp32 matrix products around the attention core (the
-// QKV and output projections of the attention layers), through rocBLAS on
-// the context's stream.  These are library GEMMs: the path's own kernel is
-// the fused core between them (attention.hip).
+// QKV and output projections of the attention layers, and the per-head
+// products of the attention backward), through rocBLAS on the context's
+// stream.  These are library GEMMs: the path's own kernels are the fused core
+// between them (attention.hip) and the backward's row passes
+// (attention_bwd.hip).
 //
 // The reference computes them with LayerOps::matmul (LayerOps.hpp:977-1001):
 // row-major C[M x N] = A[M x K] * B[K x N] in float32.  rocBLAS is
@@ -14,11 +16,39 @@
 
 namespace {
 
+// The handle's workspace is this library's own allocation, so the library
+// never reallocates it by itself: a captured graph (store.hip) holds its
+// address.  It starts at kWsBytes and grows when a product reports that it
+// needs more (the old one is retired while graphs are alive).
+constexpr size_t kWsBytes = size_t(32) << 20;
+constexpr size_t kWsMax = size_t(4) << 30;
+
+int set_workspace(mimir_ctx* ctx, rocblas_handle h, size_t bytes) {
+    void* p = nullptr;
+    hipError_t e = hipMalloc(&p, bytes);
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        return mimir::fail(ctx, MIMIR_ENOMEM, "library workspace of %zu bytes: %s", bytes, hipGetErrorString(e));
+    }
+    if (rocblas_set_workspace(h, p, bytes) != rocblas_status_success) {
+        (void)hipFree(p);
+        return mimir::fail(ctx, MIMIR_EDEVICE, "rocblas_set_workspace failed");
+    }
+    if (int st = mimir::retire_or_free(ctx, ctx->blas_ws)) return st;
+    ctx->blas_ws = p;
+    ctx->blas_ws_bytes = bytes;
+    return MIMIR_OK;
+}
+
 rocblas_handle handle_of(mimir_ctx* ctx, int* st) {
     if (!ctx->blas) {
         rocblas_handle h = nullptr;
         if (rocblas_create_handle(&h) != rocblas_status_success) {
             *st = mimir::fail(ctx, MIMIR_EDEVICE, "rocblas_create_handle failed");
+            return nullptr;
+        }
+        if ((*st = set_workspace(ctx, h, kWsBytes)) != MIMIR_OK) {
+            (void)rocblas_destroy_handle(h);
             return nullptr;
         }
         ctx->blas = h;
@@ -57,21 +87,29 @@ int gemm_f32_ex(mimir_ctx* ctx, bool trans_a, bool trans_b, int64_t M, int64_t N
     const rocblas_operation ob = trans_b ? rocblas_operation_transpose : rocblas_operation_none;
     const rocblas_operation oa = trans_a ? rocblas_operation_transpose : rocblas_operation_none;
     const auto n32 = static_cast<rocblas_int>(N), m32 = static_cast<rocblas_int>(M), k32 = static_cast<rocblas_int>(K);
-    rocblas_status s;
-    if (batch == 1)
-        s = rocblas_sgemm(h, ob, oa, n32, m32, k32, &alpha, B, static_cast<rocblas_int>(ldb), A,
-                          static_cast<rocblas_int>(lda), &beta, C, static_cast<rocblas_int>(ldc));
-    else
-        s = rocblas_sgemm_strided_batched(h, ob, oa, n32, m32, k32, &alpha, B, static_cast<rocblas_int>(ldb),
-                                          stride_b, A, static_cast<rocblas_int>(lda), stride_a, &beta, C,
-                                          static_cast<rocblas_int>(ldc), stride_c, static_cast<rocblas_int>(batch));
-    if (s != rocblas_status_success) return fail(ctx, MIMIR_EDEVICE, "rocBLAS sgemm failed (status %d)", (int)s);
-    return MIMIR_OK;
+    for (;;) {
+        rocblas_status s;
+        if (batch == 1)
+            s = rocblas_sgemm(h, ob, oa, n32, m32, k32, &alpha, B, static_cast<rocblas_int>(ldb), A,
+                              static_cast<rocblas_int>(lda), &beta, C, static_cast<rocblas_int>(ldc));
+        else
+            s = rocblas_sgemm_strided_batched(h, ob, oa, n32, m32, k32, &alpha, B, static_cast<rocblas_int>(ldb),
+                                              stride_b, A, static_cast<rocblas_int>(lda), stride_a, &beta, C,
+                                              static_cast<rocblas_int>(ldc), stride_c,
+                                              static_cast<rocblas_int>(batch));
+        if (s == rocblas_status_success) return MIMIR_OK;
+        if (s != rocblas_status_memory_error || ctx->blas_ws_bytes >= kWsMax)
+            return fail(ctx, MIMIR_EDEVICE, "rocBLAS sgemm failed (status %d)", (int)s);
+        if (int st2 = set_workspace(ctx, h, ctx->blas_ws_bytes * 4)) return st2;  // grow and try again
+    }
 }
 
 void gemm_release(mimir_ctx* ctx) {
     if (ctx->blas) (void)rocblas_destroy_handle(static_cast<rocblas_handle>(ctx->blas));
     ctx->blas = nullptr;
+    if (ctx->blas_ws) (void)hipFree(ctx->blas_ws);
+    ctx->blas_ws = nullptr;
+    ctx->blas_ws_bytes = 0;
 }
 
 }  // namespace mimir

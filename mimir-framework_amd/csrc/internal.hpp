@@ -9,6 +9,7 @@
 #include <cstdio>
 #include <string>
 #include <unordered_map>
+#include <vector>
 
 #include "../../include/mimir_hip.h"
 #include "rows.hpp"
@@ -30,9 +31,18 @@ struct mimir_ctx {
     // Device address of this GPU's fixed scratch array (backward.hip), for
     // the entry point that allocates nothing; set at context creation.
     void* noalloc_scratch = nullptr;
-    // rocBLAS handle for the attention layers' projections (gemm.hip),
-    // created on first use.
+    // rocBLAS handle for the attention layers' products (gemm.hip), created
+    // on first use, with a workspace of this library's (grown on demand).
     void* blas = nullptr;
+    void* blas_ws = nullptr;
+    size_t blas_ws_bytes = 0;
+    // Captured store graphs alive on this context (store.hip).  Their kernels
+    // hold the addresses of the scratch and the library workspace as they
+    // were at capture, so while any exists a buffer that must grow is retired
+    // (kept allocated) rather than freed; the retired buffers are freed when
+    // the last graph goes.
+    int graph_pins = 0;
+    std::vector<void*> retired;
 };
 
 struct mimir_event {
@@ -89,8 +99,16 @@ inline bool grid_for(int64_t units, int64_t per_block, unsigned* blocks) {
 }
 
 // Context scratch of at least `bytes` (runtime.hip).  Growing it waits for
-// the work already enqueued, which may still read the old buffer.
+// the work already enqueued, which may still read the old buffer (or, while
+// captured graphs hold its address, retires the old buffer instead).
 int ensure_scratch(mimir_ctx* ctx, size_t bytes, void** out);
+
+// Free a device buffer that enqueued work or captured graphs may still use:
+// retired while graphs are alive, else freed after the stream drains.
+int retire_or_free(mimir_ctx* ctx, void* p);
+// A captured graph starts / stops holding the context's buffers.
+void graph_pin(mimir_ctx* ctx);
+int graph_unpin(mimir_ctx* ctx);
 
 // Row-major fp32 C[M x N] = A[M x K] * B[K x N] on the context's stream
 // (rocBLAS; gemm.hip), and the release of its handle at context teardown.

@@ -53,12 +53,33 @@ unsigned stride_grid(int64_t n) {
 
 }  // namespace
 
+int mimir::retire_or_free(mimir_ctx* ctx, void* p) {
+    if (!p) return MIMIR_OK;
+    if (ctx->graph_pins > 0) {
+        ctx->retired.push_back(p);
+        return MIMIR_OK;
+    }
+    hipError_t e = hipStreamSynchronize(ctx->stream);
+    if (e != hipSuccess) return hip_fail(ctx, e, "hipStreamSynchronize");
+    (void)hipFree(p);
+    return MIMIR_OK;
+}
+
+void mimir::graph_pin(mimir_ctx* ctx) { ++ctx->graph_pins; }
+
+int mimir::graph_unpin(mimir_ctx* ctx) {
+    if (--ctx->graph_pins > 0 || ctx->retired.empty()) return MIMIR_OK;
+    hipError_t e = hipStreamSynchronize(ctx->stream);
+    if (e != hipSuccess) return hip_fail(ctx, e, "hipStreamSynchronize");
+    for (void* p : ctx->retired) (void)hipFree(p);
+    ctx->retired.clear();
+    return MIMIR_OK;
+}
+
 int mimir::ensure_scratch(mimir_ctx* ctx, size_t bytes, void** out) {
     if (bytes > ctx->scratch_bytes) {
         if (ctx->scratch) {
-            hipError_t e = hipStreamSynchronize(ctx->stream);
-            if (e != hipSuccess) return hip_fail(ctx, e, "hipStreamSynchronize");
-            (void)hipFree(ctx->scratch);
+            if (int st = retire_or_free(ctx, ctx->scratch)) return st;
             ctx->scratch = nullptr;
             ctx->scratch_bytes = 0;
         }
@@ -110,6 +131,7 @@ int mimir_ctx_destroy(mimir_ctx* ctx) {
         gemm_release(ctx);
         for (auto& kv : ctx->allocs) (void)hipFree(kv.first);
         if (ctx->scratch) (void)hipFree(ctx->scratch);
+        for (void* p : ctx->retired) (void)hipFree(p);
         (void)hipStreamDestroy(ctx->own_stream);
     }
     delete ctx;

@@ -23,6 +23,7 @@
 #include "common.hpp"
 #include "internal.hpp"
 
+#include <algorithm>
 #include <map>
 #include <new>
 #include <memory>
@@ -73,6 +74,9 @@ struct mimir_store {
     std::unordered_map<std::string, Slot> grads;  // last mimir_store_backward
     std::vector<std::unique_ptr<Buf>> bufs;
     std::multimap<size_t, Buf*> free_bufs;  // capacity -> idle buffer
+    // While a run is captured (mimir_store_capture): every buffer it acquires.
+    std::vector<Buf*>* capture_log = nullptr;
+    std::vector<mimir_store_graph*> graphs;  // alive captured graphs
 
     std::unordered_map<std::string, Slot>& map(int dtype) { return dtype == MIMIR_DTYPE_I32 ? i32 : f32; }
 
@@ -84,6 +88,7 @@ struct mimir_store {
         if (it != free_bufs.end() && it->first <= 2 * bytes) {
             *out = it->second;
             free_bufs.erase(it);
+            if (capture_log) capture_log->push_back(*out);
             return MIMIR_OK;
         }
         void* p = nullptr;
@@ -94,7 +99,18 @@ struct mimir_store {
         b->p = p;
         b->cap = bytes;
         *out = b;
+        if (capture_log) capture_log->push_back(b);
         return MIMIR_OK;
+    }
+
+    // Take an idle buffer out of the pool (it is about to be held).
+    void unpool(Buf* b) {
+        auto r = free_bufs.equal_range(b->cap);
+        for (auto it = r.first; it != r.second; ++it)
+            if (it->second == b) {
+                free_bufs.erase(it);
+                return;
+            }
     }
 
     void release(Buf* b) {
@@ -139,6 +155,20 @@ struct mimir_store {
         release_snaps();
         release_grads();
     }
+};
+
+// A captured mimir_store_run (mimir_store_capture).  Its kernels hold the
+// device addresses of the buffers the run used, so the graph holds a
+// reference on each of them (the pool never hands them out while it lives),
+// and it keeps its own name -> buffer maps: `in`, the tensors bound when it
+// was captured (what set_input writes), and `out`, the bindings after the
+// run (what get reads).  Index 0: float tensors, 1: int tensors.
+struct mimir_store_graph {
+    mimir_store* store = nullptr;
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+    std::vector<Buf*> held;
+    std::unordered_map<std::string, Slot> in[2], out[2];
 };
 
 namespace {
@@ -615,6 +645,10 @@ int mimir_store_create(mimir_ctx* ctx, mimir_store** out) {
 int mimir_store_destroy(mimir_store* s) {
     if (!s) return MIMIR_EINVAL;
     int st = MIMIR_OK;
+    while (!s->graphs.empty()) {
+        const int r = mimir_store_graph_destroy(s->graphs.back());
+        if (r != MIMIR_OK && st == MIMIR_OK) st = r;
+    }
     for (auto& b : s->bufs) {
         const int r = mimir_free(s->ctx, b->p);
         if (r != MIMIR_OK && st == MIMIR_OK) st = r;
@@ -905,6 +939,151 @@ int mimir_store_grad_get(mimir_store* s, const char* name, float* host, int64_t 
         return mimir_download(s->ctx, host, it->second.buf->p, static_cast<size_t>(k) * 4);
     }
     return MIMIR_OK;
+}
+
+int mimir_store_capture(mimir_store* s, const mimir_layer* layers, int32_t n_layers, mimir_store_graph** out) {
+    if (!s || !out) return MIMIR_EINVAL;
+    *out = nullptr;
+    mimir_ctx* ctx = s->ctx;
+    MIMIR_REQUIRE(ctx, n_layers >= 0 && (n_layers == 0 || layers), "mimir_store_capture: invalid argument");
+    MIMIR_REQUIRE(ctx, ctx->stream != nullptr,
+                  "mimir_store_capture: the context's stream is the null stream, which cannot be captured");
+    MIMIR_ENTER(ctx);
+    std::unique_ptr<mimir_store_graph> g(new (std::nothrow) mimir_store_graph());
+    if (!g) return MIMIR_ENOMEM;
+    g->store = s;
+    // The inputs: the bindings now, each held by the graph from here on.
+    g->in[0] = s->f32;
+    g->in[1] = s->i32;
+    for (auto& m : g->in)
+        for (auto& kv : m) {
+            Buf* b = kv.second.buf;
+            if (b->refs++ == 0) s->unpool(b);  // (bound buffers are never pooled; for symmetry)
+            if (std::find(g->held.begin(), g->held.end(), b) == g->held.end()) g->held.push_back(b);
+            else --b->refs;
+        }
+    auto drop = [&]() {
+        for (Buf* b : g->held) s->release(b);
+        g->held.clear();
+    };
+    auto rebind_inputs = [&]() {
+        for (int d = 0; d < 2; ++d) {
+            auto& m = s->map(d == 0 ? MIMIR_DTYPE_F32 : MIMIR_DTYPE_I32);
+            for (auto& kv : m) s->release(kv.second.buf);
+            m.clear();
+            for (auto& kv : g->in[d]) s->bind(d == 0 ? MIMIR_DTYPE_F32 : MIMIR_DTYPE_I32, kv.first, kv.second.buf,
+                                              kv.second.n);
+        }
+    };
+    // A first, eager run: every pool buffer, the scratch and the library
+    // workspace the run needs then exist, so the captured run allocates
+    // nothing.  The store never writes a buffer in place, so the inputs are
+    // intact afterwards and are bound again.
+    if (int st = mimir_store_run(s, layers, n_layers)) {
+        drop();
+        return st;
+    }
+    rebind_inputs();
+    hipError_t e = hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeRelaxed);
+    if (e != hipSuccess) {
+        drop();
+        return hip_fail(ctx, e, "hipStreamBeginCapture");
+    }
+    std::vector<Buf*> log;
+    s->capture_log = &log;
+    const int st = mimir_store_run(s, layers, n_layers);
+    s->capture_log = nullptr;
+    hipGraph_t graph = nullptr;
+    e = hipStreamEndCapture(ctx->stream, &graph);
+    if (st != MIMIR_OK || e != hipSuccess) {
+        if (graph) (void)hipGraphDestroy(graph);
+        (void)hipGetLastError();
+        drop();
+        return st != MIMIR_OK ? st : hip_fail(ctx, e, "hipStreamEndCapture");
+    }
+    g->graph = graph;
+    e = hipGraphInstantiate(&g->exec, graph, nullptr, nullptr, 0);
+    if (e != hipSuccess) {
+        (void)hipGraphDestroy(graph);
+        drop();
+        return hip_fail(ctx, e, "hipGraphInstantiate");
+    }
+    // Every buffer the captured run acquired, including intermediates it
+    // released back to the pool (the graph writes them on each launch).
+    for (Buf* b : log) {
+        if (std::find(g->held.begin(), g->held.end(), b) != g->held.end()) continue;
+        if (b->refs++ == 0) s->unpool(b);
+        g->held.push_back(b);
+    }
+    g->out[0] = s->f32;
+    g->out[1] = s->i32;
+    graph_pin(ctx);
+    s->graphs.push_back(g.get());
+    mimir_store_graph* gp = g.release();
+    // Compute what the outputs name now (the capture only recorded the run).
+    if (int st2 = mimir_store_graph_launch(gp)) {
+        (void)mimir_store_graph_destroy(gp);
+        return st2;
+    }
+    *out = gp;
+    return MIMIR_OK;
+}
+
+int mimir_store_graph_launch(mimir_store_graph* g) {
+    if (!g) return MIMIR_EINVAL;
+    mimir_ctx* ctx = g->store->ctx;
+    MIMIR_ENTER(ctx);
+    hipError_t e = hipGraphLaunch(g->exec, ctx->stream);
+    if (e != hipSuccess) return hip_fail(ctx, e, "hipGraphLaunch");
+    return MIMIR_OK;
+}
+
+int mimir_store_graph_set_input(mimir_store_graph* g, const char* name, int dtype, const void* host, int64_t n) {
+    if (!g) return MIMIR_EINVAL;
+    mimir_ctx* ctx = g->store->ctx;
+    MIMIR_REQUIRE(ctx, name && n >= 0 && (n == 0 || host), "mimir_store_graph_set_input: invalid argument");
+    auto& m = g->in[dtype == MIMIR_DTYPE_I32 ? 1 : 0];
+    auto it = m.find(name);
+    MIMIR_REQUIRE(ctx, it != m.end(), "mimir_store_graph_set_input: %s is not an input of the graph", name);
+    MIMIR_REQUIRE(ctx, it->second.n == n, "mimir_store_graph_set_input: %s holds %lld elements, not %lld", name,
+                  (long long)it->second.n, (long long)n);
+    if (n == 0) return MIMIR_OK;
+    return mimir_upload(ctx, it->second.buf->p, host, static_cast<size_t>(n) * 4);
+}
+
+int mimir_store_graph_get(mimir_store_graph* g, const char* name, int dtype, void* host, int64_t cap, int64_t* n) {
+    if (!g) return MIMIR_EINVAL;
+    mimir_ctx* ctx = g->store->ctx;
+    MIMIR_REQUIRE(ctx, name && n && cap >= 0, "mimir_store_graph_get: invalid argument");
+    auto& m = g->out[dtype == MIMIR_DTYPE_I32 ? 1 : 0];
+    auto it = m.find(name);
+    MIMIR_REQUIRE(ctx, it != m.end(), "mimir_store_graph_get: the graph binds no tensor named %s", name);
+    *n = it->second.n;
+    const int64_t k = cap < it->second.n ? cap : it->second.n;
+    if (k > 0) {
+        MIMIR_REQUIRE(ctx, host, "mimir_store_graph_get: null host buffer");
+        return mimir_download(ctx, host, it->second.buf->p, static_cast<size_t>(k) * 4);
+    }
+    return MIMIR_OK;
+}
+
+int mimir_store_graph_destroy(mimir_store_graph* g) {
+    if (!g) return MIMIR_EINVAL;
+    mimir_store* s = g->store;
+    mimir_ctx* ctx = s->ctx;
+    int st = enter(ctx);
+    // Launches still in flight read and write the held buffers.
+    if (st == MIMIR_OK) {
+        hipError_t e = hipStreamSynchronize(ctx->stream);
+        if (e != hipSuccess) st = hip_fail(ctx, e, "hipStreamSynchronize");
+    }
+    if (g->exec) (void)hipGraphExecDestroy(g->exec);
+    if (g->graph) (void)hipGraphDestroy(g->graph);
+    for (Buf* b : g->held) s->release(b);
+    s->graphs.erase(std::remove(s->graphs.begin(), s->graphs.end(), g), s->graphs.end());
+    const int st2 = graph_unpin(ctx);
+    delete g;
+    return st != MIMIR_OK ? st : st2;
 }
 
 }  // extern "C"

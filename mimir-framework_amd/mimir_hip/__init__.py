@@ -6,11 +6,11 @@ row-reduction layer path, reached through the C ABI of libmimir_hip.so.
 """
 from ._lib import (EDEVICE, EINVAL, ENOMEM, OK, SOFTMAX_DIV_EPS, SOFTMAX_LOG, SOFTMAX_MUL_INV,
                    HEADER_PATH, LIB_PATH, SIGNATURES, load)
-from .device import Context, DeviceArray, DeviceGraph, Event, MimirError, SafeTensors, Store, rope_table
+from .device import Context, DeviceArray, DeviceGraph, Event, MimirError, SafeTensors, Store, StoreGraph, rope_table
 from .layerops import Layer, LayerOps
 
 __all__ = [
-    "Context", "DeviceArray", "DeviceGraph", "Event", "SafeTensors", "Store", "MimirError", "Layer", "LayerOps", "rope_table", "load",
+    "Context", "DeviceArray", "DeviceGraph", "Event", "SafeTensors", "Store", "StoreGraph", "MimirError", "Layer", "LayerOps", "rope_table", "load",
     "OK", "EINVAL", "ENOMEM", "EDEVICE", "SOFTMAX_DIV_EPS", "SOFTMAX_MUL_INV", "SOFTMAX_LOG",
     "LIB_PATH", "HEADER_PATH", "SIGNATURES",
 ]

@@ -433,6 +433,12 @@ class Store:
         self.backward(graph, loss_grad)
         return graph.grads(), self.grad("__input__")
 
+    def capture(self, graph: "DeviceGraph", fin=None, iin=None):
+        """set_inputs(fin, iin), then mimir_store_capture of graph's forward:
+        a StoreGraph to replay it."""
+        self.set_inputs(fin, iin)
+        return StoreGraph(self, graph)
+
     def forward_named(self, graph: "DeviceGraph", fin=None, iin=None, training=False):
         """Model::forwardPassNamed(fin, iin, training) on the device (the
         training form keeps the backward's snapshots and applies the
@@ -440,6 +446,47 @@ class Store:
         self.set_inputs(fin, iin)
         (self.run_training if training else self.run)(graph)
         return self.get("x")
+
+
+class StoreGraph:
+    """A captured forward (mimir_store_capture): set_input() the tensors bound
+    at capture, launch(), get() what the run left bound."""
+
+    def __init__(self, store: "Store", graph: "DeviceGraph"):
+        self.store, self.ctx = store, store.ctx
+        self._graph = graph  # its layer descriptors and weights stay alive with this
+        h = c_void_p()
+        self.ctx.check(self.ctx.lib.mimir_store_capture(store.handle, graph.c_layers, len(graph.layers), byref(h)))
+        self.handle = h
+
+    def set_input(self, name, arr):
+        a = np.ascontiguousarray(arr)
+        dt = _lib.DTYPE_I32 if a.dtype.kind in "iu" else _lib.DTYPE_F32
+        a = np.ascontiguousarray(a, np.int32 if dt == _lib.DTYPE_I32 else np.float32).ravel()
+        self.ctx.check(self.ctx.lib.mimir_store_graph_set_input(self.handle, name.encode(), dt,
+                                                                a.ctypes.data_as(c_void_p), a.size))
+
+    def launch(self):
+        self.ctx.check(self.ctx.lib.mimir_store_graph_launch(self.handle))
+
+    def get(self, name="x", dtype=_lib.DTYPE_F32):
+        n = ctypes.c_int64()
+        self.ctx.check(self.ctx.lib.mimir_store_graph_get(self.handle, name.encode(), dtype, None, 0, byref(n)))
+        out = np.empty(n.value, np.int32 if dtype == _lib.DTYPE_I32 else np.float32)
+        self.ctx.check(self.ctx.lib.mimir_store_graph_get(self.handle, name.encode(), dtype,
+                                                          out.ctypes.data_as(c_void_p), n.value, byref(n)))
+        return out
+
+    def close(self):
+        if self.handle:
+            self.ctx.check(self.ctx.lib.mimir_store_graph_destroy(self.handle))
+            self.handle = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
 
 
 def branch_fields(L):
