@@ -382,6 +382,27 @@ def build_ops(rows_override=None):
     blk.nsets = lambda: 1
     ops.append(blk)
 
+    # The same block with the runtime's fusion on (mimir_store_set_fusion):
+    # Add -> LayerNorm -> GELU -> Multiply -> SiLU run as one kernel (the
+    # LayerNorm with an add prologue and an elementwise epilogue), so the
+    # block moves 4 streams of [8192x4096] instead of 12: inp, res and gate
+    # in, x out.
+    def make_block_fused(ctx, nsets):
+        x, res = G.cfg4_add()
+        gate = G.cfg4_grad((8192, 4096), 11)
+        graph = M.DeviceGraph(ctx, block_layers())
+        store = M.Store(ctx)
+        store.set_fusion(True)
+        store.set_inputs({"inp": x, "res": res, "gate": gate}, {})
+        store.run(graph)
+        return (lambda i: store.run(graph)), [[_Owned(store, graph)]]
+    bf = OpBench("cfg4_runtime_block_fused", 4,
+                 "the same block with the runtime's fusion: the five layers as one kernel on [8192x4096]",
+                 "norm_rows_vec<AddLayer, 512, 2, 512, epilogue>", 4 * 8192 * 4096 * f4 + 2 * 4096 * f4,
+                 8192, "rows", make_block_fused, lambda s: {"x": s[0][0].objs[0].get("x")})
+    bf.nsets = lambda: 1
+    ops.append(bf)
+
     # One device-resident training step of the same block: forwardPassNamed
     # (training=true) then backwardPass with the loss gradient already in HBM
     # (mimir_store_run_training + mimir_store_backward_dev).  Streams of
@@ -693,7 +714,7 @@ def cpu_leg(which, reps):
                 else:
                     t = O.time_port(lambda: np.fromfile(path, np.uint8, count=table.nbytes, offset=8 + len(hdr)), reps)
                     rec(key, t, table.nbytes, 32000, "port", "sequential read of the tensor bytes into host memory")
-        elif key == "cfg4_runtime_block":
+        elif key in ("cfg4_runtime_block", "cfg4_runtime_block_fused"):
             rows = 1024
             x, res = G.cfg4_add(rows=rows)
             gate = G.cfg4_grad((8192, 4096), 11)[:rows]
@@ -1062,7 +1083,7 @@ def parity_leg(ctx, by_key, which):
             check_arrays(key, {"ln grad_weights": (got, ref, scale)},
                          "reference (Model::backwardPass of the same five layers)",
                          f"first {rows} of 8192 rows, the LayerNorm's [dgamma | dbeta] at the end of the chain")
-        elif key == "cfg4_runtime_block" and MR.available():
+        elif key in ("cfg4_runtime_block", "cfg4_runtime_block_fused") and MR.available():
             rows = 1024
             x, res = G.cfg4_add(rows=rows)
             gate = G.cfg4_grad((8192, 4096), 11)[:rows]

@@ -487,6 +487,26 @@ int mimir_store_set_inputs(mimir_store* store, const char* const* fnames, const 
  * the message, e.g. "Missing input tensor: <name>". */
 int mimir_store_run(mimir_store* store, const mimir_layer* layers, int32_t n_layers);
 
+/* Inference fusion for mimir_store_run (and what mimir_store_capture
+ * records), off by default.  No counterpart in the reference, which stores
+ * every layer's output.  When on, a group of consecutive layers in which
+ * each reads the previous one's output runs as one kernel:
+ *   - [Add (equal sizes) ->] LayerNorm [-> elementwise chain]: the
+ *     LayerNorm kernel adds its input first and applies the chain to the
+ *     normalised values before storing (rows the register-resident kernel
+ *     takes: widths that are multiples of 4 up to 16384 floats, aligned
+ *     parameters, no LayerNorm shape override);
+ *   - an elementwise chain alone: GELU, SiLU, and Add / Multiply of equal
+ *     sizes.
+ * Every tensor the group reads crosses HBM once.  An intermediate output is
+ * written only when a layer after the group reads its name (or it is "x"
+ * and the group does not write "x" again); the other intermediates' names
+ * are left unbound, so mimir_store_get on them fails.  "x" and every name a
+ * later layer reads hold the unfused run's values bit for bit.  The second
+ * operand of a fused Add / Multiply in a chain must be bound when the group
+ * starts.  Training runs never fuse. */
+int mimir_store_set_fusion(mimir_store* store, int enable);
+
 /* mimir_store_run with the reference's training bookkeeping (forwardPassView
  * with training=true, Model.cpp:4723-4878): each layer's inputs are kept for
  * mimir_store_backward.  The store never writes a tensor in place, so the

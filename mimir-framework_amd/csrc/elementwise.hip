@@ -10,35 +10,13 @@
 // run through a scalar grid-stride kernel with the same per-element functor.
 #include "common.hpp"
 #include "internal.hpp"
+#include "pointwise.hpp"
 
 #include <math.h>
 
 using namespace mimir;
 
 namespace {
-
-// LayerOps::gelu_forward, LayerOps.hpp:556-568, computes
-//   y = x * 0.5f*(1 + tanhf(u)),  u = sqrt(2/pi)*(x + 0.044715f*x^3)
-// with the float sqrt of the float quotient as the constant.  Since
-// 0.5*(1 + tanh(u)) = 1/(1 + exp(-2u)) exactly, the kernel evaluates the
-// logistic form: one expf and one hardware reciprocal (v_rcp_f32, 1 ulp)
-// instead of the branchy tanhf, which left the op compute-bound on MI355X.
-// It is also the better-conditioned form: the reference's 1 + tanhf(u)
-// cancels for x < -3 (absolute error <= 1.5e-7 there), so the two agree to
-// the path's tolerance everywhere, including the -0 / +-inf / NaN cases
-// (exp overflow gives x * 0).
-__device__ __forceinline__ float gelu1(float x) {
-    const float k = __builtin_sqrtf(2.0f / 3.14159265359f);
-    const float u = k * (x + 0.044715f * x * x * x);
-    return x * __builtin_amdgcn_rcpf(1.0f + expf(-2.0f * u));
-}
-
-// LayerOps::silu_forward, LayerOps.hpp:570-581: y = x * (1/(1 + exp(-x))),
-// with the reciprocal taken by v_rcp_f32 (1 ulp).
-__device__ __forceinline__ float silu1(float x) {
-    const float sigmoid = __builtin_amdgcn_rcpf(1.0f + expf(-x));
-    return x * sigmoid;
-}
 
 struct Gelu {
     __device__ float operator()(float x) const { return gelu1(x); }
@@ -240,7 +218,65 @@ int run_binary(mimir_ctx* ctx, const float* a, const float* b, float* y, int64_t
     return MIMIR_OK;
 }
 
+// One 16-byte vector per thread; the steps run in registers, each binary
+// step loading its operand where it is used (many waves in flight hide the
+// latency: the kernel stays small).  The program is uniform across the grid,
+// so its branches never diverge.
+template <bool KEEP>
+__global__ __launch_bounds__(kBlock) void fused_chain_vec(const FuseProgram p, int64_t n4) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
+    if (i >= n4) return;
+    f4 v = ld4<true>(p.ins[0] + 4 * i);
+    for (int k = 0; k < p.n_steps; ++k) {
+        const FuseStep st = p.steps[k];
+        const bool bin = st.kind == kFuseAdd || st.kind == kFuseMul;
+        const f4 o = bin && st.operand >= 0 ? ld4<true>(p.ins[st.operand] + 4 * i) : v;
+        v = fuse_step4(st.kind, v, o);
+        // The chain's last value is what the next layer reads; the
+        // intermediates a later layer needs are streamed out.
+        if (st.store >= 0) {
+            if (k + 1 == p.n_steps) st_out<KEEP>(p.outs[st.store] + 4 * i, v);
+            else st4<true>(p.outs[st.store] + 4 * i, v);
+        }
+    }
+}
+
+__global__ __launch_bounds__(kBlock) void fused_chain_scalar(const FuseProgram p, int64_t first, int64_t n) {
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * kBlock;
+    for (int64_t i = first + static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x; i < n; i += stride) {
+        float v = p.ins[0][i];
+        for (int k = 0; k < p.n_steps; ++k) {
+            const FuseStep st = p.steps[k];
+            v = fuse_step1(st.kind, v, st.operand >= 0 ? p.ins[st.operand][i] : v);
+            if (st.store >= 0) p.outs[st.store][i] = v;
+        }
+    }
+}
+
 }  // namespace
+
+int mimir::fused_chain(mimir_ctx* ctx, const FuseProgram& p, int64_t n) {
+    if (n == 0) return MIMIR_OK;
+    bool aligned = true;
+    for (int k = 0; k < p.n_ins; ++k) aligned = aligned && aligned16(p.ins[k]);
+    for (int k = 0; k < p.n_outs; ++k) aligned = aligned && aligned16(p.outs[k]);
+    MIMIR_ENTER(ctx);
+    int64_t done = 0;
+    if (aligned && n / 4 > 0) {
+        const int64_t n4 = n / 4;
+        unsigned blocks;
+        if (!grid_for(n4, kBlock, &blocks)) return fail(ctx, MIMIR_EINVAL, "fused chain: grid too large");
+        if (ctx->keep_outputs) fused_chain_vec<true><<<blocks, kBlock, 0, ctx->stream>>>(p, n4);
+        else fused_chain_vec<false><<<blocks, kBlock, 0, ctx->stream>>>(p, n4);
+        if (int st = launched(ctx, "fused_chain_vec")) return st;
+        done = n4 * 4;
+    }
+    if (n > done) {
+        fused_chain_scalar<<<stride_grid(n - done), kBlock, 0, ctx->stream>>>(p, done, n);
+        return launched(ctx, "fused_chain_scalar");
+    }
+    return MIMIR_OK;
+}
 
 extern "C" {
 

@@ -122,6 +122,47 @@ int gemm_f32_ex(mimir_ctx* ctx, bool trans_a, bool trans_b, int64_t M, int64_t N
                 float beta, float* C, int64_t ldc, int64_t stride_c, int64_t batch);
 void gemm_release(mimir_ctx* ctx);
 
+// A chain of elementwise layers run as one kernel (store.hip's fusion):
+// v = ins[0]; then each step k sets v = op_k(v, operand) -- GELU, SiLU, or
+// an add / multiply with ins[operand] (operand -1: v itself) -- and, when
+// store_k >= 0, writes v to outs[store_k].  Every tensor has n floats.  The
+// per-element functions are the standalone kernels', so each stored value
+// has the bits the unfused layers would give it.
+constexpr int kFuseMax = 8;
+enum FuseKind : int32_t { kFuseGelu = 1, kFuseSilu = 2, kFuseAdd = 3, kFuseMul = 4 };
+struct FuseStep {
+    int32_t kind;
+    int32_t operand;
+    int32_t store;
+};
+struct FuseProgram {
+    const float* ins[kFuseMax];
+    float* outs[kFuseMax];
+    FuseStep steps[kFuseMax];
+    int32_t n_ins, n_outs, n_steps;
+};
+int fused_chain(mimir_ctx* ctx, const FuseProgram& p, int64_t n);
+
+// The runtime's fused LayerNorm (norm.hip): optionally an Add before it
+// (h = x + r, written to h when set) and a chain of elementwise steps after
+// it (epi, operands in epi.ins; y, when set, gets the LayerNorm output
+// itself).  rows x cols, gamma / beta as mimir_layernorm_fwd.
+struct LnFused {
+    const float* x;
+    const float* r;
+    float* h;
+    const float* g;
+    const float* b;
+    float* y;
+    int64_t rows, cols;
+    float eps;
+    FuseProgram epi;
+};
+// Whether the fused LayerNorm takes rows of `cols` floats with these
+// parameter pointers (the register-resident vector kernel).
+bool layernorm_fusable(const mimir_ctx* ctx, int64_t cols, const float* g, const float* b);
+int layernorm_fused(mimir_ctx* ctx, const LnFused& f);
+
 // Look up this context's device address of the no-allocation scratch array
 // (backward.hip); called once per context, with its device current.
 int noalloc_scratch_init(mimir_ctx* ctx);

@@ -22,12 +22,15 @@
 //              RMSNorm of h; h is also written out (the updated residual).
 #include "common.hpp"
 #include "internal.hpp"
+#include "pointwise.hpp"
 
 using namespace mimir;
 
 namespace {
 
-enum class Norm { Layer, Rms, AddRms };
+// AddLayer: the runtime's fused Add -> LayerNorm (h = x + r, written when
+// r_out is set, then LayerNorm of h).
+enum class Norm { Layer, Rms, AddRms, AddLayer };
 
 struct NormArgs {
     const float* x;
@@ -40,6 +43,10 @@ struct NormArgs {
     int64_t cols;
     int64_t w_len;    // RMSNorm: weight applies to columns < w_len
     float eps;
+    // LayerNorm epilogue (the runtime's fusion): a chain of elementwise
+    // steps on the normalised value before it is stored (y, when set, gets
+    // the LayerNorm output itself); operands index epi.ins.
+    FuseProgram epi;
 };
 
 // Scale by the RMSNorm weight where the column is below w_len.
@@ -56,8 +63,9 @@ __device__ __forceinline__ f4 rms_scale(f4 o, const float* w, int64_t w_len, int
 }
 
 // KEEP: y through the caches (mimir_ctx_set_output_caching); r_out is always
-// streamed (it is read by a later block, not the next op).
-template <Norm K, int TPR, int VPT, int BS, bool KEEP>
+// streamed (it is read by a later block, not the next op).  EPI: the
+// LayerNorm output goes through a.epi before it is stored.
+template <Norm K, int TPR, int VPT, int BS, bool KEEP, bool EPI = false>
 __global__ __launch_bounds__(BS) void norm_rows_vec(NormArgs a) {
     constexpr int RPB = BS / TPR;  // rows per workgroup
     constexpr int NW = TPR / kWave;  // waves per row
@@ -75,9 +83,10 @@ __global__ __launch_bounds__(BS) void norm_rows_vec(NormArgs a) {
 
     // LayerNorm: issue the row's loads at raised wave priority, so the loads
     // of resident rows are not held up behind other waves' reduction math.
-    if constexpr (K == Norm::Layer) __builtin_amdgcn_s_setprio(3);
+    constexpr bool kLayer = K == Norm::Layer || K == Norm::AddLayer;
+    if constexpr (kLayer) __builtin_amdgcn_s_setprio(3);
     f4 v[VPT];
-    if constexpr (K == Norm::AddRms) {
+    if constexpr (K == Norm::AddRms || K == Norm::AddLayer) {
         f4 rr[VPT];
 #pragma unroll
         for (int j = 0; j < VPT; ++j) {
@@ -90,7 +99,7 @@ __global__ __launch_bounds__(BS) void norm_rows_vec(NormArgs a) {
         for (int j = 0; j < VPT; ++j) {
             const int64_t c4 = static_cast<int64_t>(j) * TPR + t;
             v[j] = v[j] + rr[j];  // one IEEE add per element, as add_forward
-            if (c4 < c4n) st4<true>(a.r_out + base + 4 * c4, v[j]);
+            if (c4 < c4n && (K == Norm::AddRms || a.r_out)) st4<true>(a.r_out + base + 4 * c4, v[j]);
         }
     } else {
 #pragma unroll
@@ -100,10 +109,10 @@ __global__ __launch_bounds__(BS) void norm_rows_vec(NormArgs a) {
         }
     }
 
-    if constexpr (K == Norm::Layer) __builtin_amdgcn_s_setprio(0);
+    if constexpr (kLayer) __builtin_amdgcn_s_setprio(0);
 
     const float n = static_cast<float>(a.cols);
-    if constexpr (K == Norm::Layer) {
+    if constexpr (kLayer) {
         float s = 0.0f;
 #pragma unroll
         for (int j = 0; j < VPT; ++j) s += (v[j].x + v[j].y) + (v[j].z + v[j].w);
@@ -128,7 +137,26 @@ __global__ __launch_bounds__(BS) void norm_rows_vec(NormArgs a) {
                     o *= *reinterpret_cast<const f4*>(a.g + 4 * c4);
                     if (a.b) o += *reinterpret_cast<const f4*>(a.b + 4 * c4);
                 }
-                st_out<KEEP>(a.y + base + 4 * c4, o);
+                if constexpr (EPI) {
+                    const int64_t off = base + 4 * c4;
+                    const int ns = a.epi.n_steps;
+                    if (a.y) {
+                        if (ns == 0) st_out<KEEP>(a.y + off, o);
+                        else st4<true>(a.y + off, o);
+                    }
+                    for (int k = 0; k < ns; ++k) {
+                        const FuseStep st = a.epi.steps[k];
+                        const bool bin = st.kind == kFuseAdd || st.kind == kFuseMul;
+                        const f4 w = bin && st.operand >= 0 ? ld4<true>(a.epi.ins[st.operand] + off) : o;
+                        o = fuse_step4(st.kind, o, w);
+                        if (st.store >= 0) {
+                            if (k + 1 == ns) st_out<KEEP>(a.epi.outs[st.store] + off, o);
+                            else st4<true>(a.epi.outs[st.store] + off, o);
+                        }
+                    }
+                } else {
+                    st_out<KEEP>(a.y + base + 4 * c4, o);
+                }
             }
         }
     } else {
@@ -204,15 +232,26 @@ __global__ __launch_bounds__(kBlock) void norm_rows_generic(NormArgs a) {
     }
 }
 
-template <Norm K, int TPR, int VPT, int BS>
+template <Norm K, int TPR, int VPT, int BS, bool EPI = false>
 int launch_vec(mimir_ctx* ctx, const NormArgs& a) {
     unsigned blocks;
     if (!grid_for(a.rows, BS / TPR, &blocks))
         return fail(ctx, MIMIR_EINVAL, "norm: %lld rows exceed the grid limit", (long long)a.rows);
-    if (ctx->keep_outputs) norm_rows_vec<K, TPR, VPT, BS, true><<<blocks, BS, 0, ctx->stream>>>(a);
-    else norm_rows_vec<K, TPR, VPT, BS, false><<<blocks, BS, 0, ctx->stream>>>(a);
+    if (ctx->keep_outputs) norm_rows_vec<K, TPR, VPT, BS, true, EPI><<<blocks, BS, 0, ctx->stream>>>(a);
+    else norm_rows_vec<K, TPR, VPT, BS, false, EPI><<<blocks, BS, 0, ctx->stream>>>(a);
     return launched(ctx, "norm_rows_vec");
 }
+
+// The default LayerNorm shapes (rows.hpp default_norm_shape), the ones the
+// runtime's fused LayerNorm is compiled for.
+#define MIMIR_LN_FUSED_SHAPES(X) \
+    X(64, 1, 256)                \
+    X(128, 1, 256)               \
+    X(64, 4, 64)                 \
+    X(512, 1, 512)               \
+    X(512, 2, 512)               \
+    X(512, 4, 512)               \
+    X(1024, 4, 1024)
 
 // Rows the vector kernels cannot take (a width that is not a multiple of 4,
 // so rows start off 16-byte alignment, or unaligned pointers), up to
@@ -332,6 +371,28 @@ int dispatch(mimir_ctx* ctx, const NormArgs& a) {
 }
 
 }  // namespace
+
+bool mimir::layernorm_fusable(const mimir_ctx* ctx, int64_t cols, const float* g, const float* b) {
+    if (cols <= 0 || cols % 4 != 0 || (g && !aligned16(g)) || (b && !aligned16(b))) return false;
+    // With a LayerNorm shape override the unfused kernel would reduce in
+    // another order: keep the unfused path then, so both agree bit for bit.
+    if (shape_fits(ctx->tune.layernorm, cols / 4)) return false;
+    return default_layernorm_shape(cols / 4).tpr != 0;
+}
+
+int mimir::layernorm_fused(mimir_ctx* ctx, const LnFused& f) {
+    NormArgs a{f.x, f.r, f.h, f.g, f.b, f.y, f.rows, f.cols, f.cols, f.eps};
+    a.epi = f.epi;
+    if (f.rows == 0) return MIMIR_OK;
+    MIMIR_ENTER(ctx);
+    const RowShape s = default_layernorm_shape(f.cols / 4);
+#define MIMIR_LN_FUSED_CASE(T, V, B)                                                                  \
+    if (s.tpr == T && s.vpt == V && s.bs == B)                                                       \
+        return f.r ? launch_vec<Norm::AddLayer, T, V, B, true>(ctx, a) : launch_vec<Norm::Layer, T, V, B, true>(ctx, a);
+    MIMIR_LN_FUSED_SHAPES(MIMIR_LN_FUSED_CASE)
+#undef MIMIR_LN_FUSED_CASE
+    return fail(ctx, MIMIR_EINVAL, "fused LayerNorm: no row shape for %lld columns", (long long)f.cols);
+}
 
 extern "C" {
 

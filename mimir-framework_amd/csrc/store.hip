@@ -76,6 +76,7 @@ struct mimir_store {
     std::multimap<size_t, Buf*> free_bufs;  // capacity -> idle buffer
     // While a run is captured (mimir_store_capture): every buffer it acquires.
     std::vector<Buf*>* capture_log = nullptr;
+    int fuse = 0;  // mimir_store_set_fusion
     std::vector<mimir_store_graph*> graphs;  // alive captured graphs
 
     std::unordered_map<std::string, Slot>& map(int dtype) { return dtype == MIMIR_DTYPE_I32 ? i32 : f32; }
@@ -470,6 +471,227 @@ int run_layer(mimir_store* s, const mimir_layer& L, Snap* snap, bool ids_path = 
     return MIMIR_OK;
 }
 
+// Every layer but the last stores its output through the caches, where the
+// layer after it (the usual reader) finds much of it in L2 / the Infinity
+// Cache; the last layer's output is streamed, and the context's own setting
+// (mimir_ctx_set_output_caching) is restored on the way out.
+struct ChainOutputs {
+    mimir_ctx* ctx;
+    int saved;
+    explicit ChainOutputs(mimir_ctx* c) : ctx(c), saved(c->keep_outputs) {}
+    void layer(int32_t i, int32_t n) { ctx->keep_outputs = i + 1 < n && !ctx->tune.chain_streamed ? 1 : saved; }
+    ~ChainOutputs() { ctx->keep_outputs = saved; }
+};
+
+// Inference fusion (mimir_store_set_fusion): a run of consecutive
+// elementwise layers -- GELU, SiLU, and Add / Multiply of equal sizes --
+// each reading the previous one's output, runs as one kernel (fused_chain).
+// The second operand of an Add / Multiply must be a tensor bound when the
+// chain starts (not written inside it).  An intermediate output is written
+// only when a layer after the chain reads its name, or it is "x"; the others
+// are never materialised and their names are left unbound.  Values are the
+// unfused layers' bits (the same per-element functions, a + b = b + a).
+bool chain_type(int32_t t) {
+    return t == MIMIR_LAYER_GELU || t == MIMIR_LAYER_SILU || t == MIMIR_LAYER_ADD || t == MIMIR_LAYER_MULTIPLY;
+}
+
+std::string input_name(const mimir_layer& L, int k) {
+    if (L.n_inputs <= 0) return k == 0 ? "x" : "";
+    return k < L.n_inputs && L.inputs[k] ? L.inputs[k] : "";
+}
+
+std::string output_name(const mimir_layer& L) { return (L.output && *L.output) ? L.output : "x"; }
+
+// Extend a chain from layer j: consecutive elementwise layers each reading
+// the previous output (written.back()), the second operand of an Add /
+// Multiply bound in the store and not written by the group, all of n
+// floats.  Appends their steps to p (operands into p.ins) and their output
+// names to `written`; returns the first layer not taken.
+int32_t extend_chain(mimir_store* s, const mimir_layer* layers, int32_t j, int32_t n_layers, int64_t n,
+                     FuseProgram& p, std::vector<std::string>& written) {
+    auto kind_of = [](int32_t t) {
+        return t == MIMIR_LAYER_GELU ? kFuseGelu : t == MIMIR_LAYER_SILU ? kFuseSilu
+               : t == MIMIR_LAYER_ADD ? kFuseAdd : kFuseMul;
+    };
+    for (; j < n_layers && p.n_steps < kFuseMax; ++j) {
+        const mimir_layer& M = layers[j];
+        if (!chain_type(M.type)) break;
+        const std::string& cur = written.back();
+        FuseStep st{kind_of(M.type), -1, -1};
+        if (M.type == MIMIR_LAYER_GELU || M.type == MIMIR_LAYER_SILU) {
+            if (input_name(M, 0) != cur) break;
+        } else {
+            if (M.n_inputs < 2) break;
+            const std::string n0 = input_name(M, 0), n1 = input_name(M, 1);
+            if (!(n0 == cur && n1 == cur)) {
+                const std::string other = n0 == cur ? n1 : n1 == cur ? n0 : std::string();
+                if (other.empty() || p.n_ins >= kFuseMax) break;
+                if (std::find(written.begin(), written.end(), other) != written.end()) break;
+                auto it = s->f32.find(other);
+                if (it == s->f32.end() || it->second.n != n) break;
+                st.operand = p.n_ins;
+                p.ins[p.n_ins++] = static_cast<const float*>(it->second.buf->p);
+            }
+        }
+        p.steps[p.n_steps++] = st;
+        written.push_back(output_name(M));
+    }
+    return j;
+}
+
+// Whether output k of a fused group is written: the group's last; one a
+// layer after the group reads; "x" when the group does not write "x" again.
+bool materialise(const mimir_layer* layers, int32_t after, int32_t n_layers, const std::vector<std::string>& written,
+                 size_t k) {
+    const std::string& nm = written[k];
+    if (k + 1 == written.size()) return true;
+    for (int32_t q = after; q < n_layers; ++q) {
+        const mimir_layer& L = layers[q];
+        const int ni = L.n_inputs > 0 ? L.n_inputs : 1;
+        for (int t = 0; t < ni; ++t)
+            if (input_name(L, t) == nm) return true;
+    }
+    return nm == "x" && std::find(written.begin() + static_cast<long>(k) + 1, written.end(), nm) == written.end();
+}
+
+// Bind a fused group's outputs in layer order (a name written twice ends on
+// its last value); an output not materialised is unbound.
+void bind_group(mimir_store* s, const std::vector<std::string>& written, const std::vector<Buf*>& bufs, int64_t n) {
+    for (size_t k = 0; k < written.size(); ++k) {
+        if (Buf* b = bufs[k]) {
+            s->bind(MIMIR_DTYPE_F32, written[k], b, n);
+        } else {
+            auto it = s->f32.find(written[k]);
+            if (it != s->f32.end()) {
+                s->release(it->second.buf);
+                s->f32.erase(it);
+            }
+        }
+    }
+}
+
+int run_fused_chain(mimir_store* s, const mimir_layer* layers, int32_t i, int32_t n_layers, int32_t* end,
+                    ChainOutputs& chain) {
+    *end = i;
+    const mimir_layer& H = layers[i];
+    if (!chain_type(H.type)) return MIMIR_OK;
+    const bool bin = H.type == MIMIR_LAYER_ADD || H.type == MIMIR_LAYER_MULTIPLY;
+    if (bin && H.n_inputs < 2) return MIMIR_OK;
+    auto a = s->f32.find(input_name(H, 0));
+    if (a == s->f32.end() || a->second.n == 0) return MIMIR_OK;
+    const int64_t n = a->second.n;
+    FuseProgram p{};
+    p.ins[p.n_ins++] = static_cast<const float*>(a->second.buf->p);
+    FuseStep head{H.type == MIMIR_LAYER_GELU ? kFuseGelu : H.type == MIMIR_LAYER_SILU ? kFuseSilu
+                  : H.type == MIMIR_LAYER_ADD ? kFuseAdd : kFuseMul, -1, -1};
+    if (bin) {  // v = in0, then v op in1
+        auto b = s->f32.find(input_name(H, 1));
+        if (b == s->f32.end() || b->second.n != n) return MIMIR_OK;
+        head.operand = p.n_ins;
+        p.ins[p.n_ins++] = static_cast<const float*>(b->second.buf->p);
+    }
+    p.steps[p.n_steps++] = head;
+    std::vector<std::string> written{output_name(H)};
+    const int32_t j = extend_chain(s, layers, i + 1, n_layers, n, p, written);
+    if (written.size() < 2) return MIMIR_OK;
+    std::vector<Buf*> bufs(written.size(), nullptr);
+    for (size_t k = 0; k < written.size(); ++k) {
+        if (!materialise(layers, j, n_layers, written, k)) continue;
+        if (int st = s->acquire(static_cast<size_t>(n) * 4, &bufs[k])) {
+            for (Buf* b : bufs) s->discard(b);
+            return st;
+        }
+        p.steps[k].store = p.n_outs;
+        p.outs[p.n_outs++] = static_cast<float*>(bufs[k]->p);
+    }
+    chain.layer(j - 1, n_layers);  // a layer after the chain reads its output
+    if (int st = fused_chain(s->ctx, p, n)) {
+        for (Buf* b : bufs) s->discard(b);
+        return st;
+    }
+    bind_group(s, written, bufs, n);
+    *end = j;
+    return MIMIR_OK;
+}
+
+// The fused LayerNorm group: [Add ->] LayerNorm [-> elementwise chain], one
+// kernel (norm.hip layernorm_fused).  The Add (equal sizes) must feed the
+// LayerNorm; a LayerNorm with neither an Add before nor a chain after runs
+// unfused.  Checks the LayerNorm layer as run_layer does and leaves any
+// group it would refuse to the unfused path (which reports the error).
+int run_fused_norm(mimir_store* s, const mimir_layer* layers, int32_t i, int32_t n_layers, int32_t* end,
+                   ChainOutputs& chain) {
+    *end = i;
+    auto find = [&](const std::string& nm) -> const Slot* {
+        auto it = s->f32.find(nm);
+        return it == s->f32.end() ? nullptr : &it->second;
+    };
+    const mimir_layer& A = layers[i];
+    const Slot* xin = nullptr;
+    const Slot* rin = nullptr;
+    int32_t ln = i;
+    std::vector<std::string> written;
+    if (A.type == MIMIR_LAYER_ADD) {
+        if (i + 1 >= n_layers || A.n_inputs < 2) return MIMIR_OK;
+        const mimir_layer& L = layers[i + 1];
+        if (L.type != MIMIR_LAYER_LAYERNORM || input_name(L, 0) != output_name(A)) return MIMIR_OK;
+        xin = find(input_name(A, 0));
+        rin = find(input_name(A, 1));
+        if (!xin || !rin || xin->n != rin->n) return MIMIR_OK;
+        ln = i + 1;
+        written.push_back(output_name(A));
+    } else if (A.type == MIMIR_LAYER_LAYERNORM) {
+        xin = find(input_name(A, 0));
+        if (!xin) return MIMIR_OK;
+    } else {
+        return MIMIR_OK;
+    }
+    const mimir_layer& L = layers[ln];
+    const int64_t N = xin->n;
+    if (N == 0) return MIMIR_OK;
+    const int64_t nrm = L.in_features > 0 ? L.in_features : N;  // LayerOps.hpp:276-285
+    if (nrm <= 0 || N % nrm != 0) return MIMIR_OK;
+    const float* gamma = (L.affine && L.weights && L.weights_len > 0) ? L.weights : nullptr;
+    const float* beta = (gamma && L.use_bias) ? L.weights + nrm : nullptr;
+    if (gamma && L.weights_len < (beta ? 2 * nrm : nrm)) return MIMIR_OK;
+    if (!layernorm_fusable(s->ctx, nrm, gamma, beta)) return MIMIR_OK;
+    written.push_back(output_name(L));
+    const size_t first_epi = written.size();
+    LnFused f{};
+    const int32_t j = extend_chain(s, layers, ln + 1, n_layers, N, f.epi, written);
+    if (!rin && f.epi.n_steps == 0) return MIMIR_OK;  // a LayerNorm alone: the unfused kernel
+    std::vector<Buf*> bufs(written.size(), nullptr);
+    for (size_t k = 0; k < written.size(); ++k) {
+        if (!materialise(layers, j, n_layers, written, k)) continue;
+        if (int st = s->acquire(static_cast<size_t>(N) * 4, &bufs[k])) {
+            for (Buf* b : bufs) s->discard(b);
+            return st;
+        }
+        float* out = static_cast<float*>(bufs[k]->p);
+        if (rin && k == 0) f.h = out;
+        else if (k + 1 == first_epi) f.y = out;
+        else {
+            f.epi.steps[k - first_epi].store = f.epi.n_outs;
+            f.epi.outs[f.epi.n_outs++] = out;
+        }
+    }
+    f.x = static_cast<const float*>(xin->buf->p);
+    f.r = rin ? static_cast<const float*>(rin->buf->p) : nullptr;
+    f.g = gamma;
+    f.b = beta;
+    f.rows = N / nrm;
+    f.cols = nrm;
+    f.eps = L.eps;
+    chain.layer(j - 1, n_layers);
+    if (int st = layernorm_fused(s->ctx, f)) {
+        for (Buf* b : bufs) s->discard(b);
+        return st;
+    }
+    bind_group(s, written, bufs, N);
+    *end = j;
+    return MIMIR_OK;
+}
+
 // accumulate_grad's destination (Model.cpp:7329-7341): the gradient of
 // `name`, present (acc: add onto it) or new (written by the first
 // contribution).  A present gradient of another size is the reference's
@@ -739,27 +961,32 @@ int mimir_store_set_inputs(mimir_store* s, const char* const* fnames, const floa
     return MIMIR_OK;
 }
 
-// Every layer but the last stores its output through the caches, where the
-// layer after it (the usual reader) finds much of it in L2 / the Infinity
-// Cache; the last layer's output is streamed, and the context's own setting
-// (mimir_ctx_set_output_caching) is restored on the way out.
-struct ChainOutputs {
-    mimir_ctx* ctx;
-    int saved;
-    explicit ChainOutputs(mimir_ctx* c) : ctx(c), saved(c->keep_outputs) {}
-    void layer(int32_t i, int32_t n) { ctx->keep_outputs = i + 1 < n && !ctx->tune.chain_streamed ? 1 : saved; }
-    ~ChainOutputs() { ctx->keep_outputs = saved; }
-};
-
 int mimir_store_run(mimir_store* s, const mimir_layer* layers, int32_t n_layers) {
     if (!s) return MIMIR_EINVAL;
     MIMIR_REQUIRE(s->ctx, n_layers >= 0 && (n_layers == 0 || layers), "mimir_store_run: invalid argument");
     s->release_snaps();
     ChainOutputs chain(s->ctx);
-    for (int32_t i = 0; i < n_layers; ++i) {
+    for (int32_t i = 0; i < n_layers;) {
+        if (s->fuse) {
+            int32_t end = i;
+            if (int st = run_fused_norm(s, layers, i, n_layers, &end, chain)) return st;
+            if (end == i)
+                if (int st = run_fused_chain(s, layers, i, n_layers, &end, chain)) return st;
+            if (end > i) {
+                i = end;
+                continue;
+            }
+        }
         chain.layer(i, n_layers);
         if (int st = run_layer(s, layers[i], nullptr)) return st;
+        ++i;
     }
+    return MIMIR_OK;
+}
+
+int mimir_store_set_fusion(mimir_store* s, int enable) {
+    if (!s) return MIMIR_EINVAL;
+    s->fuse = enable ? 1 : 0;
     return MIMIR_OK;
 }
 

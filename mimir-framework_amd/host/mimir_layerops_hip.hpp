@@ -465,6 +465,11 @@ public:
     DeviceModel(const DeviceModel&) = delete;
     DeviceModel& operator=(const DeviceModel&) = delete;
 
+    // Inference fusion (mimir_store_set_fusion): groups of layers that feed
+    // each other run as one kernel; forwardPassNamed's "x" is unchanged bit
+    // for bit, intermediate tensors nothing reads are not kept.
+    void setFusion(bool enable) { ctx_->check(mimir_store_set_fusion(store_, enable ? 1 : 0), "DeviceModel fusion"); }
+
     // Upload every layer's weight block (Layer::getWeights / getWeightsSize);
     // call again after the host weights change.
     void syncWeights() {

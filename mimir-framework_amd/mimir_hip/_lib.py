@@ -150,6 +150,7 @@ SIGNATURES = {
     "mimir_store_grad_info": (c_int, [_P, c_char_p, _PP, POINTER(c_int64)]),
     "mimir_store_grad_get": (c_int, [_P, c_char_p, _P, c_int64, POINTER(c_int64)]),
     "mimir_store_capture": (c_int, [_P, POINTER(Layer_C), c_int32, POINTER(_P)]),
+    "mimir_store_set_fusion": (c_int, [_P, c_int]),
     "mimir_store_graph_launch": (c_int, [_P]),
     "mimir_store_graph_set_input": (c_int, [_P, c_char_p, c_int, _P, c_int64]),
     "mimir_store_graph_get": (c_int, [_P, c_char_p, c_int, _P, c_int64, POINTER(c_int64)]),

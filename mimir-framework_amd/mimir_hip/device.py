@@ -371,6 +371,10 @@ class Store:
         isz = (ctypes.c_int64 * max(1, ni))(*[v.size for v in iin.values()])
         self.ctx.check(self.ctx.lib.mimir_store_set_inputs(self.handle, fn, fd, fs, nf, inn, idd, isz, ni))
 
+    def set_fusion(self, enable=True):
+        """mimir_store_set_fusion: elementwise chains of a run as one kernel."""
+        self.ctx.check(self.ctx.lib.mimir_store_set_fusion(self.handle, int(bool(enable))))
+
     def run(self, graph: "DeviceGraph"):
         self.ctx.check(self.ctx.lib.mimir_store_run(self.handle, graph.c_layers, len(graph.layers)))
 

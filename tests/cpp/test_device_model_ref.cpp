@@ -312,6 +312,58 @@ void attention_block_model(mimir_hip::Context& c) {
     CHECK(normwise(dev_layers[1].grad_weights, m.getLayers()[1].grad_weights));  // dWqkv | dWout
 }
 
+// DeviceModel<Layer> with the runtime's fusion on: Add -> LayerNorm -> GELU
+// -> Multiply -> SiLU runs as one kernel.  Its "x" equals the unfused
+// device run bit for bit, and the reference Model to the LayerNorm's
+// tolerance (normwise 1e-5 of the largest output).
+void fused_block_model(mimir_hip::Context& c) {
+    const int rows = 16, feat = 256;
+    Model m;
+    m.push("res_add", "Add", 0);
+    m.push("ln", "LayerNorm", 2 * feat);
+    m.push("act", "GELU", 0);
+    m.push("gate", "Multiply", 0);
+    m.push("silu", "SiLU", 0);
+    auto& layers = m.getMutableLayers();
+    layers[0].inputs = {"inp", "res"};
+    layers[0].output = "h";
+    layers[1].inputs = {"h"};
+    layers[1].output = "n";
+    layers[1].in_features = feat;
+    layers[2].inputs = {"n"};
+    layers[2].output = "g";
+    layers[3].inputs = {"g", "gate"};
+    layers[3].output = "m";
+    layers[4].inputs = {"m"};
+    layers[4].output = "x";
+    m.allocateParams();
+    float* w = layers[1].getWeights();
+    for (int i = 0; i < feat; ++i) {
+        w[i] = 1.0f + 0.01f * static_cast<float>(i % 13);
+        w[feat + i] = 0.02f * static_cast<float>(i % 7) - 0.05f;
+    }
+    std::vector<float> inp(rows * feat), res(rows * feat), gate(rows * feat);
+    for (size_t i = 0; i < inp.size(); ++i) {
+        inp[i] = std::sin(0.37f * static_cast<float>(i));
+        res[i] = std::cos(0.11f * static_cast<float>(i)) * 0.5f;
+        gate[i] = std::sin(0.05f * static_cast<float>(i) + 1.0f);
+    }
+    const FMap fin{{"inp", inp}, {"res", res}, {"gate", gate}};
+    const std::vector<float> ref = m.forwardPassNamed(fin, IMap{}, false);
+    mimir_hip::DeviceModel<Layer> plain(c, m.getLayers());
+    mimir_hip::DeviceModel<Layer> fused(c, m.getLayers());
+    fused.setFusion(true);
+    const std::vector<float> a = plain.forwardPassNamed(fin, IMap{}, false);
+    const std::vector<float> b = fused.forwardPassNamed(fin, IMap{}, false);
+    CHECK(a.size() == ref.size() && b.size() == ref.size() &&
+          std::memcmp(a.data(), b.data(), a.size() * sizeof(float)) == 0);
+    float mx = 0.f;
+    for (float v : ref) mx = std::fmax(mx, std::fabs(v));
+    bool ok = !ref.empty();
+    for (size_t i = 0; ok && i < ref.size(); ++i) ok = std::fabs(b[i] - ref[i]) <= 1e-6f + 1e-5f * mx;
+    CHECK(ok);
+}
+
 }  // namespace
 
 int main() {
@@ -322,6 +374,7 @@ int main() {
         int_ids_forward(c);
         attention_at_call_site();
         attention_block_model(c);
+        fused_block_model(c);
     } catch (const std::exception& e) {
         std::fprintf(stderr, "FAIL: exception %s\n", e.what());
         return 1;

@@ -11,7 +11,11 @@ in both, since a later block reads it, not the next op).  The backward
 kernels and the device copy take the same parameter; the LayerNorm
 backward's dgamma/dbeta slot partials (ln_bwd_vec, and lr_bwd_apply over
 long rows, which also adds into dgamma / dbeta in place) are plain stores
-in both variants (the slot sums read them back next)."""
+in both variants (the slot sums read them back next).  The runtime's fused
+kernels (fused_chain_vec, and the LayerNorm with an epilogue) stream the
+intermediates a later layer reads and store only the group's last output
+by KEEP: the kept variant has both kinds of store, the streamed one only
+non-temporal stores."""
 import os
 import re
 import shutil
@@ -51,9 +55,20 @@ def test_keep_variants_store_as_intended(src, tmp_path):
     assert r.returncode == 0, r.stderr[-2000:]
     checked = 0
     for name, nt in _stores_by_kernel(out.read_text()).items():
-        keep = "Lb1EEEv" in name
-        if not nt or not (keep or "Lb0EEEv" in name):
-            continue  # not a KEEP-templated kernel, or one without vector stores
+        if not nt:
+            continue
+        norm = re.search(r"norm_rows_vec\S*Lb([01])ELb([01])EEEv", name)  # <..., KEEP, EPI>
+        chain = re.search(r"fused_chain_vecILb([01])E", name)
+        if (norm and norm.group(2) == "1") or chain:  # intermediates streamed; the last output by KEEP
+            checked += 1
+            if (norm or chain).group(1) == "1":
+                assert any(nt) and not all(nt), f"{name}: {nt}"
+            else:
+                assert all(nt), f"{name}: a streamed output lost its non-temporal hint"
+            continue
+        keep = norm.group(1) == "1" if norm else "Lb1EEEv" in name
+        if not (norm or keep or "Lb0EEEv" in name):
+            continue  # not a KEEP-templated kernel
         if src in ("backward", "runtime") and not any(k in name for k in KEEP_KERNELS):
             continue  # a bool template parameter that is not KEEP
         checked += 1
