@@ -428,14 +428,16 @@ def build_ops(rows_override=None):
     trn.nsets = lambda: 1
     ops.append(trn)
 
-    # Launch-bound: the small stack through the runtime, eager (a launch per
-    # kernel: 4 blocks x (2 LayerNorm, 3 GEMMs + the core, Add, GELU)) and as
-    # one captured graph replayed (mimir_store_capture / _graph_launch).
+    # Launch-bound: the small stack through the runtime with its fusion on
+    # (per block: LayerNorm, the attention layer's 2 GEMMs + core, then Add ->
+    # LayerNorm -> GELU as one kernel: 20 kernels), eager and as one captured
+    # graph replayed (mimir_store_capture / _graph_launch).
     def make_stack(captured):
         def make(ctx, nsets):
             layers, fin = small_stack()
             graph = M.DeviceGraph(ctx, layers)
             store = M.Store(ctx)
+            store.set_fusion(True)
             if captured:
                 sg = store.capture(graph, fin, {})
                 return (lambda i: sg.launch()), [[_Owned(sg, store, graph)]]
@@ -446,7 +448,8 @@ def build_ops(rows_override=None):
     sl, _ = small_stack()
     for key, captured in (("f1_stack_eager", False), ("f1_stack_graph", True)):
         op = OpBench(key, -1, f"runtime forward of a small transformer stack ({len(sl)} layers, [128x256], 4 "
-                     f"causal attention blocks), {'one captured graph launch' if captured else 'eager launches'}",
+                     f"causal attention blocks, fusion on), "
+                     f"{'one captured graph launch' if captured else 'eager launches'}",
                      "mimir_store_graph_launch" if captured else "mimir_store_run", 128 * 256 * f4, 128, "rows",
                      make_stack(captured))
         op.nsets = lambda: 1
