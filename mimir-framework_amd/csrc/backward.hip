@@ -25,15 +25,16 @@
 //                            width is not a multiple of 4
 //   ln_stats_generic, ln_bwd_params_part, ln_bwd_generic  any other width /
 //                            alignment
-//   embed_bwd_*              scatter-add of dy rows into the gradient table:
-//                            (id, token) pairs are sorted by id (stable radix
-//                            sort); an id with fewer than 32 tokens has its
+//   embed_sort_*, embed_bwd_* scatter-add of dy rows into the gradient table:
+//                            (id, token) pairs are sorted by id, stably (a
+//                            counting sort up to 64K tokens, rocPRIM's radix
+//                            sort above); an id with fewer than 32 tokens has its
 //                            rows added in token order by one workgroup --
 //                            the reference's sequence of float adds, bit for
 //                            bit -- and a more frequent id's rows are summed
 //                            in 32-token segments in parallel, then the
-//                            segments in order (deterministic, the
-//                            reference's sum to float32 rounding).
+//                            segment sums in a fixed grouping (deterministic,
+//                            the reference's sum to float32 rounding).
 #include "common.hpp"
 #include "internal.hpp"
 #include "ids.hpp"
@@ -41,6 +42,8 @@
 #include <math.h>
 #include <mutex>
 
+#include <rocprim/block/block_radix_sort.hpp>
+#include <rocprim/block/block_scan.hpp>
 #include <rocprim/device/device_radix_sort.hpp>
 #include <rocprim/iterator/counting_iterator.hpp>
 #include <rocprim/iterator/transform_iterator.hpp>
@@ -1117,14 +1120,33 @@ __device__ __forceinline__ int64_t run_end(const uint32_t* keys, int64_t i, int6
 // instead of one token after another: the run's positions are cut at the
 // multiples of kLongRun, embed_bwd_seg_partial sums each segment's dy rows
 // (token order) into a slot of partial rows, all segments at once, and
-// embed_bwd_seg_combine adds the run's slots in order onto the gradient row.
-// The result is deterministic; it is the reference's sequential sum
-// regrouped, so it agrees with it to the rounding of a float32 sum (the
-// path's tolerance for sums), not bit for bit.  Shorter runs stay with
-// embed_bwd_rows_vec, which adds in token order (bit-exact).
+// embed_bwd_seg_combine adds the run's slots onto the gradient row.  The
+// workgroup at a run's first segment also lists the run (id, head, end) for
+// the combine, whose grid then covers only the long runs.  The result is
+// deterministic; it is the reference's sequential sum regrouped, so it
+// agrees with it to the rounding of a float32 sum (the path's tolerance for
+// sums), not bit for bit.  Shorter runs stay with embed_bwd_rows_vec, which
+// adds in token order (bit-exact).
 constexpr int kLongRun = 32;
-constexpr int kLongSlices = 16;
 constexpr int kLongBatch = 16;
+
+// The long runs, appended in no fixed order (each entry's sum is fixed);
+// `count` is zeroed before the segment kernels run.
+struct LongRunEntry {
+    uint32_t id, head, end, pad;
+};
+struct LongRunList {
+    uint32_t* count;
+    LongRunEntry* runs;
+};
+__device__ __forceinline__ void list_long_run(const LongRunList& list, uint32_t id, int64_t head, int64_t end) {
+    const uint32_t j = atomicAdd(list.count, 1u);
+    list.runs[j] = LongRunEntry{id, static_cast<uint32_t>(head), static_cast<uint32_t>(end), 0u};
+}
+
+__global__ void zero_count_kernel(uint32_t* count) {
+    if (threadIdx.x == 0) *count = 0;
+}
 
 // The end of the run of `id` in the sorted keys, given a position j inside
 // it: the first position after j whose key differs, or n.  Each step the 64
@@ -1153,8 +1175,11 @@ __device__ __forceinline__ int64_t run_end_search(const uint32_t* keys, int64_t 
 // key, whether p is the run's first multiple of kLongRun (`first`), its head
 // (valid when `first`) and end.  `is_long` when it has kLongRun tokens or
 // more.  One ballot over positions p - kLongRun + 1 .. p finds the head of a
-// run that starts there; a run through p - kLongRun as well is long.  Must
-// be reached by all 64 lanes of the wave.
+// run that starts there; a run through p - kLongRun as well is long.  A
+// run of kLongRun tokens or more through p reaches p - kLongRun / 2 or
+// p + kLongRun / 2 (its extents on the two sides of p add up to at least
+// kLongRun - 1), so a run that reaches neither is short, known after the
+// first round trip.  Must be reached by all 64 lanes of the wave.
 struct LongRun {
     uint32_t id;
     bool first;
@@ -1164,8 +1189,11 @@ struct LongRun {
 };
 __device__ __forceinline__ LongRun long_run_at(const uint32_t* keys, int64_t p, int64_t n, uint32_t vocab) {
     LongRun r{keys[p], false, false, p, p + 1};
-    const uint32_t before = p >= kLongRun ? keys[p - kLongRun] : ~0u;  // loaded with the key: one round trip
-    if (r.id >= vocab) return r;
+    // Loaded with the key: one round trip.
+    const uint32_t before = p >= kLongRun ? keys[p - kLongRun] : ~0u;
+    const uint32_t left = p >= kLongRun / 2 ? keys[p - kLongRun / 2] : ~0u;
+    const uint32_t right = p + kLongRun / 2 < n ? keys[p + kLongRun / 2] : ~0u;
+    if (r.id >= vocab || (left != r.id && right != r.id)) return r;
     r.first = before != r.id;
     const int lane = threadIdx.x & (kWave - 1);
     if (r.first) {
@@ -1188,12 +1216,13 @@ constexpr int kSegCols = 256;
 constexpr int kSegRows = 16;
 __global__ __launch_bounds__(kSegCols) void embed_bwd_seg_partial(const uint32_t* keys, const uint32_t* toks,
                                                                   int64_t n, uint32_t vocab, const float* dy,
-                                                                  float* part, int64_t dim4) {
+                                                                  float* part, int64_t dim4, LongRunList list) {
     const int64_t m = blockIdx.x;
     const int64_t p = m * kLongRun;
     if (p >= n) return;
     const LongRun r = long_run_at(keys, p, n, vocab);
     if (!r.is_long) return;
+    if (r.first && blockIdx.y == 0 && threadIdx.x == 0) list_long_run(list, r.id, r.head, r.end);
     const int64_t c = static_cast<int64_t>(blockIdx.y) * kSegCols + threadIdx.x;
     if (c >= dim4) return;  // after the ballots of long_run_at
     const int64_t s0 = r.first ? r.head : p;
@@ -1218,37 +1247,64 @@ __global__ __launch_bounds__(kSegCols) void embed_bwd_seg_partial(const uint32_t
     reinterpret_cast<f4*>(part)[m * dim4 + c] = acc;
 }
 
-// Second level: the workgroup at the run's first multiple of kLongRun adds
-// the run's partial slots, in order, onto the id's gradient row; each of its
-// kLongSlices waves takes a slice of the 16-byte columns and keeps
-// kLongBatch slots' loads in flight.
-__global__ __launch_bounds__(kWave * kLongSlices) void embed_bwd_seg_combine(
-    const uint32_t* keys, int64_t n, uint32_t vocab, const float* part, float* grad, int64_t dim4) {
-    const int64_t m0 = blockIdx.x;
-    const int64_t p = m0 * kLongRun;
-    if (p >= n) return;
-    const LongRun r = long_run_at(keys, p, n, vocab);
-    if (!r.first || !r.is_long) return;
-    const int64_t m1 = (r.end - 1) / kLongRun + 1;  // slots m0 .. m1 - 1
+// Second level: work item (run, column block) adds the run's partial slots
+// onto kCombineCols 16-byte columns of the id's gradient row.  Each of the
+// workgroup's kCombineGroups waves sums every kCombineGroups-th slot
+// (kLongBatch loads in flight per lane); the first wave adds the groups'
+// sums, in group order, onto the gradient.  The grid strides over the
+// listed runs' items, so with no long run every workgroup leaves after one
+// load.
+constexpr int kCombineCols = kWave;
+constexpr int kCombineGroups = 4;
+constexpr int64_t kCombineGrid = 1024;
+__global__ __launch_bounds__(kWave * kCombineGroups) void embed_bwd_seg_combine(const uint32_t* count,
+                                                                                 const LongRunEntry* runs,
+                                                                                 const float* part, float* grad,
+                                                                                 int64_t dim4) {
+    __shared__ f4 sums[kCombineGroups - 1][kWave];
+    const int64_t blocks = (dim4 + kCombineCols - 1) / kCombineCols;
+    const int64_t items = static_cast<int64_t>(*count) * blocks;
+    const int grp = threadIdx.x / kWave;
     const int lane = threadIdx.x & (kWave - 1);
-    const int64_t slice = threadIdx.x / kWave;
-    const int64_t w = (dim4 + kLongSlices - 1) / kLongSlices;
-    const int64_t c1 = (slice + 1) * w < dim4 ? (slice + 1) * w : dim4;
     const f4* src = reinterpret_cast<const f4*>(part);
-    f4* g = reinterpret_cast<f4*>(grad) + static_cast<int64_t>(r.id) * dim4;
-    for (int64_t c = slice * w + lane; c < c1; c += kWave) {
-        f4 acc = __builtin_nontemporal_load(g + c);
-        int64_t j = m0;
-        for (; j + kLongBatch <= m1; j += kLongBatch) {
-            f4 v[kLongBatch];
+    for (int64_t it = blockIdx.x; it < items; it += gridDim.x) {
+        const LongRunEntry e = runs[it / blocks];
+        const int64_t c = (it % blocks) * kCombineCols + lane;
+        const int64_t m0 = (static_cast<int64_t>(e.head) + kLongRun - 1) / kLongRun;  // the run's first slot
+        const int64_t m1 = (static_cast<int64_t>(e.end) - 1) / kLongRun + 1;
+        f4* g = reinterpret_cast<f4*>(grad) + static_cast<int64_t>(e.id) * dim4;
+        f4 acc = {0.f, 0.f, 0.f, 0.f};
+        f4 gv = acc;
+        if (c < dim4) {
+            if (grp == 0) gv = __builtin_nontemporal_load(g + c);
+            bool started = false;
+            int64_t j = m0 + grp;
+            for (; j + (kLongBatch - 1) * kCombineGroups < m1; j += kLongBatch * kCombineGroups) {
+                f4 v[kLongBatch];
 #pragma unroll
-            for (int u = 0; u < kLongBatch; ++u) v[u] = src[(j + u) * dim4 + c];
-            __builtin_amdgcn_sched_barrier(0);
+                for (int u = 0; u < kLongBatch; ++u) v[u] = src[(j + u * kCombineGroups) * dim4 + c];
+                __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-            for (int u = 0; u < kLongBatch; ++u) acc += v[u];
+                for (int u = 0; u < kLongBatch; ++u) {
+                    acc = started ? acc + v[u] : v[u];
+                    started = true;
+                }
+            }
+            for (; j < m1; j += kCombineGroups) {
+                const f4 v = src[j * dim4 + c];
+                acc = started ? acc + v : v;
+                started = true;
+            }
         }
-        for (; j < m1; ++j) acc += src[j * dim4 + c];
-        __builtin_nontemporal_store(acc, g + c);
+        if (grp > 0) sums[grp - 1][lane] = acc;
+        __syncthreads();
+        if (grp == 0 && c < dim4) {
+            gv += acc;  // group 0 always holds slot m0
+            for (int q = 1; q < kCombineGroups; ++q)
+                if (m0 + q < m1) gv += sums[q - 1][lane];
+            __builtin_nontemporal_store(gv, g + c);
+        }
+        __syncthreads();  // sums is reused by the next item
     }
 }
 
@@ -1343,7 +1399,7 @@ __global__ __launch_bounds__(TPT) void embed_bwd_rows_vec(const uint32_t* keys, 
 constexpr int kMergedSegRows = 8;
 __global__ __launch_bounds__(1024, 8) void embed_bwd_rows_seg(const uint32_t* keys, const uint32_t* toks, int64_t n,
                                                                uint32_t vocab, const float* dy, float* grad,
-                                                               float* part, int64_t dim4) {
+                                                               float* part, int64_t dim4, LongRunList list) {
     const int64_t nslots = (n + kLongRun - 1) / kLongRun;
     if (blockIdx.x >= nslots) {
         embed_rows_position<1024, 1>(blockIdx.x - nslots, keys, toks, n, vocab, dy, grad, dim4, 1);
@@ -1354,6 +1410,7 @@ __global__ __launch_bounds__(1024, 8) void embed_bwd_rows_seg(const uint32_t* ke
     if (p >= n) return;
     const LongRun r = long_run_at(keys, p, n, vocab);
     if (!r.is_long) return;
+    if (r.first && threadIdx.x == 0) list_long_run(list, r.id, r.head, r.end);
     const int64_t s0 = r.first ? r.head : p;
     const int64_t s1 = p + kLongRun < r.end ? p + kLongRun : r.end;
     const f4* src = reinterpret_cast<const f4*>(dy);
@@ -1395,6 +1452,171 @@ __global__ __launch_bounds__(kBlock) void embed_bwd_rows_scalar(const uint32_t* 
 
 size_t align256(size_t b) { return (b + 255) & ~size_t(255); }
 
+// ---- The (id, token) sort as a counting sort ------------------------------
+// Tokens are cut into blocks of kSortBlock.  A token's sorted position is
+//   (tokens with a smaller key) + (tokens of earlier blocks with its key)
+//   + (tokens earlier in its own block with its key),
+// which is exactly the stable sort's order, so the result equals the radix
+// sort's bit for bit.  Three launches:
+//   embed_sort_count    per block: a stable sort of its keys in LDS gives
+//                       each token's rank among its block's tokens of the
+//                       same key, and the block's row of per-key counts
+//                       (16-bit, every row zeroed by its block first)
+//   embed_sort_offsets  per key: the counts over the blocks turned into each
+//                       block's start (the key's offset within its chunk of
+//                       kSortChunk keys plus the earlier blocks' counts),
+//                       and each chunk's total
+//   embed_sort_scatter  per token: the chunk prefix (scanned in LDS) + its
+//                       block's start for its key + its rank
+// Used up to kSortMaxBlocks blocks and kSortMaxTable count entries; above
+// that the rocPRIM radix sort below.
+constexpr int kSortBlock = 1024;
+constexpr int64_t kSortMaxBlocks = 64;
+constexpr int64_t kSortMaxTable = int64_t(1) << 24;
+constexpr int kSortChunk = 256;  // keys per workgroup of embed_sort_offsets
+constexpr int64_t kSortMaxKeys = int64_t(kSortBlock) * kSortChunk;  // chunk totals scanned by one workgroup
+
+template <int MODE>
+__global__ __launch_bounds__(kSortBlock) void embed_sort_count(const void* ids, int64_t n, int32_t vocab, int32_t pad,
+                                                               uint32_t end_bit, uint16_t* cnt, int64_t pitch,
+                                                               uint16_t* rank, uint32_t* zero) {
+    using Sort = rocprim::block_radix_sort<uint32_t, kSortBlock, 1, uint32_t>;
+    using Scan = rocprim::block_scan<uint32_t, kSortBlock>;
+    __shared__ union {
+        typename Sort::storage_type sort;
+        typename Scan::storage_type scan;
+    } st;
+    __shared__ uint32_t sk[kSortBlock];
+    const int64_t b = blockIdx.x;
+    const int i = threadIdx.x;
+    // This block's row of counts: zeroed here, the runs' counts stored after
+    // the barriers below.
+    uint4* row = reinterpret_cast<uint4*>(cnt + b * pitch);
+    for (int64_t c = i; c < pitch / 8; c += kSortBlock) row[c] = uint4{0, 0, 0, 0};
+    if (zero && b == 0 && i == 0) *zero = 0;  // a counter of the kernels after the sort
+    const uint32_t v1 = static_cast<uint32_t>(vocab) + 1;  // keys 0 .. vocab; v1 pads the last block
+    const int64_t t = b * kSortBlock + i;
+    uint32_t key[1] = {v1};
+    uint32_t idx[1] = {static_cast<uint32_t>(i)};
+    if (t < n) key[0] = EmbedKey<MODE>{ids, vocab, pad}(t);
+    Sort().sort(key, idx, st.sort, 0u, end_bit);  // LSD radix sort: stable, equal keys keep token order
+    const uint32_t k = key[0];
+    sk[i] = k;
+    __syncthreads();  // sk complete; the sort's storage free for the scan
+    const bool head = i == 0 || sk[i - 1] != k;
+    const bool tail = i == kSortBlock - 1 || sk[i + 1] != k;
+    uint32_t start = 0;
+    Scan().inclusive_scan(head ? static_cast<uint32_t>(i) : 0u, start, st.scan, rocprim::maximum<uint32_t>());
+    if (k >= v1) return;
+    rank[b * kSortBlock + idx[0]] = static_cast<uint16_t>(i - start);
+    if (tail) cnt[b * pitch + k] = static_cast<uint16_t>(i - start + 1);
+}
+
+__global__ __launch_bounds__(kSortChunk) void embed_sort_offsets(const uint16_t* cnt, int64_t nb, int64_t v1,
+                                                                 int64_t pitch, uint32_t* start, uint32_t* chunk) {
+    using Scan = rocprim::block_scan<uint32_t, kSortChunk>;
+    __shared__ typename Scan::storage_type st;
+    const int64_t k = static_cast<int64_t>(blockIdx.x) * kSortChunk + threadIdx.x;
+    uint32_t tot = 0;
+    if (k < v1) {
+        int64_t b = 0;
+        for (; b + 8 <= nb; b += 8) {
+            uint32_t v[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) v[u] = cnt[(b + u) * pitch + k];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) tot += v[u];
+        }
+        for (; b < nb; ++b) tot += cnt[b * pitch + k];
+    }
+    uint32_t run = 0, total = 0;
+    Scan().exclusive_scan(tot, run, 0u, total, st, rocprim::plus<uint32_t>());
+    if (threadIdx.x == 0) chunk[blockIdx.x] = total;
+    if (k >= v1) return;
+    int64_t b = 0;  // the counts again, from L2
+    for (; b + 8 <= nb; b += 8) {
+        uint32_t v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) v[u] = cnt[(b + u) * pitch + k];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            start[(b + u) * pitch + k] = run;
+            run += v[u];
+        }
+    }
+    for (; b < nb; ++b) {
+        start[b * pitch + k] = run;
+        run += cnt[b * pitch + k];
+    }
+}
+
+template <int MODE>
+__global__ __launch_bounds__(kSortBlock) void embed_sort_scatter(const void* ids, int64_t n, int32_t vocab,
+                                                                 int32_t pad, const uint32_t* start, int64_t pitch,
+                                                                 const uint16_t* rank, const uint32_t* chunk,
+                                                                 int64_t nchunks, uint32_t* skeys, uint32_t* stoks) {
+    using Scan = rocprim::block_scan<uint32_t, kSortBlock>;
+    __shared__ typename Scan::storage_type st;
+    __shared__ uint32_t cpre[kSortBlock];
+    const int64_t b = blockIdx.x;
+    const int64_t t = b * kSortBlock + threadIdx.x;
+    const uint32_t c = threadIdx.x < nchunks ? chunk[threadIdx.x] : 0u;
+    const uint32_t k = t < n ? EmbedKey<MODE>{ids, vocab, pad}(t) : 0u;  // loaded beside the chunk totals
+    uint32_t cp = 0;
+    Scan().exclusive_scan(c, cp, 0u, st, rocprim::plus<uint32_t>());
+    cpre[threadIdx.x] = cp;
+    __syncthreads();
+    if (t >= n) return;
+    const uint32_t pos = cpre[k / kSortChunk] + start[b * pitch + k] + rank[t];
+    if (pos >= n) return;  // cannot happen when the counts are consistent; keeps a fault out regardless
+    skeys[pos] = k;
+    stoks[pos] = static_cast<uint32_t>(t);
+}
+
+struct CountSortPlan {
+    bool ok = false;
+    int64_t nb = 0, v1 = 0, pitch = 0, nchunks = 0;
+    uint32_t end_bit = 0;
+    size_t cnt_bytes = 0, start_bytes = 0, rank_bytes = 0, chunk_bytes = 0;
+    size_t bytes() const { return cnt_bytes + start_bytes + rank_bytes + chunk_bytes; }
+};
+
+CountSortPlan count_sort_plan(int64_t n, int32_t vocab) {
+    CountSortPlan p;
+    p.nb = (n + kSortBlock - 1) / kSortBlock;
+    p.v1 = static_cast<int64_t>(vocab) + 1;
+    p.pitch = (p.v1 + 7) / 8 * 8;  // 16-byte rows of counts, zeroed with 16-byte stores
+    p.nchunks = (p.v1 + kSortChunk - 1) / kSortChunk;
+    uint32_t bits = 1;
+    while (bits < 32 && (static_cast<uint64_t>(p.v1) >> bits) != 0) ++bits;  // the padding key v1 included
+    p.end_bit = bits;
+    p.ok = p.nb <= kSortMaxBlocks && p.nb * p.pitch <= kSortMaxTable && p.v1 <= kSortMaxKeys;
+    p.cnt_bytes = align256(sizeof(uint16_t) * static_cast<size_t>(p.nb * p.pitch));
+    p.start_bytes = align256(sizeof(uint32_t) * static_cast<size_t>(p.nb * p.pitch));
+    p.rank_bytes = align256(sizeof(uint16_t) * static_cast<size_t>(p.nb * kSortBlock));
+    p.chunk_bytes = align256(sizeof(uint32_t) * static_cast<size_t>(p.nchunks));
+    return p;
+}
+
+template <int MODE>
+int count_sort(mimir_ctx* ctx, const CountSortPlan& p, const void* ids, int64_t n, int32_t vocab, int32_t pad,
+               char* temp, uint32_t* skeys, uint32_t* stoks, uint32_t* zero) {
+    uint16_t* cnt = reinterpret_cast<uint16_t*>(temp);
+    uint32_t* start = reinterpret_cast<uint32_t*>(temp + p.cnt_bytes);
+    uint16_t* rank = reinterpret_cast<uint16_t*>(temp + p.cnt_bytes + p.start_bytes);
+    uint32_t* chunk = reinterpret_cast<uint32_t*>(temp + p.cnt_bytes + p.start_bytes + p.rank_bytes);
+    const unsigned nb = static_cast<unsigned>(p.nb);
+    embed_sort_count<MODE><<<nb, kSortBlock, 0, ctx->stream>>>(ids, n, vocab, pad, p.end_bit, cnt, p.pitch, rank,
+                                                               zero);
+    if (int st = launched(ctx, "embed_sort_count")) return st;
+    embed_sort_offsets<<<static_cast<unsigned>(p.nchunks), kSortChunk, 0, ctx->stream>>>(cnt, p.nb, p.v1, p.pitch,
+                                                                                       start, chunk);
+    if (int st = launched(ctx, "embed_sort_offsets")) return st;
+    embed_sort_scatter<MODE><<<nb, kSortBlock, 0, ctx->stream>>>(ids, n, vocab, pad, start, p.pitch, rank, chunk,
+                                                                 p.nchunks, skeys, stoks);
+    return launched(ctx, "embed_sort_scatter");
+}
+
 // The (id, token) sort.  Below rocPRIM's merge-sort limit (2^20 pairs) its
 // device radix sort is a block sort followed by merge passes; 8192-pair
 // blocks (512 threads x 16) need two passes at 32768 tokens.  Measured on
@@ -1423,28 +1645,49 @@ int embed_bwd(mimir_ctx* ctx, const void* ids, int64_t n_ids, const float* dy, f
     const auto keys = rocprim::make_transform_iterator(rocprim::counting_iterator<int64_t>(0),
                                                        EmbedKey<MODE>{ids, vocab, pad});
     const rocprim::counting_iterator<uint32_t> toks(0);
+    const CountSortPlan plan = count_sort_plan(n_ids, vocab);
+    const bool counting = plan.ok && ctx->tune.embed_bwd_sort != 0;
     size_t sort_bytes = 0;
-    hipError_t e = rocprim::radix_sort_pairs<EmbedSortConfig>(nullptr, sort_bytes, keys,
-                                                              static_cast<uint32_t*>(nullptr), toks,
-                                                              static_cast<uint32_t*>(nullptr), n, 0u, end_bit,
-                                                              ctx->stream);
-    if (e != hipSuccess) return hip_fail(ctx, e, "radix_sort_pairs (size)");
+    hipError_t e = hipSuccess;
+    if (counting) {
+        sort_bytes = plan.bytes();
+    } else {
+        e = rocprim::radix_sort_pairs<EmbedSortConfig>(nullptr, sort_bytes, keys, static_cast<uint32_t*>(nullptr),
+                                                       toks, static_cast<uint32_t*>(nullptr), n, 0u, end_bit,
+                                                       ctx->stream);
+        if (e != hipSuccess) return hip_fail(ctx, e, "radix_sort_pairs (size)");
+    }
     const size_t vbytes = align256(sizeof(uint32_t) * n);
     const bool vec = (dim % 4) == 0 && aligned16(dy) && aligned16(grad);
     const bool long_runs = vec && n_ids >= kLongRun;
     // Partial rows of the long runs' segments: one slot per kLongRun positions.
     const int64_t nslots = (n_ids + kLongRun - 1) / kLongRun;
     const size_t part_bytes = long_runs ? align256(sizeof(float) * static_cast<size_t>(nslots) * dim) : 0;
+    // The long-run list: its count, then at most one entry per slot.
+    const size_t list_bytes = long_runs ? 256 + align256(sizeof(LongRunEntry) * static_cast<size_t>(nslots)) : 0;
     void* s = nullptr;
-    if (int st = ensure_scratch(ctx, 2 * vbytes + part_bytes + align256(sort_bytes), &s)) return st;
+    if (int st = ensure_scratch(ctx, 2 * vbytes + part_bytes + list_bytes + align256(sort_bytes), &s)) return st;
     char* base = static_cast<char*>(s);
     uint32_t* skeys = reinterpret_cast<uint32_t*>(base);
     uint32_t* stoks = reinterpret_cast<uint32_t*>(base + vbytes);
     float* part = reinterpret_cast<float*>(base + 2 * vbytes);
-    void* temp = base + 2 * vbytes + part_bytes;
-    e = rocprim::radix_sort_pairs<EmbedSortConfig>(temp, sort_bytes, keys, skeys, toks, stoks, n, 0u, end_bit,
-                                                   ctx->stream);
-    if (e != hipSuccess) return hip_fail(ctx, e, "radix_sort_pairs");
+    LongRunList list{nullptr, nullptr};
+    if (long_runs) {
+        list.count = reinterpret_cast<uint32_t*>(base + 2 * vbytes + part_bytes);
+        list.runs = reinterpret_cast<LongRunEntry*>(base + 2 * vbytes + part_bytes + 256);
+    }
+    char* temp = base + 2 * vbytes + part_bytes + list_bytes;
+    if (counting) {  // embed_sort_count zeroes the list's count
+        if (int st = count_sort<MODE>(ctx, plan, ids, n_ids, vocab, pad, temp, skeys, stoks, list.count)) return st;
+    } else {
+        e = rocprim::radix_sort_pairs<EmbedSortConfig>(temp, sort_bytes, keys, skeys, toks, stoks, n, 0u, end_bit,
+                                                       ctx->stream);
+        if (e != hipSuccess) return hip_fail(ctx, e, "radix_sort_pairs");
+        if (long_runs) {
+            zero_count_kernel<<<1, kWave, 0, ctx->stream>>>(list.count);
+            if (int st = launched(ctx, "zero_count_kernel")) return st;
+        }
+    }
     if (vec) {
         const uint32_t v = static_cast<uint32_t>(vocab);
         const int64_t dim4 = dim / 4;
@@ -1456,14 +1699,15 @@ int embed_bwd(mimir_ctx* ctx, const void* ids, int64_t n_ids, const float* dy, f
         const bool merged = long_runs && tpt == 1024 && n_ids + nslots <= 0x7fffffffLL &&
                             ctx->tune.embed_bwd_merged != 0;
         if (merged) {
-            embed_bwd_rows_seg<<<static_cast<unsigned>(n_ids + nslots), 1024, 0, ctx->stream>>>(skeys, stoks, n_ids,
-                                                                                             v, dy, grad, part, dim4);
+            embed_bwd_rows_seg<<<static_cast<unsigned>(n_ids + nslots), 1024, 0, ctx->stream>>>(
+                skeys, stoks, n_ids, v, dy, grad, part, dim4, list);
             if (int st = launched(ctx, "embed_bwd_rows_seg")) return st;
         } else {
             if (long_runs) {
                 const dim3 pgrid(static_cast<unsigned>(nslots),
                                  static_cast<unsigned>((dim4 + kSegCols - 1) / kSegCols));
-                embed_bwd_seg_partial<<<pgrid, kSegCols, 0, ctx->stream>>>(skeys, stoks, n_ids, v, dy, part, dim4);
+                embed_bwd_seg_partial<<<pgrid, kSegCols, 0, ctx->stream>>>(skeys, stoks, n_ids, v, dy, part, dim4,
+                                                                           list);
                 if (int st = launched(ctx, "embed_bwd_seg_partial")) return st;
             }
             if (tpt == 256)
@@ -1475,9 +1719,13 @@ int embed_bwd(mimir_ctx* ctx, const void* ids, int64_t n_ids, const float* dy, f
             if (int st = launched(ctx, "embed_bwd_rows_vec")) return st;
         }
         if (!long_runs) return MIMIR_OK;
-        // The long runs' segment partials are complete (stream order): add them.
-        embed_bwd_seg_combine<<<static_cast<unsigned>(nslots), kWave * kLongSlices, 0, ctx->stream>>>(
-            skeys, n_ids, v, part, grad, dim4);
+        // The long runs' segment partials are complete and listed (stream
+        // order): add them.  At most nslots runs of `blocks` items each.
+        const int64_t blocks = (dim4 + kCombineCols - 1) / kCombineCols;
+        const int64_t items = nslots * blocks;
+        const unsigned cgrid = static_cast<unsigned>(items < kCombineGrid ? items : kCombineGrid);
+        embed_bwd_seg_combine<<<cgrid, kWave * kCombineGroups, 0, ctx->stream>>>(list.count, list.runs, part, grad,
+                                                                                 dim4);
         return launched(ctx, "embed_bwd_seg_combine");
     }
     embed_bwd_rows_scalar<<<n, kBlock, 0, ctx->stream>>>(skeys, stoks, n_ids, static_cast<uint32_t>(vocab), dy,

@@ -9,6 +9,8 @@ the same bound relative to the magnitudes summed (float32 sums in another
 order differ by ~u * that); Multiply / Add gradients and accumulate_grad bit
 for bit; the Embedding scatter-add bit for bit for ids with fewer than 32
 tokens, and for more frequent ids (summed in segments) as a gradient sum."""
+import os
+
 import numpy as np
 import pytest
 
@@ -358,12 +360,13 @@ def test_embedding_bwd_repeats(ctx, case):
 @pytest.mark.parametrize("case", ["zipf ids, dim 4096", "runs around the long-run threshold, dim 132"])
 def test_embedding_bwd_long_runs(ctx, case):
     """Ids with 32 tokens or more: their rows are summed in 32-token segments
-    (segments cut at multiples of 32 in sorted order), then the segments in
-    order onto the gradient row, by column slices on 16 workgroups.  Zipf(1.0)
+    (segments cut at multiples of 32 in sorted order), then the segment sums
+    onto the gradient row in four slot groups per 64-column block.  Zipf(1.0)
     ids are what a text batch looks like (the top id is ~9% of the tokens);
     the second case puts runs of 1, 31, 32, 33, 63, 64, 65 and 200 tokens next
-    to each other, with 33 16-byte columns per row (uneven slices, the last one
-    partial).  Rarer ids stay bit-exact; two calls give the same bits."""
+    to each other, with 33 16-byte columns per row (a partial column block,
+    runs of 1 to 7 slots).  Rarer ids stay bit-exact; two calls give the same
+    bits."""
     if case.startswith("zipf"):
         vocab, dim, n = 2000, 4096, 8192
         r = np.arange(1, vocab + 1, dtype=np.float64) ** -1.0
@@ -381,6 +384,60 @@ def test_embedding_bwd_long_runs(ctx, case):
     assert_bitexact(_embedding_bwd_gpu(ctx, ids, dy, gt, vocab, dim, -1), got, case + ", second call")
     counts, _ = _scatter_counts_scale(ids, dy, gt, vocab, dim, -1)
     assert (counts >= 32).any() and (counts < 32).any()  # both paths ran
+
+
+@pytest.fixture(scope="module")
+def radix_ctx():
+    """A context whose Embedding backward sorts with rocPRIM's radix sort
+    (MIMIR_TUNE embsort=0) instead of the counting sort."""
+    old = os.environ.get("MIMIR_TUNE")
+    os.environ["MIMIR_TUNE"] = "embsort=0"
+    try:
+        c = M.Context(0)
+    finally:
+        if old is None:
+            del os.environ["MIMIR_TUNE"]
+        else:
+            os.environ["MIMIR_TUNE"] = old
+    yield c
+    c.close()
+
+
+@pytest.mark.parametrize("vocab,n,dist,float_ids", [
+    (32000, 32768, "uniform", False), (32000, 32768, "zipf", False), (32000, 32768, "uniform", True),
+    (1023, 65536, "uniform", False), (1024, 65535, "zipf", False), (1025, 1025, "uniform", True),
+    (1, 3000, "uniform", False), (70000, 4097, "uniform", False), (32000, 65537, "uniform", False),
+    (5, 1024, "one id", False)])
+def test_embedding_bwd_counting_sort_matches_radix_sort(ctx, radix_ctx, vocab, n, dist, float_ids):
+    """The counting sort (up to 64 blocks of 1024 tokens) puts every (id,
+    token) pair where the stable radix sort does, so the gradients are the
+    same bits: chunk edges of the key scan (vocab + 1 around 1024), padding
+    and out-of-range ids (the skipped key), a last partial block, the
+    64-block limit and just past it (the radix sort on both sides)."""
+    dim = 64
+    if dist == "zipf":
+        r = np.arange(1, vocab + 1, dtype=np.float64) ** -1.0
+        ids = rng.choice(vocab, n, p=r / r.sum()).astype(np.int32)
+    elif dist == "one id":
+        ids = np.full(n, 3, np.int32)
+    else:
+        ids = rng.integers(-2, vocab + 2, n).astype(np.int32)
+    pad = 1 if vocab > 1 else -1
+    arg = ids.astype(np.float32) + np.float32(0.25) if float_ids else ids
+    dy = rng.standard_normal((n, dim)).astype(np.float32)
+    gt = rng.standard_normal(vocab * dim).astype(np.float32)
+    got = {}
+    for name, c in (("counting", ctx), ("radix", radix_ctx)):
+        bi, bdy, bg = c.to_device(arg), c.to_device(dy), c.to_device(gt)
+        try:
+            c.embedding_bwd(bi, n, bdy, bg, gt.size, vocab, dim, pad, float_ids=float_ids)
+            got[name] = bg.numpy()
+        finally:
+            for d in (bi, bdy, bg):
+                d.free()
+    assert_bitexact(got["counting"], got["radix"], f"{dist} ids, vocab {vocab}, {n} tokens")
+    ref = O.embedding_bwd(arg, dy, gt, vocab, dim, pad)
+    _check_scatter(got["counting"], ref, arg, dy, gt, vocab, dim, pad, "grad table")
 
 
 def test_embedding_bwd_unaligned_rows_and_errors(ctx):
