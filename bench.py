@@ -351,7 +351,9 @@ def build_ops(rows_override=None):
         u = int(np.unique(ids_).size)
         top = int(np.bincount(ids_.ravel()).max())
         ops.append(OpBench(key, 3, f"Embedding backward (scatter-add) {what} -> table grad [32000x4096], "
-                           f"{u} distinct ids, longest run {top}", "radix sort + embed_bwd_rows_vec (runs, segment partials) + embed_bwd_seg_combine",
+                           f"{u} distinct ids, longest run {top}",
+                           "counting sort (embed_sort_count / _offsets / _scatter) + embed_bwd_rows_seg (runs, "
+                           "segment partials, long-run list) + embed_bwd_seg_combine",
                            32768 * 4 + 32768 * 4096 * f4 + 2 * u * 4096 * f4, 32768, "token rows", make_embb(ids_fn),
                            lambda s: {"grad": s[-1][0]}))
 
