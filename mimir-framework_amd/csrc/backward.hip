@@ -1318,31 +1318,29 @@ __global__ __launch_bounds__(kWave * kCombineGroups) void embed_bwd_seg_combine(
 // time, then added in token order.  Most workgroups leave at once, so the
 // kernel is kept small in registers: two 1024-thread workgroups fit a CU.
 constexpr int kRunBatch = 4;
+
+// The first token's row and the gradient row, for the CPT columns of this
+// thread that start at c0.
 template <int TPT, int CPT>
-__device__ __forceinline__ void embed_rows_position(int64_t i, const uint32_t* keys, const uint32_t* toks, int64_t n,
-                                                    uint32_t vocab, const float* dy, float* grad, int64_t dim4,
-                                                    int long_runs) {
-    const uint32_t id = keys[i];
-    const uint32_t t0 = toks[i];
-    if (id >= vocab || (i > 0 && keys[i - 1] == id)) return;  // not a run's head
-    const f4* src = reinterpret_cast<const f4*>(dy);
-    f4* g = reinterpret_cast<f4*>(grad) + static_cast<int64_t>(id) * dim4;
-    f4 acc[CPT], v[CPT];
-    auto load_group = [&](int64_t c0) {
+__device__ __forceinline__ void embed_rows_load(const f4* g, const f4* src, uint32_t t0, int64_t c0, int64_t dim4,
+                                                f4 (&acc)[CPT], f4 (&v)[CPT]) {
 #pragma unroll
-        for (int k = 0; k < CPT; ++k) {
-            const int64_t c = c0 + static_cast<int64_t>(k) * TPT;
-            if (c < dim4) {
-                acc[k] = __builtin_nontemporal_load(g + c);
-                v[k] = __builtin_nontemporal_load(src + static_cast<int64_t>(t0) * dim4 + c);
-            }
+    for (int k = 0; k < CPT; ++k) {
+        const int64_t c = c0 + static_cast<int64_t>(k) * TPT;
+        if (c < dim4) {
+            acc[k] = __builtin_nontemporal_load(g + c);
+            v[k] = __builtin_nontemporal_load(src + static_cast<int64_t>(t0) * dim4 + c);
         }
-    };
+    }
+}
+
+// The run at sorted positions i .. end - 1 (first token t0, its row and the
+// gradient row already loaded for columns from threadIdx.x): adds the rows
+// in token order onto the gradient row, column group by column group.
+template <int TPT, int CPT>
+__device__ __forceinline__ void embed_rows_sum(int64_t i, int64_t end, uint32_t t0, const uint32_t* toks,
+                                               const f4* src, f4* g, int64_t dim4, f4 (&acc)[CPT], f4 (&v)[CPT]) {
     int64_t c0 = threadIdx.x;
-    load_group(c0);
-    if (long_runs && i + kLongRun <= n && keys[i + kLongRun - 1] == id) return;  // a long run: segments
-    // Every lane of the wave takes part in the ballots of run_end.
-    const int64_t end = run_end(keys, i, n, id);
     while (c0 < dim4) {
 #pragma unroll
         for (int k = 0; k < CPT; ++k) acc[k] += v[k];
@@ -1374,15 +1372,63 @@ __device__ __forceinline__ void embed_rows_position(int64_t i, const uint32_t* k
             if (c < dim4) __builtin_nontemporal_store(acc[k], g + c);
         }
         c0 += static_cast<int64_t>(TPT) * CPT;
-        if (c0 < dim4) load_group(c0);
+        if (c0 < dim4) embed_rows_load<TPT, CPT>(g, src, t0, c0, dim4, acc, v);
     }
 }
 
 template <int TPT, int CPT>
+__device__ __forceinline__ void embed_rows_position(int64_t i, const uint32_t* keys, const uint32_t* toks, int64_t n,
+                                                    uint32_t vocab, const float* dy, float* grad, int64_t dim4,
+                                                    int long_runs) {
+    const uint32_t id = keys[i];
+    const uint32_t t0 = toks[i];
+    if (id >= vocab || (i > 0 && keys[i - 1] == id)) return;  // not a run's head
+    const f4* src = reinterpret_cast<const f4*>(dy);
+    f4* g = reinterpret_cast<f4*>(grad) + static_cast<int64_t>(id) * dim4;
+    f4 acc[CPT], v[CPT];
+    embed_rows_load<TPT, CPT>(g, src, t0, threadIdx.x, dim4, acc, v);
+    if (long_runs && i + kLongRun <= n && keys[i + kLongRun - 1] == id) return;  // a long run: segments
+    // Every lane of the wave takes part in the ballots of run_end.
+    const int64_t end = run_end(keys, i, n, id);
+    embed_rows_sum<TPT, CPT>(i, end, t0, toks, src, g, dim4, acc, v);
+}
+
+// The runs of the counting sort, in ascending id order: (id, first sorted
+// position, token count, first token), and how many there are.
+struct RunEntry {
+    uint32_t id, start, count, tok;
+};
+struct RunList {
+    const uint32_t* count;
+    const RunEntry* runs;
+};
+
+// Run j of the list (no workgroup when j is past the list's end), the same
+// sums as embed_rows_position at the run's head.
+template <int TPT, int CPT>
+__device__ __forceinline__ void embed_rows_run(int64_t j, const RunList& list, const uint32_t* toks,
+                                               const float* dy, float* grad, int64_t dim4, int long_runs) {
+    if (j >= *list.count) return;
+    const RunEntry e = list.runs[j];
+    if (long_runs && e.count >= static_cast<uint32_t>(kLongRun)) return;  // a long run: segments
+    const f4* src = reinterpret_cast<const f4*>(dy);
+    f4* g = reinterpret_cast<f4*>(grad) + static_cast<int64_t>(e.id) * dim4;
+    f4 acc[CPT], v[CPT];
+    embed_rows_load<TPT, CPT>(g, src, e.tok, threadIdx.x, dim4, acc, v);
+    embed_rows_sum<TPT, CPT>(e.start, static_cast<int64_t>(e.start) + e.count, e.tok, toks, src, g, dim4, acc, v);
+}
+
+// RUNS: workgroup j takes run j of the counting sort's list; otherwise
+// workgroup i takes sorted position i.  Separate instantiations, so each
+// form is compiled on its own.
+template <int TPT, int CPT, bool RUNS>
 __global__ __launch_bounds__(TPT) void embed_bwd_rows_vec(const uint32_t* keys, const uint32_t* toks, int64_t n,
                                                           uint32_t vocab, const float* dy, float* grad, int64_t dim4,
-                                                          int long_runs) {
-    embed_rows_position<TPT, CPT>(blockIdx.x, keys, toks, n, vocab, dy, grad, dim4, long_runs);
+                                                          int long_runs, RunList runs) {
+    if constexpr (RUNS)
+        embed_rows_run<TPT, CPT>(blockIdx.x, runs, toks, dy, grad, dim4, long_runs);
+    else
+        embed_rows_position<TPT, CPT>(blockIdx.x, keys, toks, n, vocab, dy, grad, dim4, long_runs);
 }
 
 // The rows kernel and the long runs' first level in one launch, so the two
@@ -1397,12 +1443,17 @@ __global__ __launch_bounds__(TPT) void embed_bwd_rows_vec(const uint32_t* keys, 
 // them); its sums are embed_bwd_seg_partial's, in the same token order, bit
 // for bit.
 constexpr int kMergedSegRows = 8;
+template <bool RUNS>
 __global__ __launch_bounds__(1024, 8) void embed_bwd_rows_seg(const uint32_t* keys, const uint32_t* toks, int64_t n,
                                                                uint32_t vocab, const float* dy, float* grad,
-                                                               float* part, int64_t dim4, LongRunList list) {
+                                                               float* part, int64_t dim4, LongRunList list,
+                                                               RunList runs) {
     const int64_t nslots = (n + kLongRun - 1) / kLongRun;
     if (blockIdx.x >= nslots) {
-        embed_rows_position<1024, 1>(blockIdx.x - nslots, keys, toks, n, vocab, dy, grad, dim4, 1);
+        if constexpr (RUNS)
+            embed_rows_run<1024, 1>(blockIdx.x - nslots, runs, toks, dy, grad, dim4, 1);
+        else
+            embed_rows_position<1024, 1>(blockIdx.x - nslots, keys, toks, n, vocab, dy, grad, dim4, 1);
         return;
     }
     const int64_t m = blockIdx.x;
@@ -1476,6 +1527,15 @@ constexpr int64_t kSortMaxTable = int64_t(1) << 24;
 constexpr int kSortChunk = 256;  // keys per workgroup of embed_sort_offsets
 constexpr int64_t kSortMaxKeys = int64_t(kSortBlock) * kSortChunk;  // chunk totals scanned by one workgroup
 
+// The run list's per-key arrays (null `idx`: no list): each key's index among
+// the keys with tokens within its chunk, its token count, and each chunk's
+// number of such keys.
+struct RunScan {
+    uint32_t* idx;
+    uint32_t* tot;
+    uint32_t* chunk;
+};
+
 template <int MODE>
 __global__ __launch_bounds__(kSortBlock) void embed_sort_count(const void* ids, int64_t n, int32_t vocab, int32_t pad,
                                                                uint32_t end_bit, uint16_t* cnt, int64_t pitch,
@@ -1513,7 +1573,8 @@ __global__ __launch_bounds__(kSortBlock) void embed_sort_count(const void* ids, 
 }
 
 __global__ __launch_bounds__(kSortChunk) void embed_sort_offsets(const uint16_t* cnt, int64_t nb, int64_t v1,
-                                                                 int64_t pitch, uint32_t* start, uint32_t* chunk) {
+                                                                 int64_t pitch, uint32_t* start, uint32_t* chunk,
+                                                                 RunScan rs) {
     using Scan = rocprim::block_scan<uint32_t, kSortChunk>;
     __shared__ typename Scan::storage_type st;
     const int64_t k = static_cast<int64_t>(blockIdx.x) * kSortChunk + threadIdx.x;
@@ -1532,6 +1593,16 @@ __global__ __launch_bounds__(kSortChunk) void embed_sort_offsets(const uint16_t*
     uint32_t run = 0, total = 0;
     Scan().exclusive_scan(tot, run, 0u, total, st, rocprim::plus<uint32_t>());
     if (threadIdx.x == 0) chunk[blockIdx.x] = total;
+    if (rs.idx) {  // the run list: keys below v1 - 1 (the skipped key) with tokens, numbered in key order
+        __syncthreads();  // the scan's storage is reused
+        uint32_t idx = 0, runs = 0;
+        Scan().exclusive_scan(k < v1 - 1 && tot > 0 ? 1u : 0u, idx, 0u, runs, st, rocprim::plus<uint32_t>());
+        if (threadIdx.x == 0) rs.chunk[blockIdx.x] = runs;
+        if (k < v1) {
+            rs.idx[k] = idx;
+            rs.tot[k] = tot;
+        }
+    }
     if (k >= v1) return;
     int64_t b = 0;  // the counts again, from L2
     for (; b + 8 <= nb; b += 8) {
@@ -1554,34 +1625,55 @@ template <int MODE>
 __global__ __launch_bounds__(kSortBlock) void embed_sort_scatter(const void* ids, int64_t n, int32_t vocab,
                                                                  int32_t pad, const uint32_t* start, int64_t pitch,
                                                                  const uint16_t* rank, const uint32_t* chunk,
-                                                                 int64_t nchunks, uint32_t* skeys, uint32_t* stoks) {
+                                                                 int64_t nchunks, uint32_t* skeys, uint32_t* stoks,
+                                                                 RunScan rs, uint32_t* nruns, RunEntry* runs) {
     using Scan = rocprim::block_scan<uint32_t, kSortBlock>;
     __shared__ typename Scan::storage_type st;
     __shared__ uint32_t cpre[kSortBlock];
+    __shared__ uint32_t rpre[kSortBlock];
     const int64_t b = blockIdx.x;
     const int64_t t = b * kSortBlock + threadIdx.x;
     const uint32_t c = threadIdx.x < nchunks ? chunk[threadIdx.x] : 0u;
+    const uint32_t rc = rs.idx && threadIdx.x < nchunks ? rs.chunk[threadIdx.x] : 0u;
     const uint32_t k = t < n ? EmbedKey<MODE>{ids, vocab, pad}(t) : 0u;  // loaded beside the chunk totals
     uint32_t cp = 0;
     Scan().exclusive_scan(c, cp, 0u, st, rocprim::plus<uint32_t>());
     cpre[threadIdx.x] = cp;
+    if (rs.idx) {
+        __syncthreads();  // the scan's storage is reused
+        uint32_t rp = 0, total = 0;
+        Scan().exclusive_scan(rc, rp, 0u, total, st, rocprim::plus<uint32_t>());
+        rpre[threadIdx.x] = rp;
+        if (b == 0 && threadIdx.x == 0) *nruns = total;
+    }
     __syncthreads();
     if (t >= n) return;
-    const uint32_t pos = cpre[k / kSortChunk] + start[b * pitch + k] + rank[t];
+    const uint32_t s = start[b * pitch + k];
+    const uint32_t r = rank[t];
+    const uint32_t pos = cpre[k / kSortChunk] + s + r;
     if (pos >= n) return;  // cannot happen when the counts are consistent; keeps a fault out regardless
     skeys[pos] = k;
     stoks[pos] = static_cast<uint32_t>(t);
+    // The run's first token (no earlier block holds its key, rank 0) lists it.
+    if (rs.idx && k < static_cast<uint32_t>(vocab) && r == 0 && s == start[k]) {
+        const uint32_t j = rpre[k / kSortChunk] + rs.idx[k];
+        if (j < n) runs[j] = RunEntry{k, pos, rs.tot[k], static_cast<uint32_t>(t)};
+    }
 }
 
 struct CountSortPlan {
     bool ok = false;
-    int64_t nb = 0, v1 = 0, pitch = 0, nchunks = 0;
+    bool runs = false;  // also the run list
+    int64_t n = 0, nb = 0, v1 = 0, pitch = 0, nchunks = 0;
     uint32_t end_bit = 0;
     size_t cnt_bytes = 0, start_bytes = 0, rank_bytes = 0, chunk_bytes = 0;
-    size_t bytes() const { return cnt_bytes + start_bytes + rank_bytes + chunk_bytes; }
+    size_t key_bytes = 0, list_bytes = 0;  // the run list's per-key arrays (x2), its count and entries
+    size_t bytes() const {
+        return cnt_bytes + start_bytes + rank_bytes + chunk_bytes + (runs ? 2 * key_bytes + chunk_bytes + list_bytes : 0);
+    }
 };
 
-CountSortPlan count_sort_plan(int64_t n, int32_t vocab) {
+CountSortPlan count_sort_plan(int64_t n, int32_t vocab, bool runs) {
     CountSortPlan p;
     p.nb = (n + kSortBlock - 1) / kSortBlock;
     p.v1 = static_cast<int64_t>(vocab) + 1;
@@ -1595,25 +1687,41 @@ CountSortPlan count_sort_plan(int64_t n, int32_t vocab) {
     p.start_bytes = align256(sizeof(uint32_t) * static_cast<size_t>(p.nb * p.pitch));
     p.rank_bytes = align256(sizeof(uint16_t) * static_cast<size_t>(p.nb * kSortBlock));
     p.chunk_bytes = align256(sizeof(uint32_t) * static_cast<size_t>(p.nchunks));
+    p.n = n;
+    p.runs = runs;
+    p.key_bytes = align256(sizeof(uint32_t) * static_cast<size_t>(p.v1));
+    p.list_bytes = 256 + align256(sizeof(RunEntry) * static_cast<size_t>(n));
     return p;
 }
 
 template <int MODE>
 int count_sort(mimir_ctx* ctx, const CountSortPlan& p, const void* ids, int64_t n, int32_t vocab, int32_t pad,
-               char* temp, uint32_t* skeys, uint32_t* stoks, uint32_t* zero) {
+               char* temp, uint32_t* skeys, uint32_t* stoks, uint32_t* zero, RunList* list) {
     uint16_t* cnt = reinterpret_cast<uint16_t*>(temp);
     uint32_t* start = reinterpret_cast<uint32_t*>(temp + p.cnt_bytes);
     uint16_t* rank = reinterpret_cast<uint16_t*>(temp + p.cnt_bytes + p.start_bytes);
     uint32_t* chunk = reinterpret_cast<uint32_t*>(temp + p.cnt_bytes + p.start_bytes + p.rank_bytes);
+    RunScan rs{nullptr, nullptr, nullptr};
+    uint32_t* nruns = nullptr;
+    RunEntry* runs = nullptr;
+    if (p.runs) {
+        char* r = temp + p.cnt_bytes + p.start_bytes + p.rank_bytes + p.chunk_bytes;
+        rs.idx = reinterpret_cast<uint32_t*>(r);
+        rs.tot = reinterpret_cast<uint32_t*>(r + p.key_bytes);
+        rs.chunk = reinterpret_cast<uint32_t*>(r + 2 * p.key_bytes);
+        nruns = reinterpret_cast<uint32_t*>(r + 2 * p.key_bytes + p.chunk_bytes);
+        runs = reinterpret_cast<RunEntry*>(r + 2 * p.key_bytes + p.chunk_bytes + 256);
+        *list = RunList{nruns, runs};
+    }
     const unsigned nb = static_cast<unsigned>(p.nb);
     embed_sort_count<MODE><<<nb, kSortBlock, 0, ctx->stream>>>(ids, n, vocab, pad, p.end_bit, cnt, p.pitch, rank,
                                                                zero);
     if (int st = launched(ctx, "embed_sort_count")) return st;
     embed_sort_offsets<<<static_cast<unsigned>(p.nchunks), kSortChunk, 0, ctx->stream>>>(cnt, p.nb, p.v1, p.pitch,
-                                                                                       start, chunk);
+                                                                                       start, chunk, rs);
     if (int st = launched(ctx, "embed_sort_offsets")) return st;
     embed_sort_scatter<MODE><<<nb, kSortBlock, 0, ctx->stream>>>(ids, n, vocab, pad, start, p.pitch, rank, chunk,
-                                                                 p.nchunks, skeys, stoks);
+                                                                 p.nchunks, skeys, stoks, rs, nruns, runs);
     return launched(ctx, "embed_sort_scatter");
 }
 
@@ -1645,7 +1753,7 @@ int embed_bwd(mimir_ctx* ctx, const void* ids, int64_t n_ids, const float* dy, f
     const auto keys = rocprim::make_transform_iterator(rocprim::counting_iterator<int64_t>(0),
                                                        EmbedKey<MODE>{ids, vocab, pad});
     const rocprim::counting_iterator<uint32_t> toks(0);
-    const CountSortPlan plan = count_sort_plan(n_ids, vocab);
+    const CountSortPlan plan = count_sort_plan(n_ids, vocab, ctx->tune.embed_bwd_runs != 0);
     const bool counting = plan.ok && ctx->tune.embed_bwd_sort != 0;
     size_t sort_bytes = 0;
     hipError_t e = hipSuccess;
@@ -1677,8 +1785,10 @@ int embed_bwd(mimir_ctx* ctx, const void* ids, int64_t n_ids, const float* dy, f
         list.runs = reinterpret_cast<LongRunEntry*>(base + 2 * vbytes + part_bytes + 256);
     }
     char* temp = base + 2 * vbytes + part_bytes + list_bytes;
+    RunList runs{nullptr, nullptr};  // with the counting sort, its runs in id order (unless MIMIR_TUNE embruns=0)
     if (counting) {  // embed_sort_count zeroes the list's count
-        if (int st = count_sort<MODE>(ctx, plan, ids, n_ids, vocab, pad, temp, skeys, stoks, list.count)) return st;
+        if (int st = count_sort<MODE>(ctx, plan, ids, n_ids, vocab, pad, temp, skeys, stoks, list.count, &runs))
+            return st;
     } else {
         e = rocprim::radix_sort_pairs<EmbedSortConfig>(temp, sort_bytes, keys, skeys, toks, stoks, n, 0u, end_bit,
                                                        ctx->stream);
@@ -1696,11 +1806,20 @@ int embed_bwd(mimir_ctx* ctx, const void* ids, int64_t n_ids, const float* dy, f
         // variant): one 16-byte column per thread in 1024-thread workgroups
         // is fastest, 2-4 columns per thread in smaller ones ~2-4% slower.
         const int tpt = ctx->tune.gather_tpt ? ctx->tune.gather_tpt : (dim4 >= 1024 ? 1024 : dim4 >= 512 ? 512 : 256);
-        const bool merged = long_runs && tpt == 1024 && n_ids + nslots <= 0x7fffffffLL &&
+        // With the run list, a workgroup per run: at most min(n, vocab) of them.
+        const int64_t rows_grid = runs.count && vocab < n_ids ? vocab : n_ids;
+        const bool merged = long_runs && tpt == 1024 && rows_grid + nslots <= 0x7fffffffLL &&
                             ctx->tune.embed_bwd_merged != 0;
+        const unsigned rg = static_cast<unsigned>(rows_grid);
+        const bool by_run = runs.count != nullptr;
         if (merged) {
-            embed_bwd_rows_seg<<<static_cast<unsigned>(n_ids + nslots), 1024, 0, ctx->stream>>>(
-                skeys, stoks, n_ids, v, dy, grad, part, dim4, list);
+            const unsigned grid = static_cast<unsigned>(rows_grid + nslots);
+            if (by_run)
+                embed_bwd_rows_seg<true><<<grid, 1024, 0, ctx->stream>>>(skeys, stoks, n_ids, v, dy, grad, part, dim4,
+                                                                        list, runs);
+            else
+                embed_bwd_rows_seg<false><<<grid, 1024, 0, ctx->stream>>>(skeys, stoks, n_ids, v, dy, grad, part,
+                                                                         dim4, list, runs);
             if (int st = launched(ctx, "embed_bwd_rows_seg")) return st;
         } else {
             if (long_runs) {
@@ -1710,12 +1829,22 @@ int embed_bwd(mimir_ctx* ctx, const void* ids, int64_t n_ids, const float* dy, f
                                                                            list);
                 if (int st = launched(ctx, "embed_bwd_seg_partial")) return st;
             }
+#define MIMIR_EMB_ROWS(T, C)                                                                                  \
+    do {                                                                                                      \
+        if (by_run)                                                                                           \
+            embed_bwd_rows_vec<T, C, true><<<rg, T, 0, ctx->stream>>>(skeys, stoks, n_ids, v, dy, grad, dim4, lr, \
+                                                                      runs);                                  \
+        else                                                                                                  \
+            embed_bwd_rows_vec<T, C, false><<<rg, T, 0, ctx->stream>>>(skeys, stoks, n_ids, v, dy, grad, dim4,  \
+                                                                       lr, runs);                             \
+    } while (0)
             if (tpt == 256)
-                embed_bwd_rows_vec<256, 4><<<n, 256, 0, ctx->stream>>>(skeys, stoks, n_ids, v, dy, grad, dim4, lr);
+                MIMIR_EMB_ROWS(256, 4);
             else if (tpt == 512)
-                embed_bwd_rows_vec<512, 2><<<n, 512, 0, ctx->stream>>>(skeys, stoks, n_ids, v, dy, grad, dim4, lr);
+                MIMIR_EMB_ROWS(512, 2);
             else
-                embed_bwd_rows_vec<1024, 1><<<n, 1024, 0, ctx->stream>>>(skeys, stoks, n_ids, v, dy, grad, dim4, lr);
+                MIMIR_EMB_ROWS(1024, 1);
+#undef MIMIR_EMB_ROWS
             if (int st = launched(ctx, "embed_bwd_rows_vec")) return st;
         }
         if (!long_runs) return MIMIR_OK;

@@ -386,21 +386,28 @@ def test_embedding_bwd_long_runs(ctx, case):
     assert (counts >= 32).any() and (counts < 32).any()  # both paths ran
 
 
-@pytest.fixture(scope="module")
-def radix_ctx():
-    """A context whose Embedding backward sorts with rocPRIM's radix sort
-    (MIMIR_TUNE embsort=0) instead of the counting sort."""
+def _tuned(tune):
     old = os.environ.get("MIMIR_TUNE")
-    os.environ["MIMIR_TUNE"] = "embsort=0"
+    os.environ["MIMIR_TUNE"] = tune
     try:
-        c = M.Context(0)
+        return M.Context(0)
     finally:
         if old is None:
             del os.environ["MIMIR_TUNE"]
         else:
             os.environ["MIMIR_TUNE"] = old
-    yield c
-    c.close()
+
+
+@pytest.fixture(scope="module")
+def sort_ctxs():
+    """Contexts whose Embedding backward sorts with rocPRIM's radix sort and
+    takes a workgroup per sorted position (MIMIR_TUNE embsort=0), or sorts by
+    counting but keeps the per-position rows kernel (embruns=0), beside the
+    default (counting sort, a workgroup per listed run)."""
+    cs = {"radix": _tuned("embsort=0"), "positions": _tuned("embruns=0")}
+    yield cs
+    for c in cs.values():
+        c.close()
 
 
 @pytest.mark.parametrize("vocab,n,dist,float_ids", [
@@ -408,12 +415,13 @@ def radix_ctx():
     (1023, 65536, "uniform", False), (1024, 65535, "zipf", False), (1025, 1025, "uniform", True),
     (1, 3000, "uniform", False), (70000, 4097, "uniform", False), (32000, 65537, "uniform", False),
     (5, 1024, "one id", False)])
-def test_embedding_bwd_counting_sort_matches_radix_sort(ctx, radix_ctx, vocab, n, dist, float_ids):
+def test_embedding_bwd_counting_sort_matches_radix_sort(ctx, sort_ctxs, vocab, n, dist, float_ids):
     """The counting sort (up to 64 blocks of 1024 tokens) puts every (id,
-    token) pair where the stable radix sort does, so the gradients are the
-    same bits: chunk edges of the key scan (vocab + 1 around 1024), padding
-    and out-of-range ids (the skipped key), a last partial block, the
-    64-block limit and just past it (the radix sort on both sides)."""
+    token) pair where the stable radix sort does, and its run list names
+    every run the per-position kernel finds, so the gradients are the same
+    bits: chunk edges of the key scan (vocab + 1 around 1024), padding and
+    out-of-range ids (the skipped key), a last partial block, the 64-block
+    limit and just past it (the radix sort on both sides)."""
     dim = 64
     if dist == "zipf":
         r = np.arange(1, vocab + 1, dtype=np.float64) ** -1.0
@@ -427,7 +435,7 @@ def test_embedding_bwd_counting_sort_matches_radix_sort(ctx, radix_ctx, vocab, n
     dy = rng.standard_normal((n, dim)).astype(np.float32)
     gt = rng.standard_normal(vocab * dim).astype(np.float32)
     got = {}
-    for name, c in (("counting", ctx), ("radix", radix_ctx)):
+    for name, c in (("counting", ctx), ("radix", sort_ctxs["radix"]), ("positions", sort_ctxs["positions"])):
         bi, bdy, bg = c.to_device(arg), c.to_device(dy), c.to_device(gt)
         try:
             c.embedding_bwd(bi, n, bdy, bg, gt.size, vocab, dim, pad, float_ids=float_ids)
@@ -436,6 +444,7 @@ def test_embedding_bwd_counting_sort_matches_radix_sort(ctx, radix_ctx, vocab, n
             for d in (bi, bdy, bg):
                 d.free()
     assert_bitexact(got["counting"], got["radix"], f"{dist} ids, vocab {vocab}, {n} tokens")
+    assert_bitexact(got["positions"], got["radix"], f"{dist} ids, vocab {vocab}, {n} tokens, per position")
     ref = O.embedding_bwd(arg, dy, gt, vocab, dim, pad)
     _check_scatter(got["counting"], ref, arg, dy, gt, vocab, dim, pad, "grad table")
 
