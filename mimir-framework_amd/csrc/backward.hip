@@ -1650,14 +1650,18 @@ __global__ __launch_bounds__(kSortBlock) void embed_sort_scatter(const void* ids
     if (t >= n) return;
     const uint32_t s = start[b * pitch + k];
     const uint32_t r = rank[t];
+    // The run list's fields for the key, loaded with the rest (one round trip).
+    const uint32_t s0 = rs.idx ? start[k] : 0u;
+    const uint32_t idx = rs.idx ? rs.idx[k] : 0u;
+    const uint32_t tot = rs.idx ? rs.tot[k] : 0u;
     const uint32_t pos = cpre[k / kSortChunk] + s + r;
     if (pos >= n) return;  // cannot happen when the counts are consistent; keeps a fault out regardless
     skeys[pos] = k;
     stoks[pos] = static_cast<uint32_t>(t);
     // The run's first token (no earlier block holds its key, rank 0) lists it.
-    if (rs.idx && k < static_cast<uint32_t>(vocab) && r == 0 && s == start[k]) {
-        const uint32_t j = rpre[k / kSortChunk] + rs.idx[k];
-        if (j < n) runs[j] = RunEntry{k, pos, rs.tot[k], static_cast<uint32_t>(t)};
+    if (rs.idx && k < static_cast<uint32_t>(vocab) && r == 0 && s == s0) {
+        const uint32_t j = rpre[k / kSortChunk] + idx;
+        if (j < n) runs[j] = RunEntry{k, pos, tot, static_cast<uint32_t>(t)};
     }
 }
 
