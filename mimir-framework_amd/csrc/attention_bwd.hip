@@ -133,6 +133,39 @@ __global__ __launch_bounds__(kBlock) void zero_rows_kernel(float* __restrict__ y
         y[(t / cols) * ld + t % cols] = 0.0f;
 }
 
+// dst[t * ld + h * D + d] = src[(h * T + t) * D + d]: n heads' [T x D]
+// blocks, stored one after another, into the rows of interleaved heads.
+// Eight floats (two 16-byte vectors) per thread when D % 4 == 0 and the
+// pointers and ld allow, else one float.
+template <bool VEC>
+__global__ __launch_bounds__(kBlock) void heads_to_rows_kernel(const float* __restrict__ src, int64_t n, int64_t T,
+                                                               int64_t D, float* __restrict__ dst, int64_t ld) {
+    const int64_t w = VEC ? D / 4 : D;  // elements (vectors or floats) per head row
+    const int64_t total = n * T * w;
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * kBlock;
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x; i < total; i += stride) {
+        const int64_t h = i / (T * w), r = i % (T * w), t = r / w, c = r % w;
+        if constexpr (VEC)
+            *reinterpret_cast<f4*>(dst + t * ld + h * D + 4 * c) = reinterpret_cast<const f4*>(src)[i];
+        else
+            dst[t * ld + h * D + c] = src[i];
+    }
+}
+
+int heads_to_rows(mimir_ctx* ctx, const float* src, int64_t n, int64_t T, int64_t D, float* dst, int64_t ld) {
+    if (n == 0 || T == 0) return MIMIR_OK;
+    const bool vec = D % 4 == 0 && ld % 4 == 0 && aligned16(src) && aligned16(dst);
+    unsigned blocks = 0;
+    if (!grid_for(n * T * (vec ? D / 4 : D), kBlock, &blocks))
+        return fail(ctx, MIMIR_EINVAL, "attention backward: grid too large");
+    blocks = std::min(blocks, 16384u);
+    if (vec)
+        heads_to_rows_kernel<true><<<blocks, kBlock, 0, ctx->stream>>>(src, n, T, D, dst, ld);
+    else
+        heads_to_rows_kernel<false><<<blocks, kBlock, 0, ctx->stream>>>(src, n, T, D, dst, ld);
+    return launched(ctx, "heads_to_rows_kernel");
+}
+
 // dst[c][r] = src[r][c] for a [rows x cols] block of rows ld_src apart; dst
 // is [cols x rows] dense.  32 x 32 tiles through LDS (one padding column so
 // the transposed reads hit distinct banks).
@@ -226,8 +259,12 @@ int64_t heads_per_group(const mimir_ctx* ctx, const CoreBwd& a) {
     if (ctx->tune.attn_bwd_heads > 0) hc = std::min<int64_t>(hc, ctx->tune.attn_bwd_heads);
     return std::max<int64_t>(1, hc);
 }
-int64_t work_floats(const mimir_ctx* ctx, const CoreBwd& a) {
-    return 2 * heads_per_group(ctx, a) * a.q_len * a.kv_len + 2 * a.heads * a.head_dim * a.kv_len;
+// P and dS of a head group, then either the group's dQ / dK / dV in head-
+// major blocks (hipBLASLt) or K^T and V^T of a sequence (rocBLAS only).
+int64_t work_floats(mimir_ctx* ctx, const CoreBwd& a) {
+    const int64_t hc = heads_per_group(ctx, a);
+    return 2 * hc * a.q_len * a.kv_len + (gemm_lt(ctx) ? hc * a.head_dim * (a.q_len + 2 * a.kv_len)
+                                                       : 2 * a.heads * a.head_dim * a.kv_len);
 }
 
 int core_bwd(mimir_ctx* ctx, const CoreBwd& a, float* work) {
@@ -245,18 +282,37 @@ int core_bwd(mimir_ctx* ctx, const CoreBwd& a, float* work) {
     const int64_t width = a.heads * D;
     float* P = work;
     float* G = work + hc * TT;
-    // K^T and V^T of one sequence, [width x kv_len]: with the head dimension
-    // as rows, the score products S = Q K^T and dP = dO V^T are plain (NN)
-    // products, which the library runs about twice as fast as the
-    // transposed-operand form on these shapes.
+    // The score products S = Q K^T and dP = dO V^T read K and V in place as
+    // transposed operands through hipBLASLt.  With rocBLAS only, whose
+    // transposed-operand form runs at about half the plain one's rate on
+    // these shapes, they read K^T and V^T of the sequence, [width x kv_len],
+    // as plain (NN) operands.  hipBLASLt writes the group's dQ, dK and dV as
+    // head-major [n][T][D] blocks (batches that do not overlap, which its
+    // split reductions need), copied into the interleaved heads after.
+    const bool lt = gemm_lt(ctx);
     float* KT = G + hc * TT;
     float* VT = KT + width * Tk;
-    // Causal: the products may run over nblk blocks of bs queries (or keys),
-    // so the key columns past a query block's diagonal -- masked, P = dS = 0
-    // there -- are not multiplied ((nblk + 1) / (2 nblk) of the full work).
-    const int64_t want_blk = ctx->tune.attn_bwd_blocks > 0 ? ctx->tune.attn_bwd_blocks : 1;
-    const int64_t nblk = a.causal ? std::max<int64_t>(1, std::min<int64_t>(want_blk, Tq / 256)) : 1;
-    const int64_t bs = nblk > 1 ? ((Tq + nblk - 1) / nblk + 63) / 64 * 64 : std::max(Tq, Tk);
+    float* SQ = G + hc * TT;
+    float* SK = SQ + hc * Tq * D;
+    float* SV = SK + hc * Tk * D;
+    // Causal: the products may run over blocks of bq queries (S, P V, dP,
+    // dQ) or bk keys (dV, dK), so the key columns past a query block's
+    // diagonal -- masked, P = dS = 0 there -- are not multiplied ((nblk + 1)
+    // / (2 nblk) of the full work).  Measured at 32 heads of 1024 x 1024 x
+    // 128: hipBLASLt keeps its rate on two query blocks for S and dP (3/4 of
+    // the work in 77 us, against 92 us whole), rocBLAS runs the query-side dQ
+    // faster on two blocks (80 against 87 us) but the key-side products
+    // slower (110 against 85 us); rocBLAS's plain S is slower on any split.
+    // hipBLASLt takes dV / dK on two key blocks in 62 us and dQ on two query
+    // blocks in 64 us.  A tuning override sets one count for all.
+    auto block_size = [&](int64_t want) {
+        const int64_t nblk = a.causal ? std::max<int64_t>(1, std::min<int64_t>(want, Tq / 256)) : 1;
+        return nblk > 1 ? ((Tq + nblk - 1) / nblk + 63) / 64 * 64 : std::max(Tq, Tk);
+    };
+    const int64_t over = ctx->tune.attn_bwd_blocks;
+    const int64_t bq = block_size(over > 0 ? over : (lt ? 2 : 1));  // S, P V, dP
+    const int64_t bdq = block_size(over > 0 ? over : 2);            // dQ
+    const int64_t bk = block_size(over > 0 ? over : (lt ? 2 : 1));  // dV, dK
     auto live = [&](int64_t q1) { return a.causal ? std::min(q1, Tk) : Tk; };  // keys queries < q1 see
     for (int64_t b = 0; b < a.batch; ++b) {
         const float* qb = a.q + b * Tq * a.ld_q;
@@ -267,63 +323,85 @@ int core_bwd(mimir_ctx* ctx, const CoreBwd& a, float* work) {
         float* dkb = a.dk + b * Tk * a.ld_dkv;
         float* dvb = a.dv + b * Tk * a.ld_dkv;
         float* attb = a.att ? a.att + b * Tq * a.ld_att : nullptr;
-        if (int st = transpose(ctx, kb, a.ld_kv, Tk, width, KT)) return st;
-        if (int st = transpose(ctx, vb, a.ld_kv, Tk, width, VT)) return st;
+        if (!lt) {
+            if (int st = transpose(ctx, kb, a.ld_kv, Tk, width, KT)) return st;
+            if (int st = transpose(ctx, vb, a.ld_kv, Tk, width, VT)) return st;
+        }
         for (int64_t h0 = 0; h0 < a.heads; h0 += hc) {
             const int64_t n = std::min(hc, a.heads - h0), off = h0 * D;
             const int64_t rows = n * Tq;
             const auto q32 = static_cast<int32_t>(Tq), k32 = static_cast<int32_t>(Tk);
             // Row-blocked products (S, attended, dP, dQ): query block [q0, q1)
             // reads keys [0, live(q1)).
-            for (int64_t q0 = 0; q0 < Tq; q0 += bs) {
-                const int64_t m = std::min(bs, Tq - q0), kl = live(q0 + m);
+            for (int64_t q0 = 0; q0 < Tq; q0 += bq) {
+                const int64_t m = std::min(bq, Tq - q0), kl = live(q0 + m);
                 // S = scale Q K^T (:6892-6905)
-                if (int st = gemm_f32_ex(ctx, false, false, m, kl, D, a.scale, qb + q0 * a.ld_q + off, a.ld_q, D,
-                                         KT + off * Tk, Tk, D * Tk, 0.0f, P + q0 * Tk, Tk, TT, n))
+                if (int st = lt ? gemm_f32_ex(ctx, false, true, m, kl, D, a.scale, qb + q0 * a.ld_q + off, a.ld_q, D,
+                                              kb + off, a.ld_kv, D, 0.0f, P + q0 * Tk, Tk, TT, n)
+                                : gemm_f32_ex(ctx, false, false, m, kl, D, a.scale, qb + q0 * a.ld_q + off, a.ld_q, D,
+                                              KT + off * Tk, Tk, D * Tk, 0.0f, P + q0 * Tk, Tk, TT, n))
                     return st;
             }
             // P = softmax(mask(S)) in place (:6906-6920); every key column is
             // written (0 where masked), so the key-blocked products below may
             // read whole columns of a block.
             if (int st = probs(ctx, P, rows, q32, k32, a.causal)) return st;
-            for (int64_t q0 = 0; q0 < Tq; q0 += bs) {
-                const int64_t m = std::min(bs, Tq - q0), kl = live(q0 + m);
+            for (int64_t q0 = 0; q0 < Tq; q0 += bq) {
+                const int64_t m = std::min(bq, Tq - q0), kl = live(q0 + m);
                 if (attb)  // attended = P V (:6922-6930)
                     if (int st = gemm_f32_ex(ctx, false, false, m, D, kl, 1.0f, P + q0 * Tk, Tk, TT, vb + off, a.ld_kv,
                                              D, 0.0f, attb + q0 * a.ld_att + off, a.ld_att, D, n))
                         return st;
                 // dP = dO V^T (:6979-6989)
-                if (int st = gemm_f32_ex(ctx, false, false, m, kl, D, 1.0f, ob + q0 * a.ld_dout + off, a.ld_dout, D,
-                                         VT + off * Tk, Tk, D * Tk, 0.0f, G + q0 * Tk, Tk, TT, n))
+                if (int st = lt ? gemm_f32_ex(ctx, false, true, m, kl, D, 1.0f, ob + q0 * a.ld_dout + off, a.ld_dout,
+                                              D, vb + off, a.ld_kv, D, 0.0f, G + q0 * Tk, Tk, TT, n)
+                                : gemm_f32_ex(ctx, false, false, m, kl, D, 1.0f, ob + q0 * a.ld_dout + off, a.ld_dout,
+                                              D, VT + off * Tk, Tk, D * Tk, 0.0f, G + q0 * Tk, Tk, TT, n))
                     return st;
             }
             // dS in place (:6991-7005), every key column written as for P
             if (int st = dsoftmax(ctx, P, G, rows, q32, k32, a.causal)) return st;
-            for (int64_t q0 = 0; q0 < Tq; q0 += bs) {  // dQ = scale dS K (:7007-7016)
-                const int64_t m = std::min(bs, Tq - q0), kl = live(q0 + m);
-                if (int st = gemm_f32_ex(ctx, false, false, m, D, kl, a.scale, G + q0 * Tk, Tk, TT, kb + off, a.ld_kv,
-                                         D, 0.0f, dqb + q0 * a.ld_dq + off, a.ld_dq, D, n))
+            for (int64_t q0 = 0; q0 < Tq; q0 += bdq) {  // dQ = scale dS K (:7007-7016)
+                const int64_t m = std::min(bdq, Tq - q0), kl = live(q0 + m);
+                if (int st = lt ? gemm_f32_ex(ctx, false, false, m, D, kl, a.scale, G + q0 * Tk, Tk, TT, kb + off,
+                                              a.ld_kv, D, 0.0f, SQ + q0 * D, D, Tq * D, n)
+                                : gemm_f32_ex(ctx, false, false, m, D, kl, a.scale, G + q0 * Tk, Tk, TT, kb + off,
+                                              a.ld_kv, D, 0.0f, dqb + q0 * a.ld_dq + off, a.ld_dq, D, n))
                     return st;
             }
+            if (lt)
+                if (int st = heads_to_rows(ctx, SQ, n, Tq, D, dqb + off, a.ld_dq)) return st;
             // Key-blocked products (dV, dK): key block [k0, k1) is seen by
             // queries [first(k0), Tq); a block no query sees gets zeros.
-            for (int64_t k0 = 0; k0 < Tk; k0 += bs) {
-                const int64_t m = std::min(bs, Tk - k0), qs = a.causal ? k0 : 0;
+            for (int64_t k0 = 0; k0 < Tk; k0 += bk) {
+                const int64_t m = std::min(bk, Tk - k0), qs = a.causal ? k0 : 0;
                 if (qs >= Tq) {
-                    if (int st = zero_rows(ctx, dvb + k0 * a.ld_dkv + off, m, n * D, a.ld_dkv)) return st;
-                    if (int st = zero_rows(ctx, dkb + k0 * a.ld_dkv + off, m, n * D, a.ld_dkv)) return st;
+                    if (!lt) {
+                        if (int st = zero_rows(ctx, dvb + k0 * a.ld_dkv + off, m, n * D, a.ld_dkv)) return st;
+                        if (int st = zero_rows(ctx, dkb + k0 * a.ld_dkv + off, m, n * D, a.ld_dkv)) return st;
+                        continue;
+                    }
+                    for (int64_t h = 0; h < n; ++h) {  // the head-major blocks' rows
+                        if (int st = zero_rows(ctx, SV + (h * Tk + k0) * D, m, D, D)) return st;
+                        if (int st = zero_rows(ctx, SK + (h * Tk + k0) * D, m, D, D)) return st;
+                    }
                     continue;
                 }
+                float* dvo = lt ? SV + k0 * D : dvb + k0 * a.ld_dkv + off;
+                float* dko = lt ? SK + k0 * D : dkb + k0 * a.ld_dkv + off;
+                const int64_t ldo = lt ? D : a.ld_dkv, so = lt ? Tk * D : D;
                 // dV = P^T dO (:6967-6977)
                 if (int st = gemm_f32_ex(ctx, true, false, m, D, Tq - qs, 1.0f, P + qs * Tk + k0, Tk, TT,
-                                         ob + qs * a.ld_dout + off, a.ld_dout, D, 0.0f, dvb + k0 * a.ld_dkv + off,
-                                         a.ld_dkv, D, n))
+                                         ob + qs * a.ld_dout + off, a.ld_dout, D, 0.0f, dvo, ldo, so, n))
                     return st;
                 // dK = scale dS^T Q (:7018-7028)
                 if (int st = gemm_f32_ex(ctx, true, false, m, D, Tq - qs, a.scale, G + qs * Tk + k0, Tk, TT,
-                                         qb + qs * a.ld_q + off, a.ld_q, D, 0.0f, dkb + k0 * a.ld_dkv + off, a.ld_dkv,
-                                         D, n))
+                                         qb + qs * a.ld_q + off, a.ld_q, D, 0.0f, dko, ldo, so, n))
                     return st;
+            }
+            if (lt) {
+                if (int st = heads_to_rows(ctx, SV, n, Tk, D, dvb + off, a.ld_dkv)) return st;
+                if (int st = heads_to_rows(ctx, SK, n, Tk, D, dkb + off, a.ld_dkv)) return st;
             }
         }
     }

@@ -31,8 +31,10 @@ struct mimir_ctx {
     // Device address of this GPU's fixed scratch array (backward.hip), for
     // the entry point that allocates nothing; set at context creation.
     void* noalloc_scratch = nullptr;
-    // rocBLAS handle for the attention layers' products (gemm.hip), created
-    // on first use, with a workspace of this library's (grown on demand).
+    // hipBLASLt state (handle and per-shape plans) and rocBLAS handle for the
+    // attention layers' products (gemm.hip), created on first use, sharing a
+    // workspace of this library's (grown on demand).
+    void* blaslt = nullptr;
     void* blas = nullptr;
     void* blas_ws = nullptr;
     size_t blas_ws_bytes = 0;
@@ -121,6 +123,9 @@ int gemm_f32_ex(mimir_ctx* ctx, bool trans_a, bool trans_b, int64_t M, int64_t N
                 const float* A, int64_t lda, int64_t stride_a, const float* B, int64_t ldb, int64_t stride_b,
                 float beta, float* C, int64_t ldc, int64_t stride_c, int64_t batch);
 void gemm_release(mimir_ctx* ctx);
+// Whether products go to hipBLASLt (unless MIMIR_TUNE blas=0), where the
+// transposed-operand forms run as fast as the plain ones.
+bool gemm_lt(mimir_ctx* ctx);
 
 // A chain of elementwise layers run as one kernel (store.hip's fusion):
 // v = ins[0]; then each step k sets v = op_k(v, operand) -- GELU, SiLU, or
