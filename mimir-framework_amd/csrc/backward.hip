@@ -1138,10 +1138,11 @@ struct LongRunEntry {
 struct LongRunList {
     uint32_t* count;
     LongRunEntry* runs;
+    uint32_t cap;  // entries: one per kLongRun positions, at least one per long run
 };
 __device__ __forceinline__ void list_long_run(const LongRunList& list, uint32_t id, int64_t head, int64_t end) {
     const uint32_t j = atomicAdd(list.count, 1u);
-    list.runs[j] = LongRunEntry{id, static_cast<uint32_t>(head), static_cast<uint32_t>(end), 0u};
+    if (j < list.cap) list.runs[j] = LongRunEntry{id, static_cast<uint32_t>(head), static_cast<uint32_t>(end), 0u};
 }
 
 __global__ void zero_count_kernel(uint32_t* count) {
@@ -1259,11 +1260,12 @@ constexpr int kCombineGroups = 4;
 constexpr int64_t kCombineGrid = 1024;
 __global__ __launch_bounds__(kWave * kCombineGroups) void embed_bwd_seg_combine(const uint32_t* count,
                                                                                  const LongRunEntry* runs,
-                                                                                 const float* part, float* grad,
-                                                                                 int64_t dim4) {
+                                                                                 uint32_t cap, const float* part,
+                                                                                 float* grad, int64_t dim4) {
     __shared__ f4 sums[kCombineGroups - 1][kWave];
     const int64_t blocks = (dim4 + kCombineCols - 1) / kCombineCols;
-    const int64_t items = static_cast<int64_t>(*count) * blocks;
+    const int64_t listed = *count < cap ? *count : cap;
+    const int64_t items = listed * blocks;
     const int grp = threadIdx.x / kWave;
     const int lane = threadIdx.x & (kWave - 1);
     const f4* src = reinterpret_cast<const f4*>(part);
@@ -1783,10 +1785,11 @@ int embed_bwd(mimir_ctx* ctx, const void* ids, int64_t n_ids, const float* dy, f
     uint32_t* skeys = reinterpret_cast<uint32_t*>(base);
     uint32_t* stoks = reinterpret_cast<uint32_t*>(base + vbytes);
     float* part = reinterpret_cast<float*>(base + 2 * vbytes);
-    LongRunList list{nullptr, nullptr};
+    LongRunList list{nullptr, nullptr, 0u};
     if (long_runs) {
         list.count = reinterpret_cast<uint32_t*>(base + 2 * vbytes + part_bytes);
         list.runs = reinterpret_cast<LongRunEntry*>(base + 2 * vbytes + part_bytes + 256);
+        list.cap = static_cast<uint32_t>(nslots);
     }
     char* temp = base + 2 * vbytes + part_bytes + list_bytes;
     RunList runs{nullptr, nullptr};  // with the counting sort, its runs in id order (unless MIMIR_TUNE embruns=0)
@@ -1857,8 +1860,8 @@ int embed_bwd(mimir_ctx* ctx, const void* ids, int64_t n_ids, const float* dy, f
         const int64_t blocks = (dim4 + kCombineCols - 1) / kCombineCols;
         const int64_t items = nslots * blocks;
         const unsigned cgrid = static_cast<unsigned>(items < kCombineGrid ? items : kCombineGrid);
-        embed_bwd_seg_combine<<<cgrid, kWave * kCombineGroups, 0, ctx->stream>>>(list.count, list.runs, part, grad,
-                                                                                 dim4);
+        embed_bwd_seg_combine<<<cgrid, kWave * kCombineGroups, 0, ctx->stream>>>(list.count, list.runs, list.cap,
+                                                                                 part, grad, dim4);
         return launched(ctx, "embed_bwd_seg_combine");
     }
     embed_bwd_rows_scalar<<<n, kBlock, 0, ctx->stream>>>(skeys, stoks, n_ids, static_cast<uint32_t>(vocab), dy,
