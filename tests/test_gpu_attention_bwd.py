@@ -111,7 +111,9 @@ CORE = [(1, 64, 64, 2, 32, True, 1.0), (1, 64, 64, 2, 32, False, 1.0), (3, 33, 3
         (2, 257, 257, 1, 200, True, 1.0),
         # longer causal rows and cross shapes with keys past every query
         (1, 600, 600, 2, 32, True, 1.0), (1, 1000, 1000, 1, 64, True, 1.0), (1, 700, 300, 1, 32, True, 1.0),
-        (1, 300, 700, 1, 32, True, 1.0), (2, 520, 520, 2, 16, True, 2.0)]
+        (1, 300, 700, 1, 32, True, 1.0), (2, 520, 520, 2, 16, True, 2.0),
+        # odd head sizes: row strides and head offsets that are not 16-byte multiples
+        (1, 45, 45, 3, 5, True, 1.0), (2, 33, 50, 2, 7, False, 1.0), (1, 260, 260, 2, 13, True, 1.0)]
 
 
 @pytest.mark.parametrize("case", CORE, ids=lambda c: "x".join(map(str, c[:6])))
