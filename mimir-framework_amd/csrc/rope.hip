@@ -15,6 +15,7 @@
 // default), so a wave instruction reads 4 head rows' half-rows (4 x 256 B
 // for D = 128).
 #include "common.hpp"
+#include "fastdiv.hpp"
 #include "internal.hpp"
 
 #include <math.h>
@@ -34,6 +35,7 @@ struct RopeArgs {
     uint32_t k_heads;
     uint32_t seq;
     uint32_t half;        // D / 2
+    FastDiv q_div, k_div, seq_div;  // the same three divisors for the vector kernel (rows < 2^32)
     int64_t q_slots;      // q head rows * Q
     int64_t total_slots;  // (q + k head rows) * Q
     int64_t pos_offset;
@@ -61,11 +63,10 @@ __global__ __launch_bounds__(kBlock) void rope_vec(RopeArgs a) {
         if (slot < a.total_slots) {
             const bool is_q = slot < a.q_slots;
             const int64_t local = is_q ? slot : slot - a.q_slots;
-            const uint32_t heads = is_q ? a.q_heads : a.k_heads;
-            const uint64_t hr = static_cast<uint64_t>(local) >> LOG2Q;  // head row
+            const uint32_t hr = static_cast<uint32_t>(local >> LOG2Q);  // head row (the host checks < 2^32)
             const int64_t i4 = 4 * (local & (Q - 1));                   // first pair of the slot
-            const uint64_t tok = hr / heads;
-            const int64_t pos = a.pos_offset + static_cast<int64_t>(tok % a.seq);
+            const uint32_t tok = fastdiv(hr, is_q ? a.q_div : a.k_div);
+            const int64_t pos = a.pos_offset + static_cast<int64_t>(fastmod(tok, a.seq_div));
             const float* src = (is_q ? a.q : a.k) + static_cast<int64_t>(hr) * D + i4;
             out[j] = (is_q ? a.q_out : a.k_out) + static_cast<int64_t>(hr) * D + i4;
             x0[j] = ld4<true>(src);
@@ -171,7 +172,10 @@ int mimir_rope_fwd(mimir_ctx* ctx, const float* q, float* q_out, int64_t q_heads
     const int64_t half = head_dim / 2;
     RopeArgs a{q, q_out, k, k_out, cos_tab, sin_tab,
                static_cast<uint32_t>(qh ? qh : 1), static_cast<uint32_t>(kh ? kh : 1),
-               static_cast<uint32_t>(seq), static_cast<uint32_t>(half), 0, 0, pos_offset};
+               static_cast<uint32_t>(seq), static_cast<uint32_t>(half), {}, {}, {}, 0, 0, pos_offset};
+    a.q_div = make_fastdiv(a.q_heads);
+    a.k_div = make_fastdiv(a.k_heads);
+    a.seq_div = make_fastdiv(a.seq ? a.seq : 1);
     bool vec = (half % 4) == 0 && aligned16(cos_tab) && aligned16(sin_tab) &&
                (!q || (aligned16(q) && aligned16(q_out))) && (!k || (aligned16(k) && aligned16(k_out)));
     const int64_t Q = half / 4;
