@@ -159,13 +159,29 @@ def test_core_backward_head_groups(group):
 @pytest.mark.parametrize("blocks", [2, 3, 4])
 @pytest.mark.parametrize("lq,lk", [(1000, 1000), (700, 300), (520, 900)])
 def test_core_backward_causal_blocks(blocks, lq, lk):
-    """The causal products over query / key blocks (a tuning override; one
-    block is the default): ragged last blocks, cross shapes, and key blocks
-    that no query sees (zeroed)."""
+    """The causal products over query / key blocks in other counts than the
+    default two (a tuning override): ragged last blocks, cross shapes, and
+    key blocks that no query sees (zeroed)."""
     c = _tuned_context(f"attnbwd_blocks={blocks}")
     try:
         q, k, v, dout = rand_core(lq + lk + blocks, 1, lq, lk, 2 * 32, 1.0)
         check_core(gpu_core_bwd(c, q, k, v, dout, 2, True), q, k, v, dout, 2, True, f"{blocks} blocks")
+    finally:
+        c.close()
+
+
+@pytest.mark.parametrize("tune", ["blas=0", "blas=0,attnbwd_blocks=2"])
+@pytest.mark.parametrize("causal", [False, True])
+def test_core_backward_rocblas(tune, causal):
+    """The rocBLAS-only path (MIMIR_TUNE blas=0): K and V transposed for the
+    plain-form score products, dQ / dK / dV written in place, with and
+    without causal blocks, and an odd head size."""
+    c = _tuned_context(tune)
+    try:
+        q, k, v, dout = rand_core(15, 1, 520, 520, 3 * 20, 1.0)
+        check_core(gpu_core_bwd(c, q, k, v, dout, 3, causal), q, k, v, dout, 3, causal, tune)
+        q, k, v, dout = rand_core(16, 1, 260, 260, 2 * 13, 1.0)
+        check_core(gpu_core_bwd(c, q, k, v, dout, 2, causal), q, k, v, dout, 2, causal, tune + ", head size 13")
     finally:
         c.close()
 
