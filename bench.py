@@ -213,8 +213,8 @@ def build_ops(rows_override=None):
     ops.append(OpBench("f4_attention_bwd", 2,
                        f"attention core backward fp32 [{ab} seq x {ah} heads x {al} tokens, head_dim {ad}, causal]: "
                        f"QKV [{ab * al}x{3 * aw}] + dout [{ab * al}x{aw}] -> dQKV [{ab * al}x{3 * aw}]",
-                       "hipBLASLt sgemm (S, dP, dQ, dV, dK on two causal blocks each) + attn_probs_kernel<16> + "
-                       "attn_dsoftmax_kernel<16> + heads_to_rows_kernel",
+                       "hipBLASLt sgemm (S, dP, dQ, dV, dK on two causal blocks each) + attn_probs_dsoftmax_kernel<16> + "
+                       "heads_to_rows_kernel",
                        7 * ab * al * aw * f4, ab * ah * al, "query rows", make_attention_bwd,
                        lambda s: {"dqkv": s[0][2]}, flops=attention_bwd_flops(ab, ah, al, al, ad, True)))
 

@@ -125,6 +125,58 @@ __global__ __launch_bounds__(kRowWaves * kWave) void attn_dsoftmax_kernel(const 
     }
 }
 
+// The two row passes in one, for rows held in registers: mask + softmax of
+// the score row s in place (attn_probs_kernel's arithmetic), then, with dP
+// already in g, dS = (dP - sum_k p_k dP_k) p in place (attn_dsoftmax_kernel's,
+// on the same p values it would read back).  The row's dP is loaded with its
+// scores, so one read of each matrix and one write of each replace the two
+// passes' three reads and two writes, with the same arithmetic in the
+// same order.
+template <int NV>
+__global__ __launch_bounds__(kRowWaves * kWave) void attn_probs_dsoftmax_kernel(float* __restrict__ s,
+                                                                                float* __restrict__ g, int64_t rows,
+                                                                                int32_t q_len, int32_t kv_len,
+                                                                                int32_t causal) {
+    static_assert(NV > 0, "register rows only");
+    const int64_t row = static_cast<int64_t>(blockIdx.x) * kRowWaves + threadIdx.x / kWave;
+    if (row >= rows) return;  // whole waves only: no barrier below
+    const int lane = threadIdx.x & (kWave - 1);
+    float* p = s + row * kv_len;
+    float* d = g + row * kv_len;
+    const int live = live_keys(row, q_len, kv_len, causal);
+    float m = live < kv_len ? kMaskedScore : -1e30f;
+    float e[NV], dv[NV];
+#pragma unroll
+    for (int c = 0; c < NV; ++c) {
+        const int j = lane + kWave * c;
+        e[c] = j < live ? p[j] : -INFINITY;
+        dv[c] = j < live ? d[j] : 0.0f;
+        m = fmaxf(m, e[c]);
+    }
+    m = wave_max(m);
+    float sum = 0.0f;
+#pragma unroll
+    for (int c = 0; c < NV; ++c) {
+        e[c] = expf(e[c] - m);
+        sum += e[c];
+    }
+    const float inv = 1.0f / (wave_sum(sum) + 1e-9f);
+    float dot = 0.0f;
+#pragma unroll
+    for (int c = 0; c < NV; ++c) {
+        const int j = lane + kWave * c;
+        e[c] = e[c] * inv;  // p_j, 0 for masked keys
+        if (j < kv_len) p[j] = e[c];
+        dot += dv[c] * (j < live ? e[c] : 0.0f);
+    }
+    dot = wave_sum(dot);
+#pragma unroll
+    for (int c = 0; c < NV; ++c) {
+        const int j = lane + kWave * c;
+        if (j < kv_len) d[j] = j < live ? (dv[c] - dot) * e[c] : 0.0f;
+    }
+}
+
 __global__ __launch_bounds__(kBlock) void zero_rows_kernel(float* __restrict__ y, int64_t rows, int64_t cols,
                                                            int64_t ld) {
     const int64_t n = rows * cols;
@@ -211,6 +263,23 @@ int probs(mimir_ctx* ctx, float* s, int64_t rows, int32_t q_len, int32_t kv_len,
     else
         attn_probs_kernel<0><<<grid, block, 0, ctx->stream>>>(s, rows, q_len, kv_len, causal);
     return launched(ctx, "attn_probs_kernel");
+}
+
+// Whether probs_dsoftmax applies: rows the register forms hold.
+bool fused_rows(int32_t kv_len) { return kv_len <= 64 * kWave; }
+
+int probs_dsoftmax(mimir_ctx* ctx, float* s, float* g, int64_t rows, int32_t q_len, int32_t kv_len,
+                   int32_t causal) {
+    unsigned blocks = 0;
+    if (!grid_for(rows, kRowWaves, &blocks)) return fail(ctx, MIMIR_EINVAL, "attention backward: grid too large");
+    const dim3 grid(blocks), block(kRowWaves * kWave);
+    if (kv_len <= 4 * kWave)
+        attn_probs_dsoftmax_kernel<4><<<grid, block, 0, ctx->stream>>>(s, g, rows, q_len, kv_len, causal);
+    else if (kv_len <= 16 * kWave)
+        attn_probs_dsoftmax_kernel<16><<<grid, block, 0, ctx->stream>>>(s, g, rows, q_len, kv_len, causal);
+    else
+        attn_probs_dsoftmax_kernel<64><<<grid, block, 0, ctx->stream>>>(s, g, rows, q_len, kv_len, causal);
+    return launched(ctx, "attn_probs_dsoftmax_kernel");
 }
 
 int dsoftmax(mimir_ctx* ctx, const float* p, float* g, int64_t rows, int32_t q_len, int32_t kv_len,
@@ -342,16 +411,23 @@ int core_bwd(mimir_ctx* ctx, const CoreBwd& a, float* work) {
                                               KT + off * Tk, Tk, D * Tk, 0.0f, P + q0 * Tk, Tk, TT, n))
                     return st;
             }
-            // P = softmax(mask(S)) in place (:6906-6920); every key column is
-            // written (0 where masked), so the key-blocked products below may
-            // read whole columns of a block.
-            if (int st = probs(ctx, P, rows, q32, k32, a.causal)) return st;
+            // P = softmax(mask(S)) in place (:6906-6920) and dS in place
+            // (:6991-7005); every key column of both is written (0 where
+            // masked), so the key-blocked products below may read whole
+            // columns of a block.  Rows held in registers take both passes in
+            // one kernel after dP; longer rows take them one before and one
+            // after it.
+            const bool fuse = fused_rows(k32);
+            if (!fuse)
+                if (int st = probs(ctx, P, rows, q32, k32, a.causal)) return st;
+            auto attended = [&](int64_t q0, int64_t m, int64_t kl) {  // attended = P V (:6922-6930)
+                return gemm_f32_ex(ctx, false, false, m, D, kl, 1.0f, P + q0 * Tk, Tk, TT, vb + off, a.ld_kv, D, 0.0f,
+                                   attb + q0 * a.ld_att + off, a.ld_att, D, n);
+            };
             for (int64_t q0 = 0; q0 < Tq; q0 += bq) {
                 const int64_t m = std::min(bq, Tq - q0), kl = live(q0 + m);
-                if (attb)  // attended = P V (:6922-6930)
-                    if (int st = gemm_f32_ex(ctx, false, false, m, D, kl, 1.0f, P + q0 * Tk, Tk, TT, vb + off, a.ld_kv,
-                                             D, 0.0f, attb + q0 * a.ld_att + off, a.ld_att, D, n))
-                        return st;
+                if (attb && !fuse)
+                    if (int st = attended(q0, m, kl)) return st;
                 // dP = dO V^T (:6979-6989)
                 if (int st = lt ? gemm_f32_ex(ctx, false, true, m, kl, D, 1.0f, ob + q0 * a.ld_dout + off, a.ld_dout,
                                               D, vb + off, a.ld_kv, D, 0.0f, G + q0 * Tk, Tk, TT, n)
@@ -359,8 +435,16 @@ int core_bwd(mimir_ctx* ctx, const CoreBwd& a, float* work) {
                                               D, VT + off * Tk, Tk, D * Tk, 0.0f, G + q0 * Tk, Tk, TT, n))
                     return st;
             }
-            // dS in place (:6991-7005), every key column written as for P
-            if (int st = dsoftmax(ctx, P, G, rows, q32, k32, a.causal)) return st;
+            if (fuse) {
+                if (int st = probs_dsoftmax(ctx, P, G, rows, q32, k32, a.causal)) return st;
+                if (attb)
+                    for (int64_t q0 = 0; q0 < Tq; q0 += bq) {
+                        const int64_t m = std::min(bq, Tq - q0);
+                        if (int st = attended(q0, m, live(q0 + m))) return st;
+                    }
+            } else if (int st = dsoftmax(ctx, P, G, rows, q32, k32, a.causal)) {
+                return st;
+            }
             for (int64_t q0 = 0; q0 < Tq; q0 += bdq) {  // dQ = scale dS K (:7007-7016)
                 const int64_t m = std::min(bdq, Tq - q0), kl = live(q0 + m);
                 if (int st = lt ? gemm_f32_ex(ctx, false, false, m, D, kl, a.scale, G + q0 * Tk, Tk, TT, kb + off,
