@@ -809,10 +809,12 @@ __global__ __launch_bounds__(BS) void ln_bwd_vec(LnBwdArgs a) {
 }
 
 // Rows of up to 4096 floats whose 16-byte vectors do not line up (a width
-// that is not a multiple of 4, or an unaligned pointer): ln_bwd_vec's scheme
-// with 4-byte columns c = j*TPR + t, TPR threads per row and kBlock/TPR rows
-// per workgroup (one wave per row up to 1024 floats: no barrier in the row
-// sums, and four rows' loads in flight per workgroup).  Each row is read
+// that is not a multiple of 4, or an unaligned pointer), and rows of at most
+// 64 floats: ln_bwd_vec's scheme with 4-byte columns c = j*TPR + t, TPR
+// threads per row and kBlock/TPR rows per workgroup (one wave per row up to
+// 1024 floats: no barrier in the row sums, and four rows' loads in flight
+// per workgroup; 16 or 32 lanes per row up to 64 floats, so a wave holds two
+// or four rows and sums them with lane-group reductions).  Each row is read
 // once; a thread reads dy[c] before it writes dx[c], so dx may alias dy.
 template <int TPR, int VPT, bool KEEP>
 __global__ __launch_bounds__(kBlock) void ln_bwd_scalar(LnBwdArgs a) {
@@ -858,7 +860,12 @@ __global__ __launch_bounds__(kBlock) void ln_bwd_scalar(LnBwdArgs a) {
             s += xv[j];
             s1 += gv[j] * gm[j];
         }
-        row_sum2<NW>(s, s1, lds[0], lds[1], sub);
+        if constexpr (TPR < kWave) {
+            s = group_sum<TPR>(s);
+            s1 = group_sum<TPR>(s1);
+        } else {
+            row_sum2<NW>(s, s1, lds[0], lds[1], sub);
+        }
         const float mean = s / n;  // :7765-7768
         float q = 0.0f, p2 = 0.0f;
 #pragma unroll
@@ -869,7 +876,12 @@ __global__ __launch_bounds__(kBlock) void ln_bwd_scalar(LnBwdArgs a) {
                 p2 += gv[j] * gm[j] * d;
             }
         }
-        row_sum2<NW>(q, p2, lds[2], lds[3], sub);
+        if constexpr (TPR < kWave) {
+            q = group_sum<TPR>(q);
+            p2 = group_sum<TPR>(p2);
+        } else {
+            row_sum2<NW>(q, p2, lds[2], lds[3], sub);
+        }
         const float var = q / n;                          // :7770-7776
         const float inv_std = 1.0f / sqrtf(var + a.eps);  // :7777
         const float s2 = p2 * inv_std;
@@ -1896,6 +1908,13 @@ int layernorm_bwd(mimir_ctx* ctx, const float* x, const float* dy, const float* 
             return st;
         if (!slots) return MIMIR_OK;
         return launch_sum_slots(ctx, slots, nslots, 2 * n, dbeta ? 2 * n : n, dgamma, dbeta, n, true, tmp);
+    }
+    // Rows of at most 64 floats: two or four rows per wave (MIMIR_TUNE
+    // lnbwd_narrow=0 keeps one row per wave, or per vector row of ln_bwd_vec).
+    if (n <= 64 && ctx->tune.lnbwd_narrow != 0 && !(vec && shape_fits(ctx->tune.lnbwd, c4))) {
+        if (n <= 16) return launch_ln_bwd_scalar<16, 1>(ctx, a, dgamma, dbeta, fixed);
+        if (n <= 32) return launch_ln_bwd_scalar<16, 2>(ctx, a, dgamma, dbeta, fixed);
+        return launch_ln_bwd_scalar<32, 2>(ctx, a, dgamma, dbeta, fixed);
     }
     if (vec) {
         const RowShape over = ctx->tune.lnbwd;

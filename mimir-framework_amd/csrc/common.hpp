@@ -77,6 +77,20 @@ __device__ __forceinline__ float wave_sum(float v) {
     return (readlane(v, 0) + readlane(v, 16)) + (readlane(v, 32) + readlane(v, 48));
 }
 
+// Sum over aligned groups of W lanes (W = 16: a DPP row; W = 32: two rows):
+// every lane of a group ends with the same value, since each step adds a
+// partner's value to its own symmetrically.
+template <int W>
+__device__ __forceinline__ float group_sum(float v) {
+    static_assert(W == 16 || W == 32, "groups of 16 or 32 lanes");
+    v += dpp<kDppQuadXor1>(v);
+    v += dpp<kDppQuadXor2>(v);
+    v += dpp<kDppRowHalfMirror>(v);
+    v += dpp<kDppRowMirror>(v);
+    if constexpr (W == 32) v += __shfl_xor(v, 16);
+    return v;
+}
+
 __device__ __forceinline__ float wave_max(float v) {
     v = fmaxf(v, dpp<kDppQuadXor1>(v));
     v = fmaxf(v, dpp<kDppQuadXor2>(v));
