@@ -11,7 +11,7 @@
 // Work unit ("slot"): 4 consecutive pairs of one head row -- a 16-byte vector
 // from the first half, the matching one from the second half, and the two
 // table vectors.  Q = D/8 slots per head row; q's slots come first, then k's.
-// Each thread handles PPT slots spaced one workgroup-width apart (PPT = 1 by
+// Each thread handles PPT slots spaced one workgroup-width apart (PPT = 4 by
 // default), so a wave instruction reads 4 head rows' half-rows (4 x 256 B
 // for D = 128).
 #include "common.hpp"
@@ -117,13 +117,15 @@ int launch_ppt(mimir_ctx* ctx, const RopeArgs& a) {
     return launched(ctx, "rope_vec");
 }
 
-// One slot per thread streams fastest on MI355X; 2 and 4 stay for sweeps.
+// Four slots per thread (a workgroup-width apart) measured best on MI355X at
+// configs[3] (332 us against 334 us for one and 341 us for two); 1 and 2
+// stay for sweeps (MIMIR_TUNE rope=1 / rope=2).
 template <int LOG2Q>
 int launch_vec(mimir_ctx* ctx, const RopeArgs& a) {
     switch (ctx->tune.rope_ppt) {
+        case 1: return launch_ppt<LOG2Q, 1>(ctx, a);
         case 2: return launch_ppt<LOG2Q, 2>(ctx, a);
-        case 4: return launch_ppt<LOG2Q, 4>(ctx, a);
-        default: return launch_ppt<LOG2Q, 1>(ctx, a);
+        default: return launch_ppt<LOG2Q, 4>(ctx, a);
     }
 }
 

@@ -348,6 +348,37 @@ def test_rope_qk(ctx, B, S, H, Hk, D):
         d.free()
 
 
+@pytest.mark.parametrize("ppt", [1, 2, 4])
+def test_rope_slots_per_thread(ppt):
+    """Each slots-per-thread form of the vector kernel (MIMIR_TUNE rope=n; 4
+    is the default), on a tail that leaves part of the last workgroup's
+    slots empty: q and k match the oracle, the same bits in every form."""
+    import os
+    old = os.environ.get("MIMIR_TUNE")
+    os.environ["MIMIR_TUNE"] = f"rope={ppt}"
+    try:
+        c = M.Context(0)
+    finally:
+        if old is None:
+            del os.environ["MIMIR_TUNE"]
+        else:
+            os.environ["MIMIR_TUNE"] = old
+    B, S, H, Hk, D = 3, 37, 5, 3, 64
+    r = np.random.default_rng(40 + ppt)
+    cos_t, sin_t = M.rope_table(S + 1, D)
+    q = r.standard_normal((B, S, H, D), dtype=np.float32)
+    k = r.standard_normal((B, S, Hk, D), dtype=np.float32)
+    try:
+        dq, dk, dc, ds = c.to_device(q), c.to_device(k), c.to_device(cos_t), c.to_device(sin_t)
+        c.rope(dq, dq, H, dk, dk, Hk, B, S, D, 1, dc, ds, S + 1)
+        assert_close(dq.numpy(), O.rope(q, cos_t, sin_t, 1), f"q rope={ppt}")
+        assert_close(dk.numpy(), O.rope(k, cos_t, sin_t, 1), f"k rope={ppt}")
+        for d in (dq, dk, dc, ds):
+            d.free()
+    finally:
+        c.close()
+
+
 # ---------------------------------------------------------------------------
 # Long rows split over many workgroups (longrow.hip)
 # ---------------------------------------------------------------------------
