@@ -1098,9 +1098,10 @@ int ln_bwd_generic_run(mimir_ctx* ctx, LnBwdArgs a, float* dgamma, float* dbeta,
 // ---------------------------------------------------------------------------
 
 // Sort key of token t: its id, or `vocab` (sorted last, skipped) for the
-// padding id and ids outside [0, vocab) (Model.cpp:7454-7455).  The sort
-// reads the keys through this (a transform iterator over the token index)
-// and the token indices from a counting iterator, so nothing is staged.
+// padding id and ids outside [0, vocab) (Model.cpp:7454-7455).  The counting
+// sort's kernels call it per token; rocPRIM's radix sort reads the keys
+// through it (a transform iterator over the token index) and the token
+// indices from a counting iterator.  Either way nothing is staged.
 template <int MODE>
 struct EmbedKey {
     const void* ids;
@@ -1448,9 +1449,9 @@ __global__ __launch_bounds__(TPT) void embed_bwd_rows_vec(const uint32_t* keys, 
 // The rows kernel and the long runs' first level in one launch, so the two
 // independent streams overlap: blocks [0, nslots) are the segments of
 // embed_bwd_seg_partial (dispatched first, so the long segments start before
-// the short rows), blocks [nslots, nslots + n) embed_bwd_rows_vec's sorted
-// positions,
-// each 1024-thread block summing its segment's rows over whole 16-byte
+// the short rows), the blocks after them embed_bwd_rows_vec's (one per
+// listed run with RUNS, else one per sorted position), the segment blocks
+// each 1024 threads summing their segment's rows over whole 16-byte
 // columns with kMergedSegRows tokens' loads in flight.  The segment path is
 // kept small enough that the kernel stays at 64 registers, so two
 // 1024-thread workgroups still fit a CU (the rows path's turnover needs
@@ -1743,8 +1744,10 @@ int count_sort(mimir_ctx* ctx, const CountSortPlan& p, const void* ids, int64_t 
     return launched(ctx, "embed_sort_scatter");
 }
 
-// The (id, token) sort.  Below rocPRIM's merge-sort limit (2^20 pairs) its
-// device radix sort is a block sort followed by merge passes; 8192-pair
+// The (id, token) sort past the counting sort's limits (more than 64 blocks
+// of tokens or too large a count table): rocPRIM's.  Below its merge-sort
+// limit (2^20 pairs) its device radix sort is a block sort followed by merge
+// passes; 8192-pair
 // blocks (512 threads x 16) need two passes at 32768 tokens.  Measured on
 // MI355X at configs[3] (32768 pairs, 15-bit keys): 28.4 us, against 33.2 us
 // for the default 1024-pair blocks (five passes), 40 us for 16384-pair
