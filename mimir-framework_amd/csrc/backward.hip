@@ -1747,8 +1747,8 @@ int count_sort(mimir_ctx* ctx, const CountSortPlan& p, const void* ids, int64_t 
 // The (id, token) sort past the counting sort's limits (more than 64 blocks
 // of tokens or too large a count table): rocPRIM's.  Below its merge-sort
 // limit (2^20 pairs) its device radix sort is a block sort followed by merge
-// passes; 8192-pair
-// blocks (512 threads x 16) need two passes at 32768 tokens.  Measured on
+// passes; 8192-pair blocks (512 threads x 16) need two passes at 32768
+// tokens.  Measured on
 // MI355X at configs[3] (32768 pairs, 15-bit keys): 28.4 us, against 33.2 us
 // for the default 1024-pair blocks (five passes), 40 us for 16384-pair
 // blocks and 60 us for onesweep.
