@@ -90,77 +90,89 @@ __device__ __forceinline__ double block_sum_f64(double v, double* lds) {
 }
 
 // Pass 1: one chunk's partial statistic.
-template <int S>
+// CPW chunks per workgroup (chunks CPW*b .. CPW*b + CPW - 1 of the row, in
+// the forward order): every chunk's loads are issued before the first
+// chunk's reductions, so a workgroup keeps CPW chunks in flight; each
+// chunk's partial is the one-chunk computation, bit for bit.
+template <int S, int CPW = 1>
 __global__ __launch_bounds__(kBlock) void lr_partial(LongArgs a) {
     __shared__ float lds[2][kBlock / kWave];
     const int64_t row = blockIdx.y;
-    const int64_t chunk = chunk_of(a);
     const int64_t c4n = a.cols >> 2;
     const int64_t base = row * a.cols;
-    f4 v[kChunkVec];
-    bool ok[kChunkVec];
+    f4 vv[CPW][kChunkVec];
+    bool okk[CPW][kChunkVec];
 #pragma unroll
-    for (int j = 0; j < kChunkVec; ++j) {
-        const int64_t c4 = chunk * kChunk4 + static_cast<int64_t>(j) * kBlock + threadIdx.x;
-        ok[j] = c4 < c4n;
-        if constexpr (S == kSumSqAdd) {
-            if (ok[j]) {
-                v[j] = ld4<false>(a.x + base + 4 * c4) + ld4<false>(a.r + base + 4 * c4);
-                st4<false>(a.r_out + base + 4 * c4, v[j]);  // the updated residual, re-read by the last pass
+    for (int i = 0; i < CPW; ++i) {
+        const int64_t chunk = CPW == 1 ? chunk_of(a) : static_cast<int64_t>(blockIdx.x) * CPW + i;
+#pragma unroll
+        for (int j = 0; j < kChunkVec; ++j) {
+            const int64_t c4 = chunk * kChunk4 + static_cast<int64_t>(j) * kBlock + threadIdx.x;
+            okk[i][j] = chunk < a.nchunks && c4 < c4n;
+            if constexpr (S == kSumSqAdd) {
+                if (okk[i][j]) {
+                    vv[i][j] = ld4<false>(a.x + base + 4 * c4) + ld4<false>(a.r + base + 4 * c4);
+                    st4<false>(a.r_out + base + 4 * c4, vv[i][j]);  // the updated residual, re-read by the last pass
+                }
+            } else {
+                if (okk[i][j]) vv[i][j] = ld4<false>(a.x + base + 4 * c4);  // kept in the caches for the next pass
             }
-        } else {
-            if (ok[j]) v[j] = ld4<false>(a.x + base + 4 * c4);  // kept in the caches for the next pass
         }
     }
-    float p0 = 0.0f, p1 = 0.0f;
-    if constexpr (S == kSoftmax) {
-        float m = -INFINITY;
 #pragma unroll
-        for (int j = 0; j < kChunkVec; ++j)
-            if (ok[j]) m = fmaxf(m, fmaxf(fmaxf(v[j].x, v[j].y), fmaxf(v[j].z, v[j].w)));
-        m = block_max<kBlock / kWave>(m, lds[0]);
-        float s = 0.0f;
-        if (m != -INFINITY) {  // an all -inf chunk contributes nothing
+    for (int i = 0; i < CPW; ++i) {
+        const int64_t chunk = CPW == 1 ? chunk_of(a) : static_cast<int64_t>(blockIdx.x) * CPW + i;
+        f4* v = vv[i];
+        const bool* ok = okk[i];
+        float p0 = 0.0f, p1 = 0.0f;
+        if constexpr (S == kSoftmax) {
+            float m = -INFINITY;
 #pragma unroll
             for (int j = 0; j < kChunkVec; ++j)
-                if (ok[j])
-                    s += (expf(v[j].x - m) + expf(v[j].y - m)) + (expf(v[j].z - m) + expf(v[j].w - m));
-        }
-        p0 = m;
-        p1 = block_sum<kBlock / kWave>(s, lds[1]);
-    } else if constexpr (S == kChan) {
-        const float x0 = a.x[base];  // the shift
-        float s = 0.0f;
+                if (ok[j]) m = fmaxf(m, fmaxf(fmaxf(v[j].x, v[j].y), fmaxf(v[j].z, v[j].w)));
+            m = block_max<kBlock / kWave>(m, lds[0]);
+            float s = 0.0f;
+            if (m != -INFINITY) {  // an all -inf chunk contributes nothing
 #pragma unroll
-        for (int j = 0; j < kChunkVec; ++j) {
-            if (!ok[j]) continue;
-            v[j] -= x0;
-            s += (v[j].x + v[j].y) + (v[j].z + v[j].w);
-        }
-        p0 = block_sum<kBlock / kWave>(s, lds[0]);
-        const float mc = p0 / chunk_len(a, chunk);  // recomputed bit for bit by the combine
-        float q = 0.0f;
+                for (int j = 0; j < kChunkVec; ++j)
+                    if (ok[j])
+                        s += (expf(v[j].x - m) + expf(v[j].y - m)) + (expf(v[j].z - m) + expf(v[j].w - m));
+            }
+            p0 = m;
+            p1 = block_sum<kBlock / kWave>(s, lds[1]);
+        } else if constexpr (S == kChan) {
+            const float x0 = a.x[base];  // the shift
+            float s = 0.0f;
 #pragma unroll
-        for (int j = 0; j < kChunkVec; ++j) {
-            if (!ok[j]) continue;
-            const f4 d = v[j] - mc;
-            q += (d.x * d.x + d.y * d.y) + (d.z * d.z + d.w * d.w);
-        }
-        p1 = block_sum<kBlock / kWave>(q, lds[1]);
-    } else {
-        float s = 0.0f;
+            for (int j = 0; j < kChunkVec; ++j) {
+                if (!ok[j]) continue;
+                v[j] -= x0;
+                s += (v[j].x + v[j].y) + (v[j].z + v[j].w);
+            }
+            p0 = block_sum<kBlock / kWave>(s, lds[0]);
+            const float mc = chunk < a.nchunks ? p0 / chunk_len(a, chunk) : 0.0f;  // recomputed bit for bit by the combine
+            float q = 0.0f;
 #pragma unroll
-        for (int j = 0; j < kChunkVec; ++j)
-            if (ok[j]) s += (v[j].x * v[j].x + v[j].y * v[j].y) + (v[j].z * v[j].z + v[j].w * v[j].w);
-        p0 = block_sum<kBlock / kWave>(s, lds[0]);
-    }
-    if (threadIdx.x == 0) {
-        float* p = a.partial + 2 * (row * a.nchunks + chunk);
-        p[0] = p0;
-        p[1] = p1;
+            for (int j = 0; j < kChunkVec; ++j) {
+                if (!ok[j]) continue;
+                const f4 d = v[j] - mc;
+                q += (d.x * d.x + d.y * d.y) + (d.z * d.z + d.w * d.w);
+            }
+            p1 = block_sum<kBlock / kWave>(q, lds[1]);
+        } else {
+            float s = 0.0f;
+#pragma unroll
+            for (int j = 0; j < kChunkVec; ++j)
+                if (ok[j]) s += (v[j].x * v[j].x + v[j].y * v[j].y) + (v[j].z * v[j].z + v[j].w * v[j].w);
+            p0 = block_sum<kBlock / kWave>(s, lds[0]);
+        }
+        if (threadIdx.x == 0 && chunk < a.nchunks) {
+            float* p = a.partial + 2 * (row * a.nchunks + chunk);
+            p[0] = p0;
+            p[1] = p1;
+        }
     }
 }
-
 // Pass 2: fold one row's chunk partials (fixed order) into its statistics.
 //   kChan  -> stats = (mean hi, mean lo, 1/sqrt(var+eps))
 //   kSumSq / kSumSqAdd -> stats = (rms, -) kSoftmax -> stats = (max, sum)
@@ -171,6 +183,22 @@ __global__ __launch_bounds__(kBlock) void lr_partial(LongArgs a) {
 // per chunk.
 constexpr int kCombine = 1024;
 constexpr int kCombineU = 8;
+
+// The first pass over `rows` rows: CPW chunks per workgroup (MIMIR_TUNE
+// lrcpw=1/2/4 overrides).  Measured on MI355X on one 2^25-float row: the
+// LayerNorm statistic (two block reductions per chunk) gains from two chunks
+// per workgroup, 75.2 -> 69.8 us for the whole op, while the one-reduction
+// passes lose 1-2% (softmax 67.2 -> 68.7 us, RMSNorm 65.0 -> 65.9 us) and
+// all lose at four.
+template <int S>
+void launch_partial(mimir_ctx* ctx, const LongArgs& a, int64_t rows) {
+    const int over = ctx->tune.lr_cpw;
+    const int cpw = over == 1 || over == 2 || over == 4 ? over : (S == kChan ? 2 : 1);
+    const dim3 grid(static_cast<unsigned>((a.nchunks + cpw - 1) / cpw), static_cast<unsigned>(rows));
+    if (cpw == 4) lr_partial<S, 4><<<grid, kBlock, 0, ctx->stream>>>(a);
+    else if (cpw == 2) lr_partial<S, 2><<<grid, kBlock, 0, ctx->stream>>>(a);
+    else lr_partial<S, 1><<<grid, kBlock, 0, ctx->stream>>>(a);
+}
 
 template <int S>
 __global__ __launch_bounds__(kCombine) void lr_combine(LongArgs a) {
@@ -332,15 +360,15 @@ int mimir::longrow_norm(mimir_ctx* ctx, int kind, const float* x, const float* r
     LongArgs fwd = a, rev = a;
     rev.reverse = 1;
     if (kind == 0) {
-        lr_partial<kChan><<<grid, kBlock, 0, ctx->stream>>>(fwd);
+        launch_partial<kChan>(ctx, fwd, rows);
         lr_combine<kChan><<<nrows, kCombine, 0, ctx->stream>>>(fwd);
         launch_apply<0, 0>(ctx, grid, rev);
     } else if (kind == 1) {
-        lr_partial<kSumSq><<<grid, kBlock, 0, ctx->stream>>>(fwd);
+        launch_partial<kSumSq>(ctx, fwd, rows);
         lr_combine<kSumSq><<<nrows, kCombine, 0, ctx->stream>>>(fwd);
         launch_apply<1, 0>(ctx, grid, rev);
     } else {
-        lr_partial<kSumSqAdd><<<grid, kBlock, 0, ctx->stream>>>(fwd);
+        launch_partial<kSumSqAdd>(ctx, fwd, rows);
         lr_combine<kSumSqAdd><<<nrows, kCombine, 0, ctx->stream>>>(fwd);
         launch_apply<2, 0>(ctx, grid, rev);
     }
@@ -353,7 +381,7 @@ int mimir::longrow_softmax(mimir_ctx* ctx, int mode, const float* x, float* y, i
     const dim3 grid(static_cast<unsigned>(a.nchunks), static_cast<unsigned>(rows));
     LongArgs rev = a;
     rev.reverse = 1;
-    lr_partial<kSoftmax><<<grid, kBlock, 0, ctx->stream>>>(a);
+    launch_partial<kSoftmax>(ctx, a, rows);
     lr_combine<kSoftmax><<<static_cast<unsigned>(rows), kCombine, 0, ctx->stream>>>(a);
     switch (mode) {
         case MIMIR_SOFTMAX_DIV_EPS: launch_apply<3, MIMIR_SOFTMAX_DIV_EPS>(ctx, grid, rev); break;
@@ -543,7 +571,7 @@ int mimir::longrow_ln_bwd(mimir_ctx* ctx, const float* x, const float* dy, const
     a.stats = a.partial + 2 * rows * a.nchunks;
     float* slot_base = use_slots ? reinterpret_cast<float*>(static_cast<char*>(s) + head) : nullptr;
     const dim3 grid(static_cast<unsigned>(a.nchunks), static_cast<unsigned>(rows));
-    lr_partial<kChan><<<grid, kBlock, 0, ctx->stream>>>(a);
+    launch_partial<kChan>(ctx, a, rows);
     lr_combine<kChan><<<static_cast<unsigned>(rows), kCombine, 0, ctx->stream>>>(a);
     LongBwdArgs b{x, dy, gamma, dx, dgamma, dbeta, rows, cols, a.nchunks, a.stats, a.partial,
                   a.stats + 4 * rows, accumulate ? 1 : 0, aligned16(dgamma) && aligned16(dbeta) ? 1 : 0, slot_base};

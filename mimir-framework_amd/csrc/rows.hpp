@@ -47,7 +47,7 @@ struct RowShape {
 // Tuning override, read once per context from MIMIR_TUNE, e.g.
 //   MIMIR_TUNE="norm=1024x1x1024,layernorm=512x2x512,softmax=64x4x64,ew=1,gather=1024,rope=1,
 //               lnbwd=512x2x512,lnbwd_grid=512,chain=0,attnbwd_heads=4,attnbwd_blocks=2,
-//               embmerge=0,embsort=0,embruns=0,blas=0,lnbwd_narrow=0"
+//               embmerge=0,embsort=0,embruns=0,blas=0,lnbwd_narrow=0,lrcpw=2"
 // Each entry selects among the compiled variants above; an entry that does
 // not fit a call (row too wide for it) is ignored for that call.  Unset, the
 // measured defaults apply.  Used for sweeps; results are identical.
@@ -69,6 +69,7 @@ struct Tuning {
                                 // over the sorted positions (0)
     int blas_lt = -1;           // library products: hipBLASLt first (-1, 1) or rocBLAS only (0)
     int lnbwd_narrow = -1;      // LayerNorm backward, rows <= 64 floats: several rows per wave (-1, 1) or not (0)
+    int lr_cpw = 0;             // long rows: 4096-float chunks per workgroup of the first pass (1, 2, 4; 0: measured default)
 };
 
 inline bool parse_shape(const char* v, RowShape* s) {
@@ -112,6 +113,7 @@ inline Tuning read_tuning() {
         else if (!std::strcmp(k, "embruns")) t.embed_bwd_runs = std::atoi(v);
         else if (!std::strcmp(k, "blas")) t.blas_lt = std::atoi(v);
         else if (!std::strcmp(k, "lnbwd_narrow")) t.lnbwd_narrow = std::atoi(v);
+        else if (!std::strcmp(k, "lrcpw")) t.lr_cpw = std::atoi(v);
     }
     return t;
 }
