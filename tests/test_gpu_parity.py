@@ -383,6 +383,37 @@ def test_rope_slots_per_thread(ppt):
 # Long rows split over many workgroups (longrow.hip)
 # ---------------------------------------------------------------------------
 
+@pytest.mark.parametrize("cpw", [1, 2, 4])
+def test_longrow_chunks_per_workgroup(ctx, cpw):
+    """The long rows' first pass with 1, 2 or 4 chunks per workgroup
+    (MIMIR_TUNE lrcpw; two for LayerNorm and one for the others by default)
+    computes each chunk's partial the same way: LayerNorm and softmax over
+    rows with a partial last chunk and a chunk count that is not a multiple
+    of the chunks per workgroup give the default's bits."""
+    import os
+    old = os.environ.get("MIMIR_TUNE")
+    os.environ["MIMIR_TUNE"] = f"lrcpw={cpw}"
+    try:
+        c = M.Context(0)
+    finally:
+        if old is None:
+            del os.environ["MIMIR_TUNE"]
+        else:
+            os.environ["MIMIR_TUNE"] = old
+    try:
+        rows, cols = 3, 4096 * 7 + 20  # 8 chunks, the last partial
+        x = (rng.standard_normal((rows, cols), dtype=np.float32) * 1.3 + 0.2)
+        g = (1 + 0.05 * rng.standard_normal(cols)).astype(np.float32)
+        b = (0.05 * rng.standard_normal(cols)).astype(np.float32)
+        for name, f in (("layernorm", lambda cc: (lambda dx, dg, db, y: cc.layernorm(dx, dg, db, y, rows, cols, 1e-5))),
+                        ("softmax", lambda cc: (lambda dx, dg, db, y: cc.softmax(dx, y, rows, cols)))):
+            got = run(c, f(c), x, g, b, out_shape=x.shape)
+            want = run(ctx, f(ctx), x, g, b, out_shape=x.shape)
+            assert_bitexact(got, want, f"{name} lrcpw={cpw}")
+    finally:
+        c.close()
+
+
 @pytest.mark.parametrize("rows,cols", [(1, 1 << 20), (3, 65536), (2, 20004), (1, 4097 * 4), (2, 20001),
                                        (300, 20004)])
 def test_longrow_layernorm_rmsnorm(ctx, rows, cols):
