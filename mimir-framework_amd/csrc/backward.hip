@@ -1683,7 +1683,7 @@ __global__ __launch_bounds__(kSortBlock) void embed_sort_scatter(const void* ids
 struct CountSortPlan {
     bool ok = false;
     bool runs = false;  // also the run list
-    int64_t n = 0, nb = 0, v1 = 0, pitch = 0, nchunks = 0;
+    int64_t nb = 0, v1 = 0, pitch = 0, nchunks = 0;
     uint32_t end_bit = 0;
     size_t cnt_bytes = 0, start_bytes = 0, rank_bytes = 0, chunk_bytes = 0;
     size_t key_bytes = 0, list_bytes = 0;  // the run list's per-key arrays (x2), its count and entries
@@ -1706,7 +1706,6 @@ CountSortPlan count_sort_plan(int64_t n, int32_t vocab, bool runs) {
     p.start_bytes = align256(sizeof(uint32_t) * static_cast<size_t>(p.nb * p.pitch));
     p.rank_bytes = align256(sizeof(uint16_t) * static_cast<size_t>(p.nb * kSortBlock));
     p.chunk_bytes = align256(sizeof(uint32_t) * static_cast<size_t>(p.nchunks));
-    p.n = n;
     p.runs = runs;
     p.key_bytes = align256(sizeof(uint32_t) * static_cast<size_t>(p.v1));
     p.list_bytes = 256 + align256(sizeof(RunEntry) * static_cast<size_t>(n));
