@@ -91,6 +91,7 @@ struct LtPlan {
 // (trans_a, trans_b, m, n, k, lda, ldb, ldc, stride_a, stride_b, stride_c, batch) of the column-major call
 using LtKey = std::tuple<int, int, int64_t, int64_t, int64_t, int64_t, int64_t, int64_t, int64_t, int64_t, int64_t,
                          int64_t>;
+constexpr size_t kMaxPlans = 1024;
 struct LtState {
     hipblasLtHandle_t handle = nullptr;
     bool failed = false;  // the handle could not be created: rocBLAS only
@@ -138,6 +139,13 @@ LtPlan* plan_of(mimir_ctx* ctx, LtState* s, bool ta, bool tb, int64_t m, int64_t
     const LtKey key{ta, tb, m, n, k, lda, ldb, ldc, sa, sb, sc, batch};
     auto it = s->plans.find(key);
     if (it != s->plans.end()) return &it->second;
+    // Shapes vary with sequence lengths: past kMaxPlans the cache starts over
+    // rather than growing without bound (a plan is a host-side heuristic
+    // query away).  Plans are only used within the call that looks them up.
+    if (s->plans.size() >= kMaxPlans) {
+        for (auto& kv : s->plans) destroy_plan(kv.second);
+        s->plans.clear();
+    }
     LtPlan p;
     const int32_t opa = ta ? HIPBLAS_OP_T : HIPBLAS_OP_N, opb = tb ? HIPBLAS_OP_T : HIPBLAS_OP_N;
     bool good = hipblasLtMatmulDescCreate(&p.desc, HIPBLAS_COMPUTE_32F, HIP_R_32F) == HIPBLAS_STATUS_SUCCESS &&
