@@ -1253,9 +1253,12 @@ def main():
         if t is not None:
             r["traffic_bytes"] = t["traffic_bytes"]
             r["traffic_over_algorithmic"] = t["traffic_over_algorithmic"]
-            for k in ("distinct_row_bytes", "distinct_row_GB_s_at_profiled_time"):
-                if k in t:
-                    r[k] = t[k]
+            if "distinct_row_bytes" in t:
+                # The gather counted by the table rows it must read at least
+                # once (repeated ids may be served by L2 or the Infinity Cache).
+                r["distinct_row_bytes"] = t["distinct_row_bytes"]
+                r["distinct_row_GB_s"] = round(t["distinct_row_bytes"] / (r["us_per_launch"] * 1e3), 1)
+                r["distinct_row_frac_of_peak"] = round(r["distinct_row_GB_s"] / PEAK_GBS, 4)
 
     traffic = load_traffic(head.key)
     host = {"cpu_model": cpu_model(), "nproc": os.cpu_count()}
