@@ -224,8 +224,12 @@ __global__ __launch_bounds__(kBlock) void add_bwd_vec(const float* dy, float* da
     const int64_t i = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
     if (i >= n4) return;
     const f4 g = ld4<true>(dy + 4 * i);
-    if (da) st_out<KEEP>(da + 4 * i, ACC_A ? ld4<true>(da + 4 * i) + g : g);
-    if (db) st_out<KEEP>(db + 4 * i, ACC_B ? ld4<true>(db + 4 * i) + g : g);
+    // Every load before the stores, which are written through (two output
+    // streams per input stream).
+    const f4 oa = ACC_A && da ? ld4<true>(da + 4 * i) + g : g;
+    const f4 ob = ACC_B && db ? ld4<true>(db + 4 * i) + g : g;
+    if (da) st_out<KEEP, kStoreThrough>(da + 4 * i, oa);
+    if (db) st_out<KEEP, kStoreThrough>(db + 4 * i, ob);
 }
 
 template <bool KEEP>
@@ -487,7 +491,7 @@ __global__ __launch_bounds__(kBlock) void add_bcast_part(const float* dy, float*
                     for (int u = 0; u < 4; ++u)
                         o[u] = acc_big ? __builtin_nontemporal_load(dst + (r + u * L) * w4) + v[u] : v[u];
 #pragma unroll
-                    for (int u = 0; u < 4; ++u) __builtin_nontemporal_store(o[u], dst + (r + u * L) * w4);
+                    for (int u = 0; u < 4; ++u) st_stream(dst + (r + u * L) * w4, o[u]);
                 }
 #pragma unroll
                 for (int u = 0; u < 4; ++u) s += (same ? o[u] : v[u]);
@@ -497,7 +501,7 @@ __global__ __launch_bounds__(kBlock) void add_bcast_part(const float* dy, float*
                 f4 o = v;
                 if (dst) {
                     o = acc_big ? __builtin_nontemporal_load(dst + r * w4) + v : v;
-                    __builtin_nontemporal_store(o, dst + r * w4);
+                    st_stream(dst + r * w4, o);
                 }
                 s += (same ? o : v);
             }
@@ -552,7 +556,7 @@ __global__ __launch_bounds__(kBlock) void add_total_part(const float* dy, float*
                 for (int u = 0; u < 4; ++u)
                     o[u] = acc_big ? __builtin_nontemporal_load(dst + i + u * kBlock) + v[u] : v[u];
 #pragma unroll
-                for (int u = 0; u < 4; ++u) __builtin_nontemporal_store(o[u], dst + i + u * kBlock);
+                for (int u = 0; u < 4; ++u) st_stream(dst + i + u * kBlock, o[u]);
             }
 #pragma unroll
             for (int u = 0; u < 4; ++u) acc += (same ? o[u] : v[u]);
@@ -562,7 +566,7 @@ __global__ __launch_bounds__(kBlock) void add_total_part(const float* dy, float*
             f4 o = v;
             if (dst) {
                 o = acc_big ? __builtin_nontemporal_load(dst + i) + v : v;
-                __builtin_nontemporal_store(o, dst + i);
+                st_stream(dst + i, o);
             }
             acc += (same ? o : v);
         }
@@ -897,7 +901,7 @@ __global__ __launch_bounds__(kBlock) void ln_bwd_scalar(LnBwdArgs a) {
                 float o = k * ((n * dxh - s1) - xh * s2);
                 if (a.acc) o = a.dx[off + c] + o;
                 if constexpr (KEEP) a.dx[off + c] = o;
-                else __builtin_nontemporal_store(o, a.dx + off + c);
+                else st_stream(a.dx + off + c, o);
             }
         }
 #pragma unroll
@@ -1317,7 +1321,7 @@ __global__ __launch_bounds__(kWave * kCombineGroups) void embed_bwd_seg_combine(
             gv += acc;  // group 0 always holds slot m0
             for (int q = 1; q < kCombineGroups; ++q)
                 if (m0 + q < m1) gv += sums[q - 1][lane];
-            __builtin_nontemporal_store(gv, g + c);
+            st_stream(g + c, gv);
         }
         __syncthreads();  // sums is reused by the next item
     }
@@ -1384,7 +1388,7 @@ __device__ __forceinline__ void embed_rows_sum(int64_t i, int64_t end, uint32_t 
 #pragma unroll
         for (int k = 0; k < CPT; ++k) {
             const int64_t c = c0 + static_cast<int64_t>(k) * TPT;
-            if (c < dim4) __builtin_nontemporal_store(acc[k], g + c);
+            if (c < dim4) st_stream(g + c, acc[k]);
         }
         c0 += static_cast<int64_t>(TPT) * CPT;
         if (c0 < dim4) embed_rows_load<TPT, CPT>(g, src, t0, c0, dim4, acc, v);
@@ -1920,7 +1924,7 @@ int layernorm_bwd(mimir_ctx* ctx, const float* x, const float* dy, const float* 
     }
     if (vec) {
         const RowShape over = ctx->tune.lnbwd;
-        const RowShape s = shape_fits(over, c4) ? over : default_norm_shape(c4);
+        const RowShape s = shape_fits(over, c4) ? over : default_lnbwd_shape(c4);
 #define MIMIR_LNBWD_CASE(T, V, B) \
         if (s.tpr == T && s.vpt == V && s.bs == B) return launch_ln_bwd_vec<T, V, B>(ctx, a, dgamma, dbeta, fixed);
         MIMIR_ROW_SHAPES(MIMIR_LNBWD_CASE)

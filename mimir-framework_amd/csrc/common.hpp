@@ -28,23 +28,78 @@ __device__ __forceinline__ f4 ld4(const float* p) {
     else return *reinterpret_cast<const f4*>(p);
 }
 
+// Streaming stores: data written once and not read again by this kernel,
+// with one of two cache policies, chosen per kernel by measurement:
+//   kStoreNt       `nt`: the line enters the XCD's L2 with a streaming hint
+//                  and reaches HBM when L2 writes it back;
+//   kStoreThrough  `sc1 nt`: device scope, so L2 writes the line through to
+//                  memory at once and holds no dirty copy.  Measured on
+//                  MI355X it lifts write-heavy streams (RoPE, GELU, the add
+//                  backward's two outputs) by 1-3 points and costs the
+//                  read-heavy ones (add, SiLU-gated product, the row ops) 1-2.
+// The non-temporal form is the compiler's store with its non-temporal hint.
+// The hint is metadata that loop-invariant code motion drops when it sinks
+// a store out of a one-trip loop (a VPT = 1 kernel), so the address first
+// passes through an empty volatile asm, which no pass can move or see
+// through.  The write-through form has no builtin and is inline assembly;
+// the compiler does not count it in its waits, and a gfx9 wave's vmcnt is
+// in order, so a later wait for a load issued before such a store also
+// waits for the store: use it where every load precedes every store.
+enum : int { kStoreNt = 0, kStoreThrough = 1 };
+
+// A pointer into global memory (address space 1), so stores through it are
+// global_store, not flat_store.
+template <typename T>
+using gptr = __attribute__((address_space(1))) T*;
+
+template <int POL = kStoreNt>
+__device__ __forceinline__ void st_stream(void* p, u4 v) {
+    if constexpr (POL == kStoreThrough) {
+        asm volatile("global_store_dwordx4 %0, %1, off sc1 nt" : : "v"(p), "v"(v) : "memory");
+    } else {
+        gptr<u4> g = (gptr<u4>)p;
+        asm volatile("" : "+v"(g));
+        __builtin_nontemporal_store(v, g);
+    }
+}
+
+template <int POL = kStoreNt>
+__device__ __forceinline__ void st_stream(float* p, f4 v) {
+    st_stream<POL>(static_cast<void*>(p), __builtin_bit_cast(u4, v));
+}
+template <int POL = kStoreNt>
+__device__ __forceinline__ void st_stream(f4* p, f4 v) {
+    st_stream<POL>(static_cast<void*>(p), __builtin_bit_cast(u4, v));
+}
+
+template <int POL = kStoreNt>
+__device__ __forceinline__ void st_stream(float* p, float v) {
+    if constexpr (POL == kStoreThrough) {
+        asm volatile("global_store_dword %0, %1, off sc1 nt" : : "v"(p), "v"(v) : "memory");
+    } else {
+        gptr<float> g = (gptr<float>)p;
+        asm volatile("" : "+v"(g));
+        __builtin_nontemporal_store(v, g);
+    }
+}
+
 template <bool NT>
 __device__ __forceinline__ void st4(float* p, f4 v) {
-    if constexpr (NT) __builtin_nontemporal_store(v, reinterpret_cast<f4*>(p));
+    if constexpr (NT) st_stream(p, v);
     else *reinterpret_cast<f4*>(p) = v;
 }
 
-// An op's output: streamed (non-temporal) unless KEEP, in which case a plain
-// store leaves the line in L2 / the Infinity Cache for the op launched next.
-// Measured on MI355X, producer -> consumer through a 128 MiB tensor: 79 us
-// with kept outputs, 92 us streamed; an op whose output is not read next is
-// ~3% faster streamed.  KEEP is a template parameter, chosen per launch: a
-// run-time flag lets the compiler merge the two stores into one plain store
-// and drop the non-temporal hint.
-template <bool KEEP>
+// An op's output: streamed unless KEEP, in which case a plain store leaves
+// the line in L2 / the Infinity Cache for the op launched next.  Measured on
+// MI355X, producer -> consumer through a 128 MiB tensor: 79 us with kept
+// outputs, 92 us streamed; an op whose output is not read next is ~3% faster
+// streamed.  KEEP is a template parameter, chosen per launch: a run-time
+// flag lets the compiler merge the two stores into one plain store and drop
+// the streaming policy.
+template <bool KEEP, int POL = kStoreNt>
 __device__ __forceinline__ void st_out(float* p, f4 v) {
     if constexpr (KEEP) *reinterpret_cast<f4*>(p) = v;
-    else __builtin_nontemporal_store(v, reinterpret_cast<f4*>(p));
+    else st_stream<POL>(p, v);
 }
 
 // ---------------------------------------------------------------------------

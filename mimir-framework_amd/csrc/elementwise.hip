@@ -74,7 +74,7 @@ __global__ __launch_bounds__(kBlock) void unary_vec(const float* x, float* y, in
 #pragma unroll
     for (int j = 0; j < VPT; ++j) {
         const int64_t i = first + static_cast<int64_t>(j) * kBlock;
-        if (i < n4) st_out<KEEP>(y + 4 * i, map4(f, v[j]));
+        if (i < n4) st_out<KEEP, kStoreThrough>(y + 4 * i, map4(f, v[j]));  // one read, one write: written through
     }
 }
 

@@ -51,7 +51,7 @@ __global__ __launch_bounds__(BS) void embed_vec(GatherArgs a) {
     for (int64_t c = t; c < dim4; c += TPT) {
         const u4 v = copy ? src[c] : u4(0u);
         if constexpr (KEEP) dst[c] = v;
-        else __builtin_nontemporal_store(v, dst + c);
+        else st_stream(dst + c, v);
     }
 }
 

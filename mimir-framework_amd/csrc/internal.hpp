@@ -31,6 +31,9 @@ struct mimir_ctx {
     // Device address of this GPU's fixed scratch array (backward.hip), for
     // the entry point that allocates nothing; set at context creation.
     void* noalloc_scratch = nullptr;
+    // This GPU's columns of 1.0f then -0.0f (mimir::kUnitCols each), the
+    // weights of a row kernel's absent scale / bias (norm.hip).
+    const float* unit_weights = nullptr;
     // hipBLASLt state (handle and per-shape plans) and rocBLAS handle for the
     // attention layers' products (gemm.hip), created on first use, sharing a
     // workspace of this library's (grown on demand).
@@ -171,6 +174,10 @@ int layernorm_fused(mimir_ctx* ctx, const LnFused& f);
 // Look up this context's device address of the no-allocation scratch array
 // (backward.hip); called once per context, with its device current.
 int noalloc_scratch_init(mimir_ctx* ctx);
+// Widest row (floats) the register-resident row kernels hold, and the
+// per-GPU set-up of their unit weights (norm.hip), run at context creation.
+constexpr int kUnitCols = 4 * 4096;
+int norm_init(mimir_ctx* ctx);
 
 // Scratch for one call: a fixed span (the no-allocation entry point's device
 // array) or, when `fixed` is null, the context's growable scratch.  A fixed

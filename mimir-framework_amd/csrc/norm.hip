@@ -26,6 +26,7 @@
 
 using namespace mimir;
 
+
 namespace {
 
 // AddLayer: the runtime's fused Add -> LayerNorm (h = x + r, written when
@@ -43,6 +44,8 @@ struct NormArgs {
     int64_t cols;
     int64_t w_len;    // RMSNorm: weight applies to columns < w_len
     float eps;
+    float inv_n;      // 1 / cols (set at launch)
+    const float* wp;  // RMSNorm weight shorter than the row (set at launch; g is then 1.0)
     // LayerNorm epilogue (the runtime's fusion): a chain of elementwise
     // steps on the normalised value before it is stored (y, when set, gets
     // the LayerNorm output itself); operands index epi.ins.
@@ -62,83 +65,169 @@ __device__ __forceinline__ f4 rms_scale(f4 o, const float* w, int64_t w_len, int
     return o;
 }
 
+// 1.0f and -0.0f for every column a vector row kernel holds, on each GPU,
+// standing in for an absent scale and bias (filled at context creation).
+__device__ __align__(16) float unit_weights[2][kUnitCols];
+
+__global__ __launch_bounds__(kBlock) void fill_unit_weights(float* p) {
+    const int i = blockIdx.x * kBlock + threadIdx.x;
+    if (i < kUnitCols) {
+        p[i] = 1.0f;
+        p[kUnitCols + i] = -0.0f;
+    }
+}
+
+// The instruction budget of these kernels is tight: at 8 TB/s one SIMD's
+// share of HBM moves a wave's 4 KiB (1 KiB loaded and stored per row slice
+// and tensor) in about 1300 cycles, ~320 wave64 VALU instructions, so every
+// per-element divide and bounds mask shows in the rate.  FULL: the row fills
+// every thread slot (cols == 4*TPR*VPT and no row past the end), so no
+// column is masked.  Per element the divisions of the reference become
+// multiplications by per-row reciprocals (1/n from the host, v_rsq for
+// 1/sqrt): within 2 ulp of the divided form.
+//
 // KEEP: y through the caches (mimir_ctx_set_output_caching); r_out is always
 // streamed (it is read by a later block, not the next op).  EPI: the
 // LayerNorm output goes through a.epi before it is stored.
-template <Norm K, int TPR, int VPT, int BS, bool KEEP, bool EPI = false>
+template <Norm K, int TPR, int VPT, int BS, bool KEEP, bool EPI, bool FULL>
 __global__ __launch_bounds__(BS) void norm_rows_vec(NormArgs a) {
     constexpr int RPB = BS / TPR;  // rows per workgroup
     constexpr int NW = TPR / kWave;  // waves per row
-    __shared__ float lds[2][BS / kWave];
+    __shared__ __attribute__((aligned(16))) float lds[2][BS / kWave];
     const int t = threadIdx.x % TPR;
     const int sub = threadIdx.x / TPR;
     const int64_t row = static_cast<int64_t>(blockIdx.x) * RPB + sub;
-    if constexpr (NW == 1) {
+    if constexpr (NW == 1 && !FULL) {
         if (row >= a.rows) return;  // whole wavefront leaves together
     }
     // Rows past the end (only in the last workgroup) keep taking part in the
     // workgroup barriers but touch no memory.
-    const int64_t c4n = row < a.rows ? (a.cols >> 2) : 0;
-    const int64_t base = row * a.cols;
+    const int c4n = FULL ? TPR * VPT : (row < a.rows ? static_cast<int>(a.cols >> 2) : 0);
+    auto live = [&](int j) { return FULL || j * TPR + t < c4n; };
+    const float* x = a.x + row * a.cols + 4 * t;
+    float* y = a.y + row * a.cols + 4 * t;
 
     // LayerNorm: issue the row's loads at raised wave priority, so the loads
     // of resident rows are not held up behind other waves' reduction math.
     constexpr bool kLayer = K == Norm::Layer || K == Norm::AddLayer;
     if constexpr (kLayer) __builtin_amdgcn_s_setprio(3);
-    f4 v[VPT];
+    // The per-column weights (L2-resident) are loaded right behind the row,
+    // with no condition: an absent scale or bias arrives as the context's
+    // 1.0 / -0.0 columns (x * 1 and x + (-0) are x exactly).  A conditional
+    // or later load would put its latency after the reduction, or make the
+    // reduction wait for it.
+    f4 v[VPT], gv[VPT], bv[VPT];
+    auto load_weights = [&]() {
+#pragma unroll
+        for (int j = 0; j < VPT; ++j) {
+            const int c4 = j * TPR + t;
+            gv[j] = live(j) ? *reinterpret_cast<const f4*>(a.g + 4 * c4) : f4(0.0f);
+            if constexpr (kLayer) bv[j] = live(j) ? *reinterpret_cast<const f4*>(a.b + 4 * c4) : f4(0.0f);
+        }
+    };
     if constexpr (K == Norm::AddRms || K == Norm::AddLayer) {
+        const float* r = a.r + row * a.cols + 4 * t;
         f4 rr[VPT];
 #pragma unroll
         for (int j = 0; j < VPT; ++j) {
-            const int64_t c4 = static_cast<int64_t>(j) * TPR + t;
-            const bool ok = c4 < c4n;
-            v[j] = ok ? ld4<true>(a.x + base + 4 * c4) : f4(0.0f);
-            rr[j] = ok ? ld4<true>(a.r + base + 4 * c4) : f4(0.0f);
+            v[j] = live(j) ? ld4<true>(x + 4 * j * TPR) : f4(0.0f);
+            rr[j] = live(j) ? ld4<true>(r + 4 * j * TPR) : f4(0.0f);
         }
+        if constexpr (kLayer) __builtin_amdgcn_s_setprio(0);
+        load_weights();
+        float* ro = a.r_out + row * a.cols + 4 * t;
 #pragma unroll
         for (int j = 0; j < VPT; ++j) {
-            const int64_t c4 = static_cast<int64_t>(j) * TPR + t;
             v[j] = v[j] + rr[j];  // one IEEE add per element, as add_forward
-            if (c4 < c4n && (K == Norm::AddRms || a.r_out)) st4<true>(a.r_out + base + 4 * c4, v[j]);
+            // add + RMSNorm's updated residual: a plain store, measured
+            // faster than a streamed one beside the streamed y (79.4 against
+            // 75.4% of 8 TB/s at configs[1]).  The runtime's fused Add ->
+            // LayerNorm streams its sum (a later block reads it).
+            if (live(j) && (K == Norm::AddRms || a.r_out)) st4<K == Norm::AddLayer>(ro + 4 * j * TPR, v[j]);
         }
     } else {
 #pragma unroll
-        for (int j = 0; j < VPT; ++j) {
-            const int64_t c4 = static_cast<int64_t>(j) * TPR + t;
-            v[j] = (c4 < c4n) ? ld4<true>(a.x + base + 4 * c4) : f4(0.0f);
-        }
+        for (int j = 0; j < VPT; ++j) v[j] = live(j) ? ld4<true>(x + 4 * j * TPR) : f4(0.0f);
+        if constexpr (kLayer) __builtin_amdgcn_s_setprio(0);
+        load_weights();
     }
 
-    if constexpr (kLayer) __builtin_amdgcn_s_setprio(0);
-
-    const float n = static_cast<float>(a.cols);
     if constexpr (kLayer) {
         float s = 0.0f;
 #pragma unroll
         for (int j = 0; j < VPT; ++j) s += (v[j].x + v[j].y) + (v[j].z + v[j].w);
-        const float mean = row_sum<NW, false>(s, lds[0], sub) / n;
-        float q = 0.0f;
+        const float sw = wave_sum(s);
+        float mean, var;
+        if constexpr (NW == 1) {
+            mean = sw * a.inv_n;
+            float q = 0.0f;
 #pragma unroll
-        for (int j = 0; j < VPT; ++j) {
-            const int64_t c4 = static_cast<int64_t>(j) * TPR + t;
-            if (c4 < c4n) {
-                const f4 d = v[j] - mean;
+            for (int j = 0; j < VPT; ++j) {
+                if (live(j)) {
+                    const f4 d = v[j] - mean;
+                    q += (d.x * d.x + d.y * d.y) + (d.z * d.z + d.w * d.w);
+                }
+            }
+            var = wave_sum(q) * a.inv_n;
+        } else if constexpr (FULL) {
+            // Mean and variance with one exchange between the row's waves.
+            // Each wave holds kPer = 256*VPT values (a power of two, so its
+            // mean S_w * (1/kPer) is exact) and reduces them to (S_w, M2_w
+            // about its own mean); one LDS round combines the parts by the
+            // pairwise update of Chan, Golub and LeVeque (1979):
+            //   mean = sum_w S_w / n,  M2 = sum_w M2_w + kPer * sum_w (S_w/kPer - mean)^2,
+            // the reference's two-pass mean and variance, regrouped.
+            constexpr float kPer = 256.0f * VPT;
+            constexpr float kInvPer = 1.0f / kPer;
+            const float mw = sw * kInvPer;
+            float q = 0.0f;
+#pragma unroll
+            for (int j = 0; j < VPT; ++j) {
+                const f4 d = v[j] - mw;
                 q += (d.x * d.x + d.y * d.y) + (d.z * d.z + d.w * d.w);
             }
+            const float m2w = wave_sum(q);
+            float2* part = reinterpret_cast<float2*>(&lds[0][0]);
+            if ((threadIdx.x & (kWave - 1)) == 0) part[threadIdx.x / kWave] = make_float2(sw, m2w);
+            __syncthreads();
+            float2 p[NW];
+#pragma unroll
+            for (int i = 0; i < NW; ++i) p[i] = part[sub * NW + i];
+            float S = 0.0f;
+#pragma unroll
+            for (int i = 0; i < NW; ++i) S += p[i].x;
+            mean = S * a.inv_n;
+            float M2 = 0.0f, D = 0.0f;
+#pragma unroll
+            for (int i = 0; i < NW; ++i) {
+                const float d = p[i].x * kInvPer - mean;
+                M2 += p[i].y;
+                D += d * d;
+            }
+            var = (M2 + kPer * D) * a.inv_n;
+        } else {
+            // Partial rows: waves hold different counts; two exchanges, the
+            // plain two-pass order.
+            mean = row_sum<NW, false>(s, lds[0], sub) * a.inv_n;
+            float q = 0.0f;
+#pragma unroll
+            for (int j = 0; j < VPT; ++j) {
+                if (live(j)) {
+                    const f4 d = v[j] - mean;
+                    q += (d.x * d.x + d.y * d.y) + (d.z * d.z + d.w * d.w);
+                }
+            }
+            var = row_sum<NW, false>(q, lds[1], sub) * a.inv_n;
         }
-        const float var = row_sum<NW, false>(q, lds[1], sub) / n;
-        const float inv_std = 1.0f / sqrtf(var + a.eps);
+        const float inv_std = __builtin_amdgcn_rsqf(var + a.eps);
 #pragma unroll
         for (int j = 0; j < VPT; ++j) {
-            const int64_t c4 = static_cast<int64_t>(j) * TPR + t;
-            if (c4 < c4n) {
+            if (live(j)) {
+                const int c4 = j * TPR + t;
                 f4 o = (v[j] - mean) * inv_std;
-                if (a.g) {
-                    o *= *reinterpret_cast<const f4*>(a.g + 4 * c4);
-                    if (a.b) o += *reinterpret_cast<const f4*>(a.b + 4 * c4);
-                }
+                o = o * gv[j] + bv[j];
                 if constexpr (EPI) {
-                    const int64_t off = base + 4 * c4;
+                    const int64_t off = row * a.cols + 4 * c4;
                     const int ns = a.epi.n_steps;
                     if (a.y) {
                         if (ns == 0) st_out<KEEP>(a.y + off, o);
@@ -155,7 +244,7 @@ __global__ __launch_bounds__(BS) void norm_rows_vec(NormArgs a) {
                         }
                     }
                 } else {
-                    st_out<KEEP>(a.y + base + 4 * c4, o);
+                    st_out<KEEP>(y + 4 * j * TPR, o);
                 }
             }
         }
@@ -164,14 +253,15 @@ __global__ __launch_bounds__(BS) void norm_rows_vec(NormArgs a) {
 #pragma unroll
         for (int j = 0; j < VPT; ++j)
             q += (v[j].x * v[j].x + v[j].y * v[j].y) + (v[j].z * v[j].z + v[j].w * v[j].w);
-        const float rms = sqrtf(row_sum<NW, false>(q, lds[0], sub) / n + a.eps);
+        const float inv_rms = __builtin_amdgcn_rsqf(row_sum<NW, false>(q, lds[0], sub) * a.inv_n + a.eps);
 #pragma unroll
         for (int j = 0; j < VPT; ++j) {
-            const int64_t c4 = static_cast<int64_t>(j) * TPR + t;
-            if (c4 < c4n) {
-                f4 o = v[j] / rms;
-                if (a.g) o = rms_scale(o, a.g, a.w_len, 4 * c4);
-                st_out<KEEP>(a.y + base + 4 * c4, o);
+            if (live(j)) {
+                const int c4 = j * TPR + t;
+                f4 o = v[j] * inv_rms * gv[j];
+                // A weight shorter than the row scales its prefix only.
+                if (a.wp) o = rms_scale(o, a.wp, a.w_len, 4 * c4);
+                st_out<KEEP>(y + 4 * j * TPR, o);
             }
         }
     }
@@ -233,12 +323,31 @@ __global__ __launch_bounds__(kBlock) void norm_rows_generic(NormArgs a) {
 }
 
 template <Norm K, int TPR, int VPT, int BS, bool EPI = false>
-int launch_vec(mimir_ctx* ctx, const NormArgs& a) {
+int launch_vec(mimir_ctx* ctx, const NormArgs& args) {
     unsigned blocks;
-    if (!grid_for(a.rows, BS / TPR, &blocks))
-        return fail(ctx, MIMIR_EINVAL, "norm: %lld rows exceed the grid limit", (long long)a.rows);
-    if (ctx->keep_outputs) norm_rows_vec<K, TPR, VPT, BS, true, EPI><<<blocks, BS, 0, ctx->stream>>>(a);
-    else norm_rows_vec<K, TPR, VPT, BS, false, EPI><<<blocks, BS, 0, ctx->stream>>>(a);
+    if (!grid_for(args.rows, BS / TPR, &blocks))
+        return fail(ctx, MIMIR_EINVAL, "norm: %lld rows exceed the grid limit", (long long)args.rows);
+    NormArgs a = args;
+    a.inv_n = 1.0f / static_cast<float>(a.cols);
+    const float* one = ctx->unit_weights;
+    const float* negzero = one + kUnitCols;
+    if constexpr (K == Norm::Layer || K == Norm::AddLayer) {
+        if (!a.g) a.g = one;
+        if (!a.b) a.b = negzero;
+    } else if (!a.g) {
+        a.g = one;
+    } else if (a.w_len < a.cols) {
+        a.wp = a.g;
+        a.g = one;
+    }
+    const bool full = a.cols == 4LL * TPR * VPT && a.rows % (BS / TPR) == 0;
+    if (ctx->keep_outputs) {
+        if (full) norm_rows_vec<K, TPR, VPT, BS, true, EPI, true><<<blocks, BS, 0, ctx->stream>>>(a);
+        else norm_rows_vec<K, TPR, VPT, BS, true, EPI, false><<<blocks, BS, 0, ctx->stream>>>(a);
+    } else {
+        if (full) norm_rows_vec<K, TPR, VPT, BS, false, EPI, true><<<blocks, BS, 0, ctx->stream>>>(a);
+        else norm_rows_vec<K, TPR, VPT, BS, false, EPI, false><<<blocks, BS, 0, ctx->stream>>>(a);
+    }
     return launched(ctx, "norm_rows_vec");
 }
 
@@ -249,7 +358,7 @@ int launch_vec(mimir_ctx* ctx, const NormArgs& a) {
     X(128, 1, 256)               \
     X(64, 4, 64)                 \
     X(512, 1, 512)               \
-    X(512, 2, 512)               \
+    X(256, 4, 256)               \
     X(512, 4, 512)               \
     X(1024, 4, 1024)
 
@@ -282,13 +391,13 @@ __global__ __launch_bounds__(kBlock) void norm_rows_scalar(NormArgs a) {
         for (int j = 0; j < VPT; ++j) {
             const int64_t c = static_cast<int64_t>(j) * kBlock + t;
             v[j] = v[j] + rr[j];
-            if (c < a.cols) __builtin_nontemporal_store(v[j], a.r_out + base + c);
+            if (c < a.cols) st_stream(a.r_out + base + c, v[j]);
         }
     }
     const float n = static_cast<float>(a.cols);
     auto put = [&](int64_t c, float o) {
         if constexpr (KEEP) a.y[base + c] = o;
-        else __builtin_nontemporal_store(o, a.y + base + c);
+        else st_stream(a.y + base + c, o);
     };
     if constexpr (K == Norm::Layer) {
         float s = 0.0f;
@@ -371,6 +480,18 @@ int dispatch(mimir_ctx* ctx, const NormArgs& a) {
 }
 
 }  // namespace
+
+int mimir::norm_init(mimir_ctx* ctx) {
+    void* p = nullptr;
+    hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(unit_weights));
+    if (e != hipSuccess) return hip_fail(ctx, e, "hipGetSymbolAddress(unit_weights)");
+    fill_unit_weights<<<(kUnitCols + kBlock - 1) / kBlock, kBlock, 0, ctx->stream>>>(static_cast<float*>(p));
+    if (int st = launched(ctx, "fill_unit_weights")) return st;
+    e = hipStreamSynchronize(ctx->stream);
+    if (e != hipSuccess) return hip_fail(ctx, e, "hipStreamSynchronize");
+    ctx->unit_weights = static_cast<const float*>(p);
+    return MIMIR_OK;
+}
 
 bool mimir::layernorm_fusable(const mimir_ctx* ctx, int64_t cols, const float* g, const float* b) {
     if (cols <= 0 || cols % 4 != 0 || (g && !aligned16(g)) || (b && !aligned16(b))) return false;

@@ -79,8 +79,9 @@ __global__ __launch_bounds__(kBlock) void rope_vec(RopeArgs a) {
     for (int j = 0; j < PPT; ++j) {
         if (out[j]) {
             rotate(x0[j], x1[j], c[j], s[j]);
-            st_out<KEEP>(out[j], x0[j]);
-            st_out<KEEP>(out[j] + a.half, x1[j]);
+            // Write-through stores: RoPE writes as much as it reads.
+            st_out<KEEP, kStoreThrough>(out[j], x0[j]);
+            st_out<KEEP, kStoreThrough>(out[j] + a.half, x1[j]);
         }
     }
 }

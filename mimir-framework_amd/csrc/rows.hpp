@@ -124,13 +124,25 @@ inline RowShape default_norm_shape(int64_t c4) {
     if (c4 <= 128) return {128, 1, 256};
     if (c4 <= 256) return {64, 4, 64};
     if (c4 <= 512) return {512, 1, 512};
-    if (c4 <= 1024) return {512, 2, 512};
+    if (c4 <= 1024) return {1024, 1, 1024};
     if (c4 <= 2048) return {512, 4, 512};
     if (c4 <= 4096) return {1024, 4, 1024};
     return {0, 0, 0};
 }
 
-inline RowShape default_layernorm_shape(int64_t c4) { return default_norm_shape(c4); }
+// The LayerNorm backward (backward.hip): the shapes its sweeps chose, which
+// keep two vectors per thread at 4096 floats.
+inline RowShape default_lnbwd_shape(int64_t c4) {
+    if (c4 > 512 && c4 <= 1024) return {512, 2, 512};
+    return default_norm_shape(c4);
+}
+
+// LayerNorm reduces twice per wave and combines (mean, M2) pairs across the
+// row's waves, so it favours fewer, fuller waves per row at 4096 floats.
+inline RowShape default_layernorm_shape(int64_t c4) {
+    if (c4 > 512 && c4 <= 1024) return {256, 4, 256};
+    return default_norm_shape(c4);
+}
 
 inline RowShape default_softmax_shape(int64_t c4) {
     if (c4 <= 64) return {64, 1, 64};

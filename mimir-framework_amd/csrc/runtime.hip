@@ -22,7 +22,7 @@ __global__ __launch_bounds__(kBlock) void copy16_kernel(const u4* __restrict__ s
     for (int64_t i = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x; i < n16; i += stride) {
         const u4 v = __builtin_nontemporal_load(src + i);
         if constexpr (KEEP) dst[i] = v;
-        else __builtin_nontemporal_store(v, dst + i);
+        else st_stream(dst + i, v);
     }
 }
 
@@ -114,7 +114,9 @@ int mimir_ctx_create(int device, mimir_ctx** out) {
         return MIMIR_EDEVICE;
     }
     ctx->stream = ctx->own_stream;
-    if (int st = noalloc_scratch_init(ctx)) {
+    int init_st = noalloc_scratch_init(ctx);
+    if (init_st == MIMIR_OK) init_st = norm_init(ctx);
+    if (int st = init_st) {
         (void)hipStreamDestroy(ctx->own_stream);
         delete ctx;
         return st;

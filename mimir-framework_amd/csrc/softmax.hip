@@ -161,7 +161,7 @@ __global__ __launch_bounds__(kBlock) void softmax_rows_scalar(SoftmaxArgs a) {
         if (c < a.cols) {
             const float o = finish<MODE>(v[j], e[j], m, sum, aux);
             if constexpr (KEEP) a.y[base + c] = o;
-            else __builtin_nontemporal_store(o, a.y + base + c);
+            else st_stream(a.y + base + c, o);
         }
     }
 }
