@@ -499,7 +499,7 @@ int mimir_attention_fwd(mimir_ctx* ctx, const float* q, int64_t ld_q, const floa
     if (batch == 0 || q_len == 0) return MIMIR_OK;
     MIMIR_REQUIRE(ctx, q && out && (kv_len == 0 || (k && v)), "attention: null pointer");
     const int64_t nqb = (q_len + kQPerBlock - 1) / kQPerBlock;
-    MIMIR_REQUIRE(ctx, batch * heads * nqb <= INT32_MAX, "attention: grid of %lld workgroups exceeds the limit",
+    MIMIR_REQUIRE(ctx, dispatch_fits(batch * heads * nqb, kThreads), "attention: grid of %lld workgroups exceeds the limit",
                   (long long)(batch * heads * nqb));
     if (int st = enter(ctx)) return st;
     AttnArgs a;
@@ -526,7 +526,7 @@ int mimir_attention_fwd(mimir_ctx* ctx, const float* q, int64_t ld_q, const floa
     if (head_dim <= 32) return launch<32>(ctx, a, vec);
     if (head_dim <= 64) return launch<64>(ctx, a, vec);
     if (head_dim <= 128) return launch<128>(ctx, a, vec);
-    MIMIR_REQUIRE(ctx, batch * heads <= INT32_MAX && (q_len + kGenericWaves - 1) / kGenericWaves <= 65535,
+    MIMIR_REQUIRE(ctx, dispatch_fits(batch * heads, kGenericWaves * kWave) && (q_len + kGenericWaves - 1) / kGenericWaves <= 65535,
                   "attention: grid exceeds the limit of the wide-head kernel");
     if (head_dim <= 256) return launch_generic<4>(ctx, a, batch, heads);
     if (head_dim <= 512) return launch_generic<8>(ctx, a, batch, heads);

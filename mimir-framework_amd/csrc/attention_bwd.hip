@@ -208,7 +208,7 @@ int heads_to_rows(mimir_ctx* ctx, const float* src, int64_t n, int64_t T, int64_
     if (n == 0 || T == 0) return MIMIR_OK;
     const bool vec = D % 4 == 0 && ld % 4 == 0 && aligned16(src) && aligned16(dst);
     unsigned blocks = 0;
-    if (!grid_for(n * T * (vec ? D / 4 : D), kBlock, &blocks))
+    if (!grid_for(n * T * (vec ? D / 4 : D), kBlock, kBlock, &blocks))
         return fail(ctx, MIMIR_EINVAL, "attention backward: grid too large");
     blocks = std::min(blocks, 16384u);
     if (vec)
@@ -245,14 +245,14 @@ int transpose(mimir_ctx* ctx, const float* src, int64_t ld_src, int64_t rows, in
 int zero_rows(mimir_ctx* ctx, float* y, int64_t rows, int64_t cols, int64_t ld) {
     if (rows == 0 || cols == 0) return MIMIR_OK;
     unsigned blocks = 0;
-    if (!grid_for(rows * cols, kBlock, &blocks)) return fail(ctx, MIMIR_EINVAL, "attention: grid too large");
+    if (!grid_for(rows * cols, kBlock, kBlock, &blocks)) return fail(ctx, MIMIR_EINVAL, "attention: grid too large");
     zero_rows_kernel<<<std::min(blocks, 8192u), kBlock, 0, ctx->stream>>>(y, rows, cols, ld);
     return launched(ctx, "zero_rows_kernel");
 }
 
 int probs(mimir_ctx* ctx, float* s, int64_t rows, int32_t q_len, int32_t kv_len, int32_t causal) {
     unsigned blocks = 0;
-    if (!grid_for(rows, kRowWaves, &blocks)) return fail(ctx, MIMIR_EINVAL, "attention backward: grid too large");
+    if (!grid_for(rows, kRowWaves, kRowWaves * kWave, &blocks)) return fail(ctx, MIMIR_EINVAL, "attention backward: grid too large");
     const dim3 grid(blocks), block(kRowWaves * kWave);
     if (kv_len <= 4 * kWave)
         attn_probs_kernel<4><<<grid, block, 0, ctx->stream>>>(s, rows, q_len, kv_len, causal);
@@ -271,7 +271,7 @@ bool fused_rows(int32_t kv_len) { return kv_len <= 64 * kWave; }
 int probs_dsoftmax(mimir_ctx* ctx, float* s, float* g, int64_t rows, int32_t q_len, int32_t kv_len,
                    int32_t causal) {
     unsigned blocks = 0;
-    if (!grid_for(rows, kRowWaves, &blocks)) return fail(ctx, MIMIR_EINVAL, "attention backward: grid too large");
+    if (!grid_for(rows, kRowWaves, kRowWaves * kWave, &blocks)) return fail(ctx, MIMIR_EINVAL, "attention backward: grid too large");
     const dim3 grid(blocks), block(kRowWaves * kWave);
     if (kv_len <= 4 * kWave)
         attn_probs_dsoftmax_kernel<4><<<grid, block, 0, ctx->stream>>>(s, g, rows, q_len, kv_len, causal);
@@ -285,7 +285,7 @@ int probs_dsoftmax(mimir_ctx* ctx, float* s, float* g, int64_t rows, int32_t q_l
 int dsoftmax(mimir_ctx* ctx, const float* p, float* g, int64_t rows, int32_t q_len, int32_t kv_len,
              int32_t causal) {
     unsigned blocks = 0;
-    if (!grid_for(rows, kRowWaves, &blocks)) return fail(ctx, MIMIR_EINVAL, "attention backward: grid too large");
+    if (!grid_for(rows, kRowWaves, kRowWaves * kWave, &blocks)) return fail(ctx, MIMIR_EINVAL, "attention backward: grid too large");
     const dim3 grid(blocks), block(kRowWaves * kWave);
     if (kv_len <= 4 * kWave)
         attn_dsoftmax_kernel<4><<<grid, block, 0, ctx->stream>>>(p, g, rows, q_len, kv_len, causal);

@@ -128,7 +128,7 @@ int run_dact(mimir_ctx* ctx, const float* x, const float* dy, float* dx, int64_t
         const int64_t n4 = n / 4;
         if (n4 > 0) {
             unsigned blocks;
-            if (!grid_for(n4, kBlock, &blocks))
+            if (!grid_for(n4, kBlock, kBlock, &blocks))
                 return fail(ctx, MIMIR_EINVAL, "%s: n=%lld exceeds the grid limit", name, (long long)n);
             if (ctx->keep_outputs) dact_vec<F, ACC, true><<<blocks, kBlock, 0, ctx->stream>>>(x, dy, dx, n4, f);
             else dact_vec<F, ACC, false><<<blocks, kBlock, 0, ctx->stream>>>(x, dy, dx, n4, f);
@@ -256,7 +256,7 @@ int accumulate(mimir_ctx* ctx, const float* src, float* dst, int64_t n, bool acc
         const int64_t n4 = n / 4;
         if (n4 > 0) {
             unsigned blocks;
-            if (!grid_for(n4, kBlock, &blocks))
+            if (!grid_for(n4, kBlock, kBlock, &blocks))
                 return fail(ctx, MIMIR_EINVAL, "%s: n=%lld exceeds the grid limit", name, (long long)n);
             const bool k = ctx->keep_outputs != 0;
             if (acc && k) acc_vec<true, true><<<blocks, kBlock, 0, ctx->stream>>>(src, dst, n4);
@@ -419,7 +419,7 @@ int launch_sum_slots(mimir_ctx* ctx, const float* part, int64_t nslots, int64_t 
                      float* out1, int64_t split, bool acc, float* tmp = nullptr) {
     unsigned blocks;
     if (width % 4 == 0 && stride % 4 == 0 && split % 4 == 0 && aligned16(part)) {
-        if (!grid_for(width / 4, kWave, &blocks))
+        if (!grid_for(width / 4, kWave, kBlock, &blocks))
             return fail(ctx, MIMIR_EINVAL, "sum_slots: width %lld exceeds the grid limit", (long long)width);
         if (tmp && aligned16(tmp) && nslots >= 4 * kGroups) {
             slot_groups4<8><<<dim3(blocks, kGroups), kBlock, 0, ctx->stream>>>(part, nslots, stride, width, tmp);
@@ -436,7 +436,7 @@ int launch_sum_slots(mimir_ctx* ctx, const float* part, int64_t nslots, int64_t 
         sum_total<<<1, 1024, 0, ctx->stream>>>(part, nslots, stride, out0, acc ? 1 : 0);
         return launched(ctx, "sum_total");
     }
-    if (!grid_for(width, kWave, &blocks))
+    if (!grid_for(width, kWave, kSumLanes * kWave, &blocks))
         return fail(ctx, MIMIR_EINVAL, "sum_slots: width %lld exceeds the grid limit", (long long)width);
     sum_slots<<<blocks, kSumLanes * kWave, 0, ctx->stream>>>(part, nslots, stride, width, out0, out1, split,
                                                              acc ? 1 : 0);
@@ -609,7 +609,7 @@ int add_bcast_bwd(mimir_ctx* ctx, const float* dy, int64_t n_big, int64_t n_smal
         void* s = nullptr;
         if (int st = ensure_scratch(ctx, sizeof(float) * static_cast<size_t>(nchunks), &s)) return st;
         unsigned blocks;
-        if (!grid_for(nchunks, 1, &blocks)) return fail(ctx, MIMIR_EINVAL, "Add backward: operand too large");
+        if (!grid_for(nchunks, 1, kBlock, &blocks)) return fail(ctx, MIMIR_EINVAL, "Add backward: operand too large");
         if (vec) add_total_part<true><<<blocks, kBlock, 0, ctx->stream>>>(dy, d_big, acc_big, n_big, chunk,
                                                                          static_cast<float*>(s));
         else add_total_part<false><<<blocks, kBlock, 0, ctx->stream>>>(dy, d_big, acc_big, n_big, chunk,
@@ -630,7 +630,7 @@ int add_bcast_bwd(mimir_ctx* ctx, const float* dy, int64_t n_big, int64_t n_smal
     if (nchunks > 65535) nchunks = 65535;
     const int64_t chunk = (rows + nchunks - 1) / nchunks;
     nchunks = (rows + chunk - 1) / chunk;
-    if (cblocks > 0x7fffffffLL) return fail(ctx, MIMIR_EINVAL, "Add backward: operand too large");
+    if (!dispatch_fits(cblocks, kBlock)) return fail(ctx, MIMIR_EINVAL, "Add backward: operand too large");
     void* s = nullptr;
     const size_t part_floats = static_cast<size_t>((nchunks + kGroups) * n_small);
     if (int st = ensure_scratch(ctx, sizeof(float) * part_floats, &s)) return st;
@@ -1065,10 +1065,10 @@ int launch_ln_bwd_scalar(mimir_ctx* ctx, LnBwdArgs a, float* dgamma, float* dbet
 }
 
 int ln_bwd_generic_run(mimir_ctx* ctx, LnBwdArgs a, float* dgamma, float* dbeta, const ScratchSpan* fixed) {
-    if (a.rows > 0x7fffffffLL)
+    if (!dispatch_fits(a.rows, kBlock))
         return fail(ctx, MIMIR_EINVAL, "LayerNorm backward: %lld rows exceed the grid limit", (long long)a.rows);
     const int64_t cblocks = (a.cols + kBlock - 1) / kBlock;
-    if (cblocks > 0x7fffffffLL) return fail(ctx, MIMIR_EINVAL, "LayerNorm backward: row too wide");
+    if (!dispatch_fits(cblocks, kBlock)) return fail(ctx, MIMIR_EINVAL, "LayerNorm backward: row too wide");
     int64_t nchunks = 0, chunk = a.rows;
     if (dgamma) {
         nchunks = (1024 + cblocks - 1) / cblocks;
@@ -1833,8 +1833,11 @@ int embed_bwd(mimir_ctx* ctx, const void* ids, int64_t n_ids, const float* dy, f
         const int tpt = ctx->tune.gather_tpt ? ctx->tune.gather_tpt : (dim4 >= 1024 ? 1024 : dim4 >= 512 ? 512 : 256);
         // With the run list, a workgroup per run: at most min(n, vocab) of them.
         const int64_t rows_grid = runs.count && vocab < n_ids ? vocab : n_ids;
-        const bool merged = long_runs && tpt == 1024 && rows_grid + nslots <= 0x7fffffffLL &&
+        const bool merged = long_runs && tpt == 1024 && dispatch_fits(rows_grid + nslots, 1024) &&
                             ctx->tune.embed_bwd_merged != 0;
+        if (!dispatch_fits(rows_grid, tpt))
+            return fail(ctx, MIMIR_EINVAL, "Embedding backward: %lld rows of %d threads exceed the grid limit",
+                        (long long)rows_grid, tpt);
         const unsigned rg = static_cast<unsigned>(rows_grid);
         const bool by_run = runs.count != nullptr;
         if (merged) {
@@ -1924,7 +1927,7 @@ int layernorm_bwd(mimir_ctx* ctx, const float* x, const float* dy, const float* 
     }
     if (vec) {
         const RowShape over = ctx->tune.lnbwd;
-        const RowShape s = shape_fits(over, c4) ? over : default_lnbwd_shape(c4);
+        const RowShape s = shape_fits(over, c4) ? over : default_norm_shape(c4);
 #define MIMIR_LNBWD_CASE(T, V, B) \
         if (s.tpr == T && s.vpt == V && s.bs == B) return launch_ln_bwd_vec<T, V, B>(ctx, a, dgamma, dbeta, fixed);
         MIMIR_ROW_SHAPES(MIMIR_LNBWD_CASE)
@@ -2021,7 +2024,7 @@ int mimir_mul_bwd(mimir_ctx* ctx, const float* a, const float* b, const float* d
         const int64_t n4 = n / 4;
         if (n4 > 0) {
             unsigned blocks;
-            if (!grid_for(n4, kBlock, &blocks))
+            if (!grid_for(n4, kBlock, kBlock, &blocks))
                 return fail(ctx, MIMIR_EINVAL, "Multiply backward: n=%lld exceeds the grid limit", (long long)n);
             if (ctx->keep_outputs) launch_mul_bwd<true>(ctx, blocks, A, B, a, b, dy, da, db, n4);
             else launch_mul_bwd<false>(ctx, blocks, A, B, a, b, dy, da, db, n4);
@@ -2054,7 +2057,7 @@ int mimir_add_bwd(mimir_ctx* ctx, const float* dy, int64_t na, int64_t nb, float
         const bool alias = da == dy || db == dy || (da && da == db);
         if (!alias && aligned16(dy) && (!da || aligned16(da)) && (!db || aligned16(db)) && (na % 4) == 0) {
             unsigned blocks;
-            if (!grid_for(na / 4, kBlock, &blocks))
+            if (!grid_for(na / 4, kBlock, kBlock, &blocks))
                 return fail(ctx, MIMIR_EINVAL, "Add backward: n=%lld exceeds the grid limit", (long long)na);
             if (ctx->keep_outputs) launch_add_bwd<true>(ctx, blocks, A, B, dy, da, db, na / 4);
             else launch_add_bwd<false>(ctx, blocks, A, B, dy, da, db, na / 4);

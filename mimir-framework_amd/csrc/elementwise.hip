@@ -152,7 +152,7 @@ unsigned stride_grid(int64_t n) {
 template <class F, int VPT>
 int launch_unary(mimir_ctx* ctx, const float* x, float* y, int64_t n4, F f, const char* name) {
     unsigned blocks;
-    if (!grid_for(n4, static_cast<int64_t>(VPT) * kBlock, &blocks))
+    if (!grid_for(n4, static_cast<int64_t>(VPT) * kBlock, kBlock, &blocks))
         return fail(ctx, MIMIR_EINVAL, "%s: n=%lld exceeds the grid limit", name, (long long)(4 * n4));
     if (ctx->keep_outputs) unary_vec<F, VPT, true><<<blocks, kBlock, 0, ctx->stream>>>(x, y, n4, f);
     else unary_vec<F, VPT, false><<<blocks, kBlock, 0, ctx->stream>>>(x, y, n4, f);
@@ -163,7 +163,7 @@ template <class F, int VPT>
 int launch_binary(mimir_ctx* ctx, const float* a, const float* b, float* y, int64_t n4, F f,
                   const char* name) {
     unsigned blocks;
-    if (!grid_for(n4, static_cast<int64_t>(VPT) * kBlock, &blocks))
+    if (!grid_for(n4, static_cast<int64_t>(VPT) * kBlock, kBlock, &blocks))
         return fail(ctx, MIMIR_EINVAL, "%s: n=%lld exceeds the grid limit", name, (long long)(4 * n4));
     if (ctx->keep_outputs) binary_vec<F, VPT, true><<<blocks, kBlock, 0, ctx->stream>>>(a, b, y, n4, f);
     else binary_vec<F, VPT, false><<<blocks, kBlock, 0, ctx->stream>>>(a, b, y, n4, f);
@@ -265,7 +265,7 @@ int mimir::fused_chain(mimir_ctx* ctx, const FuseProgram& p, int64_t n) {
     if (aligned && n / 4 > 0) {
         const int64_t n4 = n / 4;
         unsigned blocks;
-        if (!grid_for(n4, kBlock, &blocks)) return fail(ctx, MIMIR_EINVAL, "fused chain: grid too large");
+        if (!grid_for(n4, kBlock, kBlock, &blocks)) return fail(ctx, MIMIR_EINVAL, "fused chain: grid too large");
         if (ctx->keep_outputs) fused_chain_vec<true><<<blocks, kBlock, 0, ctx->stream>>>(p, n4);
         else fused_chain_vec<false><<<blocks, kBlock, 0, ctx->stream>>>(p, n4);
         if (int st = launched(ctx, "fused_chain_vec")) return st;
@@ -347,7 +347,7 @@ int mimir_add_fwd(mimir_ctx* ctx, const float* a, int64_t na, const float* b, in
     if (small_n % 4 == 0 && aligned16(big) && aligned16(small) && aligned16(y)) {
         const int64_t small_n4 = small_n / 4;
         unsigned bx;
-        if (!grid_for(small_n4, kBlock, &bx))
+        if (!grid_for(small_n4, kBlock, kBlock, &bx))
             return fail(ctx, MIMIR_EINVAL, "Add: operand of %lld exceeds the grid limit", (long long)small_n);
         // Enough rows per launch to give every CU work; each thread then strides rows.
         const int64_t want_y = (static_cast<int64_t>(2048) + bx - 1) / bx;

@@ -95,7 +95,7 @@ int run(mimir_ctx* ctx, const void* ids, int64_t n_ids, const float* table, int6
     MIMIR_ENTER(ctx);
     const GatherArgs a{ids, n_ids, table, vocab, dim, pad, y};
     unsigned blocks;
-    if (!grid_for(n_ids, kWavesPerBlock, &blocks))
+    if (!grid_for(n_ids, kWavesPerBlock, kBlock, &blocks))
         return fail(ctx, MIMIR_EINVAL, "Embedding: %lld ids exceed the grid limit", (long long)n_ids);
     if (dim % 4 == 0 && aligned16(table) && aligned16(y)) {
         const int64_t dim4 = dim / 4;
@@ -104,7 +104,7 @@ int run(mimir_ctx* ctx, const void* ids, int64_t n_ids, const float* table, int6
             tpt = dim4 <= 64 ? 64 : dim4 <= 128 ? 128 : dim4 <= 256 ? 256 : dim4 <= 512 ? 512 : 1024;
         const int bs = tpt < kBlock ? kBlock : tpt;
         unsigned vb;
-        if (!grid_for(n_ids, bs / tpt, &vb))
+        if (!grid_for(n_ids, bs / tpt, bs, &vb))
             return fail(ctx, MIMIR_EINVAL, "Embedding: %lld ids exceed the grid limit", (long long)n_ids);
         if (ctx->keep_outputs) launch_vec<MODE, true>(tpt, vb, ctx->stream, a);
         else launch_vec<MODE, false>(tpt, vb, ctx->stream, a);

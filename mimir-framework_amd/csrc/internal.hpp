@@ -94,14 +94,7 @@ inline int launched(mimir_ctx* ctx, const char* kernel) {
 
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
-// Number of 256-thread blocks for `units` work items of `per_block` each,
-// refusing grids beyond the 32-bit grid limit.
-inline bool grid_for(int64_t units, int64_t per_block, unsigned* blocks) {
-    const int64_t b = (units + per_block - 1) / per_block;
-    if (b <= 0 || b > 0x7fffffffLL) return false;
-    *blocks = static_cast<unsigned>(b);
-    return true;
-}
+// dispatch_fits / grid_for: launch-size checks (rows.hpp).
 
 // Context scratch of at least `bytes` (runtime.hip).  Growing it waits for
 // the work already enqueued, which may still read the old buffer (or, while

@@ -337,7 +337,7 @@ int setup(mimir_ctx* ctx, LongArgs& a, int64_t rows, int64_t cols) {
 // Rows wider than a register-resident workgroup takes, however many: the
 // grid is chunks x rows (rows up to 65535, the grid's y limit used here).
 bool mimir::longrow_applies(int64_t rows, int64_t cols) {
-    return cols > 16384 && rows <= 65535 && (cols + kChunkFloats - 1) / kChunkFloats <= 0x7fffffffLL;
+    return cols > 16384 && rows <= 65535 && dispatch_fits((cols + kChunkFloats - 1) / kChunkFloats, kBlock);
 }
 
 namespace {

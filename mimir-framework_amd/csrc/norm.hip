@@ -140,8 +140,8 @@ __global__ __launch_bounds__(BS) void norm_rows_vec(NormArgs a) {
         for (int j = 0; j < VPT; ++j) {
             v[j] = v[j] + rr[j];  // one IEEE add per element, as add_forward
             // add + RMSNorm's updated residual: a plain store, measured
-            // faster than a streamed one beside the streamed y (79.4 against
-            // 75.4% of 8 TB/s at configs[1]).  The runtime's fused Add ->
+            // faster than a streamed one beside the streamed y (4 points of
+            // 8 TB/s at configs[1]).  The runtime's fused Add ->
             // LayerNorm streams its sum (a later block reads it).
             if (live(j) && (K == Norm::AddRms || a.r_out)) st4<K == Norm::AddLayer>(ro + 4 * j * TPR, v[j]);
         }
@@ -325,7 +325,7 @@ __global__ __launch_bounds__(kBlock) void norm_rows_generic(NormArgs a) {
 template <Norm K, int TPR, int VPT, int BS, bool EPI = false>
 int launch_vec(mimir_ctx* ctx, const NormArgs& args) {
     unsigned blocks;
-    if (!grid_for(args.rows, BS / TPR, &blocks))
+    if (!grid_for(args.rows, BS / TPR, BS, &blocks))
         return fail(ctx, MIMIR_EINVAL, "norm: %lld rows exceed the grid limit", (long long)args.rows);
     NormArgs a = args;
     a.inv_n = 1.0f / static_cast<float>(a.cols);
@@ -470,7 +470,7 @@ int dispatch(mimir_ctx* ctx, const NormArgs& a) {
             return longrow_norm(ctx, K == Norm::Layer ? 0 : (K == Norm::Rms ? 1 : 2), a.x, a.r, a.r_out, a.g, a.b,
                                 a.w_len, a.y, a.rows, a.cols, a.eps);
     }
-    if (a.rows > 0x7fffffffLL)
+    if (!dispatch_fits(a.rows, kBlock))
         return fail(ctx, MIMIR_EINVAL, "norm: %lld rows exceed the grid limit", (long long)a.rows);
     if (!vec && a.cols <= 4 * kBlock) return launch_scalar<K, 4>(ctx, a);
     if (!vec && a.cols <= 8 * kBlock) return launch_scalar<K, 8>(ctx, a);

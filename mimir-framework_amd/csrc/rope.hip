@@ -111,7 +111,7 @@ __global__ __launch_bounds__(kBlock) void rope_scalar(RopeArgs a, int64_t q_pair
 template <int LOG2Q, int PPT>
 int launch_ppt(mimir_ctx* ctx, const RopeArgs& a) {
     unsigned blocks;
-    if (!grid_for(a.total_slots, static_cast<int64_t>(PPT) * kBlock, &blocks))
+    if (!grid_for(a.total_slots, static_cast<int64_t>(PPT) * kBlock, kBlock, &blocks))
         return fail(ctx, MIMIR_EINVAL, "RoPE: tensor exceeds the grid limit");
     if (ctx->keep_outputs) rope_vec<LOG2Q, PPT, true><<<blocks, kBlock, 0, ctx->stream>>>(a);
     else rope_vec<LOG2Q, PPT, false><<<blocks, kBlock, 0, ctx->stream>>>(a);

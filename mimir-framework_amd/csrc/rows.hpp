@@ -124,17 +124,10 @@ inline RowShape default_norm_shape(int64_t c4) {
     if (c4 <= 128) return {128, 1, 256};
     if (c4 <= 256) return {64, 4, 64};
     if (c4 <= 512) return {512, 1, 512};
-    if (c4 <= 1024) return {1024, 1, 1024};
+    if (c4 <= 1024) return {512, 2, 512};
     if (c4 <= 2048) return {512, 4, 512};
     if (c4 <= 4096) return {1024, 4, 1024};
     return {0, 0, 0};
-}
-
-// The LayerNorm backward (backward.hip): the shapes its sweeps chose, which
-// keep two vectors per thread at 4096 floats.
-inline RowShape default_lnbwd_shape(int64_t c4) {
-    if (c4 > 512 && c4 <= 1024) return {512, 2, 512};
-    return default_norm_shape(c4);
 }
 
 // LayerNorm reduces twice per wave and combines (mean, M2) pairs across the
@@ -157,6 +150,22 @@ inline RowShape default_softmax_shape(int64_t c4) {
 
 inline bool shape_fits(const RowShape& s, int64_t c4) {
     return s.tpr > 0 && static_cast<int64_t>(s.tpr) * s.vpt >= c4;
+}
+
+// Whether `blocks` workgroups of `threads` fit one grid dimension: HIP takes
+// at most 2^31 - 1 workgroups, and the dispatch packet counts the grid in
+// work-items in 32 bits, so blocks * threads must stay below 2^32.
+inline bool dispatch_fits(int64_t blocks, int64_t threads) {
+    return blocks > 0 && blocks <= 0x7fffffffLL && blocks * threads <= 0xffffffffLL;
+}
+
+// Number of workgroups of `threads` for `units` work items of `per_block`
+// each, refusing grids beyond the dispatch limits above.
+inline bool grid_for(int64_t units, int64_t per_block, int threads, unsigned* blocks) {
+    const int64_t b = (units + per_block - 1) / per_block;
+    if (!dispatch_fits(b, threads)) return false;
+    *blocks = static_cast<unsigned>(b);
+    return true;
 }
 
 }  // namespace mimir

@@ -177,7 +177,7 @@ int launch_scalar(mimir_ctx* ctx, const SoftmaxArgs& a) {
 template <int MODE, int TPR, int VPT, int BS>
 int launch_vec(mimir_ctx* ctx, const SoftmaxArgs& a) {
     unsigned blocks;
-    if (!grid_for(a.rows, BS / TPR, &blocks))
+    if (!grid_for(a.rows, BS / TPR, BS, &blocks))
         return fail(ctx, MIMIR_EINVAL, "softmax: %lld rows exceed the grid limit", (long long)a.rows);
     if (ctx->keep_outputs) softmax_rows_vec<MODE, TPR, VPT, BS, true><<<blocks, BS, 0, ctx->stream>>>(a);
     else softmax_rows_vec<MODE, TPR, VPT, BS, false><<<blocks, BS, 0, ctx->stream>>>(a);
@@ -196,7 +196,7 @@ int dispatch(mimir_ctx* ctx, const SoftmaxArgs& a) {
 #undef MIMIR_SOFTMAX_CASE
         if (longrow_applies(a.rows, a.cols)) return longrow_softmax(ctx, MODE, a.x, a.y, a.rows, a.cols);
     }
-    if (a.rows > 0x7fffffffLL)
+    if (!dispatch_fits(a.rows, kBlock))
         return fail(ctx, MIMIR_EINVAL, "softmax: %lld rows exceed the grid limit", (long long)a.rows);
     if (!vec && a.cols <= 4 * kBlock) return launch_scalar<MODE, 4>(ctx, a);
     if (!vec && a.cols <= 8 * kBlock) return launch_scalar<MODE, 8>(ctx, a);

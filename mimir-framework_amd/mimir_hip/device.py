@@ -7,6 +7,7 @@ and a non-OK status raises :class:`MimirError` carrying the library's message.
 from __future__ import annotations
 
 import ctypes
+import weakref
 from ctypes import byref, c_float, c_void_p
 
 import numpy as np
@@ -330,11 +331,17 @@ class Store:
         h = c_void_p()
         ctx.check(ctx.lib.mimir_store_create(ctx.handle, byref(h)), "mimir_store_create")
         self.handle = h
+        self._graphs = weakref.WeakSet()  # StoreGraphs captured on this store
 
     def close(self):
+        """mimir_store_destroy, which also destroys every graph captured on
+        this store: their StoreGraph objects are closed with it."""
         if self.handle:
             self.ctx.check(self.ctx.lib.mimir_store_destroy(self.handle), "mimir_store_destroy")
             self.handle = None
+        for sg in list(self._graphs):
+            sg._destroyed_by_store()
+        self._graphs.clear()
 
     def clear(self):
         self.ctx.check(self.ctx.lib.mimir_store_clear(self.handle))
@@ -458,33 +465,58 @@ class StoreGraph:
 
     def __init__(self, store: "Store", graph: "DeviceGraph"):
         self.store, self.ctx = store, store.ctx
-        self._graph = graph  # its layer descriptors and weights stay alive with this
+        self.handle = None
+        # The captured kernels hold graph's weight and gradient addresses:
+        # graph refuses to free them while this graph is open.
+        self._graph = graph
         h = c_void_p()
         self.ctx.check(self.ctx.lib.mimir_store_capture(store.handle, graph.c_layers, len(graph.layers), byref(h)))
         self.handle = h
+        store._graphs.add(self)
+        graph._holders.add(self)
+
+    def _live(self):
+        if not self.handle:
+            raise MimirError(EINVAL, "StoreGraph: closed (by close() or by closing its Store)")
+        return self.handle
+
+    def _release(self):
+        if self._graph is not None:
+            self._graph._holders.discard(self)
+            self._graph = None
+
+    def _destroyed_by_store(self):
+        # mimir_store_destroy freed the C graph: only forget the handle.
+        self.handle = None
+        self._release()
 
     def set_input(self, name, arr):
         a = np.ascontiguousarray(arr)
         dt = _lib.DTYPE_I32 if a.dtype.kind in "iu" else _lib.DTYPE_F32
         a = np.ascontiguousarray(a, np.int32 if dt == _lib.DTYPE_I32 else np.float32).ravel()
-        self.ctx.check(self.ctx.lib.mimir_store_graph_set_input(self.handle, name.encode(), dt,
+        self.ctx.check(self.ctx.lib.mimir_store_graph_set_input(self._live(), name.encode(), dt,
                                                                 a.ctypes.data_as(c_void_p), a.size))
 
     def launch(self):
-        self.ctx.check(self.ctx.lib.mimir_store_graph_launch(self.handle))
+        self.ctx.check(self.ctx.lib.mimir_store_graph_launch(self._live()))
 
     def get(self, name="x", dtype=_lib.DTYPE_F32):
+        h = self._live()
         n = ctypes.c_int64()
-        self.ctx.check(self.ctx.lib.mimir_store_graph_get(self.handle, name.encode(), dtype, None, 0, byref(n)))
+        self.ctx.check(self.ctx.lib.mimir_store_graph_get(h, name.encode(), dtype, None, 0, byref(n)))
         out = np.empty(n.value, np.int32 if dtype == _lib.DTYPE_I32 else np.float32)
-        self.ctx.check(self.ctx.lib.mimir_store_graph_get(self.handle, name.encode(), dtype,
+        self.ctx.check(self.ctx.lib.mimir_store_graph_get(h, name.encode(), dtype,
                                                           out.ctypes.data_as(c_void_p), n.value, byref(n)))
         return out
 
     def close(self):
+        """mimir_store_graph_destroy; does nothing once closed, also when its
+        Store's close() already destroyed the graph."""
         if self.handle:
             self.ctx.check(self.ctx.lib.mimir_store_graph_destroy(self.handle))
             self.handle = None
+            self.store._graphs.discard(self)
+        self._release()
 
     def __enter__(self):
         return self
@@ -511,6 +543,7 @@ class DeviceGraph:
     def __init__(self, ctx: Context, layers):
         self.ctx = ctx
         self.layers = list(layers)
+        self._holders = weakref.WeakSet()  # open StoreGraphs whose kernels use these buffers
         self._keep = []
         self.weights = []
         self.grad_bufs = []
@@ -550,6 +583,13 @@ class DeviceGraph:
                 self.ctx.upload(d, np.zeros(d.size, np.float32))
 
     def close(self):
+        """Free the weight and gradient blocks.  Refused (MimirError, EINVAL)
+        while a StoreGraph captured from this graph is open: its kernels would
+        replay reads of the freed memory."""
+        live = [sg for sg in self._holders if sg.handle]
+        if live:
+            raise MimirError(EINVAL, f"DeviceGraph.close: {len(live)} captured StoreGraph(s) still replay its "
+                                     "weights; close them (or their Store) first")
         for d in self.weights + self.grad_bufs:
             if d is not None:
                 d.free()

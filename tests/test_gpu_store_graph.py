@@ -134,6 +134,8 @@ def test_graph_refusals(ctx, stores):
 
 
 def test_store_close_destroys_its_graphs(ctx):
+    """Closing the store destroys its captured graphs; their StoreGraph
+    objects then refuse to launch, and closing them again is a no-op."""
     name, layers, fin, iin = graphs()[0]
     s = M.Store(ctx)
     g = M.DeviceGraph(ctx, layers)
@@ -142,6 +144,29 @@ def test_store_close_destroys_its_graphs(ctx):
         sg.launch()
         assert_bitexact(sg.get("x"), np.array([8, 12], np.float32), "named routing")
         s.close()  # destroys sg's graph too
-        sg.handle = None
+        assert not sg.handle
+        with pytest.raises(M.MimirError, match="closed"):
+            sg.launch()
+        sg.close()  # safe: nothing left to destroy
+        sg.close()
     finally:
+        g.close()
+
+
+def test_device_graph_close_waits_for_its_store_graphs(ctx):
+    """A DeviceGraph refuses to free its weights while a captured graph that
+    replays them is open, and frees them once that graph is closed."""
+    name, layers, fin, iin = graphs()[0]
+    s = M.Store(ctx)
+    g = M.DeviceGraph(ctx, layers)
+    try:
+        sg = s.capture(g, fin, iin)
+        with pytest.raises(M.MimirError, match="still replay"):
+            g.close()
+        sg.launch()  # the weights are still there
+        assert_bitexact(sg.get("x"), np.array([8, 12], np.float32), "replay after a refused close")
+        sg.close()
+        g.close()
+    finally:
+        s.close()
         g.close()
