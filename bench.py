@@ -530,6 +530,60 @@ def time_op(ctx, op, steps, warmup, spin_s=0.25):
     return rec
 
 
+def same_bytes_copy(ctx, nbytes, steps, warmup, cache):
+    """A plain streaming copy moving `nbytes` per launch (half read, half
+    written), timed like the ops: the practical ceiling of a stream that size.
+    Cached by size (several ops move the same bytes)."""
+    n_copy = (nbytes // 8) // 4 * 4
+    if n_copy not in cache:
+        def make(ctx, nsets):
+            sets = [[ctx.empty(n_copy), ctx.empty(n_copy)] for _ in range(nsets)]
+            return (lambda i: ctx.copy(sets[i][1], sets[i][0], n_copy * 4)), sets
+        cache[n_copy] = time_op(ctx, OpBench("copy_same_bytes", -1, "copy of the op's bytes", "copy16_kernel",
+                                             8 * n_copy, n_copy, "floats", make), steps, warmup)
+    return cache[n_copy]
+
+
+def time_queued(ctx, op, launches=200):
+    """Device-side time per launch of a small op: the launches are enqueued
+    behind ~3 ms of copies, so the GPU runs them back to back with the host
+    already out of the way; events bracket the launches alone.  (Timed one
+    Python call at a time, an op this small measures the host's call rate.)"""
+    nsets = op.nsets()
+    step, sets = op.make(ctx, nsets)
+    n = 64 << 20
+    a, b = ctx.empty(n), ctx.empty(n)
+    try:
+        for i in range(8):
+            step(i % nsets)
+        ctx.sync()
+        e0, e1 = ctx.event(), ctx.event()
+        for _ in range(40):  # ~80 us each: the GPU stays busy while the host enqueues
+            ctx.copy(b, a, n * 4)
+        e0.record()
+        for i in range(launches):
+            step(i % nsets)
+        e1.record()
+        ctx.sync()
+        us = e0.elapsed_ms(e1) * 1e3 / launches
+        e0.close()
+        e1.close()
+    finally:
+        a.free()
+        b.free()
+        for bufs in sets:
+            for buf in bufs:
+                buf.free()
+    gbs = op.nbytes / (us * 1e-6) / 1e9
+    return {"us_per_launch": round(us, 3), "GB_s": round(gbs, 1), "frac_of_peak": round(gbs / PEAK_GBS, 4),
+            "launches": launches, "method": "launches queued behind 40 copies of 256 MiB, events around the launches alone"}
+
+
+# Ops too small to time one host call at a time: their sweep figure is the
+# device-side one (time_queued), the host-driven one is kept beside it.
+QUEUED_OPS = ("cfg0_layernorm",)
+
+
 # ---------------------------------------------------------------------------
 # CPU baseline leg: the reference's own code (oracle/_ref) or, for ops with no
 # reference function, the C restatement (oracle/lib), single-threaded.
@@ -1190,13 +1244,8 @@ def main():
 
     # The practical ceiling at this size: a plain copy moving the same bytes
     # per launch (half read, half written), timed the same way.
-    n_copy = (head.nbytes // 8) // 4 * 4
-
-    def make_same_copy(ctx, nsets):
-        sets = [[ctx.empty(n_copy), ctx.empty(n_copy)] for _ in range(nsets)]
-        return (lambda i: ctx.copy(sets[i][1], sets[i][0], n_copy * 4)), sets
-    same = time_op(ctx, OpBench("copy_same_bytes", -1, "copy of the workload's bytes", "copy16_kernel",
-                                8 * n_copy, n_copy, "floats", make_same_copy), args.steps, args.warmup)
+    copies = {}
+    same = same_bytes_copy(ctx, head.nbytes, args.steps, args.warmup, copies)
     log(f"  copy of the same bytes: {same['us_per_launch']} us/launch, {same['GB_s']} GB/s")
 
     sweep = []
@@ -1204,15 +1253,30 @@ def main():
             [] if args.ops == "none" else args.ops.split(","))
     for k in keys:
         if k == head.key:
+            res["copy_same_bytes_GB_s"] = same["GB_s"]
+            res["frac_of_copy"] = round(res["GB_s"] / same["GB_s"], 4)
             sweep.append(res)
             continue
         if k == "cfg3_safetensors_ingest":
             continue
         r = time_op(ctx, by_key[k], args.op_steps, 3)
-        if r.get("bound") == "launch":
+        if k in QUEUED_OPS:
+            q = time_queued(ctx, by_key[k])
+            r.update({"host_driven": {"us_per_launch": r["us_per_launch"], "GB_s": r["GB_s"],
+                                      "note": "host-bound: one Python call per launch"},
+                      "us_per_launch": q["us_per_launch"], "GB_s": q["GB_s"],
+                      "frac_of_peak": q["frac_of_peak"], "timing": q["method"],
+                      "rows_per_s": round(by_key[k].rows / (q["us_per_launch"] * 1e-6), 1)})
+            log(f"op {k}: {r['us_per_launch']} us/launch on the GPU ({100 * r['frac_of_peak']:.1f}%); "
+                f"{r['host_driven']['us_per_launch']} us/launch host-driven (host-bound)")
+        elif r.get("bound") == "launch":
             log(f"op {k}: {r['us_per_launch']} us/launch (launch-bound)")
         else:
             log(f"op {k}: {r['us_per_launch']} us/launch, {r['GB_s']} GB/s ({100 * r['frac_of_peak']:.1f}%)")
+        if r.get("bound") not in ("mfma", "launch") and k not in QUEUED_OPS and k != "calib_copy":
+            c = same_bytes_copy(ctx, by_key[k].nbytes, args.op_steps, 3, copies)
+            r["copy_same_bytes_GB_s"] = c["GB_s"]
+            r["frac_of_copy"] = round(r["GB_s"] / c["GB_s"], 4)
         sweep.append(r)
     if args.ops == "all" or "cfg3_safetensors_ingest" in keys:
         r = time_ingest(ctx)
@@ -1315,10 +1379,12 @@ def main():
             "value": cb["value"], "unit": cb["unit"], "cores": cb["cores"], "kind": cb["kind"],
             "sample": cb["sample"], "rows_per_s": cb["rows_per_s"], **host},
         "parity": compact_parity(parity.get(head.key)),
-        "ops_fields": ["us_per_launch", "GB_s", "frac_of_peak", "parity_pass", "traffic_over_algorithmic"],
+        "ops_fields": ["us_per_launch", "GB_s", "frac_of_peak", "parity_pass", "traffic_over_algorithmic",
+                       "frac_of_copy"],
         "ops": {r["op"]: [r["us_per_launch"], r["GB_s"], r.get("frac_of_peak"),
                           r["parity"]["pass"] if "parity" in r else None,
-                          r.get("traffic_over_algorithmic")] for r in sweep if r.get("bound") not in ("mfma", "launch")},
+                          r.get("traffic_over_algorithmic"), r.get("frac_of_copy")]
+                for r in sweep if r.get("bound") not in ("mfma", "launch")},
         "mfma_ops_fields": ["us_per_launch", "TFLOP_s", "frac_of_fp32_mfma_peak", "parity_pass",
                             "cpu_GFLOP_s"],
         "mfma_ops": {r["op"]: [r["us_per_launch"], r["TFLOP_s"], r["frac_of_peak"],
