@@ -400,6 +400,73 @@ __global__ __launch_bounds__(kBlock) void slot_groups4(const float* part, int64_
     }
 }
 
+// The slot sum in one launch, for up to kTileMaxSlots slots: workgroup b
+// sums every slot for float4 columns kTileCols*b .. kTileCols*b + 7 of the
+// summed width (one workgroup per CU at the LayerNorm backward's 2048
+// columns).  Lane l of wave w holds column kTileCols*b + (l & 7) and slot
+// lane q = 8w + (l >> 3) of kTileLanes, and adds slots q, q + 128, ... in
+// order with U loads in flight (one round trip for 512 slots); each load
+// instruction reads eight slots' 128 contiguous bytes.  The 128 slot lanes
+// of a column are then added in a fixed order: the eight of a wave by three
+// lane swaps (((q0 + q1) + (q2 + q3)) + ((q4 + q5) + (q6 + q7)), the same
+// bits in every lane), the 16 waves through LDS in wave order.  The
+// two-level form (slot_groups4, then sum_slots4) costs two launches of
+// ~4.5 us each on MI355X.
+constexpr int kTileCols = 8;
+constexpr int kTileLanes = 1024 / kTileCols;
+constexpr int64_t kTileMaxSlots = 2048;  // at most four rounds of U loads per slot lane
+
+__device__ __forceinline__ f4 shfl_xor4(f4 v, int m) {
+    f4 r;
+    r.x = __shfl_xor(v.x, m);
+    r.y = __shfl_xor(v.y, m);
+    r.z = __shfl_xor(v.z, m);
+    r.w = __shfl_xor(v.w, m);
+    return r;
+}
+
+template <int U>
+__global__ __launch_bounds__(1024) void sum_slots_tile(const float* part, int64_t nslots, int64_t stride,
+                                                       int64_t width, float* out0, float* out1, int64_t split,
+                                                       int acc) {
+    constexpr int NW = 1024 / kWave;
+    __shared__ f4 lds[NW][kTileCols];
+    const int w = threadIdx.x / kWave;
+    const int l = threadIdx.x % kWave;
+    const int col = l & (kTileCols - 1);
+    const int64_t q = (kWave / kTileCols) * w + (l / kTileCols);
+    const int64_t c4 = static_cast<int64_t>(blockIdx.x) * kTileCols + col;
+    f4 s = f4(0.0f);
+    if (4 * c4 < width) {
+        const f4* p = reinterpret_cast<const f4*>(part) + c4;
+        const int64_t st4 = stride / 4;
+        int64_t k = q;
+        for (; k + (U - 1) * kTileLanes < nslots; k += U * kTileLanes) {
+            f4 v[U];
+#pragma unroll
+            for (int u = 0; u < U; ++u) v[u] = p[(k + u * kTileLanes) * st4];
+#pragma unroll
+            for (int u = 0; u < U; ++u) s += v[u];
+        }
+        for (; k < nslots; k += kTileLanes) s += p[k * st4];
+    }
+#pragma unroll
+    for (int m = kTileCols; m < kWave; m <<= 1) s += shfl_xor4(s, m);  // the wave's slot lanes, pairwise
+    if (l < kTileCols) lds[w][col] = s;
+    __syncthreads();
+    if (threadIdx.x < kTileCols && 4 * c4 < width) {
+        f4 t = lds[0][col];
+#pragma unroll
+        for (int i = 1; i < NW; ++i) t += lds[i][col];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int64_t c = 4 * c4 + i;
+            float* o = c < split ? out0 + c : out1 + (c - split);
+            *o = acc ? *o + t[i] : t[i];
+        }
+    }
+}
+
 // out[0] (+)= the sum of the first float of nslots slots (row stride
 // `stride`): 1024 threads add slots t, t+1024, ... in order, then the block
 // tree adds the threads in order.
@@ -419,6 +486,13 @@ int launch_sum_slots(mimir_ctx* ctx, const float* part, int64_t nslots, int64_t 
                      float* out1, int64_t split, bool acc, float* tmp = nullptr) {
     unsigned blocks;
     if (width % 4 == 0 && stride % 4 == 0 && split % 4 == 0 && aligned16(part)) {
+        if (nslots >= 4 * kGroups && nslots <= kTileMaxSlots) {
+            if (!grid_for(width / 4, kTileCols, 1024, &blocks))
+                return fail(ctx, MIMIR_EINVAL, "sum_slots: width %lld exceeds the grid limit", (long long)width);
+            sum_slots_tile<4><<<blocks, 1024, 0, ctx->stream>>>(part, nslots, stride, width, out0, out1, split,
+                                                               acc ? 1 : 0);
+            return launched(ctx, "sum_slots_tile");
+        }
         if (!grid_for(width / 4, kWave, kBlock, &blocks))
             return fail(ctx, MIMIR_EINVAL, "sum_slots: width %lld exceeds the grid limit", (long long)width);
         if (tmp && aligned16(tmp) && nslots >= 4 * kGroups) {

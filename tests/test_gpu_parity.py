@@ -492,6 +492,48 @@ def test_longrow_softmax_layer_whole_vector(ctx):
     assert abs(got.sum(dtype=np.float64) - 1.0) < 1e-5
 
 
+def _long_ops(c, rows, cols, wl):
+    """The long-row forward ops as (name, launch closure, oracle, float64 value)."""
+    return (
+        ("layernorm", lambda dx, dg, db, y: c.layernorm(dx, dg, db, y, rows, cols, 1e-5),
+         lambda x, g, b: O.layernorm(x, cols, g, b, 1e-5).reshape(x.shape),
+         lambda x, g, b: X.layernorm(x, cols, g, b, 1e-5)),
+        ("rmsnorm", lambda dx, dg, db, y: c.rmsnorm(dx, dg, wl, y, rows, cols, 1e-6),
+         lambda x, g, b: np.stack([O.rmsnorm_whole(x[i], g[:wl], 1e-6) for i in range(rows)]).reshape(x.shape),
+         lambda x, g, b: X.rmsnorm(x, cols, g, wl, 1e-6)),
+        ("softmax", lambda dx, dg, db, y: c.softmax(dx, y, rows, cols, M.SOFTMAX_MUL_INV),
+         lambda x, g, b: O.softmax_rows(x, M.SOFTMAX_MUL_INV),
+         lambda x, g, b: X.softmax(x, M.SOFTMAX_MUL_INV)),
+    )
+
+
+def test_longrow_repeat_launches_give_the_same_bits(ctx):
+    """The combine folds the chunk partials in a fixed order, whatever order
+    the first pass's workgroups ran in: repeated launches give the same
+    bits, with calls of other shapes in between (1025 chunks with a short
+    last one, 18 chunks over 5 rows, 65 and 193 chunks), each within the
+    path's tolerance of the oracle."""
+    shapes = [(1, 4096 * 1024 + 12),
+              (5, 70000),
+              (2, 4096 * 65),
+              (1, 4096 * 64 * 3 + 4)]
+    first = {}
+    for rep in range(3):
+        for rows, cols in shapes:
+            x = (np.random.default_rng(rows * 7 + cols).standard_normal((rows, cols), dtype=np.float32) * 1.7
+                 + 0.3)
+            g = (1 + 0.05 * np.random.default_rng(cols).standard_normal(cols)).astype(np.float32)
+            b = (0.05 * np.random.default_rng(cols + 1).standard_normal(cols)).astype(np.float32)
+            for name, f, ref, exact in _long_ops(ctx, rows, cols, cols // 2):
+                got = run(ctx, f, x, g, b, out_shape=x.shape)
+                key = (rows, cols, name)
+                if rep == 0:
+                    first[key] = got
+                    assert_close_or_nearer_exact(got, ref(x, g, b), exact(x, g, b), f"{name} {rows}x{cols}")
+                else:
+                    assert_bitexact(got, first[key], f"{name} {rows}x{cols} launch {rep}")
+
+
 # ---------------------------------------------------------------------------
 # Output store policy (mimir_ctx_set_output_caching): same bits either way
 # ---------------------------------------------------------------------------
