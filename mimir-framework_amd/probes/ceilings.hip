@@ -20,8 +20,11 @@
 //             consecutive rows, w = 1 (sequential) to 32000 (a permutation);
 //   cache     a 128 MiB read followed by a read + write of the same data:
 //             how much of the second read the MALL serves, by the first
-//             read's load policy.
-// Usage: ceilings [streams|rows|gather|cache|all]
+//             read's load policy;
+//   addresses where this process's allocations land: device memory
+//             (hipMalloc, small and large), pinned host memory
+//             (hipHostMalloc) and the host heap (not part of "all").
+// Usage: ceilings [streams|rows|gather|cache|addresses|all]
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -302,6 +305,21 @@ void cache() {
     CK(hipFree(sink));
 }
 
+void addresses() {
+    void* small = nullptr;
+    void* big = nullptr;
+    void* pinned = nullptr;
+    CK(hipMalloc(&small, 4096));
+    CK(hipMalloc(&big, size_t(1) << 30));
+    CK(hipHostMalloc(&pinned, size_t(1) << 20, 0));
+    std::vector<char> heap(16);
+    std::printf("hipMalloc(4 KiB) %p  hipMalloc(1 GiB) %p  hipHostMalloc(1 MiB) %p  host heap %p\n", small, big,
+                pinned, static_cast<void*>(heap.data()));
+    CK(hipFree(small));
+    CK(hipFree(big));
+    CK(hipHostFree(pinned));
+}
+
 }  // namespace
 
 int main(int argc, char** argv) {
@@ -314,5 +332,6 @@ int main(int argc, char** argv) {
     if (all || !std::strcmp(what, "rows")) rows();
     if (all || !std::strcmp(what, "gather")) gather();
     if (all || !std::strcmp(what, "cache")) cache();
+    if (!std::strcmp(what, "addresses")) addresses();
     return 0;
 }
