@@ -80,10 +80,12 @@ def test_layernorm_bwd(ctx, cols, affine):
 
 
 @pytest.mark.parametrize("rows,cols", [(8192, 4096), (3000, 512), (1025, 64), (70000, 16), (8192, 4095), (3000, 1023),
-                                       (70000, 17)])
+                                       (70000, 17), (100, 4096), (300, 64), (2000, 20)])
 def test_layernorm_bwd_many_rows(ctx, rows, cols):
     # Many rows per persistent-grid slot: dgamma / dbeta sums over thousands of
-    # tokens (odd widths: the 4-byte-column kernel).
+    # tokens (odd widths: the 4-byte-column kernel).  100 and 300 rows: slot
+    # counts that are not a multiple of the one-launch slot sum's 128 slot
+    # lanes; 20 columns: its last tile of 8 float4 columns half empty.
     x = rng.standard_normal((rows, cols), dtype=np.float32)
     dy = rng.standard_normal((rows, cols), dtype=np.float32)
     g = (1 + 0.02 * rng.standard_normal(cols)).astype(np.float32)
