@@ -95,9 +95,9 @@ struct DSilu {
 // dx = dy * f'(x), or dx += that (accumulate_grad into a present gradient).
 // KEEP: dx through the caches (mimir_ctx_set_output_caching), as for every
 // *_vec kernel below with a KEEP parameter.
-template <class F, bool ACC, bool KEEP>
-__global__ __launch_bounds__(kBlock) void dact_vec(const float* x, const float* dy, float* dx, int64_t n4, F f) {
-    const int64_t i = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
+template <class F, bool ACC, bool KEEP, int BS = kBlock>
+__global__ __launch_bounds__(BS) void dact_vec(const float* x, const float* dy, float* dx, int64_t n4, F f) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * BS + threadIdx.x;
     if (i >= n4) return;
     const f4 xv = ld4<true>(x + 4 * i);
     const f4 g = ld4<true>(dy + 4 * i);
@@ -127,12 +127,16 @@ int run_dact(mimir_ctx* ctx, const float* x, const float* dy, float* dx, int64_t
     if (aligned16(x) && aligned16(dy) && aligned16(dx)) {
         const int64_t n4 = n / 4;
         if (n4 > 0) {
-            unsigned blocks;
-            if (!grid_for(n4, kBlock, kBlock, &blocks))
-                return fail(ctx, MIMIR_EINVAL, "%s: n=%lld exceeds the grid limit", name, (long long)n);
-            if (ctx->keep_outputs) dact_vec<F, ACC, true><<<blocks, kBlock, 0, ctx->stream>>>(x, dy, dx, n4, f);
-            else dact_vec<F, ACC, false><<<blocks, kBlock, 0, ctx->stream>>>(x, dy, dx, n4, f);
-            if (int st = launched(ctx, name)) return st;
+            const int st = with_block(ew_block(ctx->tune), [&](auto bsc) {
+                constexpr int BS = decltype(bsc)::value;
+                unsigned blocks;
+                if (!grid_for(n4, BS, BS, &blocks))
+                    return fail(ctx, MIMIR_EINVAL, "%s: n=%lld exceeds the grid limit", name, (long long)n);
+                if (ctx->keep_outputs) dact_vec<F, ACC, true, BS><<<blocks, BS, 0, ctx->stream>>>(x, dy, dx, n4, f);
+                else dact_vec<F, ACC, false, BS><<<blocks, BS, 0, ctx->stream>>>(x, dy, dx, n4, f);
+                return launched(ctx, name);
+            });
+            if (st) return st;
         }
         done = n4 * 4;
     }
@@ -150,10 +154,10 @@ int run_dact(mimir_ctx* ctx, const float* x, const float* dy, float* dx, int64_t
 
 // g0 = dy*b and g1 = dy*a are formed before either is accumulated, as in
 // the reference, so da / db may alias dy (element for element).
-template <bool ACC_A, bool ACC_B, bool KEEP>
-__global__ __launch_bounds__(kBlock) void mul_bwd_vec(const float* a, const float* b, const float* dy, float* da,
-                                                      float* db, int64_t n4) {
-    const int64_t i = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
+template <bool ACC_A, bool ACC_B, bool KEEP, int BS = kBlock>
+__global__ __launch_bounds__(BS) void mul_bwd_vec(const float* a, const float* b, const float* dy, float* da,
+                                                  float* db, int64_t n4) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * BS + threadIdx.x;
     if (i >= n4) return;
     const f4 g = ld4<true>(dy + 4 * i);
     f4 g0 = g * ld4<true>(b + 4 * i);
@@ -219,9 +223,9 @@ __global__ __launch_bounds__(kBlock) void acc_scalar(const float* src, float* ds
 }
 
 // Equal sizes and no aliasing: da (+)= dy and db (+)= dy in one pass.
-template <bool ACC_A, bool ACC_B, bool KEEP>
-__global__ __launch_bounds__(kBlock) void add_bwd_vec(const float* dy, float* da, float* db, int64_t n4) {
-    const int64_t i = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
+template <bool ACC_A, bool ACC_B, bool KEEP, int BS = kBlock>
+__global__ __launch_bounds__(BS) void add_bwd_vec(const float* dy, float* da, float* db, int64_t n4) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * BS + threadIdx.x;
     if (i >= n4) return;
     const f4 g = ld4<true>(dy + 4 * i);
     // Every load before the stores, which are written through (two output
@@ -232,22 +236,22 @@ __global__ __launch_bounds__(kBlock) void add_bwd_vec(const float* dy, float* da
     if (db) st_out<KEEP, kStoreThrough>(db + 4 * i, ob);
 }
 
-template <bool KEEP>
+template <bool KEEP, int BS>
 void launch_mul_bwd(mimir_ctx* ctx, unsigned blocks, bool A, bool B, const float* a, const float* b, const float* dy,
                     float* da, float* db, int64_t n4) {
-    if (A && B) mul_bwd_vec<true, true, KEEP><<<blocks, kBlock, 0, ctx->stream>>>(a, b, dy, da, db, n4);
-    else if (A) mul_bwd_vec<true, false, KEEP><<<blocks, kBlock, 0, ctx->stream>>>(a, b, dy, da, db, n4);
-    else if (B) mul_bwd_vec<false, true, KEEP><<<blocks, kBlock, 0, ctx->stream>>>(a, b, dy, da, db, n4);
-    else mul_bwd_vec<false, false, KEEP><<<blocks, kBlock, 0, ctx->stream>>>(a, b, dy, da, db, n4);
+    if (A && B) mul_bwd_vec<true, true, KEEP, BS><<<blocks, BS, 0, ctx->stream>>>(a, b, dy, da, db, n4);
+    else if (A) mul_bwd_vec<true, false, KEEP, BS><<<blocks, BS, 0, ctx->stream>>>(a, b, dy, da, db, n4);
+    else if (B) mul_bwd_vec<false, true, KEEP, BS><<<blocks, BS, 0, ctx->stream>>>(a, b, dy, da, db, n4);
+    else mul_bwd_vec<false, false, KEEP, BS><<<blocks, BS, 0, ctx->stream>>>(a, b, dy, da, db, n4);
 }
 
-template <bool KEEP>
+template <bool KEEP, int BS>
 void launch_add_bwd(mimir_ctx* ctx, unsigned blocks, bool A, bool B, const float* dy, float* da, float* db,
                     int64_t n4) {
-    if (A && B) add_bwd_vec<true, true, KEEP><<<blocks, kBlock, 0, ctx->stream>>>(dy, da, db, n4);
-    else if (A) add_bwd_vec<true, false, KEEP><<<blocks, kBlock, 0, ctx->stream>>>(dy, da, db, n4);
-    else if (B) add_bwd_vec<false, true, KEEP><<<blocks, kBlock, 0, ctx->stream>>>(dy, da, db, n4);
-    else add_bwd_vec<false, false, KEEP><<<blocks, kBlock, 0, ctx->stream>>>(dy, da, db, n4);
+    if (A && B) add_bwd_vec<true, true, KEEP, BS><<<blocks, BS, 0, ctx->stream>>>(dy, da, db, n4);
+    else if (A) add_bwd_vec<true, false, KEEP, BS><<<blocks, BS, 0, ctx->stream>>>(dy, da, db, n4);
+    else if (B) add_bwd_vec<false, true, KEEP, BS><<<blocks, BS, 0, ctx->stream>>>(dy, da, db, n4);
+    else add_bwd_vec<false, false, KEEP, BS><<<blocks, BS, 0, ctx->stream>>>(dy, da, db, n4);
 }
 
 int accumulate(mimir_ctx* ctx, const float* src, float* dst, int64_t n, bool acc, const char* name) {
@@ -2097,12 +2101,16 @@ int mimir_mul_bwd(mimir_ctx* ctx, const float* a, const float* b, const float* d
     if (aligned16(a) && aligned16(b) && aligned16(dy) && (!da || aligned16(da)) && (!db || aligned16(db))) {
         const int64_t n4 = n / 4;
         if (n4 > 0) {
-            unsigned blocks;
-            if (!grid_for(n4, kBlock, kBlock, &blocks))
-                return fail(ctx, MIMIR_EINVAL, "Multiply backward: n=%lld exceeds the grid limit", (long long)n);
-            if (ctx->keep_outputs) launch_mul_bwd<true>(ctx, blocks, A, B, a, b, dy, da, db, n4);
-            else launch_mul_bwd<false>(ctx, blocks, A, B, a, b, dy, da, db, n4);
-            if (int st = launched(ctx, "mul_bwd_vec")) return st;
+            const int st = with_block(ew_block(ctx->tune), [&](auto bsc) {
+                constexpr int BS = decltype(bsc)::value;
+                unsigned blocks;
+                if (!grid_for(n4, BS, BS, &blocks))
+                    return fail(ctx, MIMIR_EINVAL, "Multiply backward: n=%lld exceeds the grid limit", (long long)n);
+                if (ctx->keep_outputs) launch_mul_bwd<true, BS>(ctx, blocks, A, B, a, b, dy, da, db, n4);
+                else launch_mul_bwd<false, BS>(ctx, blocks, A, B, a, b, dy, da, db, n4);
+                return launched(ctx, "mul_bwd_vec");
+            });
+            if (st) return st;
         }
         done = n4 * 4;
     }
@@ -2130,12 +2138,15 @@ int mimir_add_bwd(mimir_ctx* ctx, const float* dy, int64_t na, int64_t nb, float
         MIMIR_ENTER(ctx);
         const bool alias = da == dy || db == dy || (da && da == db);
         if (!alias && aligned16(dy) && (!da || aligned16(da)) && (!db || aligned16(db)) && (na % 4) == 0) {
-            unsigned blocks;
-            if (!grid_for(na / 4, kBlock, kBlock, &blocks))
-                return fail(ctx, MIMIR_EINVAL, "Add backward: n=%lld exceeds the grid limit", (long long)na);
-            if (ctx->keep_outputs) launch_add_bwd<true>(ctx, blocks, A, B, dy, da, db, na / 4);
-            else launch_add_bwd<false>(ctx, blocks, A, B, dy, da, db, na / 4);
-            return launched(ctx, "add_bwd_vec");
+            return with_block(ew_block(ctx->tune), [&](auto bsc) {
+                constexpr int BS = decltype(bsc)::value;
+                unsigned blocks;
+                if (!grid_for(na / 4, BS, BS, &blocks))
+                    return fail(ctx, MIMIR_EINVAL, "Add backward: n=%lld exceeds the grid limit", (long long)na);
+                if (ctx->keep_outputs) launch_add_bwd<true, BS>(ctx, blocks, A, B, dy, da, db, na / 4);
+                else launch_add_bwd<false, BS>(ctx, blocks, A, B, dy, da, db, na / 4);
+                return launched(ctx, "add_bwd_vec");
+            });
         }
         // Aliased gradients: the second accumulation sees the first, as the
         // reference's in-place adds into its gradient map do.

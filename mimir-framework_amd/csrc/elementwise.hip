@@ -62,30 +62,32 @@ __device__ __forceinline__ f4 map4(F f, f4 a, f4 b) {
     return f4{f(a.x, b.x), f(a.y, b.y), f(a.z, b.z), f(a.w, b.w)};
 }
 
-template <class F, int VPT, bool KEEP>
-__global__ __launch_bounds__(kBlock) void unary_vec(const float* x, float* y, int64_t n4, F f) {
-    const int64_t first = static_cast<int64_t>(blockIdx.x) * VPT * kBlock + threadIdx.x;
+// BS: the workgroup size (rows.hpp ew_block); VPT float4 per thread, a
+// workgroup-width apart.
+template <class F, int VPT, bool KEEP, int BS = kBlock>
+__global__ __launch_bounds__(BS) void unary_vec(const float* x, float* y, int64_t n4, F f) {
+    const int64_t first = static_cast<int64_t>(blockIdx.x) * VPT * BS + threadIdx.x;
     f4 v[VPT];
 #pragma unroll
     for (int j = 0; j < VPT; ++j) {
-        const int64_t i = first + static_cast<int64_t>(j) * kBlock;
+        const int64_t i = first + static_cast<int64_t>(j) * BS;
         if (i < n4) v[j] = ld4<true>(x + 4 * i);
     }
 #pragma unroll
     for (int j = 0; j < VPT; ++j) {
-        const int64_t i = first + static_cast<int64_t>(j) * kBlock;
+        const int64_t i = first + static_cast<int64_t>(j) * BS;
         if (i < n4) st_out<KEEP, kStoreThrough>(y + 4 * i, map4(f, v[j]));  // one read, one write: written through
     }
 }
 
-template <class F, int VPT, bool KEEP>
-__global__ __launch_bounds__(kBlock) void binary_vec(const float* a, const float* b, float* y,
-                                                     int64_t n4, F f) {
-    const int64_t first = static_cast<int64_t>(blockIdx.x) * VPT * kBlock + threadIdx.x;
+template <class F, int VPT, bool KEEP, int BS = kBlock>
+__global__ __launch_bounds__(BS) void binary_vec(const float* a, const float* b, float* y,
+                                                 int64_t n4, F f) {
+    const int64_t first = static_cast<int64_t>(blockIdx.x) * VPT * BS + threadIdx.x;
     f4 va[VPT], vb[VPT];
 #pragma unroll
     for (int j = 0; j < VPT; ++j) {
-        const int64_t i = first + static_cast<int64_t>(j) * kBlock;
+        const int64_t i = first + static_cast<int64_t>(j) * BS;
         if (i < n4) {
             va[j] = ld4<true>(a + 4 * i);
             vb[j] = ld4<true>(b + 4 * i);
@@ -93,7 +95,7 @@ __global__ __launch_bounds__(kBlock) void binary_vec(const float* a, const float
     }
 #pragma unroll
     for (int j = 0; j < VPT; ++j) {
-        const int64_t i = first + static_cast<int64_t>(j) * kBlock;
+        const int64_t i = first + static_cast<int64_t>(j) * BS;
         if (i < n4) st_out<KEEP>(y + 4 * i, map4(f, va[j], vb[j]));
     }
 }
@@ -149,24 +151,24 @@ unsigned stride_grid(int64_t n) {
     return static_cast<unsigned>(b < 1 ? 1 : (b > 65536 ? 65536 : b));
 }
 
-template <class F, int VPT>
+template <class F, int VPT, int BS = kBlock>
 int launch_unary(mimir_ctx* ctx, const float* x, float* y, int64_t n4, F f, const char* name) {
     unsigned blocks;
-    if (!grid_for(n4, static_cast<int64_t>(VPT) * kBlock, kBlock, &blocks))
+    if (!grid_for(n4, static_cast<int64_t>(VPT) * BS, BS, &blocks))
         return fail(ctx, MIMIR_EINVAL, "%s: n=%lld exceeds the grid limit", name, (long long)(4 * n4));
-    if (ctx->keep_outputs) unary_vec<F, VPT, true><<<blocks, kBlock, 0, ctx->stream>>>(x, y, n4, f);
-    else unary_vec<F, VPT, false><<<blocks, kBlock, 0, ctx->stream>>>(x, y, n4, f);
+    if (ctx->keep_outputs) unary_vec<F, VPT, true, BS><<<blocks, BS, 0, ctx->stream>>>(x, y, n4, f);
+    else unary_vec<F, VPT, false, BS><<<blocks, BS, 0, ctx->stream>>>(x, y, n4, f);
     return launched(ctx, name);
 }
 
-template <class F, int VPT>
+template <class F, int VPT, int BS = kBlock>
 int launch_binary(mimir_ctx* ctx, const float* a, const float* b, float* y, int64_t n4, F f,
                   const char* name) {
     unsigned blocks;
-    if (!grid_for(n4, static_cast<int64_t>(VPT) * kBlock, kBlock, &blocks))
+    if (!grid_for(n4, static_cast<int64_t>(VPT) * BS, BS, &blocks))
         return fail(ctx, MIMIR_EINVAL, "%s: n=%lld exceeds the grid limit", name, (long long)(4 * n4));
-    if (ctx->keep_outputs) binary_vec<F, VPT, true><<<blocks, kBlock, 0, ctx->stream>>>(a, b, y, n4, f);
-    else binary_vec<F, VPT, false><<<blocks, kBlock, 0, ctx->stream>>>(a, b, y, n4, f);
+    if (ctx->keep_outputs) binary_vec<F, VPT, true, BS><<<blocks, BS, 0, ctx->stream>>>(a, b, y, n4, f);
+    else binary_vec<F, VPT, false, BS><<<blocks, BS, 0, ctx->stream>>>(a, b, y, n4, f);
     return launched(ctx, name);
 }
 
@@ -180,7 +182,11 @@ int run_unary(mimir_ctx* ctx, const float* x, float* y, int64_t n, F f, const ch
             switch (ctx->tune.ew_vpt) {
                 case 2: st = launch_unary<F, 2>(ctx, x, y, n4, f, name); break;
                 case 4: st = launch_unary<F, 4>(ctx, x, y, n4, f, name); break;
-                default: st = launch_unary<F, 1>(ctx, x, y, n4, f, name); break;
+                default:
+                    st = with_block(ew_block(ctx->tune), [&](auto bs) {
+                        return launch_unary<F, 1, decltype(bs)::value>(ctx, x, y, n4, f, name);
+                    });
+                    break;
             }
             if (st) return st;
         }
@@ -204,7 +210,11 @@ int run_binary(mimir_ctx* ctx, const float* a, const float* b, float* y, int64_t
             switch (ctx->tune.ew_vpt) {
                 case 2: st = launch_binary<F, 2>(ctx, a, b, y, n4, f, name); break;
                 case 4: st = launch_binary<F, 4>(ctx, a, b, y, n4, f, name); break;
-                default: st = launch_binary<F, 1>(ctx, a, b, y, n4, f, name); break;
+                default:
+                    st = with_block(ew_block(ctx->tune), [&](auto bs) {
+                        return launch_binary<F, 1, decltype(bs)::value>(ctx, a, b, y, n4, f, name);
+                    });
+                    break;
             }
             if (st) return st;
         }
@@ -222,9 +232,9 @@ int run_binary(mimir_ctx* ctx, const float* a, const float* b, float* y, int64_t
 // step loading its operand where it is used (many waves in flight hide the
 // latency: the kernel stays small).  The program is uniform across the grid,
 // so its branches never diverge.
-template <bool KEEP>
-__global__ __launch_bounds__(kBlock) void fused_chain_vec(const FuseProgram p, int64_t n4) {
-    const int64_t i = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
+template <bool KEEP, int BS = kBlock>
+__global__ __launch_bounds__(BS) void fused_chain_vec(const FuseProgram p, int64_t n4) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * BS + threadIdx.x;
     if (i >= n4) return;
     f4 v = ld4<true>(p.ins[0] + 4 * i);
     for (int k = 0; k < p.n_steps; ++k) {
@@ -264,11 +274,15 @@ int mimir::fused_chain(mimir_ctx* ctx, const FuseProgram& p, int64_t n) {
     int64_t done = 0;
     if (aligned && n / 4 > 0) {
         const int64_t n4 = n / 4;
-        unsigned blocks;
-        if (!grid_for(n4, kBlock, kBlock, &blocks)) return fail(ctx, MIMIR_EINVAL, "fused chain: grid too large");
-        if (ctx->keep_outputs) fused_chain_vec<true><<<blocks, kBlock, 0, ctx->stream>>>(p, n4);
-        else fused_chain_vec<false><<<blocks, kBlock, 0, ctx->stream>>>(p, n4);
-        if (int st = launched(ctx, "fused_chain_vec")) return st;
+        const int st = with_block(ew_block(ctx->tune), [&](auto bsc) {
+            constexpr int BS = decltype(bsc)::value;
+            unsigned blocks;
+            if (!grid_for(n4, BS, BS, &blocks)) return fail(ctx, MIMIR_EINVAL, "fused chain: grid too large");
+            if (ctx->keep_outputs) fused_chain_vec<true, BS><<<blocks, BS, 0, ctx->stream>>>(p, n4);
+            else fused_chain_vec<false, BS><<<blocks, BS, 0, ctx->stream>>>(p, n4);
+            return launched(ctx, "fused_chain_vec");
+        });
+        if (st) return st;
         done = n4 * 4;
     }
     if (n > done) {

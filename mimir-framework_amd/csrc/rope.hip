@@ -49,16 +49,17 @@ __device__ __forceinline__ void rotate(f4& x0, f4& x1, f4 c, f4 s) {
 }
 
 // KEEP: outputs through the caches (mimir_ctx_set_output_caching).
-template <int LOG2Q, int PPT, bool KEEP>
-__global__ __launch_bounds__(kBlock) void rope_vec(RopeArgs a) {
+// BS: the workgroup size (rows.hpp rope_block).
+template <int LOG2Q, int PPT, bool KEEP, int BS = kBlock>
+__global__ __launch_bounds__(BS) void rope_vec(RopeArgs a) {
     constexpr int Q = 1 << LOG2Q;
-    const int64_t first = static_cast<int64_t>(blockIdx.x) * PPT * kBlock + threadIdx.x;
+    const int64_t first = static_cast<int64_t>(blockIdx.x) * PPT * BS + threadIdx.x;
     const int64_t D = 2 * static_cast<int64_t>(a.half);
     f4 x0[PPT], x1[PPT], c[PPT], s[PPT];
     float* out[PPT];
 #pragma unroll
     for (int j = 0; j < PPT; ++j) {
-        const int64_t slot = first + static_cast<int64_t>(j) * kBlock;
+        const int64_t slot = first + static_cast<int64_t>(j) * BS;
         out[j] = nullptr;
         if (slot < a.total_slots) {
             const bool is_q = slot < a.q_slots;
@@ -110,12 +111,15 @@ __global__ __launch_bounds__(kBlock) void rope_scalar(RopeArgs a, int64_t q_pair
 
 template <int LOG2Q, int PPT>
 int launch_ppt(mimir_ctx* ctx, const RopeArgs& a) {
-    unsigned blocks;
-    if (!grid_for(a.total_slots, static_cast<int64_t>(PPT) * kBlock, kBlock, &blocks))
-        return fail(ctx, MIMIR_EINVAL, "RoPE: tensor exceeds the grid limit");
-    if (ctx->keep_outputs) rope_vec<LOG2Q, PPT, true><<<blocks, kBlock, 0, ctx->stream>>>(a);
-    else rope_vec<LOG2Q, PPT, false><<<blocks, kBlock, 0, ctx->stream>>>(a);
-    return launched(ctx, "rope_vec");
+    return with_block(rope_block(ctx->tune), [&](auto bsc) {
+        constexpr int BS = decltype(bsc)::value;
+        unsigned blocks;
+        if (!grid_for(a.total_slots, static_cast<int64_t>(PPT) * BS, BS, &blocks))
+            return fail(ctx, MIMIR_EINVAL, "RoPE: tensor exceeds the grid limit");
+        if (ctx->keep_outputs) rope_vec<LOG2Q, PPT, true, BS><<<blocks, BS, 0, ctx->stream>>>(a);
+        else rope_vec<LOG2Q, PPT, false, BS><<<blocks, BS, 0, ctx->stream>>>(a);
+        return launched(ctx, "rope_vec");
+    });
 }
 
 // Four slots per thread (a workgroup-width apart) measured best on MI355X at

@@ -11,6 +11,7 @@
 #include <cstdint>
 #include <cstdlib>
 #include <cstring>
+#include <type_traits>
 
 namespace mimir {
 
@@ -47,7 +48,7 @@ struct RowShape {
 // Tuning override, read once per context from MIMIR_TUNE, e.g.
 //   MIMIR_TUNE="norm=1024x1x1024,layernorm=512x2x512,softmax=64x4x64,ew=1,gather=1024,rope=1,
 //               lnbwd=512x2x512,lnbwd_grid=512,chain=0,attnbwd_heads=4,attnbwd_blocks=2,
-//               embmerge=0,embsort=0,embruns=0,blas=0,lnbwd_narrow=0,lrcpw=2"
+//               embmerge=0,embsort=0,embruns=0,blas=0,lnbwd_narrow=0,lrcpw=2,ewbs=128"
 // Each entry selects among the compiled variants above; an entry that does
 // not fit a call (row too wide for it) is ignored for that call.  Unset, the
 // measured defaults apply.  Used for sweeps; results are identical.
@@ -70,6 +71,7 @@ struct Tuning {
     int blas_lt = -1;           // library products: hipBLASLt first (-1, 1) or rocBLAS only (0)
     int lnbwd_narrow = -1;      // LayerNorm backward, rows <= 64 floats: several rows per wave (-1, 1) or not (0)
     int lr_cpw = 0;             // long rows: 4096-float chunks per workgroup of the first pass (1, 2, 4; 0: measured default)
+    int ew_bs = 0;              // workgroup size of the one-float4-per-thread streaming kernels (64 .. 1024; 0: default)
 };
 
 inline bool parse_shape(const char* v, RowShape* s) {
@@ -114,6 +116,7 @@ inline Tuning read_tuning() {
         else if (!std::strcmp(k, "blas")) t.blas_lt = std::atoi(v);
         else if (!std::strcmp(k, "lnbwd_narrow")) t.lnbwd_narrow = std::atoi(v);
         else if (!std::strcmp(k, "lrcpw")) t.lr_cpw = std::atoi(v);
+        else if (!std::strcmp(k, "ewbs")) t.ew_bs = std::atoi(v);
     }
     return t;
 }
@@ -146,6 +149,36 @@ inline RowShape default_softmax_shape(int64_t c4) {
     if (c4 <= 2048) return {1024, 2, 1024};
     if (c4 <= 4096) return {1024, 4, 1024};
     return {0, 0, 0};
+}
+
+// Workgroup size of the streaming kernels that move one float4 per thread
+// (unary_vec / binary_vec, dact_vec, mul_bwd_vec, add_bwd_vec,
+// fused_chain_vec, copy16_kernel): the tuned value if it is one of the
+// compiled sizes, else the default.  Measured on MI355X at configs[4]
+// (% of 8 TB/s for 64 / 128 / 256 threads): add 82.0 / 82.0 / 79.3,
+// SiLU-gated product 83.5 / 83.3 / 81.5, multiply backward 80.6 / 81.7 / 75.9,
+// add backward 79.2 / 80.6 / 78.0, GELU backward 83.3 / 83.0 / 81.4, GELU
+// 84.5 / 84.2 / 84.3: the same stream in workgroups of 128 threads instead of
+// 256 gains up to 6 points.  RoPE (four slots per thread) keeps 256 threads
+// (82.4 against 80.6 at 128; rope_block).
+constexpr int kEwBlock = 128;
+inline int ew_block(const Tuning& t) {
+    return t.ew_bs == 64 || t.ew_bs == 128 || t.ew_bs == 256 || t.ew_bs == 512 || t.ew_bs == 1024 ? t.ew_bs
+                                                                                                  : kEwBlock;
+}
+inline int rope_block(const Tuning& t) { return t.ew_bs ? ew_block(t) : 256; }
+
+// Calls f(std::integral_constant<int, BS>{}) for the workgroup size `bs`
+// (one of 64, 128, 256, 512, 1024).
+template <class Fn>
+inline auto with_block(int bs, Fn&& f) {
+    switch (bs) {
+        case 64: return f(std::integral_constant<int, 64>{});
+        case 128: return f(std::integral_constant<int, 128>{});
+        case 512: return f(std::integral_constant<int, 512>{});
+        case 1024: return f(std::integral_constant<int, 1024>{});
+        default: return f(std::integral_constant<int, 256>{});
+    }
 }
 
 inline bool shape_fits(const RowShape& s, int64_t c4) {

@@ -15,19 +15,19 @@ namespace {
 // Streaming copy: one 16-byte vector per thread for the aligned body (the
 // grid covers it in one pass up to 2^30 workgroups), bytes for the rest.
 // KEEP: the copy stays in the caches (mimir_ctx_set_output_caching).
-template <bool KEEP>
-__global__ __launch_bounds__(kBlock) void copy16_kernel(const u4* __restrict__ src,
-                                                         u4* __restrict__ dst, int64_t n16) {
-    const int64_t stride = static_cast<int64_t>(gridDim.x) * kBlock;
-    for (int64_t i = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x; i < n16; i += stride) {
+template <bool KEEP, int BS = kBlock>
+__global__ __launch_bounds__(BS) void copy16_kernel(const u4* __restrict__ src,
+                                                     u4* __restrict__ dst, int64_t n16) {
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * BS;
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * BS + threadIdx.x; i < n16; i += stride) {
         const u4 v = __builtin_nontemporal_load(src + i);
         if constexpr (KEEP) dst[i] = v;
         else st_stream(dst + i, v);
     }
 }
 
-unsigned full_grid(int64_t n) {
-    const int64_t b = (n + kBlock - 1) / kBlock;
+unsigned full_grid(int64_t n, int bs = kBlock) {
+    const int64_t b = (n + bs - 1) / bs;
     return static_cast<unsigned>(b < 1 ? 1 : (b > (int64_t(1) << 30) ? (int64_t(1) << 30) : b));
 }
 
@@ -238,13 +238,17 @@ int mimir_copy(mimir_ctx* ctx, void* dst_dev, const void* src_dev, size_t bytes)
     if (aligned16(s) && aligned16(d)) {
         n16 = static_cast<int64_t>(bytes / 16);
         if (n16 > 0) {
-            if (ctx->keep_outputs)
-                copy16_kernel<true><<<full_grid(n16), kBlock, 0, ctx->stream>>>(
-                    reinterpret_cast<const u4*>(s), reinterpret_cast<u4*>(d), n16);
-            else
-                copy16_kernel<false><<<full_grid(n16), kBlock, 0, ctx->stream>>>(
-                    reinterpret_cast<const u4*>(s), reinterpret_cast<u4*>(d), n16);
-            if (int st = launched(ctx, "copy16_kernel")) return st;
+            const int st = with_block(ew_block(ctx->tune), [&](auto bsc) {
+                constexpr int BS = decltype(bsc)::value;
+                if (ctx->keep_outputs)
+                    copy16_kernel<true, BS><<<full_grid(n16, BS), BS, 0, ctx->stream>>>(
+                        reinterpret_cast<const u4*>(s), reinterpret_cast<u4*>(d), n16);
+                else
+                    copy16_kernel<false, BS><<<full_grid(n16, BS), BS, 0, ctx->stream>>>(
+                        reinterpret_cast<const u4*>(s), reinterpret_cast<u4*>(d), n16);
+                return launched(ctx, "copy16_kernel");
+            });
+            if (st) return st;
         }
     }
     const int64_t rest = static_cast<int64_t>(bytes) - n16 * 16;

@@ -67,8 +67,11 @@ def test_keep_variants_store_as_intended(src, tmp_path):
             else:
                 assert all(nt), f"{name}: a streamed output lost its non-temporal hint"
             continue
-        keep = norm.group(1) == "1" if norm else "Lb1EEEv" in name
-        if not (norm or keep or "Lb0EEEv" in name):
+        # KEEP is the last template parameter, or the one before a trailing
+        # workgroup size (the streaming kernels' BS).
+        tail = re.search(r"Lb([01])E(?:Li\d+E)?EEv", name)
+        keep = norm.group(1) == "1" if norm else bool(tail and tail.group(1) == "1")
+        if not (norm or tail):
             continue  # not a KEEP-templated kernel
         if src in ("backward", "runtime") and not any(k in name for k in KEEP_KERNELS):
             continue  # a bool template parameter that is not KEEP
