@@ -13,7 +13,8 @@
 //                in a fixed order (per-thread strided sums with eight loads in
 //                flight, then the DPP/LDS tree), so the result does not
 //                depend on scheduling;
-//   3. apply   : per chunk, the elementwise normalisation with the row stats.
+//   3. apply   : per quarter chunk (128 threads x 2 float4), the elementwise
+//                normalisation with the row stats.
 // LayerNorm's variance is two-pass within each chunk: the chunk is held in
 // registers, so its sum and its squared deviations about its own mean come
 // from one read.  The combine merges the chunks in float64 by the pairwise
@@ -273,25 +274,29 @@ __device__ __forceinline__ float softmax_out(float xv, float m, float s) {
 
 // Pass 3: normalise one chunk.  K: 0 LayerNorm, 1 RMSNorm, 2 add+RMSNorm, 3 softmax.
 // KEEP: y through the caches (mimir_ctx_set_output_caching).
-template <int K, int MODE, bool KEEP>
-__global__ __launch_bounds__(kBlock) void lr_apply(LongArgs a) {
+// Each workgroup of BS threads takes a piece of BS*VPT float4 of the row,
+// VPT per thread a workgroup-width apart (256 x 4: one chunk).  Pieces are
+// walked as chunks are (chunk_of).
+template <int K, int MODE, bool KEEP, int BS = kBlock, int VPT = kChunkVec>
+__global__ __launch_bounds__(BS) void lr_apply(LongArgs a) {
     const int64_t row = blockIdx.y;
-    const int64_t chunk = chunk_of(a);
     const int64_t c4n = a.cols >> 2;
+    const int64_t npieces = (c4n + BS * VPT - 1) / (BS * VPT);
+    const int64_t piece = a.reverse ? npieces - 1 - static_cast<int64_t>(blockIdx.x) : static_cast<int64_t>(blockIdx.x);
     const int64_t base = row * a.cols;
     const float s0 = a.stats[4 * row];
     const float s1 = a.stats[4 * row + 1];
     const float s2 = a.stats[4 * row + 2];
     const float* src = (K == 2) ? a.r_out : a.x;  // add+RMSNorm re-reads the residual it wrote
-    f4 v[kChunkVec];
+    f4 v[VPT];
 #pragma unroll
-    for (int j = 0; j < kChunkVec; ++j) {
-        const int64_t c4 = chunk * kChunk4 + static_cast<int64_t>(j) * kBlock + threadIdx.x;
+    for (int j = 0; j < VPT; ++j) {
+        const int64_t c4 = piece * (BS * VPT) + static_cast<int64_t>(j) * BS + threadIdx.x;
         if (c4 < c4n) v[j] = ld4<true>(src + base + 4 * c4);
     }
 #pragma unroll
-    for (int j = 0; j < kChunkVec; ++j) {
-        const int64_t c4 = chunk * kChunk4 + static_cast<int64_t>(j) * kBlock + threadIdx.x;
+    for (int j = 0; j < VPT; ++j) {
+        const int64_t c4 = piece * (BS * VPT) + static_cast<int64_t>(j) * BS + threadIdx.x;
         if (c4 >= c4n) continue;
         const int64_t c = 4 * c4;
         f4 o;
@@ -342,10 +347,29 @@ bool mimir::longrow_applies(int64_t rows, int64_t cols) {
 
 namespace {
 
+template <int K, int MODE, int BS, int VPT>
+void launch_apply_shape(mimir_ctx* ctx, const LongArgs& a) {
+    const int64_t npieces = ((a.cols >> 2) + BS * VPT - 1) / (BS * VPT);
+    const dim3 grid(static_cast<unsigned>(npieces), static_cast<unsigned>(a.rows));
+    if (ctx->keep_outputs) lr_apply<K, MODE, true, BS, VPT><<<grid, BS, 0, ctx->stream>>>(a);
+    else lr_apply<K, MODE, false, BS, VPT><<<grid, BS, 0, ctx->stream>>>(a);
+}
+
+// The apply pass's workgroup shape: 128 threads x 2 float4 (a quarter of a
+// chunk) by default, measured on MI355X on one 2^25-float row against one
+// chunk per 256 x 4: softmax 66.7 -> 64.6-64.9 us, RMSNorm 64.4-65.0 ->
+// 62.0-62.2, LayerNorm 69.4-69.6 -> 66.9-67.0 for the whole op (256 x 1,
+// 128 x 1, 512 x 1 and 1024 x 1 in between).  MIMIR_TUNE lrapply=256x4
+// selects the chunk shape, which is also the fallback when a row has more
+// quarter chunks than one launch dimension holds.
 template <int K, int MODE>
-void launch_apply(mimir_ctx* ctx, dim3 grid, const LongArgs& a) {
-    if (ctx->keep_outputs) lr_apply<K, MODE, true><<<grid, kBlock, 0, ctx->stream>>>(a);
-    else lr_apply<K, MODE, false><<<grid, kBlock, 0, ctx->stream>>>(a);
+void launch_apply(mimir_ctx* ctx, dim3, const LongArgs& a) {
+    constexpr int BS = 128, VPT = 2;
+    const bool chunk = ctx->tune.lr_apply_bs == kBlock && ctx->tune.lr_apply_vpt == kChunkVec;
+    if (!chunk && dispatch_fits(((a.cols >> 2) + BS * VPT - 1) / (BS * VPT), BS))
+        launch_apply_shape<K, MODE, BS, VPT>(ctx, a);
+    else
+        launch_apply_shape<K, MODE, kBlock, kChunkVec>(ctx, a);  // longrow_applies checked this one
 }
 
 }  // namespace

@@ -73,6 +73,8 @@ struct Tuning {
     int lnbwd_narrow = -1;      // LayerNorm backward, rows <= 64 floats: several rows per wave (-1, 1) or not (0)
     int lr_cpw = 0;             // long rows: 4096-float chunks per workgroup of the first pass (1, 2, 4; 0: measured default)
     int ew_bs = 0;              // workgroup size of the one-float4-per-thread streaming kernels (64 .. 1024; 0: default)
+    int lr_apply_bs = 0;        // long rows' apply pass shape (lrapply=256x4: the chunk shape)
+    int lr_apply_vpt = 0;
 };
 
 inline bool parse_shape(const char* v, RowShape* s) {
@@ -118,6 +120,11 @@ inline Tuning read_tuning() {
         else if (!std::strcmp(k, "lnbwd_narrow")) t.lnbwd_narrow = std::atoi(v);
         else if (!std::strcmp(k, "lrcpw")) t.lr_cpw = std::atoi(v);
         else if (!std::strcmp(k, "ewbs")) t.ew_bs = std::atoi(v);
+        else if (!std::strcmp(k, "lrapply")) {
+            char* end = nullptr;
+            t.lr_apply_bs = static_cast<int>(std::strtol(v, &end, 10));
+            t.lr_apply_vpt = *end == 'x' ? std::atoi(end + 1) : 0;
+        }
     }
     return t;
 }

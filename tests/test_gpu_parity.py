@@ -414,6 +414,48 @@ def test_longrow_chunks_per_workgroup(ctx, cpw):
         c.close()
 
 
+@pytest.mark.parametrize("rows,cols", [(3, 4096 * 7 + 20), (1, 4096 * 64 * 3 + 4), (2, 70000)])
+def test_longrow_apply_shapes_agree(ctx, rows, cols):
+    """The apply pass in its default shape (128 threads x 2 float4) and in the
+    chunk shape (MIMIR_TUNE lrapply=256x4) reads the same row statistics and
+    applies the same per-element formula: LayerNorm, RMSNorm, add+RMSNorm
+    and softmax, over rows whose last chunk is partial, give the same bits."""
+    import os
+    old = os.environ.get("MIMIR_TUNE")
+    os.environ["MIMIR_TUNE"] = "lrapply=256x4"
+    try:
+        c = M.Context(0)
+    finally:
+        if old is None:
+            del os.environ["MIMIR_TUNE"]
+        else:
+            os.environ["MIMIR_TUNE"] = old
+    try:
+        x = (rng.standard_normal((rows, cols), dtype=np.float32) * 1.3 + 0.2)
+        r = rng.standard_normal((rows, cols), dtype=np.float32)
+        g = (1 + 0.05 * rng.standard_normal(cols)).astype(np.float32)
+        b = (0.05 * rng.standard_normal(cols)).astype(np.float32)
+        ops = (("layernorm", lambda cc: (lambda dx, dr, dg, db, y: cc.layernorm(dx, dg, db, y, rows, cols, 1e-5))),
+               ("rmsnorm", lambda cc: (lambda dx, dr, dg, db, y: cc.rmsnorm(dx, dg, cols, y, rows, cols, 1e-6))),
+               ("softmax", lambda cc: (lambda dx, dr, dg, db, y: cc.softmax(dx, y, rows, cols))))
+        for name, f in ops:
+            got = run(c, f(c), x, r, g, b, out_shape=x.shape)
+            want = run(ctx, f(ctx), x, r, g, b, out_shape=x.shape)
+            assert_bitexact(got, want, f"{name} lrapply=256x4")
+        outs = []
+        for cc in (c, ctx):
+            dx, dr, dg = cc.to_device(x), cc.to_device(r), cc.to_device(g)
+            dy, dro = cc.empty(x.shape), cc.empty(x.shape)
+            cc.add_rmsnorm(dx, dr, dro, dg, dy, rows, cols, 1e-6)
+            outs.append((dy.numpy(), dro.numpy()))
+            for d in (dx, dr, dg, dy, dro):
+                d.free()
+        assert_bitexact(outs[0][0], outs[1][0], "add+RMSNorm y lrapply=256x4")
+        assert_bitexact(outs[0][1], outs[1][1], "add+RMSNorm residual lrapply=256x4")
+    finally:
+        c.close()
+
+
 @pytest.mark.parametrize("rows,cols", [(1, 1 << 20), (3, 65536), (2, 20004), (1, 4097 * 4), (2, 20001),
                                        (300, 20004)])
 def test_longrow_layernorm_rmsnorm(ctx, rows, cols):

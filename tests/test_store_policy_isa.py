@@ -67,9 +67,10 @@ def test_keep_variants_store_as_intended(src, tmp_path):
             else:
                 assert all(nt), f"{name}: a streamed output lost its non-temporal hint"
             continue
-        # KEEP is the last template parameter, or the one before a trailing
-        # workgroup size (the streaming kernels' BS).
-        tail = re.search(r"Lb([01])E(?:Li\d+E)?EEv", name)
+        # KEEP is the last template parameter, or the one before the trailing
+        # workgroup shape (the streaming kernels' BS, the long-row apply
+        # pass's BS and VPT).
+        tail = re.search(r"Lb([01])E(?:Li\d+E)*EEv", name)
         keep = norm.group(1) == "1" if norm else bool(tail and tail.group(1) == "1")
         if not (norm or tail):
             continue  # not a KEEP-templated kernel
