@@ -1189,11 +1189,11 @@ struct EmbedKey {
     const void* ids;
     int32_t vocab;
     int32_t pad;
-    __device__ uint32_t operator()(int64_t t) const {
-        const int32_t id = load_id<MODE>(ids, t);
+    __device__ uint32_t of_id(int32_t id) const {
         const bool use = !(pad >= 0 && id == pad) && id >= 0 && id < vocab;
         return use ? static_cast<uint32_t>(id) : static_cast<uint32_t>(vocab);
     }
+    __device__ uint32_t operator()(int64_t t) const { return of_id(load_id<MODE>(ids, t)); }
 };
 
 // The end of the run of `id` that starts at sorted position i: each wave
@@ -1762,19 +1762,164 @@ __global__ __launch_bounds__(kSortBlock) void embed_sort_scatter(const void* ids
     }
 }
 
+// ---- The same sort in one launch, for tables of at most kOnePassKeys keys --
+// Workgroup b (kSortBlock tokens, as above) needs, for each of its tokens,
+// the number of tokens with a smaller key and the number of earlier blocks'
+// tokens with its key.  Instead of a counts table in HBM and two more
+// launches, every workgroup counts all n keys into a histogram in LDS
+// itself: the tokens before its block first (the histogram then holds the
+// earlier blocks' counts, read off for its own keys), then the rest.  One
+// exclusive scan of the histogram, with each key's count packed beside a
+// flag for the keys below `vocab` that have tokens, gives both each key's
+// first sorted position and its run's number in key order (both below
+// 2^16: at most kOnePassBlocks blocks, kOnePassKeys keys).  Positions and
+// run list are the three-launch sort's, bit for bit.  The histogram costs
+// each workgroup n LDS atomics and a read of the ids (L2 after the first
+// touch), issued before the block sort so its latency hides under it; the
+// scan takes kOnePassPer keys per thread (odd, so the threads' strided LDS
+// reads fall in distinct banks).
+constexpr int kOnePassPer = 33;
+constexpr int64_t kOnePassKeys = int64_t(kSortBlock) * kOnePassPer;  // 33792 keys: a 132 KiB histogram
+constexpr int kOnePassBlocks = 32;  // more tokens per thread spill registers; larger launches take three
+constexpr int kOnePassVec = kOnePassBlocks / 4;  // 16-byte vectors of ids per thread
+static_assert(kOnePassKeys < 65536 && kOnePassBlocks * kSortBlock <= 65536, "keys and counts are held as 16 bits");
+
+// Adds the keys of tokens in [from, to) to the histogram.  kp holds thread
+// i's keys of tokens 4 (i + kSortBlock j) + e (e < 4, j < kOnePassVec), two
+// 16-bit keys per word; slots past n hold v1 (no token).
+__device__ __forceinline__ void count_keys(uint32_t* hist, const uint32_t (&kp)[2 * kOnePassVec], uint32_t v1,
+                                           uint32_t from, uint32_t to) {
+#pragma unroll
+    for (int j = 0; j < kOnePassVec; ++j) {
+        const uint32_t u = 4u * (threadIdx.x + static_cast<uint32_t>(kSortBlock) * j);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const uint32_t k = (kp[2 * j + (e >> 1)] >> (16 * (e & 1))) & 0xffffu;
+            if (k < v1 && u + e >= from && u + e < to) atomicAdd(hist + k, 1u);
+        }
+    }
+}
+
+template <int MODE>
+__global__ __launch_bounds__(kSortBlock) void embed_sort_onepass(const void* ids, int64_t n64, int32_t vocab,
+                                                                 int32_t pad, uint32_t end_bit, uint32_t* skeys,
+                                                                 uint32_t* stoks, uint32_t* zero, uint32_t* nruns,
+                                                                 RunEntry* runs) {
+    using Sort = rocprim::block_radix_sort<uint32_t, kSortBlock, 1, uint32_t>;
+    using Scan = rocprim::block_scan<uint32_t, kSortBlock>;
+    __shared__ uint32_t hist[kOnePassKeys];
+    __shared__ union {
+        typename Sort::storage_type sort;
+        uint32_t sk[kSortBlock];  // the block's keys in sorted order, after the sort
+    } ss;
+    __shared__ typename Scan::storage_type scan;
+    const uint32_t b = blockIdx.x;
+    const uint32_t i = threadIdx.x;
+    const uint32_t n = static_cast<uint32_t>(n64);  // at most kOnePassBlocks * kSortBlock
+    const uint32_t v1 = static_cast<uint32_t>(vocab) + 1;  // keys 0 .. vocab; v1 marks no token
+    const uint32_t b0 = b * kSortBlock;
+    const EmbedKey<MODE> kf{ids, vocab, pad};
+    const uint32_t* w32 = static_cast<const uint32_t*>(ids);
+    if (zero && b == 0 && i == 0) *zero = 0;  // a counter of the kernels after the sort
+    // This thread's token first (the sort waits for it alone), then every
+    // token's id word, as 16-byte vectors where the ids are aligned.
+    const uint32_t own = b0 + i < n ? w32[b0 + i] : 0u;
+    const bool vec = (reinterpret_cast<uintptr_t>(ids) & 15u) == 0;
+    uint32_t w[kOnePassVec][4];
+#pragma unroll
+    for (int j = 0; j < kOnePassVec; ++j) {
+        const uint32_t u = 4u * (i + static_cast<uint32_t>(kSortBlock) * j);
+        if (vec && u + 3 < n) {
+            const uint4 q = *reinterpret_cast<const uint4*>(w32 + u);
+            w[j][0] = q.x, w[j][1] = q.y, w[j][2] = q.z, w[j][3] = q.w;
+        } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) w[j][e] = u + e < n ? w32[u + e] : 0u;
+        }
+    }
+    for (uint32_t j = i; j < v1; j += kSortBlock) hist[j] = 0;  // under the loads
+    uint32_t key[1] = {b0 + i < n ? kf.of_id(id_from_word<MODE>(own)) : v1};
+    uint32_t idx[1] = {i};
+    Sort().sort(key, idx, ss.sort, 0u, end_bit);  // stable: equal keys keep token order
+    // Thread i now holds the block's i-th token in key order: its key k, its
+    // token b0 + idx, and (below) its rank among the block's tokens of key k.
+    const uint32_t k = key[0];
+    __syncthreads();  // the sort's storage becomes sk
+    ss.sk[i] = k;
+    __syncthreads();
+    const bool head = i == 0 || ss.sk[i - 1] != k;
+    uint32_t first = 0;
+    Scan().inclusive_scan(head ? i : 0u, first, scan, rocprim::maximum<uint32_t>());
+    const uint32_t rank = i - first;
+    uint32_t kp[2 * kOnePassVec];
+#pragma unroll
+    for (int j = 0; j < kOnePassVec; ++j) {
+        const uint32_t u = 4u * (i + static_cast<uint32_t>(kSortBlock) * j);
+        uint32_t kk[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) kk[e] = u + e < n ? kf.of_id(id_from_word<MODE>(w[j][e])) : v1;
+        kp[2 * j] = kk[0] | kk[1] << 16;
+        kp[2 * j + 1] = kk[2] | kk[3] << 16;
+    }
+    __syncthreads();  // the histogram is zeroed
+    count_keys(hist, kp, v1, 0, b0);
+    __syncthreads();
+    const uint32_t earlier = k < v1 ? hist[k] : 0u;  // tokens of earlier blocks with key k
+    __syncthreads();
+    count_keys(hist, kp, v1, b0, n);
+    __syncthreads();
+    // Keys i * kOnePassPer .. + kOnePassPer - 1: (run flag << 16 | count),
+    // then, in place, the exclusive prefix of those over the keys.
+    uint32_t c[kOnePassPer];
+    uint32_t sum = 0;
+#pragma unroll
+    for (int j = 0; j < kOnePassPer; ++j) {
+        const uint32_t kk = i * kOnePassPer + j;
+        const uint32_t cnt = kk < v1 ? hist[kk] : 0u;
+        c[j] = cnt | (kk < static_cast<uint32_t>(vocab) && cnt > 0 ? 1u << 16 : 0u);
+        sum += c[j];
+    }
+    uint32_t pre = 0, all = 0;
+    Scan().exclusive_scan(sum, pre, 0u, all, scan, rocprim::plus<uint32_t>());
+#pragma unroll
+    for (int j = 0; j < kOnePassPer; ++j) {
+        const uint32_t kk = i * kOnePassPer + j;
+        if (kk < v1) hist[kk] = pre;
+        pre += c[j];
+    }
+    if (nruns && b == 0 && i == 0) *nruns = all >> 16;
+    __syncthreads();
+    if (k >= v1) return;  // a padding slot of the last block
+    const uint32_t h = hist[k];
+    const uint32_t s0 = h & 0xffffu;
+    const uint32_t pos = s0 + earlier + rank;
+    const uint32_t t = b0 + idx[0];
+    if (pos < n) {  // always, when the counts are consistent; kept as a bound regardless
+        skeys[pos] = k;
+        stoks[pos] = t;
+    }
+    // The run's first token (no earlier block holds its key, rank 0) lists it.
+    if (runs && k < static_cast<uint32_t>(vocab) && earlier == 0 && rank == 0) {
+        const uint32_t j = h >> 16;
+        if (j < n) runs[j] = RunEntry{k, pos, (hist[k + 1] & 0xffffu) - s0, t};
+    }
+}
+
 struct CountSortPlan {
     bool ok = false;
-    bool runs = false;  // also the run list
+    bool runs = false;     // also the run list
+    bool onepass = false;  // embed_sort_onepass (no counts table; only the run list in scratch)
     int64_t nb = 0, v1 = 0, pitch = 0, nchunks = 0;
     uint32_t end_bit = 0;
     size_t cnt_bytes = 0, start_bytes = 0, rank_bytes = 0, chunk_bytes = 0;
     size_t key_bytes = 0, list_bytes = 0;  // the run list's per-key arrays (x2), its count and entries
     size_t bytes() const {
+        if (onepass) return runs ? list_bytes : 0;
         return cnt_bytes + start_bytes + rank_bytes + chunk_bytes + (runs ? 2 * key_bytes + chunk_bytes + list_bytes : 0);
     }
 };
 
-CountSortPlan count_sort_plan(int64_t n, int32_t vocab, bool runs) {
+CountSortPlan count_sort_plan(int64_t n, int32_t vocab, bool runs, bool onepass) {
     CountSortPlan p;
     p.nb = (n + kSortBlock - 1) / kSortBlock;
     p.v1 = static_cast<int64_t>(vocab) + 1;
@@ -1791,12 +1936,22 @@ CountSortPlan count_sort_plan(int64_t n, int32_t vocab, bool runs) {
     p.runs = runs;
     p.key_bytes = align256(sizeof(uint32_t) * static_cast<size_t>(p.v1));
     p.list_bytes = 256 + align256(sizeof(RunEntry) * static_cast<size_t>(n));
+    p.onepass = onepass && p.ok && p.v1 <= kOnePassKeys && p.nb <= kOnePassBlocks;
     return p;
 }
 
 template <int MODE>
 int count_sort(mimir_ctx* ctx, const CountSortPlan& p, const void* ids, int64_t n, int32_t vocab, int32_t pad,
                char* temp, uint32_t* skeys, uint32_t* stoks, uint32_t* zero, RunList* list) {
+    const unsigned nb = static_cast<unsigned>(p.nb);
+    if (p.onepass) {
+        uint32_t* nruns = p.runs ? reinterpret_cast<uint32_t*>(temp) : nullptr;
+        RunEntry* runs = p.runs ? reinterpret_cast<RunEntry*>(temp + 256) : nullptr;
+        if (p.runs) *list = RunList{nruns, runs};
+        embed_sort_onepass<MODE><<<nb, kSortBlock, 0, ctx->stream>>>(ids, n, vocab, pad, p.end_bit, skeys, stoks,
+                                                                     zero, nruns, runs);
+        return launched(ctx, "embed_sort_onepass");
+    }
     uint16_t* cnt = reinterpret_cast<uint16_t*>(temp);
     uint32_t* start = reinterpret_cast<uint32_t*>(temp + p.cnt_bytes);
     uint16_t* rank = reinterpret_cast<uint16_t*>(temp + p.cnt_bytes + p.start_bytes);
@@ -1813,7 +1968,6 @@ int count_sort(mimir_ctx* ctx, const CountSortPlan& p, const void* ids, int64_t 
         runs = reinterpret_cast<RunEntry*>(r + 2 * p.key_bytes + p.chunk_bytes + 256);
         *list = RunList{nruns, runs};
     }
-    const unsigned nb = static_cast<unsigned>(p.nb);
     embed_sort_count<MODE><<<nb, kSortBlock, 0, ctx->stream>>>(ids, n, vocab, pad, p.end_bit, cnt, p.pitch, rank,
                                                                zero);
     if (int st = launched(ctx, "embed_sort_count")) return st;
@@ -1855,7 +2009,7 @@ int embed_bwd(mimir_ctx* ctx, const void* ids, int64_t n_ids, const float* dy, f
     const auto keys = rocprim::make_transform_iterator(rocprim::counting_iterator<int64_t>(0),
                                                        EmbedKey<MODE>{ids, vocab, pad});
     const rocprim::counting_iterator<uint32_t> toks(0);
-    const CountSortPlan plan = count_sort_plan(n_ids, vocab, ctx->tune.embed_bwd_runs != 0);
+    const CountSortPlan plan = count_sort_plan(n_ids, vocab, ctx->tune.embed_bwd_runs != 0, ctx->tune.embed_bwd_onepass != 0);
     const bool counting = plan.ok && ctx->tune.embed_bwd_sort != 0;
     size_t sort_bytes = 0;
     hipError_t e = hipSuccess;

@@ -25,12 +25,17 @@ __device__ __forceinline__ int32_t float_id(float f) {
 // Id modes: int32 ids (Model.cpp:1152-1205); float ids (Model.cpp:5301-5334);
 // int32 ids read as float first, as the forwardPassView float path does when
 // an Embedding's input comes from the int store (Model.cpp:4836-4840).
+// The id a 32-bit word of the ids array holds (every mode reads 32 bits).
+template <int MODE>
+__device__ __forceinline__ int32_t id_from_word(uint32_t w) {
+    if constexpr (MODE == kIdsF32) return float_id(__uint_as_float(w));
+    else if constexpr (MODE == kIdsI32AsF32) return float_id(static_cast<float>(static_cast<int32_t>(w)));
+    else return static_cast<int32_t>(w);
+}
+
 template <int MODE>
 __device__ __forceinline__ int32_t load_id(const void* ids, int64_t t) {
-    if constexpr (MODE == kIdsF32) return float_id(static_cast<const float*>(ids)[t]);
-    else if constexpr (MODE == kIdsI32AsF32)
-        return float_id(static_cast<float>(static_cast<const int32_t*>(ids)[t]));
-    else return static_cast<const int32_t*>(ids)[t];
+    return id_from_word<MODE>(static_cast<const uint32_t*>(ids)[t]);
 }
 
 }  // namespace mimir

@@ -69,6 +69,8 @@ struct Tuning {
     int embed_bwd_sort = -1;    // embedding backward: counting sort where it applies (-1, 1) or rocPRIM's (0)
     int embed_bwd_runs = -1;    // embedding backward: rows kernel over the counting sort's run list (-1, 1) or
                                 // over the sorted positions (0)
+    int embed_bwd_onepass = -1; // embedding backward: the counting sort in one launch where it applies (-1, 1) or
+                                // in three (0)
     int blas_lt = -1;           // library products: hipBLASLt first (-1, 1) or rocBLAS only (0)
     int lnbwd_narrow = -1;      // LayerNorm backward, rows <= 64 floats: several rows per wave (-1, 1) or not (0)
     int lr_cpw = 0;             // long rows: 4096-float chunks per workgroup of the first pass (1, 2, 4; 0: measured default)
@@ -116,6 +118,7 @@ inline Tuning read_tuning() {
         else if (!std::strcmp(k, "embmerge")) t.embed_bwd_merged = std::atoi(v);
         else if (!std::strcmp(k, "embsort")) t.embed_bwd_sort = std::atoi(v);
         else if (!std::strcmp(k, "embruns")) t.embed_bwd_runs = std::atoi(v);
+        else if (!std::strcmp(k, "emb1pass")) t.embed_bwd_onepass = std::atoi(v);
         else if (!std::strcmp(k, "blas")) t.blas_lt = std::atoi(v);
         else if (!std::strcmp(k, "lnbwd_narrow")) t.lnbwd_narrow = std::atoi(v);
         else if (!std::strcmp(k, "lrcpw")) t.lr_cpw = std::atoi(v);

@@ -403,10 +403,12 @@ def _tuned(tune):
 @pytest.fixture(scope="module")
 def sort_ctxs():
     """Contexts whose Embedding backward sorts with rocPRIM's radix sort and
-    takes a workgroup per sorted position (MIMIR_TUNE embsort=0), or sorts by
-    counting but keeps the per-position rows kernel (embruns=0), beside the
-    default (counting sort, a workgroup per listed run)."""
-    cs = {"radix": _tuned("embsort=0"), "positions": _tuned("embruns=0")}
+    takes a workgroup per sorted position (MIMIR_TUNE embsort=0), sorts by
+    counting but keeps the per-position rows kernel (embruns=0), or counts in
+    three launches instead of one (emb1pass=0), beside the default (the
+    counting sort in one launch up to 32 blocks and 33792 keys, a workgroup per listed
+    run)."""
+    cs = {"radix": _tuned("embsort=0"), "positions": _tuned("embruns=0"), "three": _tuned("emb1pass=0")}
     yield cs
     for c in cs.values():
         c.close()
@@ -416,14 +418,17 @@ def sort_ctxs():
     (32000, 32768, "uniform", False), (32000, 32768, "zipf", False), (32000, 32768, "uniform", True),
     (1023, 65536, "uniform", False), (1024, 65535, "zipf", False), (1025, 1025, "uniform", True),
     (1, 3000, "uniform", False), (70000, 4097, "uniform", False), (32000, 65537, "uniform", False),
-    (5, 1024, "one id", False)])
+    (5, 1024, "one id", False), (33791, 20000, "uniform", False), (33792, 9000, "zipf", True),
+    (5, 65536, "one id", False), (100, 32769, "uniform", False), (40, 32768, "zipf", True)])
 def test_embedding_bwd_counting_sort_matches_radix_sort(ctx, sort_ctxs, vocab, n, dist, float_ids):
-    """The counting sort (up to 64 blocks of 1024 tokens) puts every (id,
-    token) pair where the stable radix sort does, and its run list names
-    every run the per-position kernel finds, so the gradients are the same
-    bits: chunk edges of the key scan (vocab + 1 around 1024), padding and
-    out-of-range ids (the skipped key), a last partial block, the 64-block
-    limit and just past it (the radix sort on both sides)."""
+    """The counting sort (up to 64 blocks of 1024 tokens; in one launch up to
+    32 blocks and 33792 keys, else three) puts every (id, token) pair where the stable radix
+    sort does, and its run list names every run the per-position kernel
+    finds, so the gradients are the same bits: chunk edges of the key scan
+    (vocab + 1 around 1024), padding and out-of-range ids (the skipped key), a
+    last partial block, the 64-block limit and just past it (the radix sort
+    on both sides), a table or a launch past the one-launch limits (70000
+    ids, 33793 keys, 33 blocks)."""
     dim = 64
     if dist == "zipf":
         r = np.arange(1, vocab + 1, dtype=np.float64) ** -1.0
@@ -437,7 +442,8 @@ def test_embedding_bwd_counting_sort_matches_radix_sort(ctx, sort_ctxs, vocab, n
     dy = rng.standard_normal((n, dim)).astype(np.float32)
     gt = rng.standard_normal(vocab * dim).astype(np.float32)
     got = {}
-    for name, c in (("counting", ctx), ("radix", sort_ctxs["radix"]), ("positions", sort_ctxs["positions"])):
+    for name, c in (("counting", ctx), ("radix", sort_ctxs["radix"]), ("positions", sort_ctxs["positions"]),
+                    ("three", sort_ctxs["three"])):
         bi, bdy, bg = c.to_device(arg), c.to_device(dy), c.to_device(gt)
         try:
             c.embedding_bwd(bi, n, bdy, bg, gt.size, vocab, dim, pad, float_ids=float_ids)
@@ -447,8 +453,35 @@ def test_embedding_bwd_counting_sort_matches_radix_sort(ctx, sort_ctxs, vocab, n
                 d.free()
     assert_bitexact(got["counting"], got["radix"], f"{dist} ids, vocab {vocab}, {n} tokens")
     assert_bitexact(got["positions"], got["radix"], f"{dist} ids, vocab {vocab}, {n} tokens, per position")
+    assert_bitexact(got["three"], got["radix"], f"{dist} ids, vocab {vocab}, {n} tokens, three-launch count")
     ref = O.embedding_bwd(arg, dy, gt, vocab, dim, pad)
     _check_scatter(got["counting"], ref, arg, dy, gt, vocab, dim, pad, "grad table")
+
+
+@pytest.mark.parametrize("n", [4099, 32768])
+def test_embedding_bwd_ids_off_alignment(ctx, sort_ctxs, n):
+    """Ids starting 4 bytes past a 16-byte boundary: the one-launch sort reads
+    them word by word instead of as 16-byte vectors, and places the pairs
+    where the radix sort does."""
+    vocab, dim = 3000, 64
+    ids = rng.integers(-1, vocab + 1, n).astype(np.int32)
+    dy = rng.standard_normal((n, dim)).astype(np.float32)
+    gt = rng.standard_normal(vocab * dim).astype(np.float32)
+    got = {}
+    for name, c in (("counting", ctx), ("radix", sort_ctxs["radix"])):
+        buf = c.empty(n + 1, np.int32)
+        bi = buf.offset(1, (n,))
+        c.upload(bi, ids)
+        bdy, bg = c.to_device(dy), c.to_device(gt)
+        try:
+            c.embedding_bwd(bi, n, bdy, bg, gt.size, vocab, dim, 2)
+            got[name] = bg.numpy()
+        finally:
+            for d in (buf, bdy, bg):
+                d.free()
+    assert_bitexact(got["counting"], got["radix"], f"{n} ids off alignment")
+    ref = O.embedding_bwd(ids, dy, gt, vocab, dim, 2)
+    _check_scatter(got["counting"], ref, ids, dy, gt, vocab, dim, 2, "ids off alignment")
 
 
 def test_embedding_bwd_unaligned_rows_and_errors(ctx):
