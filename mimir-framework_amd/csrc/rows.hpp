@@ -49,7 +49,8 @@ struct RowShape {
 // Tuning override, read once per context from MIMIR_TUNE, e.g.
 //   MIMIR_TUNE="norm=1024x1x1024,layernorm=512x2x512,softmax=64x4x64,ew=1,gather=1024,rope=1,
 //               lnbwd=512x2x512,lnbwd_grid=512,chain=0,attnbwd_heads=4,attnbwd_blocks=2,
-//               embmerge=0,embsort=0,embruns=0,blas=0,lnbwd_narrow=0,lrcpw=2,ewbs=128"
+//               embmerge=0,embsort=0,embruns=0,emb1pass=0,blas=0,lnbwd_narrow=0,lrcpw=2,ewbs=128,
+//               lrapply=256x4"
 // Each entry selects among the compiled variants above; an entry that does
 // not fit a call (row too wide for it) is ignored for that call.  Unset, the
 // measured defaults apply.  Used for sweeps; results are identical.
