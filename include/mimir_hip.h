@@ -33,6 +33,7 @@ extern "C" {
 #define MIMIR_EINVAL 1  /* invalid shape / argument; the reference throws here */
 #define MIMIR_ENOMEM 2  /* device allocation failed or exceeded the context cap */
 #define MIMIR_EDEVICE 3 /* HIP runtime error or no usable device */
+#define MIMIR_EBUSY 4   /* a per-GPU resource is held by another context (mimir_layernorm_bwd_noalloc) */
 
 typedef struct mimir_ctx mimir_ctx;
 typedef struct mimir_event mimir_event;
@@ -346,8 +347,13 @@ int mimir_layernorm_bwd(mimir_ctx* ctx, const float* x, const float* dy, const f
  * is a fixed 32 MiB device array that the library reserves per GPU for the
  * life of the process.  A call that needs more (e.g. width 4096 takes 17.3 MB
  * with dgamma, a width above ~7900 takes more than 32 MiB) returns EINVAL
- * before any launch.  Every call on one GPU shares that array: calls that
- * overlap on one GPU (other streams, other threads) race. */
+ * before any launch.  One context per GPU uses that array at a time: the
+ * first context to call this entry point on a GPU holds it until the context
+ * is destroyed, and a call from another context on that GPU returns
+ * MIMIR_EBUSY before any launch.  The holder's calls run in its stream's
+ * order (mimir_ctx_set_stream waits for the old stream), so they cannot
+ * overlap.  The check is host-side only: it allocates nothing and records
+ * nothing into a captured graph. */
 int mimir_layernorm_bwd_noalloc(mimir_ctx* ctx, const float* x, const float* dy, const float* gamma, float* dx,
                                 float* dgamma, float* dbeta, int64_t groups, int64_t n, float eps, int accumulate);
 

@@ -2177,13 +2177,16 @@ int layernorm_bwd(mimir_ctx* ctx, const float* x, const float* dy, const float* 
 // host-side stand-in in host code; the device address comes from
 // hipGetSymbolAddress, once per device (noalloc_scratch_init).  The LayerNorm
 // backward writes every slot it later reads, so nothing in it has to start
-// at zero; calls that overlap on one GPU share it and race.
+// at zero.  One context per GPU holds it at a time (g_noalloc_owner): its
+// calls are ordered on its stream, and another context's call is refused,
+// so no two calls can overlap on it.
 constexpr size_t kNoAllocScratchBytes = size_t(32) << 20;
 static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
 
 constexpr int kMaxDevices = 64;
 std::mutex g_noalloc_mutex;
 void* g_noalloc_ptr[kMaxDevices] = {};
+const mimir_ctx* g_noalloc_owner[kMaxDevices] = {};
 
 }  // namespace
 
@@ -2202,6 +2205,13 @@ int mimir::noalloc_scratch_init(mimir_ctx* ctx) {
     return MIMIR_OK;
 }
 
+// A context being destroyed (its stream drained) gives the array up.
+void mimir::noalloc_scratch_release(mimir_ctx* ctx) {
+    if (ctx->device < 0 || ctx->device >= kMaxDevices) return;
+    std::lock_guard<std::mutex> lock(g_noalloc_mutex);
+    if (g_noalloc_owner[ctx->device] == ctx) g_noalloc_owner[ctx->device] = nullptr;
+}
+
 extern "C" {
 
 int mimir_layernorm_bwd(mimir_ctx* ctx, const float* x, const float* dy, const float* gamma, float* dx,
@@ -2214,6 +2224,16 @@ int mimir_layernorm_bwd_noalloc(mimir_ctx* ctx, const float* x, const float* dy,
     if (!ctx) return MIMIR_EINVAL;
     if (!ctx->noalloc_scratch)
         return fail(ctx, MIMIR_EDEVICE, "LayerNorm backward (no allocation): the device scratch is not set up");
+    {
+        std::lock_guard<std::mutex> lock(g_noalloc_mutex);
+        const mimir_ctx*& owner = g_noalloc_owner[ctx->device];  // device checked by noalloc_scratch_init
+        if (owner && owner != ctx)
+            return fail(ctx, MIMIR_EBUSY,
+                        "LayerNorm backward (no allocation): GPU %d's scratch array is held by another context "
+                        "until it is destroyed",
+                        ctx->device);
+        owner = ctx;
+    }
     const ScratchSpan fixed{ctx->noalloc_scratch, kNoAllocScratchBytes};
     return layernorm_bwd(ctx, x, dy, gamma, dx, dgamma, dbeta, groups, n, eps, accumulate, &fixed);
 }

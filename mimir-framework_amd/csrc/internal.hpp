@@ -167,6 +167,8 @@ int layernorm_fused(mimir_ctx* ctx, const LnFused& f);
 // Look up this context's device address of the no-allocation scratch array
 // (backward.hip); called once per context, with its device current.
 int noalloc_scratch_init(mimir_ctx* ctx);
+// Gives up the array if `ctx` holds it (context teardown, stream drained).
+void noalloc_scratch_release(mimir_ctx* ctx);
 // Widest row (floats) the register-resident row kernels hold, and the
 // per-GPU set-up of their unit weights (norm.hip), run at context creation.
 constexpr int kUnitCols = 4 * 4096;

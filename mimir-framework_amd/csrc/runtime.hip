@@ -136,6 +136,7 @@ int mimir_ctx_destroy(mimir_ctx* ctx) {
         for (void* p : ctx->retired) (void)hipFree(p);
         (void)hipStreamDestroy(ctx->own_stream);
     }
+    noalloc_scratch_release(ctx);  // after the stream drained (or could not be entered)
     delete ctx;
     return st;
 }

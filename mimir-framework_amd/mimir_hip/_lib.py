@@ -15,7 +15,7 @@ LIB_PATH = os.path.join(PKG_ROOT, "lib", "libmimir_hip.so")
 REPO_ROOT = os.path.dirname(PKG_ROOT)
 HEADER_PATH = os.path.join(REPO_ROOT, "include", "mimir_hip.h")
 
-OK, EINVAL, ENOMEM, EDEVICE = 0, 1, 2, 3
+OK, EINVAL, ENOMEM, EDEVICE, EBUSY = 0, 1, 2, 3, 4
 SOFTMAX_DIV_EPS, SOFTMAX_MUL_INV, SOFTMAX_LOG = 0, 1, 2
 
 _P = c_void_p

@@ -22,6 +22,12 @@ def test_header_declares_the_binding_set():
     assert header_functions() == sorted(M.SIGNATURES)
 
 
+def test_status_codes_match_the_header():
+    text = open(M.HEADER_PATH).read()
+    codes = {name: int(v) for name, v in re.findall(r"#define MIMIR_(OK|E[A-Z]+) (\d+)", text)}
+    assert codes == {"OK": M.OK, "EINVAL": M.EINVAL, "ENOMEM": M.ENOMEM, "EDEVICE": M.EDEVICE, "EBUSY": M.EBUSY}
+
+
 def test_library_exports_every_declared_symbol():
     lib = M.load()
     missing = [n for n in header_functions() if not hasattr(lib, n)]

@@ -4,7 +4,9 @@ mimir_layernorm_bwd through the C ABI: bit-identical dx / dgamma / dbeta on
 two calls in a row, the second smaller, on every kernel family (register-
 resident rows, 4-byte-column rows, generic rows, rows split over many
 workgroups); a call that needs more scratch than the array holds is refused;
-and the device's free memory does not move across the calls."""
+the device's free memory does not move across the calls; and one context per
+GPU holds the array at a time (another context's call is refused with EBUSY
+until the holder is destroyed)."""
 import ctypes
 from ctypes import c_float, c_int, c_int64, c_void_p
 
@@ -123,3 +125,41 @@ def test_noalloc_allocates_nothing():
         assert _free_bytes(hip) >= before
         for d in keep:
             d.free()
+
+
+def test_noalloc_array_has_one_holder_per_gpu():
+    """The first context to call the entry point holds the GPU's array; a
+    second context's call returns EBUSY and launches nothing (its outputs
+    keep their bits); once the holder is destroyed the second context takes
+    the array and matches the allocating entry point."""
+    groups, n = 512, 4096
+    a = M.Context(0)
+    b = M.Context(0)
+    try:
+        x, dy, g, outs, keep = _case(a, groups, n, 0)
+        dx, dg, db = outs[0]
+        assert _call(a, "mimir_layernorm_bwd_noalloc", x, dy, g, dx, dg, db, groups, n) == 0
+        a.sync()
+        for d in keep:
+            d.free()
+        xb, dyb, gb, outsb, keepb = _case(b, groups, n, 0, seed=1)
+        (dx0, dg0, db0), (dx1, dg1, db1) = outsb
+        before = (dx1.numpy().copy(), dg1.numpy().copy(), db1.numpy().copy())
+        assert _call(b, "mimir_layernorm_bwd_noalloc", xb, dyb, gb, dx1, dg1, db1, groups, n) == M.EBUSY
+        assert b"another context" in b.lib.mimir_last_error(b.handle)
+        b.sync()
+        for got, was in zip((dx1.numpy(), dg1.numpy(), db1.numpy()), before):
+            assert np.array_equal(got.view(np.uint32), was.view(np.uint32)), "a refused call wrote"
+        a.close()
+        a = None
+        assert _call(b, "mimir_layernorm_bwd", xb, dyb, gb, dx0, dg0, db0, groups, n) == 0
+        assert _call(b, "mimir_layernorm_bwd_noalloc", xb, dyb, gb, dx1, dg1, db1, groups, n) == 0
+        b.sync()
+        for u, v in ((dx0, dx1), (dg0, dg1), (db0, db1)):
+            assert np.array_equal(u.numpy().view(np.uint32), v.numpy().view(np.uint32))
+        for d in keepb:
+            d.free()
+    finally:
+        if a is not None:
+            a.close()
+        b.close()
