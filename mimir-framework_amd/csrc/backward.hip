@@ -2009,7 +2009,8 @@ int embed_bwd(mimir_ctx* ctx, const void* ids, int64_t n_ids, const float* dy, f
     const auto keys = rocprim::make_transform_iterator(rocprim::counting_iterator<int64_t>(0),
                                                        EmbedKey<MODE>{ids, vocab, pad});
     const rocprim::counting_iterator<uint32_t> toks(0);
-    const CountSortPlan plan = count_sort_plan(n_ids, vocab, ctx->tune.embed_bwd_runs != 0, ctx->tune.embed_bwd_onepass != 0);
+    const CountSortPlan plan =
+        count_sort_plan(n_ids, vocab, ctx->tune.embed_bwd_runs != 0, ctx->tune.embed_bwd_onepass != 0);
     const bool counting = plan.ok && ctx->tune.embed_bwd_sort != 0;
     size_t sort_bytes = 0;
     hipError_t e = hipSuccess;

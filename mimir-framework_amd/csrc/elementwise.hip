@@ -5,9 +5,12 @@
 // workgroup-width apart (so each wave instruction moves 1 KiB of contiguous
 // data), issues all its loads before any arithmetic, and writes with
 // non-temporal stores: every input byte is read once and every output byte
-// written once.  VPT = 1 (one vector per thread, many waves in flight)
-// streams fastest on MI355X; 2 and 4 stay available for sweeps (MIMIR_TUNE).  Buffers that are not 16-byte aligned, and the n % 4 tail,
-// run through a scalar grid-stride kernel with the same per-element functor.
+// written once.  VPT = 1 (one vector per thread, many waves in flight) in
+// 128-thread workgroups streams fastest on MI355X (kEwBlock); 2 and 4 vectors
+// per thread and 64-1024-thread workgroups stay available for sweeps
+// (MIMIR_TUNE ew=, ewbs=).  Buffers that are not 16-byte aligned, and the
+// n % 4 tail, run through a scalar grid-stride kernel with the same
+// per-element functor.
 #include "common.hpp"
 #include "internal.hpp"
 #include "pointwise.hpp"

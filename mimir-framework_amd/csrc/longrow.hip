@@ -5,8 +5,8 @@
 // row (LayerOpsExt.hpp:345-378, LayerOps.hpp:325-361), and so does LayerNorm
 // when in_features is unset (LayerOps.hpp:276); a transformer's activations
 // make that row millions of elements long.  One workgroup per row would leave
-// all but one CU idle, so such rows are cut into chunks of 4096 floats, one
-// 256-thread workgroup each:
+// all but one CU idle, so such rows are cut into chunks of 4096 floats (one
+// 256-thread workgroup each for the statistics):
 //   1. partial : per chunk, the partial statistic (sum, sum of squares,
 //                sum of squared deviations, or softmax's (max, sum of exp));
 //   2. combine : one 1024-thread workgroup per row folds the chunk partials
@@ -27,7 +27,8 @@
 // mean is large against its spread keeps its precision.  Every
 // op reads x twice (statistics, then apply) and writes y once; the second
 // read walks the row backwards, so that its first part can come from the MALL
-// (measured: the apply streams at the HBM rate whatever the row size).
+// (measured on one 2^25-float row, 128 MiB: the apply pass moves its 256 MiB
+// of read and write at 7.3 TB/s, above the HBM stream rate).
 // Partials live in the context's scratch buffer, reused in stream order.
 #include "common.hpp"
 #include "internal.hpp"
