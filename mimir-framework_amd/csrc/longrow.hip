@@ -6,7 +6,7 @@
 // when in_features is unset (LayerOps.hpp:276); a transformer's activations
 // make that row millions of elements long.  One workgroup per row would leave
 // all but one CU idle, so such rows are cut into chunks of 4096 floats (one
-// 256-thread workgroup each for the statistics):
+// workgroup per chunk, or two for LayerNorm, for the statistics):
 //   1. partial : per chunk, the partial statistic (sum, sum of squares,
 //                sum of squared deviations, or softmax's (max, sum of exp));
 //   2. combine : one 1024-thread workgroup per row folds the chunk partials
@@ -96,20 +96,25 @@ __device__ __forceinline__ double block_sum_f64(double v, double* lds) {
 // the forward order): every chunk's loads are issued before the first
 // chunk's reductions, so a workgroup keeps CPW chunks in flight; each
 // chunk's partial is the one-chunk computation, bit for bit.
-template <int S, int CPW = 1>
-__global__ __launch_bounds__(kBlock) void lr_partial(LongArgs a) {
-    __shared__ float lds[2][kBlock / kWave];
+// BS threads hold a chunk, VPT = kChunk4 / BS float4 each (the chunk, its
+// partial's definition and the combine are the same for every BS; only the
+// order of the sums inside a chunk differs).
+template <int S, int CPW = 1, int BS = kBlock>
+__global__ __launch_bounds__(BS) void lr_partial(LongArgs a) {
+    constexpr int VPT = static_cast<int>(kChunk4) / BS;
+    static_assert(VPT * BS == kChunk4, "a chunk fills the workgroup's slots");
+    __shared__ float lds[2][BS / kWave];
     const int64_t row = blockIdx.y;
     const int64_t c4n = a.cols >> 2;
     const int64_t base = row * a.cols;
-    f4 vv[CPW][kChunkVec];
-    bool okk[CPW][kChunkVec];
+    f4 vv[CPW][VPT];
+    bool okk[CPW][VPT];
 #pragma unroll
     for (int i = 0; i < CPW; ++i) {
         const int64_t chunk = CPW == 1 ? chunk_of(a) : static_cast<int64_t>(blockIdx.x) * CPW + i;
 #pragma unroll
-        for (int j = 0; j < kChunkVec; ++j) {
-            const int64_t c4 = chunk * kChunk4 + static_cast<int64_t>(j) * kBlock + threadIdx.x;
+        for (int j = 0; j < VPT; ++j) {
+            const int64_t c4 = chunk * kChunk4 + static_cast<int64_t>(j) * BS + threadIdx.x;
             okk[i][j] = chunk < a.nchunks && c4 < c4n;
             if constexpr (S == kSumSqAdd) {
                 if (okk[i][j]) {
@@ -130,43 +135,43 @@ __global__ __launch_bounds__(kBlock) void lr_partial(LongArgs a) {
         if constexpr (S == kSoftmax) {
             float m = -INFINITY;
 #pragma unroll
-            for (int j = 0; j < kChunkVec; ++j)
+            for (int j = 0; j < VPT; ++j)
                 if (ok[j]) m = fmaxf(m, fmaxf(fmaxf(v[j].x, v[j].y), fmaxf(v[j].z, v[j].w)));
-            m = block_max<kBlock / kWave>(m, lds[0]);
+            m = block_max<BS / kWave>(m, lds[0]);
             float s = 0.0f;
             if (m != -INFINITY) {  // an all -inf chunk contributes nothing
 #pragma unroll
-                for (int j = 0; j < kChunkVec; ++j)
+                for (int j = 0; j < VPT; ++j)
                     if (ok[j])
                         s += (expf(v[j].x - m) + expf(v[j].y - m)) + (expf(v[j].z - m) + expf(v[j].w - m));
             }
             p0 = m;
-            p1 = block_sum<kBlock / kWave>(s, lds[1]);
+            p1 = block_sum<BS / kWave>(s, lds[1]);
         } else if constexpr (S == kChan) {
             const float x0 = a.x[base];  // the shift
             float s = 0.0f;
 #pragma unroll
-            for (int j = 0; j < kChunkVec; ++j) {
+            for (int j = 0; j < VPT; ++j) {
                 if (!ok[j]) continue;
                 v[j] -= x0;
                 s += (v[j].x + v[j].y) + (v[j].z + v[j].w);
             }
-            p0 = block_sum<kBlock / kWave>(s, lds[0]);
+            p0 = block_sum<BS / kWave>(s, lds[0]);
             const float mc = chunk < a.nchunks ? p0 / chunk_len(a, chunk) : 0.0f;  // recomputed bit for bit by the combine
             float q = 0.0f;
 #pragma unroll
-            for (int j = 0; j < kChunkVec; ++j) {
+            for (int j = 0; j < VPT; ++j) {
                 if (!ok[j]) continue;
                 const f4 d = v[j] - mc;
                 q += (d.x * d.x + d.y * d.y) + (d.z * d.z + d.w * d.w);
             }
-            p1 = block_sum<kBlock / kWave>(q, lds[1]);
+            p1 = block_sum<BS / kWave>(q, lds[1]);
         } else {
             float s = 0.0f;
 #pragma unroll
-            for (int j = 0; j < kChunkVec; ++j)
+            for (int j = 0; j < VPT; ++j)
                 if (ok[j]) s += (v[j].x * v[j].x + v[j].y * v[j].y) + (v[j].z * v[j].z + v[j].w * v[j].w);
-            p0 = block_sum<kBlock / kWave>(s, lds[0]);
+            p0 = block_sum<BS / kWave>(s, lds[0]);
         }
         if (threadIdx.x == 0 && chunk < a.nchunks) {
             float* p = a.partial + 2 * (row * a.nchunks + chunk);
@@ -192,14 +197,27 @@ constexpr int kCombineU = 8;
 // per workgroup, 75.2 -> 69.8 us for the whole op, while the one-reduction
 // passes lose 1-2% (softmax 67.2 -> 68.7 us, RMSNorm 65.0 -> 65.9 us) and
 // all lose at four.
+template <int S, int BS>
+void launch_partial_bs(mimir_ctx* ctx, const LongArgs& a, int64_t rows, int cpw) {
+    const dim3 grid(static_cast<unsigned>((a.nchunks + cpw - 1) / cpw), static_cast<unsigned>(rows));
+    if (cpw == 4) lr_partial<S, 4, BS><<<grid, BS, 0, ctx->stream>>>(a);
+    else if (cpw == 2) lr_partial<S, 2, BS><<<grid, BS, 0, ctx->stream>>>(a);
+    else lr_partial<S, 1, BS><<<grid, BS, 0, ctx->stream>>>(a);
+}
+
+// Threads per chunk (MIMIR_TUNE lrpart=256 / 512 overrides): 512 (2 float4
+// each) for the LayerNorm statistic, 256 (4 each) for the others.  Measured
+// on MI355X on one 2^25-float row, whole op, 256 / 512 threads: LayerNorm
+// 67.3-67.5 / 66.7 us, softmax 65.3-65.7 / 65.6-66.1, RMSNorm 62.6 / 62.4-62.5
+// (128 threads, 8 float4 each: 1.3-2 us slower for LayerNorm and softmax).
 template <int S>
 void launch_partial(mimir_ctx* ctx, const LongArgs& a, int64_t rows) {
     const int over = ctx->tune.lr_cpw;
     const int cpw = over == 1 || over == 2 || over == 4 ? over : (S == kChan ? 2 : 1);
-    const dim3 grid(static_cast<unsigned>((a.nchunks + cpw - 1) / cpw), static_cast<unsigned>(rows));
-    if (cpw == 4) lr_partial<S, 4><<<grid, kBlock, 0, ctx->stream>>>(a);
-    else if (cpw == 2) lr_partial<S, 2><<<grid, kBlock, 0, ctx->stream>>>(a);
-    else lr_partial<S, 1><<<grid, kBlock, 0, ctx->stream>>>(a);
+    const int bs = ctx->tune.lr_part_bs == 256 || ctx->tune.lr_part_bs == 512 ? ctx->tune.lr_part_bs
+                                                                             : (S == kChan ? 512 : kBlock);
+    if (bs == 512) launch_partial_bs<S, 512>(ctx, a, rows, cpw);
+    else launch_partial_bs<S, kBlock>(ctx, a, rows, cpw);
 }
 
 template <int S>

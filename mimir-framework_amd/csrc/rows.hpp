@@ -50,7 +50,7 @@ struct RowShape {
 //   MIMIR_TUNE="norm=1024x1x1024,layernorm=512x2x512,softmax=64x4x64,ew=1,gather=1024,rope=1,
 //               lnbwd=512x2x512,lnbwd_grid=512,chain=0,attnbwd_heads=4,attnbwd_blocks=2,
 //               embmerge=0,embsort=0,embruns=0,emb1pass=0,blas=0,lnbwd_narrow=0,lrcpw=2,ewbs=128,
-//               lrapply=256x4"
+//               lrapply=256x4,lrpart=256"
 // Each entry selects among the compiled variants above; an entry that does
 // not fit a call (row too wide for it) is ignored for that call.  Unset, the
 // measured defaults apply.  Used for sweeps; results are identical.
@@ -78,6 +78,7 @@ struct Tuning {
     int ew_bs = 0;              // workgroup size of the one-float4-per-thread streaming kernels (64 .. 1024; 0: default)
     int lr_apply_bs = 0;        // long rows' apply pass shape (lrapply=256x4: the chunk shape)
     int lr_apply_vpt = 0;
+    int lr_part_bs = 0;         // long rows' first pass: threads per 4096-float chunk (lrpart=256/512; 0: default)
 };
 
 inline bool parse_shape(const char* v, RowShape* s) {
@@ -124,6 +125,7 @@ inline Tuning read_tuning() {
         else if (!std::strcmp(k, "lnbwd_narrow")) t.lnbwd_narrow = std::atoi(v);
         else if (!std::strcmp(k, "lrcpw")) t.lr_cpw = std::atoi(v);
         else if (!std::strcmp(k, "ewbs")) t.ew_bs = std::atoi(v);
+        else if (!std::strcmp(k, "lrpart")) t.lr_part_bs = std::atoi(v);
         else if (!std::strcmp(k, "lrapply")) {
             char* end = nullptr;
             t.lr_apply_bs = static_cast<int>(std::strtol(v, &end, 10));

@@ -414,6 +414,41 @@ def test_longrow_chunks_per_workgroup(ctx, cpw):
         c.close()
 
 
+@pytest.mark.parametrize("bs", [256, 512])
+def test_longrow_first_pass_threads_per_chunk(ctx, bs):
+    """The long rows' first pass with 256 or 512 threads per 4096-float chunk
+    (MIMIR_TUNE lrpart; 512 for the LayerNorm statistic by default, 256 for
+    the others) sums each chunk in a different order: LayerNorm, RMSNorm and
+    softmax over rows with a partial last chunk stay within the oracle's
+    tolerance (or nearer the exact value) either way."""
+    import os
+    old = os.environ.get("MIMIR_TUNE")
+    os.environ["MIMIR_TUNE"] = f"lrpart={bs}"
+    try:
+        c = M.Context(0)
+    finally:
+        if old is None:
+            del os.environ["MIMIR_TUNE"]
+        else:
+            os.environ["MIMIR_TUNE"] = old
+    try:
+        rows, cols = 3, 4096 * 7 + 20
+        x = (rng.standard_normal((rows, cols), dtype=np.float32) * 1.3 + 0.2)
+        g = (1 + 0.05 * rng.standard_normal(cols)).astype(np.float32)
+        b = (0.05 * rng.standard_normal(cols)).astype(np.float32)
+        got = run(c, lambda dx, dg, db, y: c.layernorm(dx, dg, db, y, rows, cols, 1e-5), x, g, b, out_shape=x.shape)
+        assert_close_or_nearer_exact(got, O.layernorm(x, cols, g, b, 1e-5).reshape(x.shape),
+                                     X.layernorm(x, cols, g, b, 1e-5), f"long LN lrpart={bs}")
+        got = run(c, lambda dx, dw, y: c.rmsnorm(dx, dw, cols, y, rows, cols, 1e-6), x, g, out_shape=x.shape)
+        assert_close_or_nearer_exact(got, O.rmsnorm_rows(x, g, 1e-6), X.rmsnorm(x, cols, g, cols, 1e-6),
+                                     f"long RMSNorm lrpart={bs}")
+        got = run(c, lambda dx, y: c.softmax(dx, y, rows, cols), x, out_shape=x.shape)
+        assert_close_or_nearer_exact(got, O.softmax_rows(x, M.SOFTMAX_DIV_EPS), X.softmax(x, M.SOFTMAX_DIV_EPS),
+                                     f"long softmax lrpart={bs}")
+    finally:
+        c.close()
+
+
 @pytest.mark.parametrize("rows,cols", [(3, 4096 * 7 + 20), (1, 4096 * 64 * 3 + 4), (2, 70000)])
 def test_longrow_apply_shapes_agree(ctx, rows, cols):
     """The apply pass in its default shape (128 threads x 2 float4) and in the
