@@ -236,7 +236,8 @@ __global__ __launch_bounds__(kTile * 8) void transpose_kernel(const float* __res
 
 int transpose(mimir_ctx* ctx, const float* src, int64_t ld_src, int64_t rows, int64_t cols, float* dst) {
     const int64_t gx = (cols + kTile - 1) / kTile, gy = (rows + kTile - 1) / kTile;
-    if (gx > INT32_MAX || gy > 65535) return fail(ctx, MIMIR_EINVAL, "attention backward: transpose grid too large");
+    if (!dispatch_fits(gx, kTile * 8) || gy > 65535)
+        return fail(ctx, MIMIR_EINVAL, "attention backward: transpose grid too large");
     transpose_kernel<<<dim3(static_cast<unsigned>(gx), static_cast<unsigned>(gy)), kTile * 8, 0, ctx->stream>>>(
         src, ld_src, rows, cols, dst);
     return launched(ctx, "transpose_kernel");

@@ -2024,6 +2024,9 @@ int embed_bwd(mimir_ctx* ctx, const void* ids, int64_t n_ids, const float* dy, f
     }
     const size_t vbytes = align256(sizeof(uint32_t) * n);
     const bool vec = (dim % 4) == 0 && aligned16(dy) && aligned16(grad);
+    if (!vec && !dispatch_fits(n_ids, kBlock))  // the scalar rows kernel: a workgroup per sorted position
+        return fail(ctx, MIMIR_EINVAL, "Embedding backward: %lld ids of %d-float rows exceed the grid limit",
+                    (long long)n_ids, dim);
     const bool long_runs = vec && n_ids >= kLongRun;
     // Partial rows of the long runs' segments: one slot per kLongRun positions.
     const int64_t nslots = (n_ids + kLongRun - 1) / kLongRun;

@@ -496,6 +496,13 @@ def test_embedding_bwd_unaligned_rows_and_errors(ctx):
         assert_bitexact(bg.numpy(), ref, "dim 5 (scalar rows)")
         with pytest.raises(M.MimirError):
             ctx.embedding_bwd(bi, n, bdy, bg, gt.size - 1, vocab, dim, -1)  # table too small
+        # The scalar rows kernel (dim 5) takes a 256-thread workgroup per id:
+        # 2^24 + 1 ids exceed the dispatch's 2^32 work-items, refused before
+        # any launch (the buffers are far shorter than such a call would read).
+        with pytest.raises(M.MimirError) as e:
+            ctx.embedding_bwd(bi, (1 << 24) + 1, bdy, bg, gt.size, vocab, dim, -1)
+        assert e.value.status == M.EINVAL and "grid limit" in str(e.value)
+        assert_bitexact(bg.numpy(), ref, "untouched by the refused call")
     finally:
         for d in (bi, bdy, bg):
             d.free()
