@@ -1782,7 +1782,7 @@ constexpr int kOnePassPer = 33;
 constexpr int64_t kOnePassKeys = int64_t(kSortBlock) * kOnePassPer;  // 33792 keys: a 132 KiB histogram
 constexpr int kOnePassBlocks = 32;  // more tokens per thread spill registers; larger launches take three
 constexpr int kOnePassVec = kOnePassBlocks / 4;  // 16-byte vectors of ids per thread
-static_assert(kOnePassKeys < 65536 && kOnePassBlocks * kSortBlock <= 65536, "keys and counts are held as 16 bits");
+static_assert(kOnePassKeys < 65536 && kOnePassBlocks * kSortBlock < 65536, "keys, counts and positions are held as 16 bits");
 
 // Adds the keys of tokens in [from, to) to the histogram.  kp holds thread
 // i's keys of tokens 4 (i + kSortBlock j) + e (e < 4, j < kOnePassVec), two
